@@ -1,0 +1,97 @@
+"""ctypes binding of the C-ABI library libgdn_mi355x.so (declared in include/gdn_mi355x.h).
+
+The library is the only compute path: if it is missing, every op raises instead of falling back to anything.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (loads the HIP runtime the library binds to by soname)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libgdn_mi355x.so")
+
+GDN_OK, GDN_ERR_ARG, GDN_ERR_SHAPE, GDN_ERR_WORKSPACE, GDN_ERR_LAUNCH = 0, 1, 2, 3, 4
+DTYPE_F32, DTYPE_BF16 = 0, 1
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); must list every function include/gdn_mi355x.h declares
+SIGNATURES = {
+    "gdn_version": (_i, []),
+    "gdn_last_error": (ctypes.c_char_p, []),
+    "gdn_supported": (_i, [_i, _i, _i, _i]),
+    "gdn_chunk_fwd_ws_bytes": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_sz)]),
+    "gdn_chunk_bwd_ws_bytes": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_sz)]),
+    "gdn_chunk_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _f, _i, _p]),
+    "gdn_chunk_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz,
+                           _i, _i, _i, _i, _i, _f, _i, _p]),
+    "gdn_recurrent_step": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i, _p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class GDNLibraryError(RuntimeError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise GDNLibraryError(
+                    f"{LIB_PATH} is missing: build it with `python -m archbench_amd.build` (hipcc, gfx950). "
+                    "The gated DeltaNet op has no other implementation.")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype, fn.argtypes = res, args
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == GDN_OK:
+        return
+    msg = load().gdn_last_error().decode(errors="replace")
+    if rc in (GDN_ERR_ARG, GDN_ERR_SHAPE):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg} (code {rc})")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return DTYPE_BF16
+    if dt == torch.float32:
+        return DTYPE_F32
+    raise ValueError(f"gated DeltaNet kernels take bfloat16 or float32 q/k/v, got {dt}")
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_ptr(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def supported(op: str, K: int, V: int, dtype: torch.dtype) -> bool:
+    return bool(load().gdn_supported({"chunk": 0, "step": 1}[op], K, V, dtype_code(dtype)))
+
+
+def ws_bytes(kind: str, B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype) -> int:
+    out = _sz(0)
+    fn = load().gdn_chunk_fwd_ws_bytes if kind == "fwd" else load().gdn_chunk_bwd_ws_bytes
+    check(fn(B, T, H, K, V, dtype_code(dtype), ctypes.byref(out)), f"gdn_chunk_{kind}_ws_bytes")
+    return out.value

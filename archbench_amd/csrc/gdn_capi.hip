@@ -1,0 +1,184 @@
+// extern "C" entry points: argument validation, workspace carve-up and kernel sequencing.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/gdn_mi355x.h"
+#include "gdn_launch.h"
+
+namespace gdn {
+
+static thread_local char g_err[512] = "";
+
+static int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+static int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, bool backward, ChunkWs* carve, void* base) {
+  const size_t es = dtype == DT_BF16 ? 2 : 4;
+  const size_t NT = (size_t)(T + CH_TOKENS - 1) / CH_TOKENS;
+  const size_t BH = (size_t)B * H;
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t bytes) -> void* {
+    void* r = p ? p + off : nullptr;
+    off += align256(bytes);
+    return r;
+  };
+  ChunkWs ws{};
+  ws.Tm = take(BH * NT * CH_TOKENS * CH_TOKENS * es);
+  ws.P = take(BH * NT * CH_TOKENS * CH_TOKENS * es);
+  ws.W = take(BH * NT * CH_TOKENS * (size_t)K * es);
+  ws.Gc = static_cast<float*>(take(BH * NT * CH_TOKENS * 4));
+  if (backward) {
+    ws.hs = take(BH * NT * (size_t)K * V * es);
+    ws.Rs = take(BH * NT * CH_TOKENS * (size_t)V * es);
+    ws.dhs = take(BH * NT * (size_t)K * V * es);
+    ws.dRs = take(BH * NT * CH_TOKENS * (size_t)V * es);
+  }
+  if (carve) *carve = ws;
+  return off;
+}
+
+bool chunk_shape_supported(int K, int V, int dtype) {
+  const bool v_ok = V == 64 || V == 128 || V == 256;
+  if (dtype == DT_BF16) return (K == 64 || K == 128) && v_ok;
+  if (dtype == DT_F32) return K == 64 && (V == 64 || V == 128);
+  return false;
+}
+
+__global__ void copy_or_zero_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src ? src[i] : 0.f;
+}
+
+static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStream_t st) {
+  if (!dst || n == 0) return hipSuccess;
+  const int64_t blocks = (n + 255) / 256;
+  copy_or_zero_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(src, dst, n);
+  return hipGetLastError();
+}
+
+static int check_common(int B, int T, int H, int K, int V, int dtype) {
+  if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
+  if (B < 0 || T < 0 || H < 0 || K <= 0 || V <= 0)
+    return fail(GDN_ERR_ARG, "invalid sizes B=%d T=%d H=%d K=%d V=%d", B, T, H, K, V);
+  if ((int64_t)B * T * H * (K > V ? K : V) >= ((int64_t)1 << 31) * 16)
+    return fail(GDN_ERR_ARG, "tensor too large for 64-bit indexing plan");
+  return GDN_OK;
+}
+
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" {
+
+int gdn_version(void) { return 100; }
+
+const char* gdn_last_error(void) { return g_err; }
+
+int gdn_supported(int op, int K, int V, int dtype) {
+  if (op == 0) return chunk_shape_supported(K, V, dtype) ? 1 : 0;
+  if (op == 1) return (dtype == DT_F32 || dtype == DT_BF16) && step_shape_supported(K, V) ? 1 : 0;
+  return 0;
+}
+
+int gdn_chunk_fwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t* bytes) {
+  g_err[0] = 0;
+  if (int e = check_common(B, T, H, K, V, dtype)) return e;
+  if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
+  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, false, nullptr, nullptr);
+  return GDN_OK;
+}
+
+int gdn_chunk_bwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t* bytes) {
+  g_err[0] = 0;
+  if (int e = check_common(B, T, H, K, V, dtype)) return e;
+  if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
+  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, true, nullptr, nullptr);
+  return GDN_OK;
+}
+
+int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                  const float* h0, void* o, float* hT, void* ws, size_t ws_bytes, int B, int T, int H, int K,
+                  int V, float scale, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (int e = check_common(B, T, H, K, V, dtype)) return e;
+  if (!chunk_shape_supported(K, V, dtype))
+    return fail(GDN_ERR_SHAPE, "chunk kernels not compiled for K=%d V=%d dtype=%d", K, V, dtype);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t nstate = (int64_t)B * H * K * V;
+  if (B == 0 || H == 0) return GDN_OK;
+  if (T == 0) {
+    if (copy_or_zero(h0, hT, nstate, st) != hipSuccess) return fail(GDN_ERR_LAUNCH, "state copy launch failed");
+    return GDN_OK;
+  }
+  if (!q || !k || !v || !g || !beta || !o) return fail(GDN_ERR_ARG, "null input/output pointer");
+  ChunkArgs a{};
+  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, false, &a.ws, ws);
+  if (!ws || ws_bytes < need)
+    return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
+  a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.h0 = h0; a.o = o; a.hT = hT;
+  a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
+  a.scale = scale; a.dtype = dtype; a.stream = st;
+  hipError_t e = launch_fwd_intra(a);
+  if (e == hipSuccess) e = launch_fwd_state(a, false);
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "chunk forward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                  const float* h0, const void* dout, const float* dhT, void* dq, void* dk, void* dv, float* dg,
+                  float* dbeta, float* dh0, void* ws, size_t ws_bytes, int B, int T, int H, int K, int V,
+                  float scale, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (int e = check_common(B, T, H, K, V, dtype)) return e;
+  if (!chunk_shape_supported(K, V, dtype))
+    return fail(GDN_ERR_SHAPE, "chunk kernels not compiled for K=%d V=%d dtype=%d", K, V, dtype);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t nstate = (int64_t)B * H * K * V;
+  if (B == 0 || H == 0) return GDN_OK;
+  if (T == 0) {
+    if (copy_or_zero(dhT, dh0, nstate, st) != hipSuccess) return fail(GDN_ERR_LAUNCH, "state copy launch failed");
+    return GDN_OK;
+  }
+  if (!q || !k || !v || !g || !beta || !dout || !dq || !dk || !dv || !dg || !dbeta)
+    return fail(GDN_ERR_ARG, "null input/output pointer");
+  ChunkArgs a{};
+  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, true, &a.ws, ws);
+  if (!ws || ws_bytes < need)
+    return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
+  a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.h0 = h0;
+  a.dout = dout; a.dhT = dhT; a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dh0 = dh0;
+  a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
+  a.scale = scale; a.dtype = dtype; a.stream = st;
+  hipError_t e = launch_fwd_intra(a);
+  if (e == hipSuccess) e = launch_fwd_state(a, true);
+  if (e == hipSuccess) e = launch_bwd_state(a);
+  if (e == hipSuccess) e = launch_bwd_intra(a);
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "chunk backward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+int gdn_recurrent_step(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                       float* state, void* o, int B, int H, int K, int V, float scale, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (int e = check_common(B, 1, H, K, V, dtype)) return e;
+  if (!step_shape_supported(K, V)) return fail(GDN_ERR_SHAPE, "decode step not compiled for K=%d V=%d", K, V);
+  if (B == 0 || H == 0) return GDN_OK;
+  if (!q || !k || !v || !g || !beta || !state || !o) return fail(GDN_ERR_ARG, "null input/output pointer");
+  StepArgs a{q, k, v, g, beta, state, o, B, H, K, V, scale, dtype, static_cast<hipStream_t>(stream)};
+  const hipError_t e = launch_step(a);
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "decode step launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+}  // extern "C"

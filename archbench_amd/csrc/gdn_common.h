@@ -1,0 +1,131 @@
+// Shared device helpers for the gated DeltaNet kernels (gfx950 / CDNA4).
+//
+// Matrix products use the 16x16 MFMA output tile.  Operand fragments always hold 8 consecutive k values per
+// lane: lane l covers outer index (l & 15) and k = 8*(l >> 4) + j, j = 0..7.  For bf16 one
+// v_mfma_f32_16x16x32_bf16 consumes the fragment pair; for fp32 eight v_mfma_f32_16x16x4_f32 issue one k
+// slice each (slice j takes k = 8*g + j from lane group g), which is the same sum over k in another order.
+// The fp32 accumulator of a 16x16 tile holds rows 4*(l >> 4) + i (i = 0..3) of column (l & 15).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gdn {
+
+constexpr int CH = 64;         // tokens per chunk
+constexpr int NWAVE = 4;       // waves per workgroup
+constexpr int NTHR = 64 * NWAVE;
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+template <typename T> struct Frag;
+template <> struct Frag<bf16> { using type = bf16x8; };
+template <> struct Frag<float> { using type = f32x8; };
+
+// LDS row padding (elements) so that rows of a tile start on different banks.
+template <typename T> struct Pad { static constexpr int v = 16 / sizeof(T) * 1; };
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+__device__ __forceinline__ float to_f(float x) { return x; }
+__device__ __forceinline__ float to_f(bf16 x) { return static_cast<float>(x); }
+template <typename T> __device__ __forceinline__ T from_f(float x);
+template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f<bf16>(float x) { return static_cast<bf16>(x); }
+
+__device__ __forceinline__ void mma(f32x4& c, const bf16x8& a, const bf16x8& b) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f32x4& c, const f32x8& a, const f32x8& b) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], c, 0, 0, 0);
+}
+
+// Fragment with k contiguous: element (o, k) at p[o * ld + k].
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::type frag_kc(const T* p, int ld, int o0, int k0) {
+  const int l = lane_id();
+  const T* s = p + (o0 + (l & 15)) * ld + k0 + 8 * (l >> 4);
+  if constexpr (sizeof(T) == 2) {
+    return *reinterpret_cast<const bf16x8*>(s);
+  } else {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(s);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(s + 4);
+    return f32x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  }
+}
+
+// Fragment with the outer index contiguous: element (o, k) at p[k * ld + o].
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::type frag_oc(const T* p, int ld, int o0, int k0) {
+  const int l = lane_id();
+  const T* s = p + (k0 + 8 * (l >> 4)) * ld + o0 + (l & 15);
+  typename Frag<T>::type f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = s[j * ld];
+  return f;
+}
+
+template <bool KC, typename T>
+__device__ __forceinline__ typename Frag<T>::type frag(const T* p, int ld, int o0, int k0) {
+  if constexpr (KC) return frag_kc(p, ld, o0, k0);
+  else return frag_oc(p, ld, o0, k0);
+}
+
+// c += A[m0:m0+16, 0:KD] * B[0:KD, n0:n0+16].
+//   A element (m, k): AKC ? A[m*lda + k] : A[k*lda + m]
+//   B element (k, n): BKC ? B[n*ldb + k] : B[k*ldb + n]
+template <bool AKC, bool BKC, int KD, typename T>
+__device__ __forceinline__ void mma_blk(f32x4& c, const T* A, int lda, int m0, const T* B, int ldb, int n0) {
+#pragma unroll
+  for (int k0 = 0; k0 < KD; k0 += 32) {
+    const auto a = frag<AKC>(A, lda, m0, k0);
+    const auto b = frag<BKC>(B, ldb, n0, k0);
+    mma(c, a, b);
+  }
+}
+
+__device__ __forceinline__ int acc_row(int i) { return 4 * (lane_id() >> 4) + i; }
+__device__ __forceinline__ int acc_col() { return lane_id() & 15; }
+
+// Sum over the 16 lanes that share a lane group (the columns of one accumulator tile row set).
+__device__ __forceinline__ float sum16(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 8);
+  return x;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_inclusive_scan(float x) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float y = __shfl_up(x, o);
+    if (l >= o) x += y;
+  }
+  return x;
+}
+
+// Copy a rows x cols tile of T from global (row stride gld elements) into LDS (row stride sld), 16-byte
+// vectors, zero-filling rows >= valid_rows.  cols * sizeof(T) must be a multiple of 16.
+template <typename T>
+__device__ __forceinline__ void g2s_rows(T* s, int sld, const T* g, int64_t gld, int rows, int cols,
+                                         int valid_rows) {
+  constexpr int E = 16 / sizeof(T);
+  const int vpr = cols / E;
+  for (int idx = threadIdx.x; idx < rows * vpr; idx += blockDim.x) {
+    const int r = idx / vpr, c = (idx - r * vpr) * E;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (r < valid_rows) val = *reinterpret_cast<const uint4*>(g + r * gld + c);
+    *reinterpret_cast<uint4*>(s + r * sld + c) = val;
+  }
+}
+
+}  // namespace gdn

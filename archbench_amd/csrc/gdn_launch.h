@@ -1,0 +1,66 @@
+// Host-side launch interface between the C ABI (gdn_capi.hip) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace gdn {
+
+enum DType { DT_F32 = 0, DT_BF16 = 1 };
+
+constexpr int CH_TOKENS = 64;  // tokens per chunk (the kernels' CH)
+
+struct StepArgs {
+  const void *q, *k, *v;
+  const float *g, *beta;
+  float* state;
+  void* o;
+  int B, H, K, V;
+  float scale;
+  int dtype;
+  hipStream_t stream;
+};
+
+// Chunk workspace carve-up (chunk-major: [B*H][NT][...]).  All offsets are 256-byte aligned.
+struct ChunkWs {
+  void* Tm;   // [BH][NT][64][64]   (I + A)^-1 per chunk, input dtype
+  void* P;    // [BH][NT][64][64]   scale * (M o Q K^T), input dtype
+  void* W;    // [BH][NT][64][K]    Tm diag(beta gamma) K, input dtype
+  float* Gc;  // [BH][NT][64]       chunk-local cumulative log-decay
+  void* hs;   // [BH][NT][K][V]     state entering each chunk (backward only)
+  void* Rs;   // [BH][NT][64][V]    R = U - W S per chunk (backward only)
+  void* dhs;  // [BH][NT][K][V]     dL/d(state leaving each chunk) (backward only)
+  void* dRs;  // [BH][NT][64][V]    dL/dR per chunk (backward only)
+};
+
+struct ChunkArgs {
+  const void *q, *k, *v;
+  const float *g, *beta;
+  const float* h0;  // [B,H,K,V] or null
+  void* o;          // [B,T,H,V] (forward)
+  float* hT;        // [B,H,K,V] or null
+  // backward
+  const void* dout;   // [B,T,H,V]
+  const float* dhT;   // or null
+  void *dq, *dk, *dv;
+  float *dg, *dbeta;
+  float* dh0;  // or null
+  ChunkWs ws;
+  int B, T, H, K, V, NT;
+  float scale;
+  int dtype;
+  hipStream_t stream;
+};
+
+size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, bool backward, ChunkWs* carve, void* base);
+bool chunk_shape_supported(int K, int V, int dtype);
+bool step_shape_supported(int K, int V);
+
+hipError_t launch_step(const StepArgs& a);
+hipError_t launch_fwd_intra(const ChunkArgs& a);                 // Tm, P, W, Gc
+hipError_t launch_fwd_state(const ChunkArgs& a, bool backward);  // o/hT (forward) or hs/Rs (backward)
+hipError_t launch_bwd_state(const ChunkArgs& a);                 // dhs, dRs, dh0
+hipError_t launch_bwd_intra(const ChunkArgs& a);                 // dq, dk, dv, dg, dbeta
+
+}  // namespace gdn

@@ -1,0 +1,227 @@
+"""Gated DeltaNet operator API on the HIP C-ABI library.
+
+Operator level (the reference's own pattern, archbench/layers/nsgdn.py:162-216 and :352-397): functional
+``torch.library.custom_op`` ops with ``register_fake`` (so FakeTensor / ``torch.compile(dynamic=False)`` trace
+without running kernels) and ``register_autograd``; outputs are allocated here with ``torch.empty``; kernels are
+enqueued on the current stream.
+
+    archbench_amd::gdn_chunk_fwd      (q, k, v, g, beta, h0?, scale) -> (o, hT)
+    archbench_amd::gdn_chunk_bwd      (q, k, v, g, beta, h0?, do, dhT?, scale) -> (dq, dk, dv, dg, dbeta, dh0)
+    archbench_amd::gdn_recurrent_step (q, k, v, g, beta, state!, scale) -> o        (state updated in place)
+
+Python entry points with fla's signatures (the arithmetic behind archbench's ``gdn`` mixer,
+archbench/layers/fla.py:36-38):
+
+    chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=False,
+                           use_qk_l2norm_in_kernel=False) -> (o, final_state | None)
+    fused_recurrent_gated_delta_rule(...)  -> (o, final_state | None)      (decode; T = 1 uses the step kernel)
+    recurrent_step(q, k, v, g, beta, state, scale=None) -> o               (in-place decode step)
+
+There is no CPU path and no alternative backend: tensors must live on a ROCm GPU and the library must be built.
+Shape/dtype problems raise ValueError (as the reference's layer does, nsgdn.py:492-497); a missing library or
+a launch failure raises RuntimeError.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import _lib
+
+__all__ = ["chunk_gated_delta_rule", "fused_recurrent_gated_delta_rule", "recurrent_step", "chunk_fwd",
+           "chunk_bwd"]
+
+
+def _require_gpu(*ts: Optional[Tensor]) -> None:
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("the gated DeltaNet op runs only on a ROCm GPU (MI355X); got a tensor on "
+                               f"{t.device}. There is no CPU fallback.")
+
+
+def _shapes(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, h0: Optional[Tensor]):
+    if q.dim() != 4 or k.shape != q.shape:
+        raise ValueError(f"q and k must be [B, T, H, K] with equal shapes, got {tuple(q.shape)} and {tuple(k.shape)}")
+    B, T, H, K = q.shape
+    if v.dim() != 4 or tuple(v.shape[:3]) != (B, T, H):
+        raise ValueError(f"v must be [B, T, H, V] matching q's [B, T, H] = {(B, T, H)}, got {tuple(v.shape)}")
+    V = v.shape[-1]
+    if tuple(g.shape) != (B, T, H) or tuple(beta.shape) != (B, T, H):
+        raise ValueError(f"g and beta must be [B, T, H] = {(B, T, H)}, got {tuple(g.shape)} and {tuple(beta.shape)}")
+    if h0 is not None and tuple(h0.shape) != (B, H, K, V):
+        raise ValueError(f"initial_state must be [B, H, K, V] = {(B, H, K, V)}, got {tuple(h0.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"q, k, v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+    return B, T, H, K, V
+
+
+# ------------------------------------------------------------------------------------------------ chunk forward
+@torch.library.custom_op("archbench_amd::gdn_chunk_fwd", mutates_args=())
+def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, h0: Optional[Tensor],
+              scale: float) -> tuple[Tensor, Tensor]:
+    _require_gpu(q, k, v, g, beta, h0)
+    B, T, H, K, V = _shapes(q, k, v, g, beta, h0)
+    lib = _lib.load()
+    dt = _lib.dtype_code(q.dtype)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    g, beta = g.float().contiguous(), beta.float().contiguous()
+    h0 = None if h0 is None else h0.float().contiguous()
+    o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
+    hT = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
+    ws = torch.empty(_lib.ws_bytes("fwd", B, T, H, K, V, q.dtype), dtype=torch.uint8, device=q.device)
+    rc = lib.gdn_chunk_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta), _lib.ptr(h0),
+                           _lib.ptr(o), _lib.ptr(hT), _lib.ptr(ws), ws.numel(), B, T, H, K, V, float(scale), dt,
+                           _lib.stream_ptr(q.device))
+    _lib.check(rc, "gdn_chunk_fwd")
+    return o, hT
+
+
+@chunk_fwd.register_fake
+def _(q, k, v, g, beta, h0, scale):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    return q.new_empty(B, T, H, V), q.new_empty(B, H, K, V, dtype=torch.float32)
+
+
+# ----------------------------------------------------------------------------------------------- chunk backward
+@torch.library.custom_op("archbench_amd::gdn_chunk_bwd", mutates_args=())
+def chunk_bwd(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, h0: Optional[Tensor], do: Tensor,
+              dhT: Optional[Tensor], scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    _require_gpu(q, k, v, g, beta, h0, do, dhT)
+    B, T, H, K, V = _shapes(q, k, v, g, beta, h0)
+    if tuple(do.shape) != (B, T, H, V):
+        raise ValueError(f"dO must be [B, T, H, V] = {(B, T, H, V)}, got {tuple(do.shape)}")
+    lib = _lib.load()
+    dt = _lib.dtype_code(q.dtype)
+    q, k, v, do = q.contiguous(), k.contiguous(), v.contiguous(), do.to(q.dtype).contiguous()
+    g, beta = g.float().contiguous(), beta.float().contiguous()
+    h0 = None if h0 is None else h0.float().contiguous()
+    dhT = None if dhT is None else dhT.float().contiguous()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dg = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
+    db = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
+    dh0 = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
+    ws = torch.empty(_lib.ws_bytes("bwd", B, T, H, K, V, q.dtype), dtype=torch.uint8, device=q.device)
+    rc = lib.gdn_chunk_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta), _lib.ptr(h0),
+                           _lib.ptr(do), _lib.ptr(dhT), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg),
+                           _lib.ptr(db), _lib.ptr(dh0), _lib.ptr(ws), ws.numel(), B, T, H, K, V, float(scale), dt,
+                           _lib.stream_ptr(q.device))
+    _lib.check(rc, "gdn_chunk_bwd")
+    return dq, dk, dv, dg, db, dh0
+
+
+@chunk_bwd.register_fake
+def _(q, k, v, g, beta, h0, do, dhT, scale):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    f32 = dict(dtype=torch.float32)
+    return (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), q.new_empty(B, T, H, **f32),
+            q.new_empty(B, T, H, **f32), q.new_empty(B, H, K, V, **f32))
+
+
+def _chunk_setup(ctx, inputs, output):
+    q, k, v, g, beta, h0, scale = inputs
+    ctx.save_for_backward(q, k, v, g, beta, h0)
+    ctx.scale = scale
+    ctx.has_h0 = h0 is not None
+    ctx.g_dtype, ctx.beta_dtype = g.dtype, beta.dtype
+
+
+def _chunk_backward(ctx, do, dhT):
+    q, k, v, g, beta, h0 = ctx.saved_tensors
+    dq, dk, dv, dg, db, dh0 = chunk_bwd(q, k, v, g, beta, h0, do.contiguous(),
+                                        None if dhT is None else dhT.contiguous(), ctx.scale)
+    return dq, dk, dv, dg.to(ctx.g_dtype), db.to(ctx.beta_dtype), (dh0 if ctx.has_h0 else None), None
+
+
+chunk_fwd.register_autograd(_chunk_backward, setup_context=_chunk_setup)
+
+
+# ------------------------------------------------------------------------------------------------- decode step
+@torch.library.custom_op("archbench_amd::gdn_recurrent_step", mutates_args=("state",))
+def _recurrent_step(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, state: Tensor,
+                    scale: float) -> Tensor:
+    _require_gpu(q, k, v, g, beta, state)
+    if q.dim() != 3 or k.shape != q.shape or v.dim() != 3 or tuple(v.shape[:2]) != tuple(q.shape[:2]):
+        raise ValueError(f"decode step takes q, k [B, H, K] and v [B, H, V], got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
+    B, H, K = q.shape
+    V = v.shape[-1]
+    if tuple(g.shape) != (B, H) or tuple(beta.shape) != (B, H):
+        raise ValueError(f"g and beta must be [B, H] = {(B, H)}")
+    if tuple(state.shape) != (B, H, K, V) or state.dtype != torch.float32 or not state.is_contiguous():
+        raise ValueError(f"state must be a contiguous fp32 [B, H, K, V] = {(B, H, K, V)} tensor")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k, v must share a dtype")
+    lib = _lib.load()
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    g, beta = g.float().contiguous(), beta.float().contiguous()
+    o = torch.empty(B, H, V, dtype=q.dtype, device=q.device)
+    rc = lib.gdn_recurrent_step(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
+                                _lib.ptr(state), _lib.ptr(o), B, H, K, V, float(scale), _lib.dtype_code(q.dtype),
+                                _lib.stream_ptr(q.device))
+    _lib.check(rc, "gdn_recurrent_step")
+    return o
+
+
+@_recurrent_step.register_fake
+def _(q, k, v, g, beta, state, scale):
+    B, H, _ = q.shape
+    return q.new_empty(B, H, v.shape[-1])
+
+
+# ----------------------------------------------------------------------------------------------- public API
+def _l2norm(x: Tensor) -> Tensor:
+    return F.normalize(x.float(), dim=-1).to(x.dtype)
+
+
+def chunk_gated_delta_rule(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, scale: float | None = None,
+                           initial_state: Tensor | None = None, output_final_state: bool = False,
+                           use_qk_l2norm_in_kernel: bool = False, cu_seqlens: Tensor | None = None,
+                           head_first: bool = False):
+    """fla-compatible chunkwise gated delta rule: returns (o [B,T,H,V], final_state [B,H,K,V] fp32 or None).
+
+    q, k [B,T,H,K]; v [B,T,H,V] (bf16 or fp32, shared dtype); g (natural-log decay) and beta [B,T,H];
+    scale defaults to K**-0.5 (fla's default); differentiable w.r.t. q, k, v, g, beta and initial_state.
+    """
+    if head_first:
+        raise ValueError("head_first=True layouts are not supported; pass [B, T, H, *] tensors")
+    if cu_seqlens is not None:
+        raise ValueError("variable-length packing (cu_seqlens) is not supported")
+    if use_qk_l2norm_in_kernel:
+        q, k = _l2norm(q), _l2norm(k)
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    o, hT = chunk_fwd(q, k, v, g, beta, initial_state, float(scale))
+    return o, (hT if output_final_state else None)
+
+
+def recurrent_step(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, state: Tensor,
+                   scale: float | None = None) -> Tensor:
+    """One decode step on [B,H,*] inputs; ``state`` (fp32 [B,H,K,V]) is updated in place; returns o [B,H,V]."""
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    return _recurrent_step(q, k, v, g, beta, state, float(scale))
+
+
+def fused_recurrent_gated_delta_rule(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
+                                     scale: float | None = None, initial_state: Tensor | None = None,
+                                     output_final_state: bool = False, use_qk_l2norm_in_kernel: bool = False):
+    """fla-compatible recurrent entry point.  T = 1 (decode) runs the single-token step kernel on a copy of the
+    state; longer inputs run the chunk kernels, which compute the same recurrence."""
+    if use_qk_l2norm_in_kernel:
+        q, k = _l2norm(q), _l2norm(k)
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    if T == 1 and not torch.is_grad_enabled():
+        state = (torch.zeros(B, H, K, V, dtype=torch.float32, device=q.device) if initial_state is None
+                 else initial_state.float().clone().contiguous())
+        o = _recurrent_step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], beta[:, 0], state, float(scale))
+        return o[:, None], (state if output_final_state else None)
+    return chunk_gated_delta_rule(q, k, v, g, beta, scale, initial_state, output_final_state)

@@ -1,0 +1,81 @@
+/* C ABI of the MI355X-native gated DeltaNet (GDN) token-mixing op.
+ *
+ * Plain pointers and sizes only: no torch or HIP C++ types cross this boundary.  All device pointers are
+ * device memory owned by the caller (in practice torch's caching allocator); the library allocates nothing,
+ * frees nothing and never synchronises the host.  Every call enqueues its kernels on `stream` (a hipStream_t
+ * passed as void*; NULL is the default stream) and returns immediately.
+ *
+ * Layouts (row-major, contiguous):
+ *   q, k  [B, T, H, K]      v, o, dout  [B, T, H, V]       (token-major, "head_first = False")
+ *   g, beta [B, T, H] fp32  (g = natural-log decay, beta = write strength)
+ *   states h0, hT, dh0, dhT, decode state  [B, H, K, V] fp32
+ * dtype selects the element type of q, k, v, o, dout, dq, dk, dv: GDN_DTYPE_F32 or GDN_DTYPE_BF16.
+ * Gradients dg, dbeta are fp32.
+ *
+ * Return value: GDN_OK, or a GDN_ERR_* code with a message available from gdn_last_error() (thread-local).
+ */
+#ifndef GDN_MI355X_H
+#define GDN_MI355X_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN_OK 0
+#define GDN_ERR_ARG 1       /* null pointer, negative size, bad dtype code */
+#define GDN_ERR_SHAPE 2     /* (K, V, dtype) combination not compiled in */
+#define GDN_ERR_WORKSPACE 3 /* workspace missing or smaller than the *_ws_bytes query */
+#define GDN_ERR_LAUNCH 4    /* HIP reported an error while enqueueing */
+
+#define GDN_DTYPE_F32 0
+#define GDN_DTYPE_BF16 1
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int gdn_version(void);
+
+/* Message for the last error raised on the calling thread ("" if none). */
+const char* gdn_last_error(void);
+
+/* 1 if the chunk (op = 0) or decode-step (op = 1) kernels are compiled for (K, V, dtype), else 0. */
+int gdn_supported(int op, int K, int V, int dtype);
+
+/* Workspace sizes (bytes) for gdn_chunk_fwd / gdn_chunk_bwd.  The buffers the reference allocates inside
+ * its ops with torch.empty (archbench/layers/nsgdn.py:172-173, :194-197, :335, :343) are carved from this
+ * caller-owned block instead. */
+int gdn_chunk_fwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t* bytes);
+int gdn_chunk_bwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t* bytes);
+
+/* Chunkwise forward: o = GDN(q, k, v, g, beta; h0), optional final state hT.
+ * Replaces archbench::nsgdn_chunk_fwd (archbench/layers/nsgdn.py:352-363) for the plain-GDN write vector
+ * u = beta k (nsgdn.py:69), i.e. the forward of fla's chunk_gated_delta_rule behind the `gdn` mixer
+ * (archbench/layers/fla.py:36-38).  h0 and hT may be NULL (zero initial state / no final state).
+ * Any T >= 0 (ragged last chunk handled in-kernel; the reference falls back to DPLR when T % 64 != 0,
+ * nsgdn.py:402-403). */
+int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                  const float* h0, void* o, float* hT, void* ws, size_t ws_bytes, int B, int T, int H, int K,
+                  int V, float scale, int dtype, void* stream);
+
+/* Chunkwise backward: dq, dk, dv, dg, dbeta (and dh0 if non-NULL) for upstream gradients dout and dhT
+ * (dhT may be NULL).  Recomputes the chunk factors and chunk states instead of storing them in the forward.
+ * Replaces archbench::nsgdn_chunk_bwd (archbench/layers/nsgdn.py:369-382) with the chain rule through
+ * u = beta k (nsgdn.py:69) folded in, i.e. the backward of fla's chunk_gated_delta_rule. */
+int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                  const float* h0, const void* dout, const float* dhT, void* dq, void* dk, void* dv, float* dg,
+                  float* dbeta, float* dh0, void* ws, size_t ws_bytes, int B, int T, int H, int K, int V,
+                  float scale, int dtype, void* stream);
+
+/* One recurrent decode step, state updated in place:
+ *   r = beta (v - e^g S^T k),  S <- e^g S + k r^T,  o = S^T (scale q)
+ * q, k [B, H, K], v, o [B, H, V], g, beta [B, H] fp32, state [B, H, K, V] fp32.
+ * The per-token body of the reference's token scan (archbench/layers/nsgdn.py:95-106 and nsgdn_ref,
+ * nsgdn.py:413-416), i.e. fla's fused_recurrent_gated_delta_rule at T = 1 with an in-place state. */
+int gdn_recurrent_step(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                       float* state, void* o, int B, int H, int K, int V, float scale, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_MI355X_H */

@@ -1,0 +1,70 @@
+"""The C-ABI library loads, exports every symbol include/gdn_mi355x.h declares, and its host-only entry points
+(version, support query, workspace sizing, argument validation) behave -- no GPU needed."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from archbench_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "gdn_mi355x.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(gdn_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    assert {"gdn_chunk_fwd", "gdn_chunk_bwd", "gdn_recurrent_step", "gdn_chunk_fwd_ws_bytes",
+            "gdn_chunk_bwd_ws_bytes", "gdn_last_error"} <= set(names)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert set(names) == set(_lib.SIGNATURES), "binding table out of sync with the header"
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_version_and_support_table():
+    lib = _lib.load()
+    assert lib.gdn_version() >= 100
+    assert _lib.supported("chunk", 128, 128, __import__("torch").bfloat16)
+    assert _lib.supported("chunk", 64, 64, __import__("torch").float32)
+    assert _lib.supported("step", 128, 128, __import__("torch").bfloat16)
+    assert not lib.gdn_supported(0, 96, 128, 1)
+    assert not lib.gdn_supported(7, 128, 128, 1)
+
+
+def test_workspace_sizes():
+    import torch
+    fwd = _lib.ws_bytes("fwd", 8, 4096, 16, 128, 128, torch.bfloat16)
+    bwd = _lib.ws_bytes("bwd", 8, 4096, 16, 128, 128, torch.bfloat16)
+    BH, NT = 8 * 16, 64
+    # Tm, P: 64x64; W: 64xK; G: 64 fp32 per chunk
+    assert fwd == BH * NT * (64 * 64 * 2 * 2 + 64 * 128 * 2 + 64 * 4)
+    # + states entering/leaving (K x V) and R, dR (64 x V) per chunk
+    assert bwd == fwd + BH * NT * (2 * 128 * 128 * 2 + 2 * 64 * 128 * 2)
+    # ragged T rounds up to whole chunks
+    assert _lib.ws_bytes("fwd", 1, 65, 1, 64, 64, torch.float32) == 2 * _lib.ws_bytes("fwd", 1, 64, 1, 64, 64,
+                                                                                        torch.float32)
+
+
+def test_argument_errors_do_not_touch_the_gpu():
+    lib = _lib.load()
+    n = ctypes.c_size_t(0)
+    assert lib.gdn_chunk_fwd_ws_bytes(1, 64, 1, 64, 64, 5, ctypes.byref(n)) == _lib.GDN_ERR_ARG
+    assert b"dtype" in lib.gdn_last_error()
+    assert lib.gdn_chunk_fwd_ws_bytes(-1, 64, 1, 64, 64, 1, ctypes.byref(n)) == _lib.GDN_ERR_ARG
+    rc = lib.gdn_chunk_fwd(None, None, None, None, None, None, None, None, None, 0, 1, 64, 1, 96, 64, 1.0, 1, None)
+    assert rc == _lib.GDN_ERR_SHAPE
+    rc = lib.gdn_chunk_fwd(None, None, None, None, None, None, None, None, None, 0, 1, 64, 1, 64, 64, 1.0, 1, None)
+    assert rc == _lib.GDN_ERR_ARG  # null pointers rejected before any launch
+    with pytest.raises(ValueError):
+        _lib.check(_lib.GDN_ERR_SHAPE, "x")
