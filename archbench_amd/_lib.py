@@ -32,7 +32,11 @@ SIGNATURES = {
     "gdn_chunk_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz,
                            _i, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_recurrent_step": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i, _p]),
+    "gdn_profile_enable": (_i, [_i]),
+    "gdn_profile_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
+    "gdn_profile_stage_name": (ctypes.c_char_p, [_i]),
 }
+PROFILE_STAGES = 7
 
 _lock = threading.Lock()
 _lib = None
@@ -95,3 +99,26 @@ def ws_bytes(kind: str, B: int, T: int, H: int, K: int, V: int, dtype: torch.dty
     fn = load().gdn_chunk_fwd_ws_bytes if kind == "fwd" else load().gdn_chunk_bwd_ws_bytes
     check(fn(B, T, H, K, V, dtype_code(dtype), ctypes.byref(out)), f"gdn_chunk_{kind}_ws_bytes")
     return out.value
+
+
+class StageTimer:
+    """Per-kernel-stage timing with events recorded by the library on the launch stream.
+
+        with StageTimer() as st:
+            ...  # gdn calls
+        st.result  # {stage_name: (total_ms, launches)}
+    """
+
+    def __enter__(self):
+        load().gdn_profile_enable(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib = load()
+        ms = (ctypes.c_double * PROFILE_STAGES)()
+        n = (_i * PROFILE_STAGES)()
+        rc = lib.gdn_profile_read(ms, n, PROFILE_STAGES)
+        lib.gdn_profile_enable(0)
+        check(rc, "gdn_profile_read")
+        self.result = {lib.gdn_profile_stage_name(i).decode(): (ms[i], n[i]) for i in range(PROFILE_STAGES) if n[i]}
+        return False

@@ -66,6 +66,44 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
   return hipGetLastError();
 }
 
+
+// ---- per-stage event timing (diagnostic; off unless gdn_profile_enable(1) was called on this thread) ----
+enum Stage { ST_FWD_INTRA = 0, ST_FWD_STATE, ST_BWD_RECOMP_INTRA, ST_BWD_RECOMP_STATE, ST_BWD_STATE, ST_BWD_INTRA,
+             ST_STEP, ST_COUNT };
+static const char* kStageNames[ST_COUNT] = {"fwd_intra", "fwd_state", "bwd_recompute_intra",
+                                            "bwd_recompute_state", "bwd_state", "bwd_intra", "step"};
+struct ProfRec { int stage; hipEvent_t a, b; };
+struct Prof {
+  bool on = false;
+  ProfRec rec[4096];
+  int n = 0;
+  hipEvent_t pool[8192];
+  int pool_n = 0, pool_used = 0;
+};
+static thread_local Prof g_prof;
+
+static hipEvent_t prof_event() {
+  if (g_prof.pool_used < g_prof.pool_n) return g_prof.pool[g_prof.pool_used++];
+  hipEvent_t e = nullptr;
+  if (g_prof.pool_n < 8192 && hipEventCreate(&e) == hipSuccess) {
+    g_prof.pool[g_prof.pool_n++] = e;
+    g_prof.pool_used++;
+  }
+  return e;
+}
+
+// Runs `launch` and, when profiling is on, brackets it with events on `st`.
+template <typename F>
+static hipError_t timed(int stage, hipStream_t st, F&& launch) {
+  if (!g_prof.on || g_prof.n >= 4096) return launch();
+  ProfRec r{stage, prof_event(), prof_event()};
+  if (r.a) (void)hipEventRecord(r.a, st);
+  const hipError_t e = launch();
+  if (r.b) (void)hipEventRecord(r.b, st);
+  if (r.a && r.b) g_prof.rec[g_prof.n++] = r;
+  return e;
+}
+
 static int check_common(int B, int T, int H, int K, int V, int dtype) {
   if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
   if (B < 0 || T < 0 || H < 0 || K <= 0 || V <= 0)
@@ -82,6 +120,37 @@ using namespace gdn;
 extern "C" {
 
 int gdn_version(void) { return 100; }
+
+int gdn_profile_enable(int on) {
+  g_prof.on = on != 0;
+  g_prof.n = 0;
+  g_prof.pool_used = 0;
+  return GDN_OK;
+}
+
+int gdn_profile_read(double* ms_sum, int* launches, int n_stages) {
+  g_err[0] = 0;
+  if (!ms_sum || !launches || n_stages < ST_COUNT) return fail(GDN_ERR_ARG, "need arrays of %d stages", ST_COUNT);
+  for (int i = 0; i < n_stages; ++i) {
+    ms_sum[i] = 0.0;
+    launches[i] = 0;
+  }
+  for (int i = 0; i < g_prof.n; ++i) {
+    const ProfRec& r = g_prof.rec[i];
+    if (hipEventSynchronize(r.b) != hipSuccess) return fail(GDN_ERR_LAUNCH, "event synchronize failed");
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) return fail(GDN_ERR_LAUNCH, "event elapsed failed");
+    ms_sum[r.stage] += ms;
+    launches[r.stage] += 1;
+  }
+  g_prof.n = 0;
+  g_prof.pool_used = 0;
+  return GDN_OK;
+}
+
+const char* gdn_profile_stage_name(int stage) {
+  return (stage >= 0 && stage < ST_COUNT) ? kStageNames[stage] : "";
+}
 
 const char* gdn_last_error(void) { return g_err; }
 
@@ -129,8 +198,8 @@ int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g, c
   a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.h0 = h0; a.o = o; a.hT = hT;
   a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
-  hipError_t e = launch_fwd_intra(a);
-  if (e == hipSuccess) e = launch_fwd_state(a, false);
+  hipError_t e = timed(ST_FWD_INTRA, st, [&] { return launch_fwd_intra(a); });
+  if (e == hipSuccess) e = timed(ST_FWD_STATE, st, [&] { return launch_fwd_state(a, false); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "chunk forward launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }
@@ -160,10 +229,10 @@ int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, c
   a.dout = dout; a.dhT = dhT; a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dh0 = dh0;
   a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
-  hipError_t e = launch_fwd_intra(a);
-  if (e == hipSuccess) e = launch_fwd_state(a, true);
-  if (e == hipSuccess) e = launch_bwd_state(a);
-  if (e == hipSuccess) e = launch_bwd_intra(a);
+  hipError_t e = timed(ST_BWD_RECOMP_INTRA, st, [&] { return launch_fwd_intra(a); });
+  if (e == hipSuccess) e = timed(ST_BWD_RECOMP_STATE, st, [&] { return launch_fwd_state(a, true); });
+  if (e == hipSuccess) e = timed(ST_BWD_STATE, st, [&] { return launch_bwd_state(a); });
+  if (e == hipSuccess) e = timed(ST_BWD_INTRA, st, [&] { return launch_bwd_intra(a); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "chunk backward launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }
@@ -176,7 +245,7 @@ int gdn_recurrent_step(const void* q, const void* k, const void* v, const float*
   if (B == 0 || H == 0) return GDN_OK;
   if (!q || !k || !v || !g || !beta || !state || !o) return fail(GDN_ERR_ARG, "null input/output pointer");
   StepArgs a{q, k, v, g, beta, state, o, B, H, K, V, scale, dtype, static_cast<hipStream_t>(stream)};
-  const hipError_t e = launch_step(a);
+  const hipError_t e = timed(ST_STEP, a.stream, [&] { return launch_step(a); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "decode step launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }

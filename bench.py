@@ -1,0 +1,203 @@
+#!/usr/bin/env python3
+"""Gated DeltaNet benchmark on one MI355X.
+
+Headline (one JSON line on stdout): chunk forward + backward of the GDN op at B=8, T=4096, H=16, K=V=128, bf16
+inputs with fp32 state/accumulation, synthetic seeded data resident in HBM.  One step = one forward call and
+one backward call of the op (every gradient: dq, dk, dv, dg, dbeta).  tokens/s = B*T / step time.
+
+Also reported in the same line:
+  roofline      the dominant kernel of the step: algorithmic dense-MFMA FLOPs per launch over its average
+                duration (HIP events on the launch stream), against the bf16 dense MFMA peak;
+  mfma_frac     the whole step at the workload's algorithmic count 3 * F_fwd per token-head,
+                F_fwd = 2C(3K + 2V) + 6KV (C = 64);
+  fwd_only      forward alone at B=8, T=2048, H=8, K=V=128 (% of the bf16 MFMA peak);
+  decode_step   one recurrent decode step at B=256, H=16, K=V=128 with the fp32 state updated in place
+                (HBM GB/s against 8 TB/s);
+  cpu_baseline  the CPU oracle (fp32 token recurrence + exact reverse-time backward) timed on this host's
+                cores on the full headline shape (about 20 s of CPU work at ~2e3 tokens/s on 16 threads).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+MFMA_BF16_PEAK = 2.5e15  # MI355X dense bf16 MFMA, FLOP/s
+HBM_PEAK = 8.0e12        # MI355X HBM3E, B/s
+C = 64
+METRIC = "gated-DeltaNet fwd+bwd tokens/s (H16,d128,T4096) + % bf16 MFMA peak"
+
+
+def f_fwd(K: int, V: int) -> int:
+    """Algorithmic dense FLOPs per token-head of the chunk forward (the workload's counting convention)."""
+    return 2 * C * (3 * K + 2 * V) + 6 * K * V
+
+
+def stage_flops(stage: str, K: int, V: int) -> int:
+    """Dense MFMA FLOPs per token-head that each kernel stage executes (C = 64 tokens per chunk)."""
+    return {
+        "fwd_intra": 6 * C * K,                       # K K^T, Q K^T, W = Tm X
+        "fwd_state": 4 * C * V + 6 * K * V,           # U, P R; W S, Q S, Kd^T R
+        "bwd_recompute_intra": 6 * C * K,
+        "bwd_recompute_state": 2 * C * V + 4 * K * V,  # U; W S, Kd^T R
+        "bwd_state": 2 * C * V + 6 * K * V,           # P^T dO; Kd dS, Qg^T dO, W^T dR
+        "bwd_intra": 6 * C * V + 6 * K * V + 16 * C * K + 4 * C * C,
+    }.get(stage, 0)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def timed_loop(fn, steps: int, warmup: int, torch) -> float:
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(T: int) -> dict:
+    """The oracle on this host's cores (kind 'port'): bounded sample of the headline shape."""
+    import torch
+
+    from archbench_amd.synthetic import make_inputs
+    from oracle import gdn_oracle as O
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    B, H, K, V = 8, 16, 128, 128
+    x = make_inputs(B, T, H, K, V, seed=0, with_do=True)
+    t0 = time.perf_counter()
+    O.recurrent_fwd(x.q, x.k, x.v, x.g, x.beta, 1.0, None, dtype=torch.float32)
+    O.recurrent_bwd(x.q, x.k, x.v, x.g, x.beta, x.do, 1.0, None, None, ckpt=64, dtype=torch.float32)
+    dt = time.perf_counter() - t0
+    return {"value": round(B * T / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"B={B} T={T} H={H} K=V={K} fp32: token-recurrence forward + exact reverse-time backward "
+                      f"(checkpoint every 64 tokens), {dt:.1f} s on {threads} threads of '{cpu_model()}'"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-sample-T", type=int, default=4096)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["all", "train", "fwd", "decode"], default="all",
+                    help="run one workload only (profiling runs); the JSON line needs 'all' or 'train'")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures a single GPU: the gated DeltaNet op shards over batch and heads with no "
+              "communication, and this build has no multi-GPU path. Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from archbench_amd import _lib, ops
+    from archbench_amd.synthetic import make_inputs, make_step_inputs
+
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    out: dict = {}
+
+    if args.only in ("all", "train"):
+        B, T, H, K, V = 8, 4096, 16, 128, 128
+        log(f"headline fwd+bwd B={B} T={T} H={H} K={K} V={V} bf16: generating inputs")
+        x = make_inputs(B, T, H, K, V, seed=0, with_do=True).to(dev, torch.bfloat16)
+
+        def step():
+            ops.chunk_fwd(x.q, x.k, x.v, x.g, x.beta, None, 1.0)
+            ops.chunk_bwd(x.q, x.k, x.v, x.g, x.beta, None, x.do, None, 1.0)
+
+        log(f"timing {args.steps} steps after {args.warmup} warmup")
+        sec = timed_loop(step, args.steps, args.warmup, torch)
+        tokens = B * T
+        with _lib.StageTimer() as st:
+            for _ in range(max(3, min(args.steps, 10))):
+                step()
+        stages = {k: (ms / n, n) for k, (ms, n) in st.result.items()}
+        dom = max(stages, key=lambda s: stages[s][0])
+        dom_ms = stages[dom][0]
+        dom_flops = stage_flops(dom, K, V) * B * T * H
+        achieved = dom_flops / (dom_ms * 1e-3)
+        call_flops = 3 * f_fwd(K, V) * B * T * H
+        out.update({
+            "metric": METRIC, "value": round(tokens / sec, 1), "unit": "tokens/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic",
+            "config": {"workload": "gdn_chunk_fwd_bwd", "B": B, "T": T, "H": H, "K": K, "V": V, "chunk": C,
+                       "scale": 1.0, "state": "fp32", "g_shift": 4.0},
+            "mfma_frac": round(call_flops / sec / MFMA_BF16_PEAK, 4),
+            "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved / 1e12, 2),
+                         "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                         "frac": round(achieved / MFMA_BF16_PEAK, 4), "traffic": None,
+                         "flops_per_launch": dom_flops, "avg_ms": round(dom_ms, 4)},
+            "stages_ms": {k: round(v[0], 4) for k, v in stages.items()},
+        })
+        log(f"fwd+bwd {sec * 1e3:.3f} ms/step, {tokens / sec:.3e} tokens/s; stages {out['stages_ms']}")
+        del x
+        torch.cuda.empty_cache()
+
+    if args.only in ("all", "fwd"):
+        B, T, H, K, V = 8, 2048, 8, 128, 128
+        log(f"forward only B={B} T={T} H={H} K={K} V={V} bf16")
+        x = make_inputs(B, T, H, K, V, seed=0).to(dev, torch.bfloat16)
+        sec = timed_loop(lambda: ops.chunk_fwd(x.q, x.k, x.v, x.g, x.beta, None, 1.0), args.steps, args.warmup,
+                         torch)
+        out["fwd_only"] = {"workload": "gdn_chunk_fwd", "B": B, "T": T, "H": H, "K": K, "V": V,
+                           "ms": round(sec * 1e3, 4), "tokens_per_s": round(B * T / sec, 1),
+                           "mfma_frac": round(f_fwd(K, V) * B * T * H / sec / MFMA_BF16_PEAK, 4)}
+        log(f"fwd {sec * 1e3:.3f} ms")
+        del x
+        torch.cuda.empty_cache()
+
+    if args.only in ("all", "decode"):
+        B, H, K, V = 256, 16, 128, 128
+        log(f"decode step B={B} H={H} K={K} V={V} (fp32 state in place)")
+        q, k, v, g, b, S = make_step_inputs(B, H, K, V)
+        q, k, v = (t.to(dev, torch.bfloat16) for t in (q, k, v))
+        g, b, S = g.to(dev), b.to(dev), S.to(dev)
+        n_steps = max(args.steps, 50)
+        sec = timed_loop(lambda: ops.recurrent_step(q, k, v, g, b, S, 1.0), n_steps, args.warmup, torch)
+        with _lib.StageTimer() as st:
+            for _ in range(20):
+                ops.recurrent_step(q, k, v, g, b, S, 1.0)
+        kern_ms = st.result["step"][0] / st.result["step"][1]
+        nbytes = 2 * B * H * K * V * 4 + B * H * (2 * K + 2 * V) * 2 + B * H * 2 * 4
+        out["decode_step"] = {"workload": "gdn_recurrent_step", "B": B, "H": H, "K": K, "V": V,
+                              "us_per_step": round(sec * 1e6, 2), "kernel_us": round(kern_ms * 1e3, 2),
+                              "bytes_per_step": nbytes, "GB_per_s": round(nbytes / (kern_ms * 1e-3) / 1e9, 1),
+                              "hbm_frac": round(nbytes / (kern_ms * 1e-3) / HBM_PEAK, 4),
+                              "tokens_per_s": round(B / sec, 1)}
+        log(f"decode kernel {kern_ms * 1e3:.2f} us, {out['decode_step']['GB_per_s']} GB/s")
+
+    if args.only in ("all", "train") and not args.no_cpu_baseline:
+        log(f"cpu baseline (oracle, T={args.cpu_sample_T})")
+        out["cpu_baseline"] = cpu_baseline(args.cpu_sample_T)
+        log(f"cpu {out['cpu_baseline']['value']} tokens/s")
+
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

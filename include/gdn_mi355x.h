@@ -74,6 +74,16 @@ int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, c
 int gdn_recurrent_step(const void* q, const void* k, const void* v, const float* g, const float* beta,
                        float* state, void* o, int B, int H, int K, int V, float scale, int dtype, void* stream);
 
+/* Per-stage kernel timing (diagnostic; no counterpart in the reference, which times whole phases with CUDA
+ * events in archbench/logger.py:57-81).  While enabled on the calling thread, every kernel the calls above
+ * enqueue is bracketed by hipEvents on the same stream.  gdn_profile_read synchronises on those events and
+ * returns, per stage, the summed milliseconds and the number of launches (arrays of at least
+ * GDN_PROFILE_STAGES entries), then clears the record.  Stage names: gdn_profile_stage_name. */
+#define GDN_PROFILE_STAGES 7
+int gdn_profile_enable(int on);
+int gdn_profile_read(double* ms_sum, int* launches, int n_stages);
+const char* gdn_profile_stage_name(int stage);
+
 #ifdef __cplusplus
 }
 #endif
