@@ -33,11 +33,9 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, bool backwar
     return r;
   };
   ChunkWs ws{};
-  ws.Tm = take(BH * NT * CH_TOKENS * CH_TOKENS * es);
-  ws.P = take(BH * NT * CH_TOKENS * CH_TOKENS * es);
-  ws.W = take(BH * NT * CH_TOKENS * (size_t)K * es);
-  ws.Gc = static_cast<float*>(take(BH * NT * CH_TOKENS * 4));
   if (backward) {
+    ws.Tm = take(BH * NT * CH_TOKENS * CH_TOKENS * es);
+    ws.Gc = static_cast<float*>(take(BH * NT * CH_TOKENS * 4));
     ws.hs = take(BH * NT * (size_t)K * V * es);
     ws.Rs = take(BH * NT * CH_TOKENS * (size_t)V * es);
     ws.dhs = take(BH * NT * (size_t)K * V * es);
@@ -68,10 +66,8 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
 
 
 // ---- per-stage event timing (diagnostic; off unless gdn_profile_enable(1) was called on this thread) ----
-enum Stage { ST_FWD_INTRA = 0, ST_FWD_STATE, ST_BWD_RECOMP_INTRA, ST_BWD_RECOMP_STATE, ST_BWD_STATE, ST_BWD_INTRA,
-             ST_STEP, ST_COUNT };
-static const char* kStageNames[ST_COUNT] = {"fwd_intra", "fwd_state", "bwd_recompute_intra",
-                                            "bwd_recompute_state", "bwd_state", "bwd_intra", "step"};
+enum Stage { ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_COUNT };
+static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step"};
 struct ProfRec { int stage; hipEvent_t a, b; };
 struct Prof {
   bool on = false;
@@ -193,13 +189,12 @@ int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g, c
   if (!q || !k || !v || !g || !beta || !o) return fail(GDN_ERR_ARG, "null input/output pointer");
   ChunkArgs a{};
   const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, false, &a.ws, ws);
-  if (!ws || ws_bytes < need)
+  if (need && (!ws || ws_bytes < need))
     return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
   a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.h0 = h0; a.o = o; a.hT = hT;
   a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
-  hipError_t e = timed(ST_FWD_INTRA, st, [&] { return launch_fwd_intra(a); });
-  if (e == hipSuccess) e = timed(ST_FWD_STATE, st, [&] { return launch_fwd_state(a, false); });
+  const hipError_t e = timed(ST_FWD, st, [&] { return launch_fwd(a, false); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "chunk forward launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }
@@ -229,8 +224,7 @@ int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, c
   a.dout = dout; a.dhT = dhT; a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dh0 = dh0;
   a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
-  hipError_t e = timed(ST_BWD_RECOMP_INTRA, st, [&] { return launch_fwd_intra(a); });
-  if (e == hipSuccess) e = timed(ST_BWD_RECOMP_STATE, st, [&] { return launch_fwd_state(a, true); });
+  hipError_t e = timed(ST_BWD_RECOMP, st, [&] { return launch_fwd(a, true); });
   if (e == hipSuccess) e = timed(ST_BWD_STATE, st, [&] { return launch_bwd_state(a); });
   if (e == hipSuccess) e = timed(ST_BWD_INTRA, st, [&] { return launch_bwd_intra(a); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "chunk backward launch: %s", hipGetErrorString(e));

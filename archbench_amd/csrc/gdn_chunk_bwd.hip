@@ -1,11 +1,12 @@
 // Chunkwise gated delta rule, backward.
 //
-// The backward recomputes the chunk factors (fwd_intra) and the entering state of every chunk (fwd_state in
-// backward mode) rather than keeping them from the forward, then runs:
+// The backward recomputes the entering state of every chunk (the forward sweep in backward mode) rather than
+// keeping them from the forward, then runs:
 //
-// bwd_state: one workgroup per (V block, b*h), reverse over chunks, fp32 dS slab in MFMA accumulators.
+// bwd_state: one workgroup per (64-wide V block, b*h), reverse over chunks; per chunk it rebuilds the chunk
+//   factors on-chip (chunk_factors) and each wave carries a 16-column slab of dS in MFMA accumulators.
 //     dR  = P^T dO + Kd dS_C                         Kd = diag(exp(G_C - G)) K
-//     dS0 = gamma_C dS_C + s (diag(gamma) Q)^T dO - W^T dR
+//     dS0 = gamma_C dS_C + s (diag(gamma) Q)^T dO - W^T dR,   W^T dR = K^T diag(gamma) (TmB^T dR)
 //   Writes dS_C (the gradient w.r.t. the state leaving each chunk) and dR per chunk, and dh0.
 //   (The reverse state-gradient recurrence of fla's chunk_gated_delta_rule_bwd_dhu, called at
 //   archbench/layers/nsgdn.py:378.)
@@ -21,126 +22,151 @@
 //     dg  = reverse chunk-local cumsum of dG
 //   (fla's chunk_bwd_dv_local + chunk_bwd_dqkwg, the WY backward of nsgdn.py:279-330 and the reverse cumsum
 //   of nsgdn.py:381, fused per chunk.)  Reductions are deterministic: no atomics anywhere.
-#include "gdn_common.h"
+#include "gdn_chunk_common.h"
 #include "gdn_launch.h"
 
 namespace gdn {
 
 template <typename T, int K, int BV>
 __global__ __launch_bounds__(NTHR) void bwd_state_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ dout, const float* __restrict__ dhT,
-    float* __restrict__ dh0, const T* __restrict__ wsP, const T* __restrict__ wsW, const float* __restrict__ wsGc,
-    T* __restrict__ wsdH, T* __restrict__ wsdR, int T_, int H, int V, int NT, float scale) {
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ dout, const float* __restrict__ g,
+    const float* __restrict__ beta, const float* __restrict__ dhT, float* __restrict__ dh0, T* __restrict__ wsdH,
+    T* __restrict__ wsdR, int T_, int H, int V, int NT, float scale) {
   constexpr int PT = 16 / sizeof(T);
-  constexpr int LK = K + PT, LC = CH + PT;
-  constexpr int NCT = BV / 16;
-  constexpr int NST = (K / 16) * NCT;
-  constexpr int SPW = NST / NWAVE;
-  static_assert(NST % NWAVE == 0, "state slab must split evenly over the waves");
-  __shared__ __attribute__((aligned(16))) T sKd[CH * LK];
-  __shared__ __attribute__((aligned(16))) T sQgt[K * LC];
-  __shared__ __attribute__((aligned(16))) T sWt[K * LC];
-  __shared__ __attribute__((aligned(16))) T sPt[CH * LC];
-  __shared__ __attribute__((aligned(16))) T sdOt[BV * LC];
-  __shared__ __attribute__((aligned(16))) T sdSt[BV * LK];
-  __shared__ __attribute__((aligned(16))) T sdRt[BV * LC];
-  __shared__ float sG[CH];
+  constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT, LF = CH + 4;
+  constexpr int NKT = K / 16;
+  static_assert(BV / 16 / NWAVE == 1, "each wave owns one 16-column slab of dS");
+  constexpr int SCR_F = 2 * CH * LF;
+  static_assert(SCR_F * 4 >= K * LV * (int)sizeof(T), "staging must fit in the scratch region");
+  __shared__ __attribute__((aligned(16))) T sK[CH * LK];
+  __shared__ __attribute__((aligned(16))) T sQ[CH * LK];
+  __shared__ __attribute__((aligned(16))) T sdO[CH * LV];   // dO rows of this V block
+  __shared__ __attribute__((aligned(16))) T sP[CH * LC];
+  __shared__ __attribute__((aligned(16))) T sTmB[CH * LC];  // Tm diag(beta)
+  __shared__ __attribute__((aligned(16))) float sScr[SCR_F];
+  __shared__ float sG[CH], sB[CH], sGam[CH];
 
   const int vb = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh - b * H;
   const int v0 = vb * BV;
-  const int tid = threadIdx.x, w = wave_id();
+  const int w = wave_id(), l = lane_id();
+  const int c0 = 16 * w;
   const int64_t sbase = (int64_t)bh * K * V;
+  T* stage = reinterpret_cast<T*>(sScr);
 
-  f32x4 dS[SPW];
+  f32x4 dS[NKT];
 #pragma unroll
-  for (int s = 0; s < SPW; ++s) {
-    const int ti = w + NWAVE * s, mi = ti / NCT, ni = ti - mi * NCT;
+  for (int t = 0; t < NKT; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = 16 * mi + acc_row(i), vc = 16 * ni + acc_col();
-      dS[s][i] = dhT ? dhT[sbase + (int64_t)d * V + v0 + vc] : 0.f;
-    }
-  }
+    for (int i = 0; i < 4; ++i)
+      dS[t][i] = dhT ? dhT[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
+
+  RegTile<T, CH, K> rk, rq;
+  RegTile<T, CH, BV> rdo;
+  RegTok rt;
+  auto prefetch = [&](int c) {
+    const int t0 = c * CH, nvalid = min(CH, T_ - t0);
+    const int64_t row0 = ((int64_t)b * T_ + t0) * H + h;
+    rk.load(k + row0 * K, (int64_t)H * K, nvalid);
+    rq.load(q + row0 * K, (int64_t)H * K, nvalid);
+    rdo.load(dout + row0 * V + v0, (int64_t)H * V, nvalid);
+    if (w == 0) rt.load(g, beta, row0, H, nvalid);
+  };
+  prefetch(NT - 1);
 
   for (int c = NT - 1; c >= 0; --c) {
-    const int t0 = c * CH;
-    const int nvalid = min(CH, T_ - t0);
-    const int64_t row0 = ((int64_t)b * T_ + t0) * H + h;
     const int64_t cidx = (int64_t)bh * NT + c;
-    if (tid < CH) sG[tid] = wsGc[cidx * CH + tid];
-#pragma unroll
-    for (int s = 0; s < SPW; ++s) {
-      const int ti = w + NWAVE * s, mi = ti / NCT, ni = ti - mi * NCT;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = 16 * mi + acc_row(i), vc = 16 * ni + acc_col();
-        const T val = from_f<T>(dS[s][i]);
-        sdSt[vc * LK + d] = val;
-        wsdH[cidx * K * V + (int64_t)d * V + v0 + vc] = val;
-      }
-    }
-    {
-      const T* Wc = wsW + cidx * CH * K;
-      for (int idx = tid; idx < CH * K; idx += NTHR) {
-        const int i = idx / K, d = idx - i * K;
-        sWt[d * LC + i] = Wc[idx];
-      }
-      const T* Pc = wsP + cidx * CH * CH;
-      for (int idx = tid; idx < CH * CH; idx += NTHR) {
-        const int i = idx >> 6, j = idx & 63;
-        sPt[j * LC + i] = Pc[idx];
-      }
-      for (int idx = tid; idx < CH * BV; idx += NTHR) {
-        const int i = idx / BV, n = idx - i * BV;
-        sdOt[n * LC + i] = i < nvalid ? dout[(row0 + (int64_t)i * H) * V + v0 + n] : from_f<T>(0.f);
-      }
+    rk.store(sK, LK);
+    rq.store(sQ, LK);
+    rdo.store(sdO, LV);
+    if (w == 0) {
+      const float G = wave_inclusive_scan(rt.ok ? rt.g : 0.f);
+      sG[l] = G;
+      sB[l] = rt.ok ? rt.b : 0.f;
+      sGam[l] = __expf(G);
     }
     __syncthreads();
+    if (c > 0) prefetch(c - 1);
+    chunk_factors_start<T, K, 1>(sK, sQ, sG, sB, scale, sScr, sP);
+    // overlapped with the diagonal solve: K dS for this wave's columns
+    typename Frag<T>::type dSb[K / 32];
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
     const float GC = sG[CH - 1];
-    for (int idx = tid; idx < CH * K; idx += NTHR) {
-      const int j = idx / K, d = idx - j * K;
-      const float kv = j < nvalid ? to_f(k[(row0 + (int64_t)j * H) * K + d]) : 0.f;
-      const float qv = j < nvalid ? to_f(q[(row0 + (int64_t)j * H) * K + d]) : 0.f;
-      sKd[j * LK + d] = from_f<T>(__expf(GC - sG[j]) * kv);
-      sQgt[d * LC + j] = from_f<T>(__expf(sG[j]) * qv);
+    f32x4 dR[4];
+#pragma unroll
+    for (int rt_ = 0; rt_ < 4; ++rt_) {
+      f32x4 kd = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s) mma(kd, frag_kc_perm(sK, LK, 16 * rt_, 32 * s), dSb[s]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dR[rt_][i] = __expf(GC - sG[16 * rt_ + acc_row(i)]) * kd[i];
     }
-    __syncthreads();
+    // dO fragments of this wave's columns over the chunk's tokens: plain, and scaled by gamma
+    typename Frag<T>::type dOb[2], dOg[2];
 #pragma unroll
-    for (int n = 0; n < NCT; ++n) {
-      f32x4 dr = {0.f, 0.f, 0.f, 0.f};
-      mma_blk<true, true, CH>(dr, sPt, LC, 16 * w, sdOt, LC, 16 * n);
-      mma_blk<true, true, K>(dr, sKd, LK, 16 * w, sdSt, LK, 16 * n);
+    for (int ib = 0; ib < 2; ++ib) {
+      dOb[ib] = frag_oct(sdO, LV, c0, 32 * ib);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 16 * w + acc_row(i), vc = 16 * n + acc_col();
-        const T val = from_f<T>(dr[i]);
-        sdRt[vc * LC + r] = val;
-        wsdR[(cidx * CH + r) * V + v0 + vc] = val;
+      for (int e = 0; e < 8; ++e) dOg[ib][e] = from_f<T>(to_f(dOb[ib][e]) * sGam[32 * ib + 8 * (l >> 4) + e]);
+    }
+    chunk_factors_finish<T, 1>(sB, sScr, sTmB, nullptr);
+
+    // dS leaving this chunk -> global dh (bf16 [K][V] per chunk)
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) stage[(16 * t + acc_row(i)) * LV + c0 + acc_col()] = from_f<T>(dS[t][i]);
+    // dR = P^T dO + diag(exp(G_C - G)) K dS
+#pragma unroll
+    for (int rt_ = 0; rt_ < 4; ++rt_)
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) mma(dR[rt_], frag_oct(sP, LC, 16 * rt_, 32 * ib), dOb[ib]);
+    typename Frag<T>::type dRb[2];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) dRb[jb] = frag_acc2<T>(dR[2 * jb], dR[2 * jb + 1]);
+    // Z = TmB^T dR, scaled by gamma:  W^T dR = K^T (gamma Z)
+    typename Frag<T>::type Zb[2];
+    {
+      f32x4 Z[4];
+#pragma unroll
+      for (int rt_ = 0; rt_ < 4; ++rt_) {
+        Z[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) mma(Z[rt_], frag_oct_perm(sTmB, LC, 16 * rt_, 32 * jb), dRb[jb]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Z[rt_][i] *= sGam[16 * rt_ + acc_row(i)];
       }
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) Zb[jb] = frag_acc2<T>(Z[2 * jb], Z[2 * jb + 1]);
     }
+    __syncthreads();  // dh staging complete
+    s2g_rows(wsdH + cidx * K * V + v0, (int64_t)V, stage, LV, K, BV, K);
     __syncthreads();
+#pragma unroll
+    for (int rt_ = 0; rt_ < 4; ++rt_)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) stage[(16 * rt_ + acc_row(i)) * LV + c0 + acc_col()] = from_f<T>(dR[rt_][i]);
+    // dS <- gamma_C dS + s Q^T (gamma dO) - K^T (gamma Z)
     const float gC = __expf(GC);
 #pragma unroll
-    for (int s = 0; s < SPW; ++s) {
-      const int ti = w + NWAVE * s, mi = ti / NCT, ni = ti - mi * NCT;
+    for (int t = 0; t < NKT; ++t) {
       f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
-      mma_blk<true, true, CH>(a1, sQgt, LC, 16 * mi, sdOt, LC, 16 * ni);
-      mma_blk<true, true, CH>(a2, sWt, LC, 16 * mi, sdRt, LC, 16 * ni);
-      dS[s] = gC * dS[s] + scale * a1 - a2;
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) mma(a1, frag_oct(sQ, LK, 16 * t, 32 * ib), dOg[ib]);
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) mma(a2, frag_oct_perm(sK, LK, 16 * t, 32 * jb), Zb[jb]);
+      dS[t] = gC * dS[t] + scale * a1 - a2;
     }
+    __syncthreads();
+    s2g_rows(wsdR + cidx * CH * V + v0, (int64_t)V, stage, LV, CH, BV, CH);
     __syncthreads();
   }
   if (dh0) {
 #pragma unroll
-    for (int s = 0; s < SPW; ++s) {
-      const int ti = w + NWAVE * s, mi = ti / NCT, ni = ti - mi * NCT;
+    for (int t = 0; t < NKT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = 16 * mi + acc_row(i), vc = 16 * ni + acc_col();
-        dh0[sbase + (int64_t)d * V + v0 + vc] = dS[s][i];
-      }
-    }
+      for (int i = 0; i < 4; ++i) dh0[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] = dS[t][i];
   }
 }
 
@@ -340,7 +366,7 @@ __global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * w + acc_row(i);
-      const float e = (r >= cc) ? __expf(sG[r] - sG[cc]) : 0.f;
+      const float e = r >= cc ? __expf(fminf(sG[r] - sG[cc], 0.f)) : 0.f;
       const float dA = (r > cc) ? -da[i] : 0.f;
       const float Aval = bet[i] * kk[i] * e;
       const float dP = (r >= cc) ? aP[n][i] : 0.f;
@@ -413,16 +439,13 @@ __global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------------------
-template <typename T> constexpr int state_bv_b() { return 32; }
-
 template <typename T, int K>
 static hipError_t bwd_state_k(const ChunkArgs& a) {
-  constexpr int BV = state_bv_b<T>();
+  constexpr int BV = 64;
   dim3 grid(a.V / BV, a.B * a.H);
   bwd_state_kernel<T, K, BV><<<grid, NTHR, 0, a.stream>>>(
-      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.dout), a.dhT, a.dh0,
-      static_cast<const T*>(a.ws.P), static_cast<const T*>(a.ws.W), a.ws.Gc, static_cast<T*>(a.ws.dhs),
-      static_cast<T*>(a.ws.dRs), a.T, a.H, a.V, a.NT, a.scale);
+      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.dout), a.g, a.beta, a.dhT,
+      a.dh0, static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dRs), a.T, a.H, a.V, a.NT, a.scale);
   return hipGetLastError();
 }
 

@@ -26,9 +26,6 @@ template <typename T> struct Frag;
 template <> struct Frag<bf16> { using type = bf16x8; };
 template <> struct Frag<float> { using type = f32x8; };
 
-// LDS row padding (elements) so that rows of a tile start on different banks.
-template <typename T> struct Pad { static constexpr int v = 16 / sizeof(T) * 1; };
-
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
@@ -71,10 +68,13 @@ __device__ __forceinline__ typename Frag<T>::type frag_oc(const T* p, int ld, in
   return f;
 }
 
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::type frag_oct(const T* p, int ld, int o0, int k0);
+
 template <bool KC, typename T>
 __device__ __forceinline__ typename Frag<T>::type frag(const T* p, int ld, int o0, int k0) {
   if constexpr (KC) return frag_kc(p, ld, o0, k0);
-  else return frag_oc(p, ld, o0, k0);
+  else return frag_oct(p, ld, o0, k0);
 }
 
 // c += A[m0:m0+16, 0:KD] * B[0:KD, n0:n0+16].
@@ -90,6 +90,94 @@ __device__ __forceinline__ void mma_blk(f32x4& c, const T* A, int lda, int m0, c
   }
 }
 
+// ---- permuted-k fragments ---------------------------------------------------------------------------------
+// A pair of accumulator tiles covering rows [0,16) and [16,32) of a 32-row block holds, in lane group g,
+// rows 4g..4g+3 of the first tile and 16+4g..16+4g+3 of the second.  Using those 8 rows as the k-slots of a
+// fragment (slot p -> row 4g+p for p < 4, 16+4g+p-4 for p >= 4) lets an accumulator feed the next product as
+// its B operand without leaving registers; the other operand is then read with the same slot order.
+// k contiguous (element (o, k) at p[o*ld + k]), permuted slots: two 4-element reads.
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::type frag_kc_perm(const T* p, int ld, int o0, int k0) {
+  const int l = lane_id();
+  const T* s = p + (o0 + (l & 15)) * ld + k0 + 4 * (l >> 4);
+  if constexpr (sizeof(T) == 2) {
+    const bf16x4 a = *reinterpret_cast<const bf16x4*>(s);
+    const bf16x4 b = *reinterpret_cast<const bf16x4*>(s + 16);
+    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  } else {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(s);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(s + 16);
+    return f32x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  }
+}
+
+// outer index contiguous (element (o, k) at p[k*ld + o]), permuted slots.
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::type frag_oc_perm(const T* p, int ld, int o0, int k0) {
+  const int l = lane_id();
+  const T* s = p + (k0 + 4 * (l >> 4)) * ld + o0 + (l & 15);
+  typename Frag<T>::type f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[j] = s[j * ld];
+    f[4 + j] = s[(16 + j) * ld];
+  }
+  return f;
+}
+
+// ---- transposing LDS reads (bf16) ---------------------------------------------------------------------------
+// ds_read_b64_tr_b16: inside each 16-lane group, local lane m reads 4 bf16 at its address and lane i receives
+// element (i mod 4) of the loads of lanes 4j + i/4, j = 0..3.  With local lane m pointing at row kb + m/4,
+// columns o0 + 4(m mod 4) of a row-major tile, lane i receives the 4 values at rows kb..kb+3 of column o0 + i:
+// a column-major operand slice read straight from a row-major tile.
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x4 ld_tr4(const bf16* p, int ld, int o0, int kb) {
+  const int m = lane_id() & 15;
+  const bf16* a = p + (kb + (m >> 2)) * ld + o0 + 4 * (m & 3);
+  const shortx4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) shortx4*)(a));
+  return __builtin_bit_cast(bf16x4, r);
+}
+
+// Fragment of an operand stored outer-contiguous (element (o, k) at p[k*ld + o]).
+//   frag_oct:      plain slots (k = k0 + 8g + e)
+//   frag_oct_perm: permuted slots (k = k0 + 4g + e, k0 + 16 + 4g + e)
+// bf16 uses two transposing reads; fp32 falls back to scalar reads.
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::type frag_oct(const T* p, int ld, int o0, int k0) {
+  if constexpr (sizeof(T) == 2) {
+    const int g = lane_id() >> 4;
+    const bf16x4 a = ld_tr4(p, ld, o0, k0 + 8 * g), b = ld_tr4(p, ld, o0, k0 + 8 * g + 4);
+    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  } else {
+    return frag_oc(p, ld, o0, k0);
+  }
+}
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::type frag_oct_perm(const T* p, int ld, int o0, int k0);
+
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::type frag_oct_perm(const T* p, int ld, int o0, int k0) {
+  if constexpr (sizeof(T) == 2) {
+    const int g = lane_id() >> 4;
+    const bf16x4 a = ld_tr4(p, ld, o0, k0 + 4 * g), b = ld_tr4(p, ld, o0, k0 + 16 + 4 * g);
+    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  } else {
+    return frag_oc_perm(p, ld, o0, k0);
+  }
+}
+
+// Fragment from two accumulator tiles (rows [0,16) and [16,32) of a 32-row block), permuted slots.
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::type frag_acc2(const f32x4& t0, const f32x4& t1) {
+  typename Frag<T>::type f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[j] = from_f<T>(t0[j]);
+    f[4 + j] = from_f<T>(t1[j]);
+  }
+  return f;
+}
+
 __device__ __forceinline__ int acc_row(int i) { return 4 * (lane_id() >> 4) + i; }
 __device__ __forceinline__ int acc_col() { return lane_id() & 15; }
 
@@ -102,14 +190,20 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
+// Inclusive prefix sum over the 64 lanes of a wave, on DPP: shifts within each 16-lane row, then the row
+// totals broadcast forward (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float x) {
+  const int t = __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, true);
+  return x + __int_as_float(t);
+}
 __device__ __forceinline__ float wave_inclusive_scan(float x) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const float y = __shfl_up(x, o);
-    if (l >= o) x += y;
-  }
+  x = dpp_add<0x111, 0xf>(x);  // row_shr:1
+  x = dpp_add<0x112, 0xf>(x);  // row_shr:2
+  x = dpp_add<0x114, 0xf>(x);  // row_shr:4
+  x = dpp_add<0x118, 0xf>(x);  // row_shr:8
+  x = dpp_add<0x142, 0xa>(x);  // row_bcast:15
+  x = dpp_add<0x143, 0xc>(x);  // row_bcast:31
   return x;
 }
 

@@ -23,12 +23,12 @@ struct StepArgs {
 };
 
 // Chunk workspace carve-up (chunk-major: [B*H][NT][...]).  All offsets are 256-byte aligned.
+// The forward needs no workspace; the backward's recompute sweep fills Tm, Gc, hs and Rs, the reverse sweep dhs
+// and dRs, and the gradient kernel reads them all.
 struct ChunkWs {
   void* Tm;   // [BH][NT][64][64]   (I + A)^-1 per chunk, input dtype
-  void* P;    // [BH][NT][64][64]   scale * (M o Q K^T), input dtype
-  void* W;    // [BH][NT][64][K]    Tm diag(beta gamma) K, input dtype
   float* Gc;  // [BH][NT][64]       chunk-local cumulative log-decay
-  void* hs;   // [BH][NT][K][V]     state entering each chunk (backward only)
+  void* hs;   // [BH][NT][K][V]     state entering each chunk
   void* Rs;   // [BH][NT][64][V]    R = U - W S per chunk (backward only)
   void* dhs;  // [BH][NT][K][V]     dL/d(state leaving each chunk) (backward only)
   void* dRs;  // [BH][NT][64][V]    dL/dR per chunk (backward only)
@@ -58,8 +58,7 @@ bool chunk_shape_supported(int K, int V, int dtype);
 bool step_shape_supported(int K, int V);
 
 hipError_t launch_step(const StepArgs& a);
-hipError_t launch_fwd_intra(const ChunkArgs& a);                 // Tm, P, W, Gc
-hipError_t launch_fwd_state(const ChunkArgs& a, bool backward);  // o/hT (forward) or hs/Rs (backward)
+hipError_t launch_fwd(const ChunkArgs& a, bool backward);  // o/hT (forward) or hs/Rs/Tm/Gc (backward)
 hipError_t launch_bwd_state(const ChunkArgs& a);                 // dhs, dRs, dh0
 hipError_t launch_bwd_intra(const ChunkArgs& a);                 // dq, dk, dv, dg, dbeta
 

@@ -37,13 +37,12 @@ def f_fwd(K: int, V: int) -> int:
 
 
 def stage_flops(stage: str, K: int, V: int) -> int:
-    """Dense MFMA FLOPs per token-head that each kernel stage executes (C = 64 tokens per chunk)."""
+    """Algorithmic dense MFMA FLOPs per token-head of each kernel stage (C = 64 tokens per chunk).  Work a
+    stage repeats for every 64-wide V block (the chunk factors) is counted once."""
     return {
-        "fwd_intra": 6 * C * K,                       # K K^T, Q K^T, W = Tm X
-        "fwd_state": 4 * C * V + 6 * K * V,           # U, P R; W S, Q S, Kd^T R
-        "bwd_recompute_intra": 6 * C * K,
-        "bwd_recompute_state": 2 * C * V + 4 * K * V,  # U; W S, Kd^T R
-        "bwd_state": 2 * C * V + 6 * K * V,           # P^T dO; Kd dS, Qg^T dO, W^T dR
+        "fwd": 6 * C * K + 4 * C * V + 6 * K * V,            # KK^T, QK^T, W; U, PR; WS, QS, K^T R
+        "bwd_recompute": 4 * C * K + 2 * C * V + 4 * K * V,  # KK^T, W; U; WS, K^T R
+        "bwd_state": 6 * C * K + 2 * C * V + 6 * K * V,      # KK^T, QK^T, W; P^T dO; K dS, Qg^T dO, W^T dR
         "bwd_intra": 6 * C * V + 6 * K * V + 16 * C * K + 4 * C * C,
     }.get(stage, 0)
 
