@@ -87,8 +87,8 @@ __global__ __launch_bounds__(NTHR) void bwd_state_kernel(
     }
     __syncthreads();
     if (c > 0) prefetch(c - 1);
-    chunk_factors_start<T, K, 1>(sK, sQ, sG, sB, scale, sScr, sP);
-    // overlapped with the diagonal solve: K dS for this wave's columns
+    const f32x4 Dw = chunk_factors_start<T, K, 1>(sK, sQ, sG, sB, scale, sScr, sP, sTmB, nullptr);
+    // independent of the inverse: K dS for this wave's columns
     typename Frag<T>::type dSb[K / 32];
 #pragma unroll
     for (int s = 0; s < K / 32; ++s) dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
@@ -110,7 +110,7 @@ __global__ __launch_bounds__(NTHR) void bwd_state_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) dOg[ib][e] = from_f<T>(to_f(dOb[ib][e]) * sGam[32 * ib + 8 * (l >> 4) + e]);
     }
-    chunk_factors_finish<T, 1>(sB, sScr, sTmB, nullptr);
+    chunk_factors_finish<T>(Dw, sB, sScr, sTmB, nullptr);
 
     // dS leaving this chunk -> global dh (bf16 [K][V] per chunk)
 #pragma unroll

@@ -14,97 +14,111 @@
 
 namespace gdn {
 
-// 16x16x16 fp32 products for the triangular inverse (k split as slice j: k = 4*(l >> 4) + j).
-template <int LD>
-__device__ __forceinline__ void mma16_ss(f32x4& c, const float* L, const float* R) {
-  const int l = lane_id();
+// ---- 64x64 unit-lower-triangular inverse ------------------------------------------------------------------
+// Blocked by 16.  Products are 16x16x16 on "slices": an A-slice holds, in lane l (g = l >> 4), A[l & 15][4g + j],
+// a B-slice holds B[4g + j][l & 15] (j = 0..3), which is also the layout of a 16x16 fp32 accumulator.  The
+// A-slice of X is therefore the accumulator of X^T, so a chain of products stays in registers as long as both
+// X and X^T are carried.  fp32 inputs use four v_mfma_f32_16x16x4_f32; bf16 runs use the split
+// x = hi + lo (hi = bf16(x), lo = bf16(x - hi)) and three v_mfma_f32_16x16x16_bf16 (hi hi, hi lo, lo hi),
+// which keeps the inverse at about fp32 accuracy.
+__device__ __forceinline__ void split_hi_lo(const f32x4& x, shortx4& hi, shortx4& lo) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const float a = L[(l & 15) * LD + 4 * (l >> 4) + j];
-    const float b = R[(4 * (l >> 4) + j) * LD + (l & 15)];
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    const bf16 h = static_cast<bf16>(x[j]);
+    hi[j] = __builtin_bit_cast(short, h);
+    lo[j] = __builtin_bit_cast(short, static_cast<bf16>(x[j] - static_cast<float>(h)));
   }
 }
-// c += L * Y with Y an accumulator tile (lane holds rows 4*(l>>4)+j of column l&15: exactly the B slices).
-template <int LD>
-__device__ __forceinline__ void mma16_sa(f32x4& c, const float* L, const f32x4& Y) {
-  const int l = lane_id();
+template <typename T>
+__device__ __forceinline__ void mm16(f32x4& c, const f32x4& a, const f32x4& b) {
+  if constexpr (sizeof(T) == 4) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float a = L[(l & 15) * LD + 4 * (l >> 4) + j];
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Y[j], c, 0, 0, 0);
+    for (int j = 0; j < 4; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], c, 0, 0, 0);
+  } else {
+    shortx4 ah, al, bh, bl;
+    split_hi_lo(a, ah, al);
+    split_hi_lo(b, bh, bl);
+    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, c, 0, 0, 0);
   }
 }
 template <int LD>
-__device__ __forceinline__ void store_neg_tile(float* dst, const f32x4& t) {
+__device__ __forceinline__ f32x4 ld_aslice(const float* p) {
   const int l = lane_id();
+  return *reinterpret_cast<const f32x4*>(p + (l & 15) * LD + 4 * (l >> 4));
+}
+template <int LD>
+__device__ __forceinline__ f32x4 ld_bslice(const float* p) {
+  const int l = lane_id();
+  f32x4 r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) dst[(4 * (l >> 4) + i) * LD + (l & 15)] = -t[i];
+  for (int j = 0; j < 4; ++j) r[j] = p[(4 * (l >> 4) + j) * LD + (l & 15)];
+  return r;
+}
+// s * I as a slice (the same lanes hold the diagonal in the A-slice and in the accumulator layout)
+__device__ __forceinline__ f32x4 eye16(float s) {
+  const int l = lane_id();
+  f32x4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r[j] = (l & 15) == 4 * (l >> 4) + j ? s : 0.f;
+  return r;
+}
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Diagonal block D = (I + L)^-1 of a strictly lower 16x16 L (fp32 in LDS, stride LD), as an accumulator:
+// L^16 = 0, so D = (I - L)(I + L^2)(I + L^4)(I + L^8).
+template <typename T, int LD>
+__device__ __forceinline__ f32x4 inv_diag16(const float* Lp) {
+  const f32x4 La = ld_aslice<LD>(Lp), Lb = ld_bslice<LD>(Lp);  // L as A-slice; L as B-slice (= L^T A-slice)
+  const f32x4 I = eye16(1.f);
+  f32x4 L2 = zero4(), L2t = zero4(), L4 = zero4(), L4t = zero4(), L8 = zero4();
+  mm16<T>(L2, La, Lb);    // L L
+  mm16<T>(L2t, Lb, La);   // L^T L^T
+  mm16<T>(L4, L2t, L2);   // L^2 L^2
+  mm16<T>(L4t, L2, L2t);  // (L^2)^T (L^2)^T
+  mm16<T>(L8, L4t, L4);   // L^4 L^4
+  const f32x4 ImL = I - La;  // (I - L) A-slice  =  (I - L)^T B-slice
+  f32x4 Z1t = zero4(), Z2t = zero4(), D = zero4();
+  mm16<T>(Z1t, I + L2, ImL);   // Z1^T = (I + L^2)^T (I - L)^T
+  mm16<T>(Z2t, I + L4, Z1t);   // Z2^T = (I + L^4)^T Z1^T
+  mm16<T>(D, Z2t, I + L8);     // D = Z2 (I + L^8)
+  return D;
 }
 
-// (I + A)^-1 for a strictly lower 64x64 A (fp32, LDS, stride LD) into the lower blocks of Ti (stride LD), in two
-// stages so callers can overlap other work with the first:
-//   invert_diag:   wave 0 only (others return at once) -- the four 16x16 diagonal blocks D_b by right-looking
-//                  forward substitution, lane (b, c) solving column c of block b;
-//   invert_merge:  all threads, after a barrier -- T_ij = -D_i sum_{k=j}^{i-1} A_ik T_kj by distance i - j on
-//                  fp32 MFMA.  Ends with a barrier.
-// Blocks above the diagonal of Ti are left untouched (callers treat them as zero).
-template <int LD>
-__device__ __forceinline__ void invert_diag(const float* A, float* Ti) {
-  if (wave_id() != 0) return;
+// Writes block (bi, bj) of Tm (accumulator x) as TmB = Tm diag(beta) into LDS (stride LC) and, if gTm is
+// non-null, the unscaled block to global memory (64 x 64 row-major).
+template <typename T, int LC>
+__device__ __forceinline__ void put_tm_block(T* sTmB, T* gTm, const float* sB, int bi, int bj, const f32x4& x) {
   const int l = lane_id();
-  const int blk = l >> 4, cc = l & 15;
-  const float* Ab = A + 16 * blk * LD + 16 * blk;
-  float x[16];
+  const int col = 16 * bj + (l & 15);
+  const float bc = sB[col];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) x[i] = (i == cc) ? 1.f : 0.f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-#pragma unroll
-    for (int i = j + 1; i < 16; ++i) x[i] -= Ab[i * LD + j] * x[j];
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * bi + 4 * (l >> 4) + i;
+    sTmB[r * LC + col] = from_f<T>(x[i] * bc);
+    if (gTm) gTm[r * CH + col] = from_f<T>(x[i]);
   }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) Ti[(16 * blk + i) * LD + 16 * blk + cc] = x[i];
 }
 
-template <int LD>
-__device__ __forceinline__ void invert_merge(const float* A, float* Ti) {
-  const int w = wave_id();
-  auto blkp = [](const float* base, int i, int j) { return base + 16 * i * LD + 16 * j; };
-  auto blkw = [](float* base, int i, int j) { return base + 16 * i * LD + 16 * j; };
-  if (w < 3) {
-    const int j = w, i = w + 1;
-    f32x4 y = {0.f, 0.f, 0.f, 0.f}, t = {0.f, 0.f, 0.f, 0.f};
-    mma16_ss<LD>(y, blkp(A, i, j), blkp(Ti, j, j));
-    mma16_sa<LD>(t, blkp(Ti, i, i), y);
-    store_neg_tile<LD>(blkw(Ti, i, j), t);
+// Column block J of Tm for blocks below the diagonal: X_iJ = -D_i sum_{k=J}^{i-1} A_ik X_kJ, X_JJ = D_J.
+// A in sA (fp32), the diagonal blocks D_i in sD (fp32); both stride LF.  Blocks above the diagonal are zero.
+template <typename T, int J, int LF, int LC>
+__device__ __forceinline__ void tm_column(const float* sA, const float* sD, const f32x4& DJ, T* sTmB, T* gTm,
+                                          const float* sB) {
+  f32x4 X[4];
+  X[J] = DJ;
+#pragma unroll
+  for (int i = J + 1; i < 4; ++i) {
+    f32x4 Y = zero4(), Xi = zero4();
+#pragma unroll
+    for (int k = J; k < i; ++k) mm16<T>(Y, ld_aslice<LF>(sA + 16 * i * LF + 16 * k), X[k]);
+    mm16<T>(Xi, ld_aslice<LF>(sD + 16 * i * LF + 16 * i), Y);
+    X[i] = -Xi;
+    put_tm_block<T, LC>(sTmB, gTm, sB, i, J, X[i]);
   }
-  __syncthreads();
-  if (w < 2) {
-    const int j = w, i = w + 2;
-    f32x4 y = {0.f, 0.f, 0.f, 0.f}, t = {0.f, 0.f, 0.f, 0.f};
-    mma16_ss<LD>(y, blkp(A, i, j), blkp(Ti, j, j));
-    mma16_ss<LD>(y, blkp(A, i, j + 1), blkp(Ti, j + 1, j));
-    mma16_sa<LD>(t, blkp(Ti, i, i), y);
-    store_neg_tile<LD>(blkw(Ti, i, j), t);
-  }
-  __syncthreads();
-  if (w == 0) {
-    f32x4 y = {0.f, 0.f, 0.f, 0.f}, t = {0.f, 0.f, 0.f, 0.f};
-    mma16_ss<LD>(y, blkp(A, 3, 0), blkp(Ti, 0, 0));
-    mma16_ss<LD>(y, blkp(A, 3, 1), blkp(Ti, 1, 0));
-    mma16_ss<LD>(y, blkp(A, 3, 2), blkp(Ti, 2, 0));
-    mma16_sa<LD>(t, blkp(Ti, 3, 3), y);
-    store_neg_tile<LD>(blkw(Ti, 3, 0), t);
-  }
-  __syncthreads();
-}
-
-template <int LD>
-__device__ __forceinline__ void invert_unit_lower64(const float* A, float* Ti) {
-  invert_diag<LD>(A, Ti);
-  __syncthreads();
-  invert_merge<LD>(A, Ti);
+#pragma unroll
+  for (int i = 0; i < J; ++i) put_tm_block<T, LC>(sTmB, gTm, sB, i, J, zero4());
 }
 
 // A ROWS x COLS tile of T held in registers as 16-byte vectors (ROWS*COLS*sizeof(T)/16 split over NTHR threads),
@@ -164,14 +178,14 @@ __device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld,
 
 // Chunk factors in LDS, phase 1 (all threads): K K^T and Q K^T on MFMA (row block = wave), then
 //   A_ij = beta_i (K K^T)_ij exp(G_i - G_j) (i > j) -> sScr[0 : CH*LF]  (fp32, strict lower)
-//   P_ij = s (Q K^T)_ij exp(G_i - G_j) (i >= j)     -> sP  (PMODE 1: [i][j];  PMODE 2: P^T, [j][i])
-// then a barrier and the diagonal-block solve of the inverse on wave 0.  Waves 1-3 return immediately, so
-// the caller can overlap independent work before calling chunk_factors_finish (which starts with a barrier).
-// Inputs: sK (and sQ if PMODE != 0) rows of the chunk, zero past the sequence end; sG (cumulative log-decay);
-// sB (beta, zero past the end).  sScr holds 2 * CH * LF floats.
+//   P_ij = s (Q K^T)_ij exp(G_i - G_j) (i >= j)     -> sP  (PMODE 1, row-major; PMODE 0: none, sQ unused)
+// then a barrier and the diagonal block D_w of the inverse on every wave w (written to the second half of
+// sScr and to its TmB block, and returned for chunk_factors_finish).  The caller may overlap independent
+// work before calling chunk_factors_finish.  Inputs: sK (and sQ) rows of the chunk, zero past the sequence end;
+// sG (cumulative log-decay); sB (beta, zero past the end).  sScr holds 2 * CH * LF floats.
 template <typename T, int K, int PMODE>
-__device__ __forceinline__ void chunk_factors_start(const T* sK, const T* sQ, const float* sG, const float* sB,
-                                                    float scale, float* sScr, T* sP) {
+__device__ __forceinline__ f32x4 chunk_factors_start(const T* sK, const T* sQ, const float* sG, const float* sB,
+                                                     float scale, float* sScr, T* sP, T* sTmB, T* gTm) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LF = CH + 4;
   const int w = wave_id();
@@ -195,35 +209,35 @@ __device__ __forceinline__ void chunk_factors_start(const T* sK, const T* sQ, co
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * w + acc_row(i);
       const float e = __expf(fminf(Gr[i] - Gc, 0.f));
-      const float a = Br[i] * kk[i] * e;
-      const float p = scale * qk[i] * e;
-      sA[r * LF + cc] = r > cc ? a : 0.f;
-      if constexpr (PMODE == 1) sP[r * LC + cc] = from_f<T>(r >= cc ? p : 0.f);
-      if constexpr (PMODE == 2) sP[cc * LC + r] = from_f<T>(r >= cc ? p : 0.f);
+      sA[r * LF + cc] = r > cc ? Br[i] * kk[i] * e : 0.f;
+      if constexpr (PMODE == 1) sP[r * LC + cc] = from_f<T>(r >= cc ? scale * qk[i] * e : 0.f);
     }
   }
   __syncthreads();
-  invert_diag<LF>(sA, sScr + CH * LF);
+  const f32x4 D = inv_diag16<T, LF>(sA + 16 * w * LF + 16 * w);
+  float* sD = sScr + CH * LF;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sD[(16 * w + acc_row(i)) * LF + 16 * w + acc_col()] = D[i];
+  put_tm_block<T, LC>(sTmB, gTm, sB, w, w, D);
+  return D;
 }
 
-// Phase 2 (all threads): off-diagonal blocks of the inverse, then
-//   TmB = Tm diag(beta)  -> sTmB  (TMODE 1: [i][j];  TMODE 2: TmB^T, [j][i])
-//   Tm (unscaled)        -> gTm (global, 64 x 64 row-major) if non-null.
-// Ends with a barrier; sScr is free again afterwards.
-template <typename T, int TMODE>
-__device__ __forceinline__ void chunk_factors_finish(const float* sB, float* sScr, T* sTmB, T* gTm) {
+// Phase 2 (all threads): the blocks of Tm below the diagonal, column block = wave, straight into
+// TmB = Tm diag(beta) (LDS, row-major) and the global Tm (if gTm is non-null).  Starts and ends with a
+// barrier; sScr is free again afterwards.
+template <typename T>
+__device__ __forceinline__ void chunk_factors_finish(const f32x4& D, const float* sB, const float* sScr, T* sTmB,
+                                                     T* gTm) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LC = CH + PT, LF = CH + 4;
   __syncthreads();
-  invert_merge<LF>(sScr, sScr + CH * LF);
-  const float* sT = sScr + CH * LF;
-  for (int idx = threadIdx.x; idx < CH * CH; idx += NTHR) {
-    const int r = idx >> 6, cc = idx & 63;
-    const float tv = sT[r * LF + cc];  // blocks above the diagonal are never written: masked below
-    const float t = (r >> 4) >= (cc >> 4) ? tv : 0.f;
-    if constexpr (TMODE == 1) sTmB[r * LC + cc] = from_f<T>(t * sB[cc]);
-    else sTmB[cc * LC + r] = from_f<T>(t * sB[cc]);
-    if (gTm) gTm[idx] = from_f<T>(t);
+  const float* sA = sScr;
+  const float* sD = sScr + CH * LF;
+  switch (wave_id()) {
+    case 0: tm_column<T, 0, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
+    case 1: tm_column<T, 1, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
+    case 2: tm_column<T, 2, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
+    default: tm_column<T, 3, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
   }
   __syncthreads();
 }

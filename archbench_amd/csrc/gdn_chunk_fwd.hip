@@ -84,8 +84,9 @@ __global__ __launch_bounds__(NTHR) void fwd_fused_kernel(
     __syncthreads();
     if (c + 1 < NT) prefetch(c + 1);
 
-    chunk_factors_start<T, K, BWD ? 0 : 1>(sK, sQ, sG, sB, scale, sScr, sP);
-    // overlapped with the diagonal solve on wave 0:  K S and Q S for this wave's columns, Y = V - gamma K S
+    T* gTm = (BWD && vb == 0) ? wsTm + cidx * CH * CH : nullptr;
+    const f32x4 Dw = chunk_factors_start<T, K, BWD ? 0 : 1>(sK, sQ, sG, sB, scale, sScr, sP, sTmB, gTm);
+    // independent of the inverse (overlaps its latency):  K S and Q S for this wave's columns, Y = V - gamma K S
     typename Frag<T>::type Sb[K / 32];
 #pragma unroll
     for (int s = 0; s < K / 32; ++s) Sb[s] = frag_acc2<T>(S[2 * s], S[2 * s + 1]);
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(NTHR) void fwd_fused_kernel(
         Y[rt][i] = to_f(sV[r * LV + c0 + acc_col()]) - sGam[r] * ks[i];
       }
     }
-    chunk_factors_finish<T, 1>(sB, sScr, sTmB, (BWD && vb == 0) ? wsTm + cidx * CH * CH : nullptr);
+    chunk_factors_finish<T>(Dw, sB, sScr, sTmB, gTm);
 
     // ---- R = TmB Y, output, state update (this wave's 16 columns) ------------------------------------------
     typename Frag<T>::type Yb[2];
