@@ -215,13 +215,32 @@ __global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
   const int64_t row0 = ((int64_t)b * T_ + t0) * H + h;
   const int64_t cidx = (int64_t)bh * NT + c;
 
-  g2s_rows(sQ, LK, q + row0 * K, (int64_t)H * K, CH, K, nvalid);
-  g2s_rows(sK, LK, k + row0 * K, (int64_t)H * K, CH, K, nvalid);
-  g2s_rows(sTm, LC, wsTm + cidx * CH * CH, (int64_t)CH, CH, CH, CH);
+  // every global read of the chunk is issued up front as 16-byte register tiles (see RegTile); the second
+  // V slab is fetched while the first is computed
+  RegTile<T, CH, K> tq, tk;
+  RegTile<T, CH, CH> rtm;
+  RegTile<T, CH, VS> rdo, rv, rr, rdr;
+  RegTile<T, K, VS> rs0, rdsc;
+  auto load_slab = [&](int vs) {
+    rdo.load(dout + row0 * V + vs, (int64_t)H * V, nvalid);
+    rv.load(v + row0 * V + vs, (int64_t)H * V, nvalid);
+    rr.load(wsR + cidx * CH * V + vs, (int64_t)V, CH);
+    rdr.load(wsdR + cidx * CH * V + vs, (int64_t)V, CH);
+    rs0.load(wsH + cidx * K * V + vs, (int64_t)V, K);
+    rdsc.load(wsdH + cidx * K * V + vs, (int64_t)V, K);
+  };
+  tq.load(q + row0 * K, (int64_t)H * K, nvalid);
+  tk.load(k + row0 * K, (int64_t)H * K, nvalid);
+  rtm.load(wsTm + cidx * CH * CH, (int64_t)CH, CH);
+  load_slab(0);
   if (tid < CH) {
     sG[tid] = wsGc[cidx * CH + tid];
-    sB[tid] = tid < nvalid ? beta[row0 + (int64_t)tid * H] : 0.f;
+    sB[tid] = beta[row0 + (int64_t)(tid < nvalid ? tid : 0) * H];
+    if (tid >= nvalid) sB[tid] = 0.f;
   }
+  tq.store(sQ, LK);
+  tk.store(sK, LK);
+  rtm.store(sTm, LC);
 
   // ---- V phase: contractions over V, slab by slab -------------------------------------------------------
   f32x4 aP[4], aTV[4], aQg[NKT], aKd[NKT], aWn[NKT];
@@ -233,13 +252,14 @@ __global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
   float sdot = 0.f;  // partial <dS_C, S0>
 
   for (int vs = 0; vs < V; vs += VS) {
-    g2s_rows(sdO, LS, dout + row0 * V + vs, (int64_t)H * V, CH, VS, nvalid);
-    g2s_rows(sV, LS, v + row0 * V + vs, (int64_t)H * V, CH, VS, nvalid);
-    g2s_rows(sR, LS, wsR + cidx * CH * V + vs, (int64_t)V, CH, VS, CH);
-    g2s_rows(sdR, LS, wsdR + cidx * CH * V + vs, (int64_t)V, CH, VS, CH);
-    g2s_rows(sS0, LS, wsH + cidx * K * V + vs, (int64_t)V, K, VS, K);
-    g2s_rows(sdSC, LS, wsdH + cidx * K * V + vs, (int64_t)V, K, VS, K);
+    rdo.store(sdO, LS);
+    rv.store(sV, LS);
+    rr.store(sR, LS);
+    rdr.store(sdR, LS);
+    rs0.store(sS0, LS);
+    rdsc.store(sdSC, LS);
     __syncthreads();
+    if (vs + VS < V) load_slab(vs + VS);
     for (int idx = tid; idx < K * VS; idx += NTHR) {
       const int d = idx / VS, n = idx - d * VS;
       sdot += to_f(sdSC[d * LS + n]) * to_f(sS0[d * LS + n]);

@@ -1,0 +1,140 @@
+"""Gated DeltaNet mixer layer on the MI355X kernels, with the constructor and forward of the fla layer that
+archbench's ``gdn`` arch builds (archbench/layers/fla.py:36-38 via build_fla, fla.py:21-33).
+
+Constructor kwargs are those archbench passes from YAML (configs/arch/gdn.yaml:4-9: head_dim, expand_v,
+use_gate, use_short_conv, conv_size; configs/*/gdn.yaml: num_heads) plus the auto-passed hidden_size and
+layer_idx.  Input conventions follow the in-tree GDN-family layer (archbench/layers/nsgdn.py:525-534):
+q, k L2-normalised per head (q scaled by head_dim^-1/2 through the op's default scale), beta = sigmoid(.),
+g = -exp(A_log) softplus(a + dt_bias) (natural-log decay), fp32 state.  The output projection is named
+``o_proj`` so the reference's zero-init rule for output projections (archbench/model.py:14, :80-82) applies.
+
+The token mixing itself is always the HIP chunk op (training / prefill) or the HIP decode step (T = 1 with
+a recurrent state, no grad).  Projections, the short causal convolutions and the gated RMSNorm are PyTorch.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .. import ops
+
+
+class ShortConvolution(nn.Module):
+    """Depthwise causal conv1d (kernel ``size``) + SiLU over [B, T, D] (the ShortConv of nsgdn.py:457-470).
+    With ``state`` ([B, D, size-1], the previous inputs) it continues a sequence and returns the new state."""
+
+    def __init__(self, dim: int, size: int = 4, bias: bool = False):
+        super().__init__()
+        self.size = size
+        self.weight = nn.Parameter(torch.empty(dim, 1, size).uniform_(-1 / math.sqrt(size), 1 / math.sqrt(size)))
+        self.bias = nn.Parameter(torch.zeros(dim)) if bias else None
+
+    def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
+        B, T, D = x.shape
+        xt = x.transpose(1, 2)
+        if state is None:
+            state = xt.new_zeros(B, D, self.size - 1)
+        full = torch.cat([state.to(xt.dtype), xt], dim=-1)
+        y = F.conv1d(full, self.weight.to(x.dtype), None if self.bias is None else self.bias.to(x.dtype),
+                     groups=D)
+        return F.silu(y.transpose(1, 2)), full[..., -(self.size - 1):]
+
+
+class GatedRMSNorm(nn.Module):
+    """RMSNorm over the head dimension times swish(gate) (fla's FusedRMSNormGated, nsgdn.py:539-541)."""
+
+    def __init__(self, dim: int, eps: float = 1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: torch.Tensor, gate: torch.Tensor | None = None) -> torch.Tensor:
+        y = F.rms_norm(x.float(), (x.shape[-1],), self.weight.float(), self.eps)
+        if gate is not None:
+            y = y * F.silu(gate.float())
+        return y.to(x.dtype)
+
+
+class GatedDeltaNet(nn.Module):
+    def __init__(self, hidden_size: int = 2048, expand_v: float = 2.0, head_dim: int = 256, num_heads: int = 6,
+                 mode: str = "chunk", use_gate: bool = True, use_short_conv: bool = True,
+                 allow_neg_eigval: bool = False, conv_size: int = 4, conv_bias: bool = False,
+                 layer_idx: int | None = None, norm_eps: float = 1e-5, **kwargs):
+        super().__init__()
+        if mode not in ("chunk", "fused_recurrent"):
+            raise ValueError(f"unknown mode {mode!r}; choose chunk or fused_recurrent")
+        self.hidden_size, self.mode = hidden_size, mode
+        self.num_heads, self.head_k_dim = num_heads, head_dim
+        self.head_v_dim = int(head_dim * expand_v)
+        self.key_dim, self.value_dim = num_heads * head_dim, num_heads * self.head_v_dim
+        self.use_gate, self.use_short_conv, self.allow_neg_eigval = use_gate, use_short_conv, allow_neg_eigval
+        self.layer_idx = layer_idx
+        self.q_proj = nn.Linear(hidden_size, self.key_dim, bias=False)
+        self.k_proj = nn.Linear(hidden_size, self.key_dim, bias=False)
+        self.v_proj = nn.Linear(hidden_size, self.value_dim, bias=False)
+        self.a_proj = nn.Linear(hidden_size, num_heads, bias=False)
+        self.b_proj = nn.Linear(hidden_size, num_heads, bias=False)
+        A = torch.empty(num_heads).uniform_(0, 16)
+        self.A_log = nn.Parameter(torch.log(A))
+        self.A_log._no_weight_decay = True
+        dt_min, dt_max, dt_floor = 0.001, 0.1, 1e-4
+        dt = torch.exp(torch.rand(num_heads) * (math.log(dt_max) - math.log(dt_min)) + math.log(dt_min))
+        dt = dt.clamp(min=dt_floor)
+        self.dt_bias = nn.Parameter(dt + torch.log(-torch.expm1(-dt)))
+        self.dt_bias._no_weight_decay = True
+        if use_short_conv:
+            self.q_conv1d = ShortConvolution(self.key_dim, conv_size, conv_bias)
+            self.k_conv1d = ShortConvolution(self.key_dim, conv_size, conv_bias)
+            self.v_conv1d = ShortConvolution(self.value_dim, conv_size, conv_bias)
+        if use_gate:
+            self.g_proj = nn.Linear(hidden_size, self.value_dim, bias=False)
+        self.o_norm = GatedRMSNorm(self.head_v_dim, norm_eps)
+        self.o_proj = nn.Linear(self.value_dim, hidden_size, bias=False)
+
+    def forward(self, hidden_states: torch.Tensor, attention_mask: torch.Tensor | None = None,
+                past_key_values: dict | None = None, use_cache: bool = False, output_attentions: bool = False,
+                **kwargs):
+        """hidden_states [B, T, hidden]; returns (o [B, T, hidden], None, past_key_values).
+
+        ``past_key_values`` is a dict keyed by layer_idx holding {"recurrent_state", "conv_state"}; with
+        ``use_cache`` the entry is created or advanced (decode continues from it)."""
+        if attention_mask is not None:
+            raise ValueError("padding masks are not supported by the gated DeltaNet layer")
+        B, T, _ = hidden_states.shape
+        H, DK, DV = self.num_heads, self.head_k_dim, self.head_v_dim
+        entry = None if past_key_values is None else past_key_values.get(self.layer_idx)
+        conv_in = entry["conv_state"] if entry is not None else (None, None, None)
+        q, k, v = self.q_proj(hidden_states), self.k_proj(hidden_states), self.v_proj(hidden_states)
+        conv_out = (None, None, None)
+        if self.use_short_conv:
+            (q, cq), (k, ck), (v, cv) = (self.q_conv1d(q, conv_in[0]), self.k_conv1d(k, conv_in[1]),
+                                         self.v_conv1d(v, conv_in[2]))
+            conv_out = (cq, ck, cv)
+        else:
+            q, k, v = F.silu(q), F.silu(k), F.silu(v)
+        q, k, v = q.view(B, T, H, DK), k.view(B, T, H, DK), v.view(B, T, H, DV)
+        beta = self.b_proj(hidden_states).float().sigmoid()
+        if self.allow_neg_eigval:
+            beta = beta * 2.0
+        g = -self.A_log.float().exp() * F.softplus(self.a_proj(hidden_states).float() + self.dt_bias)
+        state = entry["recurrent_state"] if entry is not None else None
+        dt = hidden_states.dtype if hidden_states.dtype in (torch.bfloat16, torch.float32) else torch.bfloat16
+        q, k, v = q.to(dt), k.to(dt), v.to(dt)
+        if self.mode == "fused_recurrent" or (T == 1 and not torch.is_grad_enabled() and state is not None):
+            o, new_state = ops.fused_recurrent_gated_delta_rule(q, k, v, g, beta, initial_state=state,
+                                                                output_final_state=use_cache,
+                                                                use_qk_l2norm_in_kernel=True)
+        else:
+            o, new_state = ops.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=state,
+                                                      output_final_state=use_cache, use_qk_l2norm_in_kernel=True)
+        if use_cache:
+            if past_key_values is None:
+                past_key_values = {}
+            past_key_values[self.layer_idx] = {"recurrent_state": new_state, "conv_state": conv_out}
+        gate = self.g_proj(hidden_states).view(B, T, H, DV) if self.use_gate else None
+        o = self.o_norm(o.to(hidden_states.dtype), gate)
+        return self.o_proj(o.reshape(B, T, -1)), None, past_key_values

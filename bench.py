@@ -47,6 +47,17 @@ def stage_flops(stage: str, K: int, V: int) -> int:
     }.get(stage, 0)
 
 
+def measured_traffic() -> dict:
+    """HBM bytes per launch by stage, from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in
+    profiles/hbm_traffic.json (calibrated on a copy of known size); empty if that file is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("per_launch", {})
+    except (OSError, ValueError):
+        return {}
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -148,7 +159,8 @@ def main() -> int:
             "mfma_frac": round(call_flops / sec / MFMA_BF16_PEAK, 4),
             "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved / 1e12, 2),
                          "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
-                         "frac": round(achieved / MFMA_BF16_PEAK, 4), "traffic": None,
+                         "frac": round(achieved / MFMA_BF16_PEAK, 4),
+                         "traffic": measured_traffic().get(dom, {}).get("bytes"),
                          "flops_per_launch": dom_flops, "avg_ms": round(dom_ms, 4)},
             "stages_ms": {k: round(v[0], 4) for k, v in stages.items()},
         })
@@ -183,6 +195,7 @@ def main() -> int:
         kern_ms = st.result["step"][0] / st.result["step"][1]
         nbytes = 2 * B * H * K * V * 4 + B * H * (2 * K + 2 * V) * 2 + B * H * 2 * 4
         out["decode_step"] = {"workload": "gdn_recurrent_step", "B": B, "H": H, "K": K, "V": V,
+                              "traffic": measured_traffic().get("step", {}).get("bytes"),
                               "us_per_step": round(sec * 1e6, 2), "kernel_us": round(kern_ms * 1e3, 2),
                               "bytes_per_step": nbytes, "GB_per_s": round(nbytes / (kern_ms * 1e-3) / 1e9, 1),
                               "hbm_frac": round(nbytes / (kern_ms * 1e-3) / HBM_PEAK, 4),

@@ -1,8 +1,9 @@
 /* C ABI of the MI355X-native gated DeltaNet (GDN) token-mixing op.
  *
  * Plain pointers and sizes only: no torch or HIP C++ types cross this boundary.  All device pointers are
- * device memory owned by the caller (in practice torch's caching allocator); the library allocates nothing,
- * frees nothing and never synchronises the host.  Every call enqueues its kernels on `stream` (a hipStream_t
+ * device memory owned by the caller (in practice torch's caching allocator); the library allocates and frees no
+ * memory and never synchronises the host (the opt-in profiling calls below create hipEvents and synchronise on
+ * them, and only then).  Every call enqueues its kernels on `stream` (a hipStream_t
  * passed as void*; NULL is the default stream) and returns immediately.
  *
  * Layouts (row-major, contiguous):

@@ -1,0 +1,66 @@
+"""Module-level drop-in surface on the CPU: registry semantics (archbench/layers/__init__.py:1-26), layer
+construction from the reference's YAML kwargs, and shape propagation through the custom op's fake kernel."""
+
+import pytest
+import torch
+
+from archbench_amd import layers
+from archbench_amd.layers.fla import FLAMixer, build_fla
+from archbench_amd.layers.gdn import GatedDeltaNet
+
+GDN_YAML = dict(head_dim=128, expand_v=2.0, use_gate=True, use_short_conv=True, conv_size=4)  # arch/gdn.yaml
+
+
+def test_registry_surface():
+    assert "gdn" in layers.available()
+    with pytest.raises(KeyError, match="unknown arch"):
+        layers.build_mixer("nope", 64, 0, 2)
+    with pytest.raises(ImportError):
+        layers.build_mixer("fla:MesaNet", 64, 0, 2)
+
+
+def test_build_gdn_like_model_py():
+    m = layers.build_mixer("gdn", 512, 3, 10, num_heads=4, **GDN_YAML)  # 65m/gdn.yaml
+    assert isinstance(m, FLAMixer) and isinstance(m.layer, GatedDeltaNet)
+    L = m.layer
+    assert L.hidden_size == 512 and L.layer_idx == 3
+    assert (L.num_heads, L.head_k_dim, L.head_v_dim) == (4, 128, 256)
+    names = dict(m.named_modules())
+    assert any(n.endswith("o_proj") for n in names)  # zero-init rule of model.py:80-82 applies
+    assert L.q_proj.weight.shape == (512, 512) and L.v_proj.weight.shape == (1024, 512)
+
+
+def test_auto_kwargs_filtered_by_signature():
+    m = build_fla("GatedDeltaNet", 256, 1, 4, num_heads=2, head_dim=64)
+    assert m.layer.hidden_size == 256 and m.layer.layer_idx == 1
+
+
+def test_no_cpu_fallback():
+    m = layers.build_mixer("gdn", 64, 0, 2, num_heads=1, head_dim=64, expand_v=1.0)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        m(torch.randn(1, 8, 64))
+
+
+def test_fake_tensor_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from archbench_amd import ops
+
+    with FakeTensorMode():
+        q = torch.empty(2, 70, 3, 64, dtype=torch.bfloat16)
+        v = torch.empty(2, 70, 3, 128, dtype=torch.bfloat16)
+        g = torch.empty(2, 70, 3)
+        o, hT = ops.chunk_fwd(q, q, v, g, g, None, 1.0)
+        assert o.shape == (2, 70, 3, 128) and o.dtype == torch.bfloat16
+        assert hT.shape == (2, 3, 64, 128) and hT.dtype == torch.float32
+        grads = ops.chunk_bwd(q, q, v, g, g, None, o, None, 1.0)
+        assert [tuple(t.shape) for t in grads] == [(2, 70, 3, 64), (2, 70, 3, 64), (2, 70, 3, 128), (2, 70, 3),
+                                                   (2, 70, 3), (2, 3, 64, 128)]
+
+
+def test_shape_errors_are_value_errors():
+    from archbench_amd import ops
+
+    q = torch.empty(1, 4, 2, 64, device="meta")
+    with pytest.raises((ValueError, RuntimeError)):
+        ops._shapes(q, q[..., :32], q, q[..., 0], q[..., 0], None)
