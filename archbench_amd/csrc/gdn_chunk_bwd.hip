@@ -4,7 +4,9 @@
 // keeping them from the forward, then runs:
 //
 // bwd_state: one workgroup per (64-wide V block, b*h), reverse over chunks; per chunk it rebuilds the chunk
-//   factors on-chip (chunk_factors) and each wave carries a 16-column slab of dS in MFMA accumulators.
+//   factors on-chip and each wave carries a 16-column slab of dS in MFMA accumulators.  bf16 runs the two roles
+//   of the forward sweep (four state waves, four factor waves, two LDS buffer sets): the factors of chunk c - 1
+//   are built while the state-gradient part of chunk c runs.
 //     dR  = P^T dO + Kd dS_C                         Kd = diag(exp(G_C - G)) K
 //     dS0 = gamma_C dS_C + s (diag(gamma) Q)^T dO - W^T dR,   W^T dR = K^T diag(gamma) (TmB^T dR)
 //   Writes dS_C (the gradient w.r.t. the state leaving each chunk) and dR per chunk, and dh0.
@@ -27,146 +29,223 @@
 
 namespace gdn {
 
-template <typename T, int K, int BV>
-__global__ __launch_bounds__(NTHR) void bwd_state_kernel(
+template <typename T, int K, int BV, bool WS>
+__global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void bwd_state_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ dout, const float* __restrict__ g,
     const float* __restrict__ beta, const float* __restrict__ dhT, float* __restrict__ dh0, T* __restrict__ wsdH,
     T* __restrict__ wsdR, int T_, int H, int V, int NT, float scale) {
   constexpr int PT = 16 / sizeof(T);
-  constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT, LF = CH + 4;
+  constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
   constexpr int NKT = K / 16;
-  static_assert(BV / 16 / NWAVE == 1, "each wave owns one 16-column slab of dS");
-  constexpr int SCR_F = 2 * CH * LF;
-  static_assert(SCR_F * 4 >= K * LV * (int)sizeof(T), "staging must fit in the scratch region");
-  __shared__ __attribute__((aligned(16))) T sK[CH * LK];
-  __shared__ __attribute__((aligned(16))) T sQ[CH * LK];
-  __shared__ __attribute__((aligned(16))) T sdO[CH * LV];   // dO rows of this V block
-  __shared__ __attribute__((aligned(16))) T sP[CH * LC];
-  __shared__ __attribute__((aligned(16))) T sTmB[CH * LC];  // Tm diag(beta)
-  __shared__ __attribute__((aligned(16))) float sScr[SCR_F];
-  __shared__ float sG[CH], sB[CH], sGam[CH];
+  static_assert(BV / 16 / NWAVE == 1, "each state wave owns one 16-column slab of dS");
+  constexpr int NB = WS ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) T sK[NB][CH * LK];
+  __shared__ __attribute__((aligned(16))) T sQ[NB][CH * LK];
+  __shared__ __attribute__((aligned(16))) T sdO[NB][CH * LV];  // dO rows of this V block
+  __shared__ __attribute__((aligned(16))) T sP[NB][CH * LC];
+  __shared__ __attribute__((aligned(16))) T sTmB[NB][CH * LC];  // Tm diag(beta)
+  __shared__ __attribute__((aligned(16))) float sA[CH * (CH + 4)];
+  __shared__ __attribute__((aligned(16))) float sD[4 * DBLK];
+  __shared__ __attribute__((aligned(16))) T stage[CH * LV];  // dR of the chunk, for the coalesced store
+  __shared__ float sG[NB][CH], sB[NB][CH], sGam[NB][CH];
 
-  const int vb = blockIdx.x, bh = blockIdx.y;
+  int vb, bh;
+  sweep_block(V / BV, gridDim.x * BV / V, vb, bh);
   const int b = bh / H, h = bh - b * H;
   const int v0 = vb * BV;
   const int w = wave_id(), l = lane_id();
-  const int c0 = 16 * w;
+  const int wr = w & (NWAVE - 1);            // wave index inside its role
+  const int tid = threadIdx.x & (NTHR - 1);  // thread index inside its role
   const int64_t sbase = (int64_t)bh * K * V;
-  T* stage = reinterpret_cast<T*>(sScr);
+  auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
+  auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
-  f32x4 dS[NKT];
-#pragma unroll
-  for (int t = 0; t < NKT; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dS[t][i] = dhT ? dhT[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
-
-  RegTile<T, CH, K> rk, rq;
-  RegTile<T, CH, BV> rdo;
+  // ---- factor role: K, g, beta of a chunk, and its factors (P included) --------------------------------------
+  RegTile<T, CH, K> rk;
   RegTok rt;
-  auto prefetch = [&](int c) {
-    const int t0 = c * CH, nvalid = min(CH, T_ - t0);
-    const int64_t row0 = ((int64_t)b * T_ + t0) * H + h;
-    rk.load(k + row0 * K, (int64_t)H * K, nvalid);
-    rq.load(q + row0 * K, (int64_t)H * K, nvalid);
-    rdo.load(dout + row0 * V + v0, (int64_t)H * V, nvalid);
-    if (w == 0) rt.load(g, beta, row0, H, nvalid);
+  auto prefetch_f = [&](int c) {
+    rk.load(k + row0_of(c) * K, (int64_t)H * K, nvalid_of(c), tid);
+    if (wr == 0) rt.load(g, beta, row0_of(c), H, nvalid_of(c));
   };
-  prefetch(NT - 1);
-
-  for (int c = NT - 1; c >= 0; --c) {
-    const int64_t cidx = (int64_t)bh * NT + c;
-    rk.store(sK, LK);
-    rq.store(sQ, LK);
-    rdo.store(sdO, LV);
-    if (w == 0) {
+  auto store_f = [&](int n) {
+    rk.store(sK[n], LK, tid);
+    if (wr == 0) {
       const float G = wave_inclusive_scan(rt.ok ? rt.g : 0.f);
-      sG[l] = G;
-      sB[l] = rt.ok ? rt.b : 0.f;
-      sGam[l] = __expf(G);
+      sG[n][l] = G;
+      sB[n][l] = rt.ok ? rt.b : 0.f;
+      sGam[n][l] = __expf(G);
     }
-    __syncthreads();
-    if (c > 0) prefetch(c - 1);
-    const f32x4 Dw = chunk_factors_start<T, K, 1>(sK, sQ, sG, sB, scale, sScr, sP, sTmB, nullptr);
-    // independent of the inverse: K dS for this wave's columns
+  };
+  auto kq_diag = [&](int n) {
+    factors_kq<T, K, 1>(sK[n], sQ[n], sG[n], sB[n], scale, sA, sP[n], wr);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the diagonal block reads this wave's rows of A
+    return factors_diag<T>(sA, sD, sTmB[n], nullptr, sB[n], wr);
+  };
+
+  // ---- state role: Q and dO of a chunk, and the state-gradient part ------------------------------------------
+  RegTile<T, CH, K> rq;
+  RegTile<T, CH, BV> rdo;
+  auto prefetch_s = [&](int c) {
+    rq.load(q + row0_of(c) * K, (int64_t)H * K, nvalid_of(c), tid);
+    rdo.load(dout + row0_of(c) * V + v0, (int64_t)H * V, nvalid_of(c), tid);
+  };
+  auto store_s = [&](int n) {
+    rq.store(sQ[n], LK, tid);
+    rdo.store(sdO[n], LV, tid);
+  };
+  const int c0 = 16 * wr;
+  f32x4 dS[NKT];
+  f32x4 dR[4];
+  typename Frag<T>::type dOg[2], Zb[2];
+  auto load_dhT = [&]() {
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dS[t][i] = dhT ? dhT[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
+  };
+  // C: dS leaving the chunk -> dh (bf16 [K][V] per chunk);  dR = diag(exp(G_C - G)) K dS + P^T dO
+  auto state_C = [&](int c, int n) {
+    T* dh = wsdH + ((int64_t)bh * NT + c) * K * V + v0 + c0 + acc_col();
     typename Frag<T>::type dSb[K / 32];
 #pragma unroll
     for (int s = 0; s < K / 32; ++s) dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
-    const float GC = sG[CH - 1];
-    f32x4 dR[4];
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dh[(16 * t + acc_row(i)) * V] = from_f<T>(dS[t][i]);
+    const float GC = sG[n][CH - 1];
 #pragma unroll
     for (int rt_ = 0; rt_ < 4; ++rt_) {
       f32x4 kd = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < K / 32; ++s) mma(kd, frag_kc_perm(sK, LK, 16 * rt_, 32 * s), dSb[s]);
+      for (int s = 0; s < K / 32; ++s) mma(kd, frag_kc_perm(sK[n], LK, 16 * rt_, 32 * s), dSb[s]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dR[rt_][i] = __expf(GC - sG[16 * rt_ + acc_row(i)]) * kd[i];
+      for (int i = 0; i < 4; ++i) dR[rt_][i] = __expf(GC - sG[n][16 * rt_ + acc_row(i)]) * kd[i];
     }
     // dO fragments of this wave's columns over the chunk's tokens: plain, and scaled by gamma
-    typename Frag<T>::type dOb[2], dOg[2];
+    typename Frag<T>::type dOb[2];
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib) {
-      dOb[ib] = frag_oct(sdO, LV, c0, 32 * ib);
+      dOb[ib] = frag_oct(sdO[n], LV, c0, 32 * ib);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dOg[ib][e] = from_f<T>(to_f(dOb[ib][e]) * sGam[32 * ib + 8 * (l >> 4) + e]);
+      for (int e = 0; e < 8; ++e) dOg[ib][e] = from_f<T>(to_f(dOb[ib][e]) * sGam[n][32 * ib + 8 * (l >> 4) + e]);
     }
-    chunk_factors_finish<T>(Dw, sB, sScr, sTmB, nullptr);
-
-    // dS leaving this chunk -> global dh (bf16 [K][V] per chunk)
-#pragma unroll
-    for (int t = 0; t < NKT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) stage[(16 * t + acc_row(i)) * LV + c0 + acc_col()] = from_f<T>(dS[t][i]);
-    // dR = P^T dO + diag(exp(G_C - G)) K dS
 #pragma unroll
     for (int rt_ = 0; rt_ < 4; ++rt_)
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) mma(dR[rt_], frag_oct(sP, LC, 16 * rt_, 32 * ib), dOb[ib]);
+      for (int ib = 0; ib < 2; ++ib) mma(dR[rt_], frag_oct(sP[n], LC, 16 * rt_, 32 * ib), dOb[ib]);
+  };
+  // D: Z = gamma (TmB^T dR)  (W^T dR = K^T Z);  dR staged
+  auto state_D = [&](int n) {
     typename Frag<T>::type dRb[2];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) dRb[jb] = frag_acc2<T>(dR[2 * jb], dR[2 * jb + 1]);
-    // Z = TmB^T dR, scaled by gamma:  W^T dR = K^T (gamma Z)
-    typename Frag<T>::type Zb[2];
-    {
-      f32x4 Z[4];
+    f32x4 Z[4];
 #pragma unroll
-      for (int rt_ = 0; rt_ < 4; ++rt_) {
-        Z[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rt_ = 0; rt_ < 4; ++rt_) {
+      Z[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) mma(Z[rt_], frag_oct_perm(sTmB, LC, 16 * rt_, 32 * jb), dRb[jb]);
+      for (int jb = 0; jb < 2; ++jb) mma(Z[rt_], frag_oct_perm(sTmB[n], LC, 16 * rt_, 32 * jb), dRb[jb]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) Z[rt_][i] *= sGam[16 * rt_ + acc_row(i)];
-      }
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) Zb[jb] = frag_acc2<T>(Z[2 * jb], Z[2 * jb + 1]);
+      for (int i = 0; i < 4; ++i) Z[rt_][i] *= sGam[n][16 * rt_ + acc_row(i)];
     }
-    __syncthreads();  // dh staging complete
-    s2g_rows(wsdH + cidx * K * V + v0, (int64_t)V, stage, LV, K, BV, K);
-    __syncthreads();
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) Zb[jb] = frag_acc2<T>(Z[2 * jb], Z[2 * jb + 1]);
 #pragma unroll
     for (int rt_ = 0; rt_ < 4; ++rt_)
 #pragma unroll
       for (int i = 0; i < 4; ++i) stage[(16 * rt_ + acc_row(i)) * LV + c0 + acc_col()] = from_f<T>(dR[rt_][i]);
-    // dS <- gamma_C dS + s Q^T (gamma dO) - K^T (gamma Z)
-    const float gC = __expf(GC);
+  };
+  // E: dR -> global;  dS <- gamma_C dS + s Q^T (gamma dO) - K^T Z
+  auto state_E = [&](int c, int n) {
+    s2g_rows(wsdR + ((int64_t)bh * NT + c) * CH * V + v0, (int64_t)V, stage, LV, CH, BV, CH);
+    const float gC = __expf(sG[n][CH - 1]);
 #pragma unroll
     for (int t = 0; t < NKT; ++t) {
       f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) mma(a1, frag_oct(sQ, LK, 16 * t, 32 * ib), dOg[ib]);
+      for (int ib = 0; ib < 2; ++ib) mma(a1, frag_oct(sQ[n], LK, 16 * t, 32 * ib), dOg[ib]);
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) mma(a2, frag_oct_perm(sK, LK, 16 * t, 32 * jb), Zb[jb]);
+      for (int jb = 0; jb < 2; ++jb) mma(a2, frag_oct_perm(sK[n], LK, 16 * t, 32 * jb), Zb[jb]);
       dS[t] = gC * dS[t] + scale * a1 - a2;
     }
-    __syncthreads();
-    s2g_rows(wsdR + cidx * CH * V + v0, (int64_t)V, stage, LV, CH, BV, CH);
-    __syncthreads();
-  }
-  if (dh0) {
+  };
+  auto store_dh0 = [&]() {
+    if (dh0) {
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
+      for (int t = 0; t < NKT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dh0[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] = dS[t][i];
+        for (int i = 0; i < 4; ++i)
+          dh0[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] = dS[t][i];
+    }
+  };
+
+  if constexpr (WS) {
+    // Reverse sweep.  Both roles execute the same barriers: two in the prologue, then three per chunk; at step i
+    // the state waves work on chunk c = NT-1-i (buffer set i&1), the factor waves on chunk c-1.
+    if (w >= NWAVE) {
+      prefetch_f(NT - 1);
+      store_f(0);
+      __syncthreads();
+      prefetch_f(max(NT - 2, 0));
+      const f32x4 D0 = kq_diag(0);
+      __syncthreads();
+      factors_merge<T>(D0, sA, sD, sTmB[0], nullptr, sB[0], wr);
+      for (int i = 0; i < NT; ++i) {
+        const int c = NT - 1 - i, nn = (i & 1) ^ 1;
+        __syncthreads();  // P1
+        if (c > 0) store_f(nn);
+        prefetch_f(max(c - 2, 0));
+        __syncthreads();  // P2
+        f32x4 D = zero4();
+        if (c > 0) D = kq_diag(nn);
+        __syncthreads();  // P3
+        if (c > 0) factors_merge<T>(D, sA, sD, sTmB[nn], nullptr, sB[nn], wr);
+      }
+    } else {
+      load_dhT();
+      prefetch_s(NT - 1);
+      store_s(0);
+      __syncthreads();
+      prefetch_s(max(NT - 2, 0));
+      __syncthreads();
+      for (int i = 0; i < NT; ++i) {
+        const int c = NT - 1 - i, n = i & 1, nn = n ^ 1;
+        __syncthreads();  // P1
+        if (c > 0) store_s(nn);
+        prefetch_s(max(c - 2, 0));
+        state_C(c, n);
+        __syncthreads();  // P2
+        state_D(n);
+        __syncthreads();  // P3
+        state_E(c, n);
+      }
+      store_dh0();
+    }
+  } else {
+    load_dhT();
+    prefetch_f(NT - 1);
+    prefetch_s(NT - 1);
+    for (int c = NT - 1; c >= 0; --c) {
+      store_f(0);
+      store_s(0);
+      __syncthreads();
+      if (c > 0) {
+        prefetch_f(c - 1);
+        prefetch_s(c - 1);
+      }
+      const f32x4 D = kq_diag(0);
+      __syncthreads();  // P complete
+      state_C(c, 0);
+      factors_merge<T>(D, sA, sD, sTmB[0], nullptr, sB[0], wr);
+      __syncthreads();
+      state_D(0);
+      __syncthreads();
+      state_E(c, 0);
+      __syncthreads();
+    }
+    store_dh0();
   }
 }
 
@@ -462,8 +541,9 @@ __global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
 template <typename T, int K>
 static hipError_t bwd_state_k(const ChunkArgs& a) {
   constexpr int BV = 64;
-  dim3 grid(a.V / BV, a.B * a.H);
-  bwd_state_kernel<T, K, BV><<<grid, NTHR, 0, a.stream>>>(
+  dim3 grid(a.V / BV * a.B * a.H);
+  constexpr bool WS = sizeof(T) == 2;
+  bwd_state_kernel<T, K, BV, WS><<<grid, WS ? 2 * NTHR : NTHR, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.dout), a.g, a.beta, a.dhT,
       a.dh0, static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dRs), a.T, a.H, a.V, a.NT, a.scale);
   return hipGetLastError();

@@ -101,8 +101,12 @@ __device__ __forceinline__ void put_tm_block(T* sTmB, T* gTm, const float* sB, i
   }
 }
 
+// Compact store of the four 16x16 diagonal blocks of the inverse (fp32): block b at sD + b * DBLK, stride LDD.
+constexpr int LDD = 20;
+constexpr int DBLK = 16 * LDD;
+
 // Column block J of Tm for blocks below the diagonal: X_iJ = -D_i sum_{k=J}^{i-1} A_ik X_kJ, X_JJ = D_J.
-// A in sA (fp32), the diagonal blocks D_i in sD (fp32); both stride LF.  Blocks above the diagonal are zero.
+// A in sA (fp32, stride LF), the diagonal blocks D_i compact in sD (see LDD).  Blocks above the diagonal are zero.
 template <typename T, int J, int LF, int LC>
 __device__ __forceinline__ void tm_column(const float* sA, const float* sD, const f32x4& DJ, T* sTmB, T* gTm,
                                           const float* sB) {
@@ -113,7 +117,7 @@ __device__ __forceinline__ void tm_column(const float* sA, const float* sD, cons
     f32x4 Y = zero4(), Xi = zero4();
 #pragma unroll
     for (int k = J; k < i; ++k) mm16<T>(Y, ld_aslice<LF>(sA + 16 * i * LF + 16 * k), X[k]);
-    mm16<T>(Xi, ld_aslice<LF>(sD + 16 * i * LF + 16 * i), Y);
+    mm16<T>(Xi, ld_aslice<LDD>(sD + i * DBLK), Y);
     X[i] = -Xi;
     put_tm_block<T, LC>(sTmB, gTm, sB, i, J, X[i]);
   }
@@ -121,10 +125,10 @@ __device__ __forceinline__ void tm_column(const float* sA, const float* sD, cons
   for (int i = 0; i < J; ++i) put_tm_block<T, LC>(sTmB, gTm, sB, i, J, zero4());
 }
 
-// A ROWS x COLS tile of T held in registers as 16-byte vectors (ROWS*COLS*sizeof(T)/16 split over NTHR threads),
-// used to prefetch the next chunk while the current one is computed.  Loads are unconditional: rows past the
-// end of the sequence read row 0 instead (always in bounds) and are zeroed only when the tile is stored, so no
-// wait for the data is forced at load time.
+// A ROWS x COLS tile of T held in registers as 16-byte vectors (ROWS*COLS*sizeof(T)/16 split over the NTHR
+// threads of a four-wave group; tid = thread index inside the group), used to prefetch the next chunk while the
+// current one is computed.  Loads are unconditional: rows past the end of the sequence read row 0 instead
+// (always in bounds) and are zeroed only when the tile is stored, so no wait for the data is forced at load time.
 template <typename T, int ROWS, int COLS>
 struct RegTile {
   static constexpr int E = 16 / sizeof(T);
@@ -133,23 +137,25 @@ struct RegTile {
   static_assert(N * NTHR == ROWS * VPR && N >= 1 && N <= 32, "tile must split evenly over the workgroup");
   uint4 r[N];
   uint32_t ok;
-  __device__ __forceinline__ void load(const T* g, int64_t gld, int valid) {
+  __device__ __forceinline__ void load(const T* g, int64_t gld, int valid, int tid) {
     ok = 0;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const int idx = threadIdx.x + i * NTHR, row = idx / VPR, c = (idx - row * VPR) * E;
+      const int idx = tid + i * NTHR, row = idx / VPR, c = (idx - row * VPR) * E;
       const bool in = row < valid;
       ok |= (in ? 1u : 0u) << i;
       r[i] = *reinterpret_cast<const uint4*>(g + (in ? row : 0) * gld + c);
     }
   }
-  __device__ __forceinline__ void store(T* s, int sld) const {
+  __device__ __forceinline__ void store(T* s, int sld, int tid) const {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const int idx = threadIdx.x + i * NTHR, row = idx / VPR, c = (idx - row * VPR) * E;
+      const int idx = tid + i * NTHR, row = idx / VPR, c = (idx - row * VPR) * E;
       *reinterpret_cast<uint4*>(s + row * sld + c) = ((ok >> i) & 1u) ? r[i] : make_uint4(0, 0, 0, 0);
     }
   }
+  __device__ __forceinline__ void load(const T* g, int64_t gld, int valid) { load(g, gld, valid, threadIdx.x); }
+  __device__ __forceinline__ void store(T* s, int sld) const { store(s, sld, threadIdx.x); }
 };
 
 // Per-token scalars (g, beta) of a chunk for the first wave: same unconditional-load scheme.
@@ -176,20 +182,20 @@ __device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld,
   }
 }
 
-// Chunk factors in LDS, phase 1 (all threads): K K^T and Q K^T on MFMA (row block = wave), then
-//   A_ij = beta_i (K K^T)_ij exp(G_i - G_j) (i > j) -> sScr[0 : CH*LF]  (fp32, strict lower)
+// ---- chunk factors, in three barrier-separated phases ------------------------------------------------------
+// The sweeps call these for the *next* chunk while they run the state part of the current one, so each phase
+// is a separate function and the caller places the barriers between them.
+//
+// factors_kq: K K^T and Q K^T on MFMA (row block = wave), then
+//   A_ij = beta_i (K K^T)_ij exp(G_i - G_j) (i > j) -> sA  (fp32, strict lower)
 //   P_ij = s (Q K^T)_ij exp(G_i - G_j) (i >= j)     -> sP  (PMODE 1, row-major; PMODE 0: none, sQ unused)
-// then a barrier and the diagonal block D_w of the inverse on every wave w (written to the second half of
-// sScr and to its TmB block, and returned for chunk_factors_finish).  The caller may overlap independent
-// work before calling chunk_factors_finish.  Inputs: sK (and sQ) rows of the chunk, zero past the sequence end;
-// sG (cumulative log-decay); sB (beta, zero past the end).  sScr holds 2 * CH * LF floats.
+// Inputs: sK (and sQ) rows of the chunk, zero past the sequence end; sG (cumulative log-decay); sB (beta, zero
+// past the end).
 template <typename T, int K, int PMODE>
-__device__ __forceinline__ f32x4 chunk_factors_start(const T* sK, const T* sQ, const float* sG, const float* sB,
-                                                     float scale, float* sScr, T* sP, T* sTmB, T* gTm) {
+__device__ __forceinline__ void factors_kq(const T* sK, const T* sQ, const float* sG, const float* sB, float scale,
+                                           float* sA, T* sP, int w) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LF = CH + 4;
-  const int w = wave_id();
-  float* sA = sScr;
   // masks are selects on values computed unconditionally (exp of min(G_i - G_j, 0) cannot overflow), so the
   // epilogue has no branches around its LDS reads
   float Gr[4], Br[4];
@@ -198,11 +204,22 @@ __device__ __forceinline__ f32x4 chunk_factors_start(const T* sK, const T* sQ, c
     Gr[i] = sG[16 * w + acc_row(i)];
     Br[i] = sB[16 * w + acc_row(i)];
   }
+  // the row block's K (and Q) fragments are read once; each column block's K fragment serves both products
+  typename Frag<T>::type ak[K / 32], aq[K / 32];
+#pragma unroll
+  for (int s = 0; s < K / 32; ++s) {
+    ak[s] = frag_kc(sK, LK, 16 * w, 32 * s);
+    if constexpr (PMODE != 0) aq[s] = frag_kc(sQ, LK, 16 * w, 32 * s);
+  }
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
     f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<true, true, K>(kk, sK, LK, 16 * w, sK, LK, 16 * n);
-    if constexpr (PMODE != 0) mma_blk<true, true, K>(qk, sQ, LK, 16 * w, sK, LK, 16 * n);
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) {
+      const auto bk = frag_kc(sK, LK, 16 * n, 32 * s);
+      mma(kk, ak[s], bk);
+      if constexpr (PMODE != 0) mma(qk, aq[s], bk);
+    }
     const int cc = 16 * n + acc_col();
     const float Gc = sG[cc];
 #pragma unroll
@@ -213,33 +230,35 @@ __device__ __forceinline__ f32x4 chunk_factors_start(const T* sK, const T* sQ, c
       if constexpr (PMODE == 1) sP[r * LC + cc] = from_f<T>(r >= cc ? scale * qk[i] * e : 0.f);
     }
   }
-  __syncthreads();
+}
+
+// factors_diag (after factors_kq; it reads only the row block of A that the same wave wrote, so no barrier is
+// needed in between): wave w inverts diagonal block w of I + A, writes it to sD and to its TmB block
+// (TmB = Tm diag(beta), row-major, and the unscaled block to gTm if non-null) and returns it for factors_merge.
+template <typename T>
+__device__ __forceinline__ f32x4 factors_diag(const float* sA, float* sD, T* sTmB, T* gTm, const float* sB, int w) {
+  constexpr int PT = 16 / sizeof(T);
+  constexpr int LC = CH + PT, LF = CH + 4;
   const f32x4 D = inv_diag16<T, LF>(sA + 16 * w * LF + 16 * w);
-  float* sD = sScr + CH * LF;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sD[(16 * w + acc_row(i)) * LF + 16 * w + acc_col()] = D[i];
+  for (int i = 0; i < 4; ++i) sD[w * DBLK + acc_row(i) * LDD + acc_col()] = D[i];
   put_tm_block<T, LC>(sTmB, gTm, sB, w, w, D);
   return D;
 }
 
-// Phase 2 (all threads): the blocks of Tm below the diagonal, column block = wave, straight into
-// TmB = Tm diag(beta) (LDS, row-major) and the global Tm (if gTm is non-null).  Starts and ends with a
-// barrier; sScr is free again afterwards.
+// factors_merge (after a barrier following factors_diag): the blocks of Tm below the diagonal, column block =
+// wave w, straight into TmB (and gTm).  TmB is complete once every wave has returned (caller's barrier).
 template <typename T>
-__device__ __forceinline__ void chunk_factors_finish(const f32x4& D, const float* sB, const float* sScr, T* sTmB,
-                                                     T* gTm) {
+__device__ __forceinline__ void factors_merge(const f32x4& D, const float* sA, const float* sD, T* sTmB, T* gTm,
+                                              const float* sB, int w) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LC = CH + PT, LF = CH + 4;
-  __syncthreads();
-  const float* sA = sScr;
-  const float* sD = sScr + CH * LF;
-  switch (wave_id()) {
+  switch (w) {
     case 0: tm_column<T, 0, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
     case 1: tm_column<T, 1, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
     case 2: tm_column<T, 2, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
     default: tm_column<T, 3, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
   }
-  __syncthreads();
 }
 
 }  // namespace gdn

@@ -3,14 +3,23 @@
 //
 // Per chunk (archbench/layers/nsgdn.py:240-249 algebra; fla GDN call order cumsum -> WY -> state -> output,
 // nsgdn.py:357-362), everything stays on-chip:
-//   1. the chunk's k, q, v rows (prefetched into registers during the previous chunk) go to LDS; wave 0 scans g;
-//   2. chunk factors: K K^T, Q K^T on MFMA, A and P, the 64x64 inverse, TmB = Tm diag(beta) (recomputed per
-//      V block, never written to HBM); while wave 0 solves the diagonal blocks of the inverse, every wave
-//      already forms K S and Q S for its columns;
-//   3. state part, one 16-column slab of S per wave, fp32 in MFMA accumulators for the whole sweep:
-//        R = TmB (V - diag(gamma) K S),  O = s gamma (Q S) + P R,  S <- gamma_C S + K^T (exp(G_C - G) R)
-//      S and R reach the next product as B operands straight from the accumulators (permuted-k fragments), so
-//      waves never exchange state; only the chunk inputs are shared through LDS.
+//   chunk factors  K K^T, Q K^T on MFMA, A and P, the 64x64 inverse, TmB = Tm diag(beta) (rebuilt per V block,
+//                  never written to HBM);
+//   state part     one 16-column slab of S per wave, fp32 in MFMA accumulators for the whole sweep:
+//                    R = TmB (V - diag(gamma) K S),  O = s gamma (Q S) + P R,
+//                    S <- gamma_C S + K^T (exp(G_C - G) R)
+//                  S and R reach the next product as B operands straight from the accumulators (permuted-k
+//                  fragments), so waves never exchange state; only the chunk inputs are shared through LDS.
+//
+// bf16 (the training path) runs eight waves in two roles, two waves per SIMD, over two LDS buffer sets:
+//   waves 0-3  state part of chunk c (buffer set n), one 16-column slab of S each; they also stage V (and Q)
+//   waves 4-7  chunk factors of chunk c+1 (buffer set n^1); they also stage K, g, beta and scan g
+// The two roles share the workgroup barriers (three per chunk) but never each other's data within a chunk, so
+// each SIMD interleaves a latency-bound state wave with a latency-bound factor wave:
+//   P1  state: stage V/Q of c+1, K S, Q S, Y of c       | factors: stage K/g/beta of c+1, g scan
+//   P2  state: R, P R, O of c (staged)                   | factors: K K^T, Q K^T, diagonal inverse blocks of c+1
+//   P3  state: O store, S update of c                    | factors: off-diagonal inverse blocks of c+1
+// fp32 inputs (parity runs) do not fit two buffer sets in LDS; four waves run both roles for one chunk at a time.
 // Backward-recompute mode writes, per chunk, the entering state (bf16 [K][V]), R (bf16 [64][V]) and, from the
 // first V block, Tm and G for the gradient kernels, instead of O.
 #include "gdn_chunk_common.h"
@@ -18,175 +27,258 @@
 
 namespace gdn {
 
-template <typename T, int K, int BV, bool BWD>
-__global__ __launch_bounds__(NTHR) void fwd_fused_kernel(
+template <typename T, int K, int BV, bool BWD, bool WS>
+__global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const float* __restrict__ g,
     const float* __restrict__ beta, const float* __restrict__ h0, T* __restrict__ o, float* __restrict__ hT,
     T* __restrict__ wsH, T* __restrict__ wsR, T* __restrict__ wsTm, float* __restrict__ wsGc, int T_, int H,
     int V, int NT, float scale) {
   constexpr int PT = 16 / sizeof(T);
-  constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT, LF = CH + 4;
+  constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
   constexpr int NKT = K / 16;           // row tiles of the state slab
-  constexpr int NCW = BV / 16 / NWAVE;  // column tiles per wave
-  static_assert(NCW == 1, "each wave owns one 16-column slab of the state");
-  constexpr int SCR_F = 2 * CH * LF;  // fp32 scratch (A / inverse; then output staging)
-  static_assert(SCR_F * 4 >= (BWD ? K : CH) * LV * (int)sizeof(T), "staging must fit in the scratch region");
-  __shared__ __attribute__((aligned(16))) T sK[CH * LK];
-  __shared__ __attribute__((aligned(16))) T sQ[BWD ? 8 : CH * LK];
-  __shared__ __attribute__((aligned(16))) T sV[CH * LV];
-  __shared__ __attribute__((aligned(16))) T sP[BWD ? 8 : CH * LC];
-  __shared__ __attribute__((aligned(16))) T sTmB[CH * LC];
-  __shared__ __attribute__((aligned(16))) float sScr[SCR_F];
-  __shared__ float sG[CH], sB[CH], sGam[CH];
+  constexpr int NCW = BV / 16 / NWAVE;  // column tiles per state wave
+  static_assert(NCW == 1, "each state wave owns one 16-column slab of the state");
+  constexpr int NB = WS ? 2 : 1;                 // LDS buffer sets
+  constexpr int PMODE = BWD ? 0 : 1;             // P is needed only for O
+  constexpr int STG = (BWD ? K + CH : CH) * LV;  // staging: O, or the entering state then R
+  __shared__ __attribute__((aligned(16))) T sK[NB][CH * LK];
+  __shared__ __attribute__((aligned(16))) T sQ[NB][BWD ? 8 : CH * LK];
+  __shared__ __attribute__((aligned(16))) T sV[NB][CH * LV];
+  __shared__ __attribute__((aligned(16))) T sP[NB][BWD ? 8 : CH * LC];
+  __shared__ __attribute__((aligned(16))) T sTmB[NB][CH * LC];
+  __shared__ __attribute__((aligned(16))) float sA[CH * (CH + 4)];
+  __shared__ __attribute__((aligned(16))) float sD[4 * DBLK];
+  __shared__ __attribute__((aligned(16))) T stage[STG];
+  __shared__ float sG[NB][CH], sB[NB][CH], sGam[NB][CH];
 
-  const int vb = blockIdx.x, bh = blockIdx.y;
+  int vb, bh;
+  sweep_block(V / BV, gridDim.x * BV / V, vb, bh);
   const int b = bh / H, h = bh - b * H;
   const int v0 = vb * BV;
   const int w = wave_id(), l = lane_id();
-  const int c0 = 16 * w;  // this wave's column slab inside the V block
+  const int wr = w & (NWAVE - 1);            // wave index inside its role
+  const int tid = threadIdx.x & (NTHR - 1);  // thread index inside its role
   const int64_t sbase = (int64_t)bh * K * V;
-  T* stage = reinterpret_cast<T*>(sScr);
+  auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
+  auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
+  auto gtm_of = [&](int c) -> T* { return (BWD && vb == 0) ? wsTm + ((int64_t)bh * NT + c) * CH * CH : nullptr; };
 
-  f32x4 S[NKT];
-#pragma unroll
-  for (int t = 0; t < NKT; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      S[t][i] = h0 ? h0[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
-
-  RegTile<T, CH, K> rk, rq;
-  RegTile<T, CH, BV> rv;
+  // ---- factor role: K, g, beta of a chunk, and its factors --------------------------------------------------
+  RegTile<T, CH, K> rk;
   RegTok rt;
-  auto prefetch = [&](int c) {
-    const int t0 = c * CH, nvalid = min(CH, T_ - t0);
-    const int64_t row0 = ((int64_t)b * T_ + t0) * H + h;
-    rk.load(k + row0 * K, (int64_t)H * K, nvalid);
-    if constexpr (!BWD) rq.load(q + row0 * K, (int64_t)H * K, nvalid);
-    rv.load(v + row0 * V + v0, (int64_t)H * V, nvalid);
-    if (w == 0) rt.load(g, beta, row0, H, nvalid);
+  auto prefetch_f = [&](int c) {
+    rk.load(k + row0_of(c) * K, (int64_t)H * K, nvalid_of(c), tid);
+    if (wr == 0) rt.load(g, beta, row0_of(c), H, nvalid_of(c));
   };
-  prefetch(0);
-
-  for (int c = 0; c < NT; ++c) {
-    const int t0 = c * CH, nvalid = min(CH, T_ - t0);
-    const int64_t row0 = ((int64_t)b * T_ + t0) * H + h;
-    const int64_t cidx = (int64_t)bh * NT + c;
-    rk.store(sK, LK);
-    if constexpr (!BWD) rq.store(sQ, LK);
-    rv.store(sV, LV);
-    if (w == 0) {
+  auto store_f = [&](int c, int n) {
+    rk.store(sK[n], LK, tid);
+    if (wr == 0) {
       const float G = wave_inclusive_scan(rt.ok ? rt.g : 0.f);
-      sG[l] = G;
-      sB[l] = rt.ok ? rt.b : 0.f;
-      sGam[l] = __expf(G);
-      if (BWD && vb == 0) wsGc[cidx * CH + l] = G;
+      sG[n][l] = G;
+      sB[n][l] = rt.ok ? rt.b : 0.f;
+      sGam[n][l] = __expf(G);
+      if (BWD && vb == 0) wsGc[((int64_t)bh * NT + c) * CH + l] = G;
     }
-    __syncthreads();
-    if (c + 1 < NT) prefetch(c + 1);
+  };
+  auto kq_diag = [&](int c, int n) {
+    factors_kq<T, K, PMODE>(sK[n], sQ[n], sG[n], sB[n], scale, sA, sP[n], wr);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the diagonal block reads this wave's rows of A
+    return factors_diag<T>(sA, sD, sTmB[n], gtm_of(c), sB[n], wr);
+  };
 
-    T* gTm = (BWD && vb == 0) ? wsTm + cidx * CH * CH : nullptr;
-    const f32x4 Dw = chunk_factors_start<T, K, BWD ? 0 : 1>(sK, sQ, sG, sB, scale, sScr, sP, sTmB, gTm);
-    // independent of the inverse (overlaps its latency):  K S and Q S for this wave's columns, Y = V - gamma K S
+  // ---- state role: V (and Q) of a chunk, and the state part -------------------------------------------------
+  RegTile<T, CH, K> rq;
+  RegTile<T, CH, BV> rv;
+  auto prefetch_s = [&](int c) {
+    if constexpr (!BWD) rq.load(q + row0_of(c) * K, (int64_t)H * K, nvalid_of(c), tid);
+    rv.load(v + row0_of(c) * V + v0, (int64_t)H * V, nvalid_of(c), tid);
+  };
+  auto store_s = [&](int n) {
+    if constexpr (!BWD) rq.store(sQ[n], LK, tid);
+    rv.store(sV[n], LV, tid);
+  };
+  const int c0 = 16 * wr;  // the state wave's column slab inside the V block
+  f32x4 S[NKT];
+  f32x4 Y[4], QS[4];
+  typename Frag<T>::type Rd[2];
+  auto load_h0 = [&]() {
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        S[t][i] = h0 ? h0[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
+  };
+  // K S, Q S and Y = V - diag(gamma) K S of the chunk in buffer set n
+  auto state_C = [&](int n) {
     typename Frag<T>::type Sb[K / 32];
 #pragma unroll
     for (int s = 0; s < K / 32; ++s) Sb[s] = frag_acc2<T>(S[2 * s], S[2 * s + 1]);
-    f32x4 Y[4], QS[4];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
+    for (int rt_ = 0; rt_ < 4; ++rt_) {
       f32x4 ks = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < K / 32; ++s) mma(ks, frag_kc_perm(sK, LK, 16 * rt, 32 * s), Sb[s]);
+      for (int s = 0; s < K / 32; ++s) mma(ks, frag_kc_perm(sK[n], LK, 16 * rt_, 32 * s), Sb[s]);
       if constexpr (!BWD) {
-        QS[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        QS[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < K / 32; ++s) mma(QS[rt], frag_kc_perm(sQ, LK, 16 * rt, 32 * s), Sb[s]);
+        for (int s = 0; s < K / 32; ++s) mma(QS[rt_], frag_kc_perm(sQ[n], LK, 16 * rt_, 32 * s), Sb[s]);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * rt + acc_row(i);
-        Y[rt][i] = to_f(sV[r * LV + c0 + acc_col()]) - sGam[r] * ks[i];
+        const int r = 16 * rt_ + acc_row(i);
+        Y[rt_][i] = to_f(sV[n][r * LV + c0 + acc_col()]) - sGam[n][r] * ks[i];
       }
     }
-    chunk_factors_finish<T>(Dw, sB, sScr, sTmB, gTm);
-
-    // ---- R = TmB Y, output, state update (this wave's 16 columns) ------------------------------------------
-    typename Frag<T>::type Yb[2];
+  };
+  // R = TmB Y; O = s gamma QS + P R staged (backward mode: the entering S and R staged)
+  auto state_D = [&](int n) {
+    typename Frag<T>::type Yb[2], Rb[2];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) Yb[jb] = frag_acc2<T>(Y[2 * jb], Y[2 * jb + 1]);
     f32x4 R[4];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      R[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rt_ = 0; rt_ < 4; ++rt_) {
+      R[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) mma(R[rt], frag_kc_perm(sTmB, LC, 16 * rt, 32 * jb), Yb[jb]);
+      for (int jb = 0; jb < 2; ++jb) mma(R[rt_], frag_kc_perm(sTmB[n], LC, 16 * rt_, 32 * jb), Yb[jb]);
     }
-    const float GC = sG[CH - 1];
-    typename Frag<T>::type Rb[2], Rd[2];
+    const float GC = sG[n][CH - 1];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
       f32x4 d0, d1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        d0[i] = R[2 * jb][i] * __expf(GC - sG[32 * jb + acc_row(i)]);
-        d1[i] = R[2 * jb + 1][i] * __expf(GC - sG[32 * jb + 16 + acc_row(i)]);
+        d0[i] = R[2 * jb][i] * __expf(GC - sG[n][32 * jb + acc_row(i)]);
+        d1[i] = R[2 * jb + 1][i] * __expf(GC - sG[n][32 * jb + 16 + acc_row(i)]);
       }
       Rd[jb] = frag_acc2<T>(d0, d1);
       if constexpr (!BWD) Rb[jb] = frag_acc2<T>(R[2 * jb], R[2 * jb + 1]);
     }
     if constexpr (BWD) {
-      // entering state -> global h (bf16 [K][V] per chunk); R -> global (bf16 [64][V] per chunk)
 #pragma unroll
       for (int t = 0; t < NKT; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) stage[(16 * t + acc_row(i)) * LV + c0 + acc_col()] = from_f<T>(S[t][i]);
-      __syncthreads();
-      s2g_rows(wsH + cidx * K * V + v0, (int64_t)V, stage, LV, K, BV, K);
-      __syncthreads();
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
+      for (int rt_ = 0; rt_ < 4; ++rt_)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) stage[(16 * rt + acc_row(i)) * LV + c0 + acc_col()] = from_f<T>(R[rt][i]);
-      __syncthreads();
-      s2g_rows(wsR + cidx * CH * V + v0, (int64_t)V, stage, LV, CH, BV, CH);
+        for (int i = 0; i < 4; ++i) stage[(K + 16 * rt_ + acc_row(i)) * LV + c0 + acc_col()] = from_f<T>(R[rt_][i]);
     } else {
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
+      for (int rt_ = 0; rt_ < 4; ++rt_) {
         f32x4 pr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) mma(pr, frag_kc_perm(sP, LC, 16 * rt, 32 * jb), Rb[jb]);
+        for (int jb = 0; jb < 2; ++jb) mma(pr, frag_kc_perm(sP[n], LC, 16 * rt_, 32 * jb), Rb[jb]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int r = 16 * rt + acc_row(i);
-          stage[r * LV + c0 + acc_col()] = from_f<T>(scale * sGam[r] * QS[rt][i] + pr[i]);
+          const int r = 16 * rt_ + acc_row(i);
+          stage[r * LV + c0 + acc_col()] = from_f<T>(scale * sGam[n][r] * QS[rt_][i] + pr[i]);
         }
       }
-      __syncthreads();
-      s2g_rows(o + row0 * V + v0, (int64_t)H * V, stage, LV, CH, BV, nvalid);
     }
-    // S <- gamma_C S + K^T (exp(G_C - G) R)
-    const float gC = __expf(GC);
+  };
+  // staged rows -> global; S <- gamma_C S + K^T Rd
+  auto state_E = [&](int c, int n) {
+    const int64_t cidx = (int64_t)bh * NT + c;
+    if constexpr (BWD) {
+      s2g_rows(wsH + cidx * K * V + v0, (int64_t)V, stage, LV, K, BV, K);
+      s2g_rows(wsR + cidx * CH * V + v0, (int64_t)V, stage + K * LV, LV, CH, BV, CH);
+    } else {
+      s2g_rows(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, CH, BV, nvalid_of(c));
+    }
+    const float gC = __expf(sG[n][CH - 1]);
 #pragma unroll
     for (int t = 0; t < NKT; ++t) {
       S[t] *= gC;
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) mma(S[t], frag_oct_perm(sK, LK, 16 * t, 32 * jb), Rd[jb]);
+      for (int jb = 0; jb < 2; ++jb) mma(S[t], frag_oct_perm(sK[n], LK, 16 * t, 32 * jb), Rd[jb]);
     }
-    __syncthreads();
-  }
-  if (hT) {
+  };
+  auto store_hT = [&]() {
+    if (hT) {
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
+      for (int t = 0; t < NKT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) hT[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] = S[t][i];
+        for (int i = 0; i < 4; ++i)
+          hT[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] = S[t][i];
+    }
+  };
+
+  if constexpr (WS) {
+    // Both roles execute the same sequence of barriers: two in the prologue, then three per chunk.
+    if (w >= NWAVE) {
+      prefetch_f(0);
+      store_f(0, 0);
+      __syncthreads();  // chunk 0 inputs in buffer set 0
+      prefetch_f(min(1, NT - 1));
+      const f32x4 D0 = kq_diag(0, 0);
+      __syncthreads();
+      factors_merge<T>(D0, sA, sD, sTmB[0], gtm_of(0), sB[0], wr);
+      for (int c = 0; c < NT; ++c) {
+        const int nn = (c & 1) ^ 1;
+        const bool next = c + 1 < NT;
+        __syncthreads();  // P1: factors of c complete; buffer set nn free
+        if (next) store_f(c + 1, nn);
+        prefetch_f(min(c + 2, NT - 1));
+        __syncthreads();  // P2: inputs of c+1 in buffer set nn
+        f32x4 D = zero4();
+        if (next) D = kq_diag(c + 1, nn);
+        __syncthreads();  // P3: diagonal blocks of c+1 in sD
+        if (next) factors_merge<T>(D, sA, sD, sTmB[nn], gtm_of(c + 1), sB[nn], wr);
+      }
+    } else {
+      load_h0();
+      prefetch_s(0);
+      store_s(0);
+      __syncthreads();
+      prefetch_s(min(1, NT - 1));
+      __syncthreads();
+      for (int c = 0; c < NT; ++c) {
+        const int n = c & 1, nn = n ^ 1;
+        __syncthreads();  // P1
+        if (c + 1 < NT) store_s(nn);
+        prefetch_s(min(c + 2, NT - 1));
+        state_C(n);
+        __syncthreads();  // P2
+        state_D(n);
+        __syncthreads();  // P3
+        state_E(c, n);
+      }
+      store_hT();
+    }
+  } else {
+    load_h0();
+    prefetch_f(0);
+    prefetch_s(0);
+    for (int c = 0; c < NT; ++c) {
+      store_f(c, 0);
+      store_s(0);
+      __syncthreads();
+      if (c + 1 < NT) {
+        prefetch_f(c + 1);
+        prefetch_s(c + 1);
+      }
+      const f32x4 D = kq_diag(c, 0);
+      state_C(0);
+      __syncthreads();
+      factors_merge<T>(D, sA, sD, sTmB[0], gtm_of(c), sB[0], wr);
+      __syncthreads();
+      state_D(0);
+      __syncthreads();
+      state_E(c, 0);
+      __syncthreads();
+    }
+    store_hT();
   }
 }
 
 // ---------------------------------------------------------------------------------------------------------
 template <typename T, int K, bool BWD>
-static hipError_t fwd_fused_k(const ChunkArgs& a) {
+static hipError_t fwd_sweep_k(const ChunkArgs& a) {
   constexpr int BV = 64;
-  dim3 grid(a.V / BV, a.B * a.H);
-  fwd_fused_kernel<T, K, BV, BWD><<<grid, NTHR, 0, a.stream>>>(
+  constexpr bool WS = sizeof(T) == 2;
+  dim3 grid(a.V / BV * a.B * a.H);
+  fwd_sweep_kernel<T, K, BV, BWD, WS><<<grid, WS ? 2 * NTHR : NTHR, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.v), a.g, a.beta, a.h0,
       static_cast<T*>(a.o), BWD ? nullptr : a.hT, static_cast<T*>(a.ws.hs), static_cast<T*>(a.ws.Rs),
       static_cast<T*>(a.ws.Tm), a.ws.Gc, a.T, a.H, a.V, a.NT, a.scale);
@@ -195,10 +287,10 @@ static hipError_t fwd_fused_k(const ChunkArgs& a) {
 
 hipError_t launch_fwd(const ChunkArgs& a, bool backward) {
   if (a.dtype == DT_BF16) {
-    if (a.K == 64) return backward ? fwd_fused_k<bf16, 64, true>(a) : fwd_fused_k<bf16, 64, false>(a);
-    if (a.K == 128) return backward ? fwd_fused_k<bf16, 128, true>(a) : fwd_fused_k<bf16, 128, false>(a);
+    if (a.K == 64) return backward ? fwd_sweep_k<bf16, 64, true>(a) : fwd_sweep_k<bf16, 64, false>(a);
+    if (a.K == 128) return backward ? fwd_sweep_k<bf16, 128, true>(a) : fwd_sweep_k<bf16, 128, false>(a);
   } else {
-    if (a.K == 64) return backward ? fwd_fused_k<float, 64, true>(a) : fwd_fused_k<float, 64, false>(a);
+    if (a.K == 64) return backward ? fwd_sweep_k<float, 64, true>(a) : fwd_sweep_k<float, 64, false>(a);
   }
   return hipErrorInvalidValue;
 }

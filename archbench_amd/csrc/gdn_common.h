@@ -181,6 +181,23 @@ __device__ __forceinline__ typename Frag<T>::type frag_acc2(const f32x4& t0, con
 __device__ __forceinline__ int acc_row(int i) { return 4 * (lane_id() >> 4) + i; }
 __device__ __forceinline__ int acc_col() { return lane_id() & 15; }
 
+// Workgroup -> (V block, head) for the chunk sweeps.  Workgroups are dispatched round-robin over the 8 XCDs
+// (each with its own L2), so with a plain grid the NV V-block workgroups of one head land on different XCDs and
+// each reads the head's q/k from HBM.  With a 1-D grid of NV * BH workgroups and BH a multiple of 8, linear id L
+// runs on XCD L % 8; giving slot s = L / 8 of XCD x the head 8 * (s / NV) + x and V block s % NV keeps a head's
+// V blocks on one XCD, dispatched back to back, so the second read of its q/k is an L2 hit.
+__device__ __forceinline__ void sweep_block(int NV, int BH, int& vb, int& bh) {
+  const int L = blockIdx.x;
+  if ((BH & 7) == 0) {
+    const int x = L & 7, s = L >> 3;
+    bh = 8 * (s / NV) + x;
+    vb = s - (s / NV) * NV;
+  } else {
+    bh = L / NV;
+    vb = L - bh * NV;
+  }
+}
+
 // Sum over the 16 lanes that share a lane group (the columns of one accumulator tile row set).
 __device__ __forceinline__ float sum16(float x) {
   x += __shfl_xor(x, 1);
