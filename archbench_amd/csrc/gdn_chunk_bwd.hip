@@ -258,8 +258,13 @@ __device__ __forceinline__ float colsum_tile(const f32x4& x) {
   return s;
 }
 
+// Eight waves, two per SIMD: wave w owns row block rb = w & 3 (16 tokens of the chunk) and half hf = w >> 2 of
+// the output column tiles of every product; per-row reductions add the two halves through LDS.
+constexpr int IW = 2 * NWAVE;  // waves of the intra kernel
+constexpr int ITH = IW * 64;   // its threads
+
 template <typename T, int K, int V, int VS>
-__global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
+__global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const float* __restrict__ beta,
     const T* __restrict__ dout, const T* __restrict__ wsTm, const float* __restrict__ wsGc,
     const T* __restrict__ wsH, const T* __restrict__ wsR, const T* __restrict__ wsdH, const T* __restrict__ wsdR,
@@ -269,6 +274,7 @@ __global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
   constexpr int LK = K + PT, LC = CH + PT, LS = VS + PT;
   constexpr int NKT = K / 16;   // column tiles over K
   constexpr int NVT = VS / 16;  // column tiles over a V slab
+  constexpr int HK = NKT / 2, HV = NVT / 2, HC = 2;  // tiles per half: over K, over the slab, over the chunk
   // slab region: V phase {dO, R, dR, V : CH x LS; S0, dSC : K x LS}; K phase {dWn : CH x LK; dTm, M1, D, dPm : CH x LC}
   constexpr int SLAB_V = 4 * CH * LS + 2 * K * LS;
   constexpr int SLAB_K = CH * LK + 4 * CH * LC;
@@ -277,7 +283,8 @@ __global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
   __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
   __shared__ __attribute__((aligned(16))) T slab[SLAB];
-  __shared__ float sG[CH], sB[CH], sdG[CH], sLast[CH], sColZ[NWAVE][CH], sRed[NWAVE];
+  __shared__ float sG[CH], sB[CH], sdG[CH], sLast[CH], sColZ[NWAVE][CH], sRed[IW];
+  __shared__ float sHalf[6][CH];  // second-half partial row sums: rq, rk, dbV, rx, dbA, rz
 
   T* sdO = slab;
   T* sR = sdO + CH * LS;
@@ -291,77 +298,82 @@ __global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
   const int t0 = c * CH;
   const int nvalid = min(CH, T_ - t0);
   const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int rb = w & (NWAVE - 1), hf = w >> 2;
   const int64_t row0 = ((int64_t)b * T_ + t0) * H + h;
   const int64_t cidx = (int64_t)bh * NT + c;
 
-  // every global read of the chunk is issued up front as 16-byte register tiles (see RegTile); the second
-  // V slab is fetched while the first is computed
-  RegTile<T, CH, K> tq, tk;
-  RegTile<T, CH, CH> rtm;
-  RegTile<T, CH, VS> rdo, rv, rr, rdr;
-  RegTile<T, K, VS> rs0, rdsc;
+  // every global read of the chunk is issued up front as 16-byte register tiles (see RegTile); the next
+  // V slab is fetched while the current one is computed
+  RegTile<T, CH, K, ITH> tq, tk;
+  RegTile<T, CH, CH, ITH> rtm;
+  RegTile<T, CH, VS, ITH> rdo, rv, rr, rdr;
+  RegTile<T, K, VS, ITH> rs0, rdsc;
   auto load_slab = [&](int vs) {
-    rdo.load(dout + row0 * V + vs, (int64_t)H * V, nvalid);
-    rv.load(v + row0 * V + vs, (int64_t)H * V, nvalid);
-    rr.load(wsR + cidx * CH * V + vs, (int64_t)V, CH);
-    rdr.load(wsdR + cidx * CH * V + vs, (int64_t)V, CH);
-    rs0.load(wsH + cidx * K * V + vs, (int64_t)V, K);
-    rdsc.load(wsdH + cidx * K * V + vs, (int64_t)V, K);
+    rdo.load(dout + row0 * V + vs, (int64_t)H * V, nvalid, tid);
+    rv.load(v + row0 * V + vs, (int64_t)H * V, nvalid, tid);
+    rr.load(wsR + cidx * CH * V + vs, (int64_t)V, CH, tid);
+    rdr.load(wsdR + cidx * CH * V + vs, (int64_t)V, CH, tid);
+    rs0.load(wsH + cidx * K * V + vs, (int64_t)V, K, tid);
+    rdsc.load(wsdH + cidx * K * V + vs, (int64_t)V, K, tid);
   };
-  tq.load(q + row0 * K, (int64_t)H * K, nvalid);
-  tk.load(k + row0 * K, (int64_t)H * K, nvalid);
-  rtm.load(wsTm + cidx * CH * CH, (int64_t)CH, CH);
+  tq.load(q + row0 * K, (int64_t)H * K, nvalid, tid);
+  tk.load(k + row0 * K, (int64_t)H * K, nvalid, tid);
+  rtm.load(wsTm + cidx * CH * CH, (int64_t)CH, CH, tid);
   load_slab(0);
   if (tid < CH) {
     sG[tid] = wsGc[cidx * CH + tid];
     sB[tid] = beta[row0 + (int64_t)(tid < nvalid ? tid : 0) * H];
     if (tid >= nvalid) sB[tid] = 0.f;
   }
-  tq.store(sQ, LK);
-  tk.store(sK, LK);
-  rtm.store(sTm, LC);
+  tq.store(sQ, LK, tid);
+  tk.store(sK, LK, tid);
+  rtm.store(sTm, LC, tid);
 
   // ---- V phase: contractions over V, slab by slab -------------------------------------------------------
-  f32x4 aP[4], aTV[4], aQg[NKT], aKd[NKT], aWn[NKT];
+  // column tile j of this wave: n = HC*hf + j over the chunk, HK*hf + j over K, HV*hf + j over the slab
+  f32x4 aP[HC], aTV[HC], aQg[HK], aKd[HK], aWn[HK];
 #pragma unroll
-  for (int n = 0; n < 4; ++n) aP[n] = aTV[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < HC; ++j) aP[j] = aTV[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int n = 0; n < NKT; ++n) aQg[n] = aKd[n] = aWn[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < HK; ++j) aQg[j] = aKd[j] = aWn[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float dbV[4] = {0.f, 0.f, 0.f, 0.f};
   float sdot = 0.f;  // partial <dS_C, S0>
 
   for (int vs = 0; vs < V; vs += VS) {
-    rdo.store(sdO, LS);
-    rv.store(sV, LS);
-    rr.store(sR, LS);
-    rdr.store(sdR, LS);
-    rs0.store(sS0, LS);
-    rdsc.store(sdSC, LS);
+    rdo.store(sdO, LS, tid);
+    rv.store(sV, LS, tid);
+    rr.store(sR, LS, tid);
+    rdr.store(sdR, LS, tid);
+    rs0.store(sS0, LS, tid);
+    rdsc.store(sdSC, LS, tid);
     __syncthreads();
     if (vs + VS < V) load_slab(vs + VS);
-    for (int idx = tid; idx < K * VS; idx += NTHR) {
+    for (int idx = tid; idx < K * VS; idx += ITH) {
       const int d = idx / VS, n = idx - d * VS;
       sdot += to_f(sdSC[d * LS + n]) * to_f(sS0[d * LS + n]);
     }
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      mma_blk<true, true, VS>(aP[n], sdO, LS, 16 * w, sR, LS, 16 * n);
-      mma_blk<true, true, VS>(aTV[n], sdR, LS, 16 * w, sV, LS, 16 * n);
+    for (int j = 0; j < HC; ++j) {
+      const int n = HC * hf + j;
+      mma_blk<true, true, VS>(aP[j], sdO, LS, 16 * rb, sR, LS, 16 * n);
+      mma_blk<true, true, VS>(aTV[j], sdR, LS, 16 * rb, sV, LS, 16 * n);
     }
 #pragma unroll
-    for (int n = 0; n < NKT; ++n) {
-      mma_blk<true, true, VS>(aQg[n], sdO, LS, 16 * w, sS0, LS, 16 * n);
-      mma_blk<true, true, VS>(aKd[n], sR, LS, 16 * w, sdSC, LS, 16 * n);
-      mma_blk<true, true, VS>(aWn[n], sdR, LS, 16 * w, sS0, LS, 16 * n);
+    for (int j = 0; j < HK; ++j) {
+      const int n = HK * hf + j;
+      mma_blk<true, true, VS>(aQg[j], sdO, LS, 16 * rb, sS0, LS, 16 * n);
+      mma_blk<true, true, VS>(aKd[j], sR, LS, 16 * rb, sdSC, LS, 16 * n);
+      mma_blk<true, true, VS>(aWn[j], sdR, LS, 16 * rb, sS0, LS, 16 * n);
     }
     // dY = Tm^T dR for this slab: dv = beta dY, dbeta += dY . v
 #pragma unroll
-    for (int n = 0; n < NVT; ++n) {
+    for (int j = 0; j < HV; ++j) {
+      const int n = HV * hf + j;
       f32x4 dy = {0.f, 0.f, 0.f, 0.f};
-      mma_blk<false, false, CH>(dy, sTm, LC, 16 * w, sdR, LS, 16 * n);
+      mma_blk<false, false, CH>(dy, sTm, LC, 16 * rb, sdR, LS, 16 * n);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * w + acc_row(i), vc = 16 * n + acc_col();
+        const int r = 16 * rb + acc_row(i), vc = 16 * n + acc_col();
         dbV[i] += dy[i] * to_f(sV[r * LS + vc]);
         if (r < nvalid) dv[(row0 + (int64_t)r * H) * V + vs + vc] = from_f<T>(sB[r] * dy[i]);
       }
@@ -388,87 +400,83 @@ __global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
   const float GC = sG[CH - 1];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int r = 16 * w + acc_row(i);
+    const int r = 16 * rb + acc_row(i);
     gam[i] = __expf(sG[r]);
     dte[i] = __expf(GC - sG[r]);
     bet[i] = sB[r];
   }
-  // row dots from the V-phase accumulators
+  // row dots from the V-phase accumulators (this half's columns)
   float rq[4] = {0.f, 0.f, 0.f, 0.f}, rk[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int n = 0; n < NKT; ++n) {
+  for (int j = 0; j < HK; ++j) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * w + acc_row(i), d = 16 * n + acc_col();
-      rq[i] += aQg[n][i] * to_f(sQ[r * LK + d]);
-      rk[i] += aKd[n][i] * to_f(sK[r * LK + d]);
-      sdWn[r * LK + d] = from_f<T>(aWn[n][i]);
+      const int r = 16 * rb + acc_row(i), d = 16 * (HK * hf + j) + acc_col();
+      rq[i] += aQg[j][i] * to_f(sQ[r * LK + d]);
+      rk[i] += aKd[j][i] * to_f(sK[r * LK + d]);
+      sdWn[r * LK + d] = from_f<T>(aWn[j][i]);
     }
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    rq[i] = sum16(rq[i]);
-    rk[i] = sum16(rk[i]);
-    dbV[i] = sum16(dbV[i]);
   }
   __syncthreads();
 
   // dX = Tm^T dW = -Tm^T dWn (rows of this wave), and rx = dX . k
-  f32x4 aX[NKT];
+  f32x4 aX[HK];
   float rx[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int n = 0; n < NKT; ++n) {
+  for (int j = 0; j < HK; ++j) {
+    const int n = HK * hf + j;
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<false, false, CH>(t, sTm, LC, 16 * w, sdWn, LK, 16 * n);
-    aX[n] = -t;
+    mma_blk<false, false, CH>(t, sTm, LC, 16 * rb, sdWn, LK, 16 * n);
+    aX[j] = -t;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * w + acc_row(i), d = 16 * n + acc_col();
-      rx[i] += aX[n][i] * to_f(sK[r * LK + d]);
+      const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
+      rx[i] += aX[j][i] * to_f(sK[r * LK + d]);
     }
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) rx[i] = sum16(rx[i]);
   // dTm rows:  dTm_ij = -beta_j gamma_j (dWn K^T)_ij + beta_j (dR V^T)_ij
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
+  for (int j = 0; j < HC; ++j) {
+    const int n = HC * hf + j;
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<true, true, K>(t, sdWn, LK, 16 * w, sK, LK, 16 * n);
+    mma_blk<true, true, K>(t, sdWn, LK, 16 * rb, sK, LK, 16 * n);
     const int cc = 16 * n + acc_col();
     const float bj = sB[cc], gj = __expf(sG[cc]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * w + acc_row(i);
-      sdTm[r * LC + cc] = from_f<T>(-bj * gj * t[i] + bj * aTV[n][i]);
+      const int r = 16 * rb + acc_row(i);
+      sdTm[r * LC + cc] = from_f<T>(-bj * gj * t[i] + bj * aTV[j][i]);
     }
   }
   __syncthreads();
   // M1 = dTm Tm^T (rows of this wave)
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
+  for (int j = 0; j < HC; ++j) {
+    const int n = HC * hf + j;
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<true, true, CH>(t, sdTm, LC, 16 * w, sTm, LC, 16 * n);
+    mma_blk<true, true, CH>(t, sdTm, LC, 16 * rb, sTm, LC, 16 * n);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sM1[(16 * w + acc_row(i)) * LC + 16 * n + acc_col()] = from_f<T>(t[i]);
+    for (int i = 0; i < 4; ++i) sM1[(16 * rb + acc_row(i)) * LC + 16 * n + acc_col()] = from_f<T>(t[i]);
   }
   __syncthreads();
   // dA = -Tm^T M1, strict lower; with KK and QK recomputed: D, dPm, dbeta_A and the dG row/col sums
   float rz[4] = {0.f, 0.f, 0.f, 0.f}, dbA[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
+  for (int j = 0; j < HC; ++j) {
+    const int n = HC * hf + j;
     f32x4 da = {0.f, 0.f, 0.f, 0.f}, kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<false, false, CH>(da, sTm, LC, 16 * w, sM1, LC, 16 * n);
-    mma_blk<true, true, K>(kk, sK, LK, 16 * w, sK, LK, 16 * n);
-    mma_blk<true, true, K>(qk, sQ, LK, 16 * w, sK, LK, 16 * n);
+    mma_blk<false, false, CH>(da, sTm, LC, 16 * rb, sM1, LC, 16 * n);
+    mma_blk<true, true, K>(kk, sK, LK, 16 * rb, sK, LK, 16 * n);
+    mma_blk<true, true, K>(qk, sQ, LK, 16 * rb, sK, LK, 16 * n);
     f32x4 z;
     const int cc = 16 * n + acc_col();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * w + acc_row(i);
+      const int r = 16 * rb + acc_row(i);
       const float e = r >= cc ? __expf(fminf(sG[r] - sG[cc], 0.f)) : 0.f;
       const float dA = (r > cc) ? -da[i] : 0.f;
       const float Aval = bet[i] * kk[i] * e;
-      const float dP = (r >= cc) ? aP[n][i] : 0.f;
+      const float dP = (r >= cc) ? aP[j][i] : 0.f;
       const float Pval = scale * e * qk[i];
       sD[r * LC + cc] = from_f<T>(dA * bet[i] * e);
       sdPm[r * LC + cc] = from_f<T>(dP * scale * e);
@@ -477,49 +485,70 @@ __global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
       rz[i] += z[i];
     }
     const float cs = colsum_tile(z);
-    if (lg == 0) sColZ[w][cc] = cs;
+    if (lg == 0) sColZ[rb][cc] = cs;
   }
+  // per-row partial sums over this half's columns; the second half hands its sums to the first
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    rz[i] = sum16(rz[i]);
+    rq[i] = sum16(rq[i]);
+    rk[i] = sum16(rk[i]);
+    dbV[i] = sum16(dbV[i]);
+    rx[i] = sum16(rx[i]);
     dbA[i] = sum16(dbA[i]);
+    rz[i] = sum16(rz[i]);
+  }
+  if (hf == 1 && (l & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * rb + acc_row(i);
+      sHalf[0][r] = rq[i];
+      sHalf[1][r] = rk[i];
+      sHalf[2][r] = dbV[i];
+      sHalf[3][r] = rx[i];
+      sHalf[4][r] = dbA[i];
+      sHalf[5][r] = rz[i];
+    }
   }
   __syncthreads();
   // dq = s gamma dQg + dPm K
 #pragma unroll
-  for (int n = 0; n < NKT; ++n) {
+  for (int j = 0; j < HK; ++j) {
+    const int n = HK * hf + j;
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<true, false, CH>(t, sdPm, LC, 16 * w, sK, LK, 16 * n);
+    mma_blk<true, false, CH>(t, sdPm, LC, 16 * rb, sK, LK, 16 * n);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * w + acc_row(i), d = 16 * n + acc_col();
-      if (r < nvalid) dq[(row0 + (int64_t)r * H) * K + d] = from_f<T>(scale * gam[i] * aQg[n][i] + t[i]);
+      const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
+      if (r < nvalid) dq[(row0 + (int64_t)r * H) * K + d] = from_f<T>(scale * gam[i] * aQg[j][i] + t[i]);
     }
   }
   // dk = dte dKd + dPm^T Q + beta gamma dX + D K + D^T K
 #pragma unroll
-  for (int n = 0; n < NKT; ++n) {
+  for (int j = 0; j < HK; ++j) {
+    const int n = HK * hf + j;
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<false, false, CH>(t, sdPm, LC, 16 * w, sQ, LK, 16 * n);
-    mma_blk<true, false, CH>(t, sD, LC, 16 * w, sK, LK, 16 * n);
-    mma_blk<false, false, CH>(t, sD, LC, 16 * w, sK, LK, 16 * n);
+    mma_blk<false, false, CH>(t, sdPm, LC, 16 * rb, sQ, LK, 16 * n);
+    mma_blk<true, false, CH>(t, sD, LC, 16 * rb, sK, LK, 16 * n);
+    mma_blk<false, false, CH>(t, sD, LC, 16 * rb, sK, LK, 16 * n);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * w + acc_row(i), d = 16 * n + acc_col();
+      const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
       if (r < nvalid)
         dk[(row0 + (int64_t)r * H) * K + d] =
-            from_f<T>(dte[i] * aKd[n][i] + t[i] + bet[i] * gam[i] * aX[n][i]);
+            from_f<T>(dte[i] * aKd[j][i] + t[i] + bet[i] * gam[i] * aX[j][i]);
     }
   }
-  // dbeta and the per-row part of dG (one lane per row)
-  if ((l & 15) == 0) {
+  // dbeta and the per-row part of dG (first half, one lane per row)
+  if (hf == 0 && (l & 15) == 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * w + acc_row(i);
-      const float db = gam[i] * rx[i] + dbV[i] + dbA[i];
+      const int r = 16 * rb + acc_row(i);
+      const float q_ = rq[i] + sHalf[0][r], k_ = rk[i] + sHalf[1][r], v_ = dbV[i] + sHalf[2][r];
+      const float x_ = rx[i] + sHalf[3][r], a_ = dbA[i] + sHalf[4][r], z_ = rz[i] + sHalf[5][r];
+      const float db = gam[i] * x_ + v_ + a_;
       if (r < nvalid) dbeta[row0 + (int64_t)r * H] = db;
-      sdG[r] = scale * gam[i] * rq[i] - dte[i] * rk[i] + bet[i] * gam[i] * rx[i] + rz[i];
-      sLast[r] = dte[i] * rk[i];
+      sdG[r] = scale * gam[i] * q_ - dte[i] * k_ + bet[i] * gam[i] * x_ + z_;
+      sLast[r] = dte[i] * k_;
     }
   }
   __syncthreads();
@@ -529,7 +558,10 @@ __global__ __launch_bounds__(NTHR) void bwd_intra_kernel(
     float last = sLast[l];
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) last += __shfl_xor(last, off);
-    last += __expf(GC) * (sRed[0] + sRed[1] + sRed[2] + sRed[3]);
+    float red = 0.f;
+#pragma unroll
+    for (int i = 0; i < IW; ++i) red += sRed[i];
+    last += __expf(GC) * red;
     if (l == CH - 1) x += last;
     const float incl = wave_inclusive_scan(x);
     const float total = __shfl(incl, 63);
@@ -553,7 +585,7 @@ template <typename T, int K, int V>
 static hipError_t bwd_intra_kv(const ChunkArgs& a) {
   constexpr int VS = sizeof(T) == 2 ? 64 : 32;
   dim3 grid(a.NT, a.B * a.H);
-  bwd_intra_kernel<T, K, V, VS><<<grid, NTHR, 0, a.stream>>>(
+  bwd_intra_kernel<T, K, V, VS><<<grid, ITH, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.v), a.beta,
       static_cast<const T*>(a.dout), static_cast<const T*>(a.ws.Tm), a.ws.Gc, static_cast<const T*>(a.ws.hs),
       static_cast<const T*>(a.ws.Rs), static_cast<const T*>(a.ws.dhs), static_cast<const T*>(a.ws.dRs),

@@ -125,23 +125,23 @@ __device__ __forceinline__ void tm_column(const float* sA, const float* sD, cons
   for (int i = 0; i < J; ++i) put_tm_block<T, LC>(sTmB, gTm, sB, i, J, zero4());
 }
 
-// A ROWS x COLS tile of T held in registers as 16-byte vectors (ROWS*COLS*sizeof(T)/16 split over the NTHR
-// threads of a four-wave group; tid = thread index inside the group), used to prefetch the next chunk while the
+// A ROWS x COLS tile of T held in registers as 16-byte vectors (ROWS*COLS*sizeof(T)/16 split over the NTH
+// threads of a group; tid = thread index inside the group), used to prefetch the next chunk while the
 // current one is computed.  Loads are unconditional: rows past the end of the sequence read row 0 instead
 // (always in bounds) and are zeroed only when the tile is stored, so no wait for the data is forced at load time.
-template <typename T, int ROWS, int COLS>
+template <typename T, int ROWS, int COLS, int NTH = NTHR>
 struct RegTile {
   static constexpr int E = 16 / sizeof(T);
   static constexpr int VPR = COLS / E;
-  static constexpr int N = ROWS * VPR / NTHR;
-  static_assert(N * NTHR == ROWS * VPR && N >= 1 && N <= 32, "tile must split evenly over the workgroup");
+  static constexpr int N = ROWS * VPR / NTH;
+  static_assert(N * NTH == ROWS * VPR && N >= 1 && N <= 32, "tile must split evenly over the thread group");
   uint4 r[N];
   uint32_t ok;
   __device__ __forceinline__ void load(const T* g, int64_t gld, int valid, int tid) {
     ok = 0;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const int idx = tid + i * NTHR, row = idx / VPR, c = (idx - row * VPR) * E;
+      const int idx = tid + i * NTH, row = idx / VPR, c = (idx - row * VPR) * E;
       const bool in = row < valid;
       ok |= (in ? 1u : 0u) << i;
       r[i] = *reinterpret_cast<const uint4*>(g + (in ? row : 0) * gld + c);
@@ -150,7 +150,7 @@ struct RegTile {
   __device__ __forceinline__ void store(T* s, int sld, int tid) const {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const int idx = tid + i * NTHR, row = idx / VPR, c = (idx - row * VPR) * E;
+      const int idx = tid + i * NTH, row = idx / VPR, c = (idx - row * VPR) * E;
       *reinterpret_cast<uint4*>(s + row * sld + c) = ((ok >> i) & 1u) ? r[i] : make_uint4(0, 0, 0, 0);
     }
   }
