@@ -283,6 +283,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
   __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
   __shared__ __attribute__((aligned(16))) T slab[SLAB];
+  __shared__ __attribute__((aligned(16))) T sdv[CH * LS];  // dv of the current slab, for the coalesced store
   __shared__ float sG[CH], sB[CH], sdG[CH], sLast[CH], sColZ[NWAVE][CH], sRed[IW];
   __shared__ float sHalf[6][CH];  // second-half partial row sums: rq, rk, dbV, rx, dbA, rz
 
@@ -375,10 +376,11 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       for (int i = 0; i < 4; ++i) {
         const int r = 16 * rb + acc_row(i), vc = 16 * n + acc_col();
         dbV[i] += dy[i] * to_f(sV[r * LS + vc]);
-        if (r < nvalid) dv[(row0 + (int64_t)r * H) * V + vs + vc] = from_f<T>(sB[r] * dy[i]);
+        sdv[r * LS + vc] = from_f<T>(sB[r] * dy[i]);
       }
     }
     __syncthreads();
+    s2g_rows<T, ITH>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, CH, VS, nvalid);
   }
   // block reduce <dS_C, S0>
   {
@@ -510,6 +512,10 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     }
   }
   __syncthreads();
+  // dq and dk are staged (bf16, stride LK) in the regions of dWn and dTm/M1, free from here on
+  T* sdq = sdWn;
+  T* sdk = sdTm;
+  static_assert(CH * LK <= 2 * CH * LC, "dk staging must fit in the dTm and M1 regions");
   // dq = s gamma dQg + dPm K
 #pragma unroll
   for (int j = 0; j < HK; ++j) {
@@ -519,7 +525,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
-      if (r < nvalid) dq[(row0 + (int64_t)r * H) * K + d] = from_f<T>(scale * gam[i] * aQg[j][i] + t[i]);
+      sdq[r * LK + d] = from_f<T>(scale * gam[i] * aQg[j][i] + t[i]);
     }
   }
   // dk = dte dKd + dPm^T Q + beta gamma dX + D K + D^T K
@@ -533,9 +539,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
-      if (r < nvalid)
-        dk[(row0 + (int64_t)r * H) * K + d] =
-            from_f<T>(dte[i] * aKd[j][i] + t[i] + bet[i] * gam[i] * aX[j][i]);
+      sdk[r * LK + d] = from_f<T>(dte[i] * aKd[j][i] + t[i] + bet[i] * gam[i] * aX[j][i]);
     }
   }
   // dbeta and the per-row part of dG (first half, one lane per row)
@@ -552,6 +556,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     }
   }
   __syncthreads();
+  s2g_rows<T, ITH>(dq + row0 * K, (int64_t)H * K, sdq, LK, CH, K, nvalid);
+  s2g_rows<T, ITH>(dk + row0 * K, (int64_t)H * K, sdk, LK, CH, K, nvalid);
   if (w == 0) {
     // dG_r -= colsum_r;  dG_last += sum_r dte_r rk_r + gamma_C <dS_C, S0>;  dg = reverse cumsum of dG
     float x = sdG[l] - (sColZ[0][l] + sColZ[1][l] + sColZ[2][l] + sColZ[3][l]);

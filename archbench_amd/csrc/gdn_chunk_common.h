@@ -171,12 +171,13 @@ struct RegTok {
   }
 };
 
-// Copy a rows x cols tile from LDS (stride sld) to global (row stride gld), 16-byte vectors, rows < valid only.
-template <typename T>
+// Copy a rows x cols tile from LDS (stride sld) to global (row stride gld), 16-byte vectors, rows < valid only,
+// by the NTH threads of the workgroup.
+template <typename T, int NTH = NTHR>
 __device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld, int rows, int cols, int valid) {
   constexpr int E = 16 / sizeof(T);
   const int vpr = cols / E;
-  for (int idx = threadIdx.x; idx < rows * vpr; idx += NTHR) {
+  for (int idx = threadIdx.x; idx < rows * vpr; idx += NTH) {
     const int r = idx / vpr, c = (idx - r * vpr) * E;
     if (r < valid) *reinterpret_cast<uint4*>(g + r * gld + c) = *reinterpret_cast<const uint4*>(s + r * sld + c);
   }
