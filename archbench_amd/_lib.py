@@ -31,12 +31,16 @@ SIGNATURES = {
     "gdn_chunk_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_chunk_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz,
                            _i, _i, _i, _i, _i, _f, _i, _p]),
+    "gdn_chunk_stash_bytes": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
+    "gdn_chunk_fwd_stash": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _f, _i, _p]),
+    "gdn_chunk_bwd_stashed": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _sz,
+                                   _i, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_recurrent_step": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_profile_enable": (_i, [_i]),
     "gdn_profile_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
     "gdn_profile_stage_name": (ctypes.c_char_p, [_i]),
 }
-PROFILE_STAGES = 5
+PROFILE_STAGES = 6
 
 _lock = threading.Lock()
 _lib = None
@@ -99,6 +103,14 @@ def ws_bytes(kind: str, B: int, T: int, H: int, K: int, V: int, dtype: torch.dty
     fn = load().gdn_chunk_fwd_ws_bytes if kind == "fwd" else load().gdn_chunk_bwd_ws_bytes
     check(fn(B, T, H, K, V, dtype_code(dtype), ctypes.byref(out)), f"gdn_chunk_{kind}_ws_bytes")
     return out.value
+
+
+def stash_bytes(B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype) -> tuple[int, int]:
+    """(stash bytes for gdn_chunk_fwd_stash, workspace bytes for gdn_chunk_bwd_stashed)."""
+    st, ws = _sz(0), _sz(0)
+    check(load().gdn_chunk_stash_bytes(B, T, H, K, V, dtype_code(dtype), ctypes.byref(st), ctypes.byref(ws)),
+          "gdn_chunk_stash_bytes")
+    return st.value, ws.value
 
 
 class StageTimer:

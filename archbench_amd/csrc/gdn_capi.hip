@@ -21,7 +21,7 @@ static int fail(int code, const char* fmt, ...) {
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, bool backward, ChunkWs* carve, void* base) {
+size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, ChunkWs* carve, void* base) {
   const size_t es = dtype == DT_BF16 ? 2 : 4;
   const size_t NT = (size_t)(T + CH_TOKENS - 1) / CH_TOKENS;
   const size_t BH = (size_t)B * H;
@@ -33,15 +33,24 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, bool backwar
     return r;
   };
   ChunkWs ws{};
-  if (backward) {
+  if (parts & WS_STASH) {
     ws.Tm = take(BH * NT * CH_TOKENS * CH_TOKENS * es);
     ws.Gc = static_cast<float*>(take(BH * NT * CH_TOKENS * 4));
     ws.hs = take(BH * NT * (size_t)K * V * es);
     ws.Rs = take(BH * NT * CH_TOKENS * (size_t)V * es);
+  }
+  if (parts & WS_GRAD) {
     ws.dhs = take(BH * NT * (size_t)K * V * es);
     ws.dRs = take(BH * NT * CH_TOKENS * (size_t)V * es);
   }
-  if (carve) *carve = ws;
+  if (carve) {
+    if (parts & WS_STASH) {
+      carve->Tm = ws.Tm; carve->Gc = ws.Gc; carve->hs = ws.hs; carve->Rs = ws.Rs;
+    }
+    if (parts & WS_GRAD) {
+      carve->dhs = ws.dhs; carve->dRs = ws.dRs;
+    }
+  }
   return off;
 }
 
@@ -66,8 +75,8 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
 
 
 // ---- per-stage event timing (diagnostic; off unless gdn_profile_enable(1) was called on this thread) ----
-enum Stage { ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_COUNT };
-static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step"};
+enum Stage { ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_COUNT };
+static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step", "fwd_stash"};
 struct ProfRec { int stage; hipEvent_t a, b; };
 struct Prof {
   bool on = false;
@@ -160,7 +169,7 @@ int gdn_chunk_fwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t*
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
-  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, false, nullptr, nullptr);
+  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, 0, nullptr, nullptr);
   return GDN_OK;
 }
 
@@ -168,13 +177,28 @@ int gdn_chunk_bwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t*
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
-  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, true, nullptr, nullptr);
+  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH | WS_GRAD, nullptr, nullptr);
   return GDN_OK;
 }
 
-int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
-                  const float* h0, void* o, float* hT, void* ws, size_t ws_bytes, int B, int T, int H, int K,
-                  int V, float scale, int dtype, void* stream) {
+int gdn_chunk_stash_bytes(int B, int T, int H, int K, int V, int dtype, size_t* stash_bytes,
+                          size_t* bwd_ws_bytes) {
+  g_err[0] = 0;
+  if (int e = check_common(B, T, H, K, V, dtype)) return e;
+  if (!stash_bytes || !bwd_ws_bytes) return fail(GDN_ERR_ARG, "stash_bytes or bwd_ws_bytes is NULL");
+  *stash_bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH, nullptr, nullptr);
+  *bwd_ws_bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_GRAD, nullptr, nullptr);
+  return GDN_OK;
+}
+
+}  // extern "C"
+
+namespace gdn {
+
+// Forward: o and hT, and with `stash` the per-chunk intermediates for gdn_chunk_bwd_stashed.
+static int chunk_fwd_impl(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                          const float* h0, void* o, float* hT, void* ws, size_t ws_bytes, int B, int T, int H,
+                          int K, int V, float scale, int dtype, void* stream, bool stash) {
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!chunk_shape_supported(K, V, dtype))
@@ -188,21 +212,25 @@ int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g, c
   }
   if (!q || !k || !v || !g || !beta || !o) return fail(GDN_ERR_ARG, "null input/output pointer");
   ChunkArgs a{};
-  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, false, &a.ws, ws);
+  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, stash ? WS_STASH : 0, &a.ws, ws);
   if (need && (!ws || ws_bytes < need))
-    return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
+    return fail(GDN_ERR_WORKSPACE, "%s of %zu bytes needed, %zu given", stash ? "stash" : "workspace", need,
+                ws ? ws_bytes : (size_t)0);
   a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.h0 = h0; a.o = o; a.hT = hT;
   a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
-  const hipError_t e = timed(ST_FWD, st, [&] { return launch_fwd(a, false); });
+  const hipError_t e = stash ? timed(ST_FWD_STASH, st, [&] { return launch_fwd(a, FWD_STASH); })
+                             : timed(ST_FWD, st, [&] { return launch_fwd(a, FWD_OUT); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "chunk forward launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }
 
-int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
-                  const float* h0, const void* dout, const float* dhT, void* dq, void* dk, void* dv, float* dg,
-                  float* dbeta, float* dh0, void* ws, size_t ws_bytes, int B, int T, int H, int K, int V,
-                  float scale, int dtype, void* stream) {
+// Backward; without `stashed` the per-chunk intermediates are recomputed first.
+static int chunk_bwd_impl(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                          const float* h0, const void* dout, const float* dhT, void* dq, void* dk, void* dv,
+                          float* dg, float* dbeta, float* dh0, const void* stash, size_t stash_bytes, void* ws,
+                          size_t ws_bytes, int B, int T, int H, int K, int V, float scale, int dtype, void* stream,
+                          bool stashed) {
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!chunk_shape_supported(K, V, dtype))
@@ -217,18 +245,61 @@ int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, c
   if (!q || !k || !v || !g || !beta || !dout || !dq || !dk || !dv || !dg || !dbeta)
     return fail(GDN_ERR_ARG, "null input/output pointer");
   ChunkArgs a{};
-  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, true, &a.ws, ws);
+  if (stashed) {
+    // the stash is only read (the kernels take it through the same carve-up as the recompute path's workspace)
+    const size_t sneed = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH, &a.ws, const_cast<void*>(stash));
+    if (!stash || stash_bytes < sneed)
+      return fail(GDN_ERR_WORKSPACE, "stash of %zu bytes needed, %zu given", sneed,
+                  stash ? stash_bytes : (size_t)0);
+  }
+  const int parts = stashed ? WS_GRAD : (WS_STASH | WS_GRAD);
+  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, parts, &a.ws, ws);
   if (!ws || ws_bytes < need)
     return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
   a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.h0 = h0;
   a.dout = dout; a.dhT = dhT; a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dh0 = dh0;
   a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
-  hipError_t e = timed(ST_BWD_RECOMP, st, [&] { return launch_fwd(a, true); });
+  hipError_t e = hipSuccess;
+  if (!stashed) e = timed(ST_BWD_RECOMP, st, [&] { return launch_fwd(a, FWD_RECOMPUTE); });
   if (e == hipSuccess) e = timed(ST_BWD_STATE, st, [&] { return launch_bwd_state(a); });
   if (e == hipSuccess) e = timed(ST_BWD_INTRA, st, [&] { return launch_bwd_intra(a); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "chunk backward launch: %s", hipGetErrorString(e));
   return GDN_OK;
+}
+
+}  // namespace gdn
+
+extern "C" {
+
+int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                  const float* h0, void* o, float* hT, void* ws, size_t ws_bytes, int B, int T, int H, int K,
+                  int V, float scale, int dtype, void* stream) {
+  return chunk_fwd_impl(q, k, v, g, beta, h0, o, hT, ws, ws_bytes, B, T, H, K, V, scale, dtype, stream, false);
+}
+
+int gdn_chunk_fwd_stash(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                        const float* h0, void* o, float* hT, void* stash, size_t stash_bytes, int B, int T, int H,
+                        int K, int V, float scale, int dtype, void* stream) {
+  return chunk_fwd_impl(q, k, v, g, beta, h0, o, hT, stash, stash_bytes, B, T, H, K, V, scale, dtype, stream,
+                        true);
+}
+
+int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                  const float* h0, const void* dout, const float* dhT, void* dq, void* dk, void* dv, float* dg,
+                  float* dbeta, float* dh0, void* ws, size_t ws_bytes, int B, int T, int H, int K, int V,
+                  float scale, int dtype, void* stream) {
+  return chunk_bwd_impl(q, k, v, g, beta, h0, dout, dhT, dq, dk, dv, dg, dbeta, dh0, nullptr, 0, ws, ws_bytes, B,
+                        T, H, K, V, scale, dtype, stream, false);
+}
+
+int gdn_chunk_bwd_stashed(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                          const float* h0, const void* dout, const float* dhT, void* dq, void* dk, void* dv,
+                          float* dg, float* dbeta, float* dh0, const void* stash, size_t stash_bytes, void* ws,
+                          size_t ws_bytes, int B, int T, int H, int K, int V, float scale, int dtype,
+                          void* stream) {
+  return chunk_bwd_impl(q, k, v, g, beta, h0, dout, dhT, dq, dk, dv, dg, dbeta, dh0, stash, stash_bytes, ws,
+                        ws_bytes, B, T, H, K, V, scale, dtype, stream, true);
 }
 
 int gdn_recurrent_step(const void* q, const void* k, const void* v, const float* g, const float* beta,

@@ -46,7 +46,6 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void bwd_state_kernel(
   __shared__ __attribute__((aligned(16))) T sTmB[NB][CH * LC];  // Tm diag(beta)
   __shared__ __attribute__((aligned(16))) float sA[CH * (CH + 4)];
   __shared__ __attribute__((aligned(16))) float sD[4 * DBLK];
-  __shared__ __attribute__((aligned(16))) T stage[CH * LV];  // dR of the chunk, for the coalesced store
   __shared__ float sG[NB][CH], sB[NB][CH], sGam[NB][CH];
 
   int vb, bh;
@@ -94,6 +93,7 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void bwd_state_kernel(
     rdo.store(sdO[n], LV, tid);
   };
   const int c0 = 16 * wr;
+  const int ncb = V / 16, cb = vb * (BV / 16) + wr;  // fragment-layout column block of a state wave
   f32x4 dS[NKT];
   f32x4 dR[4];
   typename Frag<T>::type dOg[2], Zb[2];
@@ -104,16 +104,14 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void bwd_state_kernel(
       for (int i = 0; i < 4; ++i)
         dS[t][i] = dhT ? dhT[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
   };
-  // C: dS leaving the chunk -> dh (bf16 [K][V] per chunk);  dR = diag(exp(G_C - G)) K dS + P^T dO
+  // C: dS leaving the chunk -> dh (fragment layout);  dR = diag(exp(G_C - G)) K dS + P^T dO
   auto state_C = [&](int c, int n) {
-    T* dh = wsdH + ((int64_t)bh * NT + c) * K * V + v0 + c0 + acc_col();
     typename Frag<T>::type dSb[K / 32];
 #pragma unroll
-    for (int s = 0; s < K / 32; ++s) dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
-#pragma unroll
-    for (int t = 0; t < NKT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dh[(16 * t + acc_row(i)) * V] = from_f<T>(dS[t][i]);
+    for (int s = 0; s < K / 32; ++s) {
+      dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
+      store_fragblk<T>(wsdH + ((int64_t)bh * NT + c) * K * V, s, cb, ncb, dSb[s]);
+    }
     const float GC = sG[n][CH - 1];
 #pragma unroll
     for (int rt_ = 0; rt_ < 4; ++rt_) {
@@ -136,11 +134,14 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void bwd_state_kernel(
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib) mma(dR[rt_], frag_oct(sP[n], LC, 16 * rt_, 32 * ib), dOb[ib]);
   };
-  // D: Z = gamma (TmB^T dR)  (W^T dR = K^T Z);  dR staged
-  auto state_D = [&](int n) {
+  // D: dR -> global (fragment layout);  Z = gamma (TmB^T dR)  (W^T dR = K^T Z)
+  auto state_D = [&](int c, int n) {
     typename Frag<T>::type dRb[2];
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) dRb[jb] = frag_acc2<T>(dR[2 * jb], dR[2 * jb + 1]);
+    for (int jb = 0; jb < 2; ++jb) {
+      dRb[jb] = frag_acc2<T>(dR[2 * jb], dR[2 * jb + 1]);
+      store_fragblk<T>(wsdR + ((int64_t)bh * NT + c) * CH * V, jb, cb, ncb, dRb[jb]);
+    }
     f32x4 Z[4];
 #pragma unroll
     for (int rt_ = 0; rt_ < 4; ++rt_) {
@@ -152,14 +153,9 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void bwd_state_kernel(
     }
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) Zb[jb] = frag_acc2<T>(Z[2 * jb], Z[2 * jb + 1]);
-#pragma unroll
-    for (int rt_ = 0; rt_ < 4; ++rt_)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) stage[(16 * rt_ + acc_row(i)) * LV + c0 + acc_col()] = from_f<T>(dR[rt_][i]);
   };
-  // E: dR -> global;  dS <- gamma_C dS + s Q^T (gamma dO) - K^T Z
-  auto state_E = [&](int c, int n) {
-    s2g_rows(wsdR + ((int64_t)bh * NT + c) * CH * V + v0, (int64_t)V, stage, LV, CH, BV, CH);
+  // E: dS <- gamma_C dS + s Q^T (gamma dO) - K^T Z
+  auto state_E = [&](int n) {
     const float gC = __expf(sG[n][CH - 1]);
 #pragma unroll
     for (int t = 0; t < NKT; ++t) {
@@ -217,9 +213,9 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void bwd_state_kernel(
         prefetch_s(max(c - 2, 0));
         state_C(c, n);
         __syncthreads();  // P2
-        state_D(n);
+        state_D(c, n);
         __syncthreads();  // P3
-        state_E(c, n);
+        state_E(n);
       }
       store_dh0();
     }
@@ -240,9 +236,9 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void bwd_state_kernel(
       state_C(c, 0);
       factors_merge<T>(D, sA, sD, sTmB[0], nullptr, sB[0], wr);
       __syncthreads();
-      state_D(0);
+      state_D(c, 0);
       __syncthreads();
-      state_E(c, 0);
+      state_E(0);
       __syncthreads();
     }
     store_dh0();
@@ -307,15 +303,16 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   // V slab is fetched while the current one is computed
   RegTile<T, CH, K, ITH> tq, tk;
   RegTile<T, CH, CH, ITH> rtm;
-  RegTile<T, CH, VS, ITH> rdo, rv, rr, rdr;
-  RegTile<T, K, VS, ITH> rs0, rdsc;
+  RegTile<T, CH, VS, ITH> rdo, rv;
+  FragTile<T, CH, VS, ITH> rr, rdr;
+  FragTile<T, K, VS, ITH> rs0, rdsc;
   auto load_slab = [&](int vs) {
     rdo.load(dout + row0 * V + vs, (int64_t)H * V, nvalid, tid);
     rv.load(v + row0 * V + vs, (int64_t)H * V, nvalid, tid);
-    rr.load(wsR + cidx * CH * V + vs, (int64_t)V, CH, tid);
-    rdr.load(wsdR + cidx * CH * V + vs, (int64_t)V, CH, tid);
-    rs0.load(wsH + cidx * K * V + vs, (int64_t)V, K, tid);
-    rdsc.load(wsdH + cidx * K * V + vs, (int64_t)V, K, tid);
+    rr.load(wsR + cidx * CH * V, V / 16, vs / 16, tid);
+    rdr.load(wsdR + cidx * CH * V, V / 16, vs / 16, tid);
+    rs0.load(wsH + cidx * K * V, V / 16, vs / 16, tid);
+    rdsc.load(wsdH + cidx * K * V, V / 16, vs / 16, tid);
   };
   tq.load(q + row0 * K, (int64_t)H * K, nvalid, tid);
   tk.load(k + row0 * K, (int64_t)H * K, nvalid, tid);

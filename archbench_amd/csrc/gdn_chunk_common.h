@@ -171,6 +171,53 @@ struct RegTok {
   }
 };
 
+// ---- fragment layout of the per-chunk [R][V] matrices in the workspace (states, R, their gradients) --------
+// The sweeps hold S, R, dS and dR as MFMA accumulators and already form their permuted-k fragments (frag_acc2:
+// element p of lane l is row 32 s + fragblk_row(l >> 4, p) of column 16 cb + (l & 15)).  Those fragments are
+// stored as they are: block (s, cb) of an [R][V] matrix starts at element (s * V/16 + cb) * 512 and holds 8
+// elements per lane, lane-contiguous, so each wave writes a block as one contiguous vector store per lane,
+// with no staging.  The gradient kernel turns blocks back into row-major LDS tiles (FragTile).
+__device__ __forceinline__ int fragblk_row(int g, int p) { return p < 4 ? 4 * g + p : 16 + 4 * g + (p - 4); }
+template <typename T>
+__device__ __forceinline__ void store_fragblk(T* base, int s, int cb, int ncb, const typename Frag<T>::type& f) {
+  *reinterpret_cast<typename Frag<T>::type*>(base + ((int64_t)(s * ncb + cb) * 64 + lane_id()) * 8) = f;
+}
+
+// Columns [16 cb0, 16 cb0 + VS) of a fragment-layout [R][V] matrix (ncb = V / 16): loaded into registers as
+// 8-element vectors by the NTH threads of the workgroup (tid = thread index), then written to a row-major LDS
+// tile [R][ld] (column 0 = column 16 cb0).
+template <typename T, int R, int VS, int NTH>
+struct FragTile {
+  using F = typename Frag<T>::type;
+  static constexpr int NVEC = R * VS / 8;
+  static constexpr int N = (NVEC + NTH - 1) / NTH;
+  static constexpr int NCBS = VS / 16;
+  static_assert(R % 32 == 0 && VS % 16 == 0 && NVEC % 64 == 0, "whole fragment blocks only");
+  F r[N];
+  __device__ __forceinline__ void load(const T* base, int ncb, int cb0, int tid) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int idx = tid + i * NTH;
+      if (NVEC % NTH == 0 || idx < NVEC) {
+        const int blk = idx >> 6, ln = idx & 63, s = blk / NCBS, cbl = blk - s * NCBS;
+        r[i] = *reinterpret_cast<const F*>(base + ((int64_t)(s * ncb + cb0 + cbl) * 64 + ln) * 8);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(T* lds, int ld, int tid) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int idx = tid + i * NTH;
+      if (NVEC % NTH == 0 || idx < NVEC) {
+        const int blk = idx >> 6, ln = idx & 63, s = blk / NCBS, cbl = blk - s * NCBS;
+        T* dst = lds + (32 * s) * ld + 16 * cbl + (ln & 15);
+#pragma unroll
+        for (int p = 0; p < 8; ++p) dst[fragblk_row(ln >> 4, p) * ld] = r[i][p];
+      }
+    }
+  }
+};
+
 // Copy a rows x cols tile from LDS (stride sld) to global (row stride gld), 16-byte vectors, rows < valid only,
 // by the NTH threads of the workgroup.
 template <typename T, int NTH = NTHR>

@@ -20,14 +20,15 @@
 //   P2  state: R, P R, O of c (staged)                   | factors: K K^T, Q K^T, diagonal inverse blocks of c+1
 //   P3  state: O store, S update of c                    | factors: off-diagonal inverse blocks of c+1
 // fp32 inputs (parity runs) do not fit two buffer sets in LDS; four waves run both roles for one chunk at a time.
-// Backward-recompute mode writes, per chunk, the entering state (bf16 [K][V]), R (bf16 [64][V]) and, from the
-// first V block, Tm and G for the gradient kernels, instead of O.
+// MODE 0 writes O; MODE 1 (recompute for the backward) writes instead, per chunk, the entering state and R (in
+// the fragment layout, straight from the accumulators) and, from the first V block, Tm and G for the gradient
+// kernels; MODE 2 (training forward) writes both, so that the backward needs no recompute.
 #include "gdn_chunk_common.h"
 #include "gdn_launch.h"
 
 namespace gdn {
 
-template <typename T, int K, int BV, bool BWD, bool WS>
+template <typename T, int K, int BV, int MODE, bool WS>
 __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const float* __restrict__ g,
     const float* __restrict__ beta, const float* __restrict__ h0, T* __restrict__ o, float* __restrict__ hT,
@@ -38,13 +39,15 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
   constexpr int NKT = K / 16;           // row tiles of the state slab
   constexpr int NCW = BV / 16 / NWAVE;  // column tiles per state wave
   static_assert(NCW == 1, "each state wave owns one 16-column slab of the state");
-  constexpr int NB = WS ? 2 : 1;                 // LDS buffer sets
-  constexpr int PMODE = BWD ? 0 : 1;             // P is needed only for O
-  constexpr int STG = (BWD ? K + CH : CH) * LV;  // staging: O, or the entering state then R
+  constexpr int NB = WS ? 2 : 1;       // LDS buffer sets
+  constexpr bool OUT = MODE != 1;      // O is computed (needs Q and P)
+  constexpr bool SAVE = MODE != 0;     // per-chunk states, R, Tm, G are written
+  constexpr int PMODE = OUT ? 1 : 0;
+  constexpr int STG = OUT ? CH * LV : 8;  // O staging
   __shared__ __attribute__((aligned(16))) T sK[NB][CH * LK];
-  __shared__ __attribute__((aligned(16))) T sQ[NB][BWD ? 8 : CH * LK];
+  __shared__ __attribute__((aligned(16))) T sQ[NB][OUT ? CH * LK : 8];
   __shared__ __attribute__((aligned(16))) T sV[NB][CH * LV];
-  __shared__ __attribute__((aligned(16))) T sP[NB][BWD ? 8 : CH * LC];
+  __shared__ __attribute__((aligned(16))) T sP[NB][OUT ? CH * LC : 8];
   __shared__ __attribute__((aligned(16))) T sTmB[NB][CH * LC];
   __shared__ __attribute__((aligned(16))) float sA[CH * (CH + 4)];
   __shared__ __attribute__((aligned(16))) float sD[4 * DBLK];
@@ -61,7 +64,8 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
   const int64_t sbase = (int64_t)bh * K * V;
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
-  auto gtm_of = [&](int c) -> T* { return (BWD && vb == 0) ? wsTm + ((int64_t)bh * NT + c) * CH * CH : nullptr; };
+  auto gtm_of = [&](int c) -> T* { return (SAVE && vb == 0) ? wsTm + ((int64_t)bh * NT + c) * CH * CH : nullptr; };
+  const int ncb = V / 16, cb = vb * (BV / 16) + wr;  // fragment-layout column block of a state wave
 
   // ---- factor role: K, g, beta of a chunk, and its factors --------------------------------------------------
   RegTile<T, CH, K> rk;
@@ -77,7 +81,7 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
       sG[n][l] = G;
       sB[n][l] = rt.ok ? rt.b : 0.f;
       sGam[n][l] = __expf(G);
-      if (BWD && vb == 0) wsGc[((int64_t)bh * NT + c) * CH + l] = G;
+      if (SAVE && vb == 0) wsGc[((int64_t)bh * NT + c) * CH + l] = G;
     }
   };
   auto kq_diag = [&](int c, int n) {
@@ -90,11 +94,11 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
   RegTile<T, CH, K> rq;
   RegTile<T, CH, BV> rv;
   auto prefetch_s = [&](int c) {
-    if constexpr (!BWD) rq.load(q + row0_of(c) * K, (int64_t)H * K, nvalid_of(c), tid);
+    if constexpr (OUT) rq.load(q + row0_of(c) * K, (int64_t)H * K, nvalid_of(c), tid);
     rv.load(v + row0_of(c) * V + v0, (int64_t)H * V, nvalid_of(c), tid);
   };
   auto store_s = [&](int n) {
-    if constexpr (!BWD) rq.store(sQ[n], LK, tid);
+    if constexpr (OUT) rq.store(sQ[n], LK, tid);
     rv.store(sV[n], LV, tid);
   };
   const int c0 = 16 * wr;  // the state wave's column slab inside the V block
@@ -108,17 +112,21 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
       for (int i = 0; i < 4; ++i)
         S[t][i] = h0 ? h0[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
   };
-  // K S, Q S and Y = V - diag(gamma) K S of the chunk in buffer set n
-  auto state_C = [&](int n) {
+  // K S, Q S and Y = V - diag(gamma) K S of the chunk in buffer set n (the entering state saved if SAVE)
+  auto state_C = [&](int c, int n) {
     typename Frag<T>::type Sb[K / 32];
 #pragma unroll
     for (int s = 0; s < K / 32; ++s) Sb[s] = frag_acc2<T>(S[2 * s], S[2 * s + 1]);
+    if constexpr (SAVE) {
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s) store_fragblk<T>(wsH + ((int64_t)bh * NT + c) * K * V, s, cb, ncb, Sb[s]);
+    }
 #pragma unroll
     for (int rt_ = 0; rt_ < 4; ++rt_) {
       f32x4 ks = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < K / 32; ++s) mma(ks, frag_kc_perm(sK[n], LK, 16 * rt_, 32 * s), Sb[s]);
-      if constexpr (!BWD) {
+      if constexpr (OUT) {
         QS[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < K / 32; ++s) mma(QS[rt_], frag_kc_perm(sQ[n], LK, 16 * rt_, 32 * s), Sb[s]);
@@ -130,8 +138,8 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
       }
     }
   };
-  // R = TmB Y; O = s gamma QS + P R staged (backward mode: the entering S and R staged)
-  auto state_D = [&](int n) {
+  // R = TmB Y (saved if SAVE); O = s gamma QS + P R staged
+  auto state_D = [&](int c, int n) {
     typename Frag<T>::type Yb[2], Rb[2];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) Yb[jb] = frag_acc2<T>(Y[2 * jb], Y[2 * jb + 1]);
@@ -152,18 +160,10 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
         d1[i] = R[2 * jb + 1][i] * __expf(GC - sG[n][32 * jb + 16 + acc_row(i)]);
       }
       Rd[jb] = frag_acc2<T>(d0, d1);
-      if constexpr (!BWD) Rb[jb] = frag_acc2<T>(R[2 * jb], R[2 * jb + 1]);
+      Rb[jb] = frag_acc2<T>(R[2 * jb], R[2 * jb + 1]);
+      if constexpr (SAVE) store_fragblk<T>(wsR + ((int64_t)bh * NT + c) * CH * V, jb, cb, ncb, Rb[jb]);
     }
-    if constexpr (BWD) {
-#pragma unroll
-      for (int t = 0; t < NKT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) stage[(16 * t + acc_row(i)) * LV + c0 + acc_col()] = from_f<T>(S[t][i]);
-#pragma unroll
-      for (int rt_ = 0; rt_ < 4; ++rt_)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) stage[(K + 16 * rt_ + acc_row(i)) * LV + c0 + acc_col()] = from_f<T>(R[rt_][i]);
-    } else {
+    if constexpr (OUT) {
 #pragma unroll
       for (int rt_ = 0; rt_ < 4; ++rt_) {
         f32x4 pr = {0.f, 0.f, 0.f, 0.f};
@@ -177,15 +177,9 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
       }
     }
   };
-  // staged rows -> global; S <- gamma_C S + K^T Rd
+  // staged O -> global; S <- gamma_C S + K^T Rd
   auto state_E = [&](int c, int n) {
-    const int64_t cidx = (int64_t)bh * NT + c;
-    if constexpr (BWD) {
-      s2g_rows(wsH + cidx * K * V + v0, (int64_t)V, stage, LV, K, BV, K);
-      s2g_rows(wsR + cidx * CH * V + v0, (int64_t)V, stage + K * LV, LV, CH, BV, CH);
-    } else {
-      s2g_rows(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, CH, BV, nvalid_of(c));
-    }
+    if constexpr (OUT) s2g_rows(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, CH, BV, nvalid_of(c));
     const float gC = __expf(sG[n][CH - 1]);
 #pragma unroll
     for (int t = 0; t < NKT; ++t) {
@@ -238,9 +232,9 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
         __syncthreads();  // P1
         if (c + 1 < NT) store_s(nn);
         prefetch_s(min(c + 2, NT - 1));
-        state_C(n);
+        state_C(c, n);
         __syncthreads();  // P2
-        state_D(n);
+        state_D(c, n);
         __syncthreads();  // P3
         state_E(c, n);
       }
@@ -259,11 +253,11 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
         prefetch_s(c + 1);
       }
       const f32x4 D = kq_diag(c, 0);
-      state_C(0);
+      state_C(c, 0);
       __syncthreads();
       factors_merge<T>(D, sA, sD, sTmB[0], gtm_of(c), sB[0], wr);
       __syncthreads();
-      state_D(0);
+      state_D(c, 0);
       __syncthreads();
       state_E(c, 0);
       __syncthreads();
@@ -273,24 +267,33 @@ __global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void fwd_sweep_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------------------
-template <typename T, int K, bool BWD>
+template <typename T, int K, int MODE>
 static hipError_t fwd_sweep_k(const ChunkArgs& a) {
   constexpr int BV = 64;
   constexpr bool WS = sizeof(T) == 2;
   dim3 grid(a.V / BV * a.B * a.H);
-  fwd_sweep_kernel<T, K, BV, BWD, WS><<<grid, WS ? 2 * NTHR : NTHR, 0, a.stream>>>(
+  fwd_sweep_kernel<T, K, BV, MODE, WS><<<grid, WS ? 2 * NTHR : NTHR, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.v), a.g, a.beta, a.h0,
-      static_cast<T*>(a.o), BWD ? nullptr : a.hT, static_cast<T*>(a.ws.hs), static_cast<T*>(a.ws.Rs),
+      static_cast<T*>(a.o), MODE == 1 ? nullptr : a.hT, static_cast<T*>(a.ws.hs), static_cast<T*>(a.ws.Rs),
       static_cast<T*>(a.ws.Tm), a.ws.Gc, a.T, a.H, a.V, a.NT, a.scale);
   return hipGetLastError();
 }
 
-hipError_t launch_fwd(const ChunkArgs& a, bool backward) {
+template <typename T, int K>
+static hipError_t fwd_sweep_mode(const ChunkArgs& a, FwdMode mode) {
+  switch (mode) {
+    case FWD_OUT: return fwd_sweep_k<T, K, 0>(a);
+    case FWD_RECOMPUTE: return fwd_sweep_k<T, K, 1>(a);
+    default: return fwd_sweep_k<T, K, 2>(a);
+  }
+}
+
+hipError_t launch_fwd(const ChunkArgs& a, FwdMode mode) {
   if (a.dtype == DT_BF16) {
-    if (a.K == 64) return backward ? fwd_sweep_k<bf16, 64, true>(a) : fwd_sweep_k<bf16, 64, false>(a);
-    if (a.K == 128) return backward ? fwd_sweep_k<bf16, 128, true>(a) : fwd_sweep_k<bf16, 128, false>(a);
+    if (a.K == 64) return fwd_sweep_mode<bf16, 64>(a, mode);
+    if (a.K == 128) return fwd_sweep_mode<bf16, 128>(a, mode);
   } else {
-    if (a.K == 64) return backward ? fwd_sweep_k<float, 64, true>(a) : fwd_sweep_k<float, 64, false>(a);
+    if (a.K == 64) return fwd_sweep_mode<float, 64>(a, mode);
   }
   return hipErrorInvalidValue;
 }

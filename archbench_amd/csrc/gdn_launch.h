@@ -23,15 +23,16 @@ struct StepArgs {
 };
 
 // Chunk workspace carve-up (chunk-major: [B*H][NT][...]).  All offsets are 256-byte aligned.
-// The forward needs no workspace; the backward's recompute sweep fills Tm, Gc, hs and Rs, the reverse sweep dhs
-// and dRs, and the gradient kernel reads them all.
+// The plain forward needs no workspace.  Tm, Gc, hs and Rs are filled by the stashing forward or by the
+// backward's recompute sweep, dhs and dRs by the reverse sweep, and the gradient kernel reads them all.
+// hs, Rs, dhs and dRs use the fragment layout of the sweeps' accumulators (store_fragblk).
 struct ChunkWs {
   void* Tm;   // [BH][NT][64][64]   (I + A)^-1 per chunk, input dtype
   float* Gc;  // [BH][NT][64]       chunk-local cumulative log-decay
   void* hs;   // [BH][NT][K][V]     state entering each chunk
-  void* Rs;   // [BH][NT][64][V]    R = U - W S per chunk (backward only)
-  void* dhs;  // [BH][NT][K][V]     dL/d(state leaving each chunk) (backward only)
-  void* dRs;  // [BH][NT][64][V]    dL/dR per chunk (backward only)
+  void* Rs;   // [BH][NT][64][V]    R = U - W S per chunk
+  void* dhs;  // [BH][NT][K][V]     dL/d(state leaving each chunk)
+  void* dRs;  // [BH][NT][64][V]    dL/dR per chunk
 };
 
 struct ChunkArgs {
@@ -53,12 +54,17 @@ struct ChunkArgs {
   hipStream_t stream;
 };
 
-size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, bool backward, ChunkWs* carve, void* base);
+// Workspace parts: WS_STASH = {Tm, Gc, hs, Rs}, WS_GRAD = {dhs, dRs}.  Returns the bytes of the requested
+// parts laid out from `base` and, if `carve` is non-null, sets the pointers of those parts (others untouched).
+enum WsPart { WS_STASH = 1, WS_GRAD = 2 };
+size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, ChunkWs* carve, void* base);
 bool chunk_shape_supported(int K, int V, int dtype);
 bool step_shape_supported(int K, int V);
 
 hipError_t launch_step(const StepArgs& a);
-hipError_t launch_fwd(const ChunkArgs& a, bool backward);  // o/hT (forward) or hs/Rs/Tm/Gc (backward)
+// FWD_OUT: o, hT.  FWD_RECOMPUTE: hs, Rs, Tm, Gc.  FWD_STASH: both.
+enum FwdMode { FWD_OUT = 0, FWD_RECOMPUTE = 1, FWD_STASH = 2 };
+hipError_t launch_fwd(const ChunkArgs& a, FwdMode mode);
 hipError_t launch_bwd_state(const ChunkArgs& a);                 // dhs, dRs, dh0
 hipError_t launch_bwd_intra(const ChunkArgs& a);                 // dq, dk, dv, dg, dbeta
 

@@ -7,7 +7,15 @@ enqueued on the current stream.
 
     archbench_amd::gdn_chunk_fwd      (q, k, v, g, beta, h0?, scale) -> (o, hT)
     archbench_amd::gdn_chunk_bwd      (q, k, v, g, beta, h0?, do, dhT?, scale) -> (dq, dk, dv, dg, dbeta, dh0)
+    archbench_amd::gdn_chunk_fwd_stash  (q, k, v, g, beta, h0?, scale) -> (o, hT, stash)
+    archbench_amd::gdn_chunk_bwd_stashed (q, k, v, g, beta, h0?, do, dhT?, stash, scale) -> (dq, ..., dh0)
     archbench_amd::gdn_recurrent_step (q, k, v, g, beta, state!, scale) -> o        (state updated in place)
+
+Training (autograd) uses the stash pair: the forward keeps the per-chunk states, R and chunk factors in a
+uint8 ``stash`` tensor saved for the backward, which then skips its recompute sweep (the reference's forward
+likewise hands its chunk factor A to the backward, nsgdn.py:352-363, :385-388).  The stash costs
+``_lib.stash_bytes(...)[0]`` bytes of device memory per call (about 3.5x the size of v in bf16);
+``ARCHBENCH_AMD_GDN_STASH=0`` selects the recompute path (gdn_chunk_fwd + gdn_chunk_bwd) instead.
 
 Python entry points with fla's signatures (the arithmetic behind archbench's ``gdn`` mixer,
 archbench/layers/fla.py:36-38):
@@ -24,6 +32,7 @@ a launch failure raises RuntimeError.
 
 from __future__ import annotations
 
+import os
 from typing import Optional
 
 import torch
@@ -33,7 +42,7 @@ from torch import Tensor
 from . import _lib
 
 __all__ = ["chunk_gated_delta_rule", "fused_recurrent_gated_delta_rule", "recurrent_step", "chunk_fwd",
-           "chunk_bwd"]
+           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed"]
 
 
 def _require_gpu(*ts: Optional[Tensor]) -> None:
@@ -141,6 +150,97 @@ def _chunk_backward(ctx, do, dhT):
 chunk_fwd.register_autograd(_chunk_backward, setup_context=_chunk_setup)
 
 
+# ------------------------------------------------------------------------------------ training (stash) pair
+def _prep(q, k, v, g, beta, h0):
+    return (q.contiguous(), k.contiguous(), v.contiguous(), g.float().contiguous(), beta.float().contiguous(),
+            None if h0 is None else h0.float().contiguous())
+
+
+@torch.library.custom_op("archbench_amd::gdn_chunk_fwd_stash", mutates_args=())
+def chunk_fwd_stash(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, h0: Optional[Tensor],
+                    scale: float) -> tuple[Tensor, Tensor, Tensor]:
+    _require_gpu(q, k, v, g, beta, h0)
+    B, T, H, K, V = _shapes(q, k, v, g, beta, h0)
+    lib = _lib.load()
+    q, k, v, g, beta, h0 = _prep(q, k, v, g, beta, h0)
+    o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
+    hT = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
+    stash = torch.empty(_lib.stash_bytes(B, T, H, K, V, q.dtype)[0], dtype=torch.uint8, device=q.device)
+    rc = lib.gdn_chunk_fwd_stash(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta), _lib.ptr(h0),
+                                 _lib.ptr(o), _lib.ptr(hT), _lib.ptr(stash), stash.numel(), B, T, H, K, V,
+                                 float(scale), _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
+    _lib.check(rc, "gdn_chunk_fwd_stash")
+    return o, hT, stash
+
+
+@chunk_fwd_stash.register_fake
+def _(q, k, v, g, beta, h0, scale):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    n = _lib.stash_bytes(B, T, H, K, V, q.dtype)[0]
+    return (q.new_empty(B, T, H, V), q.new_empty(B, H, K, V, dtype=torch.float32),
+            q.new_empty(n, dtype=torch.uint8))
+
+
+@torch.library.custom_op("archbench_amd::gdn_chunk_bwd_stashed", mutates_args=())
+def chunk_bwd_stashed(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, h0: Optional[Tensor], do: Tensor,
+                      dhT: Optional[Tensor], stash: Tensor,
+                      scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    _require_gpu(q, k, v, g, beta, h0, do, dhT, stash)
+    B, T, H, K, V = _shapes(q, k, v, g, beta, h0)
+    if tuple(do.shape) != (B, T, H, V):
+        raise ValueError(f"dO must be [B, T, H, V] = {(B, T, H, V)}, got {tuple(do.shape)}")
+    lib = _lib.load()
+    q, k, v, g, beta, h0 = _prep(q, k, v, g, beta, h0)
+    do = do.to(q.dtype).contiguous()
+    dhT = None if dhT is None else dhT.float().contiguous()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dg = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
+    db = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
+    dh0 = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
+    ws = torch.empty(_lib.stash_bytes(B, T, H, K, V, q.dtype)[1], dtype=torch.uint8, device=q.device)
+    rc = lib.gdn_chunk_bwd_stashed(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
+                                   _lib.ptr(h0), _lib.ptr(do), _lib.ptr(dhT), _lib.ptr(dq), _lib.ptr(dk),
+                                   _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(db), _lib.ptr(dh0), _lib.ptr(stash),
+                                   stash.numel(), _lib.ptr(ws), ws.numel(), B, T, H, K, V, float(scale),
+                                   _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
+    _lib.check(rc, "gdn_chunk_bwd_stashed")
+    return dq, dk, dv, dg, db, dh0
+
+
+@chunk_bwd_stashed.register_fake
+def _(q, k, v, g, beta, h0, do, dhT, stash, scale):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    f32 = dict(dtype=torch.float32)
+    return (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), q.new_empty(B, T, H, **f32),
+            q.new_empty(B, T, H, **f32), q.new_empty(B, H, K, V, **f32))
+
+
+def _stash_setup(ctx, inputs, output):
+    q, k, v, g, beta, h0, scale = inputs
+    ctx.save_for_backward(q, k, v, g, beta, h0, output[2])
+    ctx.scale = scale
+    ctx.has_h0 = h0 is not None
+    ctx.g_dtype, ctx.beta_dtype = g.dtype, beta.dtype
+
+
+def _stash_backward(ctx, do, dhT, _dstash):
+    q, k, v, g, beta, h0, stash = ctx.saved_tensors
+    dq, dk, dv, dg, db, dh0 = chunk_bwd_stashed(q, k, v, g, beta, h0, do.contiguous(),
+                                                None if dhT is None else dhT.contiguous(), stash, ctx.scale)
+    return dq, dk, dv, dg.to(ctx.g_dtype), db.to(ctx.beta_dtype), (dh0 if ctx.has_h0 else None), None
+
+
+chunk_fwd_stash.register_autograd(_stash_backward, setup_context=_stash_setup)
+
+
+def _use_stash(*ts: Optional[Tensor]) -> bool:
+    if os.environ.get("ARCHBENCH_AMD_GDN_STASH", "1") == "0" or not torch.is_grad_enabled():
+        return False
+    return any(t is not None and t.requires_grad for t in ts)
+
+
 # ------------------------------------------------------------------------------------------------- decode step
 @torch.library.custom_op("archbench_amd::gdn_recurrent_step", mutates_args=("state",))
 def _recurrent_step(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, state: Tensor,
@@ -196,7 +296,10 @@ def chunk_gated_delta_rule(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Ten
         q, k = _l2norm(q), _l2norm(k)
     if scale is None:
         scale = q.shape[-1] ** -0.5
-    o, hT = chunk_fwd(q, k, v, g, beta, initial_state, float(scale))
+    if _use_stash(q, k, v, g, beta, initial_state):
+        o, hT, _ = chunk_fwd_stash(q, k, v, g, beta, initial_state, float(scale))
+    else:
+        o, hT = chunk_fwd(q, k, v, g, beta, initial_state, float(scale))
     return o, (hT if output_final_state else None)
 
 

@@ -2,8 +2,10 @@
 """Gated DeltaNet benchmark on one MI355X.
 
 Headline (one JSON line on stdout): chunk forward + backward of the GDN op at B=8, T=4096, H=16, K=V=128, bf16
-inputs with fp32 state/accumulation, synthetic seeded data resident in HBM.  One step = one forward call and
-one backward call of the op (every gradient: dq, dk, dv, dg, dbeta).  tokens/s = B*T / step time.
+inputs with fp32 state/accumulation, synthetic seeded data resident in HBM.  One step = one training forward
+call (gdn_chunk_fwd_stash: o and hT, keeping the per-chunk states for the backward, as autograd does) and one
+backward call (gdn_chunk_bwd_stashed: every gradient, dq, dk, dv, dg, dbeta).  tokens/s = B*T / step time.
+The recompute path (gdn_chunk_fwd + gdn_chunk_bwd, no stash) is timed beside it as recompute_ms_per_step.
 
 Also reported in the same line:
   roofline      the dominant kernel of the step: algorithmic dense-MFMA FLOPs per launch over its average
@@ -41,6 +43,7 @@ def stage_flops(stage: str, K: int, V: int) -> int:
     stage repeats for every 64-wide V block (the chunk factors) is counted once."""
     return {
         "fwd": 6 * C * K + 4 * C * V + 6 * K * V,            # KK^T, QK^T, W; U, PR; WS, QS, K^T R
+        "fwd_stash": 6 * C * K + 4 * C * V + 6 * K * V,      # the forward's products (states also written)
         "bwd_recompute": 4 * C * K + 2 * C * V + 4 * K * V,  # KK^T, W; U; WS, K^T R
         "bwd_state": 6 * C * K + 2 * C * V + 6 * K * V,      # KK^T, QK^T, W; P^T dO; K dS, Qg^T dO, W^T dR
         "bwd_intra": 6 * C * V + 6 * K * V + 16 * C * K + 4 * C * C,
@@ -134,11 +137,16 @@ def main() -> int:
         x = make_inputs(B, T, H, K, V, seed=0, with_do=True).to(dev, torch.bfloat16)
 
         def step():
+            _, _, stash = ops.chunk_fwd_stash(x.q, x.k, x.v, x.g, x.beta, None, 1.0)
+            ops.chunk_bwd_stashed(x.q, x.k, x.v, x.g, x.beta, None, x.do, None, stash, 1.0)
+
+        def step_recompute():
             ops.chunk_fwd(x.q, x.k, x.v, x.g, x.beta, None, 1.0)
             ops.chunk_bwd(x.q, x.k, x.v, x.g, x.beta, None, x.do, None, 1.0)
 
         log(f"timing {args.steps} steps after {args.warmup} warmup")
         sec = timed_loop(step, args.steps, args.warmup, torch)
+        sec_rc = timed_loop(step_recompute, max(3, args.steps // 2), 1, torch)
         tokens = B * T
         with _lib.StageTimer() as st:
             for _ in range(max(3, min(args.steps, 10))):
@@ -163,8 +171,10 @@ def main() -> int:
                          "traffic": measured_traffic().get(dom, {}).get("bytes"),
                          "flops_per_launch": dom_flops, "avg_ms": round(dom_ms, 4)},
             "stages_ms": {k: round(v[0], 4) for k, v in stages.items()},
+            "recompute_ms_per_step": round(sec_rc * 1e3, 4),
         })
-        log(f"fwd+bwd {sec * 1e3:.3f} ms/step, {tokens / sec:.3e} tokens/s; stages {out['stages_ms']}")
+        log(f"fwd+bwd {sec * 1e3:.3f} ms/step, {tokens / sec:.3e} tokens/s; stages {out['stages_ms']}; "
+            f"recompute path {sec_rc * 1e3:.3f} ms/step")
         del x
         torch.cuda.empty_cache()
 

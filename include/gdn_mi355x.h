@@ -67,6 +67,23 @@ int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, c
                   float* dbeta, float* dh0, void* ws, size_t ws_bytes, int B, int T, int H, int K, int V,
                   float scale, int dtype, void* stream);
 
+/* Training pair.  gdn_chunk_fwd_stash computes what gdn_chunk_fwd computes and also writes into `stash` the
+ * per-chunk intermediates the backward needs (chunk factors, chunk-local decay, the state entering every chunk
+ * and R = U - W S); gdn_chunk_bwd_stashed, called later with the same inputs and the same stash (unchanged in
+ * between; it is only read), is gdn_chunk_bwd without its recompute sweep, with `ws` holding only the
+ * gradient part of the workspace.  gdn_chunk_stash_bytes gives both sizes.  The reference's forward likewise
+ * returns its chunk factor A and cumulative decay g for the backward to reuse (nsgdn.py:352-363, saved at
+ * :385-388); keeping the states too trades stash_bytes of device memory for one sweep over the sequence. */
+int gdn_chunk_stash_bytes(int B, int T, int H, int K, int V, int dtype, size_t* stash_bytes, size_t* bwd_ws_bytes);
+int gdn_chunk_fwd_stash(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                        const float* h0, void* o, float* hT, void* stash, size_t stash_bytes, int B, int T, int H,
+                        int K, int V, float scale, int dtype, void* stream);
+int gdn_chunk_bwd_stashed(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                          const float* h0, const void* dout, const float* dhT, void* dq, void* dk, void* dv,
+                          float* dg, float* dbeta, float* dh0, const void* stash, size_t stash_bytes, void* ws,
+                          size_t ws_bytes, int B, int T, int H, int K, int V, float scale, int dtype,
+                          void* stream);
+
 /* One recurrent decode step, state updated in place:
  *   r = beta (v - e^g S^T k),  S <- e^g S + k r^T,  o = S^T (scale q)
  * q, k [B, H, K], v, o [B, H, V], g, beta [B, H] fp32, state [B, H, K, V] fp32.
@@ -80,7 +97,7 @@ int gdn_recurrent_step(const void* q, const void* k, const void* v, const float*
  * enqueue is bracketed by hipEvents on the same stream.  gdn_profile_read synchronises on those events and
  * returns, per stage, the summed milliseconds and the number of launches (arrays of at least
  * GDN_PROFILE_STAGES entries), then clears the record.  Stage names: gdn_profile_stage_name. */
-#define GDN_PROFILE_STAGES 5
+#define GDN_PROFILE_STAGES 6
 int gdn_profile_enable(int on);
 int gdn_profile_read(double* ms_sum, int* launches, int n_stages);
 const char* gdn_profile_stage_name(int stage);

@@ -55,6 +55,26 @@ def test_workspace_sizes():
                                                                                         torch.float32)
 
 
+def test_stash_sizes_split_the_backward_workspace():
+    import torch
+    for args in [(8, 4096, 16, 128, 128, torch.bfloat16), (1, 65, 3, 64, 64, torch.float32)]:
+        stash, grad = _lib.stash_bytes(*args)
+        assert stash + grad == _lib.ws_bytes("bwd", *args)
+    B, T, H, K, V = 8, 4096, 16, 128, 128
+    stash, grad = _lib.stash_bytes(B, T, H, K, V, torch.bfloat16)
+    # per chunk: Tm (64x64 bf16), G (64 fp32), entering state (K x V bf16), R (64 x V bf16)
+    assert stash == B * H * 64 * (64 * 64 * 2 + 64 * 4 + K * V * 2 + 64 * V * 2)
+
+
+def test_stashed_backward_rejects_missing_stash():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rc = lib.gdn_chunk_bwd_stashed(p, p, p, p, p, None, p, None, p, p, p, p, p, None, None, 0, p, 1 << 40,
+                                   1, 64, 1, 64, 64, 1.0, 1, None)
+    assert rc == _lib.GDN_ERR_WORKSPACE
+    assert b"stash" in lib.gdn_last_error()
+
+
 def test_argument_errors_do_not_touch_the_gpu():
     lib = _lib.load()
     n = ctypes.c_size_t(0)

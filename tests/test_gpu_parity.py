@@ -112,6 +112,49 @@ def test_autograd_matches_backward_op():
         assert max_abs(leaf.grad, r) <= FP32_TOL * max(1.0, r.abs().max().item()), n
 
 
+def test_autograd_recompute_path(monkeypatch):
+    """The same gradients through the recompute path (no stash kept by the forward)."""
+    monkeypatch.setenv("ARCHBENCH_AMD_GDN_STASH", "0")
+    banner("autograd through chunk_gated_delta_rule, recompute path")
+    host, dev = device_inputs(1, 100, 2, 64, 64, torch.float32, h0_std=0.1, with_do=True)
+    leaves = [t.clone().requires_grad_() for t in (dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0)]
+    q, k, v, g, b, h0 = leaves
+    o, hT = ops.chunk_gated_delta_rule(q, k, v, g, b, scale=0.3, initial_state=h0, output_final_state=True)
+    dhT = torch.full_like(hT, 0.05)
+    ((o * dev.do).sum() + (hT * dhT).sum()).backward()
+    ref = O.chunk_bwd(host.q, host.k, host.v, host.g, host.beta, host.do, 0.3, host.h0, dhT.cpu())
+    for n, leaf, r in zip(NAMES, leaves, ref):
+        assert max_abs(leaf.grad, r) <= FP32_TOL * max(1.0, r.abs().max().item()), n
+
+
+@pytest.mark.parametrize("dtype,T,K,V", [(torch.float32, 130, 64, 64), (torch.bfloat16, 200, 128, 128),
+                                         (torch.bfloat16, 64, 64, 256)])
+def test_stash_pair_equals_plain_and_recompute(dtype, T, K, V):
+    """fwd_stash gives the plain forward's o and hT bit for bit, and bwd_stashed the recompute backward's
+    gradients bit for bit (the stash holds exactly what the recompute sweep rebuilds); both against the oracle."""
+    banner(f"stash pair {dtype} T={T} K={K} V={V}")
+    host, dev = device_inputs(2, T, 2, K, V, dtype, h0_std=0.1, with_do=True, seed=3)
+    dhT = (torch.randn(2, 2, K, V, generator=torch.Generator().manual_seed(9)) * 0.1).cuda()
+    o_s, hT_s, stash = ops.chunk_fwd_stash(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, 0.5)
+    o_p, hT_p = ops.chunk_fwd(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, 0.5)
+    got = ops.chunk_bwd_stashed(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, dev.do, dhT, stash, 0.5)
+    plain = ops.chunk_bwd(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, dev.do, dhT, 0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(o_s, o_p) and torch.equal(hT_s, hT_p)
+    for n, a, b in zip(NAMES, got, plain):
+        assert torch.equal(a, b), n
+    o_ref, hT_ref = O.chunk_fwd(host.q, host.k, host.v, host.g, host.beta, 0.5, host.h0)
+    ref = O.chunk_bwd(host.q, host.k, host.v, host.g, host.beta, host.do, 0.5, host.h0, dhT.cpu())
+    if dtype == torch.float32:
+        assert max_abs(o_s, o_ref) <= FP32_TOL
+        for n, a, b in zip(NAMES, got, ref):
+            assert max_abs(a, b) <= FP32_TOL * max(1.0, b.abs().max().item()), n
+    else:
+        assert rel_l2(o_s, o_ref) <= BF16_TOL
+        for n, a, b in zip(NAMES, got, ref):
+            assert rel_l2(a, b) <= BF16_TOL, (n, rel_l2(a, b))
+
+
 def test_state_passing_on_gpu():
     banner("state passing")
     host, dev = device_inputs(2, 300, 2, 128, 128, torch.bfloat16, h0_std=0.1)
