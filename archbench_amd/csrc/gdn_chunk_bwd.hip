@@ -271,8 +271,9 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   constexpr int NKT = K / 16;   // column tiles over K
   constexpr int NVT = VS / 16;  // column tiles over a V slab
   constexpr int HK = NKT / 2, HV = NVT / 2, HC = 2;  // tiles per half: over K, over the slab, over the chunk
-  // slab region: V phase {dO, R, dR, V : CH x LS; S0, dSC : K x LS}; K phase {dWn : CH x LK; dTm, M1, D, dPm : CH x LC}
-  constexpr int SLAB_V = 4 * CH * LS + 2 * K * LS;
+  // slab region: V phase {dO, V : CH x LS; R^T, dR^T : VS x LC; S0^T, dSC^T : VS x LK (column-major, so the
+  // fragment-layout tiles are written as 4-element runs)}; K phase {dWn : CH x LK; dTm, M1, D, dPm : CH x LC}
+  constexpr int SLAB_V = 2 * CH * LS + 2 * VS * LC + 2 * VS * LK;
   constexpr int SLAB_K = CH * LK + 4 * CH * LC;
   constexpr int SLAB = SLAB_V > SLAB_K ? SLAB_V : SLAB_K;
   __shared__ __attribute__((aligned(16))) T sQ[CH * LK];
@@ -284,11 +285,11 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   __shared__ float sHalf[6][CH];  // second-half partial row sums: rq, rk, dbV, rx, dbA, rz
 
   T* sdO = slab;
-  T* sR = sdO + CH * LS;
-  T* sdR = sR + CH * LS;
-  T* sV = sdR + CH * LS;
-  T* sS0 = sV + CH * LS;
-  T* sdSC = sS0 + K * LS;
+  T* sV = sdO + CH * LS;
+  T* sRt = sV + CH * LS;     // R^T     [VS][LC]
+  T* sdRt = sRt + VS * LC;   // dR^T    [VS][LC]
+  T* sS0t = sdRt + VS * LC;  // S0^T    [VS][LK]
+  T* sdSCt = sS0t + VS * LK; // dS_C^T  [VS][LK]
 
   const int c = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh - b * H;
@@ -299,32 +300,36 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   const int64_t row0 = ((int64_t)b * T_ + t0) * H + h;
   const int64_t cidx = (int64_t)bh * NT + c;
 
-  // every global read of the chunk is issued up front as 16-byte register tiles (see RegTile); the next
-  // V slab is fetched while the current one is computed
+  // Global reads are issued as 16-byte register tiles (RegTile, FragTile) in the order they are consumed, each
+  // V slab in two groups: A = {dO, V, R, dR} (and Tm, G, beta first) feeds dO R^T, dR V^T and Tm^T dR; B =
+  // {S0, dS_C} feeds the products with the states.  Group B and Q, K stay in flight while group A is computed,
+  // and the next slab's groups are issued as soon as their registers are free.
   RegTile<T, CH, K, ITH> tq, tk;
   RegTile<T, CH, CH, ITH> rtm;
   RegTile<T, CH, VS, ITH> rdo, rv;
   FragTile<T, CH, VS, ITH> rr, rdr;
   FragTile<T, K, VS, ITH> rs0, rdsc;
-  auto load_slab = [&](int vs) {
+  auto load_a = [&](int vs) {
     rdo.load(dout + row0 * V + vs, (int64_t)H * V, nvalid, tid);
     rv.load(v + row0 * V + vs, (int64_t)H * V, nvalid, tid);
     rr.load(wsR + cidx * CH * V, V / 16, vs / 16, tid);
     rdr.load(wsdR + cidx * CH * V, V / 16, vs / 16, tid);
+  };
+  auto load_b = [&](int vs) {
     rs0.load(wsH + cidx * K * V, V / 16, vs / 16, tid);
     rdsc.load(wsdH + cidx * K * V, V / 16, vs / 16, tid);
   };
+  const float pg = wsGc[cidx * CH + (tid & (CH - 1))];
+  const float pb = beta[row0 + (int64_t)((tid & (CH - 1)) < nvalid ? (tid & (CH - 1)) : 0) * H];
+  rtm.load(wsTm + cidx * CH * CH, (int64_t)CH, CH, tid);
+  load_a(0);
+  load_b(0);
   tq.load(q + row0 * K, (int64_t)H * K, nvalid, tid);
   tk.load(k + row0 * K, (int64_t)H * K, nvalid, tid);
-  rtm.load(wsTm + cidx * CH * CH, (int64_t)CH, CH, tid);
-  load_slab(0);
   if (tid < CH) {
-    sG[tid] = wsGc[cidx * CH + tid];
-    sB[tid] = beta[row0 + (int64_t)(tid < nvalid ? tid : 0) * H];
-    if (tid >= nvalid) sB[tid] = 0.f;
+    sG[tid] = pg;
+    sB[tid] = tid < nvalid ? pb : 0.f;
   }
-  tq.store(sQ, LK, tid);
-  tk.store(sK, LK, tid);
   rtm.store(sTm, LC, tid);
 
   // ---- V phase: contractions over V, slab by slab -------------------------------------------------------
@@ -337,38 +342,26 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   float dbV[4] = {0.f, 0.f, 0.f, 0.f};
   float sdot = 0.f;  // partial <dS_C, S0>
 
+#pragma unroll 1
   for (int vs = 0; vs < V; vs += VS) {
+    // group A: dO R^T, dR V^T, dY = Tm^T dR (dv = beta dY, dbeta += dY . v)
     rdo.store(sdO, LS, tid);
     rv.store(sV, LS, tid);
-    rr.store(sR, LS, tid);
-    rdr.store(sdR, LS, tid);
-    rs0.store(sS0, LS, tid);
-    rdsc.store(sdSC, LS, tid);
+    rr.store_t(sRt, LC, tid);
+    rdr.store_t(sdRt, LC, tid);
     __syncthreads();
-    if (vs + VS < V) load_slab(vs + VS);
-    for (int idx = tid; idx < K * VS; idx += ITH) {
-      const int d = idx / VS, n = idx - d * VS;
-      sdot += to_f(sdSC[d * LS + n]) * to_f(sS0[d * LS + n]);
-    }
+    if (vs + VS < V) load_a(vs + VS);
 #pragma unroll
     for (int j = 0; j < HC; ++j) {
       const int n = HC * hf + j;
-      mma_blk<true, true, VS>(aP[j], sdO, LS, 16 * rb, sR, LS, 16 * n);
-      mma_blk<true, true, VS>(aTV[j], sdR, LS, 16 * rb, sV, LS, 16 * n);
+      mma_blk<true, false, VS>(aP[j], sdO, LS, 16 * rb, sRt, LC, 16 * n);
+      mma_blk<false, true, VS>(aTV[j], sdRt, LC, 16 * rb, sV, LS, 16 * n);
     }
-#pragma unroll
-    for (int j = 0; j < HK; ++j) {
-      const int n = HK * hf + j;
-      mma_blk<true, true, VS>(aQg[j], sdO, LS, 16 * rb, sS0, LS, 16 * n);
-      mma_blk<true, true, VS>(aKd[j], sR, LS, 16 * rb, sdSC, LS, 16 * n);
-      mma_blk<true, true, VS>(aWn[j], sdR, LS, 16 * rb, sS0, LS, 16 * n);
-    }
-    // dY = Tm^T dR for this slab: dv = beta dY, dbeta += dY . v
 #pragma unroll
     for (int j = 0; j < HV; ++j) {
       const int n = HV * hf + j;
       f32x4 dy = {0.f, 0.f, 0.f, 0.f};
-      mma_blk<false, false, CH>(dy, sTm, LC, 16 * rb, sdR, LS, 16 * n);
+      mma_blk<false, true, CH>(dy, sTm, LC, 16 * rb, sdRt, LC, 16 * n);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 16 * rb + acc_row(i), vc = 16 * n + acc_col();
@@ -376,8 +369,28 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
         sdv[r * LS + vc] = from_f<T>(sB[r] * dy[i]);
       }
     }
+    // group B: dO S0^T, R dS_C^T, dR S0^T, <dS_C, S0>
+    rs0.store_t(sS0t, LK, tid);
+    rdsc.store_t(sdSCt, LK, tid);
+    if (vs == 0) {
+      tq.store(sQ, LK, tid);
+      tk.store(sK, LK, tid);
+    }
     __syncthreads();
+    if (vs + VS < V) load_b(vs + VS);
     s2g_rows<T, ITH>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, CH, VS, nvalid);
+    for (int idx = tid; idx < K * VS; idx += ITH) {
+      const int n = idx / K, d = idx - n * K;
+      sdot += to_f(sdSCt[n * LK + d]) * to_f(sS0t[n * LK + d]);
+    }
+#pragma unroll
+    for (int j = 0; j < HK; ++j) {
+      const int n = HK * hf + j;
+      mma_blk<true, false, VS>(aQg[j], sdO, LS, 16 * rb, sS0t, LK, 16 * n);
+      mma_blk<false, false, VS>(aKd[j], sRt, LC, 16 * rb, sdSCt, LK, 16 * n);
+      mma_blk<false, false, VS>(aWn[j], sdRt, LC, 16 * rb, sS0t, LK, 16 * n);
+    }
+    __syncthreads();
   }
   // block reduce <dS_C, S0>
   {
@@ -395,13 +408,14 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   T* sdPm = sD + CH * LC;         // CH x LC   dP o s E
 
   const int lg = l >> 4;  // lane group: rows 4*lg .. 4*lg+3 of each tile
-  float gam[4], dte[4], bet[4];
+  float gam[4], dte[4], bet[4], Grow[4];
   const float GC = sG[CH - 1];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 16 * rb + acc_row(i);
-    gam[i] = __expf(sG[r]);
-    dte[i] = __expf(GC - sG[r]);
+    Grow[i] = sG[r];
+    gam[i] = __expf(Grow[i]);
+    dte[i] = __expf(GC - Grow[i]);
     bet[i] = sB[r];
   }
   // row dots from the V-phase accumulators (this half's columns)
@@ -469,10 +483,13 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     mma_blk<true, true, K>(qk, sQ, LK, 16 * rb, sK, LK, 16 * n);
     f32x4 z;
     const int cc = 16 * n + acc_col();
+    const float Gc = sG[cc];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rb + acc_row(i);
-      const float e = r >= cc ? __expf(fminf(sG[r] - sG[cc], 0.f)) : 0.f;
+      // computed unconditionally (min(., 0) keeps it finite) and masked by a select: no branch around the exp
+      const float e_all = __expf(fminf(Grow[i] - Gc, 0.f));
+      const float e = r >= cc ? e_all : 0.f;
       const float dA = (r > cc) ? -da[i] : 0.f;
       const float Aval = bet[i] * kk[i] * e;
       const float dP = (r >= cc) ? aP[j][i] : 0.f;

@@ -10,6 +10,8 @@
 // so K and V enter the MFMA products unscaled and no 64 x K factor is built per chunk.
 #pragma once
 
+#include <type_traits>
+
 #include "gdn_common.h"
 
 namespace gdn {
@@ -213,6 +215,21 @@ struct FragTile {
         T* dst = lds + (32 * s) * ld + 16 * cbl + (ln & 15);
 #pragma unroll
         for (int p = 0; p < 8; ++p) dst[fragblk_row(ln >> 4, p) * ld] = r[i][p];
+      }
+    }
+  }
+  // Column-major LDS tile [VS][ldt] (element (row, col) at col * ldt + row): the lane's rows 4g..4g+3 and
+  // 16+4g..16+4g+3 are two contiguous runs of 4, written as two vectors.  ldt must be a multiple of 4.
+  __device__ __forceinline__ void store_t(T* lds, int ldt, int tid) const {
+    using V4 = typename std::conditional<sizeof(T) == 2, bf16x4, f32x4>::type;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int idx = tid + i * NTH;
+      if (NVEC % NTH == 0 || idx < NVEC) {
+        const int blk = idx >> 6, ln = idx & 63, s = blk / NCBS, cbl = blk - s * NCBS;
+        T* dst = lds + (16 * cbl + (ln & 15)) * ldt + 32 * s + 4 * (ln >> 4);
+        *reinterpret_cast<V4*>(dst) = V4{r[i][0], r[i][1], r[i][2], r[i][3]};
+        *reinterpret_cast<V4*>(dst + 16) = V4{r[i][4], r[i][5], r[i][6], r[i][7]};
       }
     }
   }

@@ -198,12 +198,18 @@ __device__ __forceinline__ void sweep_block(int NV, int BH, int& vb, int& bh) {
   }
 }
 
-// Sum over the 16 lanes that share a lane group (the columns of one accumulator tile row set).
+// Sum over the 16 lanes of a DPP row (the columns of one accumulator tile row set), left in every lane of the
+// row: butterfly on DPP, no LDS crossbar.  quad_perm [1,0,3,2] and [2,3,0,1] sum each quad, row_half_mirror
+// (lane i <- 7 - i) adds the other quad of the half-row, row_mirror (lane i <- 15 - i) the other half-row.
+template <int CTRL>
+__device__ __forceinline__ float dpp_sum_step(float x) {
+  return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float sum16(float x) {
-  x += __shfl_xor(x, 1);
-  x += __shfl_xor(x, 2);
-  x += __shfl_xor(x, 4);
-  x += __shfl_xor(x, 8);
+  x = dpp_sum_step<0xb1>(x);   // quad_perm [1,0,3,2]
+  x = dpp_sum_step<0x4e>(x);   // quad_perm [2,3,0,1]
+  x = dpp_sum_step<0x141>(x);  // row_half_mirror
+  x = dpp_sum_step<0x140>(x);  // row_mirror
   return x;
 }
 
