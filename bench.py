@@ -8,8 +8,10 @@ backward call (gdn_chunk_bwd_stashed: every gradient, dq, dk, dv, dg, dbeta).  t
 The recompute path (gdn_chunk_fwd + gdn_chunk_bwd, no stash) is timed beside it as recompute_ms_per_step.
 
 Also reported in the same line:
-  roofline      the dominant kernel of the step: algorithmic dense-MFMA FLOPs per launch over its average
-                duration (HIP events on the launch stream), against the bf16 dense MFMA peak;
+  roofline      the dominant kernel of the step against the roofline that bounds it: its algorithmic intensity
+                (stage_flops / stage_bytes) decides between HBM (below the ridge, 2.5 PFLOP/s / 8 TB/s) and
+                MFMA; achieved = algorithmic bytes (or FLOPs) per launch over the launch's average duration
+                (HIP events on the launch stream); traffic = measured HBM bytes per launch;
   mfma_frac     the whole step at the workload's algorithmic count 3 * F_fwd per token-head,
                 F_fwd = 2C(3K + 2V) + 6KV (C = 64);
   fwd_only      forward alone at B=8, T=2048, H=8, K=V=128 (% of the bf16 MFMA peak);
@@ -47,6 +49,20 @@ def stage_flops(stage: str, K: int, V: int) -> int:
         "bwd_recompute": 4 * C * K + 2 * C * V + 4 * K * V,  # KK^T, W; U; WS, K^T R
         "bwd_state": 6 * C * K + 2 * C * V + 6 * K * V,      # KK^T, QK^T, W; P^T dO; K dS, Qg^T dO, W^T dR
         "bwd_intra": 6 * C * V + 6 * K * V + 16 * C * K + 4 * C * C,
+    }.get(stage, 0)
+
+
+def stage_bytes(stage: str, K: int, V: int, es: int = 2) -> int:
+    """Algorithmic HBM bytes per token-head of each kernel stage: every input read once and every output
+    written once (q, k: es*K; v, o, dO: es*V; g, beta, G: 4; per-chunk workspace: state es*K*V/C, R es*V,
+    Tm es*C).  Intermediates the design keeps on-chip count nothing."""
+    qk, vv, st, r, tm = es * K, es * V, es * K * V // C, es * V, es * C
+    return {
+        "fwd": 2 * qk + vv + 8 + vv,                           # q k v g beta -> o
+        "fwd_stash": 2 * qk + vv + 8 + vv + st + r + tm + 4,   # ... -> o, states, R, Tm, G
+        "bwd_recompute": qk + vv + 8 + st + r + tm + 4,        # k v g beta -> states, R, Tm, G
+        "bwd_state": 2 * qk + vv + 8 + st + r,                 # q k dO g beta -> dstates, dR
+        "bwd_intra": 2 * qk + 2 * vv + tm + 8 + 2 * st + 2 * r + 2 * qk + vv + 8,
     }.get(stage, 0)
 
 
@@ -155,7 +171,19 @@ def main() -> int:
         dom = max(stages, key=lambda s: stages[s][0])
         dom_ms = stages[dom][0]
         dom_flops = stage_flops(dom, K, V) * B * T * H
-        achieved = dom_flops / (dom_ms * 1e-3)
+        dom_bytes = stage_bytes(dom, K, V) * B * T * H
+        hbm_bound = dom_flops / dom_bytes < MFMA_BF16_PEAK / HBM_PEAK
+        if hbm_bound:
+            roof = {"kernel": dom, "bound": "hbm", "achieved": round(dom_bytes / (dom_ms * 1e-3) / 1e9, 1),
+                    "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(dom_bytes / (dom_ms * 1e-3) / HBM_PEAK, 4)}
+        else:
+            roof = {"kernel": dom, "bound": "mfma", "achieved": round(dom_flops / (dom_ms * 1e-3) / 1e12, 2),
+                    "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                    "frac": round(dom_flops / (dom_ms * 1e-3) / MFMA_BF16_PEAK, 4)}
+        roof.update({"traffic": measured_traffic().get(dom, {}).get("bytes"), "algorithmic_bytes": dom_bytes,
+                     "flops_per_launch": dom_flops,
+                     "mfma_frac": round(dom_flops / (dom_ms * 1e-3) / MFMA_BF16_PEAK, 4),
+                     "avg_ms": round(dom_ms, 4)})
         call_flops = 3 * f_fwd(K, V) * B * T * H
         out.update({
             "metric": METRIC, "value": round(tokens / sec, 1), "unit": "tokens/s", "n_gpus": 1,
@@ -165,11 +193,7 @@ def main() -> int:
             "config": {"workload": "gdn_chunk_fwd_bwd", "B": B, "T": T, "H": H, "K": K, "V": V, "chunk": C,
                        "scale": 1.0, "state": "fp32", "g_shift": 4.0},
             "mfma_frac": round(call_flops / sec / MFMA_BF16_PEAK, 4),
-            "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved / 1e12, 2),
-                         "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
-                         "frac": round(achieved / MFMA_BF16_PEAK, 4),
-                         "traffic": measured_traffic().get(dom, {}).get("bytes"),
-                         "flops_per_launch": dom_flops, "avg_ms": round(dom_ms, 4)},
+            "roofline": roof,
             "stages_ms": {k: round(v[0], 4) for k, v in stages.items()},
             "recompute_ms_per_step": round(sec_rc * 1e3, 4),
         })
