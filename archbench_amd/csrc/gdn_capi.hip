@@ -33,9 +33,12 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
     return r;
   };
   ChunkWs ws{};
-  if (parts & WS_STASH) {
+  if (parts & WS_FACT) {
     ws.Tm = take(BH * NT * CH_TOKENS * CH_TOKENS * es);
+    ws.P = take(BH * NT * CH_TOKENS * CH_TOKENS * es);
     ws.Gc = static_cast<float*>(take(BH * NT * CH_TOKENS * 4));
+  }
+  if (parts & WS_STATE) {
     ws.hs = take(BH * NT * (size_t)K * V * es);
     ws.Rs = take(BH * NT * CH_TOKENS * (size_t)V * es);
   }
@@ -44,8 +47,11 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
     ws.dRs = take(BH * NT * CH_TOKENS * (size_t)V * es);
   }
   if (carve) {
-    if (parts & WS_STASH) {
-      carve->Tm = ws.Tm; carve->Gc = ws.Gc; carve->hs = ws.hs; carve->Rs = ws.Rs;
+    if (parts & WS_FACT) {
+      carve->Tm = ws.Tm; carve->P = ws.P; carve->Gc = ws.Gc;
+    }
+    if (parts & WS_STATE) {
+      carve->hs = ws.hs; carve->Rs = ws.Rs;
     }
     if (parts & WS_GRAD) {
       carve->dhs = ws.dhs; carve->dRs = ws.dRs;
@@ -75,8 +81,9 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
 
 
 // ---- per-stage event timing (diagnostic; off unless gdn_profile_enable(1) was called on this thread) ----
-enum Stage { ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_COUNT };
-static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step", "fwd_stash"};
+enum Stage { ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_FACTORS, ST_COUNT };
+static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step", "fwd_stash",
+                                            "factors"};
 struct ProfRec { int stage; hipEvent_t a, b; };
 struct Prof {
   bool on = false;
@@ -169,7 +176,7 @@ int gdn_chunk_fwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t*
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
-  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, 0, nullptr, nullptr);
+  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT, nullptr, nullptr);
   return GDN_OK;
 }
 
@@ -177,7 +184,7 @@ int gdn_chunk_bwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t*
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
-  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH | WS_GRAD, nullptr, nullptr);
+  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT | WS_STATE | WS_GRAD, nullptr, nullptr);
   return GDN_OK;
 }
 
@@ -212,15 +219,17 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* v, const flo
   }
   if (!q || !k || !v || !g || !beta || !o) return fail(GDN_ERR_ARG, "null input/output pointer");
   ChunkArgs a{};
-  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, stash ? WS_STASH : 0, &a.ws, ws);
-  if (need && (!ws || ws_bytes < need))
+  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, stash ? WS_STASH : WS_FACT, &a.ws, ws);
+  if (!ws || ws_bytes < need)
     return fail(GDN_ERR_WORKSPACE, "%s of %zu bytes needed, %zu given", stash ? "stash" : "workspace", need,
                 ws ? ws_bytes : (size_t)0);
   a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.h0 = h0; a.o = o; a.hT = hT;
   a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
-  const hipError_t e = stash ? timed(ST_FWD_STASH, st, [&] { return launch_fwd(a, FWD_STASH); })
-                             : timed(ST_FWD, st, [&] { return launch_fwd(a, FWD_OUT); });
+  hipError_t e = timed(ST_FACTORS, st, [&] { return launch_factors(a); });
+  if (e == hipSuccess)
+    e = stash ? timed(ST_FWD_STASH, st, [&] { return launch_fwd(a, FWD_STASH); })
+              : timed(ST_FWD, st, [&] { return launch_fwd(a, FWD_OUT); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "chunk forward launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }
@@ -252,7 +261,7 @@ static int chunk_bwd_impl(const void* q, const void* k, const void* v, const flo
       return fail(GDN_ERR_WORKSPACE, "stash of %zu bytes needed, %zu given", sneed,
                   stash ? stash_bytes : (size_t)0);
   }
-  const int parts = stashed ? WS_GRAD : (WS_STASH | WS_GRAD);
+  const int parts = stashed ? WS_GRAD : (WS_FACT | WS_STATE | WS_GRAD);
   const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, parts, &a.ws, ws);
   if (!ws || ws_bytes < need)
     return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
@@ -261,7 +270,10 @@ static int chunk_bwd_impl(const void* q, const void* k, const void* v, const flo
   a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
   hipError_t e = hipSuccess;
-  if (!stashed) e = timed(ST_BWD_RECOMP, st, [&] { return launch_fwd(a, FWD_RECOMPUTE); });
+  if (!stashed) {
+    e = timed(ST_FACTORS, st, [&] { return launch_factors(a); });
+    if (e == hipSuccess) e = timed(ST_BWD_RECOMP, st, [&] { return launch_fwd(a, FWD_RECOMPUTE); });
+  }
   if (e == hipSuccess) e = timed(ST_BWD_STATE, st, [&] { return launch_bwd_state(a); });
   if (e == hipSuccess) e = timed(ST_BWD_INTRA, st, [&] { return launch_bwd_intra(a); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "chunk backward launch: %s", hipGetErrorString(e));

@@ -1,14 +1,12 @@
 // Chunkwise gated delta rule, backward.
 //
-// The backward recomputes the entering state of every chunk (the forward sweep in backward mode) rather than
-// keeping them from the forward, then runs:
+// The backward takes the chunk factors (Tm, P, G) and the state entering every chunk with R from the stashing
+// forward, or rebuilds them first (chunk factors kernel, then the forward sweep in recompute mode), then runs:
 //
-// bwd_state: one workgroup per (64-wide V block, b*h), reverse over chunks; per chunk it rebuilds the chunk
-//   factors on-chip and each wave carries a 16-column slab of dS in MFMA accumulators.  bf16 runs the two roles
-//   of the forward sweep (four state waves, four factor waves, two LDS buffer sets): the factors of chunk c - 1
-//   are built while the state-gradient part of chunk c runs.
+// bwd_state: one workgroup per (64-wide V block, b*h), reverse over chunks, reading the chunk factors; each
+//   wave carries a 16-column slab of dS in MFMA accumulators.
 //     dR  = P^T dO + Kd dS_C                         Kd = diag(exp(G_C - G)) K
-//     dS0 = gamma_C dS_C + s (diag(gamma) Q)^T dO - W^T dR,   W^T dR = K^T diag(gamma) (TmB^T dR)
+//     dS0 = gamma_C dS_C + s (diag(gamma) Q)^T dO - W^T dR,   W^T dR = K^T diag(beta gamma) (Tm^T dR)
 //   Writes dS_C (the gradient w.r.t. the state leaving each chunk) and dR per chunk, and dh0.
 //   (The reverse state-gradient recurrence of fla's chunk_gated_delta_rule_bwd_dhu, called at
 //   archbench/layers/nsgdn.py:378.)
@@ -29,219 +27,157 @@
 
 namespace gdn {
 
-template <typename T, int K, int BV, bool WS>
-__global__ __launch_bounds__(WS ? 2 * NTHR : NTHR) void bwd_state_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ dout, const float* __restrict__ g,
-    const float* __restrict__ beta, const float* __restrict__ dhT, float* __restrict__ dh0, T* __restrict__ wsdH,
-    T* __restrict__ wsdR, int T_, int H, int V, int NT, float scale) {
+template <typename T, int K, int BV>
+__global__ __launch_bounds__(NTHR) void bwd_state_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ dout, const float* __restrict__ beta,
+    const T* __restrict__ gTm, const T* __restrict__ gP, const float* __restrict__ gGc,
+    const float* __restrict__ dhT, float* __restrict__ dh0, T* __restrict__ wsdH, T* __restrict__ wsdR, int T_,
+    int H, int V, int NT, float scale) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
   constexpr int NKT = K / 16;
-  static_assert(BV / 16 / NWAVE == 1, "each state wave owns one 16-column slab of dS");
-  constexpr int NB = WS ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) T sK[NB][CH * LK];
-  __shared__ __attribute__((aligned(16))) T sQ[NB][CH * LK];
-  __shared__ __attribute__((aligned(16))) T sdO[NB][CH * LV];  // dO rows of this V block
-  __shared__ __attribute__((aligned(16))) T sP[NB][CH * LC];
-  __shared__ __attribute__((aligned(16))) T sTmB[NB][CH * LC];  // Tm diag(beta)
-  __shared__ __attribute__((aligned(16))) float sA[CH * (CH + 4)];
-  __shared__ __attribute__((aligned(16))) float sD[4 * DBLK];
-  __shared__ float sG[NB][CH], sB[NB][CH], sGam[NB][CH];
+  static_assert(BV / 16 / NWAVE == 1, "each wave owns one 16-column slab of dS");
+  __shared__ __attribute__((aligned(16))) T sK[CH * LK];
+  __shared__ __attribute__((aligned(16))) T sQ[CH * LK];
+  __shared__ __attribute__((aligned(16))) T sdO[CH * LV];  // dO rows of this V block
+  __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
+  __shared__ __attribute__((aligned(16))) T sP[CH * LC];
+  __shared__ float sG[CH], sB[CH], sGam[CH];
 
   int vb, bh;
   sweep_block(V / BV, gridDim.x * BV / V, vb, bh);
   const int b = bh / H, h = bh - b * H;
   const int v0 = vb * BV;
   const int w = wave_id(), l = lane_id();
-  const int wr = w & (NWAVE - 1);            // wave index inside its role
-  const int tid = threadIdx.x & (NTHR - 1);  // thread index inside its role
+  const int c0 = 16 * w;
+  const int ncb = V / 16, cb = vb * (BV / 16) + w;  // fragment-layout column block of this wave
   const int64_t sbase = (int64_t)bh * K * V;
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
-  // ---- factor role: K, g, beta of a chunk, and its factors (P included) --------------------------------------
-  RegTile<T, CH, K> rk;
-  RegTok rt;
-  auto prefetch_f = [&](int c) {
-    rk.load(k + row0_of(c) * K, (int64_t)H * K, nvalid_of(c), tid);
-    if (wr == 0) rt.load(g, beta, row0_of(c), H, nvalid_of(c));
-  };
-  auto store_f = [&](int n) {
-    rk.store(sK[n], LK, tid);
-    if (wr == 0) {
-      const float G = wave_inclusive_scan(rt.ok ? rt.g : 0.f);
-      sG[n][l] = G;
-      sB[n][l] = rt.ok ? rt.b : 0.f;
-      sGam[n][l] = __expf(G);
+  RegTile<T, CH, K> rk, rq;
+  RegTile<T, CH, BV> rdo;
+  RegTile<T, CH, CH> rtm, rp;
+  float pG = 0.f, pB = 0.f;
+  auto prefetch = [&](int c) {
+    const int64_t row0 = row0_of(c), cidx = (int64_t)bh * NT + c;
+    const int nv = nvalid_of(c);
+    rk.load(k + row0 * K, (int64_t)H * K, nv);
+    rq.load(q + row0 * K, (int64_t)H * K, nv);
+    rdo.load(dout + row0 * V + v0, (int64_t)H * V, nv);
+    rtm.load(gTm + cidx * CH * CH, (int64_t)CH, CH);
+    rp.load(gP + cidx * CH * CH, (int64_t)CH, CH);
+    if (w == 0) {
+      pG = gGc[cidx * CH + l];
+      pB = l < nv ? beta[row0 + (int64_t)l * H] : 0.f;
     }
-  };
-  auto kq_diag = [&](int n) {
-    factors_kq<T, K, 1>(sK[n], sQ[n], sG[n], sB[n], scale, sA, sP[n], wr);
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the diagonal block reads this wave's rows of A
-    return factors_diag<T>(sA, sD, sTmB[n], nullptr, sB[n], wr);
   };
 
-  // ---- state role: Q and dO of a chunk, and the state-gradient part ------------------------------------------
-  RegTile<T, CH, K> rq;
-  RegTile<T, CH, BV> rdo;
-  auto prefetch_s = [&](int c) {
-    rq.load(q + row0_of(c) * K, (int64_t)H * K, nvalid_of(c), tid);
-    rdo.load(dout + row0_of(c) * V + v0, (int64_t)H * V, nvalid_of(c), tid);
-  };
-  auto store_s = [&](int n) {
-    rq.store(sQ[n], LK, tid);
-    rdo.store(sdO[n], LV, tid);
-  };
-  const int c0 = 16 * wr;
-  const int ncb = V / 16, cb = vb * (BV / 16) + wr;  // fragment-layout column block of a state wave
   f32x4 dS[NKT];
-  f32x4 dR[4];
-  typename Frag<T>::type dOg[2], Zb[2];
-  auto load_dhT = [&]() {
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
+  for (int t = 0; t < NKT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        dS[t][i] = dhT ? dhT[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
-  };
-  // C: dS leaving the chunk -> dh (fragment layout);  dR = diag(exp(G_C - G)) K dS + P^T dO
-  auto state_C = [&](int c, int n) {
-    typename Frag<T>::type dSb[K / 32];
-#pragma unroll
-    for (int s = 0; s < K / 32; ++s) {
-      dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
-      store_fragblk<T>(wsdH + ((int64_t)bh * NT + c) * K * V, s, cb, ncb, dSb[s]);
+    for (int i = 0; i < 4; ++i)
+      dS[t][i] = dhT ? dhT[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
+
+  // One chunk; the first (last in time) is peeled out of the loop so that the loop is entered with the same
+  // vector memory operations in flight as its back edge carries, which keeps the compiler's wait counts for the
+  // prefetched registers from also covering the stores issued after them.
+  auto chunk = [&](int c) {
+    const int64_t cidx = (int64_t)bh * NT + c;
+    rk.store(sK, LK);
+    rq.store(sQ, LK);
+    rdo.store(sdO, LV);
+    rtm.store(sTm, LC);
+    rp.store(sP, LC);
+    if (w == 0) {
+      sG[l] = pG;
+      sB[l] = pB;
+      sGam[l] = __expf(pG);
     }
-    const float GC = sG[n][CH - 1];
+    __syncthreads();
+    if (c > 0) prefetch(c - 1);
+
+    // dS leaving the chunk -> dh (fragment layout);  dR = diag(exp(G_C - G)) K dS + P^T dO
+    const float GC = sG[CH - 1];
+    f32x4 dR[4];
+    {
+      typename Frag<T>::type dSb[K / 32];
 #pragma unroll
-    for (int rt_ = 0; rt_ < 4; ++rt_) {
-      f32x4 kd = {0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < K / 32; ++s) {
+        dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
+        store_fragblk<T>(wsdH + cidx * K * V, s, cb, ncb, dSb[s]);
+      }
 #pragma unroll
-      for (int s = 0; s < K / 32; ++s) mma(kd, frag_kc_perm(sK[n], LK, 16 * rt_, 32 * s), dSb[s]);
+      for (int rt_ = 0; rt_ < 4; ++rt_) {
+        f32x4 kd = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dR[rt_][i] = __expf(GC - sG[n][16 * rt_ + acc_row(i)]) * kd[i];
+        for (int s = 0; s < K / 32; ++s) mma(kd, frag_kc_perm(sK, LK, 16 * rt_, 32 * s), dSb[s]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dR[rt_][i] = __expf(GC - sG[16 * rt_ + acc_row(i)]) * kd[i];
+      }
     }
     // dO fragments of this wave's columns over the chunk's tokens: plain, and scaled by gamma
-    typename Frag<T>::type dOb[2];
+    typename Frag<T>::type dOg[2];
+    {
+      typename Frag<T>::type dOb[2];
 #pragma unroll
-    for (int ib = 0; ib < 2; ++ib) {
-      dOb[ib] = frag_oct(sdO[n], LV, c0, 32 * ib);
+      for (int ib = 0; ib < 2; ++ib) {
+        dOb[ib] = frag_oct(sdO, LV, c0, 32 * ib);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dOg[ib][e] = from_f<T>(to_f(dOb[ib][e]) * sGam[n][32 * ib + 8 * (l >> 4) + e]);
+        for (int e = 0; e < 8; ++e) dOg[ib][e] = from_f<T>(to_f(dOb[ib][e]) * sGam[32 * ib + 8 * (l >> 4) + e]);
+      }
+#pragma unroll
+      for (int rt_ = 0; rt_ < 4; ++rt_)
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) mma(dR[rt_], frag_oct(sP, LC, 16 * rt_, 32 * ib), dOb[ib]);
     }
+    // dR -> global (fragment layout);  Z = diag(beta gamma) Tm^T dR  (W^T dR = K^T Z)
+    typename Frag<T>::type Zb[2];
+    {
+      typename Frag<T>::type dRb[2];
 #pragma unroll
-    for (int rt_ = 0; rt_ < 4; ++rt_)
+      for (int jb = 0; jb < 2; ++jb) {
+        dRb[jb] = frag_acc2<T>(dR[2 * jb], dR[2 * jb + 1]);
+        store_fragblk<T>(wsdR + cidx * CH * V, jb, cb, ncb, dRb[jb]);
+      }
+      f32x4 Z[4];
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) mma(dR[rt_], frag_oct(sP[n], LC, 16 * rt_, 32 * ib), dOb[ib]);
-  };
-  // D: dR -> global (fragment layout);  Z = gamma (TmB^T dR)  (W^T dR = K^T Z)
-  auto state_D = [&](int c, int n) {
-    typename Frag<T>::type dRb[2];
+      for (int rt_ = 0; rt_ < 4; ++rt_) {
+        Z[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-      dRb[jb] = frag_acc2<T>(dR[2 * jb], dR[2 * jb + 1]);
-      store_fragblk<T>(wsdR + ((int64_t)bh * NT + c) * CH * V, jb, cb, ncb, dRb[jb]);
+        for (int jb = 0; jb < 2; ++jb) mma(Z[rt_], frag_oct_perm(sTm, LC, 16 * rt_, 32 * jb), dRb[jb]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * rt_ + acc_row(i);
+          Z[rt_][i] *= sB[r] * sGam[r];
+        }
+      }
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) Zb[jb] = frag_acc2<T>(Z[2 * jb], Z[2 * jb + 1]);
     }
-    f32x4 Z[4];
-#pragma unroll
-    for (int rt_ = 0; rt_ < 4; ++rt_) {
-      Z[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) mma(Z[rt_], frag_oct_perm(sTmB[n], LC, 16 * rt_, 32 * jb), dRb[jb]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) Z[rt_][i] *= sGam[n][16 * rt_ + acc_row(i)];
-    }
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb) Zb[jb] = frag_acc2<T>(Z[2 * jb], Z[2 * jb + 1]);
-  };
-  // E: dS <- gamma_C dS + s Q^T (gamma dO) - K^T Z
-  auto state_E = [&](int n) {
-    const float gC = __expf(sG[n][CH - 1]);
+    // dS <- gamma_C dS + s Q^T (gamma dO) - K^T Z
+    const float gC = __expf(GC);
 #pragma unroll
     for (int t = 0; t < NKT; ++t) {
       f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) mma(a1, frag_oct(sQ[n], LK, 16 * t, 32 * ib), dOg[ib]);
+      for (int ib = 0; ib < 2; ++ib) mma(a1, frag_oct(sQ, LK, 16 * t, 32 * ib), dOg[ib]);
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) mma(a2, frag_oct_perm(sK[n], LK, 16 * t, 32 * jb), Zb[jb]);
+      for (int jb = 0; jb < 2; ++jb) mma(a2, frag_oct_perm(sK, LK, 16 * t, 32 * jb), Zb[jb]);
       dS[t] = gC * dS[t] + scale * a1 - a2;
     }
+    __syncthreads();  // every wave done with this chunk's inputs
   };
-  auto store_dh0 = [&]() {
-    if (dh0) {
+  prefetch(NT - 1);
+  chunk(NT - 1);
+  for (int c = NT - 2; c >= 0; --c) chunk(c);
+  if (dh0) {
 #pragma unroll
-      for (int t = 0; t < NKT; ++t)
+    for (int t = 0; t < NKT; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          dh0[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] = dS[t][i];
-    }
-  };
-
-  if constexpr (WS) {
-    // Reverse sweep.  Both roles execute the same barriers: two in the prologue, then three per chunk; at step i
-    // the state waves work on chunk c = NT-1-i (buffer set i&1), the factor waves on chunk c-1.
-    if (w >= NWAVE) {
-      prefetch_f(NT - 1);
-      store_f(0);
-      __syncthreads();
-      prefetch_f(max(NT - 2, 0));
-      const f32x4 D0 = kq_diag(0);
-      __syncthreads();
-      factors_merge<T>(D0, sA, sD, sTmB[0], nullptr, sB[0], wr);
-      for (int i = 0; i < NT; ++i) {
-        const int c = NT - 1 - i, nn = (i & 1) ^ 1;
-        __syncthreads();  // P1
-        if (c > 0) store_f(nn);
-        prefetch_f(max(c - 2, 0));
-        __syncthreads();  // P2
-        f32x4 D = zero4();
-        if (c > 0) D = kq_diag(nn);
-        __syncthreads();  // P3
-        if (c > 0) factors_merge<T>(D, sA, sD, sTmB[nn], nullptr, sB[nn], wr);
-      }
-    } else {
-      load_dhT();
-      prefetch_s(NT - 1);
-      store_s(0);
-      __syncthreads();
-      prefetch_s(max(NT - 2, 0));
-      __syncthreads();
-      for (int i = 0; i < NT; ++i) {
-        const int c = NT - 1 - i, n = i & 1, nn = n ^ 1;
-        __syncthreads();  // P1
-        if (c > 0) store_s(nn);
-        prefetch_s(max(c - 2, 0));
-        state_C(c, n);
-        __syncthreads();  // P2
-        state_D(c, n);
-        __syncthreads();  // P3
-        state_E(n);
-      }
-      store_dh0();
-    }
-  } else {
-    load_dhT();
-    prefetch_f(NT - 1);
-    prefetch_s(NT - 1);
-    for (int c = NT - 1; c >= 0; --c) {
-      store_f(0);
-      store_s(0);
-      __syncthreads();
-      if (c > 0) {
-        prefetch_f(c - 1);
-        prefetch_s(c - 1);
-      }
-      const f32x4 D = kq_diag(0);
-      __syncthreads();  // P complete
-      state_C(c, 0);
-      factors_merge<T>(D, sA, sD, sTmB[0], nullptr, sB[0], wr);
-      __syncthreads();
-      state_D(c, 0);
-      __syncthreads();
-      state_E(0);
-      __syncthreads();
-    }
-    store_dh0();
+      for (int i = 0; i < 4; ++i)
+        dh0[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] = dS[t][i];
   }
 }
 
@@ -594,10 +530,10 @@ template <typename T, int K>
 static hipError_t bwd_state_k(const ChunkArgs& a) {
   constexpr int BV = 64;
   dim3 grid(a.V / BV * a.B * a.H);
-  constexpr bool WS = sizeof(T) == 2;
-  bwd_state_kernel<T, K, BV, WS><<<grid, WS ? 2 * NTHR : NTHR, 0, a.stream>>>(
-      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.dout), a.g, a.beta, a.dhT,
-      a.dh0, static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dRs), a.T, a.H, a.V, a.NT, a.scale);
+  bwd_state_kernel<T, K, BV><<<grid, NTHR, 0, a.stream>>>(
+      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.dout), a.beta,
+      static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P), a.ws.Gc, a.dhT, a.dh0,
+      static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dRs), a.T, a.H, a.V, a.NT, a.scale);
   return hipGetLastError();
 }
 

@@ -1,0 +1,85 @@
+// Chunk factors of the chunkwise gated delta rule: one workgroup per (chunk, b*h), all chunks in parallel.
+//
+// For the 64 tokens of a chunk (archbench/layers/nsgdn.py:240-249 algebra with beta folded into A's rows; the
+// cumsum -> K K^T -> solve_tril steps of fla's GDN chunk forward, nsgdn.py:357-360):
+//   G    chunk-local inclusive cumsum of g                                            -> Gc [BH][NT][64] fp32
+//   A    beta_i (k_i . k_j) exp(G_i - G_j), strictly lower, on MFMA (fp32 in LDS)
+//   Tm   (I + A)^-1: diagonal 16x16 blocks by Neumann products, blocks below by column chains (bf16x3 MFMA)
+//                                                                                     -> Tm [BH][NT][64][64]
+//   P    s (q_i . k_j) exp(G_i - G_j) for i >= j                                      -> P  [BH][NT][64][64]
+// The sweeps over the sequence (forward, recompute, reverse) read these instead of rebuilding them for every
+// 64-wide V block, and the gradient kernel reads Tm and G.  Rows past the end of the sequence hold zero k, q
+// and beta, which makes Tm the identity and P zero there.
+#include "gdn_chunk_common.h"
+#include "gdn_launch.h"
+
+namespace gdn {
+
+template <typename T, int K>
+__global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                             const float* __restrict__ g,
+                                                             const float* __restrict__ beta, T* __restrict__ gTm,
+                                                             T* __restrict__ gP, float* __restrict__ gGc, int T_,
+                                                             int H, int NT, float scale) {
+  constexpr int PT = 16 / sizeof(T);
+  constexpr int LK = K + PT, LC = CH + PT, LF = CH + 4;
+  __shared__ __attribute__((aligned(16))) T sK[CH * LK];
+  __shared__ __attribute__((aligned(16))) T sQ[CH * LK];
+  __shared__ __attribute__((aligned(16))) float sA[CH * LF];
+  __shared__ __attribute__((aligned(16))) float sD[4 * DBLK];
+  __shared__ __attribute__((aligned(16))) T sP[CH * LC];
+  __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
+  __shared__ float sG[CH], sB[CH], sOne[CH];
+
+  const int c = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / H, h = bh - b * H;
+  const int w = wave_id(), l = lane_id();
+  const int nvalid = min(CH, T_ - c * CH);
+  const int64_t row0 = ((int64_t)b * T_ + (int64_t)c * CH) * H + h;
+  const int64_t cidx = (int64_t)bh * NT + c;
+
+  RegTile<T, CH, K> rk, rq;
+  RegTok rt;
+  rk.load(k + row0 * K, (int64_t)H * K, nvalid);
+  rq.load(q + row0 * K, (int64_t)H * K, nvalid);
+  if (w == 0) rt.load(g, beta, row0, H, nvalid);
+  rk.store(sK, LK);
+  rq.store(sQ, LK);
+  if (w == 0) {
+    const float G = wave_inclusive_scan(rt.ok ? rt.g : 0.f);
+    sG[l] = G;
+    sB[l] = rt.ok ? rt.b : 0.f;
+    sOne[l] = 1.f;
+    gGc[cidx * CH + l] = G;
+  }
+  __syncthreads();
+  factors_kq<T, K, 1>(sK, sQ, sG, sB, scale, sA, sP, w);
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the diagonal block reads this wave's rows of A
+  const f32x4 D = factors_diag<T>(sA, sD, sTm, nullptr, sOne, w);
+  __syncthreads();
+  factors_merge<T>(D, sA, sD, sTm, nullptr, sOne, w);
+  __syncthreads();
+  s2g_rows(gTm + cidx * CH * CH, (int64_t)CH, sTm, LC, CH, CH, CH);
+  s2g_rows(gP + cidx * CH * CH, (int64_t)CH, sP, LC, CH, CH, CH);
+}
+
+template <typename T, int K>
+static hipError_t factors_k(const ChunkArgs& a) {
+  dim3 grid(a.NT, a.B * a.H);
+  chunk_factors_kernel<T, K><<<grid, NTHR, 0, a.stream>>>(
+      static_cast<const T*>(a.q), static_cast<const T*>(a.k), a.g, a.beta, static_cast<T*>(a.ws.Tm),
+      static_cast<T*>(a.ws.P), a.ws.Gc, a.T, a.H, a.NT, a.scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_factors(const ChunkArgs& a) {
+  if (a.dtype == DT_BF16) {
+    if (a.K == 64) return factors_k<bf16, 64>(a);
+    if (a.K == 128) return factors_k<bf16, 128>(a);
+  } else {
+    if (a.K == 64) return factors_k<float, 64>(a);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace gdn

@@ -23,11 +23,12 @@ struct StepArgs {
 };
 
 // Chunk workspace carve-up (chunk-major: [B*H][NT][...]).  All offsets are 256-byte aligned.
-// The plain forward needs no workspace.  Tm, Gc, hs and Rs are filled by the stashing forward or by the
-// backward's recompute sweep, dhs and dRs by the reverse sweep, and the gradient kernel reads them all.
+// Parts: WS_FACT = {Tm, P, Gc} (the chunk factors kernel), WS_STATE = {hs, Rs} (the stashing forward or the
+// recompute sweep), WS_GRAD = {dhs, dRs} (the reverse sweep); the gradient kernel reads all but P.
 // hs, Rs, dhs and dRs use the fragment layout of the sweeps' accumulators (store_fragblk).
 struct ChunkWs {
   void* Tm;   // [BH][NT][64][64]   (I + A)^-1 per chunk, input dtype
+  void* P;    // [BH][NT][64][64]   s (Q K^T) o exp(G_i - G_j), lower triangle incl. diagonal, input dtype
   float* Gc;  // [BH][NT][64]       chunk-local cumulative log-decay
   void* hs;   // [BH][NT][K][V]     state entering each chunk
   void* Rs;   // [BH][NT][64][V]    R = U - W S per chunk
@@ -54,14 +55,15 @@ struct ChunkArgs {
   hipStream_t stream;
 };
 
-// Workspace parts: WS_STASH = {Tm, Gc, hs, Rs}, WS_GRAD = {dhs, dRs}.  Returns the bytes of the requested
-// parts laid out from `base` and, if `carve` is non-null, sets the pointers of those parts (others untouched).
-enum WsPart { WS_STASH = 1, WS_GRAD = 2 };
+// Returns the bytes of the requested parts laid out from `base` and, if `carve` is non-null, sets the pointers
+// of those parts (others untouched).
+enum WsPart { WS_FACT = 1, WS_STATE = 2, WS_GRAD = 4, WS_STASH = WS_FACT | WS_STATE };
 size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, ChunkWs* carve, void* base);
 bool chunk_shape_supported(int K, int V, int dtype);
 bool step_shape_supported(int K, int V);
 
 hipError_t launch_step(const StepArgs& a);
+hipError_t launch_factors(const ChunkArgs& a);                  // Tm, P, Gc
 // FWD_OUT: o, hT.  FWD_RECOMPUTE: hs, Rs, Tm, Gc.  FWD_STASH: both.
 enum FwdMode { FWD_OUT = 0, FWD_RECOMPUTE = 1, FWD_STASH = 2 };
 hipError_t launch_fwd(const ChunkArgs& a, FwdMode mode);
