@@ -60,6 +60,17 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
   return off;
 }
 
+int device_cu_count() {
+  static int cached[64] = {0};  // concurrent first calls store the same value
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (dev < 64) cached[dev] = cus;
+  return cus;
+}
+
 bool chunk_shape_supported(int K, int V, int dtype) {
   const bool v_ok = V == 64 || V == 128 || V == 256;
   if (dtype == DT_BF16) return (K == 64 || K == 128) && v_ok;

@@ -10,17 +10,21 @@
 // The sweeps over the sequence (forward, recompute, reverse) read these instead of rebuilding them for every
 // 64-wide V block, and the gradient kernel reads Tm and G.  Rows past the end of the sequence hold zero k, q
 // and beta, which makes Tm the identity and P zero there.
+#include <algorithm>
+
 #include "gdn_chunk_common.h"
 #include "gdn_launch.h"
 
 namespace gdn {
 
+// Persistent: workgroup x handles items x, x + gridDim.x, ... of the (b*h, chunk) grid (item = bh * NT + c), with
+// the next item's k, q, g and beta prefetched into registers while the current one is factored.
 template <typename T, int K>
 __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k,
                                                              const float* __restrict__ g,
                                                              const float* __restrict__ beta, T* __restrict__ gTm,
                                                              T* __restrict__ gP, float* __restrict__ gGc, int T_,
-                                                             int H, int NT, float scale) {
+                                                             int H, int NT, int nitems, float scale) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LF = CH + 4;
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
@@ -31,44 +35,51 @@ __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict
   __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
   __shared__ float sG[CH], sB[CH], sOne[CH];
 
-  const int c = blockIdx.x, bh = blockIdx.y;
-  const int b = bh / H, h = bh - b * H;
   const int w = wave_id(), l = lane_id();
-  const int nvalid = min(CH, T_ - c * CH);
-  const int64_t row0 = ((int64_t)b * T_ + (int64_t)c * CH) * H + h;
-  const int64_t cidx = (int64_t)bh * NT + c;
-
   RegTile<T, CH, K> rk, rq;
   RegTok rt;
-  rk.load(k + row0 * K, (int64_t)H * K, nvalid);
-  rq.load(q + row0 * K, (int64_t)H * K, nvalid);
-  if (w == 0) rt.load(g, beta, row0, H, nvalid);
-  rk.store(sK, LK);
-  rq.store(sQ, LK);
-  if (w == 0) {
-    const float G = wave_inclusive_scan(rt.ok ? rt.g : 0.f);
-    sG[l] = G;
-    sB[l] = rt.ok ? rt.b : 0.f;
-    sOne[l] = 1.f;
-    gGc[cidx * CH + l] = G;
+  auto prefetch = [&](int it) {
+    const int bh = it / NT, c = it - bh * NT;
+    const int b = bh / H, h = bh - b * H;
+    const int nvalid = min(CH, T_ - c * CH);
+    const int64_t row0 = ((int64_t)b * T_ + (int64_t)c * CH) * H + h;
+    rk.load(k + row0 * K, (int64_t)H * K, nvalid);
+    rq.load(q + row0 * K, (int64_t)H * K, nvalid);
+    if (w == 0) rt.load(g, beta, row0, H, nvalid);
+  };
+  if (w == 0) sOne[l] = 1.f;
+  if ((int)blockIdx.x < nitems) prefetch(blockIdx.x);
+  for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
+    rk.store(sK, LK);
+    rq.store(sQ, LK);
+    if (w == 0) {
+      const float G = wave_inclusive_scan(rt.ok ? rt.g : 0.f);
+      sG[l] = G;
+      sB[l] = rt.ok ? rt.b : 0.f;
+      gGc[(int64_t)it * CH + l] = G;
+    }
+    __syncthreads();
+    if (it + (int)gridDim.x < nitems) prefetch(it + gridDim.x);
+    factors_kq<T, K, 1>(sK, sQ, sG, sB, scale, sA, sP, w);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the diagonal block reads this wave's rows of A
+    const f32x4 D = factors_diag<T>(sA, sD, sTm, nullptr, sOne, w);
+    __syncthreads();
+    factors_merge<T>(D, sA, sD, sTm, nullptr, sOne, w);
+    __syncthreads();
+    s2g_rows(gTm + (int64_t)it * CH * CH, (int64_t)CH, sTm, LC, CH, CH, CH);
+    s2g_rows(gP + (int64_t)it * CH * CH, (int64_t)CH, sP, LC, CH, CH, CH);
+    __syncthreads();  // LDS free for the next item
   }
-  __syncthreads();
-  factors_kq<T, K, 1>(sK, sQ, sG, sB, scale, sA, sP, w);
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the diagonal block reads this wave's rows of A
-  const f32x4 D = factors_diag<T>(sA, sD, sTm, nullptr, sOne, w);
-  __syncthreads();
-  factors_merge<T>(D, sA, sD, sTm, nullptr, sOne, w);
-  __syncthreads();
-  s2g_rows(gTm + cidx * CH * CH, (int64_t)CH, sTm, LC, CH, CH, CH);
-  s2g_rows(gP + cidx * CH * CH, (int64_t)CH, sP, LC, CH, CH, CH);
 }
 
 template <typename T, int K>
 static hipError_t factors_k(const ChunkArgs& a) {
-  dim3 grid(a.NT, a.B * a.H);
+  const int nitems = a.NT * a.B * a.H;
+  const int per_cu = sizeof(T) == 2 ? 2 : 1;  // workgroups resident per CU (LDS)
+  dim3 grid(std::min(nitems, per_cu * device_cu_count()));
   chunk_factors_kernel<T, K><<<grid, NTHR, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), a.g, a.beta, static_cast<T*>(a.ws.Tm),
-      static_cast<T*>(a.ws.P), a.ws.Gc, a.T, a.H, a.NT, a.scale);
+      static_cast<T*>(a.ws.P), a.ws.Gc, a.T, a.H, a.NT, nitems, a.scale);
   return hipGetLastError();
 }
 

@@ -62,6 +62,9 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
 bool chunk_shape_supported(int K, int V, int dtype);
 bool step_shape_supported(int K, int V);
 
+// Compute units of the current device (cached per device; 256 if the query fails).
+int device_cu_count();
+
 hipError_t launch_step(const StepArgs& a);
 hipError_t launch_factors(const ChunkArgs& a);                  // Tm, P, Gc
 // FWD_OUT: o, hT.  FWD_RECOMPUTE: hs, Rs, Tm, Gc.  FWD_STASH: both.
