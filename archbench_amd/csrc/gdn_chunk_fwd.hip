@@ -16,8 +16,16 @@
 
 namespace gdn {
 
+// Eight waves, two per SIMD.  Waves w and w + 4 share the 16-column slab 16 (w & 3) and each holds all of S for
+// it; the chunk's token rows are split between them (half hf = w >> 2 takes rows 32 hf .. 32 hf + 31, i.e. the
+// permuted-k fragment hf of every token-indexed product).  Each half computes K S, Q S, Y, R, P R and O for its
+// rows; the Y and Rd fragments of the other half come through LDS (16 bytes per lane each), and both halves
+// apply the full state update.
+constexpr int FW = 2 * NWAVE;  // waves of the forward sweep
+constexpr int FTH = 64 * FW;
+
 template <typename T, int K, int BV, int MODE>
-__global__ __launch_bounds__(NTHR) void fwd_sweep_kernel(
+__global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const float* __restrict__ beta,
     const float* __restrict__ h0, const T* __restrict__ gTm, const T* __restrict__ gP,
     const float* __restrict__ gGc, T* __restrict__ o, float* __restrict__ hT, T* __restrict__ wsH,
@@ -25,15 +33,17 @@ __global__ __launch_bounds__(NTHR) void fwd_sweep_kernel(
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
   constexpr int NKT = K / 16;  // row tiles of the state slab
-  static_assert(BV / 16 / NWAVE == 1, "each wave owns one 16-column slab of the state");
+  static_assert(BV / 16 / NWAVE == 1, "each wave pair owns one 16-column slab of the state");
   constexpr bool OUT = MODE != 1;   // O is computed (needs Q and P)
   constexpr bool SAVE = MODE != 0;  // per-chunk states and R are written
+  using F = typename Frag<T>::type;
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
   __shared__ __attribute__((aligned(16))) T sQ[OUT ? CH * LK : 8];
   __shared__ __attribute__((aligned(16))) T sV[CH * LV];
   __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
   __shared__ __attribute__((aligned(16))) T sP[OUT ? CH * LC : 8];
   __shared__ __attribute__((aligned(16))) T stage[OUT ? CH * LV : 8];  // O, for the coalesced store
+  __shared__ __attribute__((aligned(16))) F xY[FW][64], xR[FW][64], xRd[FW][64];  // exchange between halves
   __shared__ float sG[CH], sB[CH], sGam[CH];
 
   int vb, bh;
@@ -41,35 +51,37 @@ __global__ __launch_bounds__(NTHR) void fwd_sweep_kernel(
   const int b = bh / H, h = bh - b * H;
   const int v0 = vb * BV;
   const int w = wave_id(), l = lane_id();
-  const int c0 = 16 * w;                             // this wave's column slab inside the V block
-  const int ncb = V / 16, cb = vb * (BV / 16) + w;  // its fragment-layout column block
+  const int ws = w & (NWAVE - 1), hf = w >> 2;        // column slab, token half
+  const int c0 = 16 * ws;                             // the slab inside the V block
+  const int ncb = V / 16, cb = vb * (BV / 16) + ws;  // its fragment-layout column block
+  const int tid = threadIdx.x;
   const int64_t sbase = (int64_t)bh * K * V;
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
-  RegTile<T, CH, K> rk, rq;
-  RegTile<T, CH, BV> rv;
-  RegTile<T, CH, CH> rtm, rp;
+  RegTile<T, CH, K, FTH> rk, rq;
+  RegTile<T, CH, BV, FTH> rv;
+  RegTile<T, CH, CH, FTH> rtm, rp;
   float pG = 0.f, pB = 0.f;  // wave 0: G and beta of lane l's token
   auto prefetch = [&](int c) {
     const int64_t row0 = row0_of(c), cidx = (int64_t)bh * NT + c;
     const int nv = nvalid_of(c);
-    rk.load(k + row0 * K, (int64_t)H * K, nv);
-    if constexpr (OUT) rq.load(q + row0 * K, (int64_t)H * K, nv);
-    rv.load(v + row0 * V + v0, (int64_t)H * V, nv);
-    rtm.load(gTm + cidx * CH * CH, (int64_t)CH, CH);
-    if constexpr (OUT) rp.load(gP + cidx * CH * CH, (int64_t)CH, CH);
+    rk.load(k + row0 * K, (int64_t)H * K, nv, tid);
+    if constexpr (OUT) rq.load(q + row0 * K, (int64_t)H * K, nv, tid);
+    rv.load(v + row0 * V + v0, (int64_t)H * V, nv, tid);
+    rtm.load(gTm + cidx * CH * CH, (int64_t)CH, CH, tid);
+    if constexpr (OUT) rp.load(gP + cidx * CH * CH, (int64_t)CH, CH, tid);
     if (w == 0) {
       pG = gGc[cidx * CH + l];
       pB = l < nv ? beta[row0 + (int64_t)l * H] : 0.f;
     }
   };
   auto to_lds = [&]() {
-    rk.store(sK, LK);
-    if constexpr (OUT) rq.store(sQ, LK);
-    rv.store(sV, LV);
-    rtm.store(sTm, LC);
-    if constexpr (OUT) rp.store(sP, LC);
+    rk.store(sK, LK, tid);
+    if constexpr (OUT) rq.store(sQ, LK, tid);
+    rv.store(sV, LV, tid);
+    rtm.store(sTm, LC, tid);
+    if constexpr (OUT) rp.store(sP, LC, tid);
     if (w == 0) {
       sG[l] = pG;
       sB[l] = pB;
@@ -90,86 +102,97 @@ __global__ __launch_bounds__(NTHR) void fwd_sweep_kernel(
     __syncthreads();
     if (c + 1 < NT) prefetch(c + 1);
 
-    // K S, Q S and Y = diag(beta) (V - diag(gamma) K S); the entering state saved if SAVE
-    f32x4 Y[4], QS[4];
-    {
-      typename Frag<T>::type Sb[K / 32];
+    // rows 32 hf .. 32 hf + 31: K S, Q S and Y = diag(beta) (V - diag(gamma) K S)
+    F Sb[K / 32];
 #pragma unroll
-      for (int s = 0; s < K / 32; ++s) {
-        Sb[s] = frag_acc2<T>(S[2 * s], S[2 * s + 1]);
-        if constexpr (SAVE) store_fragblk<T>(wsH + cidx * K * V, s, cb, ncb, Sb[s]);
+    for (int s = 0; s < K / 32; ++s) {
+      Sb[s] = frag_acc2<T>(S[2 * s], S[2 * s + 1]);
+      if constexpr (SAVE) {
+        if ((s & 1) == hf) store_fragblk<T>(wsH + cidx * K * V, s, cb, ncb, Sb[s]);
+      }
+    }
+    f32x4 Y[2], QS[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int rt_ = 2 * hf + j;
+      f32x4 ks = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s) mma(ks, frag_kc_perm(sK, LK, 16 * rt_, 32 * s), Sb[s]);
+      if constexpr (OUT) {
+        QS[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < K / 32; ++s) mma(QS[j], frag_kc_perm(sQ, LK, 16 * rt_, 32 * s), Sb[s]);
       }
 #pragma unroll
-      for (int rt_ = 0; rt_ < 4; ++rt_) {
-        f32x4 ks = {0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * rt_ + acc_row(i);
+        Y[j][i] = sB[r] * (to_f(sV[r * LV + c0 + acc_col()]) - sGam[r] * ks[i]);
+      }
+    }
+    // (fragments are selected by value, never indexed by the half: registers cannot be indexed at run time)
+    const F Ymine = frag_acc2<T>(Y[0], Y[1]);
+    xY[w][l] = Ymine;
+    __syncthreads();
+    const F Yother = xY[w ^ NWAVE][l];
+    const F Yb0 = hf ? Yother : Ymine, Yb1 = hf ? Ymine : Yother;
+
+    // R = Tm Y for the half's rows (saved if SAVE); Rd = exp(G_C - G) R; O = s gamma QS + P R staged
+    f32x4 R[2];
 #pragma unroll
-        for (int s = 0; s < K / 32; ++s) mma(ks, frag_kc_perm(sK, LK, 16 * rt_, 32 * s), Sb[s]);
-        if constexpr (OUT) {
-          QS[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; ++j) {
+      R[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      mma(R[j], frag_kc_perm(sTm, LC, 16 * (2 * hf + j), 0), Yb0);
+      mma(R[j], frag_kc_perm(sTm, LC, 16 * (2 * hf + j), 32), Yb1);
+    }
+    const float GC = sG[CH - 1];
+    F Rdmine;
+    {
+      f32x4 d0, d1;
 #pragma unroll
-          for (int s = 0; s < K / 32; ++s) mma(QS[rt_], frag_kc_perm(sQ, LK, 16 * rt_, 32 * s), Sb[s]);
-        }
+      for (int i = 0; i < 4; ++i) {
+        d0[i] = R[0][i] * __expf(GC - sG[32 * hf + acc_row(i)]);
+        d1[i] = R[1][i] * __expf(GC - sG[32 * hf + 16 + acc_row(i)]);
+      }
+      Rdmine = frag_acc2<T>(d0, d1);
+      xRd[w][l] = Rdmine;
+    }
+    const F Rbmine = frag_acc2<T>(R[0], R[1]);
+    if constexpr (OUT) xR[w][l] = Rbmine;
+    if constexpr (SAVE) store_fragblk<T>(wsR + cidx * CH * V, hf, cb, ncb, Rbmine);
+    __syncthreads();  // R and Rd fragments of both halves exchanged
+    const F Rdother = xRd[w ^ NWAVE][l];
+    const F Rd0 = hf ? Rdother : Rdmine, Rd1 = hf ? Rdmine : Rdother;
+    if constexpr (OUT) {
+      const F Rbother = xR[w ^ NWAVE][l];
+      const F Rb0 = hf ? Rbother : Rbmine, Rb1 = hf ? Rbmine : Rbother;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int rt_ = 2 * hf + j;
+        f32x4 pr = {0.f, 0.f, 0.f, 0.f};
+        mma(pr, frag_kc_perm(sP, LC, 16 * rt_, 0), Rb0);
+        mma(pr, frag_kc_perm(sP, LC, 16 * rt_, 32), Rb1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = 16 * rt_ + acc_row(i);
-          Y[rt_][i] = sB[r] * (to_f(sV[r * LV + c0 + acc_col()]) - sGam[r] * ks[i]);
+          stage[r * LV + c0 + acc_col()] = from_f<T>(scale * sGam[r] * QS[j][i] + pr[i]);
         }
       }
     }
-    // R = Tm Y (saved if SAVE); Rd = exp(G_C - G) R for the state update; O = s gamma QS + P R staged
-    typename Frag<T>::type Rd[2];
-    {
-      typename Frag<T>::type Yb[2], Rb[2];
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) Yb[jb] = frag_acc2<T>(Y[2 * jb], Y[2 * jb + 1]);
-      f32x4 R[4];
-#pragma unroll
-      for (int rt_ = 0; rt_ < 4; ++rt_) {
-        R[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) mma(R[rt_], frag_kc_perm(sTm, LC, 16 * rt_, 32 * jb), Yb[jb]);
-      }
-      const float GC = sG[CH - 1];
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        f32x4 d0, d1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          d0[i] = R[2 * jb][i] * __expf(GC - sG[32 * jb + acc_row(i)]);
-          d1[i] = R[2 * jb + 1][i] * __expf(GC - sG[32 * jb + 16 + acc_row(i)]);
-        }
-        Rd[jb] = frag_acc2<T>(d0, d1);
-        Rb[jb] = frag_acc2<T>(R[2 * jb], R[2 * jb + 1]);
-        if constexpr (SAVE) store_fragblk<T>(wsR + cidx * CH * V, jb, cb, ncb, Rb[jb]);
-      }
-      if constexpr (OUT) {
-#pragma unroll
-        for (int rt_ = 0; rt_ < 4; ++rt_) {
-          f32x4 pr = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int jb = 0; jb < 2; ++jb) mma(pr, frag_kc_perm(sP, LC, 16 * rt_, 32 * jb), Rb[jb]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = 16 * rt_ + acc_row(i);
-            stage[r * LV + c0 + acc_col()] = from_f<T>(scale * sGam[r] * QS[rt_][i] + pr[i]);
-          }
-        }
-      }
-    }
-    // S <- gamma_C S + K^T Rd
-    const float gC = __expf(sG[CH - 1]);
+    // S <- gamma_C S + K^T Rd (all rows of K, both halves of the chunk)
+    const float gC = __expf(GC);
 #pragma unroll
     for (int t = 0; t < NKT; ++t) {
       S[t] *= gC;
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) mma(S[t], frag_oct_perm(sK, LK, 16 * t, 32 * jb), Rd[jb]);
+      mma(S[t], frag_oct_perm(sK, LK, 16 * t, 0), Rd0);
+      mma(S[t], frag_oct_perm(sK, LK, 16 * t, 32), Rd1);
     }
     __syncthreads();  // O staged; every wave done with this chunk's inputs
-    if constexpr (OUT) s2g_rows(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, CH, BV, nvalid_of(c));
+    if constexpr (OUT)
+      s2g_rows<T, FTH>(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, CH, BV, nvalid_of(c));
   };
   prefetch(0);
   for (int c = 0; c < NT; ++c) chunk(c);
-  if (hT) {
+  if (hT && hf == 0) {
 #pragma unroll
     for (int t = 0; t < NKT; ++t)
 #pragma unroll
@@ -182,7 +205,7 @@ template <typename T, int K, int MODE>
 static hipError_t fwd_sweep_k(const ChunkArgs& a) {
   constexpr int BV = 64;
   dim3 grid(a.V / BV * a.B * a.H);
-  fwd_sweep_kernel<T, K, BV, MODE><<<grid, NTHR, 0, a.stream>>>(
+  fwd_sweep_kernel<T, K, BV, MODE><<<grid, FTH, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.v), a.beta, a.h0,
       static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P), a.ws.Gc, static_cast<T*>(a.o),
       MODE == 1 ? nullptr : a.hT, static_cast<T*>(a.ws.hs), static_cast<T*>(a.ws.Rs), a.T, a.H, a.V, a.NT,
