@@ -27,21 +27,32 @@
 
 namespace gdn {
 
+// Eight waves, two per SIMD: waves w and w + 4 share the 16-column slab 16 (w & 3) of dS.  Half hf = w >> 2
+// holds rows 64 hf .. of dS (K = 128; rows K/2 hf .. in general) and computes dR and Z for the chunk's token
+// rows 32 hf .. 32 hf + 31.  Per chunk the halves swap through LDS: the partial K dS of the other half's token
+// rows (fp32), then the dR fragments, then the Z fragments (16 bytes per lane each).
+constexpr int SW = 2 * NWAVE;  // waves of the reverse sweep
+constexpr int STH = 64 * SW;
+
 template <typename T, int K, int BV>
-__global__ __launch_bounds__(NTHR) void bwd_state_kernel(
+__global__ __launch_bounds__(STH) void bwd_state_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ dout, const float* __restrict__ beta,
     const T* __restrict__ gTm, const T* __restrict__ gP, const float* __restrict__ gGc,
     const float* __restrict__ dhT, float* __restrict__ dh0, T* __restrict__ wsdH, T* __restrict__ wsdR, int T_,
     int H, int V, int NT, float scale) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
-  constexpr int NKT = K / 16;
-  static_assert(BV / 16 / NWAVE == 1, "each wave owns one 16-column slab of dS");
+  constexpr int NKH = K / 32;     // row tiles of dS per half
+  constexpr int NSH = K / 64;     // 32-row fragments of dS per half
+  static_assert(BV / 16 / NWAVE == 1, "each wave pair owns one 16-column slab of dS");
+  using F = typename Frag<T>::type;
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
   __shared__ __attribute__((aligned(16))) T sQ[CH * LK];
   __shared__ __attribute__((aligned(16))) T sdO[CH * LV];  // dO rows of this V block
   __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
   __shared__ __attribute__((aligned(16))) T sP[CH * LC];
+  __shared__ __attribute__((aligned(16))) f32x4 xKd[SW][2][64];      // partial K dS for the other half's rows
+  __shared__ __attribute__((aligned(16))) F xR[SW][64], xZ[SW][64];  // dR and Z fragments
   __shared__ float sG[CH], sB[CH], sGam[CH];
 
   int vb, bh;
@@ -49,47 +60,47 @@ __global__ __launch_bounds__(NTHR) void bwd_state_kernel(
   const int b = bh / H, h = bh - b * H;
   const int v0 = vb * BV;
   const int w = wave_id(), l = lane_id();
-  const int c0 = 16 * w;
-  const int ncb = V / 16, cb = vb * (BV / 16) + w;  // fragment-layout column block of this wave
+  const int ws = w & (NWAVE - 1), hf = w >> 2;  // column slab; half of dS's rows and of the chunk's tokens
+  const int c0 = 16 * ws;
+  const int ncb = V / 16, cb = vb * (BV / 16) + ws;  // fragment-layout column block of the slab
+  const int k0 = (K / 2) * hf;                       // first dS row of this half
+  const int tid = threadIdx.x;
   const int64_t sbase = (int64_t)bh * K * V;
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
-  RegTile<T, CH, K> rk, rq;
-  RegTile<T, CH, BV> rdo;
-  RegTile<T, CH, CH> rtm, rp;
+  RegTile<T, CH, K, STH> rk, rq;
+  RegTile<T, CH, BV, STH> rdo;
+  RegTile<T, CH, CH, STH> rtm, rp;
   float pG = 0.f, pB = 0.f;
   auto prefetch = [&](int c) {
     const int64_t row0 = row0_of(c), cidx = (int64_t)bh * NT + c;
     const int nv = nvalid_of(c);
-    rk.load(k + row0 * K, (int64_t)H * K, nv);
-    rq.load(q + row0 * K, (int64_t)H * K, nv);
-    rdo.load(dout + row0 * V + v0, (int64_t)H * V, nv);
-    rtm.load(gTm + cidx * CH * CH, (int64_t)CH, CH);
-    rp.load(gP + cidx * CH * CH, (int64_t)CH, CH);
+    rk.load(k + row0 * K, (int64_t)H * K, nv, tid);
+    rq.load(q + row0 * K, (int64_t)H * K, nv, tid);
+    rdo.load(dout + row0 * V + v0, (int64_t)H * V, nv, tid);
+    rtm.load(gTm + cidx * CH * CH, (int64_t)CH, CH, tid);
+    rp.load(gP + cidx * CH * CH, (int64_t)CH, CH, tid);
     if (w == 0) {
       pG = gGc[cidx * CH + l];
       pB = l < nv ? beta[row0 + (int64_t)l * H] : 0.f;
     }
   };
 
-  f32x4 dS[NKT];
+  f32x4 dS[NKH];
 #pragma unroll
-  for (int t = 0; t < NKT; ++t)
+  for (int t = 0; t < NKH; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      dS[t][i] = dhT ? dhT[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
+      dS[t][i] = dhT ? dhT[sbase + (int64_t)(k0 + 16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
 
-  // One chunk; the first (last in time) is peeled out of the loop so that the loop is entered with the same
-  // vector memory operations in flight as its back edge carries, which keeps the compiler's wait counts for the
-  // prefetched registers from also covering the stores issued after them.
   auto chunk = [&](int c) {
     const int64_t cidx = (int64_t)bh * NT + c;
-    rk.store(sK, LK);
-    rq.store(sQ, LK);
-    rdo.store(sdO, LV);
-    rtm.store(sTm, LC);
-    rp.store(sP, LC);
+    rk.store(sK, LK, tid);
+    rq.store(sQ, LK, tid);
+    rdo.store(sdO, LV, tid);
+    rtm.store(sTm, LC, tid);
+    rp.store(sP, LC, tid);
     if (w == 0) {
       sG[l] = pG;
       sB[l] = pB;
@@ -98,86 +109,90 @@ __global__ __launch_bounds__(NTHR) void bwd_state_kernel(
     __syncthreads();
     if (c > 0) prefetch(c - 1);
 
-    // dS leaving the chunk -> dh (fragment layout);  dR = diag(exp(G_C - G)) K dS + P^T dO
+    // dS leaving the chunk -> dh (fragment layout); partial K dS over this half's rows, for all tokens
     const float GC = sG[CH - 1];
-    f32x4 dR[4];
-    {
-      typename Frag<T>::type dSb[K / 32];
+    F dSb[NSH];
 #pragma unroll
-      for (int s = 0; s < K / 32; ++s) {
-        dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
-        store_fragblk<T>(wsdH + cidx * K * V, s, cb, ncb, dSb[s]);
-      }
+    for (int s = 0; s < NSH; ++s) {
+      dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
+      store_fragblk<T>(wsdH + cidx * K * V, NSH * hf + s, cb, ncb, dSb[s]);
+    }
+    f32x4 kd[4];
 #pragma unroll
-      for (int rt_ = 0; rt_ < 4; ++rt_) {
-        f32x4 kd = {0.f, 0.f, 0.f, 0.f};
+    for (int rt_ = 0; rt_ < 4; ++rt_) {
+      kd[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < K / 32; ++s) mma(kd, frag_kc_perm(sK, LK, 16 * rt_, 32 * s), dSb[s]);
+      for (int s = 0; s < NSH; ++s) mma(kd[rt_], frag_kc_perm(sK, LK, 16 * rt_, k0 + 32 * s), dSb[s]);
+    }
+    // (values are selected by the half, never indexed by it: registers cannot be indexed at run time)
+    xKd[w][0][l] = hf ? kd[0] : kd[2];  // the other half's token rows
+    xKd[w][1][l] = hf ? kd[1] : kd[3];
+    F dOb[2], dOg[2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dR[rt_][i] = __expf(GC - sG[16 * rt_ + acc_row(i)]) * kd[i];
+    for (int ib = 0; ib < 2; ++ib) {
+      dOb[ib] = frag_oct(sdO, LV, c0, 32 * ib);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dOg[ib][e] = from_f<T>(to_f(dOb[ib][e]) * sGam[32 * ib + 8 * (l >> 4) + e]);
+    }
+    __syncthreads();
+    // dR (this half's token rows) = diag(exp(G_C - G)) K dS + P^T dO
+    f32x4 dR[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int rt_ = 2 * hf + j;
+      const f32x4 mine = hf ? kd[2 + j] : kd[j];
+      const f32x4 other = xKd[w ^ NWAVE][j][l];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dR[j][i] = __expf(GC - sG[16 * rt_ + acc_row(i)]) * (mine[i] + other[i]);
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) mma(dR[j], frag_oct(sP, LC, 16 * rt_, 32 * ib), dOb[ib]);
+    }
+    // dR -> global and to the other half; Z (this half's token rows) = diag(beta gamma) Tm^T dR
+    const F dRmine = frag_acc2<T>(dR[0], dR[1]);
+    store_fragblk<T>(wsdR + cidx * CH * V, hf, cb, ncb, dRmine);
+    xR[w][l] = dRmine;
+    __syncthreads();
+    const F dRother = xR[w ^ NWAVE][l];
+    const F dR0 = hf ? dRother : dRmine, dR1 = hf ? dRmine : dRother;
+    f32x4 Z[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int rt_ = 2 * hf + j;
+      Z[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, 0), dR0);
+      mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, 32), dR1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * rt_ + acc_row(i);
+        Z[j][i] *= sB[r] * sGam[r];
       }
     }
-    // dO fragments of this wave's columns over the chunk's tokens: plain, and scaled by gamma
-    typename Frag<T>::type dOg[2];
-    {
-      typename Frag<T>::type dOb[2];
-#pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
-        dOb[ib] = frag_oct(sdO, LV, c0, 32 * ib);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dOg[ib][e] = from_f<T>(to_f(dOb[ib][e]) * sGam[32 * ib + 8 * (l >> 4) + e]);
-      }
-#pragma unroll
-      for (int rt_ = 0; rt_ < 4; ++rt_)
-#pragma unroll
-        for (int ib = 0; ib < 2; ++ib) mma(dR[rt_], frag_oct(sP, LC, 16 * rt_, 32 * ib), dOb[ib]);
-    }
-    // dR -> global (fragment layout);  Z = diag(beta gamma) Tm^T dR  (W^T dR = K^T Z)
-    typename Frag<T>::type Zb[2];
-    {
-      typename Frag<T>::type dRb[2];
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        dRb[jb] = frag_acc2<T>(dR[2 * jb], dR[2 * jb + 1]);
-        store_fragblk<T>(wsdR + cidx * CH * V, jb, cb, ncb, dRb[jb]);
-      }
-      f32x4 Z[4];
-#pragma unroll
-      for (int rt_ = 0; rt_ < 4; ++rt_) {
-        Z[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) mma(Z[rt_], frag_oct_perm(sTm, LC, 16 * rt_, 32 * jb), dRb[jb]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 16 * rt_ + acc_row(i);
-          Z[rt_][i] *= sB[r] * sGam[r];
-        }
-      }
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) Zb[jb] = frag_acc2<T>(Z[2 * jb], Z[2 * jb + 1]);
-    }
-    // dS <- gamma_C dS + s Q^T (gamma dO) - K^T Z
+    const F Zmine = frag_acc2<T>(Z[0], Z[1]);
+    xZ[w][l] = Zmine;
+    __syncthreads();
+    const F Zother = xZ[w ^ NWAVE][l];
+    const F Zb0 = hf ? Zother : Zmine, Zb1 = hf ? Zmine : Zother;
+    // this half's rows of dS <- gamma_C dS + s Q^T (gamma dO) - K^T Z
     const float gC = __expf(GC);
 #pragma unroll
-    for (int t = 0; t < NKT; ++t) {
+    for (int t = 0; t < NKH; ++t) {
       f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) mma(a1, frag_oct(sQ, LK, 16 * t, 32 * ib), dOg[ib]);
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) mma(a2, frag_oct_perm(sK, LK, 16 * t, 32 * jb), Zb[jb]);
+      for (int ib = 0; ib < 2; ++ib) mma(a1, frag_oct(sQ, LK, k0 + 16 * t, 32 * ib), dOg[ib]);
+      mma(a2, frag_oct_perm(sK, LK, k0 + 16 * t, 0), Zb0);
+      mma(a2, frag_oct_perm(sK, LK, k0 + 16 * t, 32), Zb1);
       dS[t] = gC * dS[t] + scale * a1 - a2;
     }
     __syncthreads();  // every wave done with this chunk's inputs
   };
   prefetch(NT - 1);
-  chunk(NT - 1);
-  for (int c = NT - 2; c >= 0; --c) chunk(c);
+  for (int c = NT - 1; c >= 0; --c) chunk(c);
   if (dh0) {
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
+    for (int t = 0; t < NKH; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        dh0[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] = dS[t][i];
+        dh0[sbase + (int64_t)(k0 + 16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] = dS[t][i];
   }
 }
 
@@ -530,7 +545,7 @@ template <typename T, int K>
 static hipError_t bwd_state_k(const ChunkArgs& a) {
   constexpr int BV = 64;
   dim3 grid(a.V / BV * a.B * a.H);
-  bwd_state_kernel<T, K, BV><<<grid, NTHR, 0, a.stream>>>(
+  bwd_state_kernel<T, K, BV><<<grid, STH, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.dout), a.beta,
       static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P), a.ws.Gc, a.dhT, a.dh0,
       static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dRs), a.T, a.H, a.V, a.NT, a.scale);
