@@ -73,12 +73,18 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
   RegTile<T, CH, BV, STH> rdo;
   RegTile<T, CH, CH, STH> rtm, rp;
   float pG = 0.f, pB = 0.f;
+  // The next chunk's reads go out in two batches (k, q, dO after the first barrier; Tm, P, G, beta after the
+  // dR exchange), so that no wave stalls on a full memory queue for the whole set at once.
   auto prefetch = [&](int c) {
-    const int64_t row0 = row0_of(c), cidx = (int64_t)bh * NT + c;
+    const int64_t row0 = row0_of(c);
     const int nv = nvalid_of(c);
     rk.load(k + row0 * K, (int64_t)H * K, nv, tid);
     rq.load(q + row0 * K, (int64_t)H * K, nv, tid);
     rdo.load(dout + row0 * V + v0, (int64_t)H * V, nv, tid);
+  };
+  auto prefetch2 = [&](int c) {
+    const int64_t row0 = row0_of(c), cidx = (int64_t)bh * NT + c;
+    const int nv = nvalid_of(c);
     rtm.load(gTm + cidx * CH * CH, (int64_t)CH, CH, tid);
     rp.load(gP + cidx * CH * CH, (int64_t)CH, CH, tid);
     if (w == 0) {
@@ -152,6 +158,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     store_fragblk<T>(wsdR + cidx * CH * V, hf, cb, ncb, dRmine);
     xR[w][l] = dRmine;
     __syncthreads();
+    if (c > 0) prefetch2(c - 1);
     const F dRother = xR[w ^ NWAVE][l];
     const F dR0 = hf ? dRother : dRmine, dR1 = hf ? dRmine : dRother;
     f32x4 Z[2];
@@ -186,6 +193,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     __syncthreads();  // every wave done with this chunk's inputs
   };
   prefetch(NT - 1);
+  prefetch2(NT - 1);
   for (int c = NT - 1; c >= 0; --c) chunk(c);
   if (dh0) {
 #pragma unroll

@@ -63,12 +63,18 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
   RegTile<T, CH, BV, FTH> rv;
   RegTile<T, CH, CH, FTH> rtm, rp;
   float pG = 0.f, pB = 0.f;  // wave 0: G and beta of lane l's token
+  // The next chunk's reads go out in two batches (k, q, v after the first barrier; Tm, P, G, beta after the
+  // second exchange), so that no wave stalls on a full memory queue for the whole set at once.
   auto prefetch = [&](int c) {
-    const int64_t row0 = row0_of(c), cidx = (int64_t)bh * NT + c;
+    const int64_t row0 = row0_of(c);
     const int nv = nvalid_of(c);
     rk.load(k + row0 * K, (int64_t)H * K, nv, tid);
     if constexpr (OUT) rq.load(q + row0 * K, (int64_t)H * K, nv, tid);
     rv.load(v + row0 * V + v0, (int64_t)H * V, nv, tid);
+  };
+  auto prefetch2 = [&](int c) {
+    const int64_t row0 = row0_of(c), cidx = (int64_t)bh * NT + c;
+    const int nv = nvalid_of(c);
     rtm.load(gTm + cidx * CH * CH, (int64_t)CH, CH, tid);
     if constexpr (OUT) rp.load(gP + cidx * CH * CH, (int64_t)CH, CH, tid);
     if (w == 0) {
@@ -160,6 +166,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     if constexpr (OUT) xR[w][l] = Rbmine;
     if constexpr (SAVE) store_fragblk<T>(wsR + cidx * CH * V, hf, cb, ncb, Rbmine);
     __syncthreads();  // R and Rd fragments of both halves exchanged
+    if (c + 1 < NT) prefetch2(c + 1);
     const F Rdother = xRd[w ^ NWAVE][l];
     const F Rd0 = hf ? Rdother : Rdmine, Rd1 = hf ? Rdmine : Rdother;
     if constexpr (OUT) {
@@ -191,6 +198,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
       s2g_rows<T, FTH>(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, CH, BV, nvalid_of(c));
   };
   prefetch(0);
+  prefetch2(0);
   for (int c = 0; c < NT; ++c) chunk(c);
   if (hT && hf == 0) {
 #pragma unroll
