@@ -36,11 +36,14 @@ SIGNATURES = {
     "gdn_chunk_bwd_stashed": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _sz,
                                    _i, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_recurrent_step": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i, _p]),
+    "gdn_short_conv_fwd": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
+    "gdn_short_conv_bwd_ws_bytes": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
+    "gdn_short_conv_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _i, _p]),
     "gdn_profile_enable": (_i, [_i]),
     "gdn_profile_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
     "gdn_profile_stage_name": (ctypes.c_char_p, [_i]),
 }
-PROFILE_STAGES = 7
+PROFILE_STAGES = 9
 
 _lock = threading.Lock()
 _lib = None
@@ -111,6 +114,12 @@ def stash_bytes(B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype) -> t
     check(load().gdn_chunk_stash_bytes(B, T, H, K, V, dtype_code(dtype), ctypes.byref(st), ctypes.byref(ws)),
           "gdn_chunk_stash_bytes")
     return st.value, ws.value
+
+
+def conv_ws_bytes(B: int, T: int, D: int, W: int) -> int:
+    out = _sz(0)
+    check(load().gdn_short_conv_bwd_ws_bytes(B, T, D, W, ctypes.byref(out)), "gdn_short_conv_bwd_ws_bytes")
+    return out.value
 
 
 class StageTimer:

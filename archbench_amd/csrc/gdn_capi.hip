@@ -83,6 +83,21 @@ __global__ void copy_or_zero_kernel(const float* __restrict__ src, float* __rest
   if (i < n) dst[i] = src ? src[i] : 0.f;
 }
 
+// Word copy (or zero fill when src is null) as a kernel rather than hipMemcpyAsync / hipMemsetAsync, so that
+// callers may capture these calls in a HIP graph.
+__global__ void copy_or_zero_words_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src ? src[i] : 0u;
+}
+
+static hipError_t copy_or_zero_bytes(const void* src, void* dst, size_t bytes, hipStream_t st) {
+  const int64_t n = (int64_t)(bytes / 4);  // every buffer here is a whole number of 32-bit words
+  if (!dst || n == 0) return hipSuccess;
+  copy_or_zero_words_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st>>>(
+      static_cast<const uint32_t*>(src), static_cast<uint32_t*>(dst), n);
+  return hipGetLastError();
+}
+
 static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStream_t st) {
   if (!dst || n == 0) return hipSuccess;
   const int64_t blocks = (n + 255) / 256;
@@ -92,9 +107,12 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
 
 
 // ---- per-stage event timing (diagnostic; off unless gdn_profile_enable(1) was called on this thread) ----
-enum Stage { ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_FACTORS, ST_COUNT };
+enum Stage {
+  ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_FACTORS, ST_CONV_FWD,
+  ST_CONV_BWD, ST_COUNT
+};
 static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step", "fwd_stash",
-                                            "factors"};
+                                            "factors", "conv_fwd", "conv_bwd"};
 struct ProfRec { int stage; hipEvent_t a, b; };
 struct Prof {
   bool on = false;
@@ -323,6 +341,75 @@ int gdn_chunk_bwd_stashed(const void* q, const void* k, const void* v, const flo
                           void* stream) {
   return chunk_bwd_impl(q, k, v, g, beta, h0, dout, dhT, dq, dk, dv, dg, dbeta, dh0, stash, stash_bytes, ws,
                         ws_bytes, B, T, H, K, V, scale, dtype, stream, true);
+}
+
+int gdn_short_conv_bwd_ws_bytes(int B, int T, int D, int W, size_t* bytes) {
+  g_err[0] = 0;
+  if (B < 0 || T < 0 || D <= 0 || W <= 0) return fail(GDN_ERR_ARG, "invalid sizes B=%d T=%d D=%d W=%d", B, T, D, W);
+  if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
+  *bytes = conv_ws_bytes(B, T, D, W);
+  return GDN_OK;
+}
+
+static int conv_check(int B, int T, int D, int W, int norm_group, int dtype) {
+  if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
+  if (B < 0 || T < 0 || D <= 0 || W <= 0 || norm_group < 0)
+    return fail(GDN_ERR_ARG, "invalid sizes B=%d T=%d D=%d W=%d norm_group=%d", B, T, D, W, norm_group);
+  if (!conv_shape_supported(D, W, norm_group))
+    return fail(GDN_ERR_SHAPE, "short conv not compiled for D=%d W=%d norm_group=%d (D %% 8 == 0, W = 4, "
+                "norm_group in {0, 64, 128, 256} dividing D)", D, W, norm_group);
+  return GDN_OK;
+}
+
+int gdn_short_conv_fwd(const void* x, const float* w, const float* bias, const void* state_in, void* y,
+                       void* state_out, int B, int T, int D, int W, int norm_group, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (int e = conv_check(B, T, D, W, norm_group, dtype)) return e;
+  if (B == 0) return GDN_OK;
+  if (T == 0) {
+    if (state_out && state_out != state_in) {
+      const size_t n = (size_t)B * D * (W - 1) * (dtype == DT_BF16 ? 2 : 4);
+      const hipError_t e = copy_or_zero_bytes(state_in, state_out, n, static_cast<hipStream_t>(stream));
+      if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "conv state copy: %s", hipGetErrorString(e));
+    }
+    return GDN_OK;
+  }
+  if (!x || !w || !y) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (state_out && state_out == state_in) return fail(GDN_ERR_ARG, "state_out must not alias state_in");
+  ConvArgs a{};
+  a.x = x; a.w = w; a.bias = bias; a.state_in = state_in; a.y = y; a.state_out = state_out;
+  a.B = B; a.T = T; a.D = D; a.norm_group = norm_group; a.dtype = dtype;
+  a.stream = static_cast<hipStream_t>(stream);
+  const hipError_t e = timed(ST_CONV_FWD, a.stream, [&] { return launch_conv(a, false); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "short conv forward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+int gdn_short_conv_bwd(const void* x, const float* w, const float* bias, const void* state_in, const void* dy,
+                       void* dx, float* dw, float* dbias, void* dstate_in, void* ws, size_t ws_bytes, int B, int T,
+                       int D, int W, int norm_group, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (int e = conv_check(B, T, D, W, norm_group, dtype)) return e;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (B == 0 || T == 0) {
+    hipError_t e = copy_or_zero_bytes(nullptr, dw, (size_t)D * W * 4, st);
+    if (e == hipSuccess) e = copy_or_zero_bytes(nullptr, dbias, (size_t)D * 4, st);
+    if (e == hipSuccess)
+      e = copy_or_zero_bytes(nullptr, dstate_in, (size_t)B * D * (W - 1) * (dtype == DT_BF16 ? 2 : 4), st);
+    if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "short conv zero-fill: %s", hipGetErrorString(e));
+    return GDN_OK;
+  }
+  if (!x || !w || !dy || !dx || !dw) return fail(GDN_ERR_ARG, "null input/output pointer");
+  const size_t need = conv_ws_bytes(B, T, D, W);
+  if (!ws || ws_bytes < need)
+    return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
+  ConvArgs a{};
+  a.x = x; a.w = w; a.bias = bias; a.state_in = state_in; a.dy = dy; a.dx = dx; a.dstate_in = dstate_in;
+  a.dw = dw; a.dbias = dbias; a.ws = ws;
+  a.B = B; a.T = T; a.D = D; a.norm_group = norm_group; a.dtype = dtype; a.stream = st;
+  const hipError_t e = timed(ST_CONV_BWD, st, [&] { return launch_conv(a, true); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "short conv backward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
 }
 
 int gdn_recurrent_step(const void* q, const void* k, const void* v, const float* g, const float* beta,

@@ -62,6 +62,26 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
 bool chunk_shape_supported(int K, int V, int dtype);
 bool step_shape_supported(int K, int V);
 
+// Short causal convolution + SiLU (+ per-group L2 normalisation), gdn_conv.hip.
+struct ConvArgs {
+  const void* x;          // [B, T, D]
+  const float* w;         // [D, W]
+  const float* bias;      // [D] or null
+  const void* state_in;   // [B, D, W-1] or null (zeros)
+  void* y;                // [B, T, D] (forward)
+  void* state_out;        // [B, D, W-1] or null (forward)
+  const void* dy;         // backward
+  void* dx;
+  void* dstate_in;        // or null
+  float *dw, *dbias;      // dbias may be null
+  void* ws;
+  int B, T, D, norm_group, dtype;
+  hipStream_t stream;
+};
+size_t conv_ws_bytes(int B, int T, int D, int W);
+bool conv_shape_supported(int D, int W, int norm_group);
+hipError_t launch_conv(const ConvArgs& a, bool backward);
+
 // Compute units of the current device (cached per device; 256 if the query fails).
 int device_cu_count();
 

@@ -24,24 +24,22 @@ from .. import ops
 
 
 class ShortConvolution(nn.Module):
-    """Depthwise causal conv1d (kernel ``size``) + SiLU over [B, T, D] (the ShortConv of nsgdn.py:457-470).
-    With ``state`` ([B, D, size-1], the previous inputs) it continues a sequence and returns the new state."""
+    """Depthwise causal conv1d (kernel ``size``) + SiLU over [B, T, D] (the ShortConv of nsgdn.py:457-470), on
+    the HIP kernel (``ops.short_conv``).  With ``state`` ([B, D, size-1], the previous inputs) it continues a
+    sequence; it always returns the new state.  ``norm_group`` > 0 L2-normalises each group of that many
+    channels after the SiLU (one head of q or k, nsgdn.py:527-528)."""
 
-    def __init__(self, dim: int, size: int = 4, bias: bool = False):
+    def __init__(self, dim: int, size: int = 4, bias: bool = False, norm_group: int = 0):
         super().__init__()
-        self.size = size
+        self.size, self.norm_group = size, norm_group
         self.weight = nn.Parameter(torch.empty(dim, 1, size).uniform_(-1 / math.sqrt(size), 1 / math.sqrt(size)))
         self.bias = nn.Parameter(torch.zeros(dim)) if bias else None
 
     def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
-        B, T, D = x.shape
-        xt = x.transpose(1, 2)
-        if state is None:
-            state = xt.new_zeros(B, D, self.size - 1)
-        full = torch.cat([state.to(xt.dtype), xt], dim=-1)
-        y = F.conv1d(full, self.weight.to(x.dtype), None if self.bias is None else self.bias.to(x.dtype),
-                     groups=D)
-        return F.silu(y.transpose(1, 2)), full[..., -(self.size - 1):]
+        # the weight is rounded to the activation dtype first, as the reference's conv runs it (nsgdn.py:464)
+        w = self.weight.squeeze(1).to(x.dtype).float()
+        b = None if self.bias is None else self.bias.to(x.dtype).float()
+        return ops.short_conv(x, w, b, state, self.norm_group)
 
 
 class GatedRMSNorm(nn.Module):
@@ -87,8 +85,9 @@ class GatedDeltaNet(nn.Module):
         self.dt_bias = nn.Parameter(dt + torch.log(-torch.expm1(-dt)))
         self.dt_bias._no_weight_decay = True
         if use_short_conv:
-            self.q_conv1d = ShortConvolution(self.key_dim, conv_size, conv_bias)
-            self.k_conv1d = ShortConvolution(self.key_dim, conv_size, conv_bias)
+            # q and k leave their convolution L2-normalised per head (the op's in-kernel normalisation then off)
+            self.q_conv1d = ShortConvolution(self.key_dim, conv_size, conv_bias, norm_group=head_dim)
+            self.k_conv1d = ShortConvolution(self.key_dim, conv_size, conv_bias, norm_group=head_dim)
             self.v_conv1d = ShortConvolution(self.value_dim, conv_size, conv_bias)
         if use_gate:
             self.g_proj = nn.Linear(hidden_size, self.value_dim, bias=False)
@@ -124,13 +123,14 @@ class GatedDeltaNet(nn.Module):
         state = entry["recurrent_state"] if entry is not None else None
         dt = hidden_states.dtype if hidden_states.dtype in (torch.bfloat16, torch.float32) else torch.bfloat16
         q, k, v = q.to(dt), k.to(dt), v.to(dt)
+        l2 = not self.use_short_conv  # the convolutions already normalised q and k
         if self.mode == "fused_recurrent" or (T == 1 and not torch.is_grad_enabled() and state is not None):
             o, new_state = ops.fused_recurrent_gated_delta_rule(q, k, v, g, beta, initial_state=state,
                                                                 output_final_state=use_cache,
-                                                                use_qk_l2norm_in_kernel=True)
+                                                                use_qk_l2norm_in_kernel=l2)
         else:
             o, new_state = ops.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=state,
-                                                      output_final_state=use_cache, use_qk_l2norm_in_kernel=True)
+                                                      output_final_state=use_cache, use_qk_l2norm_in_kernel=l2)
         if use_cache:
             if past_key_values is None:
                 past_key_values = {}

@@ -42,7 +42,7 @@ from torch import Tensor
 from . import _lib
 
 __all__ = ["chunk_gated_delta_rule", "fused_recurrent_gated_delta_rule", "recurrent_step", "chunk_fwd",
-           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed"]
+           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "short_conv"]
 
 
 def _require_gpu(*ts: Optional[Tensor]) -> None:
@@ -239,6 +239,111 @@ def _use_stash(*ts: Optional[Tensor]) -> bool:
     if os.environ.get("ARCHBENCH_AMD_GDN_STASH", "1") == "0" or not torch.is_grad_enabled():
         return False
     return any(t is not None and t.requires_grad for t in ts)
+
+
+# ------------------------------------------------------------------------------------ short causal conv + SiLU
+# The ShortConv in front of the op (archbench/layers/nsgdn.py:420-470: archbench::causal_conv_silu and its
+# backward as custom ops), with fla ShortConvolution's optional bias and decode state, and the per-head L2
+# normalisation of q and k (nsgdn.py:527-528) fused in when norm_group > 0.
+def _conv_shapes(x: Tensor, w: Tensor, bias: Optional[Tensor], state: Optional[Tensor]):
+    if x.dim() != 3:
+        raise ValueError(f"x must be [B, T, D], got {tuple(x.shape)}")
+    B, T, D = x.shape
+    if w.dim() != 2 or w.shape[0] != D:
+        raise ValueError(f"w must be [D, W] with D = {D}, got {tuple(w.shape)}")
+    W = w.shape[1]
+    if bias is not None and tuple(bias.shape) != (D,):
+        raise ValueError(f"bias must be [D] = [{D}], got {tuple(bias.shape)}")
+    if state is not None and tuple(state.shape) != (B, D, W - 1):
+        raise ValueError(f"conv state must be [B, D, W-1] = {(B, D, W - 1)}, got {tuple(state.shape)}")
+    return B, T, D, W
+
+
+@torch.library.custom_op("archbench_amd::short_conv", mutates_args=())
+def short_conv(x: Tensor, w: Tensor, bias: Optional[Tensor], state: Optional[Tensor],
+               norm_group: int) -> tuple[Tensor, Tensor]:
+    """(y [B,T,D], new_state [B,D,W-1]): y = silu(causal depthwise conv(x)) (+ L2 norm per norm_group channels)."""
+    _require_gpu(x, w, bias, state)
+    B, T, D, W = _conv_shapes(x, w, bias, state)
+    lib = _lib.load()
+    x = x.contiguous()
+    w = w.float().contiguous()
+    bias = None if bias is None else bias.float().contiguous()
+    state = None if state is None else state.to(x.dtype).contiguous()
+    y = torch.empty_like(x)
+    new_state = torch.empty(B, D, W - 1, dtype=x.dtype, device=x.device)
+    rc = lib.gdn_short_conv_fwd(_lib.ptr(x), _lib.ptr(w), _lib.ptr(bias), _lib.ptr(state), _lib.ptr(y),
+                                _lib.ptr(new_state), B, T, D, W, int(norm_group), _lib.dtype_code(x.dtype),
+                                _lib.stream_ptr(x.device))
+    _lib.check(rc, "gdn_short_conv_fwd")
+    return y, new_state
+
+
+@short_conv.register_fake
+def _(x, w, bias, state, norm_group):
+    B, T, D = x.shape
+    return torch.empty_like(x), x.new_empty(B, D, w.shape[1] - 1)
+
+
+@torch.library.custom_op("archbench_amd::short_conv_bwd", mutates_args=())
+def short_conv_bwd(x: Tensor, w: Tensor, bias: Optional[Tensor], state: Optional[Tensor], dy: Tensor,
+                   norm_group: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(dx, dw [D,W] fp32, dbias [D] fp32, dstate [B,D,W-1]); dbias / dstate are zeros-shaped if not needed."""
+    _require_gpu(x, w, bias, state, dy)
+    B, T, D, W = _conv_shapes(x, w, bias, state)
+    lib = _lib.load()
+    x, dy = x.contiguous(), dy.to(x.dtype).contiguous()
+    w = w.float().contiguous()
+    bias = None if bias is None else bias.float().contiguous()
+    state = None if state is None else state.to(x.dtype).contiguous()
+    dx = torch.empty_like(x)
+    dw = torch.empty(D, W, dtype=torch.float32, device=x.device)
+    db = torch.empty(D, dtype=torch.float32, device=x.device)
+    dstate = torch.empty(B, D, W - 1, dtype=x.dtype, device=x.device)
+    ws = torch.empty(_lib.conv_ws_bytes(B, T, D, W), dtype=torch.uint8, device=x.device)
+    rc = lib.gdn_short_conv_bwd(_lib.ptr(x), _lib.ptr(w), _lib.ptr(bias), _lib.ptr(state), _lib.ptr(dy),
+                                _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(dstate), _lib.ptr(ws), ws.numel(),
+                                B, T, D, W, int(norm_group), _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device))
+    _lib.check(rc, "gdn_short_conv_bwd")
+    return dx, dw, db, dstate
+
+
+@short_conv_bwd.register_fake
+def _(x, w, bias, state, dy, norm_group):
+    B, T, D = x.shape
+    W = w.shape[1]
+    f32 = dict(dtype=torch.float32)
+    return torch.empty_like(x), w.new_empty(D, W, **f32), w.new_empty(D, **f32), x.new_empty(B, D, W - 1)
+
+
+def _conv_setup(ctx, inputs, output):
+    x, w, bias, state, norm_group = inputs
+    ctx.save_for_backward(x, w, bias, state)
+    ctx.norm_group = norm_group
+    ctx.w_dtype = w.dtype
+    ctx.has_bias, ctx.has_state = bias is not None, state is not None
+    ctx.set_materialize_grads(False)
+
+
+def _conv_backward(ctx, dy, dstate_out):
+    x, w, bias, state = ctx.saved_tensors
+    if dy is None:
+        dy = torch.zeros_like(x)
+    dx, dw, db, dstate = short_conv_bwd(x, w, bias, state, dy.contiguous(), ctx.norm_group)
+    if dstate_out is not None:
+        # new_state is the last W-1 entries of [state | x^T]: the tail of x, reaching into the old state when
+        # T < W-1
+        W1, T = dstate_out.shape[-1], x.shape[1]
+        if T >= W1:
+            dx[:, T - W1:, :] += dstate_out.transpose(1, 2).to(dx.dtype)
+        else:
+            full = torch.cat([dstate.float(), dx.float().transpose(1, 2)], dim=-1)
+            full[..., -W1:] += dstate_out.float()
+            dstate, dx = full[..., :W1].to(dstate.dtype), full[..., W1:].transpose(1, 2).to(dx.dtype).contiguous()
+    return (dx, dw.to(ctx.w_dtype), (db if ctx.has_bias else None), (dstate if ctx.has_state else None), None)
+
+
+short_conv.register_autograd(_conv_backward, setup_context=_conv_setup)
 
 
 # ------------------------------------------------------------------------------------------------- decode step

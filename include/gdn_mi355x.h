@@ -92,12 +92,29 @@ int gdn_chunk_bwd_stashed(const void* q, const void* k, const void* v, const flo
 int gdn_recurrent_step(const void* q, const void* k, const void* v, const float* g, const float* beta,
                        float* state, void* o, int B, int H, int K, int V, float scale, int dtype, void* stream);
 
+/* Short causal depthwise convolution + SiLU in front of the op, optionally followed by an L2 normalisation over
+ * each group of norm_group channels (one head of q or k):
+ *   z[t,c] = bias[c] + sum_i w[c,i] x[t-(W-1)+i, c],   y = silu(z),   y <- y / max(||y||_group, 1e-12).
+ * Replaces the ShortConv + causal_conv1d custom ops archbench::causal_conv_silu / _bwd
+ * (archbench/layers/nsgdn.py:420-470; fla's ShortConvolution in GatedDeltaNet) and the per-head normalisation
+ * of q and k (nsgdn.py:527-528).  x, y, dy, dx [B, T, D] token-major in dtype; w [D, W] and bias [D] fp32 (bias
+ * may be NULL); conv states [B, D, W-1] in dtype, the previous W-1 inputs oldest first (state_in NULL = zeros;
+ * state_out NULL = not returned; it must not alias state_in).  Compiled for W = 4, D % 8 == 0, norm_group in {0 (none), 64, 128, 256}.
+ * The backward writes dx, dw [D, W] fp32, dbias [D] fp32 (if non-NULL) and dstate_in (if non-NULL); its
+ * workspace holds per-chunk partial sums of dw, reduced in a fixed order (deterministic). */
+int gdn_short_conv_fwd(const void* x, const float* w, const float* bias, const void* state_in, void* y,
+                       void* state_out, int B, int T, int D, int W, int norm_group, int dtype, void* stream);
+int gdn_short_conv_bwd_ws_bytes(int B, int T, int D, int W, size_t* bytes);
+int gdn_short_conv_bwd(const void* x, const float* w, const float* bias, const void* state_in, const void* dy,
+                       void* dx, float* dw, float* dbias, void* dstate_in, void* ws, size_t ws_bytes, int B, int T,
+                       int D, int W, int norm_group, int dtype, void* stream);
+
 /* Per-stage kernel timing (diagnostic; no counterpart in the reference, which times whole phases with CUDA
  * events in archbench/logger.py:57-81).  While enabled on the calling thread, every kernel the calls above
  * enqueue is bracketed by hipEvents on the same stream.  gdn_profile_read synchronises on those events and
  * returns, per stage, the summed milliseconds and the number of launches (arrays of at least
  * GDN_PROFILE_STAGES entries), then clears the record.  Stage names: gdn_profile_stage_name. */
-#define GDN_PROFILE_STAGES 7
+#define GDN_PROFILE_STAGES 9
 int gdn_profile_enable(int on);
 int gdn_profile_read(double* ms_sum, int* launches, int n_stages);
 const char* gdn_profile_stage_name(int stage);

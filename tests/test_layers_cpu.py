@@ -64,3 +64,25 @@ def test_shape_errors_are_value_errors():
     q = torch.empty(1, 4, 2, 64, device="meta")
     with pytest.raises((ValueError, RuntimeError)):
         ops._shapes(q, q[..., :32], q, q[..., 0], q[..., 0], None)
+
+
+def test_short_conv_fake_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from archbench_amd import ops
+
+    with FakeTensorMode():
+        x = torch.empty(2, 70, 512, dtype=torch.bfloat16)
+        w = torch.empty(512, 4)
+        y, st = ops.short_conv(x, w, None, None, 128)
+        assert y.shape == x.shape and y.dtype == torch.bfloat16 and st.shape == (2, 512, 3)
+        dx, dw, db, dst = ops.short_conv_bwd(x, w, None, None, x, 128)
+        assert dx.shape == x.shape and dw.shape == (512, 4) and dw.dtype == torch.float32
+        assert db.shape == (512,) and dst.shape == (2, 512, 3) and dst.dtype == torch.bfloat16
+
+
+def test_short_conv_cpu_raises():
+    from archbench_amd import ops
+
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.short_conv(torch.randn(1, 4, 512), torch.randn(512, 4), None, None, 0)
