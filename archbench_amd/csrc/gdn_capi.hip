@@ -21,6 +21,13 @@ static int fail(int code, const char* fmt, ...) {
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// The kernels move rows with 16-byte vector accesses: every array argument must be 16-byte aligned (any hipMalloc
+// or torch allocation is; an offset view may not be).
+template <typename... P>
+static bool misaligned(const P*... p) {
+  return ((reinterpret_cast<uintptr_t>(p) & 15) | ...) != 0;
+}
+
 size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, ChunkWs* carve, void* base) {
   const size_t es = dtype == DT_BF16 ? 2 : 4;
   const size_t NT = (size_t)(T + CH_TOKENS - 1) / CH_TOKENS;
@@ -247,6 +254,7 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* v, const flo
     return GDN_OK;
   }
   if (!q || !k || !v || !g || !beta || !o) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(q, k, v, g, beta, h0, o, hT, ws)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   ChunkArgs a{};
   const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, stash ? WS_STASH : WS_FACT, &a.ws, ws);
   if (!ws || ws_bytes < need)
@@ -282,6 +290,8 @@ static int chunk_bwd_impl(const void* q, const void* k, const void* v, const flo
   }
   if (!q || !k || !v || !g || !beta || !dout || !dq || !dk || !dv || !dg || !dbeta)
     return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(q, k, v, g, beta, h0, dout, dhT, dq, dk, dv, dg, dbeta, dh0, stash, ws))
+    return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   ChunkArgs a{};
   if (stashed) {
     // the stash is only read (the kernels take it through the same carve-up as the recompute path's workspace)
@@ -356,7 +366,7 @@ static int conv_check(int B, int T, int D, int W, int norm_group, int dtype) {
   if (B < 0 || T < 0 || D <= 0 || W <= 0 || norm_group < 0)
     return fail(GDN_ERR_ARG, "invalid sizes B=%d T=%d D=%d W=%d norm_group=%d", B, T, D, W, norm_group);
   if (!conv_shape_supported(D, W, norm_group))
-    return fail(GDN_ERR_SHAPE, "short conv not compiled for D=%d W=%d norm_group=%d (D %% 8 == 0, W = 4, "
+    return fail(GDN_ERR_SHAPE, "short conv not compiled for D=%d W=%d norm_group=%d (D %% 4 == 0, W = 4, "
                 "norm_group in {0, 64, 128, 256} dividing D)", D, W, norm_group);
   return GDN_OK;
 }
@@ -376,6 +386,7 @@ int gdn_short_conv_fwd(const void* x, const float* w, const float* bias, const v
   }
   if (!x || !w || !y) return fail(GDN_ERR_ARG, "null input/output pointer");
   if (state_out && state_out == state_in) return fail(GDN_ERR_ARG, "state_out must not alias state_in");
+  if (misaligned(x, w, bias, state_in, y, state_out)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   ConvArgs a{};
   a.x = x; a.w = w; a.bias = bias; a.state_in = state_in; a.y = y; a.state_out = state_out;
   a.B = B; a.T = T; a.D = D; a.norm_group = norm_group; a.dtype = dtype;
@@ -400,6 +411,8 @@ int gdn_short_conv_bwd(const void* x, const float* w, const float* bias, const v
     return GDN_OK;
   }
   if (!x || !w || !dy || !dx || !dw) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(x, w, bias, state_in, dy, dx, dw, dbias, dstate_in, ws))
+    return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   const size_t need = conv_ws_bytes(B, T, D, W);
   if (!ws || ws_bytes < need)
     return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
@@ -419,6 +432,7 @@ int gdn_recurrent_step(const void* q, const void* k, const void* v, const float*
   if (!step_shape_supported(K, V)) return fail(GDN_ERR_SHAPE, "decode step not compiled for K=%d V=%d", K, V);
   if (B == 0 || H == 0) return GDN_OK;
   if (!q || !k || !v || !g || !beta || !state || !o) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(q, k, v, g, beta, state, o)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   StepArgs a{q, k, v, g, beta, state, o, B, H, K, V, scale, dtype, static_cast<hipStream_t>(stream)};
   const hipError_t e = timed(ST_STEP, a.stream, [&] { return launch_step(a); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "decode step launch: %s", hipGetErrorString(e));

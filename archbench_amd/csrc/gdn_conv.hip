@@ -7,131 +7,137 @@
 //
 // Layout: x, y, dy, dx [B, T, D] token-major (channel-last), w [D, W] fp32, bias [D] fp32, conv states
 // [B, D, W-1] in the activation dtype (the previous W-1 inputs, oldest first).
-// Mapping: one wave per (512 channels, 64-token chunk, b); each lane holds 8 consecutive channels, so every token
-// row is one 16-byte access per lane and a wave covers 1 KB contiguous.  The W-1 inputs before a chunk are
-// re-read (a (W-1)/64 halo).  A normalisation group of NG channels spans NG/8 lanes and is reduced with lane
-// shuffles.  HBM-bound: x read once, y written once.
+// Mapping: one wave per (256 channels, 64-token chunk, b); each lane holds 4 consecutive channels, so every token
+// row is one 8-byte (bf16) or 16-byte (fp32) access per lane and a wave covers 512 B / 1 KB contiguous.  The W-1
+// inputs before a chunk are re-read (a (W-1)/64 halo).  A normalisation group of NG channels spans NG/4 lanes and
+// is reduced with lane shuffles.  HBM-bound: x read once, y written once.
 // Backward: each wave recomputes z for its chunk plus W-1 tokens of look-ahead, forms dz and emits dx with a
 // W-token delay; dw and dbias are summed per wave into a per-chunk partial and reduced over chunks in a fixed
 // order by a second kernel (deterministic, no atomics).
+#include <type_traits>
+
 #include "gdn_common.h"
 #include "gdn_launch.h"
 
 namespace gdn {
 
-constexpr int CONV_L = 64;    // tokens per wave
-constexpr int CONV_CW = 512;  // channels per wave
-constexpr int CONV_UF = 8;    // token rows loaded per batch, forward
-constexpr int CONV_UB = 4;    // token rows of x and of dy loaded per batch, backward
+constexpr int CONV_L = 64;  // tokens per wave
+constexpr int CONV_CPL = 4;  // consecutive channels per lane
+constexpr int CONV_CW = 64 * CONV_CPL;  // channels per wave
+constexpr int CONV_WAVES = 4;  // waves per workgroup, on adjacent channel blocks of the same chunk
+constexpr int CONV_UF = 8;  // token rows per load batch, forward
+constexpr int CONV_UB = 8;  // token rows of x and of dy per load batch, backward
 
-// 8 consecutive channels of one token row as loaded (16 B in bf16, 32 B in fp32), converted at use so a batch
-// of loads is in flight at once
+// CONV_CPL = 4 consecutive channels of one token row as loaded (8 B in bf16, 16 B in fp32), converted at use so
+// that a whole batch of loads is in flight at once
 template <typename T>
-struct Row8;
+struct Row4;
 template <>
-struct Row8<bf16> {
-  bf16x8 r;
-  __device__ __forceinline__ void load(const bf16* p) { r = *reinterpret_cast<const bf16x8*>(p); }
-  __device__ __forceinline__ void get(float (&v)[8]) const {
+struct Row4<bf16> {
+  bf16x4 r;
+  __device__ __forceinline__ void load(const bf16* p) { r = *reinterpret_cast<const bf16x4*>(p); }
+  __device__ __forceinline__ void get(float (&v)[4]) const {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(r[j]);
+    for (int j = 0; j < 4; ++j) v[j] = static_cast<float>(r[j]);
   }
 };
 template <>
-struct Row8<float> {
-  f32x4 a, b;
-  __device__ __forceinline__ void load(const float* p) {
-    a = *reinterpret_cast<const f32x4*>(p);
-    b = *reinterpret_cast<const f32x4*>(p + 4);
-  }
-  __device__ __forceinline__ void get(float (&v)[8]) const {
+struct Row4<float> {
+  f32x4 r;
+  __device__ __forceinline__ void load(const float* p) { r = *reinterpret_cast<const f32x4*>(p); }
+  __device__ __forceinline__ void get(float (&v)[4]) const {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v[j] = a[j];
-      v[4 + j] = b[j];
-    }
+    for (int j = 0; j < 4; ++j) v[j] = r[j];
   }
 };
 
 template <typename T>
-__device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
-  Row8<T> r;
-  r.load(p);
-  r.get(v);
-}
-template <typename T>
-__device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
+__device__ __forceinline__ void store4(T* p, const float (&v)[4]) {
   if constexpr (sizeof(T) == 2) {
-    bf16x8 r;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = static_cast<bf16>(v[j]);
-    *reinterpret_cast<bf16x8*>(p) = r;
+    *reinterpret_cast<bf16x4*>(p) = bf16x4{static_cast<bf16>(v[0]), static_cast<bf16>(v[1]),
+                                           static_cast<bf16>(v[2]), static_cast<bf16>(v[3])};
   } else {
     *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
   }
 }
-// sum over the NG/8 lanes of a normalisation group (aligned groups of 1, 2, 4, 8, 16 or 32 lanes)
+// sum over the NG / CONV_CPL lanes of a normalisation group (aligned runs of lanes), the same value in every lane:
+// within 16 lanes by DPP butterflies on the VALU (xor 1, xor 2, then half-row and row mirrors), across rows by
+// lane shuffles
 template <int NG>
 __device__ __forceinline__ float group_sum(float s) {
-  if constexpr (NG >= 16) s += __shfl_xor(s, 1);
-  if constexpr (NG >= 32) s += __shfl_xor(s, 2);
-  if constexpr (NG >= 64) s += __shfl_xor(s, 4);
-  if constexpr (NG >= 128) s += __shfl_xor(s, 8);
-  if constexpr (NG >= 256) s += __shfl_xor(s, 16);
+  constexpr int LANES = NG / CONV_CPL;
+  if constexpr (LANES >= 2) s = dpp_sum_step<0xb1>(s);
+  if constexpr (LANES >= 4) s = dpp_sum_step<0x4e>(s);
+  if constexpr (LANES >= 8) s = dpp_sum_step<0x141>(s);
+  if constexpr (LANES >= 16) s = dpp_sum_step<0x140>(s);
+  if constexpr (LANES >= 32) s += __shfl_xor(s, 16);
+  if constexpr (LANES >= 64) s += __shfl_xor(s, 32);
   return s;
 }
-__device__ __forceinline__ float sigmoidf(float z) { return 1.f / (1.f + __expf(-z)); }
+// hardware reciprocal (1 ulp) in place of an IEEE division
+__device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float sigmoidf(float z) { return rcp(1.f + __expf(-z)); }
 constexpr float NORM_EPS = 1e-12f;  // F.normalize's eps
 
 template <typename T, int W>
-__device__ __forceinline__ void load_window(const T* x, const T* state_in, int64_t xrow0, int64_t srow, int D,
-                                            int t0, float (&win)[W - 1][8]) {
+__device__ __forceinline__ void load_window(const T* xl, const T* state_in, int64_t srow, int D, int t0,
+                                            float (&win)[W - 1][CONV_CPL]) {
   // inputs at t0 - (W-1) .. t0 - 1; negative positions from the conv state (zero if none)
 #pragma unroll
   for (int i = 0; i < W - 1; ++i) {
     const int t = t0 - (W - 1) + i;
     if (t >= 0) {
-      load8(x + xrow0 + (int64_t)t * D, win[i]);
+      Row4<T> r;
+      r.load(xl + (int64_t)t * D);
+      r.get(win[i]);
     } else if (state_in) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) win[i][j] = to_f(state_in[srow + (int64_t)j * (W - 1) + (W - 1) + t]);
+      for (int j = 0; j < CONV_CPL; ++j) win[i][j] = to_f(state_in[srow + (int64_t)j * (W - 1) + (W - 1) + t]);
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) win[i][j] = 0.f;
+      for (int j = 0; j < CONV_CPL; ++j) win[i][j] = 0.f;
     }
   }
 }
 
-// grid (B * nchunk, ceil(D / CONV_CW)), 64 threads
+// grid B * nchunk * ceil(D / (CONV_WAVES * CONV_CW)) (channel groups fastest), CONV_WAVES waves, each
+// independent: consecutive workgroups cover adjacent channels of the same token rows.  Rows are loaded in batches of CONV_UF with the next batch in
+// flight while the current one is computed; the prefetch of the last batch re-reads it (start clamped to
+// t1 - CONV_UF) so every load stays inside the chunk.
 template <typename T, int W, int NG>
-__global__ __launch_bounds__(64) void conv_silu_fwd_kernel(const T* __restrict__ x, const float* __restrict__ w,
+__global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_fwd_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                            const float* __restrict__ bias,
                                                            const T* __restrict__ state_in, T* __restrict__ y,
                                                            T* __restrict__ state_out, int Tn, int D, int nchunk) {
+  constexpr int CPL = CONV_CPL, U = CONV_UF;
   const int l = lane_id();
-  const int c = blockIdx.y * CONV_CW + 8 * l;
-  const int b = blockIdx.x / nchunk, ch = blockIdx.x - b * nchunk;
+  const int ncg = (D + CONV_WAVES * CONV_CW - 1) / (CONV_WAVES * CONV_CW);
+  const int part = blockIdx.x / ncg, cg = blockIdx.x - part * ncg;  // part = b * nchunk + chunk
+  const int cw0 = (cg * CONV_WAVES + wave_id()) * CONV_CW;
+  if (cw0 >= D) return;  // a wave wholly past the channels (waves never synchronise)
+  const int c = cw0 + CPL * l;
+  const int b = part / nchunk, ch = part - b * nchunk;
   const int t0 = ch * CONV_L, t1 = min(Tn, t0 + CONV_L);
   const bool on = c < D;
   const int cc = on ? c : 0;  // clamped: lanes past D compute on channel 0 and store nothing
-  const int64_t xrow0 = (int64_t)b * Tn * D + cc;
+  const T* xl = x + (int64_t)b * Tn * D + cc;
+  T* yl = y + (int64_t)b * Tn * D + cc;
   const int64_t srow = ((int64_t)b * D + cc) * (W - 1);
-  float wk[8][W], bk[8];
+  float wk[CPL][W], bk[CPL];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < CPL; ++j) {
 #pragma unroll
     for (int i = 0; i < W; ++i) wk[j][i] = w[(cc + j) * W + i];
     bk[j] = bias ? bias[cc + j] : 0.f;
   }
-  float win[W - 1][8];
-  load_window<T, W>(x, state_in, xrow0, srow, D, t0, win);
-  auto step = [&](int t, const Row8<T>& row) {
-    float xt[8], yt[8];
+  float win[W - 1][CPL];
+  load_window<T, W>(xl, state_in, srow, D, t0, win);
+  auto step = [&](int t, const Row4<T>& row) {
+    float xt[CPL], yt[CPL];
     row.get(xt);
     float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < CPL; ++j) {
       float z = bk[j] + wk[j][W - 1] * xt[j];
 #pragma unroll
       for (int i = 0; i < W - 1; ++i) z += wk[j][i] * win[i][j];
@@ -139,70 +145,89 @@ __global__ __launch_bounds__(64) void conv_silu_fwd_kernel(const T* __restrict__
       ss += yt[j] * yt[j];
     }
     if constexpr (NG > 0) {
-      const float inv = 1.f / fmaxf(sqrtf(group_sum<NG>(ss)), NORM_EPS);
+      const float inv = rcp(fmaxf(sqrtf(group_sum<NG>(ss)), NORM_EPS));
 #pragma unroll
-      for (int j = 0; j < 8; ++j) yt[j] *= inv;
+      for (int j = 0; j < CPL; ++j) yt[j] *= inv;
     }
-    if (on) store8(y + xrow0 + (int64_t)t * D, yt);
+    if (on) store4(yl + (int64_t)t * D, yt);
 #pragma unroll
     for (int i = 0; i + 1 < W - 1; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) win[i][j] = win[i + 1][j];
+      for (int j = 0; j < CPL; ++j) win[i][j] = win[i + 1][j];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) win[W - 2][j] = xt[j];
+    for (int j = 0; j < CPL; ++j) win[W - 2][j] = xt[j];
   };
+  const int nfull = (t1 - t0) / U;
   int t = t0;
-  for (; t + CONV_UF <= t1; t += CONV_UF) {
-    Row8<T> rows[CONV_UF];
+  if (nfull > 0) {
+    Row4<T> buf[U];
 #pragma unroll
-    for (int u = 0; u < CONV_UF; ++u) rows[u].load(x + xrow0 + (int64_t)(t + u) * D);
+    for (int u = 0; u < U; ++u) buf[u].load(xl + (int64_t)(t0 + u) * D);
+    for (int n = 0; n < nfull; ++n, t += U) {
+      Row4<T> cur[U];
 #pragma unroll
-    for (int u = 0; u < CONV_UF; ++u) step(t + u, rows[u]);
+      for (int u = 0; u < U; ++u) cur[u] = buf[u];
+      const int tn = min(t + U, t1 - U);
+#pragma unroll
+      for (int u = 0; u < U; ++u) buf[u].load(xl + (int64_t)(tn + u) * D);
+#pragma unroll
+      for (int u = 0; u < U; ++u) step(t + u, cur[u]);
+    }
   }
   for (; t < t1; ++t) {
-    Row8<T> row;
-    row.load(x + xrow0 + (int64_t)t * D);
+    Row4<T> row;
+    row.load(xl + (int64_t)t * D);
     step(t, row);
   }
   // the last W-1 inputs become the new conv state (written by the chunk that holds the sequence end; for
   // Tn < W-1 part of it still comes from the old state, which must not be the same buffer)
   if (state_out && on && t1 == Tn) {
-    float last[W - 1][8];
-    load_window<T, W>(x, state_in, xrow0, srow, D, Tn, last);
+    float last[W - 1][CPL];
+    load_window<T, W>(xl, state_in, srow, D, Tn, last);
 #pragma unroll
     for (int i = 0; i < W - 1; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) state_out[srow + (int64_t)j * (W - 1) + i] = from_f<T>(last[i][j]);
+      for (int j = 0; j < CPL; ++j) state_out[srow + (int64_t)j * (W - 1) + i] = from_f<T>(last[i][j]);
   }
 }
 
-// grid (B * nchunk, ceil(D / CONV_CW)), 64 threads; partial sums of dw and dbias per (b, chunk) = blockIdx.x
+// grid and waves as in the forward; partial sums of dw and dbias per (b, chunk) = part.
+// Each wave recomputes z over its chunk plus W-1 tokens of look-ahead, forms dz, and emits dx with a W-1 token
+// delay; rows of x and dy are loaded in double-buffered batches of CONV_UB as in the forward.
 template <typename T, int W, int NG>
-__global__ __launch_bounds__(64) void conv_silu_bwd_kernel(const T* __restrict__ x, const float* __restrict__ w,
+__global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                            const float* __restrict__ bias,
                                                            const T* __restrict__ state_in,
                                                            const T* __restrict__ dy, T* __restrict__ dx,
                                                            T* __restrict__ dstate_in, float* __restrict__ dw_part,
                                                            float* __restrict__ db_part, int Tn, int D, int nchunk) {
+  constexpr int CPL = CONV_CPL, U = CONV_UB;
   const int l = lane_id();
-  const int c = blockIdx.y * CONV_CW + 8 * l;
-  const int b = blockIdx.x / nchunk, ch = blockIdx.x - b * nchunk;
+  const int ncg = (D + CONV_WAVES * CONV_CW - 1) / (CONV_WAVES * CONV_CW);
+  const int part = blockIdx.x / ncg, cg = blockIdx.x - part * ncg;  // part = b * nchunk + chunk
+  const int cw0 = (cg * CONV_WAVES + wave_id()) * CONV_CW;
+  if (cw0 >= D) return;  // a wave wholly past the channels (waves never synchronise)
+  const int c = cw0 + CPL * l;
+  const int b = part / nchunk, ch = part - b * nchunk;
   const int t0 = ch * CONV_L, t1 = min(Tn, t0 + CONV_L);
   const bool on = c < D;
   const int cc = on ? c : 0;
-  const int64_t xrow0 = (int64_t)b * Tn * D + cc;
+  const int64_t off = (int64_t)b * Tn * D + cc;
+  const T* xl = x + off;
+  const T* dyl = dy + off;
+  T* dxl = dx + off;
   const int64_t srow = ((int64_t)b * D + cc) * (W - 1);
-  float wk[8][W], bk[8];
+  float wk[CPL][W], bk[CPL];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < CPL; ++j) {
 #pragma unroll
     for (int i = 0; i < W; ++i) wk[j][i] = w[(cc + j) * W + i];
     bk[j] = bias ? bias[cc + j] : 0.f;
   }
-  float win[W - 1][8], dzw[W - 1][8], dwa[8][W], dba[8];
-  load_window<T, W>(x, state_in, xrow0, srow, D, t0, win);
+  float win[W - 1][CPL], dzw[W - 1][CPL], dwa[CPL][W], dba[CPL];
+  load_window<T, W>(xl, state_in, srow, D, t0, win);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < CPL; ++j) {
     dba[j] = 0.f;
 #pragma unroll
     for (int i = 0; i < W; ++i) dwa[j][i] = 0.f;
@@ -211,34 +236,34 @@ __global__ __launch_bounds__(64) void conv_silu_bwd_kernel(const T* __restrict__
   }
   // dx[p] = sum_i w[i] dz[p + W-1 - i]: emitted at s = p + W-1 from dz[s] and the W-1 dz before it (dzw).  This
   // wave emits dx for its own tokens, and for chunk 0 also the state gradient (p = -(W-1) .. -1).
-  auto emit = [&](int s, const float (&dz)[8], bool have_dz) {
+  auto emit = [&](int s, const float (&dz)[CPL], bool have_dz) {
     const int p = s - (W - 1);
     if (p >= t0 || (t0 == 0 && p >= -(W - 1))) {
-      float o[8];
+      float o[CPL];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < CPL; ++j) {
         o[j] = have_dz ? wk[j][0] * dz[j] : 0.f;
 #pragma unroll
         for (int i = 1; i < W; ++i) o[j] += wk[j][i] * dzw[W - 1 - i][j];
       }
       if (on) {
         if (p >= 0) {
-          store8(dx + xrow0 + (int64_t)p * D, o);
+          store4(dxl + (int64_t)p * D, o);
         } else if (dstate_in) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) dstate_in[srow + (int64_t)j * (W - 1) + (W - 1) + p] = from_f<T>(o[j]);
+          for (int j = 0; j < CPL; ++j) dstate_in[srow + (int64_t)j * (W - 1) + (W - 1) + p] = from_f<T>(o[j]);
         }
       }
     }
   };
-  // s runs over the chunk and W-1 tokens of look-ahead
-  auto step = [&](int s, const Row8<T>& xrow, const Row8<T>& dyrow) {
-    float xs[8], ds[8], dz[8];
+  // own = the chunk's own tokens, which carry dw and dbias (the W-1 look-ahead tokens only feed dx)
+  auto step = [&](int s, const Row4<T>& xrow, const Row4<T>& dyrow, auto own) {
+    float xs[CPL], ds[CPL], dz[CPL];
     xrow.get(xs);
     dyrow.get(ds);
-    float z[8], sg[8], ysl[8], ss = 0.f;
+    float z[CPL], sg[CPL], ysl[CPL], ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < CPL; ++j) {
       z[j] = bk[j] + wk[j][W - 1] * xs[j];
 #pragma unroll
       for (int i = 0; i < W - 1; ++i) z[j] += wk[j][i] * win[i][j];
@@ -248,20 +273,20 @@ __global__ __launch_bounds__(64) void conv_silu_bwd_kernel(const T* __restrict__
     }
     if constexpr (NG > 0) {
       const float nrm = sqrtf(group_sum<NG>(ss));
-      const float inv = 1.f / fmaxf(nrm, NORM_EPS);
+      const float inv = rcp(fmaxf(nrm, NORM_EPS));
       float dot = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) dot += ysl[j] * inv * ds[j];
+      for (int j = 0; j < CPL; ++j) dot += ysl[j] * inv * ds[j];
       dot = group_sum<NG>(dot);
       const bool big = nrm > NORM_EPS;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ds[j] = big ? (ds[j] - ysl[j] * inv * dot) * inv : ds[j] * inv;
+      for (int j = 0; j < CPL; ++j) ds[j] = big ? (ds[j] - ysl[j] * inv * dot) * inv : ds[j] * inv;
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) dz[j] = ds[j] * sg[j] * (1.f + z[j] * (1.f - sg[j]));
-    if (s < t1) {  // this chunk's own tokens carry dw and dbias
+    for (int j = 0; j < CPL; ++j) dz[j] = ds[j] * sg[j] * (1.f + z[j] * (1.f - sg[j]));
+    if constexpr (decltype(own)::value) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < CPL; ++j) {
         dba[j] += dz[j];
         dwa[j][W - 1] += dz[j] * xs[j];
 #pragma unroll
@@ -272,71 +297,114 @@ __global__ __launch_bounds__(64) void conv_silu_bwd_kernel(const T* __restrict__
 #pragma unroll
     for (int i = 0; i + 1 < W - 1; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < CPL; ++j) {
         win[i][j] = win[i + 1][j];
         dzw[i][j] = dzw[i + 1][j];
       }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < CPL; ++j) {
       win[W - 2][j] = xs[j];
       dzw[W - 2][j] = dz[j];
     }
   };
-  const int send = min(Tn, t1 + W - 1);
+  using Own = std::true_type;
+  using LookAhead = std::false_type;
+  const int nfull = (t1 - t0) / U;
   int s = t0;
-  for (; s + CONV_UB <= send; s += CONV_UB) {
-    Row8<T> xr[CONV_UB], dr[CONV_UB];
+  if (nfull > 0) {
+    Row4<T> bx[U], bd[U];
 #pragma unroll
-    for (int u = 0; u < CONV_UB; ++u) {
-      xr[u].load(x + xrow0 + (int64_t)(s + u) * D);
-      dr[u].load(dy + xrow0 + (int64_t)(s + u) * D);
+    for (int u = 0; u < U; ++u) {
+      bx[u].load(xl + (int64_t)(t0 + u) * D);
+      bd[u].load(dyl + (int64_t)(t0 + u) * D);
     }
+    for (int n = 0; n < nfull; ++n, s += U) {
+      Row4<T> cx[U], cd[U];
 #pragma unroll
-    for (int u = 0; u < CONV_UB; ++u) step(s + u, xr[u], dr[u]);
+      for (int u = 0; u < U; ++u) {
+        cx[u] = bx[u];
+        cd[u] = bd[u];
+      }
+      const int sn = min(s + U, t1 - U);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        bx[u].load(xl + (int64_t)(sn + u) * D);
+        bd[u].load(dyl + (int64_t)(sn + u) * D);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) step(s + u, cx[u], cd[u], Own{});
+    }
   }
+  for (; s < t1; ++s) {
+    Row4<T> xr, dr;
+    xr.load(xl + (int64_t)s * D);
+    dr.load(dyl + (int64_t)s * D);
+    step(s, xr, dr, Own{});
+  }
+  const int send = min(Tn, t1 + W - 1);
   for (; s < send; ++s) {
-    Row8<T> xr, dr;
-    xr.load(x + xrow0 + (int64_t)s * D);
-    dr.load(dy + xrow0 + (int64_t)s * D);
-    step(s, xr, dr);
+    Row4<T> xr, dr;
+    xr.load(xl + (int64_t)s * D);
+    dr.load(dyl + (int64_t)s * D);
+    step(s, xr, dr, LookAhead{});
   }
   // past the sequence end dz = 0: flush the remaining dx of the chunk's tail (and of the state when Tn is short)
   for (; s < t1 + W - 1; ++s) {
-    const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const float zero[CPL] = {};
     emit(s, zero, false);
 #pragma unroll
     for (int i = 0; i + 1 < W - 1; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) dzw[i][j] = dzw[i + 1][j];
+      for (int j = 0; j < CPL; ++j) dzw[i][j] = dzw[i + 1][j];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) dzw[W - 2][j] = 0.f;
+    for (int j = 0; j < CPL; ++j) dzw[W - 2][j] = 0.f;
   }
   if (on) {
-    const int64_t part = (int64_t)blockIdx.x * D + cc;
+    const int64_t row = (int64_t)part * D + cc;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < CPL; ++j) {
 #pragma unroll
-      for (int i = 0; i < W; ++i) dw_part[(part + j) * W + i] = dwa[j][i];
-      db_part[part + j] = dba[j];
+      for (int i = 0; i < W; ++i) dw_part[(row + j) * W + i] = dwa[j][i];
+      db_part[row + j] = dba[j];
     }
   }
 }
 
-// dw[c, i] = sum over the B * nchunk partials in order; dbias likewise.
+// dw[c, i] and dbias[c]: the B * nchunk partials summed in a fixed order.  One workgroup per 64 consecutive
+// outputs of the concatenation [dw (D * W) | dbias (D)]; wave v sums partials v, v + 4, ... (coalesced 256-byte
+// rows), then lane sums of the four waves are added in wave order.
+constexpr int RED_COLS = 64;
 __global__ __launch_bounds__(256) void conv_param_reduce_kernel(const float* __restrict__ dw_part,
                                                                 const float* __restrict__ db_part,
                                                                 float* __restrict__ dw, float* __restrict__ db,
                                                                 int nparts, int D, int W) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < D * W) {
-    float s = 0.f;
-    for (int p = 0; p < nparts; ++p) s += dw_part[(int64_t)p * D * W + i];
-    dw[i] = s;
-  } else if (i < D * W + D && db) {
-    const int c = i - D * W;
-    float s = 0.f;
-    for (int p = 0; p < nparts; ++p) s += db_part[(int64_t)p * D + c];
-    db[c] = s;
+  __shared__ float red[4][RED_COLS];
+  const int v = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int i = blockIdx.x * RED_COLS + l;  // index into [dw | dbias]
+  const int ndw = D * W;
+  const bool is_dw = i < ndw, valid = i < ndw + D;
+  const float* src = is_dw ? dw_part + i : db_part + (i - ndw);
+  const int64_t stride = is_dw ? ndw : D;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;  // four chains in flight, combined in a fixed order
+  if (valid) {
+    int p = v;
+    for (; p + 12 < nparts; p += 16) {
+      a0 += src[(int64_t)p * stride];
+      a1 += src[(int64_t)(p + 4) * stride];
+      a2 += src[(int64_t)(p + 8) * stride];
+      a3 += src[(int64_t)(p + 12) * stride];
+    }
+    for (; p < nparts; p += 4) a0 += src[(int64_t)p * stride];
+  }
+  red[v][l] = (a0 + a1) + (a2 + a3);
+  __syncthreads();
+  if (v == 0 && valid) {
+    const float r = ((red[0][l] + red[1][l]) + red[2][l]) + red[3][l];
+    if (is_dw) {
+      dw[i] = r;
+    } else if (db) {
+      db[i - ndw] = r;
+    }
   }
 }
 
@@ -347,15 +415,17 @@ size_t conv_ws_bytes(int B, int T, int D, int W) {
 }
 
 bool conv_shape_supported(int D, int W, int norm_group) {
-  return D > 0 && D % 8 == 0 && W == 4 &&
+  return D > 0 && D % CONV_CPL == 0 && W == 4 &&
          (norm_group == 0 || ((norm_group == 64 || norm_group == 128 || norm_group == 256) && D % norm_group == 0));
 }
+
+constexpr int CONV_WG_CH = CONV_WAVES * CONV_CW;
 
 template <typename T, int NG>
 static hipError_t conv_fwd_k(const ConvArgs& a) {
   const int nchunk = (a.T + CONV_L - 1) / CONV_L;
-  dim3 grid(a.B * nchunk, (a.D + CONV_CW - 1) / CONV_CW);
-  conv_silu_fwd_kernel<T, 4, NG><<<grid, 64, 0, a.stream>>>(
+  dim3 grid((a.D + CONV_WG_CH - 1) / CONV_WG_CH * a.B * nchunk);
+  conv_silu_fwd_kernel<T, 4, NG><<<grid, 64 * CONV_WAVES, 0, a.stream>>>(
       static_cast<const T*>(a.x), a.w, a.bias, static_cast<const T*>(a.state_in), static_cast<T*>(a.y),
       static_cast<T*>(a.state_out), a.T, a.D, nchunk);
   return hipGetLastError();
@@ -368,14 +438,14 @@ static hipError_t conv_bwd_k(const ConvArgs& a) {
   float* dw_part = static_cast<float*>(a.ws);
   float* db_part = reinterpret_cast<float*>(static_cast<char*>(a.ws) +
                                             (((size_t)nparts * a.D * 4 * 4 + 255) & ~size_t(255)));
-  dim3 grid(nparts, (a.D + CONV_CW - 1) / CONV_CW);
-  conv_silu_bwd_kernel<T, 4, NG><<<grid, 64, 0, a.stream>>>(
+  dim3 grid((a.D + CONV_WG_CH - 1) / CONV_WG_CH * nparts);
+  conv_silu_bwd_kernel<T, 4, NG><<<grid, 64 * CONV_WAVES, 0, a.stream>>>(
       static_cast<const T*>(a.x), a.w, a.bias, static_cast<const T*>(a.state_in), static_cast<const T*>(a.dy),
       static_cast<T*>(a.dx), static_cast<T*>(a.dstate_in), dw_part, db_part, a.T, a.D, nchunk);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  conv_param_reduce_kernel<<<dim3((a.D * 4 + a.D + 255) / 256), 256, 0, a.stream>>>(dw_part, db_part, a.dw,
-                                                                                   a.dbias, nparts, a.D, 4);
+  conv_param_reduce_kernel<<<dim3((a.D * 4 + a.D + RED_COLS - 1) / RED_COLS), 256, 0, a.stream>>>(
+      dw_part, db_part, a.dw, a.dbias, nparts, a.D, 4);
   return hipGetLastError();
 }
 

@@ -52,6 +52,17 @@ def _require_gpu(*ts: Optional[Tensor]) -> None:
                                f"{t.device}. There is no CPU fallback.")
 
 
+def _arg(t: Optional[Tensor], dtype: Optional[torch.dtype] = None) -> Optional[Tensor]:
+    """A kernel argument: ``dtype``, contiguous and 16-byte aligned (the C ABI requires it; an offset view is
+    copied)."""
+    if t is None:
+        return None
+    if dtype is not None:
+        t = t.to(dtype)
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _shapes(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, h0: Optional[Tensor]):
     if q.dim() != 4 or k.shape != q.shape:
         raise ValueError(f"q and k must be [B, T, H, K] with equal shapes, got {tuple(q.shape)} and {tuple(k.shape)}")
@@ -76,9 +87,8 @@ def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, h0: Opti
     B, T, H, K, V = _shapes(q, k, v, g, beta, h0)
     lib = _lib.load()
     dt = _lib.dtype_code(q.dtype)
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    g, beta = g.float().contiguous(), beta.float().contiguous()
-    h0 = None if h0 is None else h0.float().contiguous()
+    q, k, v = _arg(q), _arg(k), _arg(v)
+    g, beta, h0 = _arg(g, torch.float32), _arg(beta, torch.float32), _arg(h0, torch.float32)
     o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
     hT = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
     ws = torch.empty(_lib.ws_bytes("fwd", B, T, H, K, V, q.dtype), dtype=torch.uint8, device=q.device)
@@ -106,10 +116,9 @@ def chunk_bwd(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, h0: Opti
         raise ValueError(f"dO must be [B, T, H, V] = {(B, T, H, V)}, got {tuple(do.shape)}")
     lib = _lib.load()
     dt = _lib.dtype_code(q.dtype)
-    q, k, v, do = q.contiguous(), k.contiguous(), v.contiguous(), do.to(q.dtype).contiguous()
-    g, beta = g.float().contiguous(), beta.float().contiguous()
-    h0 = None if h0 is None else h0.float().contiguous()
-    dhT = None if dhT is None else dhT.float().contiguous()
+    q, k, v, do = _arg(q), _arg(k), _arg(v), _arg(do, q.dtype)
+    g, beta, h0 = _arg(g, torch.float32), _arg(beta, torch.float32), _arg(h0, torch.float32)
+    dhT = _arg(dhT, torch.float32)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dg = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
     db = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
@@ -152,8 +161,8 @@ chunk_fwd.register_autograd(_chunk_backward, setup_context=_chunk_setup)
 
 # ------------------------------------------------------------------------------------ training (stash) pair
 def _prep(q, k, v, g, beta, h0):
-    return (q.contiguous(), k.contiguous(), v.contiguous(), g.float().contiguous(), beta.float().contiguous(),
-            None if h0 is None else h0.float().contiguous())
+    return (_arg(q), _arg(k), _arg(v), _arg(g, torch.float32), _arg(beta, torch.float32),
+            _arg(h0, torch.float32))
 
 
 @torch.library.custom_op("archbench_amd::gdn_chunk_fwd_stash", mutates_args=())
@@ -192,8 +201,8 @@ def chunk_bwd_stashed(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, 
         raise ValueError(f"dO must be [B, T, H, V] = {(B, T, H, V)}, got {tuple(do.shape)}")
     lib = _lib.load()
     q, k, v, g, beta, h0 = _prep(q, k, v, g, beta, h0)
-    do = do.to(q.dtype).contiguous()
-    dhT = None if dhT is None else dhT.float().contiguous()
+    do = _arg(do, q.dtype)
+    dhT = _arg(dhT, torch.float32)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dg = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
     db = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
@@ -266,10 +275,8 @@ def short_conv(x: Tensor, w: Tensor, bias: Optional[Tensor], state: Optional[Ten
     _require_gpu(x, w, bias, state)
     B, T, D, W = _conv_shapes(x, w, bias, state)
     lib = _lib.load()
-    x = x.contiguous()
-    w = w.float().contiguous()
-    bias = None if bias is None else bias.float().contiguous()
-    state = None if state is None else state.to(x.dtype).contiguous()
+    x = _arg(x)
+    w, bias, state = _arg(w, torch.float32), _arg(bias, torch.float32), _arg(state, x.dtype)
     y = torch.empty_like(x)
     new_state = torch.empty(B, D, W - 1, dtype=x.dtype, device=x.device)
     rc = lib.gdn_short_conv_fwd(_lib.ptr(x), _lib.ptr(w), _lib.ptr(bias), _lib.ptr(state), _lib.ptr(y),
@@ -292,10 +299,8 @@ def short_conv_bwd(x: Tensor, w: Tensor, bias: Optional[Tensor], state: Optional
     _require_gpu(x, w, bias, state, dy)
     B, T, D, W = _conv_shapes(x, w, bias, state)
     lib = _lib.load()
-    x, dy = x.contiguous(), dy.to(x.dtype).contiguous()
-    w = w.float().contiguous()
-    bias = None if bias is None else bias.float().contiguous()
-    state = None if state is None else state.to(x.dtype).contiguous()
+    x, dy = _arg(x), _arg(dy, x.dtype)
+    w, bias, state = _arg(w, torch.float32), _arg(bias, torch.float32), _arg(state, x.dtype)
     dx = torch.empty_like(x)
     dw = torch.empty(D, W, dtype=torch.float32, device=x.device)
     db = torch.empty(D, dtype=torch.float32, device=x.device)
@@ -363,8 +368,8 @@ def _recurrent_step(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, st
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("q, k, v must share a dtype")
     lib = _lib.load()
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    g, beta = g.float().contiguous(), beta.float().contiguous()
+    q, k, v = _arg(q), _arg(k), _arg(v)
+    g, beta = _arg(g, torch.float32), _arg(beta, torch.float32)
     o = torch.empty(B, H, V, dtype=q.dtype, device=q.device)
     rc = lib.gdn_recurrent_step(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
                                 _lib.ptr(state), _lib.ptr(o), B, H, K, V, float(scale), _lib.dtype_code(q.dtype),

@@ -17,6 +17,10 @@ Also reported in the same line:
   fwd_only      forward alone at B=8, T=2048, H=8, K=V=128 (% of the bf16 MFMA peak);
   decode_step   one recurrent decode step at B=256, H=16, K=V=128 with the fp32 state updated in place
                 (HBM GB/s against 8 TB/s);
+  short_conv    the causal depthwise conv (kernel 4) + SiLU in front of the op at the layer's shape, B=8, T=4096,
+                D = H*K = 2048 channels, bf16: with the per-head (128-channel) L2 normalisation of q and k, and
+                without (v); forward and backward kernel times, HBM GB/s against 8 TB/s on the algorithmic bytes
+                (forward: x read, y written; backward: x and dy read, dx written);
   cpu_baseline  the CPU oracle (fp32 token recurrence + exact reverse-time backward) timed on this host's
                 cores on the full headline shape (about 20 s of CPU work at ~2e3 tokens/s on 16 threads).
 """
@@ -129,7 +133,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-sample-T", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "train", "fwd", "decode"], default="all",
+    ap.add_argument("--only", choices=["all", "train", "fwd", "decode", "conv"], default="all",
                     help="run one workload only (profiling runs); the JSON line needs 'all' or 'train'")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -235,6 +239,36 @@ def main() -> int:
                               "hbm_frac": round(nbytes / (kern_ms * 1e-3) / HBM_PEAK, 4),
                               "tokens_per_s": round(B / sec, 1)}
         log(f"decode kernel {kern_ms * 1e3:.2f} us, {out['decode_step']['GB_per_s']} GB/s")
+
+    if args.only in ("all", "conv"):
+        B, T, D = 8, 4096, 2048
+        log(f"short conv B={B} T={T} D={D} kernel 4 bf16")
+        gen = torch.Generator(device=dev).manual_seed(0)
+        xc = torch.randn(B, T, D, device=dev, generator=gen).to(torch.bfloat16)
+        dyc = torch.randn(B, T, D, device=dev, generator=gen).to(torch.bfloat16)
+        wc = torch.randn(D, 4, device=dev, generator=gen) * 0.5
+        res = {}
+        for name, ng in (("qk_norm128", 128), ("v_plain", 0)):
+            def conv_step():
+                ops.short_conv(xc, wc, None, None, ng)
+                ops.short_conv_bwd(xc, wc, None, None, dyc, ng)
+            timed_loop(conv_step, 3, 2, torch)
+            with _lib.StageTimer() as st:
+                for _ in range(max(10, min(args.steps, 30))):
+                    conv_step()
+            f_ms = st.result["conv_fwd"][0] / st.result["conv_fwd"][1]
+            b_ms = st.result["conv_bwd"][0] / st.result["conv_bwd"][1]
+            fb, bb = 2 * B * T * D * 2, 3 * B * T * D * 2
+            res[name] = {"norm_group": ng, "fwd_us": round(f_ms * 1e3, 2), "bwd_us": round(b_ms * 1e3, 2),
+                         "fwd_GB_per_s": round(fb / (f_ms * 1e-3) / 1e9, 1),
+                         "bwd_GB_per_s": round(bb / (b_ms * 1e-3) / 1e9, 1),
+                         "fwd_hbm_frac": round(fb / (f_ms * 1e-3) / HBM_PEAK, 4),
+                         "bwd_hbm_frac": round(bb / (b_ms * 1e-3) / HBM_PEAK, 4)}
+            log(f"short conv {name}: fwd {f_ms * 1e3:.1f} us ({res[name]['fwd_GB_per_s']} GB/s), "
+                f"bwd {b_ms * 1e3:.1f} us ({res[name]['bwd_GB_per_s']} GB/s)")
+        out["short_conv"] = {"workload": "gdn_short_conv", "B": B, "T": T, "D": D, "W": 4, **res}
+        del xc, dyc
+        torch.cuda.empty_cache()
 
     if args.only in ("all", "train") and not args.no_cpu_baseline:
         log(f"cpu baseline (oracle, T={args.cpu_sample_T})")

@@ -6,6 +6,9 @@
  * them, and only then).  Every call enqueues its kernels on `stream` (a hipStream_t
  * passed as void*; NULL is the default stream) and returns immediately.
  *
+ * Every array pointer must be 16-byte aligned (the kernels move rows with 16-byte accesses); any hipMalloc or
+ * torch allocation is, an offset view may not be (GDN_ERR_ARG).
+ *
  * Layouts (row-major, contiguous):
  *   q, k  [B, T, H, K]      v, o, dout  [B, T, H, V]       (token-major, "head_first = False")
  *   g, beta [B, T, H] fp32  (g = natural-log decay, beta = write strength)
@@ -99,7 +102,7 @@ int gdn_recurrent_step(const void* q, const void* k, const void* v, const float*
  * (archbench/layers/nsgdn.py:420-470; fla's ShortConvolution in GatedDeltaNet) and the per-head normalisation
  * of q and k (nsgdn.py:527-528).  x, y, dy, dx [B, T, D] token-major in dtype; w [D, W] and bias [D] fp32 (bias
  * may be NULL); conv states [B, D, W-1] in dtype, the previous W-1 inputs oldest first (state_in NULL = zeros;
- * state_out NULL = not returned; it must not alias state_in).  Compiled for W = 4, D % 8 == 0, norm_group in {0 (none), 64, 128, 256}.
+ * state_out NULL = not returned; it must not alias state_in).  Compiled for W = 4, D % 4 == 0, norm_group in {0 (none), 64, 128, 256}.
  * The backward writes dx, dw [D, W] fp32, dbias [D] fp32 (if non-NULL) and dstate_in (if non-NULL); its
  * workspace holds per-chunk partial sums of dw, reduced in a fixed order (deterministic). */
 int gdn_short_conv_fwd(const void* x, const float* w, const float* bias, const void* state_in, void* y,

@@ -112,9 +112,13 @@ def test_conv_empty_sequence():
 
 def test_conv_rejects_unsupported_shapes():
     banner("short conv shape errors")
-    x = torch.randn(1, 8, 12, device="cuda")
+    x = torch.randn(1, 8, 10, device="cuda")
     with pytest.raises(ValueError, match="not compiled"):
-        ops.short_conv(x, torch.randn(12, W, device="cuda"), None, None, 0)  # D % 8 != 0
+        ops.short_conv(x, torch.randn(10, W, device="cuda"), None, None, 0)  # D % 4 != 0
+    x, w12 = torch.randn(2, 8, 12), torch.randn(12, W)  # D = 12: three lanes of one wave
+    y, _ = ops.short_conv(x.cuda(), w12.cuda(), None, None, 0)
+    y_ref, _ = CO.short_conv_fwd(x, w12, None, None, 0)
+    assert max_abs(y, y_ref) <= 1e-5
     x = torch.randn(1, 8, 512, device="cuda")
     with pytest.raises(ValueError, match="not compiled"):
         ops.short_conv(x, torch.randn(512, W, device="cuda"), None, None, 96)  # unsupported group
