@@ -20,6 +20,7 @@ _p = ctypes.c_void_p
 _i = ctypes.c_int
 _f = ctypes.c_float
 _sz = ctypes.c_size_t
+_i64 = ctypes.c_int64
 
 # name -> (restype, argtypes); must list every function include/gdn_mi355x.h declares
 SIGNATURES = {
@@ -39,11 +40,17 @@ SIGNATURES = {
     "gdn_short_conv_fwd": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "gdn_short_conv_bwd_ws_bytes": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
     "gdn_short_conv_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _i, _p]),
+    "gdn_gated_rmsnorm_fwd": (_i, [_p, _p, _p, _p, _i64, _i, _f, _i, _p]),
+    "gdn_gated_rmsnorm_bwd_ws_bytes": (_i, [_i64, _i, ctypes.POINTER(_sz)]),
+    "gdn_gated_rmsnorm_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i, _f, _i, _p]),
+    "gdn_gates_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i, _f, _f, _i, _p]),
+    "gdn_gates_bwd_ws_bytes": (_i, [_i64, _i, ctypes.POINTER(_sz)]),
+    "gdn_gates_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i, _f, _f, _i, _p]),
     "gdn_profile_enable": (_i, [_i]),
     "gdn_profile_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
     "gdn_profile_stage_name": (ctypes.c_char_p, [_i]),
 }
-PROFILE_STAGES = 9
+PROFILE_STAGES = 13
 
 _lock = threading.Lock()
 _lib = None
@@ -119,6 +126,18 @@ def stash_bytes(B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype) -> t
 def conv_ws_bytes(B: int, T: int, D: int, W: int) -> int:
     out = _sz(0)
     check(load().gdn_short_conv_bwd_ws_bytes(B, T, D, W, ctypes.byref(out)), "gdn_short_conv_bwd_ws_bytes")
+    return out.value
+
+
+def norm_ws_bytes(rows: int, dim: int) -> int:
+    out = _sz(0)
+    check(load().gdn_gated_rmsnorm_bwd_ws_bytes(rows, dim, ctypes.byref(out)), "gdn_gated_rmsnorm_bwd_ws_bytes")
+    return out.value
+
+
+def gates_ws_bytes(ntok: int, H: int) -> int:
+    out = _sz(0)
+    check(load().gdn_gates_bwd_ws_bytes(ntok, H, ctypes.byref(out)), "gdn_gates_bwd_ws_bytes")
     return out.value
 
 

@@ -116,10 +116,10 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
 // ---- per-stage event timing (diagnostic; off unless gdn_profile_enable(1) was called on this thread) ----
 enum Stage {
   ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_FACTORS, ST_CONV_FWD,
-  ST_CONV_BWD, ST_COUNT
+  ST_CONV_BWD, ST_NORM_FWD, ST_NORM_BWD, ST_GATES_FWD, ST_GATES_BWD, ST_COUNT
 };
 static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step", "fwd_stash",
-                                            "factors", "conv_fwd", "conv_bwd"};
+                                            "factors", "conv_fwd", "conv_bwd", "norm_fwd", "norm_bwd", "gates_fwd", "gates_bwd"};
 struct ProfRec { int stage; hipEvent_t a, b; };
 struct Prof {
   bool on = false;
@@ -422,6 +422,117 @@ int gdn_short_conv_bwd(const void* x, const float* w, const float* bias, const v
   a.B = B; a.T = T; a.D = D; a.norm_group = norm_group; a.dtype = dtype; a.stream = st;
   const hipError_t e = timed(ST_CONV_BWD, st, [&] { return launch_conv(a, true); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "short conv backward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+static int norm_check(int64_t rows, int dim, float eps, int dtype) {
+  if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
+  if (rows < 0 || !(eps >= 0.f)) return fail(GDN_ERR_ARG, "invalid rows=%lld eps=%g", (long long)rows, eps);
+  if (!norm_shape_supported(dim)) return fail(GDN_ERR_SHAPE, "gated RMSNorm not compiled for dim=%d (64, 128, 256)", dim);
+  return GDN_OK;
+}
+
+int gdn_gated_rmsnorm_fwd(const void* x, const void* gate, const float* weight, void* y, int64_t rows, int dim,
+                          float eps, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (int e = norm_check(rows, dim, eps, dtype)) return e;
+  if (rows == 0) return GDN_OK;
+  if (!x || !y) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(x, gate, y)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
+  NormArgs a{};
+  a.x = x; a.gate = gate; a.w = weight; a.y = y; a.rows = rows; a.DV = dim; a.dtype = dtype; a.eps = eps;
+  a.stream = static_cast<hipStream_t>(stream);
+  const hipError_t e = timed(ST_NORM_FWD, a.stream, [&] { return launch_norm(a, false); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "gated RMSNorm forward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+int gdn_gated_rmsnorm_bwd_ws_bytes(int64_t rows, int dim, size_t* bytes) {
+  g_err[0] = 0;
+  if (int e = norm_check(rows, dim, 0.f, DT_F32)) return e;
+  if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
+  *bytes = rows ? norm_ws_bytes(rows, dim) : 0;
+  return GDN_OK;
+}
+
+int gdn_gated_rmsnorm_bwd(const void* x, const void* gate, const float* weight, const void* dy, void* dx,
+                          void* dgate, float* dweight, void* ws, size_t ws_bytes, int64_t rows, int dim, float eps,
+                          int dtype, void* stream) {
+  g_err[0] = 0;
+  if (int e = norm_check(rows, dim, eps, dtype)) return e;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rows == 0) {
+    if (copy_or_zero_bytes(nullptr, dweight, (size_t)dim * 4, st) != hipSuccess)
+      return fail(GDN_ERR_LAUNCH, "gated RMSNorm zero-fill launch failed");
+    return GDN_OK;
+  }
+  if (!x || !dy || !dx || (gate && !dgate)) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(x, gate, dy, dx, dgate, ws)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
+  const size_t need = norm_ws_bytes(rows, dim);
+  if (!ws || ws_bytes < need)
+    return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
+  NormArgs a{};
+  a.x = x; a.gate = gate; a.w = weight; a.dy = dy; a.dx = dx; a.dgate = dgate; a.dw = dweight; a.ws = ws;
+  a.rows = rows; a.DV = dim; a.dtype = dtype; a.eps = eps; a.stream = st;
+  const hipError_t e = timed(ST_NORM_BWD, st, [&] { return launch_norm(a, true); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "gated RMSNorm backward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+static int gates_check(int64_t ntok, int H, int dtype) {
+  if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
+  if (ntok < 0 || H <= 0) return fail(GDN_ERR_ARG, "invalid sizes ntok=%lld H=%d", (long long)ntok, H);
+  return GDN_OK;
+}
+
+int gdn_gates_fwd(const void* a, const void* b, const float* A_log, const float* dt_bias, const float* b_bias,
+                  float* g, float* beta, int64_t ntok, int H, float beta_scale, float g_min, int dtype,
+                  void* stream) {
+  g_err[0] = 0;
+  if (int e = gates_check(ntok, H, dtype)) return e;
+  if (ntok == 0) return GDN_OK;
+  if (!a || !b || !A_log || !g || !beta) return fail(GDN_ERR_ARG, "null input/output pointer");
+  GateArgs ga{};
+  ga.a = a; ga.b = b; ga.A_log = A_log; ga.dt_bias = dt_bias; ga.b_bias = b_bias; ga.g = g; ga.beta = beta;
+  ga.ntok = ntok; ga.H = H; ga.dtype = dtype; ga.beta_scale = beta_scale; ga.g_min = g_min;
+  ga.stream = static_cast<hipStream_t>(stream);
+  const hipError_t e = timed(ST_GATES_FWD, ga.stream, [&] { return launch_gates(ga, false); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "gates forward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+int gdn_gates_bwd_ws_bytes(int64_t ntok, int H, size_t* bytes) {
+  g_err[0] = 0;
+  if (int e = gates_check(ntok, H, DT_F32)) return e;
+  if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
+  *bytes = ntok ? gates_ws_bytes(ntok, H) : 0;
+  return GDN_OK;
+}
+
+int gdn_gates_bwd(const void* a, const void* b, const float* A_log, const float* dt_bias, const float* b_bias,
+                  const float* dg, const float* dbeta, void* da, void* db, float* dA_log, float* ddt_bias,
+                  float* db_bias, void* ws, size_t ws_bytes, int64_t ntok, int H, float beta_scale, float g_min,
+                  int dtype, void* stream) {
+  g_err[0] = 0;
+  if (int e = gates_check(ntok, H, dtype)) return e;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (ntok == 0) {
+    hipError_t e = copy_or_zero_bytes(nullptr, dA_log, (size_t)H * 4, st);
+    if (e == hipSuccess) e = copy_or_zero_bytes(nullptr, ddt_bias, (size_t)H * 4, st);
+    if (e == hipSuccess) e = copy_or_zero_bytes(nullptr, db_bias, (size_t)H * 4, st);
+    if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "gates zero-fill: %s", hipGetErrorString(e));
+    return GDN_OK;
+  }
+  if (!a || !b || !A_log || !dg || !dbeta || !da || !db) return fail(GDN_ERR_ARG, "null input/output pointer");
+  const size_t need = gates_ws_bytes(ntok, H);
+  if (!ws || ws_bytes < need)
+    return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
+  GateArgs ga{};
+  ga.a = a; ga.b = b; ga.A_log = A_log; ga.dt_bias = dt_bias; ga.b_bias = b_bias; ga.dg = dg; ga.dbeta = dbeta;
+  ga.da = da; ga.db = db; ga.dA_log = dA_log; ga.ddt_bias = ddt_bias; ga.db_bias = db_bias; ga.ws = ws;
+  ga.ntok = ntok; ga.H = H; ga.dtype = dtype; ga.beta_scale = beta_scale; ga.g_min = g_min; ga.stream = st;
+  const hipError_t e = timed(ST_GATES_BWD, st, [&] { return launch_gates(ga, true); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "gates backward launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }
 

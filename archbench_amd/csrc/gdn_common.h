@@ -213,6 +213,63 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
+// hardware reciprocal (1 ulp) in place of an IEEE division, and the logistic function on it
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float fast_sigmoid(float z) { return fast_rcp(1.f + __expf(-z)); }
+
+// 8 consecutive elements of a row as loaded (16 B in bf16, 32 B in fp32), converted to fp32 at use
+template <typename T>
+struct Row8;
+template <>
+struct Row8<bf16> {
+  bf16x8 r;
+  __device__ __forceinline__ void load(const bf16* p) { r = *reinterpret_cast<const bf16x8*>(p); }
+  __device__ __forceinline__ void get(float (&v)[8]) const {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(r[j]);
+  }
+};
+template <>
+struct Row8<float> {
+  f32x4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const f32x4*>(p);
+    b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ void get(float (&v)[8]) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = a[j];
+      v[4 + j] = b[j];
+    }
+  }
+};
+template <typename T>
+__device__ __forceinline__ void store_row8(T* p, const float (&v)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    bf16x8 r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = static_cast<bf16>(v[j]);
+    *reinterpret_cast<bf16x8*>(p) = r;
+  } else {
+    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  }
+}
+
+// Sum over aligned runs of LANES lanes (1, 2, 4, ..., 64), the same value left in every lane of the run: DPP
+// butterflies within 16 lanes (as sum16), lane shuffles across rows.
+template <int LANES>
+__device__ __forceinline__ float lane_group_sum(float s) {
+  if constexpr (LANES >= 2) s = dpp_sum_step<0xb1>(s);
+  if constexpr (LANES >= 4) s = dpp_sum_step<0x4e>(s);
+  if constexpr (LANES >= 8) s = dpp_sum_step<0x141>(s);
+  if constexpr (LANES >= 16) s = dpp_sum_step<0x140>(s);
+  if constexpr (LANES >= 32) s += __shfl_xor(s, 16);
+  if constexpr (LANES >= 64) s += __shfl_xor(s, 32);
+  return s;
+}
+
 // Inclusive prefix sum over the 64 lanes of a wave, on DPP: shifts within each 16-lane row, then the row
 // totals broadcast forward (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3).
 template <int CTRL, int ROW_MASK>

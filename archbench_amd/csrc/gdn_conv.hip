@@ -13,7 +13,7 @@
 // is reduced with lane shuffles.  HBM-bound: x read once, y written once.
 // Backward: each wave recomputes z for its chunk plus W-1 tokens of look-ahead, forms dz and emits dx with a
 // W-token delay; dw and dbias are summed per wave into a per-chunk partial and reduced over chunks in a fixed
-// order by a second kernel (deterministic, no atomics).
+// order by column_sum_kernel (deterministic, no atomics).
 #include <type_traits>
 
 #include "gdn_common.h"
@@ -60,23 +60,11 @@ __device__ __forceinline__ void store4(T* p, const float (&v)[4]) {
     *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
   }
 }
-// sum over the NG / CONV_CPL lanes of a normalisation group (aligned runs of lanes), the same value in every lane:
-// within 16 lanes by DPP butterflies on the VALU (xor 1, xor 2, then half-row and row mirrors), across rows by
-// lane shuffles
+// sum over the NG / CONV_CPL lanes of a normalisation group (aligned runs of lanes), the same value in every lane
 template <int NG>
 __device__ __forceinline__ float group_sum(float s) {
-  constexpr int LANES = NG / CONV_CPL;
-  if constexpr (LANES >= 2) s = dpp_sum_step<0xb1>(s);
-  if constexpr (LANES >= 4) s = dpp_sum_step<0x4e>(s);
-  if constexpr (LANES >= 8) s = dpp_sum_step<0x141>(s);
-  if constexpr (LANES >= 16) s = dpp_sum_step<0x140>(s);
-  if constexpr (LANES >= 32) s += __shfl_xor(s, 16);
-  if constexpr (LANES >= 64) s += __shfl_xor(s, 32);
-  return s;
+  return lane_group_sum<NG / CONV_CPL>(s);
 }
-// hardware reciprocal (1 ulp) in place of an IEEE division
-__device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
-__device__ __forceinline__ float sigmoidf(float z) { return rcp(1.f + __expf(-z)); }
 constexpr float NORM_EPS = 1e-12f;  // F.normalize's eps
 
 template <typename T, int W>
@@ -141,11 +129,11 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_fwd_kernel(const T*
       float z = bk[j] + wk[j][W - 1] * xt[j];
 #pragma unroll
       for (int i = 0; i < W - 1; ++i) z += wk[j][i] * win[i][j];
-      yt[j] = z * sigmoidf(z);
+      yt[j] = z * fast_sigmoid(z);
       ss += yt[j] * yt[j];
     }
     if constexpr (NG > 0) {
-      const float inv = rcp(fmaxf(sqrtf(group_sum<NG>(ss)), NORM_EPS));
+      const float inv = fast_rcp(fmaxf(sqrtf(group_sum<NG>(ss)), NORM_EPS));
 #pragma unroll
       for (int j = 0; j < CPL; ++j) yt[j] *= inv;
     }
@@ -199,8 +187,8 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
                                                            const float* __restrict__ bias,
                                                            const T* __restrict__ state_in,
                                                            const T* __restrict__ dy, T* __restrict__ dx,
-                                                           T* __restrict__ dstate_in, float* __restrict__ dw_part,
-                                                           float* __restrict__ db_part, int Tn, int D, int nchunk) {
+                                                           T* __restrict__ dstate_in, float* __restrict__ part_out,
+                                                           int Tn, int D, int nchunk) {
   constexpr int CPL = CONV_CPL, U = CONV_UB;
   const int l = lane_id();
   const int ncg = (D + CONV_WAVES * CONV_CW - 1) / (CONV_WAVES * CONV_CW);
@@ -267,13 +255,13 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
       z[j] = bk[j] + wk[j][W - 1] * xs[j];
 #pragma unroll
       for (int i = 0; i < W - 1; ++i) z[j] += wk[j][i] * win[i][j];
-      sg[j] = sigmoidf(z[j]);
+      sg[j] = fast_sigmoid(z[j]);
       ysl[j] = z[j] * sg[j];
       ss += ysl[j] * ysl[j];
     }
     if constexpr (NG > 0) {
       const float nrm = sqrtf(group_sum<NG>(ss));
-      const float inv = rcp(fmaxf(nrm, NORM_EPS));
+      const float inv = fast_rcp(fmaxf(nrm, NORM_EPS));
       float dot = 0.f;
 #pragma unroll
       for (int j = 0; j < CPL; ++j) dot += ysl[j] * inv * ds[j];
@@ -360,50 +348,12 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
     for (int j = 0; j < CPL; ++j) dzw[W - 2][j] = 0.f;
   }
   if (on) {
-    const int64_t row = (int64_t)part * D + cc;
+    float* row = part_out + (int64_t)part * (D * W + D);  // [dw (D x W) | dbias (D)] of this (b, chunk)
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
 #pragma unroll
-      for (int i = 0; i < W; ++i) dw_part[(row + j) * W + i] = dwa[j][i];
-      db_part[row + j] = dba[j];
-    }
-  }
-}
-
-// dw[c, i] and dbias[c]: the B * nchunk partials summed in a fixed order.  One workgroup per 64 consecutive
-// outputs of the concatenation [dw (D * W) | dbias (D)]; wave v sums partials v, v + 4, ... (coalesced 256-byte
-// rows), then lane sums of the four waves are added in wave order.
-constexpr int RED_COLS = 64;
-__global__ __launch_bounds__(256) void conv_param_reduce_kernel(const float* __restrict__ dw_part,
-                                                                const float* __restrict__ db_part,
-                                                                float* __restrict__ dw, float* __restrict__ db,
-                                                                int nparts, int D, int W) {
-  __shared__ float red[4][RED_COLS];
-  const int v = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int i = blockIdx.x * RED_COLS + l;  // index into [dw | dbias]
-  const int ndw = D * W;
-  const bool is_dw = i < ndw, valid = i < ndw + D;
-  const float* src = is_dw ? dw_part + i : db_part + (i - ndw);
-  const int64_t stride = is_dw ? ndw : D;
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;  // four chains in flight, combined in a fixed order
-  if (valid) {
-    int p = v;
-    for (; p + 12 < nparts; p += 16) {
-      a0 += src[(int64_t)p * stride];
-      a1 += src[(int64_t)(p + 4) * stride];
-      a2 += src[(int64_t)(p + 8) * stride];
-      a3 += src[(int64_t)(p + 12) * stride];
-    }
-    for (; p < nparts; p += 4) a0 += src[(int64_t)p * stride];
-  }
-  red[v][l] = (a0 + a1) + (a2 + a3);
-  __syncthreads();
-  if (v == 0 && valid) {
-    const float r = ((red[0][l] + red[1][l]) + red[2][l]) + red[3][l];
-    if (is_dw) {
-      dw[i] = r;
-    } else if (db) {
-      db[i - ndw] = r;
+      for (int i = 0; i < W; ++i) row[(cc + j) * W + i] = dwa[j][i];
+      row[D * W + cc + j] = dba[j];
     }
   }
 }
@@ -411,7 +361,7 @@ __global__ __launch_bounds__(256) void conv_param_reduce_kernel(const float* __r
 // ---------------------------------------------------------------------------------------------------------
 size_t conv_ws_bytes(int B, int T, int D, int W) {
   const size_t nparts = (size_t)B * ((T + CONV_L - 1) / CONV_L);
-  return ((nparts * D * W * 4 + 255) & ~size_t(255)) + ((nparts * D * 4 + 255) & ~size_t(255));
+  return (nparts * (size_t)(D * W + D) * 4 + 255) & ~size_t(255);
 }
 
 bool conv_shape_supported(int D, int W, int norm_group) {
@@ -435,18 +385,15 @@ template <typename T, int NG>
 static hipError_t conv_bwd_k(const ConvArgs& a) {
   const int nchunk = (a.T + CONV_L - 1) / CONV_L;
   const int nparts = a.B * nchunk;
-  float* dw_part = static_cast<float*>(a.ws);
-  float* db_part = reinterpret_cast<float*>(static_cast<char*>(a.ws) +
-                                            (((size_t)nparts * a.D * 4 * 4 + 255) & ~size_t(255)));
+  float* part = static_cast<float*>(a.ws);
   dim3 grid((a.D + CONV_WG_CH - 1) / CONV_WG_CH * nparts);
   conv_silu_bwd_kernel<T, 4, NG><<<grid, 64 * CONV_WAVES, 0, a.stream>>>(
       static_cast<const T*>(a.x), a.w, a.bias, static_cast<const T*>(a.state_in), static_cast<const T*>(a.dy),
-      static_cast<T*>(a.dx), static_cast<T*>(a.dstate_in), dw_part, db_part, a.T, a.D, nchunk);
+      static_cast<T*>(a.dx), static_cast<T*>(a.dstate_in), part, a.T, a.D, nchunk);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  conv_param_reduce_kernel<<<dim3((a.D * 4 + a.D + RED_COLS - 1) / RED_COLS), 256, 0, a.stream>>>(
-      dw_part, db_part, a.dw, a.dbias, nparts, a.D, 4);
-  return hipGetLastError();
+  return launch_column_sum(part, nparts, a.D * 4 + a.D, ColumnOut{{a.dw, a.dbias, nullptr}, {a.D * 4, a.D, 0}},
+                           a.stream);
 }
 
 template <typename T>

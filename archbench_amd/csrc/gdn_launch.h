@@ -82,6 +82,51 @@ size_t conv_ws_bytes(int B, int T, int D, int W);
 bool conv_shape_supported(int D, int W, int norm_group);
 hipError_t launch_conv(const ConvArgs& a, bool backward);
 
+// Destinations of consecutive column ranges: columns [0, n[0]) go to p[0], the next n[1] to p[1], the next n[2]
+// to p[2]; a null p drops its range.
+struct ColumnOut {
+  float* p[3];
+  int n[3];
+};
+// out[c] = sum over p < nparts of part[p * ld + c] (c < n[0] + n[1] + n[2]), in a fixed order.
+hipError_t launch_column_sum(const float* part, int64_t nparts, int64_t ld, ColumnOut out, hipStream_t stream);
+
+// Gated RMSNorm over rows of DV channels (x, gate, y, dy, dx, dgate [rows, DV] in dtype; gate may be null).
+struct NormArgs {
+  const void* x;
+  const void* gate;
+  const float* w;  // [DV] or null (ones)
+  void* y;         // forward
+  const void* dy;  // backward
+  void *dx, *dgate;
+  float* dw;       // [DV] or null
+  void* ws;        // backward: norm_ws_bytes
+  int64_t rows;
+  int DV, dtype;
+  float eps;
+  hipStream_t stream;
+};
+bool norm_shape_supported(int DV);
+size_t norm_ws_bytes(int64_t rows, int DV);
+hipError_t launch_norm(const NormArgs& a, bool backward);
+
+// Gate functions over [ntok, H] (a, b, da, db in dtype; g, beta, dg, dbeta fp32).
+struct GateArgs {
+  const void *a, *b;
+  const float *A_log, *dt_bias, *b_bias;  // [H]; dt_bias, b_bias may be null (zero)
+  float *g, *beta;                        // forward
+  const float *dg, *dbeta;                // backward
+  void *da, *db;
+  float *dA_log, *ddt_bias, *db_bias;     // [H]; null = not wanted
+  void* ws;                               // backward: gates_ws_bytes
+  int64_t ntok;
+  int H, dtype;
+  float beta_scale, g_min;
+  hipStream_t stream;
+};
+size_t gates_ws_bytes(int64_t ntok, int H);
+hipError_t launch_gates(const GateArgs& a, bool backward);
+
 // Compute units of the current device (cached per device; 256 if the query fails).
 int device_cu_count();
 

@@ -9,7 +9,8 @@ g = -exp(A_log) softplus(a + dt_bias) (natural-log decay), fp32 state.  The outp
 ``o_proj`` so the reference's zero-init rule for output projections (archbench/model.py:14, :80-82) applies.
 
 The token mixing itself is always the HIP chunk op (training / prefill) or the HIP decode step (T = 1 with
-a recurrent state, no grad).  Projections, the short causal convolutions and the gated RMSNorm are PyTorch.
+a recurrent state, no grad).  The short causal convolutions (with the q / k normalisation fused in), the gate
+functions and the output gated RMSNorm run on their own HIP kernels; the projections are PyTorch linears.
 """
 
 from __future__ import annotations
@@ -43,7 +44,8 @@ class ShortConvolution(nn.Module):
 
 
 class GatedRMSNorm(nn.Module):
-    """RMSNorm over the head dimension times swish(gate) (fla's FusedRMSNormGated, nsgdn.py:539-541)."""
+    """RMSNorm over the head dimension times swish(gate) (fla's FusedRMSNormGated, nsgdn.py:539-541), one HIP
+    pass (``ops.gated_rmsnorm``), fp32 arithmetic, output in x's dtype."""
 
     def __init__(self, dim: int, eps: float = 1e-5):
         super().__init__()
@@ -51,10 +53,7 @@ class GatedRMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x: torch.Tensor, gate: torch.Tensor | None = None) -> torch.Tensor:
-        y = F.rms_norm(x.float(), (x.shape[-1],), self.weight.float(), self.eps)
-        if gate is not None:
-            y = y * F.silu(gate.float())
-        return y.to(x.dtype)
+        return ops.gated_rmsnorm(x, gate, self.weight, self.eps)
 
 
 class GatedDeltaNet(nn.Module):
@@ -116,10 +115,9 @@ class GatedDeltaNet(nn.Module):
         else:
             q, k, v = F.silu(q), F.silu(k), F.silu(v)
         q, k, v = q.view(B, T, H, DK), k.view(B, T, H, DK), v.view(B, T, H, DV)
-        beta = self.b_proj(hidden_states).float().sigmoid()
-        if self.allow_neg_eigval:
-            beta = beta * 2.0
-        g = -self.A_log.float().exp() * F.softplus(self.a_proj(hidden_states).float() + self.dt_bias)
+        # g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b) (x2 with negative eigenvalues), one HIP pass
+        g, beta = ops.gdn_gates(self.a_proj(hidden_states), self.b_proj(hidden_states), self.A_log, self.dt_bias,
+                                None, 2.0 if self.allow_neg_eigval else 1.0, float("-inf"))
         state = entry["recurrent_state"] if entry is not None else None
         dt = hidden_states.dtype if hidden_states.dtype in (torch.bfloat16, torch.float32) else torch.bfloat16
         q, k, v = q.to(dt), k.to(dt), v.to(dt)

@@ -42,7 +42,7 @@ from torch import Tensor
 from . import _lib
 
 __all__ = ["chunk_gated_delta_rule", "fused_recurrent_gated_delta_rule", "recurrent_step", "chunk_fwd",
-           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "short_conv"]
+           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "short_conv", "gated_rmsnorm", "gdn_gates"]
 
 
 def _require_gpu(*ts: Optional[Tensor]) -> None:
@@ -349,6 +349,166 @@ def _conv_backward(ctx, dy, dstate_out):
 
 
 short_conv.register_autograd(_conv_backward, setup_context=_conv_setup)
+
+
+# ---------------------------------------------------------------------------------------------- gated RMSNorm
+# The output normalisation of the mixer (fla FusedRMSNormGated; nsgdn.py:539-541: self.norm(y) * silu(g)) as one
+# pass: y = x * rsqrt(mean(x^2) + eps) * weight * silu(gate) over the last dimension, fp32 arithmetic.
+def _norm_rows(x: Tensor, gate: Optional[Tensor], weight: Optional[Tensor]):
+    if x.dim() < 1 or x.shape[-1] == 0:
+        raise ValueError(f"x must have a non-empty last dimension, got {tuple(x.shape)}")
+    dim = x.shape[-1]
+    if gate is not None and gate.shape != x.shape:
+        raise ValueError(f"gate must match x's shape {tuple(x.shape)}, got {tuple(gate.shape)}")
+    if weight is not None and tuple(weight.shape) != (dim,):
+        raise ValueError(f"weight must be [{dim}], got {tuple(weight.shape)}")
+    return x.numel() // dim, dim
+
+
+@torch.library.custom_op("archbench_amd::gated_rmsnorm", mutates_args=())
+def gated_rmsnorm(x: Tensor, gate: Optional[Tensor], weight: Optional[Tensor], eps: float) -> Tensor:
+    _require_gpu(x, gate, weight)
+    rows, dim = _norm_rows(x, gate, weight)
+    lib = _lib.load()
+    x, gate, weight = _arg(x), _arg(gate, x.dtype), _arg(weight, torch.float32)
+    y = torch.empty_like(x)
+    rc = lib.gdn_gated_rmsnorm_fwd(_lib.ptr(x), _lib.ptr(gate), _lib.ptr(weight), _lib.ptr(y), rows, dim,
+                                   float(eps), _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device))
+    _lib.check(rc, "gdn_gated_rmsnorm_fwd")
+    return y
+
+
+@gated_rmsnorm.register_fake
+def _(x, gate, weight, eps):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("archbench_amd::gated_rmsnorm_bwd", mutates_args=())
+def gated_rmsnorm_bwd(x: Tensor, gate: Optional[Tensor], weight: Optional[Tensor], dy: Tensor,
+                      eps: float) -> tuple[Tensor, Tensor, Tensor]:
+    """(dx, dgate (zeros-shaped [0] without a gate), dweight [dim] fp32)."""
+    _require_gpu(x, gate, weight, dy)
+    rows, dim = _norm_rows(x, gate, weight)
+    lib = _lib.load()
+    x, gate, weight, dy = _arg(x), _arg(gate, x.dtype), _arg(weight, torch.float32), _arg(dy, x.dtype)
+    dx = torch.empty_like(x)
+    dgate = torch.empty_like(x) if gate is not None else x.new_empty(0)
+    dw = torch.empty(dim, dtype=torch.float32, device=x.device)
+    ws = torch.empty(_lib.norm_ws_bytes(rows, dim), dtype=torch.uint8, device=x.device)
+    rc = lib.gdn_gated_rmsnorm_bwd(_lib.ptr(x), _lib.ptr(gate), _lib.ptr(weight), _lib.ptr(dy), _lib.ptr(dx),
+                                   _lib.ptr(dgate) if gate is not None else None, _lib.ptr(dw), _lib.ptr(ws),
+                                   ws.numel(), rows, dim, float(eps), _lib.dtype_code(x.dtype),
+                                   _lib.stream_ptr(x.device))
+    _lib.check(rc, "gdn_gated_rmsnorm_bwd")
+    return dx, dgate, dw
+
+
+@gated_rmsnorm_bwd.register_fake
+def _(x, gate, weight, dy, eps):
+    return (torch.empty_like(x), torch.empty_like(x) if gate is not None else x.new_empty(0),
+            x.new_empty(x.shape[-1], dtype=torch.float32))
+
+
+def _norm_setup(ctx, inputs, output):
+    x, gate, weight, eps = inputs
+    ctx.save_for_backward(x, gate, weight)
+    ctx.eps = eps
+    ctx.w_dtype = None if weight is None else weight.dtype
+
+
+def _norm_backward(ctx, dy):
+    x, gate, weight = ctx.saved_tensors
+    dx, dgate, dw = gated_rmsnorm_bwd(x, gate, weight, dy, ctx.eps)
+    return (dx, (dgate.to(gate.dtype) if gate is not None else None),
+            (dw.to(ctx.w_dtype) if weight is not None else None), None)
+
+
+gated_rmsnorm.register_autograd(_norm_backward, setup_context=_norm_setup)
+
+
+# ------------------------------------------------------------------------------------------------------ gates
+# g = max(-exp(A_log) * softplus(a + dt_bias), g_min) and beta = beta_scale * sigmoid(b + b_bias) per token and
+# head (nsgdn.py:531-533; fla GatedDeltaNet's g and beta), one pass forward and one backward.
+def _gate_shapes(a: Tensor, b: Tensor, A_log: Tensor, dt_bias: Optional[Tensor], b_bias: Optional[Tensor]):
+    if a.dim() < 1 or b.shape != a.shape:
+        raise ValueError(f"a and b must share a shape [..., H], got {tuple(a.shape)} and {tuple(b.shape)}")
+    H = a.shape[-1]
+    for n, t in (("A_log", A_log), ("dt_bias", dt_bias), ("b_bias", b_bias)):
+        if t is not None and tuple(t.shape) != (H,):
+            raise ValueError(f"{n} must be [H] = [{H}], got {tuple(t.shape)}")
+    if H == 0:
+        raise ValueError("H must be positive")
+    return a.numel() // H, H
+
+
+@torch.library.custom_op("archbench_amd::gdn_gates", mutates_args=())
+def gdn_gates(a: Tensor, b: Tensor, A_log: Tensor, dt_bias: Optional[Tensor], b_bias: Optional[Tensor],
+              beta_scale: float, g_min: float) -> tuple[Tensor, Tensor]:
+    """(g, beta), fp32, shaped like a."""
+    _require_gpu(a, b, A_log, dt_bias, b_bias)
+    ntok, H = _gate_shapes(a, b, A_log, dt_bias, b_bias)
+    lib = _lib.load()
+    a, b = _arg(a), _arg(b, a.dtype)
+    A_log, dt_bias, b_bias = _arg(A_log, torch.float32), _arg(dt_bias, torch.float32), _arg(b_bias, torch.float32)
+    g = torch.empty(a.shape, dtype=torch.float32, device=a.device)
+    beta = torch.empty(a.shape, dtype=torch.float32, device=a.device)
+    rc = lib.gdn_gates_fwd(_lib.ptr(a), _lib.ptr(b), _lib.ptr(A_log), _lib.ptr(dt_bias), _lib.ptr(b_bias),
+                           _lib.ptr(g), _lib.ptr(beta), ntok, H, float(beta_scale), float(g_min),
+                           _lib.dtype_code(a.dtype), _lib.stream_ptr(a.device))
+    _lib.check(rc, "gdn_gates_fwd")
+    return g, beta
+
+
+@gdn_gates.register_fake
+def _(a, b, A_log, dt_bias, b_bias, beta_scale, g_min):
+    return a.new_empty(a.shape, dtype=torch.float32), a.new_empty(a.shape, dtype=torch.float32)
+
+
+@torch.library.custom_op("archbench_amd::gdn_gates_bwd", mutates_args=())
+def gdn_gates_bwd(a: Tensor, b: Tensor, A_log: Tensor, dt_bias: Optional[Tensor], b_bias: Optional[Tensor],
+                  dg: Tensor, dbeta: Tensor, beta_scale: float,
+                  g_min: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(da, db, dA_log, ddt_bias, db_bias); the three [H] gradients fp32."""
+    _require_gpu(a, b, A_log, dt_bias, b_bias, dg, dbeta)
+    ntok, H = _gate_shapes(a, b, A_log, dt_bias, b_bias)
+    lib = _lib.load()
+    a, b = _arg(a), _arg(b, a.dtype)
+    A_log, dt_bias, b_bias = _arg(A_log, torch.float32), _arg(dt_bias, torch.float32), _arg(b_bias, torch.float32)
+    dg, dbeta = _arg(dg, torch.float32), _arg(dbeta, torch.float32)
+    da, db = torch.empty_like(a), torch.empty_like(a)
+    dA, ddt, dbb = (torch.empty(H, dtype=torch.float32, device=a.device) for _ in range(3))
+    ws = torch.empty(_lib.gates_ws_bytes(ntok, H), dtype=torch.uint8, device=a.device)
+    rc = lib.gdn_gates_bwd(_lib.ptr(a), _lib.ptr(b), _lib.ptr(A_log), _lib.ptr(dt_bias), _lib.ptr(b_bias),
+                           _lib.ptr(dg), _lib.ptr(dbeta), _lib.ptr(da), _lib.ptr(db), _lib.ptr(dA), _lib.ptr(ddt),
+                           _lib.ptr(dbb), _lib.ptr(ws), ws.numel(), ntok, H, float(beta_scale), float(g_min),
+                           _lib.dtype_code(a.dtype), _lib.stream_ptr(a.device))
+    _lib.check(rc, "gdn_gates_bwd")
+    return da, db, dA, ddt, dbb
+
+
+@gdn_gates_bwd.register_fake
+def _(a, b, A_log, dt_bias, b_bias, dg, dbeta, beta_scale, g_min):
+    H = a.shape[-1]
+    f32 = dict(dtype=torch.float32)
+    return (torch.empty_like(a), torch.empty_like(a), a.new_empty(H, **f32), a.new_empty(H, **f32),
+            a.new_empty(H, **f32))
+
+
+def _gates_setup(ctx, inputs, output):
+    a, b, A_log, dt_bias, b_bias, beta_scale, g_min = inputs
+    ctx.save_for_backward(a, b, A_log, dt_bias, b_bias)
+    ctx.beta_scale, ctx.g_min = beta_scale, g_min
+    ctx.set_materialize_grads(True)
+
+
+def _gates_backward(ctx, dg, dbeta):
+    a, b, A_log, dt_bias, b_bias = ctx.saved_tensors
+    da, db, dA, ddt, dbb = gdn_gates_bwd(a, b, A_log, dt_bias, b_bias, dg, dbeta, ctx.beta_scale, ctx.g_min)
+    return (da, db.to(b.dtype), dA.to(A_log.dtype), None if dt_bias is None else ddt.to(dt_bias.dtype),
+            None if b_bias is None else dbb.to(b_bias.dtype), None, None)
+
+
+gdn_gates.register_autograd(_gates_backward, setup_context=_gates_setup)
 
 
 # ------------------------------------------------------------------------------------------------- decode step

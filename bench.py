@@ -21,6 +21,9 @@ Also reported in the same line:
                 D = H*K = 2048 channels, bf16: with the per-head (128-channel) L2 normalisation of q and k, and
                 without (v); forward and backward kernel times, HBM GB/s against 8 TB/s on the algorithmic bytes
                 (forward: x read, y written; backward: x and dy read, dx written);
+  gated_rmsnorm the output norm(o) * silu(gate) over B*T*H = 524288 rows of DV = 128, bf16, forward and backward
+                (HBM GB/s: forward reads x and gate, writes y; backward reads x, gate, dy, writes dx, dgate);
+  gates         g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b) over B*T = 32768 tokens x H = 16;
   cpu_baseline  the CPU oracle (fp32 token recurrence + exact reverse-time backward) timed on this host's
                 cores on the full headline shape (about 20 s of CPU work at ~2e3 tokens/s on 16 threads).
 """
@@ -133,7 +136,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-sample-T", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "train", "fwd", "decode", "conv"], default="all",
+    ap.add_argument("--only", choices=["all", "train", "fwd", "decode", "conv", "norm"], default="all",
                     help="run one workload only (profiling runs); the JSON line needs 'all' or 'train'")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -268,6 +271,42 @@ def main() -> int:
                 f"bwd {b_ms * 1e3:.1f} us ({res[name]['bwd_GB_per_s']} GB/s)")
         out["short_conv"] = {"workload": "gdn_short_conv", "B": B, "T": T, "D": D, "W": 4, **res}
         del xc, dyc
+        torch.cuda.empty_cache()
+
+    if args.only in ("all", "norm"):
+        rows, dim, ntok, H = 8 * 4096 * 16, 128, 8 * 4096, 16
+        log(f"gated RMSNorm rows={rows} dim={dim} and gates ntok={ntok} H={H}, bf16")
+        gen = torch.Generator(device=dev).manual_seed(1)
+        xn, gn, dyn = (torch.randn(rows, dim, device=dev, generator=gen).to(torch.bfloat16) for _ in range(3))
+        wn = torch.rand(dim, device=dev, generator=gen) + 0.5
+        ga, gb = (torch.randn(ntok, H, device=dev, generator=gen).to(torch.bfloat16) for _ in range(2))
+        gA, gdt = torch.rand(H, device=dev, generator=gen), torch.randn(H, device=dev, generator=gen)
+        gdg, gdb = (torch.randn(ntok, H, device=dev, generator=gen) for _ in range(2))
+
+        def norm_step():
+            ops.gated_rmsnorm(xn, gn, wn, 1e-5)
+            ops.gated_rmsnorm_bwd(xn, gn, wn, dyn, 1e-5)
+            ops.gdn_gates(ga, gb, gA, gdt, None, 1.0, float("-inf"))
+            ops.gdn_gates_bwd(ga, gb, gA, gdt, None, gdg, gdb, 1.0, float("-inf"))
+
+        timed_loop(norm_step, 3, 2, torch)
+        with _lib.StageTimer() as st:
+            for _ in range(max(10, min(args.steps, 30))):
+                norm_step()
+        us = {k: st.result[k][0] / st.result[k][1] * 1e3 for k in ("norm_fwd", "norm_bwd", "gates_fwd", "gates_bwd")}
+        E = rows * dim * 2
+        out["gated_rmsnorm"] = {"workload": "gdn_gated_rmsnorm", "rows": rows, "dim": dim,
+                                "fwd_us": round(us["norm_fwd"], 2), "bwd_us": round(us["norm_bwd"], 2),
+                                "fwd_GB_per_s": round(3 * E / us["norm_fwd"] / 1e3, 1),
+                                "bwd_GB_per_s": round(5 * E / us["norm_bwd"] / 1e3, 1),
+                                "fwd_hbm_frac": round(3 * E / (us["norm_fwd"] * 1e-6) / HBM_PEAK, 4),
+                                "bwd_hbm_frac": round(5 * E / (us["norm_bwd"] * 1e-6) / HBM_PEAK, 4)}
+        out["gates"] = {"workload": "gdn_gates", "ntok": ntok, "H": H, "fwd_us": round(us["gates_fwd"], 2),
+                        "bwd_us": round(us["gates_bwd"], 2)}
+        log(f"gated RMSNorm fwd {us['norm_fwd']:.1f} us ({out['gated_rmsnorm']['fwd_GB_per_s']} GB/s), bwd "
+            f"{us['norm_bwd']:.1f} us ({out['gated_rmsnorm']['bwd_GB_per_s']} GB/s); gates fwd "
+            f"{us['gates_fwd']:.1f} us, bwd {us['gates_bwd']:.1f} us")
+        del xn, gn, dyn
         torch.cuda.empty_cache()
 
     if args.only in ("all", "train") and not args.no_cpu_baseline:

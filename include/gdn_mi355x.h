@@ -22,6 +22,7 @@
 #define GDN_MI355X_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -112,12 +113,42 @@ int gdn_short_conv_bwd(const void* x, const float* w, const float* bias, const v
                        void* dx, float* dw, float* dbias, void* dstate_in, void* ws, size_t ws_bytes, int B, int T,
                        int D, int W, int norm_group, int dtype, void* stream);
 
+/* Gated RMSNorm of the op's output, per row of `dim` channels (one head of one token):
+ *   y = x * rsqrt(mean(x^2) + eps) * weight * silu(gate)
+ * Replaces the output normalisation of the mixer: fla's FusedRMSNormGated in GatedDeltaNet and the reference's
+ * self.norm(y) followed by y * F.silu(g) (archbench/layers/nsgdn.py:539-541), as one pass (fp32 arithmetic).
+ * x, gate, y, dy, dx, dgate [rows, dim] in dtype; gate may be NULL (plain RMSNorm; dgate unused); weight [dim]
+ * fp32 or NULL (ones).  dim in {64, 128, 256}.  The backward writes dx, dgate and dweight (if non-NULL; summed
+ * over rows in a fixed order through the workspace). */
+int gdn_gated_rmsnorm_fwd(const void* x, const void* gate, const float* weight, void* y, int64_t rows, int dim,
+                          float eps, int dtype, void* stream);
+int gdn_gated_rmsnorm_bwd_ws_bytes(int64_t rows, int dim, size_t* bytes);
+int gdn_gated_rmsnorm_bwd(const void* x, const void* gate, const float* weight, const void* dy, void* dx,
+                          void* dgate, float* dweight, void* ws, size_t ws_bytes, int64_t rows, int dim, float eps,
+                          int dtype, void* stream);
+
+/* Decay and write-strength gates from their projections, per token and head:
+ *   g    = max(-exp(A_log[h]) * softplus(a + dt_bias[h]), g_min)      (natural-log decay; g_min = -inf: none)
+ *   beta = beta_scale * sigmoid(b + b_bias[h])
+ * Replaces nsgdn.py:531-533 (la = -softplus(ab[:H] + dt_bias) * exp(A_log), clamp_min(la_min), beta =
+ * sigmoid(ab[H:] + b_bias)) and fla GatedDeltaNet's g / beta (beta_scale 2 for allow_neg_eigval).  a, b, da, db
+ * [ntok, H] in dtype; A_log, dt_bias, b_bias [H] fp32 (dt_bias, b_bias may be NULL = 0); g, beta, dg, dbeta
+ * [ntok, H] fp32.  The backward writes da, db and, where non-NULL, dA_log, ddt_bias, db_bias (summed over tokens
+ * in a fixed order through the workspace). */
+int gdn_gates_fwd(const void* a, const void* b, const float* A_log, const float* dt_bias, const float* b_bias,
+                  float* g, float* beta, int64_t ntok, int H, float beta_scale, float g_min, int dtype, void* stream);
+int gdn_gates_bwd_ws_bytes(int64_t ntok, int H, size_t* bytes);
+int gdn_gates_bwd(const void* a, const void* b, const float* A_log, const float* dt_bias, const float* b_bias,
+                  const float* dg, const float* dbeta, void* da, void* db, float* dA_log, float* ddt_bias,
+                  float* db_bias, void* ws, size_t ws_bytes, int64_t ntok, int H, float beta_scale, float g_min,
+                  int dtype, void* stream);
+
 /* Per-stage kernel timing (diagnostic; no counterpart in the reference, which times whole phases with CUDA
  * events in archbench/logger.py:57-81).  While enabled on the calling thread, every kernel the calls above
  * enqueue is bracketed by hipEvents on the same stream.  gdn_profile_read synchronises on those events and
  * returns, per stage, the summed milliseconds and the number of launches (arrays of at least
  * GDN_PROFILE_STAGES entries), then clears the record.  Stage names: gdn_profile_stage_name. */
-#define GDN_PROFILE_STAGES 9
+#define GDN_PROFILE_STAGES 13
 int gdn_profile_enable(int on);
 int gdn_profile_read(double* ms_sum, int* launches, int n_stages);
 const char* gdn_profile_stage_name(int stage);

@@ -1,0 +1,140 @@
+"""Gated RMSNorm and the g / beta gates on the GPU against the CPU oracle (oracle/norm_oracle.py), through the C
+ABI via ops.gated_rmsnorm(_bwd) and ops.gdn_gates(_bwd): fp32 max-abs error <= 1e-4 relative to the output scale,
+bf16 outputs rel-L2 <= 1e-2; ragged row counts, every supported head size, optional gate / weight / biases, the
+clamp and beta scale, the autograd wrappers, and determinism of the parameter-gradient sums."""
+
+import pytest
+import torch
+
+from archbench_amd import ops
+from oracle import norm_oracle as N
+from tests.gpu_util import banner, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _check(got, ref, dtype, what, tol32=1e-4):
+    if dtype == torch.float32:
+        err = max_abs(got, ref) / max(1.0, ref.abs().max().item())
+        assert err <= tol32, f"{what}: max-abs error {err:.3g}"
+    else:
+        err = rel_l2(got, ref)
+        assert err <= 1e-2, f"{what}: rel-L2 error {err:.3g}"
+
+
+NORM_CASES = [(rows, dim, gate, weight) for dim in (64, 128, 256) for rows in (1, 7, 100, 1000)
+              for (gate, weight) in ((True, True), (False, True), (True, False))]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("rows,dim,with_gate,with_weight", NORM_CASES)
+def test_norm_matches_oracle(dtype, rows, dim, with_gate, with_weight):
+    banner(f"gated rmsnorm rows={rows} dim={dim} gate={with_gate} weight={with_weight} {dtype}")
+    x = torch.randn(rows, dim, generator=_g(rows + dim)).to(dtype).float()
+    gate = torch.randn(rows, dim, generator=_g(1)).to(dtype).float() if with_gate else None
+    w = (torch.rand(dim, generator=_g(2)) + 0.5) if with_weight else None
+    dy = torch.randn(rows, dim, generator=_g(3)).to(dtype).float()
+    dev = lambda t, dt=dtype: None if t is None else t.to("cuda", dt)
+    y = ops.gated_rmsnorm(dev(x), dev(gate), dev(w, torch.float32), 1e-5)
+    dx, dgate, dw = ops.gated_rmsnorm_bwd(dev(x), dev(gate), dev(w, torch.float32), dev(dy), 1e-5)
+    torch.cuda.synchronize()
+    _check(y, N.gated_rmsnorm_fwd(x, gate, w, 1e-5), dtype, "y")
+    dx_r, dg_r, dw_r = N.gated_rmsnorm_bwd(x, gate, w, dy, 1e-5)
+    _check(dx, dx_r, dtype, "dx")
+    if with_gate:
+        _check(dgate, dg_r, dtype, "dgate")
+    ref_dw = dw_r if with_weight else N.gated_rmsnorm_bwd(x, gate, torch.ones(dim), dy, 1e-5)[2]
+    _check(dw, ref_dw, torch.float32 if dtype == torch.float32 else dtype, "dweight")
+
+
+def test_norm_autograd_and_layer_shape():
+    """Autograd through the op at the layer's shape (B=2, T=300, H=4, DV=128, bf16), against the oracle."""
+    banner("gated rmsnorm autograd")
+    B, T, H, DV = 2, 300, 4, 128
+    x = torch.randn(B, T, H, DV, generator=_g(4)).bfloat16()
+    gate = torch.randn(B, T, H, DV, generator=_g(5)).bfloat16()
+    w = torch.rand(DV, generator=_g(6)) + 0.5
+    dy = torch.randn(B, T, H, DV, generator=_g(7)).bfloat16()
+    leaves = [t.cuda().requires_grad_() for t in (x, gate, w)]
+    y = ops.gated_rmsnorm(*leaves, 1e-6)
+    y.backward(dy.cuda())
+    ref = N.gated_rmsnorm_bwd(x.float(), gate.float(), w, dy.float(), 1e-6)
+    assert rel_l2(y, N.gated_rmsnorm_fwd(x.float(), gate.float(), w, 1e-6)) <= 1e-2
+    for n, leaf, r in zip(("dx", "dgate", "dw"), leaves, ref):
+        assert rel_l2(leaf.grad, r) <= 1e-2, n
+
+
+def test_norm_large_deterministic():
+    """rows = 8*4096*16 at DV = 128 (the headline shape's output): two backward calls agree bit for bit, and dw
+    matches the oracle computed in fp32 on the CPU."""
+    banner("gated rmsnorm rows=524288 dim=128 determinism")
+    rows, dim = 8 * 4096 * 16, 128
+    x = torch.randn(rows, dim, device="cuda").bfloat16()
+    gate = torch.randn(rows, dim, device="cuda").bfloat16()
+    w = torch.rand(dim, device="cuda") + 0.5
+    dy = torch.randn(rows, dim, device="cuda").bfloat16()
+    r1 = ops.gated_rmsnorm_bwd(x, gate, w, dy, 1e-5)
+    r2 = ops.gated_rmsnorm_bwd(x, gate, w, dy, 1e-5)
+    for a, b in zip(r1, r2):
+        assert torch.equal(a, b)
+    _, _, dw_ref = N.gated_rmsnorm_bwd(x.cpu().float(), gate.cpu().float(), w.cpu(), dy.cpu().float(), 1e-5,
+                                       dtype=torch.float32)
+    assert rel_l2(r1[2], dw_ref) <= 1e-4
+
+
+GATE_CASES = [(ntok, H, biases, scale, gmin) for (ntok, H) in ((1, 6), (100, 16), (5000, 16), (300, 100))
+              for (biases, scale, gmin) in ((True, 1.0, float("-inf")), (False, 2.0, -1.5))]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("ntok,H,biases,beta_scale,g_min", GATE_CASES)
+def test_gates_match_oracle(dtype, ntok, H, biases, beta_scale, g_min):
+    banner(f"gates ntok={ntok} H={H} biases={biases} scale={beta_scale} g_min={g_min} {dtype}")
+    a = (torch.randn(ntok, H, generator=_g(ntok + H)) * 3).to(dtype).float()
+    b = (torch.randn(ntok, H, generator=_g(8)) * 2).to(dtype).float()
+    A_log = torch.rand(H, generator=_g(9)).mul(15).add(1).log()
+    dt_bias = torch.randn(H, generator=_g(10)) if biases else None
+    b_bias = torch.randn(H, generator=_g(11)) if biases else None
+    dg = torch.randn(ntok, H, generator=_g(12))
+    dbeta = torch.randn(ntok, H, generator=_g(13))
+    dev = lambda t, dt=torch.float32: None if t is None else t.to("cuda", dt)
+    g, beta = ops.gdn_gates(dev(a, dtype), dev(b, dtype), dev(A_log), dev(dt_bias), dev(b_bias), beta_scale, g_min)
+    grads = ops.gdn_gates_bwd(dev(a, dtype), dev(b, dtype), dev(A_log), dev(dt_bias), dev(b_bias), dev(dg),
+                              dev(dbeta), beta_scale, g_min)
+    torch.cuda.synchronize()
+    g_r, beta_r = N.gates_fwd(a, b, A_log, dt_bias, b_bias, beta_scale, g_min)
+    _check(g, g_r, torch.float32, "g")
+    _check(beta, beta_r, torch.float32, "beta")
+    ref = N.gates_bwd(a, b, A_log, dt_bias, b_bias, dg, dbeta, beta_scale, g_min)
+    for n, got, r in zip(("da", "db", "dA_log", "ddt_bias", "db_bias"), grads, ref):
+        if r is not None:
+            _check(got, r, dtype if n in ("da", "db") else torch.float32, n, tol32=1e-4)
+
+
+def test_gates_autograd():
+    banner("gates autograd")
+    H = 16
+    a = torch.randn(2, 50, H, generator=_g(14)) * 3
+    b = torch.randn(2, 50, H, generator=_g(15))
+    A_log, dt_bias, b_bias = torch.rand(H, generator=_g(16)), torch.randn(H, generator=_g(17)), torch.zeros(H)
+    dg, dbeta = torch.randn(2, 50, H, generator=_g(18)), torch.randn(2, 50, H, generator=_g(19))
+    leaves = [t.cuda().requires_grad_() for t in (a, b, A_log, dt_bias, b_bias)]
+    g, beta = ops.gdn_gates(*leaves, 1.0, float("-inf"))
+    ((g * dg.cuda()).sum() + (beta * dbeta.cuda()).sum()).backward()
+    ref = N.gates_bwd(a, b, A_log, dt_bias, b_bias, dg, dbeta)
+    for leaf, r in zip(leaves, ref):
+        assert max_abs(leaf.grad, r) <= 1e-4 * max(1.0, r.abs().max().item())
+
+
+def test_norm_and_gates_shape_errors():
+    banner("norm / gates shape errors")
+    x = torch.randn(4, 96, device="cuda")
+    with pytest.raises(ValueError, match="not compiled"):
+        ops.gated_rmsnorm(x, None, None, 1e-5)
+    with pytest.raises(ValueError):
+        ops.gdn_gates(torch.randn(3, 4, device="cuda"), torch.randn(3, 5, device="cuda"),
+                      torch.randn(4, device="cuda"), None, None, 1.0, float("-inf"))
