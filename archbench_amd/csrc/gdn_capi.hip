@@ -116,10 +116,11 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
 // ---- per-stage event timing (diagnostic; off unless gdn_profile_enable(1) was called on this thread) ----
 enum Stage {
   ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_FACTORS, ST_CONV_FWD,
-  ST_CONV_BWD, ST_NORM_FWD, ST_NORM_BWD, ST_GATES_FWD, ST_GATES_BWD, ST_COUNT
+  ST_CONV_BWD, ST_NORM_FWD, ST_NORM_BWD, ST_GATES_FWD, ST_GATES_BWD, ST_L2_FWD, ST_L2_BWD, ST_COUNT
 };
 static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step", "fwd_stash",
-                                            "factors", "conv_fwd", "conv_bwd", "norm_fwd", "norm_bwd", "gates_fwd", "gates_bwd"};
+                                            "factors", "conv_fwd", "conv_bwd", "norm_fwd", "norm_bwd", "gates_fwd", "gates_bwd",
+                                            "l2norm_fwd", "l2norm_bwd"};
 struct ProfRec { int stage; hipEvent_t a, b; };
 struct Prof {
   bool on = false;
@@ -476,6 +477,35 @@ int gdn_gated_rmsnorm_bwd(const void* x, const void* gate, const float* weight, 
   a.rows = rows; a.DV = dim; a.dtype = dtype; a.eps = eps; a.stream = st;
   const hipError_t e = timed(ST_NORM_BWD, st, [&] { return launch_norm(a, true); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "gated RMSNorm backward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+int gdn_l2norm_fwd(const void* x, void* y, int64_t rows, int dim, float eps, float scale, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (int e = norm_check(rows, dim, eps, dtype)) return e;
+  if (rows == 0) return GDN_OK;
+  if (!x || !y) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(x, y)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
+  NormArgs a{};
+  a.x = x; a.y = y; a.rows = rows; a.DV = dim; a.dtype = dtype; a.eps = eps; a.l2 = true; a.scale = scale;
+  a.stream = static_cast<hipStream_t>(stream);
+  const hipError_t e = timed(ST_L2_FWD, a.stream, [&] { return launch_norm(a, false); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "L2 norm forward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+int gdn_l2norm_bwd(const void* x, const void* dy, void* dx, int64_t rows, int dim, float eps, float scale, int dtype,
+                   void* stream) {
+  g_err[0] = 0;
+  if (int e = norm_check(rows, dim, eps, dtype)) return e;
+  if (rows == 0) return GDN_OK;
+  if (!x || !dy || !dx) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(x, dy, dx)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
+  NormArgs a{};
+  a.x = x; a.dy = dy; a.dx = dx; a.rows = rows; a.DV = dim; a.dtype = dtype; a.eps = eps; a.l2 = true;
+  a.scale = scale; a.stream = static_cast<hipStream_t>(stream);
+  const hipError_t e = timed(ST_L2_BWD, a.stream, [&] { return launch_norm(a, true); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "L2 norm backward launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }
 

@@ -91,7 +91,8 @@ struct ColumnOut {
 // out[c] = sum over p < nparts of part[p * ld + c] (c < n[0] + n[1] + n[2]), in a fixed order.
 hipError_t launch_column_sum(const float* part, int64_t nparts, int64_t ld, ColumnOut out, hipStream_t stream);
 
-// Gated RMSNorm over rows of DV channels (x, gate, y, dy, dx, dgate [rows, DV] in dtype; gate may be null).
+// Gated RMSNorm over rows of DV channels (x, gate, y, dy, dx, dgate [rows, DV] in dtype; gate may be null), or
+// with l2 set the scaled L2 normalisation y = scale * x / max(||x||, eps) (no gate, no weight).
 struct NormArgs {
   const void* x;
   const void* gate;
@@ -104,6 +105,8 @@ struct NormArgs {
   int64_t rows;
   int DV, dtype;
   float eps;
+  bool l2;
+  float scale;  // l2 only
   hipStream_t stream;
 };
 bool norm_shape_supported(int DV);

@@ -4,6 +4,8 @@
 //    self.norm(y) * silu(g), archbench/layers/nsgdn.py:539-541), per row of DV channels (one head of one token):
 //      y = x * rsqrt(mean(x^2) + eps) * w * silu(gate)            (gate optional)
 //    forward and backward (dx, dgate, dw), fp32 arithmetic, x / gate / y in the activation dtype;
+//  * L2 normalisation of q and k per head with a scale (nsgdn.py:527-528, F.normalize(.) * DK^-1/2; fla's
+//    use_qk_l2norm_in_kernel):  y = scale * x / max(||x||, eps), forward and backward on the same kernels;
 //  * the gate functions (nsgdn.py:531-533; fla GatedDeltaNet's g and beta):
 //      g    = max(-exp(A_log[h]) * softplus(a + dt_bias[h]), g_min)
 //      beta = beta_scale * sigmoid(b + b_bias[h])
@@ -26,20 +28,24 @@ namespace gdn {
 constexpr int NORM_U = 4;      // row groups per load batch
 constexpr int NORM_WAVES = 4;  // waves per workgroup
 
-template <typename T, int DV, bool GATE>
-__global__ __launch_bounds__(64 * NORM_WAVES) void gated_rmsnorm_fwd_kernel(const T* __restrict__ x,
-                                                                            const T* __restrict__ gate,
-                                                                            const float* __restrict__ w,
-                                                                            T* __restrict__ y, int64_t rows,
-                                                                            float eps) {
+// what a row pass computes
+enum NormMode { RMS = 0, RMS_GATE = 1, L2 = 2 };
+
+template <typename T, int DV, int MODE>
+__global__ __launch_bounds__(64 * NORM_WAVES) void row_norm_fwd_kernel(const T* __restrict__ x,
+                                                                       const T* __restrict__ gate,
+                                                                       const float* __restrict__ w,
+                                                                       T* __restrict__ y, int64_t rows, float eps,
+                                                                       float scale) {
   constexpr int LPR = DV / 8, RPW = 64 / LPR, U = NORM_U;
+  constexpr bool GATE = MODE == RMS_GATE;
   const int l = lane_id();
   const int sub = l / LPR, c0 = (l % LPR) * 8;
   const int64_t row0 = ((int64_t)blockIdx.x * NORM_WAVES + wave_id()) * (RPW * U);
   if (row0 >= rows) return;  // waves never synchronise
   float wk[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) wk[j] = w ? w[c0 + j] : 1.f;
+  for (int j = 0; j < 8; ++j) wk[j] = MODE == L2 ? scale : (w ? w[c0 + j] : 1.f);
   Row8<T> xr[U], gr[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -55,7 +61,8 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void gated_rmsnorm_fwd_kernel(cons
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss += xs[j] * xs[j];
-    const float rs = rsqrtf(lane_group_sum<LPR>(ss) * (1.f / DV) + eps);
+    const float rs = MODE == L2 ? 1.f / fmaxf(sqrtf(lane_group_sum<LPR>(ss)), eps)
+                                : rsqrtf(lane_group_sum<LPR>(ss) * (1.f / DV) + eps);
     if constexpr (GATE) {
       float gs[8];
       gr[u].get(gs);
@@ -72,18 +79,19 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void gated_rmsnorm_fwd_kernel(cons
 // Persistent over batches of NORM_U row groups (wave v takes batches v, v + waves, ...); dw accumulates in
 // registers, then over the rows of a wave (lane shuffles) and the waves of the workgroup (LDS, fixed order) into
 // one partial row per workgroup.
-template <typename T, int DV, bool GATE>
-__global__ __launch_bounds__(64 * NORM_WAVES) void gated_rmsnorm_bwd_kernel(
+template <typename T, int DV, int MODE>
+__global__ __launch_bounds__(64 * NORM_WAVES) void row_norm_bwd_kernel(
     const T* __restrict__ x, const T* __restrict__ gate, const float* __restrict__ w, const T* __restrict__ dy,
-    T* __restrict__ dx, T* __restrict__ dgate, float* __restrict__ dw_part, int64_t rows, float eps) {
+    T* __restrict__ dx, T* __restrict__ dgate, float* __restrict__ dw_part, int64_t rows, float eps, float scale) {
   constexpr int LPR = DV / 8, RPW = 64 / LPR, U = NORM_U;
+  constexpr bool GATE = MODE == RMS_GATE;
   __shared__ float red[NORM_WAVES][DV];
   const int l = lane_id(), wv = wave_id();
   const int sub = l / LPR, c0 = (l % LPR) * 8;
   float wk[8], dwa[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    wk[j] = w ? w[c0 + j] : 1.f;
+    wk[j] = MODE == L2 ? scale : (w ? w[c0 + j] : 1.f);
     dwa[j] = 0.f;
   }
   const int64_t stride = (int64_t)gridDim.x * NORM_WAVES * (RPW * U);
@@ -106,7 +114,11 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void gated_rmsnorm_bwd_kernel(
       float ss = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss += xs[j] * xs[j];
-      const float rs = rsqrtf(lane_group_sum<LPR>(ss) * (1.f / DV) + eps);
+      // RMS: rs = (mean(x^2) + eps)^-1/2, smooth in x.  L2: rs = 1 / max(||x||, eps), constant (no row term in
+      // the gradient) while the norm is below eps
+      const float nrm2 = lane_group_sum<LPR>(ss);
+      const float rs = MODE == L2 ? 1.f / fmaxf(sqrtf(nrm2), eps) : rsqrtf(nrm2 * (1.f / DV) + eps);
+      const float rowterm = MODE == L2 ? (sqrtf(nrm2) > eps ? 1.f : 0.f) : 1.f / DV;
       float xh[8], du[8], dot = 0.f;
       if constexpr (GATE) gr[u].get(gs);
 #pragma unroll
@@ -121,7 +133,7 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void gated_rmsnorm_bwd_kernel(
         du[j] = dyh * wk[j];
         dot += du[j] * xh[j];
       }
-      dot = lane_group_sum<LPR>(dot) * (1.f / DV);
+      dot = lane_group_sum<LPR>(dot) * rowterm;
       float o[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[j] = rs * (du[j] - xh[j] * dot);
@@ -133,6 +145,7 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void gated_rmsnorm_bwd_kernel(
       }
     }
   }
+  if constexpr (MODE == L2) return;  // no parameter gradient (uniform exit: no barrier follows)
   // lanes with the same channels (l mod LPR) hold different rows: butterfly over them
 #pragma unroll
   for (int m = LPR; m < 64; m <<= 1)
@@ -231,37 +244,42 @@ size_t norm_ws_bytes(int64_t rows, int DV) {
 
 bool norm_shape_supported(int DV) { return DV == 64 || DV == 128 || DV == 256; }
 
-template <typename T, int DV, bool GATE>
+template <typename T, int DV, int MODE>
 static hipError_t norm_k(const NormArgs& a, bool backward) {
   if (!backward) {
-    gated_rmsnorm_fwd_kernel<T, DV, GATE><<<dim3(norm_grid_fwd(a.rows, DV)), 64 * NORM_WAVES, 0, a.stream>>>(
-        static_cast<const T*>(a.x), static_cast<const T*>(a.gate), a.w, static_cast<T*>(a.y), a.rows, a.eps);
+    row_norm_fwd_kernel<T, DV, MODE><<<dim3(norm_grid_fwd(a.rows, DV)), 64 * NORM_WAVES, 0, a.stream>>>(
+        static_cast<const T*>(a.x), static_cast<const T*>(a.gate), a.w, static_cast<T*>(a.y), a.rows, a.eps,
+        a.scale);
     return hipGetLastError();
   }
   const int nwg = norm_bwd_workgroups(a.rows, DV);
   float* part = static_cast<float*>(a.ws);
-  gated_rmsnorm_bwd_kernel<T, DV, GATE><<<dim3(nwg), 64 * NORM_WAVES, 0, a.stream>>>(
+  row_norm_bwd_kernel<T, DV, MODE><<<dim3(nwg), 64 * NORM_WAVES, 0, a.stream>>>(
       static_cast<const T*>(a.x), static_cast<const T*>(a.gate), a.w, static_cast<const T*>(a.dy),
-      static_cast<T*>(a.dx), static_cast<T*>(a.dgate), part, a.rows, a.eps);
+      static_cast<T*>(a.dx), static_cast<T*>(a.dgate), part, a.rows, a.eps, a.scale);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || !a.dw) return e;
+  if (e != hipSuccess || MODE == L2 || !a.dw) return e;
   return launch_column_sum(part, nwg, DV, ColumnOut{{a.dw, nullptr, nullptr}, {DV, 0, 0}}, a.stream);
 }
 
-template <typename T, bool GATE>
+template <typename T, int MODE>
 static hipError_t norm_dim(const NormArgs& a, bool backward) {
   switch (a.DV) {
-    case 64: return norm_k<T, 64, GATE>(a, backward);
-    case 128: return norm_k<T, 128, GATE>(a, backward);
-    case 256: return norm_k<T, 256, GATE>(a, backward);
+    case 64: return norm_k<T, 64, MODE>(a, backward);
+    case 128: return norm_k<T, 128, MODE>(a, backward);
+    case 256: return norm_k<T, 256, MODE>(a, backward);
   }
   return hipErrorInvalidValue;
 }
 
+template <typename T>
+static hipError_t norm_mode(const NormArgs& a, bool backward) {
+  if (a.l2) return norm_dim<T, L2>(a, backward);
+  return a.gate ? norm_dim<T, RMS_GATE>(a, backward) : norm_dim<T, RMS>(a, backward);
+}
+
 hipError_t launch_norm(const NormArgs& a, bool backward) {
-  const bool gate = a.gate != nullptr;
-  if (a.dtype == DT_BF16) return gate ? norm_dim<bf16, true>(a, backward) : norm_dim<bf16, false>(a, backward);
-  return gate ? norm_dim<float, true>(a, backward) : norm_dim<float, false>(a, backward);
+  return a.dtype == DT_BF16 ? norm_mode<bf16>(a, backward) : norm_mode<float>(a, backward);
 }
 
 static int gates_tile_tokens(int H) { return std::max(1, GATE_TILE / H); }

@@ -36,13 +36,12 @@ import os
 from typing import Optional
 
 import torch
-import torch.nn.functional as F
 from torch import Tensor
 
 from . import _lib
 
 __all__ = ["chunk_gated_delta_rule", "fused_recurrent_gated_delta_rule", "recurrent_step", "chunk_fwd",
-           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "short_conv", "gated_rmsnorm", "gdn_gates"]
+           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "short_conv", "gated_rmsnorm", "l2norm", "gdn_gates"]
 
 
 def _require_gpu(*ts: Optional[Tensor]) -> None:
@@ -426,6 +425,59 @@ def _norm_backward(ctx, dy):
 gated_rmsnorm.register_autograd(_norm_backward, setup_context=_norm_setup)
 
 
+# ---------------------------------------------------------------------------------------------------- L2 norm
+# y = scale * x / max(||x||, eps) over the last dimension: the per-head q / k normalisation (nsgdn.py:527-528,
+# F.normalize(.) * DK^-1/2) where it is not fused into the short convolution.
+@torch.library.custom_op("archbench_amd::l2norm", mutates_args=())
+def l2norm(x: Tensor, eps: float, scale: float) -> Tensor:
+    _require_gpu(x)
+    rows, dim = _norm_rows(x, None, None)
+    lib = _lib.load()
+    x = _arg(x)
+    y = torch.empty_like(x)
+    rc = lib.gdn_l2norm_fwd(_lib.ptr(x), _lib.ptr(y), rows, dim, float(eps), float(scale), _lib.dtype_code(x.dtype),
+                            _lib.stream_ptr(x.device))
+    _lib.check(rc, "gdn_l2norm_fwd")
+    return y
+
+
+@l2norm.register_fake
+def _(x, eps, scale):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("archbench_amd::l2norm_bwd", mutates_args=())
+def l2norm_bwd(x: Tensor, dy: Tensor, eps: float, scale: float) -> Tensor:
+    _require_gpu(x, dy)
+    rows, dim = _norm_rows(x, None, None)
+    lib = _lib.load()
+    x, dy = _arg(x), _arg(dy, x.dtype)
+    dx = torch.empty_like(x)
+    rc = lib.gdn_l2norm_bwd(_lib.ptr(x), _lib.ptr(dy), _lib.ptr(dx), rows, dim, float(eps), float(scale),
+                            _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device))
+    _lib.check(rc, "gdn_l2norm_bwd")
+    return dx
+
+
+@l2norm_bwd.register_fake
+def _(x, dy, eps, scale):
+    return torch.empty_like(x)
+
+
+def _l2_setup(ctx, inputs, output):
+    x, eps, scale = inputs
+    ctx.save_for_backward(x)
+    ctx.eps, ctx.scale = eps, scale
+
+
+def _l2_backward(ctx, dy):
+    (x,) = ctx.saved_tensors
+    return l2norm_bwd(x, dy, ctx.eps, ctx.scale), None, None
+
+
+l2norm.register_autograd(_l2_backward, setup_context=_l2_setup)
+
+
 # ------------------------------------------------------------------------------------------------------ gates
 # g = max(-exp(A_log) * softplus(a + dt_bias), g_min) and beta = beta_scale * sigmoid(b + b_bias) per token and
 # head (nsgdn.py:531-533; fla GatedDeltaNet's g and beta), one pass forward and one backward.
@@ -546,7 +598,8 @@ def _(q, k, v, g, beta, state, scale):
 
 # ----------------------------------------------------------------------------------------------- public API
 def _l2norm(x: Tensor) -> Tensor:
-    return F.normalize(x.float(), dim=-1).to(x.dtype)
+    """F.normalize over the last dimension (eps 1e-12) on the HIP row-norm kernel."""
+    return l2norm(x, 1e-12, 1.0)
 
 
 def chunk_gated_delta_rule(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, scale: float | None = None,

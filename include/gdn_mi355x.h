@@ -127,6 +127,15 @@ int gdn_gated_rmsnorm_bwd(const void* x, const void* gate, const float* weight, 
                           void* dgate, float* dweight, void* ws, size_t ws_bytes, int64_t rows, int dim, float eps,
                           int dtype, void* stream);
 
+/* L2 normalisation with a scale over rows of `dim` channels (one head of q or k):
+ *   y = scale * x / max(||x||, eps)
+ * Replaces the per-head normalisation of q and k (archbench/layers/nsgdn.py:527-528: F.normalize(.) * DK^-1/2,
+ * and fla's use_qk_l2norm_in_kernel) where it is not fused into the short convolution.  x, y, dy, dx [rows, dim]
+ * in dtype; dim in {64, 128, 256}; no workspace (no parameters). */
+int gdn_l2norm_fwd(const void* x, void* y, int64_t rows, int dim, float eps, float scale, int dtype, void* stream);
+int gdn_l2norm_bwd(const void* x, const void* dy, void* dx, int64_t rows, int dim, float eps, float scale, int dtype,
+                   void* stream);
+
 /* Decay and write-strength gates from their projections, per token and head:
  *   g    = max(-exp(A_log[h]) * softplus(a + dt_bias[h]), g_min)      (natural-log decay; g_min = -inf: none)
  *   beta = beta_scale * sigmoid(b + b_bias[h])
@@ -148,7 +157,7 @@ int gdn_gates_bwd(const void* a, const void* b, const float* A_log, const float*
  * enqueue is bracketed by hipEvents on the same stream.  gdn_profile_read synchronises on those events and
  * returns, per stage, the summed milliseconds and the number of launches (arrays of at least
  * GDN_PROFILE_STAGES entries), then clears the record.  Stage names: gdn_profile_stage_name. */
-#define GDN_PROFILE_STAGES 13
+#define GDN_PROFILE_STAGES 15
 int gdn_profile_enable(int on);
 int gdn_profile_read(double* ms_sum, int* launches, int n_stages);
 const char* gdn_profile_stage_name(int stage);

@@ -13,11 +13,13 @@ What it restates (reference file:line, paths relative to the archbench tree):
 * ``gates_fwd`` -- ``la = -softplus(ab[..., :H] + dt_bias) * exp(A_log)``, ``la.clamp_min(la_min)``,
   ``beta = sigmoid(ab[..., H:] + b_bias)`` (nsgdn.py:531-534), with fla GatedDeltaNet's ``beta * 2`` option
   (allow_neg_eigval) as ``beta_scale``.  softplus is log(1 + e^x), and x itself above 20 (torch's threshold).
+* ``l2norm_fwd`` -- the per-head normalisation of q and k, ``F.normalize(.) * DK**-0.5`` (nsgdn.py:527-528):
+  scale * x / max(||x||, eps).
 * ``*_bwd`` -- gradients of the above by autograd in the oracle's dtype.
 
 Parity status: pinned in tests/test_norm_oracle.py against torch's own F.rms_norm / F.silu / F.softplus /
-torch.sigmoid composition (the reference's code path), closed forms (constant rows, unit weight, zero gate),
-scale invariance of the norm, and fp64 gradcheck.
+torch.sigmoid / F.normalize composition (the reference's code path), closed forms (constant rows, unit weight,
+zero gate, unit-norm rows), scale invariance of the norms, and fp64 gradcheck.
 """
 
 from __future__ import annotations
@@ -71,3 +73,15 @@ def gates_bwd(a, b, A_log, dt_bias, b_bias, dg, dbeta, beta_scale: float = 1.0, 
     g, beta = gates_fwd(*leaves, beta_scale=beta_scale, g_min=g_min, dtype=dtype)
     (g * dg.to("cpu", dtype) + beta * dbeta.to("cpu", dtype)).sum().backward()
     return tuple(None if t is None else t.grad for t in leaves)
+
+
+def l2norm_fwd(x, eps: float = 1e-12, scale: float = 1.0, dtype=torch.float64):
+    """scale * x / max(||x||, eps) over the last dimension (F.normalize, nsgdn.py:527-528)."""
+    x = x.to("cpu", dtype)
+    return scale * x / torch.clamp(x.norm(dim=-1, keepdim=True), min=eps)
+
+
+def l2norm_bwd(x, dy, eps: float = 1e-12, scale: float = 1.0, dtype=torch.float64):
+    xs = x.detach().to("cpu", dtype).requires_grad_()
+    (l2norm_fwd(xs, eps, scale, dtype) * dy.to("cpu", dtype)).sum().backward()
+    return xs.grad

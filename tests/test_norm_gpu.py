@@ -138,3 +138,41 @@ def test_norm_and_gates_shape_errors():
     with pytest.raises(ValueError):
         ops.gdn_gates(torch.randn(3, 4, device="cuda"), torch.randn(3, 5, device="cuda"),
                       torch.randn(4, device="cuda"), None, None, 1.0, float("-inf"))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("rows,dim", [(1, 64), (37, 128), (1000, 256), (4099, 128)])
+def test_l2norm_matches_oracle(dtype, rows, dim):
+    banner(f"l2norm rows={rows} dim={dim} {dtype}")
+    x = torch.randn(rows, dim, generator=_g(rows)).to(dtype).float()
+    x[0] *= 1e-4  # a row whose norm is below eps = 1e-2: divided by eps, gradient without the row term
+    dy = torch.randn(rows, dim, generator=_g(22)).to(dtype).float()
+    eps, scale = 1e-2, dim ** -0.5
+    y = ops.l2norm(x.to("cuda", dtype), eps, scale)
+    dx = ops.l2norm_bwd(x.to("cuda", dtype), dy.to("cuda", dtype), eps, scale)
+    torch.cuda.synchronize()
+    _check(y, N.l2norm_fwd(x, eps, scale), dtype, "y")
+    _check(dx, N.l2norm_bwd(x, dy, eps, scale), dtype, "dx")
+    if dtype == torch.float32:
+        assert max_abs(y[0], N.l2norm_fwd(x[:1], eps, scale)[0]) <= 1e-6
+
+
+def test_op_l2norm_in_kernel_path():
+    """chunk_gated_delta_rule(use_qk_l2norm_in_kernel=True) normalises q and k on the HIP kernel before the op:
+    equal to normalising first with the oracle and calling the op, values and gradients."""
+    banner("chunk op with use_qk_l2norm_in_kernel")
+    B, T, H, K, V = 1, 100, 2, 64, 64
+    q, k = (torch.randn(B, T, H, K, generator=_g(s)) for s in (23, 24))
+    v = torch.randn(B, T, H, V, generator=_g(25))
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=_g(26)) + 4)
+    beta = torch.rand(B, T, H, generator=_g(27))
+    do = torch.randn(B, T, H, V, generator=_g(28))
+    lq, lk = (t.cuda().requires_grad_() for t in (q, k))
+    o1, _ = ops.chunk_gated_delta_rule(lq, lk, v.cuda(), g.cuda(), beta.cuda(), use_qk_l2norm_in_kernel=True)
+    o1.backward(do.cuda())
+    rq, rk = (t.clone().requires_grad_() for t in (q, k))
+    nq, nk = (N.l2norm_fwd(t, 1e-12, 1.0, dtype=torch.float32) for t in (rq, rk))
+    o2, _ = ops.chunk_gated_delta_rule(nq.cuda(), nk.cuda(), v.cuda(), g.cuda(), beta.cuda())
+    o2.backward(do.cuda())
+    assert max_abs(o1, o2) <= 1e-4
+    assert max_abs(lq.grad, rq.grad) <= 1e-4 and max_abs(lk.grad, rk.grad) <= 1e-4

@@ -95,3 +95,18 @@ def test_gates_gradients():
     g_unc = -F.softplus(a + dt_bias) * A_log.exp()
     want = torch.where(g_unc >= -2.0, g_unc * dg, torch.zeros_like(dg)).sum((0, 1))
     torch.testing.assert_close(got[2], want)
+
+
+def test_l2norm_matches_normalize():
+    x = torch.randn(3, 4, 128, generator=_g(20), dtype=torch.float64)
+    torch.testing.assert_close(N.l2norm_fwd(x, 1e-12, 128 ** -0.5), F.normalize(x, dim=-1) * 128 ** -0.5)  # :527
+    # unit rows unchanged at scale 1; rows below eps are divided by eps, not by their norm
+    u = F.normalize(x, dim=-1)
+    torch.testing.assert_close(N.l2norm_fwd(u), u)
+    tiny = torch.full((1, 64), 1e-8, dtype=torch.float64)
+    torch.testing.assert_close(N.l2norm_fwd(tiny, 1e-3), tiny / 1e-3)
+    # gradient: orthogonal to x for rows above eps (the projection (I - x x^T / |x|^2) / |x|)
+    dy = torch.randn(3, 4, 128, generator=_g(21), dtype=torch.float64)
+    dx = N.l2norm_bwd(x, dy)
+    assert (dx * x).sum(-1).abs().max() < 1e-12
+    assert torch.autograd.gradcheck(lambda a: N.l2norm_fwd(a, 1e-12, 0.5), (x[:1, :1].clone().requires_grad_(),))
