@@ -36,6 +36,9 @@ SIGNATURES = {
     "gdn_chunk_fwd_stash": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_chunk_bwd_stashed": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _sz,
                                    _i, _i, _i, _i, _i, _f, _i, _p]),
+    "gdn_nsgdn_chunk_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _f, _i, _p]),
+    "gdn_nsgdn_chunk_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _sz,
+                                 _i, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_recurrent_step": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_short_conv_fwd": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "gdn_short_conv_bwd_ws_bytes": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),

@@ -239,10 +239,11 @@ int gdn_chunk_stash_bytes(int B, int T, int H, int K, int V, int dtype, size_t* 
 
 namespace gdn {
 
-// Forward: o and hT, and with `stash` the per-chunk intermediates for gdn_chunk_bwd_stashed.
-static int chunk_fwd_impl(const void* q, const void* k, const void* v, const float* g, const float* beta,
-                          const float* h0, void* o, float* hT, void* ws, size_t ws_bytes, int B, int T, int H,
-                          int K, int V, float scale, int dtype, void* stream, bool stash) {
+// Forward: o and hT, and with `stash` the per-chunk intermediates for gdn_chunk_bwd_stashed.  With write keys u
+// (non-null) beta may be null.
+static int chunk_fwd_impl(const void* q, const void* k, const void* u, const void* v, const float* g,
+                          const float* beta, const float* h0, void* o, float* hT, void* ws, size_t ws_bytes, int B,
+                          int T, int H, int K, int V, float scale, int dtype, void* stream, bool stash) {
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!chunk_shape_supported(K, V, dtype))
@@ -254,14 +255,16 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* v, const flo
     if (copy_or_zero(h0, hT, nstate, st) != hipSuccess) return fail(GDN_ERR_LAUNCH, "state copy launch failed");
     return GDN_OK;
   }
-  if (!q || !k || !v || !g || !beta || !o) return fail(GDN_ERR_ARG, "null input/output pointer");
-  if (misaligned(q, k, v, g, beta, h0, o, hT, ws)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
+  if (!q || !k || !v || !g || (!beta && !u) || !o) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (u && dtype != DT_BF16) return fail(GDN_ERR_SHAPE, "separate write keys are compiled for bf16 only");
+  if (misaligned(q, k, u, v, g, beta, h0, o, hT, ws))
+    return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   ChunkArgs a{};
   const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, stash ? WS_STASH : WS_FACT, &a.ws, ws);
   if (!ws || ws_bytes < need)
     return fail(GDN_ERR_WORKSPACE, "%s of %zu bytes needed, %zu given", stash ? "stash" : "workspace", need,
                 ws ? ws_bytes : (size_t)0);
-  a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.h0 = h0; a.o = o; a.hT = hT;
+  a.q = q; a.k = k; a.u = u; a.v = v; a.g = g; a.beta = beta; a.h0 = h0; a.o = o; a.hT = hT;
   a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
   hipError_t e = timed(ST_FACTORS, st, [&] { return launch_factors(a); });
@@ -272,12 +275,13 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* v, const flo
   return GDN_OK;
 }
 
-// Backward; without `stashed` the per-chunk intermediates are recomputed first.
-static int chunk_bwd_impl(const void* q, const void* k, const void* v, const float* g, const float* beta,
-                          const float* h0, const void* dout, const float* dhT, void* dq, void* dk, void* dv,
-                          float* dg, float* dbeta, float* dh0, const void* stash, size_t stash_bytes, void* ws,
-                          size_t ws_bytes, int B, int T, int H, int K, int V, float scale, int dtype, void* stream,
-                          bool stashed) {
+// Backward; without `stashed` the per-chunk intermediates are recomputed first.  With write keys u (non-null)
+// du is written apart from dk, and beta / dbeta may be null.
+static int chunk_bwd_impl(const void* q, const void* k, const void* u, const void* v, const float* g,
+                          const float* beta, const float* h0, const void* dout, const float* dhT, void* dq, void* dk,
+                          void* du, void* dv, float* dg, float* dbeta, float* dh0, const void* stash,
+                          size_t stash_bytes, void* ws, size_t ws_bytes, int B, int T, int H, int K, int V,
+                          float scale, int dtype, void* stream, bool stashed) {
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!chunk_shape_supported(K, V, dtype))
@@ -289,9 +293,11 @@ static int chunk_bwd_impl(const void* q, const void* k, const void* v, const flo
     if (copy_or_zero(dhT, dh0, nstate, st) != hipSuccess) return fail(GDN_ERR_LAUNCH, "state copy launch failed");
     return GDN_OK;
   }
-  if (!q || !k || !v || !g || !beta || !dout || !dq || !dk || !dv || !dg || !dbeta)
+  if (!q || !k || !v || !g || !dout || !dq || !dk || !dv || !dg || (u ? !du : (!beta || !dbeta)))
     return fail(GDN_ERR_ARG, "null input/output pointer");
-  if (misaligned(q, k, v, g, beta, h0, dout, dhT, dq, dk, dv, dg, dbeta, dh0, stash, ws))
+  if (u && !stashed) return fail(GDN_ERR_ARG, "separate write keys: the backward needs the forward's stash");
+  if (u && dtype != DT_BF16) return fail(GDN_ERR_SHAPE, "separate write keys are compiled for bf16 only");
+  if (misaligned(q, k, u, v, g, beta, h0, dout, dhT, dq, dk, du, dv, dg, dbeta, dh0, stash, ws))
     return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   ChunkArgs a{};
   if (stashed) {
@@ -305,8 +311,8 @@ static int chunk_bwd_impl(const void* q, const void* k, const void* v, const flo
   const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, parts, &a.ws, ws);
   if (!ws || ws_bytes < need)
     return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
-  a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.h0 = h0;
-  a.dout = dout; a.dhT = dhT; a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dh0 = dh0;
+  a.q = q; a.k = k; a.u = u; a.v = v; a.g = g; a.beta = beta; a.h0 = h0;
+  a.dout = dout; a.dhT = dhT; a.dq = dq; a.dk = dk; a.du = du; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dh0 = dh0;
   a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
   hipError_t e = hipSuccess;
@@ -327,22 +333,23 @@ extern "C" {
 int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
                   const float* h0, void* o, float* hT, void* ws, size_t ws_bytes, int B, int T, int H, int K,
                   int V, float scale, int dtype, void* stream) {
-  return chunk_fwd_impl(q, k, v, g, beta, h0, o, hT, ws, ws_bytes, B, T, H, K, V, scale, dtype, stream, false);
+  return chunk_fwd_impl(q, k, nullptr, v, g, beta, h0, o, hT, ws, ws_bytes, B, T, H, K, V, scale, dtype, stream,
+                        false);
 }
 
 int gdn_chunk_fwd_stash(const void* q, const void* k, const void* v, const float* g, const float* beta,
                         const float* h0, void* o, float* hT, void* stash, size_t stash_bytes, int B, int T, int H,
                         int K, int V, float scale, int dtype, void* stream) {
-  return chunk_fwd_impl(q, k, v, g, beta, h0, o, hT, stash, stash_bytes, B, T, H, K, V, scale, dtype, stream,
-                        true);
+  return chunk_fwd_impl(q, k, nullptr, v, g, beta, h0, o, hT, stash, stash_bytes, B, T, H, K, V, scale, dtype,
+                        stream, true);
 }
 
 int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
                   const float* h0, const void* dout, const float* dhT, void* dq, void* dk, void* dv, float* dg,
                   float* dbeta, float* dh0, void* ws, size_t ws_bytes, int B, int T, int H, int K, int V,
                   float scale, int dtype, void* stream) {
-  return chunk_bwd_impl(q, k, v, g, beta, h0, dout, dhT, dq, dk, dv, dg, dbeta, dh0, nullptr, 0, ws, ws_bytes, B,
-                        T, H, K, V, scale, dtype, stream, false);
+  return chunk_bwd_impl(q, k, nullptr, v, g, beta, h0, dout, dhT, dq, dk, nullptr, dv, dg, dbeta, dh0, nullptr, 0,
+                        ws, ws_bytes, B, T, H, K, V, scale, dtype, stream, false);
 }
 
 int gdn_chunk_bwd_stashed(const void* q, const void* k, const void* v, const float* g, const float* beta,
@@ -350,8 +357,31 @@ int gdn_chunk_bwd_stashed(const void* q, const void* k, const void* v, const flo
                           float* dg, float* dbeta, float* dh0, const void* stash, size_t stash_bytes, void* ws,
                           size_t ws_bytes, int B, int T, int H, int K, int V, float scale, int dtype,
                           void* stream) {
-  return chunk_bwd_impl(q, k, v, g, beta, h0, dout, dhT, dq, dk, dv, dg, dbeta, dh0, stash, stash_bytes, ws,
-                        ws_bytes, B, T, H, K, V, scale, dtype, stream, true);
+  return chunk_bwd_impl(q, k, nullptr, v, g, beta, h0, dout, dhT, dq, dk, nullptr, dv, dg, dbeta, dh0, stash,
+                        stash_bytes, ws, ws_bytes, B, T, H, K, V, scale, dtype, stream, true);
+}
+
+int gdn_nsgdn_chunk_fwd(const void* q, const void* k, const void* u, const void* v, const float* la,
+                        const float* h0, void* y, float* hT, void* stash, size_t stash_bytes, int B, int T, int H,
+                        int K, int V, float scale, int dtype, void* stream) {
+  if (!u) {
+    g_err[0] = 0;
+    return fail(GDN_ERR_ARG, "null input/output pointer");
+  }
+  return chunk_fwd_impl(q, k, u, v, la, nullptr, h0, y, hT, stash, stash_bytes, B, T, H, K, V, scale, dtype,
+                        stream, true);
+}
+
+int gdn_nsgdn_chunk_bwd(const void* q, const void* k, const void* u, const void* v, const float* la,
+                        const float* h0, const void* dy, const float* dhT, void* dq, void* dk, void* du, void* dv,
+                        float* dla, float* dh0, const void* stash, size_t stash_bytes, void* ws, size_t ws_bytes,
+                        int B, int T, int H, int K, int V, float scale, int dtype, void* stream) {
+  if (!u) {
+    g_err[0] = 0;
+    return fail(GDN_ERR_ARG, "null input/output pointer");
+  }
+  return chunk_bwd_impl(q, k, u, v, la, nullptr, h0, dy, dhT, dq, dk, du, dv, dla, nullptr, dh0, stash,
+                        stash_bytes, ws, ws_bytes, B, T, H, K, V, scale, dtype, stream, true);
 }
 
 int gdn_short_conv_bwd_ws_bytes(int B, int T, int D, int W, size_t* bytes) {

@@ -22,6 +22,11 @@
 //     dg  = reverse chunk-local cumsum of dG
 //   (fla's chunk_bwd_dv_local + chunk_bwd_dqkwg, the WY backward of nsgdn.py:279-330 and the reverse cumsum
 //   of nsgdn.py:381, fused per chunk.)  Reductions are deterministic: no atomics anywhere.
+//
+// SEPU (separate write keys U, the n-step family's nsgdn_chunk_bwd, nsgdn.py:369-382): U replaces K wherever K
+// is a write key -- Kd dS_C in dR, the column side of K K^T and Q K^T, and the state update -- and the
+// gradients split into dk (read: beta gamma Tm^T dW + D U) and du (write: dte R dS_C^T + (dP o sE)^T Q + D^T K);
+// beta may be absent (row scale 1, no dbeta).
 #include "gdn_chunk_common.h"
 #include "gdn_launch.h"
 
@@ -34,9 +39,10 @@ namespace gdn {
 constexpr int SW = 2 * NWAVE;  // waves of the reverse sweep
 constexpr int STH = 64 * SW;
 
-template <typename T, int K, int BV>
+template <typename T, int K, int BV, bool SEPU>
 __global__ __launch_bounds__(STH) void bwd_state_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ dout, const float* __restrict__ beta,
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u, const T* __restrict__ dout,
+    const float* __restrict__ beta,
     const T* __restrict__ gTm, const T* __restrict__ gP, const float* __restrict__ gGc,
     const float* __restrict__ dhT, float* __restrict__ dh0, T* __restrict__ wsdH, T* __restrict__ wsdR, int T_,
     int H, int V, int NT, float scale) {
@@ -47,6 +53,8 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
   static_assert(BV / 16 / NWAVE == 1, "each wave pair owns one 16-column slab of dS");
   using F = typename Frag<T>::type;
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
+  __shared__ __attribute__((aligned(16))) T sU_[SEPU ? CH * LK : 8];
+  T* sU = SEPU ? sU_ : sK;  // write keys
   __shared__ __attribute__((aligned(16))) T sQ[CH * LK];
   __shared__ __attribute__((aligned(16))) T sdO[CH * LV];  // dO rows of this V block
   __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
@@ -69,7 +77,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
-  RegTile<T, CH, K, STH> rk, rq;
+  RegTile<T, CH, K, STH> rk, rq, ru;
   RegTile<T, CH, BV, STH> rdo;
   RegTile<T, CH, CH, STH> rtm, rp;
   float pG = 0.f, pB = 0.f;
@@ -79,6 +87,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     const int64_t row0 = row0_of(c);
     const int nv = nvalid_of(c);
     rk.load(k + row0 * K, (int64_t)H * K, nv, tid);
+    if constexpr (SEPU) ru.load(u + row0 * K, (int64_t)H * K, nv, tid);
     rq.load(q + row0 * K, (int64_t)H * K, nv, tid);
     rdo.load(dout + row0 * V + v0, (int64_t)H * V, nv, tid);
   };
@@ -89,7 +98,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     rp.load(gP + cidx * CH * CH, (int64_t)CH, CH, tid);
     if (w == 0) {
       pG = gGc[cidx * CH + l];
-      pB = l < nv ? beta[row0 + (int64_t)l * H] : 0.f;
+      pB = l < nv ? (beta ? beta[row0 + (int64_t)l * H] : 1.f) : 0.f;
     }
   };
 
@@ -103,6 +112,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
   auto chunk = [&](int c) {
     const int64_t cidx = (int64_t)bh * NT + c;
     rk.store(sK, LK, tid);
+    if constexpr (SEPU) ru.store(sU, LK, tid);
     rq.store(sQ, LK, tid);
     rdo.store(sdO, LV, tid);
     rtm.store(sTm, LC, tid);
@@ -115,7 +125,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     __syncthreads();
     if (c > 0) prefetch(c - 1);
 
-    // dS leaving the chunk -> dh (fragment layout); partial K dS over this half's rows, for all tokens
+    // dS leaving the chunk -> dh (fragment layout); partial U dS over this half's rows, for all tokens
     const float GC = sG[CH - 1];
     F dSb[NSH];
 #pragma unroll
@@ -128,7 +138,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     for (int rt_ = 0; rt_ < 4; ++rt_) {
       kd[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < NSH; ++s) mma(kd[rt_], frag_kc_perm(sK, LK, 16 * rt_, k0 + 32 * s), dSb[s]);
+      for (int s = 0; s < NSH; ++s) mma(kd[rt_], frag_kc_perm(sU, LK, 16 * rt_, k0 + 32 * s), dSb[s]);
     }
     // (values are selected by the half, never indexed by it: registers cannot be indexed at run time)
     xKd[w][0][l] = hf ? kd[0] : kd[2];  // the other half's token rows
@@ -218,13 +228,14 @@ __device__ __forceinline__ float colsum_tile(const f32x4& x) {
 constexpr int IW = 2 * NWAVE;  // waves of the intra kernel
 constexpr int ITH = IW * 64;   // its threads
 
-template <typename T, int K, int V, int VS>
+template <typename T, int K, int V, int VS, bool SEPU>
 __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const float* __restrict__ beta,
-    const T* __restrict__ dout, const T* __restrict__ wsTm, const float* __restrict__ wsGc,
-    const T* __restrict__ wsH, const T* __restrict__ wsR, const T* __restrict__ wsdH, const T* __restrict__ wsdR,
-    T* __restrict__ dq, T* __restrict__ dk, T* __restrict__ dv, float* __restrict__ dg,
-    float* __restrict__ dbeta, int T_, int H, int NT, float scale) {
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u, const T* __restrict__ v,
+    const float* __restrict__ beta, const T* __restrict__ dout, const T* __restrict__ wsTm,
+    const float* __restrict__ wsGc, const T* __restrict__ wsH, const T* __restrict__ wsR,
+    const T* __restrict__ wsdH, const T* __restrict__ wsdR, T* __restrict__ dq, T* __restrict__ dk,
+    T* __restrict__ du, T* __restrict__ dv, float* __restrict__ dg, float* __restrict__ dbeta, int T_, int H,
+    int NT, float scale) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LS = VS + PT;
   constexpr int NKT = K / 16;   // column tiles over K
@@ -237,6 +248,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   constexpr int SLAB = SLAB_V > SLAB_K ? SLAB_V : SLAB_K;
   __shared__ __attribute__((aligned(16))) T sQ[CH * LK];
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
+  __shared__ __attribute__((aligned(16))) T sU_[SEPU ? CH * LK : 8];
+  T* sU = SEPU ? sU_ : sK;  // write keys
   __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
   __shared__ __attribute__((aligned(16))) T slab[SLAB];
   __shared__ __attribute__((aligned(16))) T sdv[CH * LS];  // dv of the current slab, for the coalesced store
@@ -263,7 +276,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   // V slab in two groups: A = {dO, V, R, dR} (and Tm, G, beta first) feeds dO R^T, dR V^T and Tm^T dR; B =
   // {S0, dS_C} feeds the products with the states.  Group B and Q, K stay in flight while group A is computed,
   // and the next slab's groups are issued as soon as their registers are free.
-  RegTile<T, CH, K, ITH> tq, tk;
+  RegTile<T, CH, K, ITH> tq, tk, tu;
   RegTile<T, CH, CH, ITH> rtm;
   RegTile<T, CH, VS, ITH> rdo, rv;
   FragTile<T, CH, VS, ITH> rr, rdr;
@@ -279,12 +292,13 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     rdsc.load(wsdH + cidx * K * V, V / 16, vs / 16, tid);
   };
   const float pg = wsGc[cidx * CH + (tid & (CH - 1))];
-  const float pb = beta[row0 + (int64_t)((tid & (CH - 1)) < nvalid ? (tid & (CH - 1)) : 0) * H];
+  const float pb = beta ? beta[row0 + (int64_t)((tid & (CH - 1)) < nvalid ? (tid & (CH - 1)) : 0) * H] : 1.f;
   rtm.load(wsTm + cidx * CH * CH, (int64_t)CH, CH, tid);
   load_a(0);
   load_b(0);
   tq.load(q + row0 * K, (int64_t)H * K, nvalid, tid);
   tk.load(k + row0 * K, (int64_t)H * K, nvalid, tid);
+  if constexpr (SEPU) tu.load(u + row0 * K, (int64_t)H * K, nvalid, tid);
   if (tid < CH) {
     sG[tid] = pg;
     sB[tid] = tid < nvalid ? pb : 0.f;
@@ -334,6 +348,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     if (vs == 0) {
       tq.store(sQ, LK, tid);
       tk.store(sK, LK, tid);
+      if constexpr (SEPU) tu.store(sU, LK, tid);
     }
     __syncthreads();
     if (vs + VS < V) load_b(vs + VS);
@@ -385,7 +400,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rb + acc_row(i), d = 16 * (HK * hf + j) + acc_col();
       rq[i] += aQg[j][i] * to_f(sQ[r * LK + d]);
-      rk[i] += aKd[j][i] * to_f(sK[r * LK + d]);
+      rk[i] += aKd[j][i] * to_f(sU[r * LK + d]);
       sdWn[r * LK + d] = from_f<T>(aWn[j][i]);
     }
   }
@@ -438,8 +453,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     const int n = HC * hf + j;
     f32x4 da = {0.f, 0.f, 0.f, 0.f}, kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
     mma_blk<false, false, CH>(da, sTm, LC, 16 * rb, sM1, LC, 16 * n);
-    mma_blk<true, true, K>(kk, sK, LK, 16 * rb, sK, LK, 16 * n);
-    mma_blk<true, true, K>(qk, sQ, LK, 16 * rb, sK, LK, 16 * n);
+    mma_blk<true, true, K>(kk, sK, LK, 16 * rb, sU, LK, 16 * n);
+    mma_blk<true, true, K>(qk, sQ, LK, 16 * rb, sU, LK, 16 * n);
     f32x4 z;
     const int cc = 16 * n + acc_col();
     const float Gc = sG[cc];
@@ -489,30 +504,49 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   T* sdq = sdWn;
   T* sdk = sdTm;
   static_assert(CH * LK <= 2 * CH * LC, "dk staging must fit in the dTm and M1 regions");
-  // dq = s gamma dQg + dPm K
+  // dq = s gamma dQg + dPm U
 #pragma unroll
   for (int j = 0; j < HK; ++j) {
     const int n = HK * hf + j;
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<true, false, CH>(t, sdPm, LC, 16 * rb, sK, LK, 16 * n);
+    mma_blk<true, false, CH>(t, sdPm, LC, 16 * rb, sU, LK, 16 * n);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
       sdq[r * LK + d] = from_f<T>(scale * gam[i] * aQg[j][i] + t[i]);
     }
   }
-  // dk = dte dKd + dPm^T Q + beta gamma dX + D K + D^T K
+  if constexpr (!SEPU) {
+    // dk = dte dKd + dPm^T Q + beta gamma dX + D K + D^T K
 #pragma unroll
-  for (int j = 0; j < HK; ++j) {
-    const int n = HK * hf + j;
-    f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<false, false, CH>(t, sdPm, LC, 16 * rb, sQ, LK, 16 * n);
-    mma_blk<true, false, CH>(t, sD, LC, 16 * rb, sK, LK, 16 * n);
-    mma_blk<false, false, CH>(t, sD, LC, 16 * rb, sK, LK, 16 * n);
+    for (int j = 0; j < HK; ++j) {
+      const int n = HK * hf + j;
+      f32x4 t = {0.f, 0.f, 0.f, 0.f};
+      mma_blk<false, false, CH>(t, sdPm, LC, 16 * rb, sQ, LK, 16 * n);
+      mma_blk<true, false, CH>(t, sD, LC, 16 * rb, sK, LK, 16 * n);
+      mma_blk<false, false, CH>(t, sD, LC, 16 * rb, sK, LK, 16 * n);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
-      sdk[r * LK + d] = from_f<T>(dte[i] * aKd[j][i] + t[i] + bet[i] * gam[i] * aX[j][i]);
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
+        sdk[r * LK + d] = from_f<T>(dte[i] * aKd[j][i] + t[i] + bet[i] * gam[i] * aX[j][i]);
+      }
+    }
+  } else {
+    // read side: dk = beta gamma dX + D U;  write side (kept in aKd until its staging area is free):
+    // du = dte dKd + dPm^T Q + D^T K
+#pragma unroll
+    for (int j = 0; j < HK; ++j) {
+      const int n = HK * hf + j;
+      f32x4 t = {0.f, 0.f, 0.f, 0.f}, t2 = {0.f, 0.f, 0.f, 0.f};
+      mma_blk<true, false, CH>(t, sD, LC, 16 * rb, sU, LK, 16 * n);
+      mma_blk<false, false, CH>(t2, sdPm, LC, 16 * rb, sQ, LK, 16 * n);
+      mma_blk<false, false, CH>(t2, sD, LC, 16 * rb, sK, LK, 16 * n);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
+        sdk[r * LK + d] = from_f<T>(t[i] + bet[i] * gam[i] * aX[j][i]);
+        aKd[j][i] = dte[i] * aKd[j][i] + t2[i];
+      }
     }
   }
   // dbeta and the per-row part of dG (first half, one lane per row)
@@ -523,7 +557,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       const float q_ = rq[i] + sHalf[0][r], k_ = rk[i] + sHalf[1][r], v_ = dbV[i] + sHalf[2][r];
       const float x_ = rx[i] + sHalf[3][r], a_ = dbA[i] + sHalf[4][r], z_ = rz[i] + sHalf[5][r];
       const float db = gam[i] * x_ + v_ + a_;
-      if (r < nvalid) dbeta[row0 + (int64_t)r * H] = db;
+      if (dbeta && r < nvalid) dbeta[row0 + (int64_t)r * H] = db;
       sdG[r] = scale * gam[i] * q_ - dte[i] * k_ + bet[i] * gam[i] * x_ + z_;
       sLast[r] = dte[i] * k_;
     }
@@ -531,6 +565,17 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   __syncthreads();
   s2g_rows<T, ITH>(dq + row0 * K, (int64_t)H * K, sdq, LK, CH, K, nvalid);
   s2g_rows<T, ITH>(dk + row0 * K, (int64_t)H * K, sdk, LK, CH, K, nvalid);
+  if constexpr (SEPU) {
+    // du staged in the D and dPm regions, free once every wave has passed the barrier above
+    T* sdu = sD;
+#pragma unroll
+    for (int j = 0; j < HK; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sdu[(16 * rb + acc_row(i)) * LK + 16 * (HK * hf + j) + acc_col()] = from_f<T>(aKd[j][i]);
+    __syncthreads();
+    s2g_rows<T, ITH>(du + row0 * K, (int64_t)H * K, sdu, LK, CH, K, nvalid);
+  }
   if (w == 0) {
     // dG_r -= colsum_r;  dG_last += sum_r dte_r rk_r + gamma_C <dS_C, S0>;  dg = reverse cumsum of dG
     float x = sdG[l] - (sColZ[0][l] + sColZ[1][l] + sColZ[2][l] + sColZ[3][l]);
@@ -549,56 +594,67 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------------------
-template <typename T, int K>
+template <typename T, int K, bool SEPU>
 static hipError_t bwd_state_k(const ChunkArgs& a) {
   constexpr int BV = 64;
   dim3 grid(a.V / BV * a.B * a.H);
-  bwd_state_kernel<T, K, BV><<<grid, STH, 0, a.stream>>>(
-      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.dout), a.beta,
-      static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P), a.ws.Gc, a.dhT, a.dh0,
-      static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dRs), a.T, a.H, a.V, a.NT, a.scale);
-  return hipGetLastError();
-}
-
-template <typename T, int K, int V>
-static hipError_t bwd_intra_kv(const ChunkArgs& a) {
-  constexpr int VS = sizeof(T) == 2 ? 64 : 32;
-  dim3 grid(a.NT, a.B * a.H);
-  bwd_intra_kernel<T, K, V, VS><<<grid, ITH, 0, a.stream>>>(
-      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.v), a.beta,
-      static_cast<const T*>(a.dout), static_cast<const T*>(a.ws.Tm), a.ws.Gc, static_cast<const T*>(a.ws.hs),
-      static_cast<const T*>(a.ws.Rs), static_cast<const T*>(a.ws.dhs), static_cast<const T*>(a.ws.dRs),
-      static_cast<T*>(a.dq), static_cast<T*>(a.dk), static_cast<T*>(a.dv), a.dg, a.dbeta, a.T, a.H, a.NT,
+  bwd_state_kernel<T, K, BV, SEPU><<<grid, STH, 0, a.stream>>>(
+      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
+      static_cast<const T*>(a.dout), a.beta, static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P),
+      a.ws.Gc, a.dhT, a.dh0, static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dRs), a.T, a.H, a.V, a.NT,
       a.scale);
   return hipGetLastError();
 }
 
-template <typename T, int K>
+template <typename T, int K, int V, bool SEPU>
+static hipError_t bwd_intra_kv(const ChunkArgs& a) {
+  constexpr int VS = sizeof(T) == 2 ? 64 : 32;
+  dim3 grid(a.NT, a.B * a.H);
+  bwd_intra_kernel<T, K, V, VS, SEPU><<<grid, ITH, 0, a.stream>>>(
+      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
+      static_cast<const T*>(a.v), a.beta, static_cast<const T*>(a.dout), static_cast<const T*>(a.ws.Tm),
+      a.ws.Gc, static_cast<const T*>(a.ws.hs), static_cast<const T*>(a.ws.Rs), static_cast<const T*>(a.ws.dhs),
+      static_cast<const T*>(a.ws.dRs), static_cast<T*>(a.dq), static_cast<T*>(a.dk), static_cast<T*>(a.du),
+      static_cast<T*>(a.dv), a.dg, a.dbeta, a.T, a.H, a.NT, a.scale);
+  return hipGetLastError();
+}
+
+template <typename T, int K, bool SEPU>
 static hipError_t bwd_intra_k(const ChunkArgs& a) {
-  if (a.V == 64) return bwd_intra_kv<T, K, 64>(a);
-  if (a.V == 128) return bwd_intra_kv<T, K, 128>(a);
-  if (a.V == 256) return bwd_intra_kv<T, K, 256>(a);
+  if (a.V == 64) return bwd_intra_kv<T, K, 64, SEPU>(a);
+  if (a.V == 128) return bwd_intra_kv<T, K, 128, SEPU>(a);
+  if (a.V == 256) return bwd_intra_kv<T, K, 256, SEPU>(a);
+  return hipErrorInvalidValue;
+}
+
+template <bool SEPU>
+static hipError_t bwd_state_dispatch(const ChunkArgs& a) {
+  if (a.dtype == DT_BF16) {
+    if (a.K == 64) return bwd_state_k<bf16, 64, SEPU>(a);
+    if (a.K == 128) return bwd_state_k<bf16, 128, SEPU>(a);
+  } else if constexpr (!SEPU) {  // separate write keys: bf16 only
+    if (a.K == 64) return bwd_state_k<float, 64, SEPU>(a);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <bool SEPU>
+static hipError_t bwd_intra_dispatch(const ChunkArgs& a) {
+  if (a.dtype == DT_BF16) {
+    if (a.K == 64) return bwd_intra_k<bf16, 64, SEPU>(a);
+    if (a.K == 128) return bwd_intra_k<bf16, 128, SEPU>(a);
+  } else if constexpr (!SEPU) {  // separate write keys: bf16 only
+    if (a.K == 64) return bwd_intra_k<float, 64, SEPU>(a);
+  }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_bwd_state(const ChunkArgs& a) {
-  if (a.dtype == DT_BF16) {
-    if (a.K == 64) return bwd_state_k<bf16, 64>(a);
-    if (a.K == 128) return bwd_state_k<bf16, 128>(a);
-  } else {
-    if (a.K == 64) return bwd_state_k<float, 64>(a);
-  }
-  return hipErrorInvalidValue;
+  return a.u ? bwd_state_dispatch<true>(a) : bwd_state_dispatch<false>(a);
 }
 
 hipError_t launch_bwd_intra(const ChunkArgs& a) {
-  if (a.dtype == DT_BF16) {
-    if (a.K == 64) return bwd_intra_k<bf16, 64>(a);
-    if (a.K == 128) return bwd_intra_k<bf16, 128>(a);
-  } else {
-    if (a.K == 64) return bwd_intra_k<float, 64>(a);
-  }
-  return hipErrorInvalidValue;
+  return a.u ? bwd_intra_dispatch<true>(a) : bwd_intra_dispatch<false>(a);
 }
 
 }  // namespace gdn

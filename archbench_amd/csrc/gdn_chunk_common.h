@@ -169,7 +169,7 @@ struct RegTok {
     ok = l < valid;
     const int64_t off = row0 + (ok ? l : 0) * stride;
     g = pg[off];
-    b = pb[off];
+    b = pb ? pb[off] : 1.f;  // no beta: row scale 1
   }
 };
 
@@ -251,14 +251,14 @@ __device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld,
 // The sweeps call these for the *next* chunk while they run the state part of the current one, so each phase
 // is a separate function and the caller places the barriers between them.
 //
-// factors_kq: K K^T and Q K^T on MFMA (row block = wave), then
-//   A_ij = beta_i (K K^T)_ij exp(G_i - G_j) (i > j) -> sA  (fp32, strict lower)
-//   P_ij = s (Q K^T)_ij exp(G_i - G_j) (i >= j)     -> sP  (PMODE 1, row-major; PMODE 0: none, sQ unused)
-// Inputs: sK (and sQ) rows of the chunk, zero past the sequence end; sG (cumulative log-decay); sB (beta, zero
-// past the end).
+// factors_kq: K U^T and Q U^T on MFMA (row block = wave), then
+//   A_ij = beta_i (K U^T)_ij exp(G_i - G_j) (i > j) -> sA  (fp32, strict lower)
+//   P_ij = s (Q U^T)_ij exp(G_i - G_j) (i >= j)     -> sP  (PMODE 1, row-major; PMODE 0: none, sQ unused)
+// U is the write key (U = K for the gated delta rule).  Inputs: sK, sU (and sQ) rows of the chunk, zero past the
+// sequence end; sG (cumulative log-decay); sB (row scale beta, zero past the end).
 template <typename T, int K, int PMODE>
-__device__ __forceinline__ void factors_kq(const T* sK, const T* sQ, const float* sG, const float* sB, float scale,
-                                           float* sA, T* sP, int w) {
+__device__ __forceinline__ void factors_kq(const T* sK, const T* sU, const T* sQ, const float* sG, const float* sB,
+                                           float scale, float* sA, T* sP, int w) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LF = CH + 4;
   // masks are selects on values computed unconditionally (exp of min(G_i - G_j, 0) cannot overflow), so the
@@ -269,7 +269,7 @@ __device__ __forceinline__ void factors_kq(const T* sK, const T* sQ, const float
     Gr[i] = sG[16 * w + acc_row(i)];
     Br[i] = sB[16 * w + acc_row(i)];
   }
-  // the row block's K (and Q) fragments are read once; each column block's K fragment serves both products
+  // the row block's K (and Q) fragments are read once; each column block's U fragment serves both products
   typename Frag<T>::type ak[K / 32], aq[K / 32];
 #pragma unroll
   for (int s = 0; s < K / 32; ++s) {
@@ -281,7 +281,7 @@ __device__ __forceinline__ void factors_kq(const T* sK, const T* sQ, const float
     f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < K / 32; ++s) {
-      const auto bk = frag_kc(sK, LK, 16 * n, 32 * s);
+      const auto bk = frag_kc(sU, LK, 16 * n, 32 * s);
       mma(kk, ak[s], bk);
       if constexpr (PMODE != 0) mma(qk, aq[s], bk);
     }

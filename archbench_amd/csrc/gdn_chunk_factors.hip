@@ -3,10 +3,13 @@
 // For the 64 tokens of a chunk (archbench/layers/nsgdn.py:240-249 algebra with beta folded into A's rows; the
 // cumsum -> K K^T -> solve_tril steps of fla's GDN chunk forward, nsgdn.py:357-360):
 //   G    chunk-local inclusive cumsum of g                                            -> Gc [BH][NT][64] fp32
-//   A    beta_i (k_i . k_j) exp(G_i - G_j), strictly lower, on MFMA (fp32 in LDS)
+//   A    beta_i (k_i . u_j) exp(G_i - G_j), strictly lower, on MFMA (fp32 in LDS)
 //   Tm   (I + A)^-1: diagonal 16x16 blocks by Neumann products, blocks below by column chains (bf16x3 MFMA)
 //                                                                                     -> Tm [BH][NT][64][64]
-//   P    s (q_i . k_j) exp(G_i - G_j) for i >= j                                      -> P  [BH][NT][64][64]
+//   P    s (q_i . u_j) exp(G_i - G_j) for i >= j                                      -> P  [BH][NT][64][64]
+// u is the write key: u = k for the gated delta rule (SEPU false); with separate write keys (SEPU, the n-step
+// family, archbench/layers/nsgdn.py:240-249 with L_ij = (k_i . u_j) gamma_i / gamma_j) u is loaded too and
+// beta may be absent (row scale 1).
 // The sweeps over the sequence (forward, recompute, reverse) read these instead of rebuilding them for every
 // 64-wide V block, and the gradient kernel reads Tm and G.  Rows past the end of the sequence hold zero k, q
 // and beta, which makes Tm the identity and P zero there.
@@ -19,9 +22,9 @@ namespace gdn {
 
 // Persistent: workgroup x handles items x, x + gridDim.x, ... of the (b*h, chunk) grid (item = bh * NT + c), with
 // the next item's k, q, g and beta prefetched into registers while the current one is factored.
-template <typename T, int K>
+template <typename T, int K, bool SEPU>
 __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k,
-                                                             const float* __restrict__ g,
+                                                             const T* __restrict__ u, const float* __restrict__ g,
                                                              const float* __restrict__ beta, T* __restrict__ gTm,
                                                              T* __restrict__ gP, float* __restrict__ gGc, int T_,
                                                              int H, int NT, int nitems, float scale) {
@@ -29,6 +32,8 @@ __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict
   constexpr int LK = K + PT, LC = CH + PT, LF = CH + 4;
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
   __shared__ __attribute__((aligned(16))) T sQ[CH * LK];
+  __shared__ __attribute__((aligned(16))) T sU_[SEPU ? CH * LK : 8];
+  T* sU = SEPU ? sU_ : sK;
   __shared__ __attribute__((aligned(16))) float sA[CH * LF];
   __shared__ __attribute__((aligned(16))) float sD[4 * DBLK];
   __shared__ __attribute__((aligned(16))) T sP[CH * LC];
@@ -36,7 +41,7 @@ __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict
   __shared__ float sG[CH], sB[CH], sOne[CH];
 
   const int w = wave_id(), l = lane_id();
-  RegTile<T, CH, K> rk, rq;
+  RegTile<T, CH, K> rk, rq, ru;
   RegTok rt;
   auto prefetch = [&](int it) {
     const int bh = it / NT, c = it - bh * NT;
@@ -45,6 +50,7 @@ __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict
     const int64_t row0 = ((int64_t)b * T_ + (int64_t)c * CH) * H + h;
     rk.load(k + row0 * K, (int64_t)H * K, nvalid);
     rq.load(q + row0 * K, (int64_t)H * K, nvalid);
+    if constexpr (SEPU) ru.load(u + row0 * K, (int64_t)H * K, nvalid);
     if (w == 0) rt.load(g, beta, row0, H, nvalid);
   };
   if (w == 0) sOne[l] = 1.f;
@@ -52,6 +58,7 @@ __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict
   for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
     rk.store(sK, LK);
     rq.store(sQ, LK);
+    if constexpr (SEPU) ru.store(sU, LK);
     if (w == 0) {
       const float G = wave_inclusive_scan(rt.ok ? rt.g : 0.f);
       sG[l] = G;
@@ -60,7 +67,7 @@ __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict
     }
     __syncthreads();
     if (it + (int)gridDim.x < nitems) prefetch(it + gridDim.x);
-    factors_kq<T, K, 1>(sK, sQ, sG, sB, scale, sA, sP, w);
+    factors_kq<T, K, 1>(sK, sU, sQ, sG, sB, scale, sA, sP, w);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the diagonal block reads this wave's rows of A
     const f32x4 D = factors_diag<T>(sA, sD, sTm, nullptr, sOne, w);
     __syncthreads();
@@ -72,25 +79,30 @@ __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict
   }
 }
 
-template <typename T, int K>
+template <typename T, int K, bool SEPU>
 static hipError_t factors_k(const ChunkArgs& a) {
   const int nitems = a.NT * a.B * a.H;
-  const int per_cu = sizeof(T) == 2 ? 2 : 1;  // workgroups resident per CU (LDS)
+  const int per_cu = sizeof(T) == 2 && !SEPU ? 2 : 1;  // workgroups resident per CU (LDS)
   dim3 grid(std::min(nitems, per_cu * device_cu_count()));
-  chunk_factors_kernel<T, K><<<grid, NTHR, 0, a.stream>>>(
-      static_cast<const T*>(a.q), static_cast<const T*>(a.k), a.g, a.beta, static_cast<T*>(a.ws.Tm),
-      static_cast<T*>(a.ws.P), a.ws.Gc, a.T, a.H, a.NT, nitems, a.scale);
+  chunk_factors_kernel<T, K, SEPU><<<grid, NTHR, 0, a.stream>>>(
+      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u), a.g, a.beta,
+      static_cast<T*>(a.ws.Tm), static_cast<T*>(a.ws.P), a.ws.Gc, a.T, a.H, a.NT, nitems, a.scale);
   return hipGetLastError();
 }
 
-hipError_t launch_factors(const ChunkArgs& a) {
+template <bool SEPU>
+static hipError_t factors_dispatch(const ChunkArgs& a) {
   if (a.dtype == DT_BF16) {
-    if (a.K == 64) return factors_k<bf16, 64>(a);
-    if (a.K == 128) return factors_k<bf16, 128>(a);
-  } else {
-    if (a.K == 64) return factors_k<float, 64>(a);
+    if (a.K == 64) return factors_k<bf16, 64, SEPU>(a);
+    if (a.K == 128) return factors_k<bf16, 128, SEPU>(a);
+  } else if constexpr (!SEPU) {  // separate write keys: bf16 only
+    if (a.K == 64) return factors_k<float, 64, SEPU>(a);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_factors(const ChunkArgs& a) {
+  return a.u ? factors_dispatch<true>(a) : factors_dispatch<false>(a);
 }
 
 }  // namespace gdn

@@ -11,6 +11,8 @@
 // prefetched into registers one chunk ahead.
 // MODE 0 writes O (and hT); MODE 1 (recompute for the backward) writes instead the state entering every chunk
 // and R, in the fragment layout straight from the accumulators; MODE 2 (training forward) writes both.
+// SEPU (separate write keys u, nsgdn.py:240-249): the state update is S <- gamma_C S + U^T (exp(G_C - G) R) with
+// U loaded beside K; K keeps the read K S; beta may be absent (row scale 1).
 #include "gdn_chunk_common.h"
 #include "gdn_launch.h"
 
@@ -24,9 +26,10 @@ namespace gdn {
 constexpr int FW = 2 * NWAVE;  // waves of the forward sweep
 constexpr int FTH = 64 * FW;
 
-template <typename T, int K, int BV, int MODE>
+template <typename T, int K, int BV, int MODE, bool SEPU>
 __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const float* __restrict__ beta,
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u, const T* __restrict__ v,
+    const float* __restrict__ beta,
     const float* __restrict__ h0, const T* __restrict__ gTm, const T* __restrict__ gP,
     const float* __restrict__ gGc, T* __restrict__ o, float* __restrict__ hT, T* __restrict__ wsH,
     T* __restrict__ wsR, int T_, int H, int V, int NT, float scale) {
@@ -38,6 +41,8 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
   constexpr bool SAVE = MODE != 0;  // per-chunk states and R are written
   using F = typename Frag<T>::type;
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
+  __shared__ __attribute__((aligned(16))) T sU_[SEPU ? CH * LK : 8];
+  T* sU = SEPU ? sU_ : sK;  // write keys
   __shared__ __attribute__((aligned(16))) T sQ[OUT ? CH * LK : 8];
   __shared__ __attribute__((aligned(16))) T sV[CH * LV];
   __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
@@ -59,7 +64,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
-  RegTile<T, CH, K, FTH> rk, rq;
+  RegTile<T, CH, K, FTH> rk, rq, ru;
   RegTile<T, CH, BV, FTH> rv;
   RegTile<T, CH, CH, FTH> rtm, rp;
   float pG = 0.f, pB = 0.f;  // wave 0: G and beta of lane l's token
@@ -69,6 +74,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     const int64_t row0 = row0_of(c);
     const int nv = nvalid_of(c);
     rk.load(k + row0 * K, (int64_t)H * K, nv, tid);
+    if constexpr (SEPU) ru.load(u + row0 * K, (int64_t)H * K, nv, tid);
     if constexpr (OUT) rq.load(q + row0 * K, (int64_t)H * K, nv, tid);
     rv.load(v + row0 * V + v0, (int64_t)H * V, nv, tid);
   };
@@ -79,11 +85,12 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     if constexpr (OUT) rp.load(gP + cidx * CH * CH, (int64_t)CH, CH, tid);
     if (w == 0) {
       pG = gGc[cidx * CH + l];
-      pB = l < nv ? beta[row0 + (int64_t)l * H] : 0.f;
+      pB = l < nv ? (beta ? beta[row0 + (int64_t)l * H] : 1.f) : 0.f;
     }
   };
   auto to_lds = [&]() {
     rk.store(sK, LK, tid);
+    if constexpr (SEPU) ru.store(sU, LK, tid);
     if constexpr (OUT) rq.store(sQ, LK, tid);
     rv.store(sV, LV, tid);
     rtm.store(sTm, LC, tid);
@@ -185,13 +192,13 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
         }
       }
     }
-    // S <- gamma_C S + K^T Rd (all rows of K, both halves of the chunk)
+    // S <- gamma_C S + U^T Rd (all rows of U, both halves of the chunk)
     const float gC = __expf(GC);
 #pragma unroll
     for (int t = 0; t < NKT; ++t) {
       S[t] *= gC;
-      mma(S[t], frag_oct_perm(sK, LK, 16 * t, 0), Rd0);
-      mma(S[t], frag_oct_perm(sK, LK, 16 * t, 32), Rd1);
+      mma(S[t], frag_oct_perm(sU, LK, 16 * t, 0), Rd0);
+      mma(S[t], frag_oct_perm(sU, LK, 16 * t, 32), Rd1);
     }
     __syncthreads();  // O staged; every wave done with this chunk's inputs
     if constexpr (OUT)
@@ -209,12 +216,13 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------------------
-template <typename T, int K, int MODE>
+template <typename T, int K, int MODE, bool SEPU>
 static hipError_t fwd_sweep_k(const ChunkArgs& a) {
   constexpr int BV = 64;
   dim3 grid(a.V / BV * a.B * a.H);
-  fwd_sweep_kernel<T, K, BV, MODE><<<grid, FTH, 0, a.stream>>>(
-      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.v), a.beta, a.h0,
+  fwd_sweep_kernel<T, K, BV, MODE, SEPU><<<grid, FTH, 0, a.stream>>>(
+      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
+      static_cast<const T*>(a.v), a.beta, a.h0,
       static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P), a.ws.Gc, static_cast<T*>(a.o),
       MODE == 1 ? nullptr : a.hT, static_cast<T*>(a.ws.hs), static_cast<T*>(a.ws.Rs), a.T, a.H, a.V, a.NT,
       a.scale);
@@ -223,10 +231,16 @@ static hipError_t fwd_sweep_k(const ChunkArgs& a) {
 
 template <typename T, int K>
 static hipError_t fwd_sweep_mode(const ChunkArgs& a, FwdMode mode) {
+  if constexpr (sizeof(T) == 2) {
+    if (a.u) {  // separate write keys: the training pair only (stashing forward)
+      if (mode == FWD_STASH) return fwd_sweep_k<T, K, 2, true>(a);
+      return hipErrorInvalidValue;
+    }
+  }
   switch (mode) {
-    case FWD_OUT: return fwd_sweep_k<T, K, 0>(a);
-    case FWD_RECOMPUTE: return fwd_sweep_k<T, K, 1>(a);
-    default: return fwd_sweep_k<T, K, 2>(a);
+    case FWD_OUT: return fwd_sweep_k<T, K, 0, false>(a);
+    case FWD_RECOMPUTE: return fwd_sweep_k<T, K, 1, false>(a);
+    default: return fwd_sweep_k<T, K, 2, false>(a);
   }
 }
 
@@ -234,7 +248,7 @@ hipError_t launch_fwd(const ChunkArgs& a, FwdMode mode) {
   if (a.dtype == DT_BF16) {
     if (a.K == 64) return fwd_sweep_mode<bf16, 64>(a, mode);
     if (a.K == 128) return fwd_sweep_mode<bf16, 128>(a, mode);
-  } else {
+  } else if (!a.u) {  // separate write keys: bf16 only
     if (a.K == 64) return fwd_sweep_mode<float, 64>(a, mode);
   }
   return hipErrorInvalidValue;

@@ -36,8 +36,12 @@ struct ChunkWs {
   void* dRs;  // [BH][NT][64][V]    dL/dR per chunk
 };
 
+// Separate read and write keys: with u non-null the write (state update, the column side of K K^T and Q K^T, the
+// dR term U dS) uses u [B,T,H,K] while the read (K S) keeps k, and the backward writes du apart from dk; beta
+// may then be null (row scale 1).  With u null, u = k (the gated delta rule).
 struct ChunkArgs {
   const void *q, *k, *v;
+  const void* u;  // write keys or null
   const float *g, *beta;
   const float* h0;  // [B,H,K,V] or null
   void* o;          // [B,T,H,V] (forward)
@@ -46,6 +50,7 @@ struct ChunkArgs {
   const void* dout;   // [B,T,H,V]
   const float* dhT;   // or null
   void *dq, *dk, *dv;
+  void* du;  // with u
   float *dg, *dbeta;
   float* dh0;  // or null
   ChunkWs ws;

@@ -41,7 +41,7 @@ from torch import Tensor
 from . import _lib
 
 __all__ = ["chunk_gated_delta_rule", "fused_recurrent_gated_delta_rule", "recurrent_step", "chunk_fwd",
-           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "short_conv", "gated_rmsnorm", "l2norm", "gdn_gates"]
+           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "nsgdn_scan_chunk", "short_conv", "gated_rmsnorm", "l2norm", "gdn_gates"]
 
 
 def _require_gpu(*ts: Optional[Tensor]) -> None:
@@ -247,6 +247,107 @@ def _use_stash(*ts: Optional[Tensor]) -> bool:
     if os.environ.get("ARCHBENCH_AMD_GDN_STASH", "1") == "0" or not torch.is_grad_enabled():
         return False
     return any(t is not None and t.requires_grad for t in ts)
+
+
+# ---------------------------------------------------------------------- separate read / write vectors (nsgdn)
+# archbench::nsgdn_chunk_fwd / _bwd (nsgdn.py:352-397): S~ = e^la S, r = v - S~^T k, S = S~ + u r^T, y = S^T q,
+# on the same chunk kernels with u as the write key.  The forward fills the stash the backward reads (the
+# reference's forward likewise returns its g and A for the backward).  bf16 (the reference casts to bf16).
+def _nsgdn_shapes(q, k, u, v, la, h0):
+    if u.shape != q.shape:
+        raise ValueError(f"u must match q's shape {tuple(q.shape)}, got {tuple(u.shape)}")
+    if not (q.dtype == k.dtype == u.dtype == v.dtype == torch.bfloat16):
+        raise ValueError("the n-step chunk op takes bfloat16 q, k, u, v (as archbench's nsgdn_scan_chunk)")
+    return _shapes(q, k, v, la, la, h0)
+
+
+@torch.library.custom_op("archbench_amd::nsgdn_chunk_fwd", mutates_args=())
+def nsgdn_chunk_fwd(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor, h0: Optional[Tensor],
+                    scale: float) -> tuple[Tensor, Tensor, Tensor]:
+    """(y, hT, stash)."""
+    _require_gpu(q, k, u, v, la, h0)
+    B, T, H, K, V = _nsgdn_shapes(q, k, u, v, la, h0)
+    lib = _lib.load()
+    q, k, u, v, la, h0 = _arg(q), _arg(k), _arg(u), _arg(v), _arg(la, torch.float32), _arg(h0, torch.float32)
+    y = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
+    hT = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
+    stash = torch.empty(_lib.stash_bytes(B, T, H, K, V, q.dtype)[0], dtype=torch.uint8, device=q.device)
+    rc = lib.gdn_nsgdn_chunk_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(u), _lib.ptr(v), _lib.ptr(la), _lib.ptr(h0),
+                                 _lib.ptr(y), _lib.ptr(hT), _lib.ptr(stash), stash.numel(), B, T, H, K, V,
+                                 float(scale), _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
+    _lib.check(rc, "gdn_nsgdn_chunk_fwd")
+    return y, hT, stash
+
+
+@nsgdn_chunk_fwd.register_fake
+def _(q, k, u, v, la, h0, scale):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    n = _lib.stash_bytes(B, T, H, K, V, q.dtype)[0]
+    return (q.new_empty(B, T, H, V), q.new_empty(B, H, K, V, dtype=torch.float32),
+            q.new_empty(n, dtype=torch.uint8))
+
+
+@torch.library.custom_op("archbench_amd::nsgdn_chunk_bwd", mutates_args=())
+def nsgdn_chunk_bwd(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor, h0: Optional[Tensor], dy: Tensor,
+                    dhT: Optional[Tensor], stash: Tensor,
+                    scale: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(dq, dk, du, dv, dla, dh0)."""
+    _require_gpu(q, k, u, v, la, h0, dy, dhT, stash)
+    B, T, H, K, V = _nsgdn_shapes(q, k, u, v, la, h0)
+    lib = _lib.load()
+    q, k, u, v, la, h0 = _arg(q), _arg(k), _arg(u), _arg(v), _arg(la, torch.float32), _arg(h0, torch.float32)
+    dy, dhT = _arg(dy, q.dtype), _arg(dhT, torch.float32)
+    dq, dk, du, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(u), torch.empty_like(v)
+    dla = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
+    dh0 = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
+    ws = torch.empty(_lib.stash_bytes(B, T, H, K, V, q.dtype)[1], dtype=torch.uint8, device=q.device)
+    rc = lib.gdn_nsgdn_chunk_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(u), _lib.ptr(v), _lib.ptr(la), _lib.ptr(h0),
+                                 _lib.ptr(dy), _lib.ptr(dhT), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(du),
+                                 _lib.ptr(dv), _lib.ptr(dla), _lib.ptr(dh0), _lib.ptr(stash), stash.numel(),
+                                 _lib.ptr(ws), ws.numel(), B, T, H, K, V, float(scale), _lib.dtype_code(q.dtype),
+                                 _lib.stream_ptr(q.device))
+    _lib.check(rc, "gdn_nsgdn_chunk_bwd")
+    return dq, dk, du, dv, dla, dh0
+
+
+@nsgdn_chunk_bwd.register_fake
+def _(q, k, u, v, la, h0, dy, dhT, stash, scale):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    f32 = dict(dtype=torch.float32)
+    return (torch.empty_like(q), torch.empty_like(k), torch.empty_like(u), torch.empty_like(v),
+            q.new_empty(B, T, H, **f32), q.new_empty(B, H, K, V, **f32))
+
+
+def _nsgdn_setup(ctx, inputs, output):
+    q, k, u, v, la, h0, scale = inputs
+    ctx.save_for_backward(q, k, u, v, la, h0, output[2])
+    ctx.scale = scale
+    ctx.has_h0 = h0 is not None
+    ctx.la_dtype = la.dtype
+
+
+def _nsgdn_backward(ctx, dy, dhT, _dstash):
+    q, k, u, v, la, h0, stash = ctx.saved_tensors
+    if dy is None:
+        dy = torch.zeros(*q.shape[:3], v.shape[-1], dtype=q.dtype, device=q.device)
+    dq, dk, du, dv, dla, dh0 = nsgdn_chunk_bwd(q, k, u, v, la, h0, dy.contiguous(),
+                                               None if dhT is None else dhT.contiguous(), stash, ctx.scale)
+    return dq, dk, du, dv, dla.to(ctx.la_dtype), (dh0 if ctx.has_h0 else None), None
+
+
+nsgdn_chunk_fwd.register_autograd(_nsgdn_backward, setup_context=_nsgdn_setup)
+
+
+def nsgdn_scan_chunk(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor, scale: float = 1.0,
+                     initial_state: Tensor | None = None, output_final_state: bool = False):
+    """archbench's nsgdn_scan_chunk (nsgdn.py:400-405) on the HIP chunk kernels: returns y [B,T,H,V] in bf16
+    (and the fp32 final state with ``output_final_state``).  Differentiable w.r.t. q, k, u, v, la and
+    initial_state.  Any T (the reference falls back to its DPLR path when T % 64 != 0, nsgdn.py:402-403)."""
+    dt = torch.bfloat16
+    y, hT, _ = nsgdn_chunk_fwd(q.to(dt), k.to(dt), u.to(dt), v.to(dt), la.float(), initial_state, float(scale))
+    return (y, hT) if output_final_state else y
 
 
 # ------------------------------------------------------------------------------------ short causal conv + SiLU

@@ -88,6 +88,24 @@ int gdn_chunk_bwd_stashed(const void* q, const void* k, const void* v, const flo
                           size_t ws_bytes, int B, int T, int H, int K, int V, float scale, int dtype,
                           void* stream);
 
+/* The same chunk pipeline with separate read and write vectors (the n-step GDN family, archbench's `nsgdn`
+ * mixer): per token
+ *   S~ = e^la S,   r = v - S~^T k,   S = S~ + u r^T,   y = S^T (scale q)
+ * (nsgdn_ref, archbench/layers/nsgdn.py:408-417; the chunked form nsgdn.py:240-249 with
+ * L_ij = (k_i . u_j) gamma_i / gamma_j).  Replaces the custom ops archbench::nsgdn_chunk_fwd / _bwd
+ * (nsgdn.py:352-397): the reference's forward returns (y, g, A) for its backward, this one fills the stash of
+ * gdn_chunk_stash_bytes (same sizes); the backward reads it and writes dq, dk, du, dv, dla (and dh0).  u has
+ * q's shape and dtype; la (natural-log decay) [B,T,H] fp32; h0, hT, dhT, dh0 as for the chunk op (optional);
+ * the reference calls it with scale 1 (q pre-scaled) and no states.  bf16 only (as the reference's op, which
+ * casts to bf16, nsgdn.py:400-405); K and V as for the chunk op. */
+int gdn_nsgdn_chunk_fwd(const void* q, const void* k, const void* u, const void* v, const float* la,
+                        const float* h0, void* y, float* hT, void* stash, size_t stash_bytes, int B, int T, int H,
+                        int K, int V, float scale, int dtype, void* stream);
+int gdn_nsgdn_chunk_bwd(const void* q, const void* k, const void* u, const void* v, const float* la,
+                        const float* h0, const void* dy, const float* dhT, void* dq, void* dk, void* du, void* dv,
+                        float* dla, float* dh0, const void* stash, size_t stash_bytes, void* ws, size_t ws_bytes,
+                        int B, int T, int H, int K, int V, float scale, int dtype, void* stream);
+
 /* One recurrent decode step, state updated in place:
  *   r = beta (v - e^g S^T k),  S <- e^g S + k r^T,  o = S^T (scale q)
  * q, k [B, H, K], v, o [B, H, V], g, beta [B, H] fp32, state [B, H, K, V] fp32.
