@@ -2,8 +2,9 @@
 
 ``register(name)`` decorates a builder, ``available()`` lists names, ``build_mixer(name, d_model, layer_idx,
 n_layer, **kwargs)`` builds one; an unknown name raises KeyError and ``"fla:<Class>"`` routes to
-``build_fla`` exactly as in the reference.  Only the gated DeltaNet mixer (``"gdn"``) is provided here, on the
-MI355X kernels; the reference's other mixers are outside this package.
+``build_fla`` exactly as in the reference.  The gated DeltaNet mixers are provided here, on the MI355X kernels:
+``"gdn"`` (fla's GatedDeltaNet, archbench/layers/fla.py:36-38) and ``"nsgdn"`` (the n-step family,
+archbench/layers/nsgdn.py:545-547); the reference's other mixers are outside this package.
 """
 
 from __future__ import annotations
@@ -34,3 +35,4 @@ def build_mixer(name: str, d_model: int, layer_idx: int, n_layer: int, **kwargs)
 
 
 from . import fla  # noqa: E402,F401  (registers "gdn")
+from . import nsgdn  # noqa: E402,F401  (registers "nsgdn")

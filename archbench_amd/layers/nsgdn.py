@@ -1,0 +1,117 @@
+"""The n-step gated DeltaNet mixer (archbench's ``nsgdn`` arch) on the MI355X kernels.
+
+Constructor and parameter names follow ``NStepGDN`` (archbench/layers/nsgdn.py:473-516): ``in_proj`` (q, k, v,
+gate, and the a / b gate inputs in one projection), ``conv.weight`` [2*H*DK + H*DV, 1, conv_size], ``A_log``,
+``dt_bias``, ``b_bias``, ``lam``, ``norm`` (RMSNorm over DV) and ``o_proj``, so the reference's checkpoints and
+zero-init rule for ``o_proj`` (archbench/model.py:14, :80-82) apply.  The forward computes what
+``NStepGDN.forward`` does (nsgdn.py:518-542):
+
+    qkv = conv(in_proj(x)) with SiLU           -> ops.short_conv, three calls on the weight's row slices, q and k
+                                                  L2-normalised per head inside the conv (nsgdn.py:527-528)
+    la, beta from ab                           -> ops.gdn_gates (nsgdn.py:531-534, optional la_min clamp)
+    u = write_direction(k, p, beta, lam, n)    -> PyTorch elementwise (nsgdn.py:61-75, :535-536)
+    y = scan(q, k, u, v, la)                   -> ops.nsgdn_scan_chunk, the chunk kernels with write keys u; the
+                                                  q scale DK^-1/2 is the op's scale instead of a separate pass
+    y = norm(y) * silu(g); o_proj              -> ops.gated_rmsnorm
+
+``scan_impl`` is accepted for config compatibility; every choice runs the HIP chunk kernels (there is no CPU or
+Triton path here).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .. import ops
+from . import register
+
+
+def write_direction(k: torch.Tensor, p: torch.Tensor, beta: torch.Tensor, lam: torch.Tensor,
+                    n_steps: int) -> torch.Tensor:
+    """u_1 = beta k; then n_steps - 1 steps u <- u - lam beta (p . u) p_perp, p_perp = p - (p . k) k
+    (nsgdn.py:61-75).  k, p [B,T,H,K]; beta [B,T,H]; lam [H]."""
+    b = beta[..., None]
+    u = b * k
+    if n_steps > 1:
+        lb = lam[None, None, :, None] * b
+        p_perp = p - (p * k).sum(-1, keepdim=True) * k
+        for _ in range(n_steps - 1):
+            u = u - lb * (p * u).sum(-1, keepdim=True) * p_perp
+    return u
+
+
+class NStepGDN(nn.Module):
+    def __init__(self, d_model: int, num_heads: int = 8, head_dim: int = 128, expand_v: float = 2.0,
+                 n_steps: int = 2, lam: float = 1.0, use_gate: bool = True, use_short_conv: bool = True,
+                 conv_size: int = 4, norm_eps: float = 1e-5, scan_impl: str = "chunk", la_min: float | None = None,
+                 layer_idx: int | None = None):
+        super().__init__()
+        DK, DV = head_dim, int(head_dim * expand_v)
+        if DK & (DK - 1) or DV & (DV - 1):
+            raise ValueError("head_dim and head_dim * expand_v must be powers of 2")
+        if n_steps < 1:
+            raise ValueError("n_steps must be >= 1")
+        if lam <= 0:
+            raise ValueError("lam must be > 0")
+        if scan_impl not in ("chunk", "dplr", "triton", "ref"):
+            raise ValueError(f"unknown scan_impl {scan_impl!r}")
+        self.H, self.DK, self.DV, self.n_steps = num_heads, DK, DV, n_steps
+        self.qk_dim, self.v_dim = num_heads * DK, num_heads * DV
+        self.use_gate = use_gate
+        self.n_gate = self.v_dim if use_gate else 0
+        width = 2 * self.qk_dim + self.v_dim + self.n_gate + 2 * num_heads
+        self.in_proj = nn.Linear(d_model, (width + 7) // 8 * 8, bias=False)
+        self.conv = _ConvWeight(2 * self.qk_dim + self.v_dim, conv_size) if use_short_conv else None
+        self.A_log = nn.Parameter(torch.empty(num_heads).uniform_(1, 16).log())
+        dt = torch.exp(torch.rand(num_heads) * (math.log(0.1) - math.log(0.001)) + math.log(0.001))
+        self.dt_bias = nn.Parameter(dt + torch.log(-torch.expm1(-dt)))
+        self.b_bias = nn.Parameter(torch.zeros(num_heads))
+        self.lam = nn.Parameter(torch.full((num_heads,), math.log(math.expm1(lam))))
+        self.norm = nn.RMSNorm(DV, eps=norm_eps)
+        self.scan_impl, self.la_min, self.layer_idx = scan_impl, la_min, layer_idx
+        self.o_proj = nn.Linear(self.v_dim, d_model, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        B, T, _ = x.shape
+        H, DK, DV = self.H, self.DK, self.DV
+        n_qkv = 2 * self.qk_dim + self.v_dim
+        proj = self.in_proj(x)
+        qkv = proj[..., :n_qkv]
+        g = proj[..., n_qkv:n_qkv + self.n_gate]
+        ab = proj[..., n_qkv + self.n_gate:n_qkv + self.n_gate + 2 * H]
+        qs, ks, vs = qkv[..., :self.qk_dim], qkv[..., self.qk_dim:2 * self.qk_dim], qkv[..., 2 * self.qk_dim:]
+        if self.conv is not None:
+            w = self.conv.weight.squeeze(1).to(qkv.dtype).float()  # rounded as the reference's conv runs it
+            q, _ = ops.short_conv(qs, w[:self.qk_dim], None, None, DK)
+            k, _ = ops.short_conv(ks, w[self.qk_dim:2 * self.qk_dim], None, None, DK)
+            v, _ = ops.short_conv(vs, w[2 * self.qk_dim:], None, None, 0)
+        else:
+            q, k, v = ops.l2norm(qs, 1e-12, 1.0), ops.l2norm(ks, 1e-12, 1.0), vs
+        q, k, v = q.view(B, T, H, DK), k.view(B, T, H, DK), v.reshape(B, T, H, DV)
+        la, beta = ops.gdn_gates(ab[..., :H], ab[..., H:], self.A_log, self.dt_bias, self.b_bias, 1.0,
+                                 float("-inf") if self.la_min is None else float(self.la_min))
+        kf = k.float()
+        p = F.pad(kf[:, :-1], (0, 0, 0, 0, 1, 0))
+        u = write_direction(kf, p, beta, F.softplus(self.lam.float()), self.n_steps)
+        y = ops.nsgdn_scan_chunk(q, k, u, v, la, scale=DK ** -0.5)
+        gate = g.view(B, T, H, DV) if self.use_gate else None
+        y = ops.gated_rmsnorm(y.to(x.dtype), gate, self.norm.weight, self.norm.eps or 1e-5)
+        return self.o_proj(y.reshape(B, T, -1))
+
+
+class _ConvWeight(nn.Module):
+    """Holds the depthwise conv weight [D, 1, size] under the reference's name (ShortConv.weight, nsgdn.py:457-462)."""
+
+    def __init__(self, dim: int, size: int):
+        super().__init__()
+        self.size = size
+        self.weight = nn.Parameter(torch.empty(dim, 1, size).uniform_(-1 / math.sqrt(size), 1 / math.sqrt(size)))
+
+
+@register("nsgdn")
+def build_nsgdn(d_model: int, layer_idx: int, n_layer: int, **kwargs):
+    return NStepGDN(d_model, layer_idx=layer_idx, **kwargs)

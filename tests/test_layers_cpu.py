@@ -86,3 +86,16 @@ def test_short_conv_cpu_raises():
 
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         ops.short_conv(torch.randn(1, 4, 512), torch.randn(512, 4), None, None, 0)
+
+
+def test_nsgdn_registered_and_no_cpu_fallback():
+    assert "nsgdn" in layers.available()
+    m = layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=64, expand_v=2.0, n_steps=2, lam=1.0)
+    names = {n for n, _ in m.named_parameters()}
+    assert {"in_proj.weight", "conv.weight", "A_log", "dt_bias", "b_bias", "lam", "norm.weight",
+            "o_proj.weight"} <= names
+    assert m.conv.weight.shape == (2 * 128 + 256, 1, 4)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        m(torch.randn(1, 8, 128))
+    with pytest.raises(ValueError):
+        layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=48)
