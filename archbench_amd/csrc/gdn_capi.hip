@@ -116,11 +116,11 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
 // ---- per-stage event timing (diagnostic; off unless gdn_profile_enable(1) was called on this thread) ----
 enum Stage {
   ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_FACTORS, ST_CONV_FWD,
-  ST_CONV_BWD, ST_NORM_FWD, ST_NORM_BWD, ST_GATES_FWD, ST_GATES_BWD, ST_L2_FWD, ST_L2_BWD, ST_COUNT
+  ST_CONV_BWD, ST_NORM_FWD, ST_NORM_BWD, ST_GATES_FWD, ST_GATES_BWD, ST_L2_FWD, ST_L2_BWD, ST_CE, ST_COUNT
 };
 static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step", "fwd_stash",
                                             "factors", "conv_fwd", "conv_bwd", "norm_fwd", "norm_bwd", "gates_fwd", "gates_bwd",
-                                            "l2norm_fwd", "l2norm_bwd"};
+                                            "l2norm_fwd", "l2norm_bwd", "cross_entropy"};
 struct ProfRec { int stage; hipEvent_t a, b; };
 struct Prof {
   bool on = false;
@@ -536,6 +536,26 @@ int gdn_l2norm_bwd(const void* x, const void* dy, void* dx, int64_t rows, int di
   a.scale = scale; a.stream = static_cast<hipStream_t>(stream);
   const hipError_t e = timed(ST_L2_BWD, a.stream, [&] { return launch_norm(a, true); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "L2 norm backward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+int gdn_cross_entropy_fwd_bwd(void* logits, const int64_t* target, float* loss, float* lse, const float* dloss,
+                              int64_t N, int V, int64_t ld, int64_t ignore_index, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
+  if (N < 0) return fail(GDN_ERR_ARG, "invalid N=%lld", (long long)N);
+  if (!ce_shape_supported(V, ld))
+    return fail(GDN_ERR_SHAPE, "cross entropy not compiled for V=%d ld=%lld (V %% 8 == 0, ld %% 8 == 0, V <= 65536)",
+                V, (long long)ld);
+  if (N == 0) return GDN_OK;
+  if (!logits || !target || !loss) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(logits)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
+  CeArgs a{};
+  a.logits = logits; a.target = target; a.loss = loss; a.lse = lse; a.dloss = dloss;
+  a.N = N; a.ld = ld; a.V = V; a.dtype = dtype; a.ignore_index = ignore_index;
+  a.stream = static_cast<hipStream_t>(stream);
+  const hipError_t e = timed(ST_CE, a.stream, [&] { return launch_ce(a); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "cross entropy launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }
 

@@ -135,6 +135,21 @@ struct GateArgs {
 size_t gates_ws_bytes(int64_t ntok, int H);
 hipError_t launch_gates(const GateArgs& a, bool backward);
 
+// Cross-entropy forward + backward in place on logits rows (gdn_ce.hip).
+struct CeArgs {
+  void* logits;            // [N, ld] in dtype; overwritten with dloss * (softmax - onehot)
+  const int64_t* target;   // [N]
+  float* loss;             // [N] per-row loss (0 for ignored rows)
+  float* lse;              // [N] or null
+  const float* dloss;      // device scalar (gradient of each row's loss) or null (1)
+  int64_t N, ld;
+  int V, dtype;
+  int64_t ignore_index;
+  hipStream_t stream;
+};
+bool ce_shape_supported(int V, int64_t ld);
+hipError_t launch_ce(const CeArgs& a);
+
 // Compute units of the current device (cached per device; 256 if the query fails).
 int device_cu_count();
 

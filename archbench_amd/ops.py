@@ -41,7 +41,7 @@ from torch import Tensor
 from . import _lib
 
 __all__ = ["chunk_gated_delta_rule", "fused_recurrent_gated_delta_rule", "recurrent_step", "chunk_fwd",
-           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "nsgdn_scan_chunk", "short_conv", "gated_rmsnorm", "l2norm", "gdn_gates"]
+           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "nsgdn_scan_chunk", "short_conv", "gated_rmsnorm", "l2norm", "gdn_gates", "cross_entropy_fwd_bwd_"]
 
 
 def _require_gpu(*ts: Optional[Tensor]) -> None:
@@ -662,6 +662,37 @@ def _gates_backward(ctx, dg, dbeta):
 
 
 gdn_gates.register_autograd(_gates_backward, setup_context=_gates_setup)
+
+
+# ------------------------------------------------------------------------------------------- cross entropy
+# Forward + backward of the cross-entropy in one pass, in place on a logits chunk (fla's cross_entropy_fwd +
+# cross_entropy_bwd(inplace_backward=True) in archbench/fused_ce.py:33-45).
+@torch.library.custom_op("archbench_amd::cross_entropy_fwd_bwd_", mutates_args=("logits",))
+def cross_entropy_fwd_bwd_(logits: Tensor, target: Tensor, dloss: Optional[Tensor],
+                           ignore_index: int) -> tuple[Tensor, Tensor]:
+    """(loss per row fp32, lse per row fp32); logits [N, V] become dloss * (softmax - onehot)."""
+    _require_gpu(logits, target, dloss)
+    if logits.dim() != 2 or target.shape != logits.shape[:1]:
+        raise ValueError(f"logits must be [N, V] and target [N], got {tuple(logits.shape)}, {tuple(target.shape)}")
+    if logits.stride(1) != 1 or logits.data_ptr() % 16:
+        raise ValueError("logits rows must be contiguous and 16-byte aligned (updated in place)")
+    N, V = logits.shape
+    lib = _lib.load()
+    target = _arg(target, torch.int64)
+    dloss = _arg(dloss, torch.float32)
+    loss = torch.empty(N, dtype=torch.float32, device=logits.device)
+    lse = torch.empty(N, dtype=torch.float32, device=logits.device)
+    rc = lib.gdn_cross_entropy_fwd_bwd(_lib.ptr(logits), _lib.ptr(target), _lib.ptr(loss), _lib.ptr(lse),
+                                       _lib.ptr(dloss), N, V, logits.stride(0), int(ignore_index),
+                                       _lib.dtype_code(logits.dtype), _lib.stream_ptr(logits.device))
+    _lib.check(rc, "gdn_cross_entropy_fwd_bwd")
+    return loss, lse
+
+
+@cross_entropy_fwd_bwd_.register_fake
+def _(logits, target, dloss, ignore_index):
+    N = logits.shape[0]
+    return logits.new_empty(N, dtype=torch.float32), logits.new_empty(N, dtype=torch.float32)
 
 
 # ------------------------------------------------------------------------------------------------- decode step

@@ -24,6 +24,9 @@ Also reported in the same line:
   gated_rmsnorm the output norm(o) * silu(gate) over B*T*H = 524288 rows of DV = 128, bf16, forward and backward
                 (HBM GB/s: forward reads x and gate, writes y; backward reads x, gate, dy, writes dx, dgate);
   gates         g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b) over B*T = 32768 tokens x H = 16;
+  fused_linear_ce  archbench's chunked linear + cross-entropy (fused_ce.py) at N = 8*4096 tokens, d_model 1024,
+                vocabulary 50304, bf16, one chunk: the GEMMs are hipBLASLt, the per-row loss + in-place gradient is
+                the HIP kernel (HBM GB/s on one read and one write of the logits);
   cpu_baseline  the CPU oracle (fp32 token recurrence + exact reverse-time backward) timed on this host's
                 cores on the full headline shape (about 20 s of CPU work at ~2e3 tokens/s on 16 threads).
 """
@@ -136,7 +139,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-sample-T", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "train", "fwd", "decode", "conv", "norm"], default="all",
+    ap.add_argument("--only", choices=["all", "train", "fwd", "decode", "conv", "norm", "ce"], default="all",
                     help="run one workload only (profiling runs); the JSON line needs 'all' or 'train'")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -307,6 +310,38 @@ def main() -> int:
             f"{us['norm_bwd']:.1f} us ({out['gated_rmsnorm']['bwd_GB_per_s']} GB/s); gates fwd "
             f"{us['gates_fwd']:.1f} us, bwd {us['gates_bwd']:.1f} us")
         del xn, gn, dyn
+        torch.cuda.empty_cache()
+
+    if args.only in ("all", "ce"):
+        from archbench_amd import fused_ce
+
+        N, Hd, Vv, nch = 8 * 4096, 1024, 50304, 1
+        log(f"fused linear cross-entropy N={N} d_model={Hd} vocab={Vv} bf16, {nch} chunks")
+        gen = torch.Generator(device=dev).manual_seed(2)
+        xc = torch.randn(N, Hd, device=dev, generator=gen).to(torch.bfloat16).requires_grad_()
+        wc = (torch.randn(Vv, Hd, device=dev, generator=gen) * 0.02).to(torch.bfloat16).requires_grad_()
+        tc = torch.randint(0, Vv, (N,), device=dev, generator=gen)
+
+        def ce_step():
+            fused_ce.fused_linear_cross_entropy(xc, tc, wc, num_chunks=nch).backward()
+            xc.grad = wc.grad = None
+
+        sec = timed_loop(ce_step, max(3, min(args.steps, 10)), 2, torch)
+        with _lib.StageTimer() as st:
+            ce_step()
+        ce_ms = st.result["cross_entropy"][0]
+        flops = 3 * 2 * N * Vv * Hd
+        ce_bytes = 2 * N * Vv * 2
+        out["fused_linear_ce"] = {"workload": "fused_linear_cross_entropy", "N": N, "d_model": Hd, "vocab": Vv,
+                                  "chunks": nch, "ms": round(sec * 1e3, 3), "tokens_per_s": round(N / sec, 1),
+                                  "gemm_mfma_frac": round(flops / (sec - ce_ms * 1e-3) / MFMA_BF16_PEAK, 4),
+                                  "ce_kernel_ms": round(ce_ms, 4),
+                                  "ce_GB_per_s": round(ce_bytes / (ce_ms * 1e-3) / 1e9, 1),
+                                  "ce_hbm_frac": round(ce_bytes / (ce_ms * 1e-3) / HBM_PEAK, 4)}
+        log(f"fused linear CE {sec * 1e3:.2f} ms ({N / sec:.3e} tokens/s); CE kernels {ce_ms:.3f} ms "
+            f"({out['fused_linear_ce']['ce_GB_per_s']} GB/s); GEMMs at "
+            f"{out['fused_linear_ce']['gemm_mfma_frac'] * 100:.1f}% of bf16 peak")
+        del xc, wc
         torch.cuda.empty_cache()
 
     if args.only in ("all", "train") and not args.no_cpu_baseline:

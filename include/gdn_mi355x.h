@@ -170,12 +170,21 @@ int gdn_gates_bwd(const void* a, const void* b, const float* A_log, const float*
                   float* db_bias, void* ws, size_t ws_bytes, int64_t ntok, int H, float beta_scale, float g_min,
                   int dtype, void* stream);
 
+/* Cross-entropy forward and backward in one pass, in place on a chunk of logits [N, ld] (dtype; V classes,
+ * V % 8 == 0, ld % 8 == 0, V <= 65536): loss[i] = logsumexp(x_i) - x_i,target[i] (0 where target == ignore_index,
+ * NaN for a target outside [0, V)), lse[i] (if non-NULL), and x_i <- dloss * (softmax(x_i) - onehot(target_i))
+ * (zeros for ignored rows), with dloss read from a device scalar (NULL = 1).  Replaces fla's cross_entropy_fwd +
+ * cross_entropy_bwd(inplace_backward=True) on each chunk of archbench's fused linear cross-entropy
+ * (archbench/fused_ce.py:33-45); the chunk GEMMs around it stay library GEMMs. */
+int gdn_cross_entropy_fwd_bwd(void* logits, const int64_t* target, float* loss, float* lse, const float* dloss,
+                              int64_t N, int V, int64_t ld, int64_t ignore_index, int dtype, void* stream);
+
 /* Per-stage kernel timing (diagnostic; no counterpart in the reference, which times whole phases with CUDA
  * events in archbench/logger.py:57-81).  While enabled on the calling thread, every kernel the calls above
  * enqueue is bracketed by hipEvents on the same stream.  gdn_profile_read synchronises on those events and
  * returns, per stage, the summed milliseconds and the number of launches (arrays of at least
  * GDN_PROFILE_STAGES entries), then clears the record.  Stage names: gdn_profile_stage_name. */
-#define GDN_PROFILE_STAGES 15
+#define GDN_PROFILE_STAGES 16
 int gdn_profile_enable(int on);
 int gdn_profile_read(double* ms_sum, int* launches, int n_stages);
 const char* gdn_profile_stage_name(int stage);
