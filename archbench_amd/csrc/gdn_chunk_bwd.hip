@@ -342,9 +342,15 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
         sdv[r * LS + vc] = from_f<T>(sB[r] * dy[i]);
       }
     }
-    // group B: dO S0^T, R dS_C^T, dR S0^T, <dS_C, S0>
+    // group B: dO S0^T, R dS_C^T, dR S0^T, <dS_C, S0> (the last from the registers: each thread holds the same
+    // elements of both tiles)
     rs0.store_t(sS0t, LK, tid);
     rdsc.store_t(sdSCt, LK, tid);
+#pragma unroll
+    for (int i = 0; i < decltype(rs0)::N; ++i)
+      if (decltype(rs0)::NVEC % ITH == 0 || tid + i * ITH < decltype(rs0)::NVEC)  // loaded by this thread
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sdot += to_f(rdsc.r[i][e]) * to_f(rs0.r[i][e]);
     if (vs == 0) {
       tq.store(sQ, LK, tid);
       tk.store(sK, LK, tid);
@@ -353,10 +359,6 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     __syncthreads();
     if (vs + VS < V) load_b(vs + VS);
     s2g_rows<T, ITH>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, CH, VS, nvalid);
-    for (int idx = tid; idx < K * VS; idx += ITH) {
-      const int n = idx / K, d = idx - n * K;
-      sdot += to_f(sdSCt[n * LK + d]) * to_f(sS0t[n * LK + d]);
-    }
 #pragma unroll
     for (int j = 0; j < HK; ++j) {
       const int n = HK * hf + j;
