@@ -38,6 +38,19 @@ namespace gdn {
 // rows (fp32), then the dR fragments, then the Z fragments (16 bytes per lane each).
 constexpr int SW = 2 * NWAVE;  // waves of the reverse sweep
 constexpr int STH = 64 * SW;
+#ifndef GDN_STATE_NT_LOAD
+#define GDN_STATE_NT_LOAD false
+#endif
+#ifndef GDN_STATE_NT_STORE
+#define GDN_STATE_NT_STORE true
+#endif
+#ifndef GDN_INTRA_NT
+#define GDN_INTRA_NT true
+#endif
+// the two V-block workgroups of a head read the same q, k, Tm and P (the second from L2): ordinary loads; dS_C and
+// dR are written once, nontemporal
+constexpr bool STATE_NT_LOAD = GDN_STATE_NT_LOAD, STATE_NT_STORE = GDN_STATE_NT_STORE;
+constexpr bool INTRA_NT = GDN_INTRA_NT;  // every read and write of the gradient kernel is single-use
 
 template <typename T, int K, int BV, bool SEPU>
 __global__ __launch_bounds__(STH) void bwd_state_kernel(
@@ -77,9 +90,9 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
-  RegTile<T, CH, K, STH> rk, rq, ru;
-  RegTile<T, CH, BV, STH> rdo;
-  RegTile<T, CH, CH, STH> rtm, rp;
+  RegTile<T, CH, K, STH, STATE_NT_LOAD> rk, rq, ru;
+  RegTile<T, CH, BV, STH, STATE_NT_LOAD> rdo;
+  RegTile<T, CH, CH, STH, STATE_NT_LOAD> rtm, rp;
   float pG = 0.f, pB = 0.f;
   // The next chunk's reads go out in two batches (k, q, dO after the first barrier; Tm, P, G, beta after the
   // dR exchange), so that no wave stalls on a full memory queue for the whole set at once.
@@ -131,7 +144,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
 #pragma unroll
     for (int s = 0; s < NSH; ++s) {
       dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
-      store_fragblk<T>(wsdH + cidx * K * V, NSH * hf + s, cb, ncb, dSb[s]);
+      store_fragblk<T, STATE_NT_STORE>(wsdH + cidx * K * V, NSH * hf + s, cb, ncb, dSb[s]);
     }
     f32x4 kd[4];
 #pragma unroll
@@ -165,7 +178,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     }
     // dR -> global and to the other half; Z (this half's token rows) = diag(beta gamma) Tm^T dR
     const F dRmine = frag_acc2<T>(dR[0], dR[1]);
-    store_fragblk<T>(wsdR + cidx * CH * V, hf, cb, ncb, dRmine);
+    store_fragblk<T, STATE_NT_STORE>(wsdR + cidx * CH * V, hf, cb, ncb, dRmine);
     xR[w][l] = dRmine;
     __syncthreads();
     if (c > 0) prefetch2(c - 1);
@@ -276,11 +289,11 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   // V slab in two groups: A = {dO, V, R, dR} (and Tm, G, beta first) feeds dO R^T, dR V^T and Tm^T dR; B =
   // {S0, dS_C} feeds the products with the states.  Group B and Q, K stay in flight while group A is computed,
   // and the next slab's groups are issued as soon as their registers are free.
-  RegTile<T, CH, K, ITH> tq, tk, tu;
-  RegTile<T, CH, CH, ITH> rtm;
-  RegTile<T, CH, VS, ITH> rdo, rv;
-  FragTile<T, CH, VS, ITH> rr, rdr;
-  FragTile<T, K, VS, ITH> rs0, rdsc;
+  RegTile<T, CH, K, ITH, INTRA_NT> tq, tk, tu;
+  RegTile<T, CH, CH, ITH, INTRA_NT> rtm;
+  RegTile<T, CH, VS, ITH, INTRA_NT> rdo, rv;
+  FragTile<T, CH, VS, ITH, INTRA_NT> rr, rdr;
+  FragTile<T, K, VS, ITH, INTRA_NT> rs0, rdsc;
   auto load_a = [&](int vs) {
     rdo.load(dout + row0 * V + vs, (int64_t)H * V, nvalid, tid);
     rv.load(v + row0 * V + vs, (int64_t)H * V, nvalid, tid);
@@ -358,7 +371,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     }
     __syncthreads();
     if (vs + VS < V) load_b(vs + VS);
-    s2g_rows<T, ITH>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, CH, VS, nvalid);
+    s2g_rows<T, ITH, INTRA_NT>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, CH, VS, nvalid);
 #pragma unroll
     for (int j = 0; j < HK; ++j) {
       const int n = HK * hf + j;
@@ -565,8 +578,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     }
   }
   __syncthreads();
-  s2g_rows<T, ITH>(dq + row0 * K, (int64_t)H * K, sdq, LK, CH, K, nvalid);
-  s2g_rows<T, ITH>(dk + row0 * K, (int64_t)H * K, sdk, LK, CH, K, nvalid);
+  s2g_rows<T, ITH, INTRA_NT>(dq + row0 * K, (int64_t)H * K, sdq, LK, CH, K, nvalid);
+  s2g_rows<T, ITH, INTRA_NT>(dk + row0 * K, (int64_t)H * K, sdk, LK, CH, K, nvalid);
   if constexpr (SEPU) {
     // du staged in the D and dPm regions, free once every wave has passed the barrier above
     T* sdu = sD;
@@ -576,7 +589,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       for (int i = 0; i < 4; ++i)
         sdu[(16 * rb + acc_row(i)) * LK + 16 * (HK * hf + j) + acc_col()] = from_f<T>(aKd[j][i]);
     __syncthreads();
-    s2g_rows<T, ITH>(du + row0 * K, (int64_t)H * K, sdu, LK, CH, K, nvalid);
+    s2g_rows<T, ITH, INTRA_NT>(du + row0 * K, (int64_t)H * K, sdu, LK, CH, K, nvalid);
   }
   if (w == 0) {
     // dG_r -= colsum_r;  dG_last += sum_r dte_r rk_r + gamma_C <dS_C, S0>;  dg = reverse cumsum of dG

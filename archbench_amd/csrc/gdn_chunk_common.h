@@ -127,11 +127,26 @@ __device__ __forceinline__ void tm_column(const float* sA, const float* sD, cons
   for (int i = 0; i < J; ++i) put_tm_block<T, LC>(sTmB, gTm, sB, i, J, zero4());
 }
 
+// Global accesses with the nontemporal hint (NT) stream past the caches' normal replacement: every kernel that
+// reads an input once and writes each output once runs faster with it (measured per kernel; the reverse sweep,
+// whose two V-block workgroups of a head share q, k, Tm and P through L2, keeps ordinary loads).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  if constexpr (NT) return __builtin_bit_cast(uint4, __builtin_nontemporal_load(static_cast<const u32x4*>(p)));
+  else return *static_cast<const uint4*>(p);
+}
+template <bool NT>
+__device__ __forceinline__ void st16(void* p, const uint4& v) {
+  if constexpr (NT) __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), static_cast<u32x4*>(p));
+  else *static_cast<uint4*>(p) = v;
+}
+
 // A ROWS x COLS tile of T held in registers as 16-byte vectors (ROWS*COLS*sizeof(T)/16 split over the NTH
 // threads of a group; tid = thread index inside the group), used to prefetch the next chunk while the
 // current one is computed.  Loads are unconditional: rows past the end of the sequence read row 0 instead
 // (always in bounds) and are zeroed only when the tile is stored, so no wait for the data is forced at load time.
-template <typename T, int ROWS, int COLS, int NTH = NTHR>
+template <typename T, int ROWS, int COLS, int NTH = NTHR, bool NT = false>
 struct RegTile {
   static constexpr int E = 16 / sizeof(T);
   static constexpr int VPR = COLS / E;
@@ -146,7 +161,7 @@ struct RegTile {
       const int idx = tid + i * NTH, row = idx / VPR, c = (idx - row * VPR) * E;
       const bool in = row < valid;
       ok |= (in ? 1u : 0u) << i;
-      r[i] = *reinterpret_cast<const uint4*>(g + (in ? row : 0) * gld + c);
+      r[i] = ld16<NT>(g + (in ? row : 0) * gld + c);
     }
   }
   __device__ __forceinline__ void store(T* s, int sld, int tid) const {
@@ -180,15 +195,17 @@ struct RegTok {
 // elements per lane, lane-contiguous, so each wave writes a block as one contiguous vector store per lane,
 // with no staging.  The gradient kernel turns blocks back into row-major LDS tiles (FragTile).
 __device__ __forceinline__ int fragblk_row(int g, int p) { return p < 4 ? 4 * g + p : 16 + 4 * g + (p - 4); }
-template <typename T>
+template <typename T, bool NT = false>
 __device__ __forceinline__ void store_fragblk(T* base, int s, int cb, int ncb, const typename Frag<T>::type& f) {
-  *reinterpret_cast<typename Frag<T>::type*>(base + ((int64_t)(s * ncb + cb) * 64 + lane_id()) * 8) = f;
+  auto* p = reinterpret_cast<typename Frag<T>::type*>(base + ((int64_t)(s * ncb + cb) * 64 + lane_id()) * 8);
+  if constexpr (NT) __builtin_nontemporal_store(f, p);
+  else *p = f;
 }
 
 // Columns [16 cb0, 16 cb0 + VS) of a fragment-layout [R][V] matrix (ncb = V / 16): loaded into registers as
 // 8-element vectors by the NTH threads of the workgroup (tid = thread index), then written to a row-major LDS
 // tile [R][ld] (column 0 = column 16 cb0).
-template <typename T, int R, int VS, int NTH>
+template <typename T, int R, int VS, int NTH, bool NT = false>
 struct FragTile {
   using F = typename Frag<T>::type;
   static constexpr int NVEC = R * VS / 8;
@@ -202,7 +219,9 @@ struct FragTile {
       const int idx = tid + i * NTH;
       if (NVEC % NTH == 0 || idx < NVEC) {
         const int blk = idx >> 6, ln = idx & 63, s = blk / NCBS, cbl = blk - s * NCBS;
-        r[i] = *reinterpret_cast<const F*>(base + ((int64_t)(s * ncb + cb0 + cbl) * 64 + ln) * 8);
+        const F* p = reinterpret_cast<const F*>(base + ((int64_t)(s * ncb + cb0 + cbl) * 64 + ln) * 8);
+        if constexpr (NT) r[i] = __builtin_nontemporal_load(p);
+        else r[i] = *p;
       }
     }
   }
@@ -237,13 +256,13 @@ struct FragTile {
 
 // Copy a rows x cols tile from LDS (stride sld) to global (row stride gld), 16-byte vectors, rows < valid only,
 // by the NTH threads of the workgroup.
-template <typename T, int NTH = NTHR>
+template <typename T, int NTH = NTHR, bool NT = false>
 __device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld, int rows, int cols, int valid) {
   constexpr int E = 16 / sizeof(T);
   const int vpr = cols / E;
   for (int idx = threadIdx.x; idx < rows * vpr; idx += NTH) {
     const int r = idx / vpr, c = (idx - r * vpr) * E;
-    if (r < valid) *reinterpret_cast<uint4*>(g + r * gld + c) = *reinterpret_cast<const uint4*>(s + r * sld + c);
+    if (r < valid) st16<NT>(g + r * gld + c, *reinterpret_cast<const uint4*>(s + r * sld + c));
   }
 }
 

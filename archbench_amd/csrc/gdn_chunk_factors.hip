@@ -41,7 +41,7 @@ __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict
   __shared__ float sG[CH], sB[CH], sOne[CH];
 
   const int w = wave_id(), l = lane_id();
-  RegTile<T, CH, K> rk, rq, ru;
+  RegTile<T, CH, K, NTHR, true> rk, rq, ru;  // k, q, u are read once here: nontemporal
   RegTok rt;
   auto prefetch = [&](int it) {
     const int bh = it / NT, c = it - bh * NT;
@@ -73,8 +73,8 @@ __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict
     __syncthreads();
     factors_merge<T>(D, sA, sD, sTm, nullptr, sOne, w);
     __syncthreads();
-    s2g_rows(gTm + (int64_t)it * CH * CH, (int64_t)CH, sTm, LC, CH, CH, CH);
-    s2g_rows(gP + (int64_t)it * CH * CH, (int64_t)CH, sP, LC, CH, CH, CH);
+    s2g_rows<T, NTHR, true>(gTm + (int64_t)it * CH * CH, (int64_t)CH, sTm, LC, CH, CH, CH);
+    s2g_rows<T, NTHR, true>(gP + (int64_t)it * CH * CH, (int64_t)CH, sP, LC, CH, CH, CH);
     __syncthreads();  // LDS free for the next item
   }
 }

@@ -25,6 +25,11 @@ namespace gdn {
 // apply the full state update.
 constexpr int FW = 2 * NWAVE;  // waves of the forward sweep
 constexpr int FTH = 64 * FW;
+#ifndef GDN_FWD_NT_LOAD
+#define GDN_FWD_NT_LOAD true
+#endif
+constexpr bool FWD_NT_LOAD = GDN_FWD_NT_LOAD;  // chunk inputs (measured faster with the hint)
+constexpr bool FWD_NT_STORE = true;            // O, and the stashed states and R: written once
 
 template <typename T, int K, int BV, int MODE, bool SEPU>
 __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
@@ -64,9 +69,9 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
-  RegTile<T, CH, K, FTH> rk, rq, ru;
-  RegTile<T, CH, BV, FTH> rv;
-  RegTile<T, CH, CH, FTH> rtm, rp;
+  RegTile<T, CH, K, FTH, FWD_NT_LOAD> rk, rq, ru;
+  RegTile<T, CH, BV, FTH, FWD_NT_LOAD> rv;
+  RegTile<T, CH, CH, FTH, FWD_NT_LOAD> rtm, rp;
   float pG = 0.f, pB = 0.f;  // wave 0: G and beta of lane l's token
   // The next chunk's reads go out in two batches (k, q, v after the first barrier; Tm, P, G, beta after the
   // second exchange), so that no wave stalls on a full memory queue for the whole set at once.
@@ -121,7 +126,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     for (int s = 0; s < K / 32; ++s) {
       Sb[s] = frag_acc2<T>(S[2 * s], S[2 * s + 1]);
       if constexpr (SAVE) {
-        if ((s & 1) == hf) store_fragblk<T>(wsH + cidx * K * V, s, cb, ncb, Sb[s]);
+        if ((s & 1) == hf) store_fragblk<T, FWD_NT_STORE>(wsH + cidx * K * V, s, cb, ncb, Sb[s]);
       }
     }
     f32x4 Y[2], QS[2];
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     }
     const F Rbmine = frag_acc2<T>(R[0], R[1]);
     if constexpr (OUT) xR[w][l] = Rbmine;
-    if constexpr (SAVE) store_fragblk<T>(wsR + cidx * CH * V, hf, cb, ncb, Rbmine);
+    if constexpr (SAVE) store_fragblk<T, FWD_NT_STORE>(wsR + cidx * CH * V, hf, cb, ncb, Rbmine);
     __syncthreads();  // R and Rd fragments of both halves exchanged
     if (c + 1 < NT) prefetch2(c + 1);
     const F Rdother = xRd[w ^ NWAVE][l];
@@ -202,7 +207,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     }
     __syncthreads();  // O staged; every wave done with this chunk's inputs
     if constexpr (OUT)
-      s2g_rows<T, FTH>(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, CH, BV, nvalid_of(c));
+      s2g_rows<T, FTH, FWD_NT_STORE>(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, CH, BV, nvalid_of(c));
   };
   prefetch(0);
   prefetch2(0);

@@ -217,13 +217,15 @@ __device__ __forceinline__ float sum16(float x) {
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 __device__ __forceinline__ float fast_sigmoid(float z) { return fast_rcp(1.f + __expf(-z)); }
 
-// 8 consecutive elements of a row as loaded (16 B in bf16, 32 B in fp32), converted to fp32 at use
+// 8 consecutive elements of a row as loaded (16 B in bf16, 32 B in fp32), converted to fp32 at use.  The row
+// kernels read and write each element once, so loads and stores carry the nontemporal hint (measured: the
+// gated RMSNorm forward 77 -> 67 us, the cross-entropy kernel 634 -> 573 us)
 template <typename T>
 struct Row8;
 template <>
 struct Row8<bf16> {
   bf16x8 r;
-  __device__ __forceinline__ void load(const bf16* p) { r = *reinterpret_cast<const bf16x8*>(p); }
+  __device__ __forceinline__ void load(const bf16* p) { r = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p)); }
   __device__ __forceinline__ void get(float (&v)[8]) const {
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = static_cast<float>(r[j]);
@@ -233,8 +235,8 @@ template <>
 struct Row8<float> {
   f32x4 a, b;
   __device__ __forceinline__ void load(const float* p) {
-    a = *reinterpret_cast<const f32x4*>(p);
-    b = *reinterpret_cast<const f32x4*>(p + 4);
+    a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
   }
   __device__ __forceinline__ void get(float (&v)[8]) const {
 #pragma unroll
@@ -250,10 +252,10 @@ __device__ __forceinline__ void store_row8(T* p, const float (&v)[8]) {
     bf16x8 r;
 #pragma unroll
     for (int j = 0; j < 8; ++j) r[j] = static_cast<bf16>(v[j]);
-    *reinterpret_cast<bf16x8*>(p) = r;
+    __builtin_nontemporal_store(r, reinterpret_cast<bf16x8*>(p));
   } else {
-    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+    __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4*>(p));
+    __builtin_nontemporal_store(f32x4{v[4], v[5], v[6], v[7]}, reinterpret_cast<f32x4*>(p + 4));
   }
 }
 

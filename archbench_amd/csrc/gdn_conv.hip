@@ -29,13 +29,16 @@ constexpr int CONV_UF = 8;  // token rows per load batch, forward
 constexpr int CONV_UB = 8;  // token rows of x and of dy per load batch, backward
 
 // CONV_CPL = 4 consecutive channels of one token row as loaded (8 B in bf16, 16 B in fp32), converted at use so
-// that a whole batch of loads is in flight at once
+// that a whole batch of loads is in flight at once.  load_nt / store4<T, true> carry the nontemporal hint: the
+// backward reads x and dy and writes dx once each and runs 7-17% faster with it; the forward, whose workgroups
+// re-read a few halo rows of their neighbours, runs slower with it and keeps ordinary accesses.
 template <typename T>
 struct Row4;
 template <>
 struct Row4<bf16> {
   bf16x4 r;
   __device__ __forceinline__ void load(const bf16* p) { r = *reinterpret_cast<const bf16x4*>(p); }
+  __device__ __forceinline__ void load_nt(const bf16* p) { r = __builtin_nontemporal_load(reinterpret_cast<const bf16x4*>(p)); }
   __device__ __forceinline__ void get(float (&v)[4]) const {
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = static_cast<float>(r[j]);
@@ -45,19 +48,23 @@ template <>
 struct Row4<float> {
   f32x4 r;
   __device__ __forceinline__ void load(const float* p) { r = *reinterpret_cast<const f32x4*>(p); }
+  __device__ __forceinline__ void load_nt(const float* p) { r = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p)); }
   __device__ __forceinline__ void get(float (&v)[4]) const {
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = r[j];
   }
 };
 
-template <typename T>
+template <typename T, bool NT = false>
 __device__ __forceinline__ void store4(T* p, const float (&v)[4]) {
   if constexpr (sizeof(T) == 2) {
-    *reinterpret_cast<bf16x4*>(p) = bf16x4{static_cast<bf16>(v[0]), static_cast<bf16>(v[1]),
-                                           static_cast<bf16>(v[2]), static_cast<bf16>(v[3])};
+    const bf16x4 r{static_cast<bf16>(v[0]), static_cast<bf16>(v[1]), static_cast<bf16>(v[2]), static_cast<bf16>(v[3])};
+    if constexpr (NT) __builtin_nontemporal_store(r, reinterpret_cast<bf16x4*>(p));
+    else *reinterpret_cast<bf16x4*>(p) = r;
   } else {
-    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+    const f32x4 r{v[0], v[1], v[2], v[3]};
+    if constexpr (NT) __builtin_nontemporal_store(r, reinterpret_cast<f32x4*>(p));
+    else *reinterpret_cast<f32x4*>(p) = r;
   }
 }
 // sum over the NG / CONV_CPL lanes of a normalisation group (aligned runs of lanes), the same value in every lane
@@ -236,7 +243,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
       }
       if (on) {
         if (p >= 0) {
-          store4(dxl + (int64_t)p * D, o);
+          store4<T, true>(dxl + (int64_t)p * D, o);
         } else if (dstate_in) {
 #pragma unroll
           for (int j = 0; j < CPL; ++j) dstate_in[srow + (int64_t)j * (W - 1) + (W - 1) + p] = from_f<T>(o[j]);
@@ -303,8 +310,8 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
     Row4<T> bx[U], bd[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      bx[u].load(xl + (int64_t)(t0 + u) * D);
-      bd[u].load(dyl + (int64_t)(t0 + u) * D);
+      bx[u].load_nt(xl + (int64_t)(t0 + u) * D);
+      bd[u].load_nt(dyl + (int64_t)(t0 + u) * D);
     }
     for (int n = 0; n < nfull; ++n, s += U) {
       Row4<T> cx[U], cd[U];
@@ -316,8 +323,8 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
       const int sn = min(s + U, t1 - U);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        bx[u].load(xl + (int64_t)(sn + u) * D);
-        bd[u].load(dyl + (int64_t)(sn + u) * D);
+        bx[u].load_nt(xl + (int64_t)(sn + u) * D);
+        bd[u].load_nt(dyl + (int64_t)(sn + u) * D);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) step(s + u, cx[u], cd[u], Own{});
@@ -325,15 +332,15 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
   }
   for (; s < t1; ++s) {
     Row4<T> xr, dr;
-    xr.load(xl + (int64_t)s * D);
-    dr.load(dyl + (int64_t)s * D);
+    xr.load_nt(xl + (int64_t)s * D);
+    dr.load_nt(dyl + (int64_t)s * D);
     step(s, xr, dr, Own{});
   }
   const int send = min(Tn, t1 + W - 1);
   for (; s < send; ++s) {
     Row4<T> xr, dr;
-    xr.load(xl + (int64_t)s * D);
-    dr.load(dyl + (int64_t)s * D);
+    xr.load_nt(xl + (int64_t)s * D);
+    dr.load_nt(dyl + (int64_t)s * D);
     step(s, xr, dr, LookAhead{});
   }
   // past the sequence end dz = 0: flush the remaining dx of the chunk's tail (and of the state when Tn is short)
