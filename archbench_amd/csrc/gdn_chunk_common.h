@@ -267,14 +267,15 @@ __device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld,
 }
 
 // ---- chunk factors, in three barrier-separated phases ------------------------------------------------------
-// The sweeps call these for the *next* chunk while they run the state part of the current one, so each phase
-// is a separate function and the caller places the barriers between them.
+// Each phase is a separate function; the caller places the barriers between them.
 //
 // factors_kq: K U^T and Q U^T on MFMA (row block = wave), then
 //   A_ij = beta_i (K U^T)_ij exp(G_i - G_j) (i > j) -> sA  (fp32, strict lower)
 //   P_ij = s (Q U^T)_ij exp(G_i - G_j) (i >= j)     -> sP  (PMODE 1, row-major; PMODE 0: none, sQ unused)
 // U is the write key (U = K for the gated delta rule).  Inputs: sK, sU (and sQ) rows of the chunk, zero past the
-// sequence end; sG (cumulative log-decay); sB (row scale beta, zero past the end).
+// sequence end; sG (cumulative log-decay); sB (row scale beta, zero past the end).  Wave w reads only rows
+// 16w..16w+15 of sK and sQ and writes only the same rows of sA and sP, and its K and Q fragments are all read
+// before its first write, so sA may share memory with sQ row for row (same row pitch in bytes).
 template <typename T, int K, int PMODE>
 __device__ __forceinline__ void factors_kq(const T* sK, const T* sU, const T* sQ, const float* sG, const float* sB,
                                            float scale, float* sA, T* sP, int w) {
@@ -295,6 +296,7 @@ __device__ __forceinline__ void factors_kq(const T* sK, const T* sU, const T* sQ
     ak[s] = frag_kc(sK, LK, 16 * w, 32 * s);
     if constexpr (PMODE != 0) aq[s] = frag_kc(sQ, LK, 16 * w, 32 * s);
   }
+  asm volatile("" ::: "memory");  // the reads above stay ahead of the sA writes below (sA may overlay sQ)
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
     f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};

@@ -22,22 +22,30 @@ namespace gdn {
 
 // Persistent: workgroup x handles items x, x + gridDim.x, ... of the (b*h, chunk) grid (item = bh * NT + c), with
 // the next item's k, q, g and beta prefetched into registers while the current one is factored.
+// LDS overlays keep a workgroup at about 50 KB (bf16, K = 128), so three share a CU: A (fp32) overlays Q row for
+// row where the row pitches match (see factors_kq), and Tm overlays K once every wave has finished K U^T.
+template <typename T, int K>
+constexpr bool factors_a_on_q() { return (K + 16 / (int)sizeof(T)) * (int)sizeof(T) == (CH + 4) * 4; }
+
 template <typename T, int K, bool SEPU>
-__global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k,
-                                                             const T* __restrict__ u, const float* __restrict__ g,
-                                                             const float* __restrict__ beta, T* __restrict__ gTm,
-                                                             T* __restrict__ gP, float* __restrict__ gGc, int T_,
-                                                             int H, int NT, int nitems, float scale) {
+__global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3)))
+void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u,
+                          const float* __restrict__ g, const float* __restrict__ beta, T* __restrict__ gTm,
+                          T* __restrict__ gP, float* __restrict__ gGc, int T_, int H, int NT, int nitems,
+                          float scale) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LF = CH + 4;
-  __shared__ __attribute__((aligned(16))) T sK[CH * LK];
-  __shared__ __attribute__((aligned(16))) T sQ[CH * LK];
+  constexpr bool A_ON_Q = factors_a_on_q<T, K>();
+  static_assert(LC <= LK, "Tm must fit in the K tile");
+  __shared__ __attribute__((aligned(16))) T sK[CH * LK];  // K, then Tm (stride LC)
+  __shared__ __attribute__((aligned(16))) T sQ[CH * LK];  // Q, then A where the pitches match
   __shared__ __attribute__((aligned(16))) T sU_[SEPU ? CH * LK : 8];
   T* sU = SEPU ? sU_ : sK;
-  __shared__ __attribute__((aligned(16))) float sA[CH * LF];
+  __shared__ __attribute__((aligned(16))) float sA_[A_ON_Q ? 4 : CH * LF];
+  float* sA = A_ON_Q ? reinterpret_cast<float*>(sQ) : sA_;
   __shared__ __attribute__((aligned(16))) float sD[4 * DBLK];
   __shared__ __attribute__((aligned(16))) T sP[CH * LC];
-  __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
+  T* sTm = sK;
   __shared__ float sG[CH], sB[CH], sOne[CH];
 
   const int w = wave_id(), l = lane_id();
@@ -68,7 +76,7 @@ __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict
     __syncthreads();
     if (it + (int)gridDim.x < nitems) prefetch(it + gridDim.x);
     factors_kq<T, K, 1>(sK, sU, sQ, sG, sB, scale, sA, sP, w);
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the diagonal block reads this wave's rows of A
+    __syncthreads();  // every wave done with K (Tm overwrites it); A written
     const f32x4 D = factors_diag<T>(sA, sD, sTm, nullptr, sOne, w);
     __syncthreads();
     factors_merge<T>(D, sA, sD, sTm, nullptr, sOne, w);
@@ -82,7 +90,7 @@ __global__ __launch_bounds__(NTHR) void chunk_factors_kernel(const T* __restrict
 template <typename T, int K, bool SEPU>
 static hipError_t factors_k(const ChunkArgs& a) {
   const int nitems = a.NT * a.B * a.H;
-  const int per_cu = sizeof(T) == 2 && !SEPU ? 2 : 1;  // workgroups resident per CU (LDS)
+  const int per_cu = sizeof(T) == 2 && !SEPU ? 3 : 2;  // workgroups resident per CU (LDS)
   dim3 grid(std::min(nitems, per_cu * device_cu_count()));
   chunk_factors_kernel<T, K, SEPU><<<grid, NTHR, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u), a.g, a.beta,
