@@ -155,6 +155,21 @@ def test_stash_pair_equals_plain_and_recompute(dtype, T, K, V):
             assert rel_l2(a, b) <= BF16_TOL, (n, rel_l2(a, b))
 
 
+def test_training_pair_repeatable_bitwise():
+    """Every reduction is in a fixed order (no atomics): two runs of the training pair on the same inputs give
+    identical bits, at a shape with thousands of workgroups and a ragged last chunk."""
+    banner("training pair repeatability B=4 T=1000 H=8 K=V=128 bf16")
+    _, dev = device_inputs(4, 1000, 8, 128, 128, torch.bfloat16, h0_std=0.1, with_do=True, seed=21)
+    runs = []
+    for _ in range(2):
+        o, hT, stash = ops.chunk_fwd_stash(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, 0.7)
+        grads = ops.chunk_bwd_stashed(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, dev.do, None, stash, 0.7)
+        torch.cuda.synchronize()
+        runs.append((o, hT) + tuple(grads))
+    for n, a, b in zip(("o", "hT", *NAMES), runs[0], runs[1]):
+        assert torch.equal(a, b), n
+
+
 def test_state_passing_on_gpu():
     banner("state passing")
     host, dev = device_inputs(2, 300, 2, 128, 128, torch.bfloat16, h0_std=0.1)
