@@ -17,21 +17,11 @@ namespace gdn {
 constexpr int CE_THREADS = 1024;
 constexpr int CE_WAVES = CE_THREADS / 64;
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m));
-  return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) x += __shfl_xor(x, m);
-  return x;
-}
 
 // reduce over the block: every thread gets the result
 template <bool MAX>
 __device__ __forceinline__ float block_reduce(float x, float* red) {
-  x = MAX ? wave_max(x) : wave_sum(x);
+  x = MAX ? wave_max64(x) : wave_sum64(x);
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) red[w] = x;
   __syncthreads();

@@ -230,10 +230,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
 // ---------------------------------------------------------------------------------------------------------
 // Sum of the 4 rows a lane holds plus the other 3 lane groups: the per-column sum of a 16x16 tile.
 __device__ __forceinline__ float colsum_tile(const f32x4& x) {
-  float s = x[0] + x[1] + x[2] + x[3];
-  s += __shfl_xor(s, 16);
-  s += __shfl_xor(s, 32);
-  return s;
+  return xor32_sum(xor16_sum(x[0] + x[1] + x[2] + x[3]));
 }
 
 // Eight waves, two per SIMD: wave w owns row block rb = w & 3 (16 tokens of the chunk) and half hf = w >> 2 of
@@ -383,9 +380,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   }
   // block reduce <dS_C, S0>
   {
-    float x = sdot;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    const float x = wave_sum64(sdot);
     if (l == 0) sRed[w] = x;
   }
 
@@ -594,16 +589,14 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   if (w == 0) {
     // dG_r -= colsum_r;  dG_last += sum_r dte_r rk_r + gamma_C <dS_C, S0>;  dg = reverse cumsum of dG
     float x = sdG[l] - (sColZ[0][l] + sColZ[1][l] + sColZ[2][l] + sColZ[3][l]);
-    float last = sLast[l];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) last += __shfl_xor(last, off);
+    float last = wave_sum64(sLast[l]);
     float red = 0.f;
 #pragma unroll
     for (int i = 0; i < IW; ++i) red += sRed[i];
     last += __expf(GC) * red;
     if (l == CH - 1) x += last;
     const float incl = wave_inclusive_scan(x);
-    const float total = __shfl(incl, 63);
+    const float total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), 63));
     if (l < nvalid) dg[row0 + (int64_t)l * H] = total - incl + x;
   }
 }

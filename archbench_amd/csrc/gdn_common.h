@@ -259,16 +259,52 @@ __device__ __forceinline__ void store_row8(T* p, const float (&v)[8]) {
   }
 }
 
+// Across the 16-lane rows of a wave, without the LDS crossbar: v_permlane16_swap returns x's rows (0,0,2,2) and
+// (1,1,3,3), v_permlane32_swap rows (0,1,0,1) and (2,3,2,3) (each lane keeps its position inside the row), so one
+// swap and one add (or max) combine lanes l and l ^ 16, or l and l ^ 32.
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// lanes l and l ^ 8 inside a row (row_ror:8)
+__device__ __forceinline__ float xor8_sum(float x) { return dpp_sum_step<0x128>(x); }
+
+// Sum / max over the whole wave, the result in every lane
+__device__ __forceinline__ float wave_sum64(float x) { return xor32_sum(xor16_sum(sum16(x))); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_max_step(float x) {
+  return fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false)));
+}
+__device__ __forceinline__ float wave_max64(float x) {
+  x = dpp_max_step<0xb1>(x);
+  x = dpp_max_step<0x4e>(x);
+  x = dpp_max_step<0x141>(x);
+  x = dpp_max_step<0x140>(x);
+  return xor32_max(xor16_max(x));
+}
+
 // Sum over aligned runs of LANES lanes (1, 2, 4, ..., 64), the same value left in every lane of the run: DPP
-// butterflies within 16 lanes (as sum16), lane shuffles across rows.
+// butterflies within 16 lanes (as sum16), row swaps across rows.
 template <int LANES>
 __device__ __forceinline__ float lane_group_sum(float s) {
   if constexpr (LANES >= 2) s = dpp_sum_step<0xb1>(s);
   if constexpr (LANES >= 4) s = dpp_sum_step<0x4e>(s);
   if constexpr (LANES >= 8) s = dpp_sum_step<0x141>(s);
   if constexpr (LANES >= 16) s = dpp_sum_step<0x140>(s);
-  if constexpr (LANES >= 32) s += __shfl_xor(s, 16);
-  if constexpr (LANES >= 64) s += __shfl_xor(s, 32);
+  if constexpr (LANES >= 32) s = xor16_sum(s);
+  if constexpr (LANES >= 64) s = xor32_sum(s);
   return s;
 }
 
@@ -287,21 +323,6 @@ __device__ __forceinline__ float wave_inclusive_scan(float x) {
   x = dpp_add<0x142, 0xa>(x);  // row_bcast:15
   x = dpp_add<0x143, 0xc>(x);  // row_bcast:31
   return x;
-}
-
-// Copy a rows x cols tile of T from global (row stride gld elements) into LDS (row stride sld), 16-byte
-// vectors, zero-filling rows >= valid_rows.  cols * sizeof(T) must be a multiple of 16.
-template <typename T>
-__device__ __forceinline__ void g2s_rows(T* s, int sld, const T* g, int64_t gld, int rows, int cols,
-                                         int valid_rows) {
-  constexpr int E = 16 / sizeof(T);
-  const int vpr = cols / E;
-  for (int idx = threadIdx.x; idx < rows * vpr; idx += blockDim.x) {
-    const int r = idx / vpr, c = (idx - r * vpr) * E;
-    uint4 val = make_uint4(0, 0, 0, 0);
-    if (r < valid_rows) val = *reinterpret_cast<const uint4*>(g + r * gld + c);
-    *reinterpret_cast<uint4*>(s + r * sld + c) = val;
-  }
 }
 
 }  // namespace gdn

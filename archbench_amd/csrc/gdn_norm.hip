@@ -148,9 +148,11 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void row_norm_bwd_kernel(
   if constexpr (MODE == L2) return;  // no parameter gradient (uniform exit: no barrier follows)
   // lanes with the same channels (l mod LPR) hold different rows: butterfly over them
 #pragma unroll
-  for (int m = LPR; m < 64; m <<= 1)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) dwa[j] += __shfl_xor(dwa[j], m);
+  for (int j = 0; j < 8; ++j) {
+    if constexpr (LPR <= 8) dwa[j] = xor8_sum(dwa[j]);
+    if constexpr (LPR <= 16) dwa[j] = xor16_sum(dwa[j]);
+    dwa[j] = xor32_sum(dwa[j]);
+  }
   if (sub == 0) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) red[wv][c0 + j] = dwa[j];

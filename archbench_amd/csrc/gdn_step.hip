@@ -42,8 +42,7 @@ __global__ __launch_bounds__(256) void step_kernel(const T* __restrict__ q, cons
   if (tid < 64) {
     float x = 0.f;
     for (int i = tid; i < K; i += 64) x += sk[i] * sq[i];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    x = wave_sum64(x);
     if (tid == 0) s_kq = x;
   }
   f32x4 ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
