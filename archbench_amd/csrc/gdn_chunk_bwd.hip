@@ -345,10 +345,12 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       const int n = HV * hf + j;
       f32x4 dy = {0.f, 0.f, 0.f, 0.f};
       mma_blk<false, true, CH>(dy, sTm, LC, 16 * rb, sdRt, LC, 16 * n);
+      float vv[4];
+      acc_vals(sV, LS, 16 * rb, 16 * n, vv);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 16 * rb + acc_row(i), vc = 16 * n + acc_col();
-        dbV[i] += dy[i] * to_f(sV[r * LS + vc]);
+        dbV[i] += dy[i] * vv[i];
         sdv[r * LS + vc] = from_f<T>(sB[r] * dy[i]);
       }
     }
@@ -406,11 +408,14 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   float rq[4] = {0.f, 0.f, 0.f, 0.f}, rk[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < HK; ++j) {
+    float qv[4], uv[4];
+    acc_vals(sQ, LK, 16 * rb, 16 * (HK * hf + j), qv);
+    acc_vals(sU, LK, 16 * rb, 16 * (HK * hf + j), uv);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rb + acc_row(i), d = 16 * (HK * hf + j) + acc_col();
-      rq[i] += aQg[j][i] * to_f(sQ[r * LK + d]);
-      rk[i] += aKd[j][i] * to_f(sU[r * LK + d]);
+      rq[i] += aQg[j][i] * qv[i];
+      rk[i] += aKd[j][i] * uv[i];
       sdWn[r * LK + d] = from_f<T>(aWn[j][i]);
     }
   }
@@ -425,11 +430,10 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
     mma_blk<false, false, CH>(t, sTm, LC, 16 * rb, sdWn, LK, 16 * n);
     aX[j] = -t;
+    float kv[4];
+    acc_vals(sK, LK, 16 * rb, 16 * n, kv);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
-      rx[i] += aX[j][i] * to_f(sK[r * LK + d]);
-    }
+    for (int i = 0; i < 4; ++i) rx[i] += aX[j][i] * kv[i];
   }
   // dTm rows:  dTm_ij = -beta_j gamma_j (dWn K^T)_ij + beta_j (dR V^T)_ij
 #pragma unroll

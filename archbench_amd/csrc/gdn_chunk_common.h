@@ -266,6 +266,20 @@ __device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld,
   }
 }
 
+// The elements of a row-major LDS tile at this lane's accumulator positions of output tile (rows r0.., columns
+// c0..): rows r0 + 4 (l >> 4) + i (i = 0..3) of column c0 + (l & 15).  bf16: one transposing read.
+template <typename T>
+__device__ __forceinline__ void acc_vals(const T* p, int ld, int r0, int c0, float (&v)[4]) {
+  if constexpr (sizeof(T) == 2) {
+    const bf16x4 t = ld_tr4(p, ld, c0, r0 + 4 * (lane_id() >> 4));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = to_f(t[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = p[(r0 + acc_row(i)) * ld + c0 + acc_col()];
+  }
+}
+
 // ---- chunk factors, in three barrier-separated phases ------------------------------------------------------
 // Each phase is a separate function; the caller places the barriers between them.
 //

@@ -141,10 +141,12 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
 #pragma unroll
         for (int s = 0; s < K / 32; ++s) mma(QS[j], frag_kc_perm(sQ, LK, 16 * rt_, 32 * s), Sb[s]);
       }
+      float vv[4];
+      acc_vals(sV, LV, 16 * rt_, c0, vv);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 16 * rt_ + acc_row(i);
-        Y[j][i] = sB[r] * (to_f(sV[r * LV + c0 + acc_col()]) - sGam[r] * ks[i]);
+        Y[j][i] = sB[r] * (vv[i] - sGam[r] * ks[i]);
       }
     }
     // (fragments are selected by value, never indexed by the half: registers cannot be indexed at run time)
