@@ -159,6 +159,10 @@ static int check_common(int B, int T, int H, int K, int V, int dtype) {
     return fail(GDN_ERR_ARG, "invalid sizes B=%d T=%d H=%d K=%d V=%d", B, T, H, K, V);
   if ((int64_t)B * T * H * (K > V ? K : V) >= ((int64_t)1 << 31) * 16)
     return fail(GDN_ERR_ARG, "tensor too large for 64-bit indexing plan");
+  // the chunk kernels address one chunk's 64 token rows (row stride H*K or H*V) with 32-bit byte offsets
+  if ((int64_t)H * (K > V ? K : V) * CH_TOKENS * (dtype == DT_BF16 ? 2 : 4) >= ((int64_t)1 << 31))
+    return fail(GDN_ERR_ARG, "H * max(K, V) = %lld too large for a chunk's 32-bit row offsets",
+                (long long)H * (K > V ? K : V));
   return GDN_OK;
 }
 

@@ -69,9 +69,9 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
-  RegTile<T, CH, K, FTH, FWD_NT_LOAD> rk, rq, ru;
-  RegTile<T, CH, BV, FTH, FWD_NT_LOAD> rv;
-  RegTile<T, CH, CH, FTH, FWD_NT_LOAD> rtm, rp;
+  RegTile<T, CH, K, FTH, FWD_NT_LOAD, false> rk, rq, ru;
+  RegTile<T, CH, BV, FTH, FWD_NT_LOAD, false> rv;
+  RegTile<T, CH, CH, FTH, FWD_NT_LOAD, false> rtm, rp;
   float pG = 0.f, pB = 0.f;  // wave 0: G and beta of lane l's token
   // The next chunk's reads go out in two batches (k, q, v after the first barrier; Tm, P, G, beta after the
   // second exchange), so that no wave stalls on a full memory queue for the whole set at once.
