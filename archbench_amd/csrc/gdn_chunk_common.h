@@ -231,15 +231,23 @@ struct FragTile {
   static constexpr int NCBS = VS / 16;
   static_assert(R % 32 == 0 && VS % 16 == 0 && NVEC % 64 == 0, "whole fragment blocks only");
   F r[N];
+  // base: the chunk's [R][16 ncb] matrix; bf16 reads go through a buffer resource over it (32-bit offsets)
   __device__ __forceinline__ void load(const T* base, int ncb, int cb0, int tid) {
+    [[maybe_unused]] const auto rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), 0, R * ncb * 16 * (int)sizeof(T), BUF_RSRC_WORD3);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int idx = tid + i * NTH;
       if (NVEC % NTH == 0 || idx < NVEC) {
         const int blk = idx >> 6, ln = idx & 63, s = blk / NCBS, cbl = blk - s * NCBS;
-        const F* p = reinterpret_cast<const F*>(base + ((int64_t)(s * ncb + cb0 + cbl) * 64 + ln) * 8);
-        if constexpr (NT) r[i] = __builtin_nontemporal_load(p);
-        else r[i] = *p;
+        const int e = ((s * ncb + cb0 + cbl) * 64 + ln) * 8;
+        if constexpr (sizeof(T) == 2) {
+          r[i] = __builtin_bit_cast(F, __builtin_amdgcn_raw_buffer_load_b128(rs, e * 2, 0, NT ? 2 : 0));
+        } else {
+          const F* p = reinterpret_cast<const F*>(base + e);
+          if constexpr (NT) r[i] = __builtin_nontemporal_load(p);
+          else r[i] = *p;
+        }
       }
     }
   }
@@ -278,9 +286,13 @@ template <typename T, int NTH = NTHR, bool NT = false>
 __device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld, int rows, int cols, int valid) {
   constexpr int E = 16 / sizeof(T);
   const int vpr = cols / E;
+  // buffer stores over the valid rows only: the range check drops the rest (32-bit offsets, as for RegTile)
+  const int nbytes = valid > 0 ? ((valid - 1) * (int)gld + cols) * (int)sizeof(T) : 0;
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc(g, 0, nbytes, BUF_RSRC_WORD3);
   for (int idx = threadIdx.x; idx < rows * vpr; idx += NTH) {
     const int r = idx / vpr, c = (idx - r * vpr) * E;
-    if (r < valid) st16<NT>(g + r * gld + c, *reinterpret_cast<const uint4*>(s + r * sld + c));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(s + r * sld + c)),
+                                           rs, (r * (int)gld + c) * (int)sizeof(T), 0, NT ? 2 : 0);
   }
 }
 
