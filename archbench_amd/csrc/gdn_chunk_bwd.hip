@@ -144,7 +144,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
 #pragma unroll
     for (int s = 0; s < NSH; ++s) {
       dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
-      store_fragblk<T, STATE_NT_STORE>(wsdH + cidx * K * V, NSH * hf + s, cb, ncb, dSb[s]);
+      store_fragblk<T, STATE_NT_STORE>(wsdH + cidx * K * V, K, NSH * hf + s, cb, ncb, dSb[s]);
     }
     f32x4 kd[4];
 #pragma unroll
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     }
     // dR -> global and to the other half; Z (this half's token rows) = diag(beta gamma) Tm^T dR
     const F dRmine = frag_acc2<T>(dR[0], dR[1]);
-    store_fragblk<T, STATE_NT_STORE>(wsdR + cidx * CH * V, hf, cb, ncb, dRmine);
+    store_fragblk<T, STATE_NT_STORE>(wsdR + cidx * CH * V, CH, hf, cb, ncb, dRmine);
     xR[w][l] = dRmine;
     __syncthreads();
     if (c > 0) prefetch2(c - 1);

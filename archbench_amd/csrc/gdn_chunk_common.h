@@ -214,10 +214,18 @@ struct RegTok {
 // with no staging.  The gradient kernel turns blocks back into row-major LDS tiles (FragTile).
 __device__ __forceinline__ int fragblk_row(int g, int p) { return p < 4 ? 4 * g + p : 16 + 4 * g + (p - 4); }
 template <typename T, bool NT = false>
-__device__ __forceinline__ void store_fragblk(T* base, int s, int cb, int ncb, const typename Frag<T>::type& f) {
-  auto* p = reinterpret_cast<typename Frag<T>::type*>(base + ((int64_t)(s * ncb + cb) * 64 + lane_id()) * 8);
-  if constexpr (NT) __builtin_nontemporal_store(f, p);
-  else *p = f;
+__device__ __forceinline__ void store_fragblk(T* base, int rows, int s, int cb, int ncb,
+                                              const typename Frag<T>::type& f) {
+  // base: the chunk's [rows][16 ncb] matrix; bf16 blocks are written through a buffer resource over it
+  const int e = ((s * ncb + cb) * 64 + lane_id()) * 8;
+  if constexpr (sizeof(T) == 2) {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(base, 0, rows * ncb * 16 * 2, BUF_RSRC_WORD3);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f), rs, e * 2, 0, NT ? 2 : 0);
+  } else {
+    auto* p = reinterpret_cast<typename Frag<T>::type*>(base + e);
+    if constexpr (NT) __builtin_nontemporal_store(f, p);
+    else *p = f;
+  }
 }
 
 // Columns [16 cb0, 16 cb0 + VS) of a fragment-layout [R][V] matrix (ncb = V / 16): loaded into registers as

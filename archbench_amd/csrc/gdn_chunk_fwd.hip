@@ -126,7 +126,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     for (int s = 0; s < K / 32; ++s) {
       Sb[s] = frag_acc2<T>(S[2 * s], S[2 * s + 1]);
       if constexpr (SAVE) {
-        if ((s & 1) == hf) store_fragblk<T, FWD_NT_STORE>(wsH + cidx * K * V, s, cb, ncb, Sb[s]);
+        if ((s & 1) == hf) store_fragblk<T, FWD_NT_STORE>(wsH + cidx * K * V, K, s, cb, ncb, Sb[s]);
       }
     }
     f32x4 Y[2], QS[2];
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     }
     const F Rbmine = frag_acc2<T>(R[0], R[1]);
     if constexpr (OUT) xR[w][l] = Rbmine;
-    if constexpr (SAVE) store_fragblk<T, FWD_NT_STORE>(wsR + cidx * CH * V, hf, cb, ncb, Rbmine);
+    if constexpr (SAVE) store_fragblk<T, FWD_NT_STORE>(wsR + cidx * CH * V, CH, hf, cb, ncb, Rbmine);
     __syncthreads();  // R and Rd fragments of both halves exchanged
     if (c + 1 < NT) prefetch2(c + 1);
     const F Rdother = xRd[w ^ NWAVE][l];
