@@ -400,6 +400,8 @@ static int conv_check(int B, int T, int D, int W, int norm_group, int dtype) {
   if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
   if (B < 0 || T < 0 || D <= 0 || W <= 0 || norm_group < 0)
     return fail(GDN_ERR_ARG, "invalid sizes B=%d T=%d D=%d W=%d norm_group=%d", B, T, D, W, norm_group);
+  if ((int64_t)T * D * (dtype == DT_BF16 ? 2 : 4) >= ((int64_t)1 << 31))
+    return fail(GDN_ERR_ARG, "T * D = %lld too large for the conv backward's 32-bit row offsets", (long long)T * D);
   if (!conv_shape_supported(D, W, norm_group))
     return fail(GDN_ERR_SHAPE, "short conv not compiled for D=%d W=%d norm_group=%d (D %% 4 == 0, W = 4, "
                 "norm_group in {0, 64, 128, 256} dividing D)", D, W, norm_group);

@@ -130,7 +130,6 @@ __device__ __forceinline__ void tm_column(const float* sA, const float* sD, cons
 // Global accesses with the nontemporal hint (NT) stream past the caches' normal replacement: every kernel that
 // reads an input once and writes each output once runs faster with it (measured per kernel; the reverse sweep,
 // whose two V-block workgroups of a head share q, k, Tm and P through L2, keeps ordinary loads).
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 template <bool NT>
 __device__ __forceinline__ uint4 ld16(const void* p) {
   if constexpr (NT) return __builtin_bit_cast(uint4, __builtin_nontemporal_load(static_cast<const u32x4*>(p)));
@@ -151,7 +150,6 @@ __device__ __forceinline__ void st16(void* p, const uint4& v) {
 //  * otherwise, global loads: rows past the end read row 0 instead (always in bounds) and are zeroed only when
 //    the tile is stored, so no wait for the data is forced at load time.
 // (Measured: BUF is 4% faster in the reverse sweep and 2% slower in the forward sweep.)
-constexpr int BUF_RSRC_WORD3 = 0x00020000;  // raw buffer, 32-bit data format (CDNA)
 template <typename T, int ROWS, int COLS, int NTH = NTHR, bool NT = false, bool BUF = true>
 struct RegTile {
   static constexpr int E = 16 / sizeof(T);

@@ -21,6 +21,13 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Word 3 of a raw buffer resource (__builtin_amdgcn_make_buffer_rsrc) on CDNA: 32-bit data format.  Buffer
+// accesses take a uniform base in SGPRs and a 32-bit per-lane byte offset, and the hardware range check returns
+// zeros for loads (and drops stores) at or past num_records.
+constexpr int BUF_RSRC_WORD3 = 0x00020000;
 
 template <typename T> struct Frag;
 template <> struct Frag<bf16> { using type = bf16x8; };

@@ -29,16 +29,20 @@ constexpr int CONV_UF = 8;  // token rows per load batch, forward
 constexpr int CONV_UB = 8;  // token rows of x and of dy per load batch, backward
 
 // CONV_CPL = 4 consecutive channels of one token row as loaded (8 B in bf16, 16 B in fp32), converted at use so
-// that a whole batch of loads is in flight at once.  load_nt / store4<T, true> carry the nontemporal hint: the
-// backward reads x and dy and writes dx once each and runs 7-17% faster with it; the forward, whose workgroups
-// re-read a few halo rows of their neighbours, runs slower with it and keeps ordinary accesses.
+// that a whole batch of loads is in flight at once.  The backward reads x and dy and writes dx once each through
+// buffer resources with the nontemporal hint (load_buf_nt / store4_buf_nt: 7-17% faster than ordinary global
+// accesses, and 32-bit offsets spare it the 64-bit address arithmetic of a VALU-bound loop); the forward, whose
+// workgroups re-read a few halo rows of their neighbours, runs slower with the hint and keeps ordinary loads.
 template <typename T>
 struct Row4;
 template <>
 struct Row4<bf16> {
   bf16x4 r;
   __device__ __forceinline__ void load(const bf16* p) { r = *reinterpret_cast<const bf16x4*>(p); }
-  __device__ __forceinline__ void load_nt(const bf16* p) { r = __builtin_nontemporal_load(reinterpret_cast<const bf16x4*>(p)); }
+  // nontemporal buffer read at byte offset off
+  __device__ __forceinline__ void load_buf_nt(__amdgpu_buffer_rsrc_t rs, int off) {
+    r = __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 2));
+  }
   __device__ __forceinline__ void get(float (&v)[4]) const {
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = static_cast<float>(r[j]);
@@ -48,23 +52,32 @@ template <>
 struct Row4<float> {
   f32x4 r;
   __device__ __forceinline__ void load(const float* p) { r = *reinterpret_cast<const f32x4*>(p); }
-  __device__ __forceinline__ void load_nt(const float* p) { r = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p)); }
+  __device__ __forceinline__ void load_buf_nt(__amdgpu_buffer_rsrc_t rs, int off) {
+    r = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 2));
+  }
   __device__ __forceinline__ void get(float (&v)[4]) const {
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = r[j];
   }
 };
 
-template <typename T, bool NT = false>
+template <typename T>
 __device__ __forceinline__ void store4(T* p, const float (&v)[4]) {
   if constexpr (sizeof(T) == 2) {
-    const bf16x4 r{static_cast<bf16>(v[0]), static_cast<bf16>(v[1]), static_cast<bf16>(v[2]), static_cast<bf16>(v[3])};
-    if constexpr (NT) __builtin_nontemporal_store(r, reinterpret_cast<bf16x4*>(p));
-    else *reinterpret_cast<bf16x4*>(p) = r;
+    *reinterpret_cast<bf16x4*>(p) =
+        bf16x4{static_cast<bf16>(v[0]), static_cast<bf16>(v[1]), static_cast<bf16>(v[2]), static_cast<bf16>(v[3])};
   } else {
-    const f32x4 r{v[0], v[1], v[2], v[3]};
-    if constexpr (NT) __builtin_nontemporal_store(r, reinterpret_cast<f32x4*>(p));
-    else *reinterpret_cast<f32x4*>(p) = r;
+    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+  }
+}
+// nontemporal buffer write of 4 consecutive channels at byte offset off
+template <typename T>
+__device__ __forceinline__ void store4_buf_nt(__amdgpu_buffer_rsrc_t rs, int off, const float (&v)[4]) {
+  if constexpr (sizeof(T) == 2) {
+    const bf16x4 r{static_cast<bf16>(v[0]), static_cast<bf16>(v[1]), static_cast<bf16>(v[2]), static_cast<bf16>(v[3])};
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, r), rs, off, 0, 2);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]}), rs, off, 0, 2);
   }
 }
 // sum over the NG / CONV_CPL lanes of a normalisation group (aligned runs of lanes), the same value in every lane
@@ -209,9 +222,15 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
   const int cc = on ? c : 0;
   const int64_t off = (int64_t)b * Tn * D + cc;
   const T* xl = x + off;
-  const T* dyl = dy + off;
-  T* dxl = dx + off;
   const int64_t srow = ((int64_t)b * D + cc) * (W - 1);
+  // the batch element's [Tn][D] rows of x, dy and dx as buffer resources (uniform base, 32-bit offsets: the
+  // host keeps Tn * D * sizeof(T) under 2 GiB); token t, this lane's channels at byte offset boff(t)
+  const int64_t bbase = (int64_t)b * Tn * D;
+  const int bbytes = Tn * D * (int)sizeof(T);
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(x + bbase), 0, bbytes, BUF_RSRC_WORD3);
+  const auto rdy = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(dy + bbase), 0, bbytes, BUF_RSRC_WORD3);
+  const auto rdx = __builtin_amdgcn_make_buffer_rsrc(dx + bbase, 0, bbytes, BUF_RSRC_WORD3);
+  auto boff = [&](int t) { return (t * D + cc) * (int)sizeof(T); };
   float wk[CPL][W], bk[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -243,7 +262,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
       }
       if (on) {
         if (p >= 0) {
-          store4<T, true>(dxl + (int64_t)p * D, o);
+          store4_buf_nt<T>(rdx, boff(p), o);
         } else if (dstate_in) {
 #pragma unroll
           for (int j = 0; j < CPL; ++j) dstate_in[srow + (int64_t)j * (W - 1) + (W - 1) + p] = from_f<T>(o[j]);
@@ -310,8 +329,8 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
     Row4<T> bx[U], bd[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      bx[u].load_nt(xl + (int64_t)(t0 + u) * D);
-      bd[u].load_nt(dyl + (int64_t)(t0 + u) * D);
+      bx[u].load_buf_nt(rx, boff(t0 + u));
+      bd[u].load_buf_nt(rdy, boff(t0 + u));
     }
     for (int n = 0; n < nfull; ++n, s += U) {
       Row4<T> cx[U], cd[U];
@@ -323,8 +342,8 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
       const int sn = min(s + U, t1 - U);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        bx[u].load_nt(xl + (int64_t)(sn + u) * D);
-        bd[u].load_nt(dyl + (int64_t)(sn + u) * D);
+        bx[u].load_buf_nt(rx, boff(sn + u));
+        bd[u].load_buf_nt(rdy, boff(sn + u));
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) step(s + u, cx[u], cd[u], Own{});
@@ -332,15 +351,15 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
   }
   for (; s < t1; ++s) {
     Row4<T> xr, dr;
-    xr.load_nt(xl + (int64_t)s * D);
-    dr.load_nt(dyl + (int64_t)s * D);
+    xr.load_buf_nt(rx, boff(s));
+    dr.load_buf_nt(rdy, boff(s));
     step(s, xr, dr, Own{});
   }
   const int send = min(Tn, t1 + W - 1);
   for (; s < send; ++s) {
     Row4<T> xr, dr;
-    xr.load_nt(xl + (int64_t)s * D);
-    dr.load_nt(dyl + (int64_t)s * D);
+    xr.load_buf_nt(rx, boff(s));
+    dr.load_buf_nt(rdy, boff(s));
     step(s, xr, dr, LookAhead{});
   }
   // past the sequence end dz = 0: flush the remaining dx of the chunk's tail (and of the state when Tn is short)
