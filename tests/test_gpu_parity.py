@@ -170,6 +170,33 @@ def test_training_pair_repeatable_bitwise():
         assert torch.equal(a, b), n
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_random_shapes_training_pair(seed):
+    """Seeded random shapes (ragged T, one to four heads, every compiled K x V pair, random scale, with and
+    without states) through the training pair against the fp64 oracle (rel-L2 <= 1e-2)."""
+    rng = torch.Generator().manual_seed(1000 + seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=rng))]
+    B, T, H = pick([1, 2, 3]), int(torch.randint(1, 300, (1,), generator=rng)), pick([1, 2, 4])
+    K, V = pick([(64, 64), (64, 128), (64, 256), (128, 64), (128, 128), (128, 256)])
+    scale = float(torch.empty(1).uniform_(0.3, 1.2, generator=rng))
+    states = bool(seed % 2)
+    banner(f"random training pair seed={seed} B={B} T={T} H={H} K={K} V={V} scale={scale:.3f} states={states}")
+    host, dev = device_inputs(B, T, H, K, V, torch.bfloat16, seed=seed, h0_std=0.1 if states else None,
+                              with_do=True)
+    dhT = (torch.randn(B, H, K, V, generator=rng) * 0.1).cuda() if states else None
+    o, hT, stash = ops.chunk_fwd_stash(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, scale)
+    got = ops.chunk_bwd_stashed(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, dev.do, dhT, stash, scale)
+    torch.cuda.synchronize()
+    o_ref, hT_ref = O.chunk_fwd(host.q, host.k, host.v, host.g, host.beta, scale, host.h0)
+    ref = O.chunk_bwd(host.q, host.k, host.v, host.g, host.beta, host.do, scale, host.h0,
+                      None if dhT is None else dhT.cpu())
+    assert rel_l2(o, o_ref) <= BF16_TOL
+    assert rel_l2(hT, hT_ref) <= BF16_TOL
+    for n, a, b in zip(NAMES, got, ref):
+        if b is not None:
+            assert rel_l2(a, b) <= BF16_TOL, (n, rel_l2(a, b))
+
+
 def test_state_passing_on_gpu():
     banner("state passing")
     host, dev = device_inputs(2, 300, 2, 128, 128, torch.bfloat16, h0_std=0.1)
