@@ -228,6 +228,18 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// One reduce-scatter round over a 16-lane DPP row: values a[0 .. 2N) -> a[0 .. N).  The lane whose bit `hi` is
+// clear keeps a[k] and sends a[k + N], its partner (DPP pattern CTRL, which pairs lanes with opposite bits)
+// the reverse; each keeps its value plus the one it receives.
+template <int N, int CTRL>
+__device__ __forceinline__ void rs_round(float* a, int hi) {
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const float keep = hi ? a[k + N] : a[k], send = hi ? a[k] : a[k + N];
+    a[k] = keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), CTRL, 0xf, 0xf, false));
+  }
+}
+
 // Sum of the 4 rows a lane holds plus the other 3 lane groups: the per-column sum of a 16x16 tile.
 __device__ __forceinline__ float colsum_tile(const f32x4& x) {
   return xor32_sum(xor16_sum(x[0] + x[1] + x[2] + x[3]));
@@ -264,7 +276,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   __shared__ __attribute__((aligned(16))) T slab[SLAB];
   __shared__ __attribute__((aligned(16))) T sdv[CH * LS];  // dv of the current slab, for the coalesced store
   __shared__ float sG[CH], sB[CH], sdG[CH], sLast[CH], sColZ[NWAVE][CH], sRed[IW];
-  __shared__ float sHalf[6][CH];  // second-half partial row sums: rq, rk, dbV, rx, dbA, rz
+  __shared__ float sRow[2][6][CH];  // per-half row sums: rq, rk, dbV, rx, dbA, rz
 
   T* sdO = slab;
   T* sV = sdO + CH * LS;
@@ -491,27 +503,33 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     const float cs = colsum_tile(z);
     if (lg == 0) sColZ[rb][cc] = cs;
   }
-  // per-row partial sums over this half's columns; the second half hands its sums to the first
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    rq[i] = sum16(rq[i]);
-    rk[i] = sum16(rk[i]);
-    dbV[i] = sum16(dbV[i]);
-    rx[i] = sum16(rx[i]);
-    dbA[i] = sum16(dbA[i]);
-    rz[i] = sum16(rz[i]);
-  }
-  if (hf == 1 && (l & 15) == 0) {
+  // Per-row sums over this half's columns: the 24 partials of a lane (6 quantities x its 4 rows, value index
+  // 4 q + i) are summed over the 16 lanes of the lane group by a reduce-scatter -- each DPP exchange halves the
+  // number of values held (12 pairs with the mirrored lane, 6 with the half-row mirror, 3 with lane ^ 2, then
+  // lane ^ 1) -- instead of a 4-step butterfly per value.  Lane p (in its group) ends with the total of value
+  // f0 = (p & 1) + s and, like lane p ^ 1, of value f1 = 2 + s (s = 3 bit1 + 6 bit2 + 12 bit3 of p), and writes
+  // them to sRow for this half.
+  {
+    float a[24];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * rb + acc_row(i);
-      sHalf[0][r] = rq[i];
-      sHalf[1][r] = rk[i];
-      sHalf[2][r] = dbV[i];
-      sHalf[3][r] = rx[i];
-      sHalf[4][r] = dbA[i];
-      sHalf[5][r] = rz[i];
+      a[i] = rq[i];
+      a[4 + i] = rk[i];
+      a[8 + i] = dbV[i];
+      a[12 + i] = rx[i];
+      a[16 + i] = dbA[i];
+      a[20 + i] = rz[i];
     }
+    const int p = l & 15;
+    rs_round<12, 0x140>(a, (p >> 3) & 1);  // row_mirror: lane 15 - p
+    rs_round<6, 0x141>(a, (p >> 2) & 1);   // row_half_mirror: lane 7 - p within the half-row
+    rs_round<3, 0x4e>(a, (p >> 1) & 1);    // quad_perm [2,3,0,1]: lane p ^ 2
+    rs_round<1, 0xb1>(a, p & 1);           // quad_perm [1,0,3,2]: lane p ^ 1
+    const float z1 = dpp_sum_step<0xb1>(a[2]);
+    const int sb = 3 * ((p >> 1) & 1) + 6 * ((p >> 2) & 1) + 12 * ((p >> 3) & 1);
+    const int f0 = sb + (p & 1), f1 = sb + 2;
+    sRow[hf][f0 >> 2][16 * rb + 4 * lg + (f0 & 3)] = a[0];
+    if ((p & 1) == 0) sRow[hf][f1 >> 2][16 * rb + 4 * lg + (f1 & 3)] = z1;
   }
   __syncthreads();
   // dq and dk are staged (bf16, stride LK) in the regions of dWn and dTm/M1, free from here on
@@ -568,8 +586,9 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rb + acc_row(i);
-      const float q_ = rq[i] + sHalf[0][r], k_ = rk[i] + sHalf[1][r], v_ = dbV[i] + sHalf[2][r];
-      const float x_ = rx[i] + sHalf[3][r], a_ = dbA[i] + sHalf[4][r], z_ = rz[i] + sHalf[5][r];
+      const float q_ = sRow[0][0][r] + sRow[1][0][r], k_ = sRow[0][1][r] + sRow[1][1][r];
+      const float v_ = sRow[0][2][r] + sRow[1][2][r], x_ = sRow[0][3][r] + sRow[1][3][r];
+      const float a_ = sRow[0][4][r] + sRow[1][4][r], z_ = sRow[0][5][r] + sRow[1][5][r];
       const float db = gam[i] * x_ + v_ + a_;
       if (dbeta && r < nvalid) dbeta[row0 + (int64_t)r * H] = db;
       sdG[r] = scale * gam[i] * q_ - dte[i] * k_ + bet[i] * gam[i] * x_ + z_;
