@@ -536,50 +536,63 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   T* sdq = sdWn;
   T* sdk = sdTm;
   static_assert(CH * LK <= 2 * CH * LC, "dk staging must fit in the dTm and M1 regions");
-  // dq = s gamma dQg + dPm U
+  // dq = s gamma dQg + dPm U.  (Here and below every tile of a product is computed before any is stored: with no
+  // LDS store in between, the row block's A fragments are read once for all column tiles.)
+  {
+    f32x4 t[HK];
 #pragma unroll
-  for (int j = 0; j < HK; ++j) {
-    const int n = HK * hf + j;
-    f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<true, false, CH>(t, sdPm, LC, 16 * rb, sU, LK, 16 * n);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
-      sdq[r * LK + d] = from_f<T>(scale * gam[i] * aQg[j][i] + t[i]);
+    for (int j = 0; j < HK; ++j) {
+      t[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      mma_blk<true, false, CH>(t[j], sdPm, LC, 16 * rb, sU, LK, 16 * (HK * hf + j));
     }
+#pragma unroll
+    for (int j = 0; j < HK; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * rb + acc_row(i), d = 16 * (HK * hf + j) + acc_col();
+        sdq[r * LK + d] = from_f<T>(scale * gam[i] * aQg[j][i] + t[j][i]);
+      }
   }
   if constexpr (!SEPU) {
     // dk = dte dKd + dPm^T Q + beta gamma dX + D K + D^T K
+    f32x4 t[HK];
 #pragma unroll
     for (int j = 0; j < HK; ++j) {
       const int n = HK * hf + j;
-      f32x4 t = {0.f, 0.f, 0.f, 0.f};
-      mma_blk<false, false, CH>(t, sdPm, LC, 16 * rb, sQ, LK, 16 * n);
-      mma_blk<true, false, CH>(t, sD, LC, 16 * rb, sK, LK, 16 * n);
-      mma_blk<false, false, CH>(t, sD, LC, 16 * rb, sK, LK, 16 * n);
+      t[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      mma_blk<false, false, CH>(t[j], sdPm, LC, 16 * rb, sQ, LK, 16 * n);
+      mma_blk<true, false, CH>(t[j], sD, LC, 16 * rb, sK, LK, 16 * n);
+      mma_blk<false, false, CH>(t[j], sD, LC, 16 * rb, sK, LK, 16 * n);
+    }
+#pragma unroll
+    for (int j = 0; j < HK; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
-        sdk[r * LK + d] = from_f<T>(dte[i] * aKd[j][i] + t[i] + bet[i] * gam[i] * aX[j][i]);
+        const int r = 16 * rb + acc_row(i), d = 16 * (HK * hf + j) + acc_col();
+        sdk[r * LK + d] = from_f<T>(dte[i] * aKd[j][i] + t[j][i] + bet[i] * gam[i] * aX[j][i]);
       }
-    }
   } else {
     // read side: dk = beta gamma dX + D U;  write side (kept in aKd until its staging area is free):
     // du = dte dKd + dPm^T Q + D^T K
+    f32x4 t[HK];
 #pragma unroll
     for (int j = 0; j < HK; ++j) {
       const int n = HK * hf + j;
-      f32x4 t = {0.f, 0.f, 0.f, 0.f}, t2 = {0.f, 0.f, 0.f, 0.f};
-      mma_blk<true, false, CH>(t, sD, LC, 16 * rb, sU, LK, 16 * n);
+      f32x4 t2 = {0.f, 0.f, 0.f, 0.f};
+      t[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      mma_blk<true, false, CH>(t[j], sD, LC, 16 * rb, sU, LK, 16 * n);
       mma_blk<false, false, CH>(t2, sdPm, LC, 16 * rb, sQ, LK, 16 * n);
       mma_blk<false, false, CH>(t2, sD, LC, 16 * rb, sK, LK, 16 * n);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 16 * rb + acc_row(i), d = 16 * n + acc_col();
-        sdk[r * LK + d] = from_f<T>(t[i] + bet[i] * gam[i] * aX[j][i]);
-        aKd[j][i] = dte[i] * aKd[j][i] + t2[i];
-      }
+      for (int i = 0; i < 4; ++i) aKd[j][i] = dte[i] * aKd[j][i] + t2[i];
     }
+#pragma unroll
+    for (int j = 0; j < HK; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * rb + acc_row(i), d = 16 * (HK * hf + j) + acc_col();
+        sdk[r * LK + d] = from_f<T>(t[j][i] + bet[i] * gam[i] * aX[j][i]);
+      }
   }
   // dbeta and the per-row part of dG (first half, one lane per row)
   if (hf == 0 && (l & 15) == 0) {
