@@ -257,7 +257,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     const float* __restrict__ wsGc, const T* __restrict__ wsH, const T* __restrict__ wsR,
     const T* __restrict__ wsdH, const T* __restrict__ wsdR, T* __restrict__ dq, T* __restrict__ dk,
     T* __restrict__ du, T* __restrict__ dv, float* __restrict__ dg, float* __restrict__ dbeta, int T_, int H,
-    int NT, float scale) {
+    int NT, int BH, float scale) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LS = VS + PT;
   constexpr int NKT = K / 16;   // column tiles over K
@@ -285,14 +285,19 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   T* sS0t = sdRt + VS * LC;  // S0^T    [VS][LK]
   T* sdSCt = sS0t + VS * LK; // dS_C^T  [VS][LK]
 
-  const int c = blockIdx.x, bh = blockIdx.y;
-  const int b = bh / H, h = bh - b * H;
-  const int t0 = c * CH;
-  const int nvalid = min(CH, T_ - t0);
-  const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
   const int rb = w & (NWAVE - 1), hf = w >> 2;
-  const int64_t row0 = ((int64_t)b * T_ + t0) * H + h;
-  const int64_t cidx = (int64_t)bh * NT + c;
+  const int nchunk = BH * NT;
+  // thread index and lane, re-derived opaquely in every chunk iteration (see the lane-dependent helpers)
+  int tid = threadIdx.x, l = tid & 63;
+
+  // Chunk ci = bh NT + c (also its index in the workspace): first row in the token-major tensors, valid rows.
+  auto chunk_rows = [&](int ci, int& nv) -> int64_t {
+    const int bh = (int)((unsigned)ci / (unsigned)NT), c = ci - bh * NT;
+    const int b = bh / H, h = bh - b * H;
+    nv = min(CH, T_ - c * CH);
+    return ((int64_t)b * T_ + c * CH) * H + h;
+  };
 
   // Global reads are issued as 16-byte register tiles (RegTile, FragTile) in the order they are consumed, each
   // V slab in two groups: A = {dO, V, R, dR} (and Tm, G, beta first) feeds dO R^T, dR V^T and Tm^T dR; B =
@@ -303,21 +308,47 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   RegTile<T, CH, VS, ITH, INTRA_NT> rdo, rv;
   FragTile<T, CH, VS, ITH, INTRA_NT> rr, rdr;
   FragTile<T, K, VS, ITH, INTRA_NT> rs0, rdsc;
-  auto load_a = [&](int vs) {
-    rdo.load(dout + row0 * V + vs, (int64_t)H * V, nvalid, tid);
-    rv.load(v + row0 * V + vs, (int64_t)H * V, nvalid, tid);
-    rr.load(wsR + cidx * CH * V, V / 16, vs / 16, tid);
-    rdr.load(wsdR + cidx * CH * V, V / 16, vs / 16, tid);
+  auto load_a = [&](int64_t ci, int64_t r0, int nv, int vs) {
+    rdo.load(dout + r0 * V + vs, (int64_t)H * V, nv, tid);
+    rv.load(v + r0 * V + vs, (int64_t)H * V, nv, tid);
+    rr.load(wsR + ci * CH * V, V / 16, vs / 16, tid);
+    rdr.load(wsdR + ci * CH * V, V / 16, vs / 16, tid);
   };
-  auto load_b = [&](int vs) {
-    rs0.load(wsH + cidx * K * V, V / 16, vs / 16, tid);
-    rdsc.load(wsdH + cidx * K * V, V / 16, vs / 16, tid);
+  auto load_b = [&](int64_t ci, int vs) {
+    rs0.load(wsH + ci * K * V, V / 16, vs / 16, tid);
+    rdsc.load(wsdH + ci * K * V, V / 16, vs / 16, tid);
   };
-  const float pg = wsGc[cidx * CH + (tid & (CH - 1))];
-  const float pb = beta ? beta[row0 + (int64_t)((tid & (CH - 1)) < nvalid ? (tid & (CH - 1)) : 0) * H] : 1.f;
-  rtm.load(wsTm + cidx * CH * CH, (int64_t)CH, CH, tid);
-  load_a(0);
-  load_b(0);
+  // The reads a chunk needs first: G, beta, Tm and the first slab's groups.  The workgroups are persistent (one
+  // per CU, looping over chunks) and issue these for their next chunk at the start of the current chunk's K
+  // phase, which reads no global memory: the loads are served while the K phase computes.
+  float pg, pb;
+  auto load_first = [&](int ci, bool order) {
+    int nv;
+    const int64_t r0 = chunk_rows(ci, nv);
+    pg = wsGc[(int64_t)ci * CH + (tid & (CH - 1))];
+    pb = beta ? beta[r0 + (int64_t)((tid & (CH - 1)) < nv ? (tid & (CH - 1)) : 0) * H] : 1.f;
+    rtm.load(wsTm + (int64_t)ci * CH * CH, (int64_t)CH, CH, tid);
+    load_a(ci, r0, nv, 0);
+    if (order) {
+      // A bare barrier (no fence: nothing waits for the loads) so that every wave has issued Tm and group A
+      // before any wave issues group B, Q and K.  The memory path serves a CU's loads roughly in issue order and
+      // the older waves issue first, so without it the second wave of each SIMD gets its group A behind the
+      // first waves' B, Q and K, and the first barrier waits for nearly all of the chunk's first reads.
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    load_b(ci, 0);
+  };
+  if ((int)blockIdx.x < nchunk) load_first(blockIdx.x, true);
+
+#pragma unroll 1
+  for (int ci = blockIdx.x; ci < nchunk; ci += gridDim.x) {
+  asm volatile("" : "+v"(tid));
+  l = tid & 63;
+  int nvalid;
+  const int64_t row0 = chunk_rows(ci, nvalid);
+  const int64_t cidx = ci;
   tq.load(q + row0 * K, (int64_t)H * K, nvalid, tid);
   tk.load(k + row0 * K, (int64_t)H * K, nvalid, tid);
   if constexpr (SEPU) tu.load(u + row0 * K, (int64_t)H * K, nvalid, tid);
@@ -337,7 +368,9 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   float dbV[4] = {0.f, 0.f, 0.f, 0.f};
   float sdot = 0.f;  // partial <dS_C, S0>
 
-#pragma unroll 1
+  // Unrolled up to two slabs: with the slab tests resolved at compile time the compiler counts the loads in
+  // flight exactly (four slabs unrolled would spill).
+#pragma unroll(V / VS <= 2 ? V / VS : 1)
   for (int vs = 0; vs < V; vs += VS) {
     // group A: dO R^T, dR V^T, dY = Tm^T dR (dv = beta dY, dbeta += dY . v)
     rdo.store(sdO, LS, tid);
@@ -345,23 +378,23 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     rr.store_t(sRt, LC, tid);
     rdr.store_t(sdRt, LC, tid);
     __syncthreads();
-    if (vs + VS < V) load_a(vs + VS);
+    if (vs + VS < V) load_a(cidx, row0, nvalid, vs + VS);
 #pragma unroll
     for (int j = 0; j < HC; ++j) {
       const int n = HC * hf + j;
-      mma_blk<true, false, VS>(aP[j], sdO, LS, 16 * rb, sRt, LC, 16 * n);
-      mma_blk<false, true, VS>(aTV[j], sdRt, LC, 16 * rb, sV, LS, 16 * n);
+      mma_blk<true, false, VS>(aP[j], sdO, LS, 16 * rb, sRt, LC, 16 * n, l);
+      mma_blk<false, true, VS>(aTV[j], sdRt, LC, 16 * rb, sV, LS, 16 * n, l);
     }
 #pragma unroll
     for (int j = 0; j < HV; ++j) {
       const int n = HV * hf + j;
       f32x4 dy = {0.f, 0.f, 0.f, 0.f};
-      mma_blk<false, true, CH>(dy, sTm, LC, 16 * rb, sdRt, LC, 16 * n);
+      mma_blk<false, true, CH>(dy, sTm, LC, 16 * rb, sdRt, LC, 16 * n, l);
       float vv[4];
-      acc_vals(sV, LS, 16 * rb, 16 * n, vv);
+      acc_vals(sV, LS, 16 * rb, 16 * n, vv, l);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * rb + acc_row(i), vc = 16 * n + acc_col();
+        const int r = 16 * rb + acc_row(i, l), vc = 16 * n + acc_col(l);
         dbV[i] += dy[i] * vv[i];
         sdv[r * LS + vc] = from_f<T>(sB[r] * dy[i]);
       }
@@ -381,14 +414,14 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       if constexpr (SEPU) tu.store(sU, LK, tid);
     }
     __syncthreads();
-    if (vs + VS < V) load_b(vs + VS);
-    s2g_rows<T, ITH, INTRA_NT>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, CH, VS, nvalid);
+    if (vs + VS < V) load_b(cidx, vs + VS);
+    s2g_rows<T, ITH, INTRA_NT>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, CH, VS, nvalid, tid);
 #pragma unroll
     for (int j = 0; j < HK; ++j) {
       const int n = HK * hf + j;
-      mma_blk<true, false, VS>(aQg[j], sdO, LS, 16 * rb, sS0t, LK, 16 * n);
-      mma_blk<false, false, VS>(aKd[j], sRt, LC, 16 * rb, sdSCt, LK, 16 * n);
-      mma_blk<false, false, VS>(aWn[j], sdRt, LC, 16 * rb, sS0t, LK, 16 * n);
+      mma_blk<true, false, VS>(aQg[j], sdO, LS, 16 * rb, sS0t, LK, 16 * n, l);
+      mma_blk<false, false, VS>(aKd[j], sRt, LC, 16 * rb, sdSCt, LK, 16 * n, l);
+      mma_blk<false, false, VS>(aWn[j], sdRt, LC, 16 * rb, sS0t, LK, 16 * n, l);
     }
     __syncthreads();
   }
@@ -399,6 +432,10 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   }
 
   // ---- K phase --------------------------------------------------------------------------------------------
+  // Issued unconditionally (the last chunk of a workgroup reads its own chunk again, 0.3% of the traffic): after
+  // a conditional block the compiler could not count the loads in flight and would wait for all of them at the
+  // first reuse of a register of the chunk's earlier reads.
+  load_first(ci + (int)gridDim.x < nchunk ? ci + (int)gridDim.x : ci, false);
   T* sdWn = slab;                 // CH x LK   dR S0^T (= -dW)
   T* sdTm = sdWn + CH * LK;       // CH x LC
   T* sM1 = sdTm + CH * LC;        // CH x LC   dTm Tm^T
@@ -410,7 +447,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   const float GC = sG[CH - 1];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int r = 16 * rb + acc_row(i);
+    const int r = 16 * rb + acc_row(i, l);
     Grow[i] = sG[r];
     gam[i] = __expf(Grow[i]);
     dte[i] = __expf(GC - Grow[i]);
@@ -421,11 +458,11 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 #pragma unroll
   for (int j = 0; j < HK; ++j) {
     float qv[4], uv[4];
-    acc_vals(sQ, LK, 16 * rb, 16 * (HK * hf + j), qv);
-    acc_vals(sU, LK, 16 * rb, 16 * (HK * hf + j), uv);
+    acc_vals(sQ, LK, 16 * rb, 16 * (HK * hf + j), qv, l);
+    acc_vals(sU, LK, 16 * rb, 16 * (HK * hf + j), uv, l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * rb + acc_row(i), d = 16 * (HK * hf + j) + acc_col();
+      const int r = 16 * rb + acc_row(i, l), d = 16 * (HK * hf + j) + acc_col(l);
       rq[i] += aQg[j][i] * qv[i];
       rk[i] += aKd[j][i] * uv[i];
       sdWn[r * LK + d] = from_f<T>(aWn[j][i]);
@@ -440,10 +477,10 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   for (int j = 0; j < HK; ++j) {
     const int n = HK * hf + j;
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<false, false, CH>(t, sTm, LC, 16 * rb, sdWn, LK, 16 * n);
+    mma_blk<false, false, CH>(t, sTm, LC, 16 * rb, sdWn, LK, 16 * n, l);
     aX[j] = -t;
     float kv[4];
-    acc_vals(sK, LK, 16 * rb, 16 * n, kv);
+    acc_vals(sK, LK, 16 * rb, 16 * n, kv, l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) rx[i] += aX[j][i] * kv[i];
   }
@@ -452,12 +489,12 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   for (int j = 0; j < HC; ++j) {
     const int n = HC * hf + j;
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<true, true, K>(t, sdWn, LK, 16 * rb, sK, LK, 16 * n);
-    const int cc = 16 * n + acc_col();
+    mma_blk<true, true, K>(t, sdWn, LK, 16 * rb, sK, LK, 16 * n, l);
+    const int cc = 16 * n + acc_col(l);
     const float bj = sB[cc], gj = __expf(sG[cc]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * rb + acc_row(i);
+      const int r = 16 * rb + acc_row(i, l);
       sdTm[r * LC + cc] = from_f<T>(-bj * gj * t[i] + bj * aTV[j][i]);
     }
   }
@@ -467,9 +504,9 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   for (int j = 0; j < HC; ++j) {
     const int n = HC * hf + j;
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<true, true, CH>(t, sdTm, LC, 16 * rb, sTm, LC, 16 * n);
+    mma_blk<true, true, CH>(t, sdTm, LC, 16 * rb, sTm, LC, 16 * n, l);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sM1[(16 * rb + acc_row(i)) * LC + 16 * n + acc_col()] = from_f<T>(t[i]);
+    for (int i = 0; i < 4; ++i) sM1[(16 * rb + acc_row(i, l)) * LC + 16 * n + acc_col(l)] = from_f<T>(t[i]);
   }
   __syncthreads();
   // dA = -Tm^T M1, strict lower; with KK and QK recomputed: D, dPm, dbeta_A and the dG row/col sums
@@ -478,15 +515,15 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   for (int j = 0; j < HC; ++j) {
     const int n = HC * hf + j;
     f32x4 da = {0.f, 0.f, 0.f, 0.f}, kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<false, false, CH>(da, sTm, LC, 16 * rb, sM1, LC, 16 * n);
-    mma_blk<true, true, K>(kk, sK, LK, 16 * rb, sU, LK, 16 * n);
-    mma_blk<true, true, K>(qk, sQ, LK, 16 * rb, sU, LK, 16 * n);
+    mma_blk<false, false, CH>(da, sTm, LC, 16 * rb, sM1, LC, 16 * n, l);
+    mma_blk<true, true, K>(kk, sK, LK, 16 * rb, sU, LK, 16 * n, l);
+    mma_blk<true, true, K>(qk, sQ, LK, 16 * rb, sU, LK, 16 * n, l);
     f32x4 z;
-    const int cc = 16 * n + acc_col();
+    const int cc = 16 * n + acc_col(l);
     const float Gc = sG[cc];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * rb + acc_row(i);
+      const int r = 16 * rb + acc_row(i, l);
       // computed unconditionally (min(., 0) keeps it finite) and masked by a select: no branch around the exp
       const float e_all = __expf(fminf(Grow[i] - Gc, 0.f));
       const float e = r >= cc ? e_all : 0.f;
@@ -543,13 +580,13 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 #pragma unroll
     for (int j = 0; j < HK; ++j) {
       t[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      mma_blk<true, false, CH>(t[j], sdPm, LC, 16 * rb, sU, LK, 16 * (HK * hf + j));
+      mma_blk<true, false, CH>(t[j], sdPm, LC, 16 * rb, sU, LK, 16 * (HK * hf + j), l);
     }
 #pragma unroll
     for (int j = 0; j < HK; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * rb + acc_row(i), d = 16 * (HK * hf + j) + acc_col();
+        const int r = 16 * rb + acc_row(i, l), d = 16 * (HK * hf + j) + acc_col(l);
         sdq[r * LK + d] = from_f<T>(scale * gam[i] * aQg[j][i] + t[j][i]);
       }
   }
@@ -560,15 +597,15 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     for (int j = 0; j < HK; ++j) {
       const int n = HK * hf + j;
       t[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      mma_blk<false, false, CH>(t[j], sdPm, LC, 16 * rb, sQ, LK, 16 * n);
-      mma_blk<true, false, CH>(t[j], sD, LC, 16 * rb, sK, LK, 16 * n);
-      mma_blk<false, false, CH>(t[j], sD, LC, 16 * rb, sK, LK, 16 * n);
+      mma_blk<false, false, CH>(t[j], sdPm, LC, 16 * rb, sQ, LK, 16 * n, l);
+      mma_blk<true, false, CH>(t[j], sD, LC, 16 * rb, sK, LK, 16 * n, l);
+      mma_blk<false, false, CH>(t[j], sD, LC, 16 * rb, sK, LK, 16 * n, l);
     }
 #pragma unroll
     for (int j = 0; j < HK; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * rb + acc_row(i), d = 16 * (HK * hf + j) + acc_col();
+        const int r = 16 * rb + acc_row(i, l), d = 16 * (HK * hf + j) + acc_col(l);
         sdk[r * LK + d] = from_f<T>(dte[i] * aKd[j][i] + t[j][i] + bet[i] * gam[i] * aX[j][i]);
       }
   } else {
@@ -580,9 +617,9 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       const int n = HK * hf + j;
       f32x4 t2 = {0.f, 0.f, 0.f, 0.f};
       t[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      mma_blk<true, false, CH>(t[j], sD, LC, 16 * rb, sU, LK, 16 * n);
-      mma_blk<false, false, CH>(t2, sdPm, LC, 16 * rb, sQ, LK, 16 * n);
-      mma_blk<false, false, CH>(t2, sD, LC, 16 * rb, sK, LK, 16 * n);
+      mma_blk<true, false, CH>(t[j], sD, LC, 16 * rb, sU, LK, 16 * n, l);
+      mma_blk<false, false, CH>(t2, sdPm, LC, 16 * rb, sQ, LK, 16 * n, l);
+      mma_blk<false, false, CH>(t2, sD, LC, 16 * rb, sK, LK, 16 * n, l);
 #pragma unroll
       for (int i = 0; i < 4; ++i) aKd[j][i] = dte[i] * aKd[j][i] + t2[i];
     }
@@ -590,7 +627,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     for (int j = 0; j < HK; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * rb + acc_row(i), d = 16 * (HK * hf + j) + acc_col();
+        const int r = 16 * rb + acc_row(i, l), d = 16 * (HK * hf + j) + acc_col(l);
         sdk[r * LK + d] = from_f<T>(t[j][i] + bet[i] * gam[i] * aX[j][i]);
       }
   }
@@ -598,7 +635,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   if (hf == 0 && (l & 15) == 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * rb + acc_row(i);
+      const int r = 16 * rb + acc_row(i, l);
       const float q_ = sRow[0][0][r] + sRow[1][0][r], k_ = sRow[0][1][r] + sRow[1][1][r];
       const float v_ = sRow[0][2][r] + sRow[1][2][r], x_ = sRow[0][3][r] + sRow[1][3][r];
       const float a_ = sRow[0][4][r] + sRow[1][4][r], z_ = sRow[0][5][r] + sRow[1][5][r];
@@ -609,8 +646,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     }
   }
   __syncthreads();
-  s2g_rows<T, ITH, INTRA_NT>(dq + row0 * K, (int64_t)H * K, sdq, LK, CH, K, nvalid);
-  s2g_rows<T, ITH, INTRA_NT>(dk + row0 * K, (int64_t)H * K, sdk, LK, CH, K, nvalid);
+  s2g_rows<T, ITH, INTRA_NT>(dq + row0 * K, (int64_t)H * K, sdq, LK, CH, K, nvalid, tid);
+  s2g_rows<T, ITH, INTRA_NT>(dk + row0 * K, (int64_t)H * K, sdk, LK, CH, K, nvalid, tid);
   if constexpr (SEPU) {
     // du staged in the D and dPm regions, free once every wave has passed the barrier above
     T* sdu = sD;
@@ -618,9 +655,9 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     for (int j = 0; j < HK; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        sdu[(16 * rb + acc_row(i)) * LK + 16 * (HK * hf + j) + acc_col()] = from_f<T>(aKd[j][i]);
+        sdu[(16 * rb + acc_row(i, l)) * LK + 16 * (HK * hf + j) + acc_col(l)] = from_f<T>(aKd[j][i]);
     __syncthreads();
-    s2g_rows<T, ITH, INTRA_NT>(du + row0 * K, (int64_t)H * K, sdu, LK, CH, K, nvalid);
+    s2g_rows<T, ITH, INTRA_NT>(du + row0 * K, (int64_t)H * K, sdu, LK, CH, K, nvalid, tid);
   }
   if (w == 0) {
     // dG_r -= colsum_r;  dG_last += sum_r dte_r rk_r + gamma_C <dS_C, S0>;  dg = reverse cumsum of dG
@@ -634,6 +671,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     const float incl = wave_inclusive_scan(x);
     const float total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), 63));
     if (l < nvalid) dg[row0 + (int64_t)l * H] = total - incl + x;
+  }
+  __syncthreads();  // the next chunk overwrites the LDS read above
   }
 }
 
@@ -653,13 +692,15 @@ static hipError_t bwd_state_k(const ChunkArgs& a) {
 template <typename T, int K, int V, bool SEPU>
 static hipError_t bwd_intra_kv(const ChunkArgs& a) {
   constexpr int VS = sizeof(T) == 2 ? 64 : 32;
-  dim3 grid(a.NT, a.B * a.H);
+  // persistent: one workgroup per CU (the LDS use allows no more), each looping over chunks
+  const int nchunk = a.NT * a.B * a.H;
+  dim3 grid(std::min(nchunk, device_cu_count()));
   bwd_intra_kernel<T, K, V, VS, SEPU><<<grid, ITH, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
       static_cast<const T*>(a.v), a.beta, static_cast<const T*>(a.dout), static_cast<const T*>(a.ws.Tm),
       a.ws.Gc, static_cast<const T*>(a.ws.hs), static_cast<const T*>(a.ws.Rs), static_cast<const T*>(a.ws.dhs),
       static_cast<const T*>(a.ws.dRs), static_cast<T*>(a.dq), static_cast<T*>(a.dk), static_cast<T*>(a.du),
-      static_cast<T*>(a.dv), a.dg, a.dbeta, a.T, a.H, a.NT, a.scale);
+      static_cast<T*>(a.dv), a.dg, a.dbeta, a.T, a.H, a.NT, a.B * a.H, a.scale);
   return hipGetLastError();
 }
 

@@ -289,13 +289,14 @@ struct FragTile {
 // Copy a rows x cols tile from LDS (stride sld) to global (row stride gld), 16-byte vectors, rows < valid only,
 // by the NTH threads of the workgroup.
 template <typename T, int NTH = NTHR, bool NT = false>
-__device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld, int rows, int cols, int valid) {
+__device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld, int rows, int cols, int valid,
+                                         int tid = threadIdx.x) {
   constexpr int E = 16 / sizeof(T);
   const int vpr = cols / E;
   // buffer stores over the valid rows only: the range check drops the rest (32-bit offsets, as for RegTile)
   const int nbytes = valid > 0 ? ((valid - 1) * (int)gld + cols) * (int)sizeof(T) : 0;
   const auto rs = __builtin_amdgcn_make_buffer_rsrc(g, 0, nbytes, BUF_RSRC_WORD3);
-  for (int idx = threadIdx.x; idx < rows * vpr; idx += NTH) {
+  for (int idx = tid; idx < rows * vpr; idx += NTH) {
     const int r = idx / vpr, c = (idx - r * vpr) * E;
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(s + r * sld + c)),
                                            rs, (r * (int)gld + c) * (int)sizeof(T), 0, NT ? 2 : 0);
@@ -305,14 +306,14 @@ __device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld,
 // The elements of a row-major LDS tile at this lane's accumulator positions of output tile (rows r0.., columns
 // c0..): rows r0 + 4 (l >> 4) + i (i = 0..3) of column c0 + (l & 15).  bf16: one transposing read.
 template <typename T>
-__device__ __forceinline__ void acc_vals(const T* p, int ld, int r0, int c0, float (&v)[4]) {
+__device__ __forceinline__ void acc_vals(const T* p, int ld, int r0, int c0, float (&v)[4], int l = lane_id()) {
   if constexpr (sizeof(T) == 2) {
-    const bf16x4 t = ld_tr4(p, ld, c0, r0 + 4 * (lane_id() >> 4));
+    const bf16x4 t = ld_tr4(p, ld, c0, r0 + 4 * (l >> 4), l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = to_f(t[i]);
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = p[(r0 + acc_row(i)) * ld + c0 + acc_col()];
+    for (int i = 0; i < 4; ++i) v[i] = p[(r0 + acc_row(i, l)) * ld + c0 + acc_col(l)];
   }
 }
 

@@ -50,10 +50,13 @@ __device__ __forceinline__ void mma(f32x4& c, const f32x8& a, const f32x8& b) {
   for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], c, 0, 0, 0);
 }
 
+// Lane-dependent helpers take the lane as a trailing argument (default: this thread's lane).  A kernel that
+// loops over work items passes a lane value re-derived in every iteration, so that the address arithmetic is
+// redone there rather than hoisted out of the loop and held in registers for its whole length.
+
 // Fragment with k contiguous: element (o, k) at p[o * ld + k].
 template <typename T>
-__device__ __forceinline__ typename Frag<T>::type frag_kc(const T* p, int ld, int o0, int k0) {
-  const int l = lane_id();
+__device__ __forceinline__ typename Frag<T>::type frag_kc(const T* p, int ld, int o0, int k0, int l = lane_id()) {
   const T* s = p + (o0 + (l & 15)) * ld + k0 + 8 * (l >> 4);
   if constexpr (sizeof(T) == 2) {
     return *reinterpret_cast<const bf16x8*>(s);
@@ -66,8 +69,7 @@ __device__ __forceinline__ typename Frag<T>::type frag_kc(const T* p, int ld, in
 
 // Fragment with the outer index contiguous: element (o, k) at p[k * ld + o].
 template <typename T>
-__device__ __forceinline__ typename Frag<T>::type frag_oc(const T* p, int ld, int o0, int k0) {
-  const int l = lane_id();
+__device__ __forceinline__ typename Frag<T>::type frag_oc(const T* p, int ld, int o0, int k0, int l = lane_id()) {
   const T* s = p + (k0 + 8 * (l >> 4)) * ld + o0 + (l & 15);
   typename Frag<T>::type f;
 #pragma unroll
@@ -76,23 +78,24 @@ __device__ __forceinline__ typename Frag<T>::type frag_oc(const T* p, int ld, in
 }
 
 template <typename T>
-__device__ __forceinline__ typename Frag<T>::type frag_oct(const T* p, int ld, int o0, int k0);
+__device__ __forceinline__ typename Frag<T>::type frag_oct(const T* p, int ld, int o0, int k0, int l = lane_id());
 
 template <bool KC, typename T>
-__device__ __forceinline__ typename Frag<T>::type frag(const T* p, int ld, int o0, int k0) {
-  if constexpr (KC) return frag_kc(p, ld, o0, k0);
-  else return frag_oct(p, ld, o0, k0);
+__device__ __forceinline__ typename Frag<T>::type frag(const T* p, int ld, int o0, int k0, int l = lane_id()) {
+  if constexpr (KC) return frag_kc(p, ld, o0, k0, l);
+  else return frag_oct(p, ld, o0, k0, l);
 }
 
 // c += A[m0:m0+16, 0:KD] * B[0:KD, n0:n0+16].
 //   A element (m, k): AKC ? A[m*lda + k] : A[k*lda + m]
 //   B element (k, n): BKC ? B[n*ldb + k] : B[k*ldb + n]
 template <bool AKC, bool BKC, int KD, typename T>
-__device__ __forceinline__ void mma_blk(f32x4& c, const T* A, int lda, int m0, const T* B, int ldb, int n0) {
+__device__ __forceinline__ void mma_blk(f32x4& c, const T* A, int lda, int m0, const T* B, int ldb, int n0,
+                                        int l = lane_id()) {
 #pragma unroll
   for (int k0 = 0; k0 < KD; k0 += 32) {
-    const auto a = frag<AKC>(A, lda, m0, k0);
-    const auto b = frag<BKC>(B, ldb, n0, k0);
+    const auto a = frag<AKC>(A, lda, m0, k0, l);
+    const auto b = frag<BKC>(B, ldb, n0, k0, l);
     mma(c, a, b);
   }
 }
@@ -138,8 +141,8 @@ __device__ __forceinline__ typename Frag<T>::type frag_oc_perm(const T* p, int l
 // columns o0 + 4(m mod 4) of a row-major tile, lane i receives the 4 values at rows kb..kb+3 of column o0 + i:
 // a column-major operand slice read straight from a row-major tile.
 typedef short shortx4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ bf16x4 ld_tr4(const bf16* p, int ld, int o0, int kb) {
-  const int m = lane_id() & 15;
+__device__ __forceinline__ bf16x4 ld_tr4(const bf16* p, int ld, int o0, int kb, int l = lane_id()) {
+  const int m = l & 15;
   const bf16* a = p + (kb + (m >> 2)) * ld + o0 + 4 * (m & 3);
   const shortx4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) shortx4*)(a));
   return __builtin_bit_cast(bf16x4, r);
@@ -150,13 +153,13 @@ __device__ __forceinline__ bf16x4 ld_tr4(const bf16* p, int ld, int o0, int kb) 
 //   frag_oct_perm: permuted slots (k = k0 + 4g + e, k0 + 16 + 4g + e)
 // bf16 uses two transposing reads; fp32 falls back to scalar reads.
 template <typename T>
-__device__ __forceinline__ typename Frag<T>::type frag_oct(const T* p, int ld, int o0, int k0) {
+__device__ __forceinline__ typename Frag<T>::type frag_oct(const T* p, int ld, int o0, int k0, int l) {
   if constexpr (sizeof(T) == 2) {
-    const int g = lane_id() >> 4;
-    const bf16x4 a = ld_tr4(p, ld, o0, k0 + 8 * g), b = ld_tr4(p, ld, o0, k0 + 8 * g + 4);
+    const int g = l >> 4;
+    const bf16x4 a = ld_tr4(p, ld, o0, k0 + 8 * g, l), b = ld_tr4(p, ld, o0, k0 + 8 * g + 4, l);
     return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   } else {
-    return frag_oc(p, ld, o0, k0);
+    return frag_oc(p, ld, o0, k0, l);
   }
 }
 template <typename T>
@@ -185,8 +188,8 @@ __device__ __forceinline__ typename Frag<T>::type frag_acc2(const f32x4& t0, con
   return f;
 }
 
-__device__ __forceinline__ int acc_row(int i) { return 4 * (lane_id() >> 4) + i; }
-__device__ __forceinline__ int acc_col() { return lane_id() & 15; }
+__device__ __forceinline__ int acc_row(int i, int l = lane_id()) { return 4 * (l >> 4) + i; }
+__device__ __forceinline__ int acc_col(int l = lane_id()) { return l & 15; }
 
 // Workgroup -> (V block, head) for the chunk sweeps.  Workgroups are dispatched round-robin over the 8 XCDs
 // (each with its own L2), so with a plain grid the NV V-block workgroups of one head land on different XCDs and
