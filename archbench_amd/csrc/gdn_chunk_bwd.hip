@@ -415,7 +415,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     }
     __syncthreads();
     if (vs + VS < V) load_b(cidx, vs + VS);
-    s2g_rows<T, ITH, INTRA_NT>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, CH, VS, nvalid, tid);
+    s2g_rows<T, CH, VS, ITH, INTRA_NT>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, nvalid, tid);
 #pragma unroll
     for (int j = 0; j < HK; ++j) {
       const int n = HK * hf + j;
@@ -646,8 +646,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     }
   }
   __syncthreads();
-  s2g_rows<T, ITH, INTRA_NT>(dq + row0 * K, (int64_t)H * K, sdq, LK, CH, K, nvalid, tid);
-  s2g_rows<T, ITH, INTRA_NT>(dk + row0 * K, (int64_t)H * K, sdk, LK, CH, K, nvalid, tid);
+  s2g_rows<T, CH, K, ITH, INTRA_NT>(dq + row0 * K, (int64_t)H * K, sdq, LK, nvalid, tid);
+  s2g_rows<T, CH, K, ITH, INTRA_NT>(dk + row0 * K, (int64_t)H * K, sdk, LK, nvalid, tid);
   if constexpr (SEPU) {
     // du staged in the D and dPm regions, free once every wave has passed the barrier above
     T* sdu = sD;
@@ -657,7 +657,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       for (int i = 0; i < 4; ++i)
         sdu[(16 * rb + acc_row(i, l)) * LK + 16 * (HK * hf + j) + acc_col(l)] = from_f<T>(aKd[j][i]);
     __syncthreads();
-    s2g_rows<T, ITH, INTRA_NT>(du + row0 * K, (int64_t)H * K, sdu, LK, CH, K, nvalid, tid);
+    s2g_rows<T, CH, K, ITH, INTRA_NT>(du + row0 * K, (int64_t)H * K, sdu, LK, nvalid, tid);
   }
   if (w == 0) {
     // dG_r -= colsum_r;  dG_last += sum_r dte_r rk_r + gamma_C <dS_C, S0>;  dg = reverse cumsum of dG

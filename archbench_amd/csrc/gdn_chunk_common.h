@@ -286,20 +286,25 @@ struct FragTile {
   }
 };
 
-// Copy a rows x cols tile from LDS (stride sld) to global (row stride gld), 16-byte vectors, rows < valid only,
-// by the NTH threads of the workgroup.
-template <typename T, int NTH = NTHR, bool NT = false>
-__device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld, int rows, int cols, int valid,
-                                         int tid = threadIdx.x) {
-  constexpr int E = 16 / sizeof(T);
-  const int vpr = cols / E;
-  // buffer stores over the valid rows only: the range check drops the rest (32-bit offsets, as for RegTile)
-  const int nbytes = valid > 0 ? ((valid - 1) * (int)gld + cols) * (int)sizeof(T) : 0;
+// Copy a ROWS x COLS tile from LDS (stride sld) to global (row stride gld), 16-byte vectors, rows < valid only,
+// by the NTH threads of the workgroup (tid = thread index).  The trip count is a compile-time constant and the
+// stores are unconditional (a buffer resource over the valid rows drops the rest), so the compiler knows how
+// many stores each thread has in flight and a later wait for an earlier load need not wait for these stores.
+template <typename T, int ROWS, int COLS, int NTH = NTHR, bool NT = false>
+__device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld, int valid, int tid = threadIdx.x) {
+  constexpr int E = 16 / sizeof(T), VPR = COLS / E, NV = ROWS * VPR, N = (NV + NTH - 1) / NTH;
+  static_assert(VPR * E == COLS, "whole 16-byte vectors per row");
+  // 32-bit offsets, as for RegTile
+  const int nbytes = valid > 0 ? ((valid - 1) * (int)gld + COLS) * (int)sizeof(T) : 0;
   const auto rs = __builtin_amdgcn_make_buffer_rsrc(g, 0, nbytes, BUF_RSRC_WORD3);
-  for (int idx = tid; idx < rows * vpr; idx += NTH) {
-    const int r = idx / vpr, c = (idx - r * vpr) * E;
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(s + r * sld + c)),
-                                           rs, (r * (int)gld + c) * (int)sizeof(T), 0, NT ? 2 : 0);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int idx = tid + i * NTH;
+    if (NV % NTH == 0 || idx < NV) {
+      const int r = idx / VPR, c = (idx - r * VPR) * E;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(s + r * sld + c)),
+                                             rs, (r * (int)gld + c) * (int)sizeof(T), 0, NT ? 2 : 0);
+    }
   }
 }
 

@@ -81,8 +81,8 @@ void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, cons
     __syncthreads();
     factors_merge<T>(D, sA, sD, sTm, nullptr, sOne, w);
     __syncthreads();
-    s2g_rows<T, NTHR, true>(gTm + (int64_t)it * CH * CH, (int64_t)CH, sTm, LC, CH, CH, CH);
-    s2g_rows<T, NTHR, true>(gP + (int64_t)it * CH * CH, (int64_t)CH, sP, LC, CH, CH, CH);
+    s2g_rows<T, CH, CH, NTHR, true>(gTm + (int64_t)it * CH * CH, (int64_t)CH, sTm, LC, CH);
+    s2g_rows<T, CH, CH, NTHR, true>(gP + (int64_t)it * CH * CH, (int64_t)CH, sP, LC, CH);
     __syncthreads();  // LDS free for the next item
   }
 }

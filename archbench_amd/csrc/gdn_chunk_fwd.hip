@@ -209,7 +209,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     }
     __syncthreads();  // O staged; every wave done with this chunk's inputs
     if constexpr (OUT)
-      s2g_rows<T, FTH, FWD_NT_STORE>(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, CH, BV, nvalid_of(c));
+      s2g_rows<T, CH, BV, FTH, FWD_NT_STORE>(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, nvalid_of(c));
   };
   prefetch(0);
   prefetch2(0);
