@@ -322,7 +322,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   // per CU, looping over chunks) and issue these for their next chunk at the start of the current chunk's K
   // phase, which reads no global memory: the loads are served while the K phase computes.
   float pg, pb;
-  auto load_first = [&](int ci, bool order) {
+  auto load_first = [&](int ci, bool order, bool with_b) {
     int nv;
     const int64_t r0 = chunk_rows(ci, nv);
     pg = wsGc[(int64_t)ci * CH + (tid & (CH - 1))];
@@ -338,9 +338,9 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
     }
-    load_b(ci, 0);
+    if (with_b) load_b(ci, 0);
   };
-  if ((int)blockIdx.x < nchunk) load_first(blockIdx.x, true);
+  if ((int)blockIdx.x < nchunk) load_first(blockIdx.x, true, true);
 
 #pragma unroll 1
   for (int ci = blockIdx.x; ci < nchunk; ci += gridDim.x) {
@@ -435,7 +435,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   // Issued unconditionally (the last chunk of a workgroup reads its own chunk again, 0.3% of the traffic): after
   // a conditional block the compiler could not count the loads in flight and would wait for all of them at the
   // first reuse of a register of the chunk's earlier reads.
-  load_first(ci + (int)gridDim.x < nchunk ? ci + (int)gridDim.x : ci, false);
+  const int cnext = ci + (int)gridDim.x < nchunk ? ci + (int)gridDim.x : ci;
+  load_first(cnext, false, false);  // group B after the first K-phase products, not all at once
   T* sdWn = slab;                 // CH x LK   dR S0^T (= -dW)
   T* sdTm = sdWn + CH * LK;       // CH x LC
   T* sM1 = sdTm + CH * LC;        // CH x LC   dTm Tm^T
@@ -484,6 +485,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) rx[i] += aX[j][i] * kv[i];
   }
+  load_b(cnext, 0);
   // dTm rows:  dTm_ij = -beta_j gamma_j (dWn K^T)_ij + beta_j (dR V^T)_ij
 #pragma unroll
   for (int j = 0; j < HC; ++j) {
@@ -659,6 +661,10 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     __syncthreads();
     s2g_rows<T, CH, K, ITH, INTRA_NT>(du + row0 * K, (int64_t)H * K, sdu, LK, nvalid, tid);
   }
+  // The next chunk overwrites the staged rows read above.  Wave 0's reverse cumsum below reads only sdG, sColZ,
+  // sLast and sRed, which the next chunk writes after barriers that wave 0 must reach first, so the other waves
+  // go on into the next chunk meanwhile.
+  __syncthreads();
   if (w == 0) {
     // dG_r -= colsum_r;  dG_last += sum_r dte_r rk_r + gamma_C <dS_C, S0>;  dg = reverse cumsum of dG
     float x = sdG[l] - (sColZ[0][l] + sColZ[1][l] + sColZ[2][l] + sColZ[3][l]);
@@ -672,7 +678,6 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     const float total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), 63));
     if (l < nvalid) dg[row0 + (int64_t)l * H] = total - incl + x;
   }
-  __syncthreads();  // the next chunk overwrites the LDS read above
   }
 }
 
