@@ -526,17 +526,17 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rb + acc_row(i, l);
-      // computed unconditionally (min(., 0) keeps it finite) and masked by a select: no branch around the exp
-      const float e_all = __expf(fminf(Grow[i] - Gc, 0.f));
-      const float e = r >= cc ? e_all : 0.f;
-      const float dA = (r > cc) ? -da[i] : 0.f;
-      const float Aval = bet[i] * kk[i] * e;
-      const float dP = (r >= cc) ? aP[j][i] : 0.f;
-      const float Pval = scale * e * qk[i];
-      sD[r * LC + cc] = from_f<T>(dA * bet[i] * e);
-      sdPm[r * LC + cc] = from_f<T>(dP * scale * e);
-      dbA[i] += dA * kk[i] * e;
-      z[i] = dP * Pval + dA * Aval;
+      // e = exp(G_r - G_c) on and below the diagonal, computed unconditionally (min(., 0) keeps it finite) and
+      // masked by a select: no branch around the exp.  With u = dA e (strictly below) and w = dP s e:
+      //   D = u beta_r,  dPm = w,  dbeta_A += u (K U^T),  z = dP P + dA A = w (Q U^T) + D (K U^T)
+      const float e = r >= cc ? __expf(fminf(Grow[i] - Gc, 0.f)) : 0.f;
+      const float u = r > cc ? -da[i] * e : 0.f;
+      const float wv = aP[j][i] * (scale * e);
+      const float Dv = u * bet[i];
+      sD[r * LC + cc] = from_f<T>(Dv);
+      sdPm[r * LC + cc] = from_f<T>(wv);
+      dbA[i] += u * kk[i];
+      z[i] = wv * qk[i] + Dv * kk[i];
       rz[i] += z[i];
     }
     const float cs = colsum_tile(z);
