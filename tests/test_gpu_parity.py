@@ -170,6 +170,31 @@ def test_training_pair_repeatable_bitwise():
         assert torch.equal(a, b), n
 
 
+@pytest.mark.parametrize("K,V", [(128, 128), (128, 64), (64, 256), (64, 128)])
+def test_training_pair_many_chunks_per_workgroup(K, V):
+    """The gradient kernel's workgroups are persistent (at most one per CU, each looping over chunks and
+    prefetching the next one during the current one): with 768 chunks of which the last of every sequence is
+    ragged (T = 1000), each workgroup runs several chunks, ragged ones included.  Two heads are checked against
+    the fp64 oracle, every head against the plain (recompute) backward."""
+    B, T, H = 4, 1000, 12
+    banner(f"training pair, many chunks per workgroup B={B} T={T} H={H} K={K} V={V} bf16")
+    host, dev = device_inputs(B, T, H, K, V, torch.bfloat16, seed=31, h0_std=0.1, with_do=True)
+    dhT = torch.randn(B, H, K, V, generator=torch.Generator().manual_seed(32)) * 0.1
+    o, hT, stash = ops.chunk_fwd_stash(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, 0.6)
+    grads = ops.chunk_bwd_stashed(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, dev.do, dhT.cuda(), stash, 0.6)
+    plain = ops.chunk_bwd(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, dev.do, dhT.cuda(), 0.6)
+    torch.cuda.synchronize()
+    for n, a, b in zip(NAMES, grads, plain):
+        assert rel_l2(a, b) <= BF16_TOL, (n, rel_l2(a, b))
+    for bi, h in ((0, 0), (3, 11)):
+        s = lambda x: x[bi:bi + 1, :, h:h + 1]
+        ref = O.chunk_bwd(s(host.q), s(host.k), s(host.v), s(host.g), s(host.beta), s(host.do), 0.6,
+                          host.h0[bi:bi + 1, h:h + 1], dhT[bi:bi + 1, h:h + 1])
+        for n, got, r in zip(NAMES[:5], grads[:5], ref[:5]):
+            assert rel_l2(s(got), r) <= BF16_TOL, (bi, h, n, rel_l2(s(got), r))
+        assert rel_l2(grads[5][bi:bi + 1, h:h + 1], ref[5]) <= BF16_TOL, (bi, h, "dh0")
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_random_shapes_training_pair(seed):
     """Seeded random shapes (ragged T, one to four heads, every compiled K x V pair, random scale, with and
