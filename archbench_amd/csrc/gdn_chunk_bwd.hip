@@ -319,8 +319,10 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     rdsc.load(wsdH + ci * K * V, V / 16, vs / 16, tid);
   };
   // The reads a chunk needs first: G, beta, Tm and the first slab's groups.  The workgroups are persistent (one
-  // per CU, looping over chunks) and issue these for their next chunk at the start of the current chunk's K
-  // phase, which reads no global memory: the loads are served while the K phase computes.
+  // per CU, looping over chunks) and issue these for their next chunk during the current chunk's K phase, which
+  // reads no global memory: the loads are served while the K phase computes.  They go out in two groups (G,
+  // beta, Tm, group A after the K phase's first barrier; group B after its second): issued together, the
+  // waves stalled on the memory queue instead of computing.
   float pg, pb;
   auto load_first = [&](int ci, bool order, bool with_b) {
     int nv;
@@ -432,11 +434,10 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   }
 
   // ---- K phase --------------------------------------------------------------------------------------------
-  // Issued unconditionally (the last chunk of a workgroup reads its own chunk again, 0.3% of the traffic): after
-  // a conditional block the compiler could not count the loads in flight and would wait for all of them at the
-  // first reuse of a register of the chunk's earlier reads.
+  // The next chunk's reads are issued unconditionally (the last chunk of a workgroup reads its own chunk again,
+  // 0.3% of the traffic): after a conditional block the compiler could not count the loads in flight and would
+  // wait for all of them at the first reuse of a register of the chunk's earlier reads.
   const int cnext = ci + (int)gridDim.x < nchunk ? ci + (int)gridDim.x : ci;
-  load_first(cnext, false, false);  // group B after the first K-phase products, not all at once
   T* sdWn = slab;                 // CH x LK   dR S0^T (= -dW)
   T* sdTm = sdWn + CH * LK;       // CH x LC
   T* sM1 = sdTm + CH * LC;        // CH x LC   dTm Tm^T
@@ -470,6 +471,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     }
   }
   __syncthreads();
+  load_first(cnext, false, false);
 
   // dX = Tm^T dW = -Tm^T dWn (rows of this wave), and rx = dX . k
   f32x4 aX[HK];
@@ -485,7 +487,6 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) rx[i] += aX[j][i] * kv[i];
   }
-  load_b(cnext, 0);
   // dTm rows:  dTm_ij = -beta_j gamma_j (dWn K^T)_ij + beta_j (dR V^T)_ij
 #pragma unroll
   for (int j = 0; j < HC; ++j) {
@@ -501,6 +502,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     }
   }
   __syncthreads();
+  load_b(cnext, 0);
   // M1 = dTm Tm^T (rows of this wave)
 #pragma unroll
   for (int j = 0; j < HC; ++j) {
