@@ -94,15 +94,20 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
   RegTile<T, CH, BV, STH, STATE_NT_LOAD> rdo;
   RegTile<T, CH, CH, STH, STATE_NT_LOAD> rtm, rp;
   float pG = 0.f, pB = 0.f;
-  // The next chunk's reads go out in two batches (k, q, dO after the first barrier; Tm, P, G, beta after the
-  // dR exchange), so that no wave stalls on a full memory queue for the whole set at once.
-  auto prefetch = [&](int c) {
+  // The next chunk's reads go out in three batches (k, q after the first barrier, dO after the second; Tm, P,
+  // G, beta after the dR exchange), so that no wave stalls on a full memory queue for the whole set at once
+  // (three batches measured 2% faster than two).
+  auto prefetch = [&](int c, int part) {
     const int64_t row0 = row0_of(c);
     const int nv = nvalid_of(c);
-    rk.load(k + row0 * K, (int64_t)H * K, nv, tid);
-    if constexpr (SEPU) ru.load(u + row0 * K, (int64_t)H * K, nv, tid);
-    rq.load(q + row0 * K, (int64_t)H * K, nv, tid);
-    rdo.load(dout + row0 * V + v0, (int64_t)H * V, nv, tid);
+    if (part != 2) {
+      rk.load(k + row0 * K, (int64_t)H * K, nv, tid);
+      if constexpr (SEPU) ru.load(u + row0 * K, (int64_t)H * K, nv, tid);
+      rq.load(q + row0 * K, (int64_t)H * K, nv, tid);
+    }
+    if (part != 1) {
+      rdo.load(dout + row0 * V + v0, (int64_t)H * V, nv, tid);
+    }
   };
   auto prefetch2 = [&](int c) {
     const int64_t row0 = row0_of(c), cidx = (int64_t)bh * NT + c;
@@ -136,7 +141,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
       sGam[l] = __expf(pG);
     }
     __syncthreads();
-    if (c > 0) prefetch(c - 1);
+    if (c > 0) prefetch(c - 1, 1);
 
     // dS leaving the chunk -> dh (fragment layout); partial U dS over this half's rows, for all tokens
     const float GC = sG[CH - 1];
@@ -164,6 +169,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
       for (int e = 0; e < 8; ++e) dOg[ib][e] = from_f<T>(to_f(dOb[ib][e]) * sGam[32 * ib + 8 * (l >> 4) + e]);
     }
     __syncthreads();
+    if (c > 0) prefetch(c - 1, 2);
     // dR (this half's token rows) = diag(exp(G_C - G)) K dS + P^T dO
     f32x4 dR[2];
 #pragma unroll
@@ -215,7 +221,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     }
     __syncthreads();  // every wave done with this chunk's inputs
   };
-  prefetch(NT - 1);
+  prefetch(NT - 1, 0);
   prefetch2(NT - 1);
   for (int c = NT - 1; c >= 0; --c) chunk(c);
   if (dh0) {
