@@ -21,7 +21,8 @@
 namespace gdn {
 
 // Persistent: workgroup x handles items x, x + gridDim.x, ... of the (b*h, chunk) grid (item = bh * NT + c), with
-// the next item's k, q, g and beta prefetched into registers while the current one is factored.
+// the next item's k, q, g and beta prefetched into registers while the current one is factored, in two batches
+// (k after the first barrier, q, g, beta after the second: 6% faster than all at once).
 // LDS overlays keep a workgroup at about 50 KB (bf16, K = 128), so three share a CU: A (fp32) overlays Q row for
 // row where the row pitches match (see factors_kq), and Tm overlays K once every wave has finished K U^T.
 template <typename T, int K>
@@ -51,18 +52,22 @@ void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, cons
   const int w = wave_id(), l = lane_id();
   RegTile<T, CH, K, NTHR, true> rk, rq, ru;  // k, q, u are read once here: nontemporal
   RegTok rt;
-  auto prefetch = [&](int it) {
+  auto prefetch = [&](int it, int part) {
     const int bh = it / NT, c = it - bh * NT;
     const int b = bh / H, h = bh - b * H;
     const int nvalid = min(CH, T_ - c * CH);
     const int64_t row0 = ((int64_t)b * T_ + (int64_t)c * CH) * H + h;
-    rk.load(k + row0 * K, (int64_t)H * K, nvalid);
-    rq.load(q + row0 * K, (int64_t)H * K, nvalid);
-    if constexpr (SEPU) ru.load(u + row0 * K, (int64_t)H * K, nvalid);
-    if (w == 0) rt.load(g, beta, row0, H, nvalid);
+    if (part != 2) {
+      rk.load(k + row0 * K, (int64_t)H * K, nvalid);
+      if constexpr (SEPU) ru.load(u + row0 * K, (int64_t)H * K, nvalid);
+    }
+    if (part != 1) {
+      rq.load(q + row0 * K, (int64_t)H * K, nvalid);
+      if (w == 0) rt.load(g, beta, row0, H, nvalid);
+    }
   };
   if (w == 0) sOne[l] = 1.f;
-  if ((int)blockIdx.x < nitems) prefetch(blockIdx.x);
+  if ((int)blockIdx.x < nitems) prefetch(blockIdx.x, 0);
   for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
     rk.store(sK, LK);
     rq.store(sQ, LK);
@@ -74,9 +79,11 @@ void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, cons
       gGc[(int64_t)it * CH + l] = G;
     }
     __syncthreads();
-    if (it + (int)gridDim.x < nitems) prefetch(it + gridDim.x);
+    const int itn = it + (int)gridDim.x;
+    if (itn < nitems) prefetch(itn, 1);
     factors_kq<T, K, 1>(sK, sU, sQ, sG, sB, scale, sA, sP, w);
     __syncthreads();  // every wave done with K (Tm overwrites it); A written
+    if (itn < nitems) prefetch(itn, 2);
     const f32x4 D = factors_diag<T>(sA, sD, sTm, nullptr, sOne, w);
     __syncthreads();
     factors_merge<T>(D, sA, sD, sTm, nullptr, sOne, w);
