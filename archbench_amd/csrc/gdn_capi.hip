@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <string.h>
 
+
 #include "../../include/gdn_mi355x.h"
 #include "gdn_launch.h"
 
@@ -153,6 +154,17 @@ static hipError_t timed(int stage, hipStream_t st, F&& launch) {
   return e;
 }
 
+// The chunk kernels are compiled for K in {64, 128}, V in {64, 128, 256} in bf16, and for K = 64, V in {64, 128}
+// in fp32 (the fp32 kernels hold whole fp32 tiles in LDS; at K = 128 they would not fit beside the state).
+static int shape_error(int K, int V, int dtype) {
+  if (dtype == DT_F32 && chunk_shape_supported(K, V, DT_BF16))
+    return fail(GDN_ERR_SHAPE, "fp32 chunk kernels are compiled for K=64, V in {64, 128} only; K=%d V=%d runs in "
+                "bf16 (pass bf16 q/k/v, e.g. under torch.autocast(dtype=torch.bfloat16) as archbench's trainer does)",
+                K, V);
+  return fail(GDN_ERR_SHAPE, "chunk kernels not compiled for K=%d V=%d dtype=%d (bf16: K in {64, 128}, "
+              "V in {64, 128, 256}; fp32: K=64, V in {64, 128})", K, V, dtype);
+}
+
 static int check_common(int B, int T, int H, int K, int V, int dtype) {
   if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
   if (B < 0 || T < 0 || H < 0 || K <= 0 || V <= 0)
@@ -251,7 +263,7 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* u, const voi
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!chunk_shape_supported(K, V, dtype))
-    return fail(GDN_ERR_SHAPE, "chunk kernels not compiled for K=%d V=%d dtype=%d", K, V, dtype);
+    return shape_error(K, V, dtype);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t nstate = (int64_t)B * H * K * V;
   if (B == 0 || H == 0) return GDN_OK;
@@ -289,7 +301,7 @@ static int chunk_bwd_impl(const void* q, const void* k, const void* u, const voi
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!chunk_shape_supported(K, V, dtype))
-    return fail(GDN_ERR_SHAPE, "chunk kernels not compiled for K=%d V=%d dtype=%d", K, V, dtype);
+    return shape_error(K, V, dtype);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t nstate = (int64_t)B * H * K * V;
   if (B == 0 || H == 0) return GDN_OK;
@@ -565,9 +577,11 @@ int gdn_cross_entropy_fwd_bwd(void* logits, const int64_t* target, float* loss, 
   return GDN_OK;
 }
 
-static int gates_check(int64_t ntok, int H, int dtype) {
+static int gates_check(int64_t ntok, int H, int dtype, bool backward = false) {
   if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
   if (ntok < 0 || H <= 0) return fail(GDN_ERR_ARG, "invalid sizes ntok=%lld H=%d", (long long)ntok, H);
+  if (backward && H > gates_max_heads())
+    return fail(GDN_ERR_SHAPE, "gates backward takes at most %d heads, got H=%d", gates_max_heads(), H);
   return GDN_OK;
 }
 
@@ -589,7 +603,7 @@ int gdn_gates_fwd(const void* a, const void* b, const float* A_log, const float*
 
 int gdn_gates_bwd_ws_bytes(int64_t ntok, int H, size_t* bytes) {
   g_err[0] = 0;
-  if (int e = gates_check(ntok, H, DT_F32)) return e;
+  if (int e = gates_check(ntok, H, DT_F32, true)) return e;
   if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
   *bytes = ntok ? gates_ws_bytes(ntok, H) : 0;
   return GDN_OK;
@@ -600,7 +614,7 @@ int gdn_gates_bwd(const void* a, const void* b, const float* A_log, const float*
                   float* db_bias, void* ws, size_t ws_bytes, int64_t ntok, int H, float beta_scale, float g_min,
                   int dtype, void* stream) {
   g_err[0] = 0;
-  if (int e = gates_check(ntok, H, dtype)) return e;
+  if (int e = gates_check(ntok, H, dtype, true)) return e;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (ntok == 0) {
     hipError_t e = copy_or_zero_bytes(nullptr, dA_log, (size_t)H * 4, st);

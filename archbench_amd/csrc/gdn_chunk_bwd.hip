@@ -38,19 +38,10 @@ namespace gdn {
 // rows (fp32), then the dR fragments, then the Z fragments (16 bytes per lane each).
 constexpr int SW = 2 * NWAVE;  // waves of the reverse sweep
 constexpr int STH = 64 * SW;
-#ifndef GDN_STATE_NT_LOAD
-#define GDN_STATE_NT_LOAD false
-#endif
-#ifndef GDN_STATE_NT_STORE
-#define GDN_STATE_NT_STORE true
-#endif
-#ifndef GDN_INTRA_NT
-#define GDN_INTRA_NT true
-#endif
 // the two V-block workgroups of a head read the same q, k, Tm and P (the second from L2): ordinary loads; dS_C and
 // dR are written once, nontemporal
-constexpr bool STATE_NT_LOAD = GDN_STATE_NT_LOAD, STATE_NT_STORE = GDN_STATE_NT_STORE;
-constexpr bool INTRA_NT = GDN_INTRA_NT;  // every read and write of the gradient kernel is single-use
+constexpr bool STATE_NT_LOAD = false, STATE_NT_STORE = true;
+constexpr bool INTRA_NT = true;  // every read and write of the gradient kernel is single-use
 
 template <typename T, int K, int BV, bool SEPU>
 __global__ __launch_bounds__(STH) void bwd_state_kernel(

@@ -25,10 +25,7 @@ namespace gdn {
 // apply the full state update.
 constexpr int FW = 2 * NWAVE;  // waves of the forward sweep
 constexpr int FTH = 64 * FW;
-#ifndef GDN_FWD_NT_LOAD
-#define GDN_FWD_NT_LOAD true
-#endif
-constexpr bool FWD_NT_LOAD = GDN_FWD_NT_LOAD;  // chunk inputs (measured faster with the hint)
+constexpr bool FWD_NT_LOAD = true;             // chunk inputs (measured faster with the hint)
 constexpr bool FWD_NT_STORE = true;            // O, and the stashed states and R: written once
 
 template <typename T, int K, int BV, int MODE, bool SEPU>

@@ -133,6 +133,8 @@ struct GateArgs {
   hipStream_t stream;
 };
 size_t gates_ws_bytes(int64_t ntok, int H);
+// The backward stages one tile of per-element gradients in LDS: at most this many heads per token.
+int gates_max_heads();
 hipError_t launch_gates(const GateArgs& a, bool backward);
 
 // Cross-entropy forward + backward in place on logits rows (gdn_ce.hip).

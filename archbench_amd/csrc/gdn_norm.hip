@@ -286,6 +286,8 @@ hipError_t launch_norm(const NormArgs& a, bool backward) {
 
 static int gates_tile_tokens(int H) { return std::max(1, GATE_TILE / H); }
 
+int gates_max_heads() { return GATE_TILE; }
+
 size_t gates_ws_bytes(int64_t ntok, int H) {
   const int64_t nwg = (ntok + gates_tile_tokens(H) - 1) / gates_tile_tokens(H);
   return ((size_t)nwg * 3 * H * 4 + 255) & ~size_t(255);

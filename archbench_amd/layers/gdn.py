@@ -119,13 +119,18 @@ class GatedDeltaNet(nn.Module):
         g, beta = ops.gdn_gates(self.a_proj(hidden_states), self.b_proj(hidden_states), self.A_log, self.dt_bias,
                                 None, 2.0 if self.allow_neg_eigval else 1.0, float("-inf"))
         state = entry["recurrent_state"] if entry is not None else None
-        dt = hidden_states.dtype if hidden_states.dtype in (torch.bfloat16, torch.float32) else torch.bfloat16
-        q, k, v = q.to(dt), k.to(dt), v.to(dt)
+        # The op runs in the dtype the projections produced, as fla's layer passes them on: bf16 under the
+        # trainer's bf16 autocast (archbench/trainer.py:66), even though the block hands the mixer fp32 hidden
+        # states (archbench/model.py:44-45); fp32 only for a caller that runs the projections in fp32.
+        if q.dtype not in (torch.bfloat16, torch.float32):
+            q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
         l2 = not self.use_short_conv  # the convolutions already normalised q and k
         if self.mode == "fused_recurrent" or (T == 1 and not torch.is_grad_enabled() and state is not None):
+            # decode: the cache owns its fp32 state, which the step kernel advances in place
             o, new_state = ops.fused_recurrent_gated_delta_rule(q, k, v, g, beta, initial_state=state,
                                                                 output_final_state=use_cache,
-                                                                use_qk_l2norm_in_kernel=l2)
+                                                                use_qk_l2norm_in_kernel=l2,
+                                                                inplace_final_state=use_cache)
         else:
             o, new_state = ops.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=state,
                                                       output_final_state=use_cache, use_qk_l2norm_in_kernel=l2)
@@ -134,5 +139,5 @@ class GatedDeltaNet(nn.Module):
                 past_key_values = {}
             past_key_values[self.layer_idx] = {"recurrent_state": new_state, "conv_state": conv_out}
         gate = self.g_proj(hidden_states).view(B, T, H, DV) if self.use_gate else None
-        o = self.o_norm(o.to(hidden_states.dtype), gate)
+        o = self.o_norm(o, gate)
         return self.o_proj(o.reshape(B, T, -1)), None, past_key_values

@@ -766,20 +766,43 @@ def recurrent_step(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, sta
     return _recurrent_step(q, k, v, g, beta, state, float(scale))
 
 
+def _owns_state(state: Tensor | None, B: int, H: int, K: int, V: int) -> bool:
+    """True if ``state`` can be advanced in place: a contiguous fp32 [B, H, K, V] tensor outside autograd."""
+    return (state is not None and state.dtype == torch.float32 and state.is_contiguous()
+            and tuple(state.shape) == (B, H, K, V) and not state.requires_grad)
+
+
 def fused_recurrent_gated_delta_rule(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
                                      scale: float | None = None, initial_state: Tensor | None = None,
-                                     output_final_state: bool = False, use_qk_l2norm_in_kernel: bool = False):
-    """fla-compatible recurrent entry point.  T = 1 (decode) runs the single-token step kernel on a copy of the
-    state; longer inputs run the chunk kernels, which compute the same recurrence."""
+                                     output_final_state: bool = False, use_qk_l2norm_in_kernel: bool = False,
+                                     inplace_final_state: bool = False):
+    """fla-compatible recurrent entry point.  T = 1 without grad (decode) runs the single-token step kernel
+    where it is compiled for (K, V) and the chunk kernels elsewhere; longer inputs run the chunk kernels, which
+    compute the same recurrence.
+
+    With ``inplace_final_state`` and an ``initial_state`` that is a contiguous fp32 [B, H, K, V] tensor, that
+    tensor is advanced in place and returned as the final state (one read and one write of the state per step;
+    fla's fused recurrent kernel offers the same flag).  Otherwise the initial state is left untouched and the
+    final state is a new tensor."""
     if use_qk_l2norm_in_kernel:
         q, k = _l2norm(q), _l2norm(k)
     if scale is None:
         scale = q.shape[-1] ** -0.5
     B, T, H, K = q.shape
     V = v.shape[-1]
-    if T == 1 and not torch.is_grad_enabled():
-        state = (torch.zeros(B, H, K, V, dtype=torch.float32, device=q.device) if initial_state is None
-                 else initial_state.float().clone().contiguous())
+    inplace = inplace_final_state and _owns_state(initial_state, B, H, K, V)
+    if T == 1 and not torch.is_grad_enabled() and _lib.supported("step", K, V, q.dtype):
+        if inplace:
+            state = initial_state
+        elif initial_state is None:
+            state = torch.zeros(B, H, K, V, dtype=torch.float32, device=q.device)
+        else:
+            state = initial_state.float().clone().contiguous()
         o = _recurrent_step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], beta[:, 0], state, float(scale))
-        return o[:, None], (state if output_final_state else None)
-    return chunk_gated_delta_rule(q, k, v, g, beta, scale, initial_state, output_final_state)
+        return o[:, None], (state if output_final_state or inplace else None)
+    o, hT = chunk_gated_delta_rule(q, k, v, g, beta, scale, initial_state, output_final_state or inplace)
+    if inplace:
+        with torch.no_grad():
+            initial_state.copy_(hT)
+        hT = initial_state
+    return o, hT

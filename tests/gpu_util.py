@@ -30,3 +30,13 @@ def device_inputs(B, T, H, K, V, dtype, seed=0, g_shift=4.0, h0_std=None, with_d
     host = type(x)(r(x.q), r(x.k), r(x.v), x.g, x.beta, x.h0, r(x.do))
     dev = x.to("cuda", dtype)
     return host, dev
+
+
+def assert_fp32_close(what: str, names, got, ref, tol: float) -> None:
+    """fp32 bar: absolute max-abs error <= tol for every tensor; the achieved errors (and each reference's
+    largest magnitude, for scale) are printed before the check."""
+    errs = {n: (max_abs(a, b), b.abs().max().item()) for n, a, b in zip(names, got, ref) if b is not None}
+    print(f"[fp32 max-abs] {what}: " + ", ".join(f"{n} {e:.2e} (|ref| {m:.3g})" for n, (e, m) in errs.items()),
+          flush=True)
+    bad = {n: e for n, (e, _) in errs.items() if not e <= tol}
+    assert not bad, f"{what}: max-abs above {tol}: {bad}"

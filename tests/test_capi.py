@@ -88,3 +88,26 @@ def test_argument_errors_do_not_touch_the_gpu():
     assert rc == _lib.GDN_ERR_ARG  # null pointers rejected before any launch
     with pytest.raises(ValueError):
         _lib.check(_lib.GDN_ERR_SHAPE, "x")
+
+
+def test_gates_backward_rejects_too_many_heads():
+    """The gates backward stages a tile of per-element gradients in LDS (1024 elements): more heads than that
+    per token are refused before anything is launched."""
+    lib = _lib.load()
+    n = ctypes.c_size_t(0)
+    assert lib.gdn_gates_bwd_ws_bytes(4, 1024, ctypes.byref(n)) == _lib.GDN_OK
+    assert lib.gdn_gates_bwd_ws_bytes(4, 1025, ctypes.byref(n)) == _lib.GDN_ERR_SHAPE
+    assert b"1024" in lib.gdn_last_error()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rc = lib.gdn_gates_bwd(p, p, p, None, None, p, p, p, p, None, None, None, p, 1 << 30, 4, 2000, 1.0,
+                           float("-inf"), 1, None)
+    assert rc == _lib.GDN_ERR_SHAPE
+
+
+def test_fp32_head_size_error_names_the_bf16_route():
+    """fp32 chunk kernels exist for K = 64 only; K = 128 in fp32 is refused with a message pointing to bf16."""
+    lib = _lib.load()
+    rc = lib.gdn_chunk_fwd(None, None, None, None, None, None, None, None, None, 0, 1, 64, 1, 128, 256, 1.0,
+                           _lib.DTYPE_F32, None)
+    assert rc == _lib.GDN_ERR_SHAPE
+    assert b"bf16" in lib.gdn_last_error() and b"K=64" in lib.gdn_last_error()

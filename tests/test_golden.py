@@ -1,6 +1,7 @@
 """Known-answer vectors (tests/golden/gdn_cfg0_slice.npz, written by tests/golden/make_golden.py from the fp64
 oracle on a slice of config 0): the input generator and the oracle must reproduce them on the CPU, and the
-HIP kernels must match them on the GPU at the fp32 bar (max-abs <= 1e-4, gradients relative to their scale)."""
+HIP kernels must match them on the GPU at the fp32 bar (absolute max-abs <= 1e-4 for the output, the final
+state and every gradient)."""
 
 import os
 
@@ -41,6 +42,7 @@ def test_oracle_reproduces_fixture_outputs():
 @pytest.mark.gpu
 def test_kernels_match_fixture_fp32():
     from archbench_amd import ops
+    from tests.gpu_util import assert_fp32_close
 
     f = {k: v.cuda() for k, v in load().items()}
     s = float(f["scale"])
@@ -48,6 +50,5 @@ def test_kernels_match_fixture_fp32():
     assert (o - f["o"]).abs().max().item() <= 1e-4
     assert (hT - f["hT"]).abs().max().item() <= 1e-4
     grads = ops.chunk_bwd(f["q"], f["k"], f["v"], f["g"], f["beta"], None, f["do"], f["dhT"], s)
-    for n, a in zip(["dq", "dk", "dv", "dg", "dbeta", "dh0"], grads):
-        ref = f[n]
-        assert (a - ref).abs().max().item() <= 1e-4 * max(1.0, ref.abs().max().item()), n
+    names = ["dq", "dk", "dv", "dg", "dbeta", "dh0"]
+    assert_fp32_close("golden cfg0 slice", names, grads, [f[n] for n in names], 1e-4)

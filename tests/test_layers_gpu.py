@@ -5,7 +5,7 @@ torch.library.opcheck."""
 import pytest
 import torch
 
-from archbench_amd import layers, ops
+from archbench_amd import _lib, layers, ops
 from oracle import gdn_oracle as O
 from tests.gpu_util import banner, rel_l2
 
@@ -55,6 +55,58 @@ def test_layer_matches_oracle_forward_backward(monkeypatch):
         assert rel_l2(g1[n], p.grad) <= 2e-2, n
 
 
+GDN_YAML = dict(head_dim=128, expand_v=2.0, use_gate=True, use_short_conv=True, conv_size=4)  # arch/gdn.yaml
+
+
+def test_reference_config_under_autocast(monkeypatch):
+    """The mixer exactly as archbench's model builds it for configs/65m/gdn.yaml (d_model 512, 4 heads, head_dim
+    128, expand_v 2 -> K = 128, V = 256), fed fp32 hidden states under bf16 autocast as Block.forward does under
+    the trainer (model.py:44-45, trainer.py:66): the op must run its bf16 kernels, and output, input gradient and
+    every parameter gradient must match the same layer with the token mixing in the fp64 oracle."""
+    banner("layer at configs/65m/gdn.yaml under bf16 autocast vs oracle-backed layer")
+    torch.manual_seed(5)
+    m = layers.build_mixer("gdn", 512, 0, 10, num_heads=4, **GDN_YAML).cuda()
+    for p in m.parameters():
+        if p.dim() == 2:
+            torch.nn.init.normal_(p, std=0.03)
+    seen = []
+    real = ops.chunk_gated_delta_rule
+
+    def spy(q, k, v, *a, **kw):
+        seen.append((q.dtype, k.dtype, v.dtype, q.shape[-1], v.shape[-1]))
+        return real(q, k, v, *a, **kw)
+
+    monkeypatch.setattr("archbench_amd.layers.gdn.ops.chunk_gated_delta_rule", spy)
+    x = torch.randn(2, 200, 512, device="cuda", generator=torch.Generator("cuda").manual_seed(2))
+    x1 = x.clone().requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y1 = m(x1)
+    dy = torch.randn(y1.shape, device="cuda", generator=torch.Generator("cuda").manual_seed(3))
+    (y1.float() * dy).sum().backward()
+    assert seen == [(torch.bfloat16, torch.bfloat16, torch.bfloat16, 128, 256)], seen
+    g1 = {n: p.grad.clone() for n, p in m.named_parameters()}
+    m.zero_grad()
+    monkeypatch.setattr("archbench_amd.layers.gdn.ops.chunk_gated_delta_rule", _oracle_op)
+    x2 = x.clone().requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y2 = m(x2)
+    (y2.float() * dy).sum().backward()
+    errs = {"y": rel_l2(y1.float(), y2.float()), "dx": rel_l2(x1.grad, x2.grad)}
+    errs.update({n: rel_l2(g1[n], p.grad) for n, p in m.named_parameters()})
+    print("rel-L2 vs oracle-backed layer:", {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    assert errs["y"] <= 1e-2 and errs["dx"] <= 1e-2, errs
+    for n, p in m.named_parameters():
+        assert errs[n] <= 2e-2, (n, errs[n])
+
+
+def test_fp32_layer_at_k128_raises_with_bf16_hint():
+    """Without autocast the projections are fp32; the fp32 kernels exist for K = 64 only, so the reference
+    config's K = 128 is refused with a message naming the bf16 route (no silent precision change)."""
+    m = layers.build_mixer("gdn", 256, 0, 2, num_heads=2, **GDN_YAML).cuda()
+    with pytest.raises(ValueError, match="bf16"):
+        m(torch.randn(1, 64, 256, device="cuda"))
+
+
 def test_prefill_then_decode_matches_full_sequence():
     banner("prefill + decode cache")
     m = _layer(3).eval()
@@ -97,3 +149,56 @@ def test_opcheck():
             b.requires_grad_(), h0.requires_grad_(), 0.5)
     torch.library.opcheck(torch.ops.archbench_amd.gdn_chunk_fwd.default, args,
                           test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
+
+
+def test_decode_advances_cache_state_in_place(monkeypatch):
+    """A cached decode step advances the cache's own fp32 state tensor (same storage, no copy of the state) and
+    equals the oracle's step from the state before it."""
+    banner("decode step in place on the cache state")
+    m = _layer(4).eval()
+    x = torch.randn(2, 65, 256, device="cuda", generator=torch.Generator("cuda").manual_seed(6))
+    seen = []
+    real = ops.fused_recurrent_gated_delta_rule
+
+    def spy(q, k, v, g, beta, **kw):
+        seen.append((q.detach().float().cpu(), k.detach().float().cpu(), v.detach().float().cpu(), g.cpu(),
+                     beta.cpu(), kw["initial_state"].clone().cpu()))
+        return real(q, k, v, g, beta, **kw)
+
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        cache = {}
+        _, _, cache = m.layer(x[:, :64], use_cache=True, past_key_values=cache)
+        S = cache[0]["recurrent_state"]
+        ptr = S.data_ptr()
+        monkeypatch.setattr("archbench_amd.layers.gdn.ops.fused_recurrent_gated_delta_rule", spy)
+        _, _, cache = m.layer(x[:, 64:65], use_cache=True, past_key_values=cache)
+    S1 = cache[0]["recurrent_state"]
+    assert S1 is S and S1.data_ptr() == ptr
+    q, k, v, g, beta, S0 = seen[0]
+    o_ref, S_ref = O.step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], beta[:, 0], S0, 64 ** -0.5)
+    assert rel_l2(S1, S_ref) <= 1e-5
+
+
+@pytest.mark.parametrize("K,V", [(64, 256), (128, 64)])
+def test_decode_shapes_without_step_kernel(K, V):
+    """Decode at (K, V) pairs the step kernel is not compiled for runs through the chunk kernels (which cover
+    them), in place when asked, and agrees with the oracle step."""
+    banner(f"decode without a step kernel K={K} V={V}")
+    assert not _lib.supported("step", K, V, torch.bfloat16) and _lib.supported("chunk", K, V, torch.bfloat16)
+    B, H = 3, 2
+    gen = torch.Generator().manual_seed(7)
+    q = torch.nn.functional.normalize(torch.randn(B, 1, H, K, generator=gen), dim=-1)
+    k = torch.nn.functional.normalize(torch.randn(B, 1, H, K, generator=gen), dim=-1)
+    v = torch.randn(B, 1, H, V, generator=gen)
+    g = torch.nn.functional.logsigmoid(torch.randn(B, 1, H, generator=gen) + 4)
+    b = torch.sigmoid(torch.randn(B, 1, H, generator=gen))
+    S0 = torch.randn(B, H, K, V, generator=gen) * 0.1
+    r = lambda t: t.to(torch.bfloat16).float()
+    o_ref, S_ref = O.step(r(q[:, 0]), r(k[:, 0]), r(v[:, 0]), g[:, 0], b[:, 0], S0, 0.5)
+    S = S0.cuda()
+    with torch.no_grad():
+        o, S1 = ops.fused_recurrent_gated_delta_rule(*(t.cuda().to(torch.bfloat16) for t in (q, k, v)), g.cuda(),
+                                                     b.cuda(), scale=0.5, initial_state=S,
+                                                     output_final_state=True, inplace_final_state=True)
+    assert S1 is S
+    assert rel_l2(o[:, 0], o_ref) <= 1e-2 and rel_l2(S, S_ref) <= 1e-2
