@@ -3,6 +3,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <mutex>
 
 #include "../../include/gdn_mi355x.h"
 #include "gdn_launch.h"
@@ -351,6 +353,85 @@ int gdn_chunk_fwd(const void* q, const void* k, const void* v, const float* g, c
                   int V, float scale, int dtype, void* stream) {
   return chunk_fwd_impl(q, k, nullptr, v, g, beta, h0, o, hT, ws, ws_bytes, B, T, H, K, V, scale, dtype, stream,
                         false);
+}
+
+}  // extern "C"
+
+namespace gdn {
+
+// ---- allocation-free forward ----------------------------------------------------------------------------------
+// The chunk-factor workspace of gdn_chunk_fwd_noalloc lives in this file-scope device array: each GPU the library
+// runs on holds its own copy (GDN_NOALLOC_SCRATCH_BYTES) from module load to process exit.  Host code never
+// passes the array's name to a kernel (on the host it is a stand-in, not a device address): its device address is
+// looked up once per device with that device current and kept in g_scratch_ptr.  Nothing in it needs clearing:
+// the factors kernel writes every byte the forward sweep then reads.
+static __device__ __align__(256) unsigned char scratch[GDN_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];  // per device ordinal
+
+static int scratch_for_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(GDN_ERR_LAUNCH, "no usable current HIP device (ordinal %d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(GDN_ERR_LAUNCH, "scratch symbol lookup on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GDN_OK;
+}
+
+}  // namespace gdn
+
+extern "C" {
+
+int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                          const float* h0, void* o, float* hT, int B, int T, int H, int K, int V, float scale,
+                          int dtype, void* stream) {
+  g_err[0] = 0;
+  if (int e = check_common(B, T, H, K, V, dtype)) return e;
+  if (!chunk_shape_supported(K, V, dtype)) return shape_error(K, V, dtype);
+  const size_t cap = GDN_NOALLOC_SCRATCH_BYTES;
+  const size_t one = chunk_ws_bytes(1, T, H, K, V, dtype, WS_FACT, nullptr, nullptr);
+  if (one > cap)
+    return fail(GDN_ERR_WORKSPACE, "one sequence needs %zu bytes of chunk factors (H * ceil(T/64) = %lld chunks), "
+                "more than the %zu-byte scratch of the allocation-free forward; use gdn_chunk_fwd", one,
+                (long long)H * ((T + CH_TOKENS - 1) / CH_TOKENS), cap);
+  void* ws = nullptr;
+  if (int e = scratch_for_current_device(&ws)) return e;
+  // As many sequences per launch group as fit; the groups run one after another on the stream, each reusing the
+  // scratch.  Splitting the batch moves every pointer by whole sequences, which keeps the 16-byte alignment the
+  // kernels need as long as a sequence's g / beta rows (T * H fp32) are a multiple of 16 bytes.
+  int nb = (int)std::min<size_t>((size_t)(B > 0 ? B : 1), cap / one);
+  while (nb > 1 && chunk_ws_bytes(nb, T, H, K, V, dtype, WS_FACT, nullptr, nullptr) > cap) --nb;
+  if (nb < B && ((size_t)T * H * 4) % 16 != 0)
+    return fail(GDN_ERR_WORKSPACE, "B=%d sequences need %zu bytes of chunk factors, more than the %zu-byte scratch, "
+                "and T * H = %lld is not a multiple of 4, so the batch cannot be split; use gdn_chunk_fwd", B,
+                chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT, nullptr, nullptr), cap, (long long)T * H);
+  const size_t es = dtype == DT_BF16 ? 2 : 4;
+  const char* cq = static_cast<const char*>(q);
+  const char* ck = static_cast<const char*>(k);
+  const char* cv = static_cast<const char*>(v);
+  char* co = static_cast<char*>(o);
+  if (B == 0)  // nothing to compute; the shared checks still run
+    return chunk_fwd_impl(q, k, nullptr, v, g, beta, h0, o, hT, ws, cap, 0, T, H, K, V, scale, dtype, stream, false);
+  for (int b0 = 0; b0 < B; b0 += nb) {
+    const int n = B - b0 < nb ? B - b0 : nb;
+    const int64_t tok = (int64_t)b0 * T * H;  // token rows before this group
+    const int64_t st = (int64_t)b0 * H * K * V;
+    const int e = chunk_fwd_impl(cq ? cq + tok * K * es : nullptr, ck ? ck + tok * K * es : nullptr, nullptr,
+                                 cv ? cv + tok * V * es : nullptr, g ? g + tok : nullptr,
+                                 beta ? beta + tok : nullptr, h0 ? h0 + st : nullptr,
+                                 co ? co + tok * V * es : nullptr, hT ? hT + st : nullptr, ws, cap, n, T, H, K, V,
+                                 scale, dtype, stream, false);
+    if (e != GDN_OK) return e;
+  }
+  return GDN_OK;
 }
 
 int gdn_chunk_fwd_stash(const void* q, const void* k, const void* v, const float* g, const float* beta,

@@ -71,6 +71,21 @@ int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, c
                   float* dbeta, float* dh0, void* ws, size_t ws_bytes, int B, int T, int H, int K, int V,
                   float scale, int dtype, void* stream);
 
+/* Allocation-free chunkwise forward.  No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It computes
+ * exactly what gdn_chunk_fwd computes, with the same kernels, but takes no workspace: the chunk factors go to a
+ * scratch array of GDN_NOALLOC_SCRATCH_BYTES that the library keeps in device memory on each GPU it runs on
+ * (until the process ends).  The call allocates and frees nothing.  Limit: one sequence's factors,
+ * H * ceil(T/64) chunks of 16,640 bytes (bf16; 33,024 in fp32), must fit in the scratch; larger batches run as
+ * consecutive groups of sequences on `stream` (this needs T * H to be a multiple of 4), otherwise
+ * GDN_ERR_WORKSPACE.  Every call on one GPU shares that GPU's scratch, so calls that overlap in time on one GPU
+ * (concurrent streams, or several host threads) race and give wrong results: serialise them.  The stream must
+ * belong to the calling thread's current device. */
+#define GDN_NOALLOC_SCRATCH_BYTES ((size_t)80 << 20)
+int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                          const float* h0, void* o, float* hT, int B, int T, int H, int K, int V, float scale,
+                          int dtype, void* stream);
+
 /* Training pair.  gdn_chunk_fwd_stash computes what gdn_chunk_fwd computes and also writes into `stash` the
  * per-chunk intermediates the backward needs (chunk factors, chunk-local decay, the state entering every chunk
  * and R = U - W S); gdn_chunk_bwd_stashed, called later with the same inputs and the same stash (unchanged in

@@ -1,0 +1,64 @@
+"""gdn_chunk_fwd_noalloc (the allocation-free forward) against gdn_chunk_fwd, both through the C ABI: same
+kernels, so o and hT must agree bit for bit.  Two calls in a row on the shared scratch (the second smaller, so
+it runs over what the first left there), a batch large enough to run as several sequence groups, and the size
+limit refused before anything is launched."""
+
+import ctypes
+
+import pytest
+import torch
+
+from archbench_amd import _lib
+from tests.gpu_util import banner, device_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _both(B, T, H, K, V, dtype, h0_std, seed, scale):
+    banner(f"noalloc fwd B={B} T={T} H={H} K={K} V={V} {dtype} h0={h0_std}")
+    lib = _lib.load()
+    _, d = device_inputs(B, T, H, K, V, dtype, seed=seed, h0_std=h0_std)
+    dt = _lib.dtype_code(dtype)
+    stream = _lib.stream_ptr(d.q.device)
+    o_ref = torch.empty(B, T, H, V, dtype=dtype, device="cuda")
+    hT_ref = torch.empty(B, H, K, V, device="cuda")
+    ws = torch.empty(_lib.ws_bytes("fwd", B, T, H, K, V, dtype), dtype=torch.uint8, device="cuda")
+    rc = lib.gdn_chunk_fwd(_ptr(d.q), _ptr(d.k), _ptr(d.v), _ptr(d.g), _ptr(d.beta), _ptr(d.h0), _ptr(o_ref),
+                           _ptr(hT_ref), _ptr(ws), ws.numel(), B, T, H, K, V, scale, dt, stream)
+    _lib.check(rc, "gdn_chunk_fwd")
+    o = torch.full((B, T, H, V), float("nan"), dtype=dtype, device="cuda")
+    hT = torch.full((B, H, K, V), float("nan"), device="cuda")
+    rc = lib.gdn_chunk_fwd_noalloc(_ptr(d.q), _ptr(d.k), _ptr(d.v), _ptr(d.g), _ptr(d.beta), _ptr(d.h0), _ptr(o),
+                                   _ptr(hT), B, T, H, K, V, scale, dt, stream)
+    _lib.check(rc, "gdn_chunk_fwd_noalloc")
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref), (o - o_ref).abs().max().item()
+    assert torch.equal(hT, hT_ref), (hT - hT_ref).abs().max().item()
+
+
+def test_two_calls_in_a_row_second_smaller():
+    _both(4, 1000, 8, 128, 128, torch.bfloat16, 0.1, 11, 0.7)
+    _both(1, 130, 2, 64, 64, torch.bfloat16, None, 12, 1.0)
+
+
+def test_fp32_call():
+    _both(2, 300, 2, 64, 64, torch.float32, 0.1, 13, 0.5)
+
+
+def test_batch_in_sequence_groups():
+    """B=8, T=4096, H=16 bf16 needs 136 MB of factors: more than the scratch, so the call runs as consecutive
+    groups of sequences, each reusing the scratch."""
+    _both(8, 4096, 16, 128, 128, torch.bfloat16, None, 14, 1.0)
+
+
+def test_limit_refused_before_launch():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
+    rc = lib.gdn_chunk_fwd_noalloc(p, p, p, p, p, None, p, None, 1, 1 << 20, 16, 128, 128, 1.0,
+                                   _lib.DTYPE_BF16, None)
+    assert rc == _lib.GDN_ERR_WORKSPACE
+    assert b"scratch" in lib.gdn_last_error()
