@@ -54,7 +54,7 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
   }
   if (parts & WS_GRAD) {
     ws.dhs = take(BH * NT * (size_t)K * V * es);
-    ws.dRs = take(BH * NT * CH_TOKENS * (size_t)V * es);
+    ws.dYs = take(BH * NT * CH_TOKENS * (size_t)V * es);
   }
   if (carve) {
     if (parts & WS_FACT) {
@@ -64,7 +64,7 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
       carve->hs = ws.hs; carve->Rs = ws.Rs;
     }
     if (parts & WS_GRAD) {
-      carve->dhs = ws.dhs; carve->dRs = ws.dRs;
+      carve->dhs = ws.dhs; carve->dYs = ws.dYs;
     }
   }
   return off;

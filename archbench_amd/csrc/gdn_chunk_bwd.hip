@@ -6,18 +6,20 @@
 // bwd_state: one workgroup per (64-wide V block, b*h), reverse over chunks, reading the chunk factors; each
 //   wave carries a 16-column slab of dS in MFMA accumulators.
 //     dR  = P^T dO + Kd dS_C                         Kd = diag(exp(G_C - G)) K
-//     dS0 = gamma_C dS_C + s (diag(gamma) Q)^T dO - W^T dR,   W^T dR = K^T diag(beta gamma) (Tm^T dR)
-//   Writes dS_C (the gradient w.r.t. the state leaving each chunk) and dR per chunk, and dh0.
+//     dY  = Tm^T dR                                  (the gradient w.r.t. Y, where R = Tm Y, Y = beta (V - gamma K S0))
+//     dS0 = gamma_C dS_C + s (diag(gamma) Q)^T dO - K^T diag(beta gamma) dY
+//   Writes dS_C (the gradient w.r.t. the state leaving each chunk) and dY per chunk, and dh0.
 //   (The reverse state-gradient recurrence of fla's chunk_gated_delta_rule_bwd_dhu, called at
 //   archbench/layers/nsgdn.py:378.)
 //
-// bwd_intra: one workgroup per (chunk, b*h) with the full K and V of the chunk; all gradients:
+// bwd_intra: persistent, one workgroup per CU looping over (chunk, b*h) items with the full K and V of a chunk;
+// all gradients.  With R = Tm Y the WY backward needs no Tm: dA = -Tm^T (dR Y^T) Tm^T = -(Tm^T dR)(Tm Y)^T =
+// -dY R^T, and the gradient through Y's K S0 term is -beta gamma dY S0^T, so
 //     dq  = s gamma (dO S0^T) + (dP o sE) K                         dP = dO R^T  (i >= j)
-//     dk  = dte (R dS_C^T) + (dP o sE)^T Q + beta gamma (Tm^T dW) + (D + D^T) K
-//     dv  = beta (Tm^T dR)                                          dW = -dR S0^T
-//     dA  = -Tm^T (dW X^T + dR Y^T) Tm^T  (strict lower),  D = dA o beta_i E,  X = beta gamma K, Y = beta V
-//     dbeta = gamma (Tm^T dW . k) + (Tm^T dR . v) + rowsum(dA o KK o E)
-//     dG  = s gamma (dO S0^T . q) - dte (R dS_C^T . k) + beta gamma (Tm^T dW . k)
+//     dk  = dte (R dS_C^T) + (dP o sE)^T Q - beta gamma (dY S0^T) + (D + D^T) K
+//     dv  = beta dY                                                 dA = -dY R^T (strict lower), D = dA o beta_i E
+//     dbeta = -gamma (dY S0^T . k) + (dY . v) + rowsum(dA o KK o E)
+//     dG  = s gamma (dO S0^T . q) - dte (R dS_C^T . k) - beta gamma (dY S0^T . k)
 //           + rowsum - colsum of (dP o P + dA o A),   dG_last += sum dte (R dS_C^T . k) + gamma_C <dS_C, S0>
 //     dg  = reverse chunk-local cumsum of dG
 //   (fla's chunk_bwd_dv_local + chunk_bwd_dqkwg, the WY backward of nsgdn.py:279-330 and the reverse cumsum
@@ -25,7 +27,7 @@
 //
 // SEPU (separate write keys U, the n-step family's nsgdn_chunk_bwd, nsgdn.py:369-382): U replaces K wherever K
 // is a write key -- Kd dS_C in dR, the column side of K K^T and Q K^T, and the state update -- and the
-// gradients split into dk (read: beta gamma Tm^T dW + D U) and du (write: dte R dS_C^T + (dP o sE)^T Q + D^T K);
+// gradients split into dk (read: -beta gamma dY S0^T + D U) and du (write: dte R dS_C^T + (dP o sE)^T Q + D^T K);
 // beta may be absent (row scale 1, no dbeta).
 #include "gdn_chunk_common.h"
 #include "gdn_launch.h"
@@ -48,7 +50,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u, const T* __restrict__ dout,
     const float* __restrict__ beta,
     const T* __restrict__ gTm, const T* __restrict__ gP, const float* __restrict__ gGc,
-    const float* __restrict__ dhT, float* __restrict__ dh0, T* __restrict__ wsdH, T* __restrict__ wsdR, int T_,
+    const float* __restrict__ dhT, float* __restrict__ dh0, T* __restrict__ wsdH, T* __restrict__ wsdY, int T_,
     int H, int V, int NT, float scale) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
@@ -173,9 +175,8 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib) mma(dR[j], frag_oct(sP, LC, 16 * rt_, 32 * ib), dOb[ib]);
     }
-    // dR -> global and to the other half; Z (this half's token rows) = diag(beta gamma) Tm^T dR
+    // dR to the other half; dY (this half's token rows) = Tm^T dR -> global; Z = diag(beta gamma) dY
     const F dRmine = frag_acc2<T>(dR[0], dR[1]);
-    store_fragblk<T, STATE_NT_STORE>(wsdR + cidx * CH * V, CH, hf, cb, ncb, dRmine);
     xR[w][l] = dRmine;
     __syncthreads();
     if (c > 0) prefetch2(c - 1);
@@ -188,12 +189,15 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
       Z[j] = f32x4{0.f, 0.f, 0.f, 0.f};
       mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, 0), dR0);
       mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, 32), dR1);
+    }
+    store_fragblk<T, STATE_NT_STORE>(wsdY + cidx * CH * V, CH, hf, cb, ncb, frag_acc2<T>(Z[0], Z[1]));
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * rt_ + acc_row(i);
+        const int r = 16 * (2 * hf + j) + acc_row(i);
         Z[j][i] *= sB[r] * sGam[r];
       }
-    }
     const F Zmine = frag_acc2<T>(Z[0], Z[1]);
     xZ[w][l] = Zmine;
     __syncthreads();
@@ -250,26 +254,24 @@ constexpr int ITH = IW * 64;   // its threads
 template <typename T, int K, int V, int VS, bool SEPU>
 __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u, const T* __restrict__ v,
-    const float* __restrict__ beta, const T* __restrict__ dout, const T* __restrict__ wsTm,
-    const float* __restrict__ wsGc, const T* __restrict__ wsH, const T* __restrict__ wsR,
-    const T* __restrict__ wsdH, const T* __restrict__ wsdR, T* __restrict__ dq, T* __restrict__ dk,
-    T* __restrict__ du, T* __restrict__ dv, float* __restrict__ dg, float* __restrict__ dbeta, int T_, int H,
-    int NT, int BH, float scale) {
+    const float* __restrict__ beta, const T* __restrict__ dout, const float* __restrict__ wsGc,
+    const T* __restrict__ wsH, const T* __restrict__ wsR, const T* __restrict__ wsdH, const T* __restrict__ wsdY,
+    T* __restrict__ dq, T* __restrict__ dk, T* __restrict__ du, T* __restrict__ dv, float* __restrict__ dg,
+    float* __restrict__ dbeta, int T_, int H, int NT, int BH, float scale) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LS = VS + PT;
   constexpr int NKT = K / 16;   // column tiles over K
   constexpr int NVT = VS / 16;  // column tiles over a V slab
   constexpr int HK = NKT / 2, HV = NVT / 2, HC = 2;  // tiles per half: over K, over the slab, over the chunk
-  // slab region: V phase {dO, V : CH x LS; R^T, dR^T : VS x LC; S0^T, dSC^T : VS x LK (column-major, so the
-  // fragment-layout tiles are written as 4-element runs)}; K phase {dWn : CH x LK; dTm, M1, D, dPm : CH x LC}
+  // slab region: V phase {dO, V : CH x LS; R^T, dY^T : VS x LC; S0^T, dSC^T : VS x LK (column-major, so the
+  // fragment-layout tiles are written as 4-element runs)}; K phase {dq, dk staging : CH x LK; D, dPm : CH x LC}
   constexpr int SLAB_V = 2 * CH * LS + 2 * VS * LC + 2 * VS * LK;
-  constexpr int SLAB_K = CH * LK + 4 * CH * LC;
+  constexpr int SLAB_K = 2 * CH * LK + 2 * CH * LC;
   constexpr int SLAB = SLAB_V > SLAB_K ? SLAB_V : SLAB_K;
   __shared__ __attribute__((aligned(16))) T sQ[CH * LK];
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
   __shared__ __attribute__((aligned(16))) T sU_[SEPU ? CH * LK : 8];
   T* sU = SEPU ? sU_ : sK;  // write keys
-  __shared__ __attribute__((aligned(16))) T sTm[CH * LC];
   __shared__ __attribute__((aligned(16))) T slab[SLAB];
   __shared__ __attribute__((aligned(16))) T sdv[CH * LS];  // dv of the current slab, for the coalesced store
   __shared__ float sG[CH], sB[CH], sdG[CH], sLast[CH], sColZ[NWAVE][CH], sRed[IW];
@@ -277,10 +279,10 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 
   T* sdO = slab;
   T* sV = sdO + CH * LS;
-  T* sRt = sV + CH * LS;     // R^T     [VS][LC]
-  T* sdRt = sRt + VS * LC;   // dR^T    [VS][LC]
-  T* sS0t = sdRt + VS * LC;  // S0^T    [VS][LK]
-  T* sdSCt = sS0t + VS * LK; // dS_C^T  [VS][LK]
+  T* sRt = sV + CH * LS;      // R^T     [VS][LC]
+  T* sdYt = sRt + VS * LC;    // dY^T    [VS][LC]
+  T* sS0t = sdYt + VS * LC;   // S0^T    [VS][LK]
+  T* sdSCt = sS0t + VS * LK;  // dS_C^T  [VS][LK]
 
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
   const int rb = w & (NWAVE - 1), hf = w >> 2;
@@ -297,42 +299,39 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   };
 
   // Global reads are issued as 16-byte register tiles (RegTile, FragTile) in the order they are consumed, each
-  // V slab in two groups: A = {dO, V, R, dR} (and Tm, G, beta first) feeds dO R^T, dR V^T and Tm^T dR; B =
-  // {S0, dS_C} feeds the products with the states.  Group B and Q, K stay in flight while group A is computed,
-  // and the next slab's groups are issued as soon as their registers are free.
+  // V slab in two groups: A = {dO, V, R, dY} (and G, beta first) feeds dO R^T, dY R^T and dv; B = {S0, dS_C}
+  // feeds the products with the states.  Group B and Q, K stay in flight while group A is computed, and the
+  // next slab's groups are issued as soon as their registers are free.
   RegTile<T, CH, K, ITH, INTRA_NT> tq, tk, tu;
-  RegTile<T, CH, CH, ITH, INTRA_NT> rtm;
   RegTile<T, CH, VS, ITH, INTRA_NT> rdo, rv;
-  FragTile<T, CH, VS, ITH, INTRA_NT> rr, rdr;
+  FragTile<T, CH, VS, ITH, INTRA_NT> rr, rdy;
   FragTile<T, K, VS, ITH, INTRA_NT> rs0, rdsc;
   auto load_a = [&](int64_t ci, int64_t r0, int nv, int vs) {
     rdo.load(dout + r0 * V + vs, (int64_t)H * V, nv, tid);
     rv.load(v + r0 * V + vs, (int64_t)H * V, nv, tid);
     rr.load(wsR + ci * CH * V, V / 16, vs / 16, tid);
-    rdr.load(wsdR + ci * CH * V, V / 16, vs / 16, tid);
+    rdy.load(wsdY + ci * CH * V, V / 16, vs / 16, tid);
   };
   auto load_b = [&](int64_t ci, int vs) {
     rs0.load(wsH + ci * K * V, V / 16, vs / 16, tid);
     rdsc.load(wsdH + ci * K * V, V / 16, vs / 16, tid);
   };
-  // The reads a chunk needs first: G, beta, Tm and the first slab's groups.  The workgroups are persistent (one
-  // per CU, looping over chunks) and issue these for their next chunk during the current chunk's K phase, which
-  // reads no global memory: the loads are served while the K phase computes.  They go out in two groups (G,
-  // beta, Tm, group A after the K phase's first barrier; group B after its second): issued together, the
-  // waves stalled on the memory queue instead of computing.
+  // The reads a chunk needs first: G, beta and the first slab's groups.  The workgroups are persistent (one per
+  // CU, looping over chunks) and issue these for their next chunk during the current chunk's K phase, which reads
+  // no global memory: the loads are served while the K phase computes (group A at the K phase's start, group B
+  // after its first barrier: issued together, the waves stalled on the memory queue instead of computing).
   float pg, pb;
   auto load_first = [&](int ci, bool order, bool with_b) {
     int nv;
     const int64_t r0 = chunk_rows(ci, nv);
     pg = wsGc[(int64_t)ci * CH + (tid & (CH - 1))];
     pb = beta ? beta[r0 + (int64_t)((tid & (CH - 1)) < nv ? (tid & (CH - 1)) : 0) * H] : 1.f;
-    rtm.load(wsTm + (int64_t)ci * CH * CH, (int64_t)CH, CH, tid);
     load_a(ci, r0, nv, 0);
     if (order) {
-      // A bare barrier (no fence: nothing waits for the loads) so that every wave has issued Tm and group A
-      // before any wave issues group B, Q and K.  The memory path serves a CU's loads roughly in issue order and
-      // the older waves issue first, so without it the second wave of each SIMD gets its group A behind the
-      // first waves' B, Q and K, and the first barrier waits for nearly all of the chunk's first reads.
+      // A bare barrier (no fence: nothing waits for the loads) so that every wave has issued group A before any
+      // wave issues group B, Q and K.  The memory path serves a CU's loads roughly in issue order and the older
+      // waves issue first, so without it the second wave of each SIMD gets its group A behind the first waves'
+      // B, Q and K, and the first barrier waits for nearly all of the chunk's first reads.
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
@@ -355,15 +354,14 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     sG[tid] = pg;
     sB[tid] = tid < nvalid ? pb : 0.f;
   }
-  rtm.store(sTm, LC, tid);
 
   // ---- V phase: contractions over V, slab by slab -------------------------------------------------------
   // column tile j of this wave: n = HC*hf + j over the chunk, HK*hf + j over K, HV*hf + j over the slab
-  f32x4 aP[HC], aTV[HC], aQg[HK], aKd[HK], aWn[HK];
+  f32x4 aP[HC], aDA[HC], aQg[HK], aKd[HK], aKY[HK];
 #pragma unroll
-  for (int j = 0; j < HC; ++j) aP[j] = aTV[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < HC; ++j) aP[j] = aDA[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < HK; ++j) aQg[j] = aKd[j] = aWn[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < HK; ++j) aQg[j] = aKd[j] = aKY[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float dbV[4] = {0.f, 0.f, 0.f, 0.f};
   float sdot = 0.f;  // partial <dS_C, S0>
 
@@ -371,34 +369,32 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   // flight exactly (four slabs unrolled would spill).
 #pragma unroll(V / VS <= 2 ? V / VS : 1)
   for (int vs = 0; vs < V; vs += VS) {
-    // group A: dO R^T, dR V^T, dY = Tm^T dR (dv = beta dY, dbeta += dY . v)
+    // group A: dO R^T, dY R^T; dv = beta dY and dbeta += dY . v
     rdo.store(sdO, LS, tid);
     rv.store(sV, LS, tid);
     rr.store_t(sRt, LC, tid);
-    rdr.store_t(sdRt, LC, tid);
+    rdy.store_t(sdYt, LC, tid);
     __syncthreads();
     if (vs + VS < V) load_a(cidx, row0, nvalid, vs + VS);
 #pragma unroll
     for (int j = 0; j < HC; ++j) {
       const int n = HC * hf + j;
       mma_blk<true, false, VS>(aP[j], sdO, LS, 16 * rb, sRt, LC, 16 * n, l);
-      mma_blk<false, true, VS>(aTV[j], sdRt, LC, 16 * rb, sV, LS, 16 * n, l);
+      mma_blk<false, false, VS>(aDA[j], sdYt, LC, 16 * rb, sRt, LC, 16 * n, l);
     }
 #pragma unroll
     for (int j = 0; j < HV; ++j) {
-      const int n = HV * hf + j;
-      f32x4 dy = {0.f, 0.f, 0.f, 0.f};
-      mma_blk<false, true, CH>(dy, sTm, LC, 16 * rb, sdRt, LC, 16 * n, l);
-      float vv[4];
-      acc_vals(sV, LS, 16 * rb, 16 * n, vv, l);
+      const int vc = 16 * (HV * hf + j) + acc_col(l), r0 = 16 * rb + 4 * (l >> 4);
+      float dy[4], vv[4];
+      run4(sdYt, LC, vc, r0, dy);
+      acc_vals(sV, LS, 16 * rb, 16 * (HV * hf + j), vv, l);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * rb + acc_row(i, l), vc = 16 * n + acc_col(l);
         dbV[i] += dy[i] * vv[i];
-        sdv[r * LS + vc] = from_f<T>(sB[r] * dy[i]);
+        sdv[(r0 + i) * LS + vc] = from_f<T>(sB[r0 + i] * dy[i]);
       }
     }
-    // group B: dO S0^T, R dS_C^T, dR S0^T, <dS_C, S0> (the last from the registers: each thread holds the same
+    // group B: dO S0^T, R dS_C^T, dY S0^T, <dS_C, S0> (the last from the registers: each thread holds the same
     // elements of both tiles)
     rs0.store_t(sS0t, LK, tid);
     rdsc.store_t(sdSCt, LK, tid);
@@ -420,7 +416,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       const int n = HK * hf + j;
       mma_blk<true, false, VS>(aQg[j], sdO, LS, 16 * rb, sS0t, LK, 16 * n, l);
       mma_blk<false, false, VS>(aKd[j], sRt, LC, 16 * rb, sdSCt, LK, 16 * n, l);
-      mma_blk<false, false, VS>(aWn[j], sdRt, LC, 16 * rb, sS0t, LK, 16 * n, l);
+      mma_blk<false, false, VS>(aKY[j], sdYt, LC, 16 * rb, sS0t, LK, 16 * n, l);
     }
     __syncthreads();
   }
@@ -435,11 +431,10 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   // 0.3% of the traffic): after a conditional block the compiler could not count the loads in flight and would
   // wait for all of them at the first reuse of a register of the chunk's earlier reads.
   const int cnext = ci + (int)gridDim.x < nchunk ? ci + (int)gridDim.x : ci;
-  T* sdWn = slab;                 // CH x LK   dR S0^T (= -dW)
-  T* sdTm = sdWn + CH * LK;       // CH x LC
-  T* sM1 = sdTm + CH * LC;        // CH x LC   dTm Tm^T
-  T* sD = sM1 + CH * LC;          // CH x LC   D = dA o beta_i E
-  T* sdPm = sD + CH * LC;         // CH x LC   dP o s E
+  T* sdq = slab;             // CH x LK   dq staging
+  T* sdk = sdq + CH * LK;    // CH x LK   dk staging
+  T* sD = sdk + CH * LK;     // CH x LC   D = dA o beta_i E
+  T* sdPm = sD + CH * LC;    // CH x LC   dP o s E
 
   const int lg = l >> 4;  // lane group: rows 4*lg .. 4*lg+3 of each tile
   float gam[4], dte[4], bet[4], Grow[4];
@@ -452,71 +447,29 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     dte[i] = __expf(GC - Grow[i]);
     bet[i] = sB[r];
   }
-  // row dots from the V-phase accumulators (this half's columns)
-  float rq[4] = {0.f, 0.f, 0.f, 0.f}, rk[4] = {0.f, 0.f, 0.f, 0.f};
+  // row dots from the V-phase accumulators (this half's columns); dX = -dY S0^T, so rx = dX . k = -aKY . k
+  float rq[4] = {0.f, 0.f, 0.f, 0.f}, rk[4] = {0.f, 0.f, 0.f, 0.f}, rx[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < HK; ++j) {
-    float qv[4], uv[4];
+    float qv[4], uv[4], kv[4];
     acc_vals(sQ, LK, 16 * rb, 16 * (HK * hf + j), qv, l);
     acc_vals(sU, LK, 16 * rb, 16 * (HK * hf + j), uv, l);
+    if constexpr (SEPU) acc_vals(sK, LK, 16 * rb, 16 * (HK * hf + j), kv, l);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * rb + acc_row(i, l), d = 16 * (HK * hf + j) + acc_col(l);
       rq[i] += aQg[j][i] * qv[i];
       rk[i] += aKd[j][i] * uv[i];
-      sdWn[r * LK + d] = from_f<T>(aWn[j][i]);
+      rx[i] -= aKY[j][i] * (SEPU ? kv[i] : uv[i]);
     }
   }
-  __syncthreads();
   load_first(cnext, false, false);
 
-  // dX = Tm^T dW = -Tm^T dWn (rows of this wave), and rx = dX . k
-  f32x4 aX[HK];
-  float rx[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < HK; ++j) {
-    const int n = HK * hf + j;
-    f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<false, false, CH>(t, sTm, LC, 16 * rb, sdWn, LK, 16 * n, l);
-    aX[j] = -t;
-    float kv[4];
-    acc_vals(sK, LK, 16 * rb, 16 * n, kv, l);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) rx[i] += aX[j][i] * kv[i];
-  }
-  // dTm rows:  dTm_ij = -beta_j gamma_j (dWn K^T)_ij + beta_j (dR V^T)_ij
-#pragma unroll
-  for (int j = 0; j < HC; ++j) {
-    const int n = HC * hf + j;
-    f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<true, true, K>(t, sdWn, LK, 16 * rb, sK, LK, 16 * n, l);
-    const int cc = 16 * n + acc_col(l);
-    const float bj = sB[cc], gj = __expf(sG[cc]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 16 * rb + acc_row(i, l);
-      sdTm[r * LC + cc] = from_f<T>(-bj * gj * t[i] + bj * aTV[j][i]);
-    }
-  }
-  __syncthreads();
-  load_b(cnext, 0);
-  // M1 = dTm Tm^T (rows of this wave)
-#pragma unroll
-  for (int j = 0; j < HC; ++j) {
-    const int n = HC * hf + j;
-    f32x4 t = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<true, true, CH>(t, sdTm, LC, 16 * rb, sTm, LC, 16 * n, l);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sM1[(16 * rb + acc_row(i, l)) * LC + 16 * n + acc_col(l)] = from_f<T>(t[i]);
-  }
-  __syncthreads();
-  // dA = -Tm^T M1, strict lower; with KK and QK recomputed: D, dPm, dbeta_A and the dG row/col sums
+  // dA = -dY R^T, strict lower; with KK and QK recomputed: D, dPm, dbeta_A and the dG row/col sums
   float rz[4] = {0.f, 0.f, 0.f, 0.f}, dbA[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < HC; ++j) {
     const int n = HC * hf + j;
-    f32x4 da = {0.f, 0.f, 0.f, 0.f}, kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
-    mma_blk<false, false, CH>(da, sTm, LC, 16 * rb, sM1, LC, 16 * n, l);
+    f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
     mma_blk<true, true, K>(kk, sK, LK, 16 * rb, sU, LK, 16 * n, l);
     mma_blk<true, true, K>(qk, sQ, LK, 16 * rb, sU, LK, 16 * n, l);
     f32x4 z;
@@ -529,12 +482,12 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       // masked by a select: no branch around the exp.  With u = dA e (strictly below) and w = dP s e:
       //   D = u beta_r,  dPm = w,  dbeta_A += u (K U^T),  z = dP P + dA A = w (Q U^T) + D (K U^T)
       const float e = r >= cc ? __expf(fminf(Grow[i] - Gc, 0.f)) : 0.f;
-      const float u = r > cc ? -da[i] * e : 0.f;
+      const float uu = r > cc ? -aDA[j][i] * e : 0.f;
       const float wv = aP[j][i] * (scale * e);
-      const float Dv = u * bet[i];
+      const float Dv = uu * bet[i];
       sD[r * LC + cc] = from_f<T>(Dv);
       sdPm[r * LC + cc] = from_f<T>(wv);
-      dbA[i] += u * kk[i];
+      dbA[i] += uu * kk[i];
       z[i] = wv * qk[i] + Dv * kk[i];
       rz[i] += z[i];
     }
@@ -570,10 +523,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     if ((p & 1) == 0) sRow[hf][f1 >> 2][16 * rb + 4 * lg + (f1 & 3)] = z1;
   }
   __syncthreads();
-  // dq and dk are staged (bf16, stride LK) in the regions of dWn and dTm/M1, free from here on
-  T* sdq = sdWn;
-  T* sdk = sdTm;
-  static_assert(CH * LK <= 2 * CH * LC, "dk staging must fit in the dTm and M1 regions");
+  load_b(cnext, 0);
   // dq = s gamma dQg + dPm U.  (Here and below every tile of a product is computed before any is stored: with no
   // LDS store in between, the row block's A fragments are read once for all column tiles.)
   {
@@ -592,7 +542,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       }
   }
   if constexpr (!SEPU) {
-    // dk = dte dKd + dPm^T Q + beta gamma dX + D K + D^T K
+    // dk = dte dKd + dPm^T Q + D K + D^T K - beta gamma dKY
     f32x4 t[HK];
 #pragma unroll
     for (int j = 0; j < HK; ++j) {
@@ -607,10 +557,10 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 16 * rb + acc_row(i, l), d = 16 * (HK * hf + j) + acc_col(l);
-        sdk[r * LK + d] = from_f<T>(dte[i] * aKd[j][i] + t[j][i] + bet[i] * gam[i] * aX[j][i]);
+        sdk[r * LK + d] = from_f<T>(dte[i] * aKd[j][i] + t[j][i] - bet[i] * gam[i] * aKY[j][i]);
       }
   } else {
-    // read side: dk = beta gamma dX + D U;  write side (kept in aKd until its staging area is free):
+    // read side: dk = D U - beta gamma dKY;  write side (kept in aKd until its staging area is free):
     // du = dte dKd + dPm^T Q + D^T K
     f32x4 t[HK];
 #pragma unroll
@@ -629,7 +579,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 16 * rb + acc_row(i, l), d = 16 * (HK * hf + j) + acc_col(l);
-        sdk[r * LK + d] = from_f<T>(t[j][i] + bet[i] * gam[i] * aX[j][i]);
+        sdk[r * LK + d] = from_f<T>(t[j][i] - bet[i] * gam[i] * aKY[j][i]);
       }
   }
   // dbeta and the per-row part of dG (first half, one lane per row)
@@ -688,7 +638,7 @@ static hipError_t bwd_state_k(const ChunkArgs& a) {
   bwd_state_kernel<T, K, BV, SEPU><<<grid, STH, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
       static_cast<const T*>(a.dout), a.beta, static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P),
-      a.ws.Gc, a.dhT, a.dh0, static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dRs), a.T, a.H, a.V, a.NT,
+      a.ws.Gc, a.dhT, a.dh0, static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dYs), a.T, a.H, a.V, a.NT,
       a.scale);
   return hipGetLastError();
 }
@@ -701,9 +651,9 @@ static hipError_t bwd_intra_kv(const ChunkArgs& a) {
   dim3 grid(std::min(nchunk, device_cu_count()));
   bwd_intra_kernel<T, K, V, VS, SEPU><<<grid, ITH, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
-      static_cast<const T*>(a.v), a.beta, static_cast<const T*>(a.dout), static_cast<const T*>(a.ws.Tm),
+      static_cast<const T*>(a.v), a.beta, static_cast<const T*>(a.dout),
       a.ws.Gc, static_cast<const T*>(a.ws.hs), static_cast<const T*>(a.ws.Rs), static_cast<const T*>(a.ws.dhs),
-      static_cast<const T*>(a.ws.dRs), static_cast<T*>(a.dq), static_cast<T*>(a.dk), static_cast<T*>(a.du),
+      static_cast<const T*>(a.ws.dYs), static_cast<T*>(a.dq), static_cast<T*>(a.dk), static_cast<T*>(a.du),
       static_cast<T*>(a.dv), a.dg, a.dbeta, a.T, a.H, a.NT, a.B * a.H, a.scale);
   return hipGetLastError();
 }

@@ -322,6 +322,22 @@ __device__ __forceinline__ void acc_vals(const T* p, int ld, int r0, int c0, flo
   }
 }
 
+// Four consecutive elements p[c * ld + r0 .. r0 + 3] of a tile stored with r contiguous (one 8-byte read in bf16,
+// 16 bytes in fp32; r0 a multiple of 4 and c * ld * sizeof(T) a multiple of 8 or 16): the accumulator positions
+// of this lane in a column-major tile.
+template <typename T>
+__device__ __forceinline__ void run4(const T* p, int ld, int c, int r0, float (&v)[4]) {
+  if constexpr (sizeof(T) == 2) {
+    const bf16x4 t = *reinterpret_cast<const bf16x4*>(p + c * ld + r0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = to_f(t[i]);
+  } else {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(p + c * ld + r0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = t[i];
+  }
+}
+
 // ---- chunk factors, in three barrier-separated phases ------------------------------------------------------
 // Each phase is a separate function; the caller places the barriers between them.
 //

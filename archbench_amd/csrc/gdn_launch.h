@@ -24,8 +24,8 @@ struct StepArgs {
 
 // Chunk workspace carve-up (chunk-major: [B*H][NT][...]).  All offsets are 256-byte aligned.
 // Parts: WS_FACT = {Tm, P, Gc} (the chunk factors kernel), WS_STATE = {hs, Rs} (the stashing forward or the
-// recompute sweep), WS_GRAD = {dhs, dRs} (the reverse sweep); the gradient kernel reads all but P.
-// hs, Rs, dhs and dRs use the fragment layout of the sweeps' accumulators (store_fragblk).
+// recompute sweep), WS_GRAD = {dhs, dYs} (the reverse sweep); the gradient kernel reads Gc, hs, Rs, dhs, dYs.
+// hs, Rs, dhs and dYs use the fragment layout of the sweeps' accumulators (store_fragblk).
 struct ChunkWs {
   void* Tm;   // [BH][NT][64][64]   (I + A)^-1 per chunk, input dtype
   void* P;    // [BH][NT][64][64]   s (Q K^T) o exp(G_i - G_j), lower triangle incl. diagonal, input dtype
@@ -33,7 +33,7 @@ struct ChunkWs {
   void* hs;   // [BH][NT][K][V]     state entering each chunk
   void* Rs;   // [BH][NT][64][V]    R = U - W S per chunk
   void* dhs;  // [BH][NT][K][V]     dL/d(state leaving each chunk)
-  void* dRs;  // [BH][NT][64][V]    dL/dR per chunk
+  void* dYs;  // [BH][NT][64][V]    dY = Tm^T dL/dR per chunk (the gradient w.r.t. Y, R = Tm Y)
 };
 
 // Separate read and write keys: with u non-null the write (state update, the column side of K K^T and Q K^T, the
@@ -160,7 +160,7 @@ hipError_t launch_factors(const ChunkArgs& a);                  // Tm, P, Gc
 // FWD_OUT: o, hT.  FWD_RECOMPUTE: hs, Rs, Tm, Gc.  FWD_STASH: both.
 enum FwdMode { FWD_OUT = 0, FWD_RECOMPUTE = 1, FWD_STASH = 2 };
 hipError_t launch_fwd(const ChunkArgs& a, FwdMode mode);
-hipError_t launch_bwd_state(const ChunkArgs& a);                 // dhs, dRs, dh0
+hipError_t launch_bwd_state(const ChunkArgs& a);                 // dhs, dYs, dh0
 hipError_t launch_bwd_intra(const ChunkArgs& a);                 // dq, dk, dv, dg, dbeta
 
 }  // namespace gdn

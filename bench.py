@@ -58,7 +58,7 @@ def stage_flops(stage: str, K: int, V: int) -> int:
         "fwd_stash": 6 * C * K + 4 * C * V + 6 * K * V,      # the forward's products (states also written)
         "bwd_recompute": 4 * C * K + 2 * C * V + 4 * K * V,  # KK^T, W; U; WS, K^T R
         "bwd_state": 6 * C * K + 2 * C * V + 6 * K * V,      # KK^T, QK^T, W; P^T dO; K dS, Qg^T dO, W^T dR
-        "bwd_intra": 6 * C * V + 6 * K * V + 16 * C * K + 4 * C * C,
+        "bwd_intra": 4 * C * V + 6 * K * V + 12 * C * K,     # dO R^T, dY R^T; dO S0^T, R dSC^T, dY S0^T; KK^T, QK^T, dq, dk
     }.get(stage, 0)
 
 
@@ -71,8 +71,8 @@ def stage_bytes(stage: str, K: int, V: int, es: int = 2) -> int:
         "fwd": 2 * qk + vv + 8 + vv,                           # q k v g beta -> o
         "fwd_stash": 2 * qk + vv + 8 + vv + st + r + tm + 4,   # ... -> o, states, R, Tm, G
         "bwd_recompute": qk + vv + 8 + st + r + tm + 4,        # k v g beta -> states, R, Tm, G
-        "bwd_state": 2 * qk + vv + 8 + st + r,                 # q k dO g beta -> dstates, dR
-        "bwd_intra": 2 * qk + 2 * vv + tm + 8 + 2 * st + 2 * r + 2 * qk + vv + 8,
+        "bwd_state": 2 * qk + vv + 8 + st + r,                 # q k dO g beta -> dstates, dY
+        "bwd_intra": 2 * qk + 2 * vv + 8 + 2 * st + 2 * r + 2 * qk + vv + 8,  # ... G, S0, dSC, R, dY -> dq dk dv dg db
     }.get(stage, 0)
 
 
