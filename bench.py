@@ -8,13 +8,25 @@ backward call (gdn_chunk_bwd_stashed: every gradient, dq, dk, dv, dg, dbeta).  t
 The recompute path (gdn_chunk_fwd + gdn_chunk_bwd, no stash) is timed beside it as recompute_ms_per_step.
 
 Also reported in the same line:
-  roofline      the dominant kernel of the step against the roofline that bounds it: its algorithmic intensity
-                (stage_flops / stage_bytes) decides between HBM (below the ridge, 2.5 PFLOP/s / 8 TB/s) and
-                MFMA; achieved = algorithmic bytes (or FLOPs) per launch over the launch's average duration
-                (HIP events on the launch stream); traffic = measured HBM bytes per launch;
+  roofline      the training step (its four kernels: chunk factors, forward sweep, reverse sweep, gradient kernel)
+                on the workload's own algorithmic basis: 3 * F_fwd FLOPs and 2,840 bytes per token-head (q, k, v, g,
+                beta read and o written by the forward; q, k, v, dO, g, beta read and dq, dk, dv, dg, dbeta written by
+                the backward, at K = V = 128 bf16).  Its intensity (190 FLOP/B) is below the ridge (2.5 PFLOP/s /
+                8 TB/s = 312), so HBM bounds it: achieved = algorithmic bytes / step time (HIP events on the launch
+                stream over the timed loop), against 8 TB/s; mfma_frac and the MFMA ceiling that bound allows
+                (190 FLOP/B x 8 TB/s / 2.5 PFLOP/s) are given beside it.  traffic = the HBM bytes the step's kernels
+                actually move (rocprofv3 FETCH_SIZE / WRITE_SIZE per kernel, profiles/hbm_traffic.json), and
+                traffic_ratio = traffic / algorithmic bytes (the bytes the design moves beyond the minimum);
+  kernels       each kernel of the step: time per launch (HIP events around each launch, a separate loop),
+                its design bytes (every input and workspace buffer read once, every output written once) and
+                design FLOPs (the dense MFMA products it performs), measured traffic, and, where the profile holds
+                them, rocprofv3's MfmaUtil (MFMA busy cycles / (active cycles x SIMDs)) and executed bf16 MFMA FLOPs;
   mfma_frac     the whole step at the workload's algorithmic count 3 * F_fwd per token-head,
                 F_fwd = 2C(3K + 2V) + 6KV (C = 64);
   fwd_only      forward alone at B=8, T=2048, H=8, K=V=128 (% of the bf16 MFMA peak);
+  long_context  forward + backward at B=1, T=16384, H=16, K=128, V=256, nonzero initial state, slow decay
+                (g = logsigmoid(N(0,1) + 6)), the training pair with dh0; tokens/s and % of the bf16 MFMA peak at
+                3 * F_fwd(128, 256) per token-head;
   decode_step   one recurrent decode step at B=256, H=16, K=V=128 with the fp32 state updated in place
                 (HBM GB/s against 8 TB/s);
   short_conv    the causal depthwise conv (kernel 4) + SiLU in front of the op at the layer's shape, B=8, T=4096,
@@ -51,40 +63,65 @@ def f_fwd(K: int, V: int) -> int:
 
 
 def stage_flops(stage: str, K: int, V: int) -> int:
-    """Algorithmic dense MFMA FLOPs per token-head of each kernel stage (C = 64 tokens per chunk).  Work a
-    stage repeats for every 64-wide V block (the chunk factors) is counted once."""
+    """Dense MFMA FLOPs per token-head that each kernel performs (C = 64 tokens per chunk; the 64 x 64 inverse
+    of the chunk factors is not counted).  A product an (M x N) = (M x L)(L x N) counts 2 M N L, divided by the
+    C tokens of its chunk."""
     return {
-        "fwd": 6 * C * K + 4 * C * V + 6 * K * V,            # KK^T, QK^T, W; U, PR; WS, QS, K^T R
-        "fwd_stash": 6 * C * K + 4 * C * V + 6 * K * V,      # the forward's products (states also written)
-        "bwd_recompute": 4 * C * K + 2 * C * V + 4 * K * V,  # KK^T, W; U; WS, K^T R
-        "bwd_state": 6 * C * K + 2 * C * V + 6 * K * V,      # KK^T, QK^T, W; P^T dO; K dS, Qg^T dO, W^T dR
-        "bwd_intra": 4 * C * V + 6 * K * V + 12 * C * K,     # dO R^T, dY R^T; dO S0^T, R dSC^T, dY S0^T; KK^T, QK^T, dq, dk
+        "factors": 4 * C * K,                                # K K^T, Q K^T
+        "fwd": 6 * K * V + 4 * C * V,                        # K S, Q S, K^T R; Tm Y, P R
+        "fwd_stash": 6 * K * V + 4 * C * V,                  # the same, states and R also written
+        "bwd_recompute": 4 * K * V + 2 * C * V,              # K S, K^T R; Tm Y
+        "bwd_state": 6 * K * V + 4 * C * V,                  # K dS, Q^T dO, K^T Z; P^T dO, Tm^T dR
+        "bwd_intra": 6 * K * V + 4 * C * V + 12 * C * K,     # dO S0^T, R dSC^T, dY S0^T; dO R^T, dY R^T;
+                                                             # K K^T, Q K^T, dPm K, dPm^T Q, D K, D^T K
     }.get(stage, 0)
 
 
 def stage_bytes(stage: str, K: int, V: int, es: int = 2) -> int:
-    """Algorithmic HBM bytes per token-head of each kernel stage: every input read once and every output
-    written once (q, k: es*K; v, o, dO: es*V; g, beta, G: 4; per-chunk workspace: state es*K*V/C, R es*V,
-    Tm es*C).  Intermediates the design keeps on-chip count nothing."""
-    qk, vv, st, r, tm = es * K, es * V, es * K * V // C, es * V, es * C
+    """Design HBM bytes per token-head of each kernel: every input and workspace buffer read once, every output
+    written once (q, k: es*K; v, o, dO, dv, R, dY: es*V; g, beta, G, dg, dbeta: 4; Tm, P: es*C per token; a
+    chunk's state or state gradient: es*K*V/C per token).  The second V-block workgroup's reads of q, k, Tm
+    and P in the sweeps, which hit L2, count once."""
+    qk, vv, st, tm = es * K, es * V, es * K * V // C, es * C
     return {
-        "fwd": 2 * qk + vv + 8 + vv,                           # q k v g beta -> o
-        "fwd_stash": 2 * qk + vv + 8 + vv + st + r + tm + 4,   # ... -> o, states, R, Tm, G
-        "bwd_recompute": qk + vv + 8 + st + r + tm + 4,        # k v g beta -> states, R, Tm, G
-        "bwd_state": 2 * qk + vv + 8 + st + r,                 # q k dO g beta -> dstates, dY
-        "bwd_intra": 2 * qk + 2 * vv + 8 + 2 * st + 2 * r + 2 * qk + vv + 8,  # ... G, S0, dSC, R, dY -> dq dk dv dg db
+        "factors": 2 * qk + 8 + 2 * tm + 4,                  # q k g beta -> Tm P G
+        "fwd": 2 * qk + vv + 8 + 2 * tm + vv,                # q k v beta G Tm P -> o
+        "fwd_stash": 2 * qk + vv + 8 + 2 * tm + vv + st + vv,  # ... -> o, states, R
+        "bwd_recompute": qk + vv + 8 + tm + st + vv,         # k v beta G Tm -> states, R
+        "bwd_state": 2 * qk + vv + 8 + 2 * tm + st + vv,     # q k dO beta G Tm P -> dstates, dY
+        "bwd_intra": 2 * qk + 2 * vv + 8 + 2 * st + 2 * vv + 2 * qk + vv + 8,  # q k v dO beta G S0 dSC R dY ->
+                                                                             # dq dk dv dg dbeta
     }.get(stage, 0)
+
+
+def algo_bytes_step(K: int, V: int, es: int = 2) -> int:
+    """Minimum HBM bytes per token-head of one training step (forward + backward) at the op boundary: the
+    forward reads q, k, v, g, beta and writes o; the backward reads q, k, v, dO, g, beta and writes dq, dk, dv,
+    dg, dbeta (2,840 bytes at K = V = 128 bf16)."""
+    fwd = es * (2 * K + V) + 8 + es * V
+    bwd = es * (2 * K + 2 * V) + 8 + es * (2 * K + V) + 8
+    return fwd + bwd
+
+
+def _profile_json(name: str) -> dict:
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
 
 
 def measured_traffic() -> dict:
     """HBM bytes per launch by stage, from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in
     profiles/hbm_traffic.json (calibrated on a copy of known size); empty if that file is absent."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
-    try:
-        with open(path) as f:
-            return json.load(f).get("per_launch", {})
-    except (OSError, ValueError):
-        return {}
+    return _profile_json("hbm_traffic.json").get("per_launch", {})
+
+
+def measured_mfma() -> dict:
+    """MfmaUtil and executed bf16 MFMA FLOPs per launch by stage, from the rocprofv3 counter run summarised in
+    profiles/mfma_counters.json; empty if that file is absent."""
+    return _profile_json("mfma_counters.json").get("per_launch", {})
 
 
 def cpu_model() -> str:
@@ -97,15 +134,22 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def timed_loop(fn, steps: int, warmup: int, torch) -> float:
+def timed_loop(fn, steps: int, warmup: int, torch, events: bool = False):
+    """Seconds per call of fn over `steps` calls after `warmup` untimed ones, by the host clock between two
+    synchronisations; with events, also the GPU time between HIP events recorded on the current stream (the
+    stream the library launches on) around the same calls: (host_s, event_s)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    e0.record()
     for _ in range(steps):
         fn()
+    e1.record()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / steps
+    host = (time.perf_counter() - t0) / steps
+    return (host, e0.elapsed_time(e1) * 1e-3 / steps) if events else host
 
 
 def log(msg: str) -> None:
@@ -142,9 +186,18 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-sample-T", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "train", "fwd", "decode", "conv", "norm", "ce"], default="all",
-                    help="run one workload only (profiling runs); the JSON line needs 'all' or 'train'")
+    ap.add_argument("--only", default="all",
+                    help="comma-separated workloads to run (all, train, fwd, long, decode, conv, norm, ce), for "
+                         "profiling runs; the JSON line needs 'all' or 'train'")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="end with two device copies of 256 MiB (the known-size dispatch that calibrates rocprofv3's "
+                         "FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
+    only = set(args.only.split(","))
+    known = {"all", "train", "fwd", "long", "decode", "conv", "norm", "ce"}
+    if not only <= known:
+        ap.error(f"--only: unknown workload(s) {sorted(only - known)}; choose from {sorted(known)}")
+    want = lambda w: "all" in only or w in only
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures a single GPU: the gated DeltaNet op shards over batch and heads with no "
               "communication, and this build has no multi-GPU path. Run with --gpus 1.", file=sys.stderr)
@@ -160,7 +213,7 @@ def main() -> int:
     torch.cuda.set_device(dev)
     out: dict = {}
 
-    if args.only in ("all", "train"):
+    if want("train"):
         B, T, H, K, V = 8, 4096, 16, 128, 128
         log(f"headline fwd+bwd B={B} T={T} H={H} K={K} V={V} bf16: generating inputs")
         x = make_inputs(B, T, H, K, V, seed=0, with_do=True).to(dev, torch.bfloat16)
@@ -174,30 +227,45 @@ def main() -> int:
             ops.chunk_bwd(x.q, x.k, x.v, x.g, x.beta, None, x.do, None, 1.0)
 
         log(f"timing {args.steps} steps after {args.warmup} warmup")
-        sec = timed_loop(step, args.steps, args.warmup, torch)
+        sec, sec_ev = timed_loop(step, args.steps, args.warmup, torch, events=True)
         sec_rc = timed_loop(step_recompute, max(3, args.steps // 2), 1, torch)
         tokens = B * T
         with _lib.StageTimer() as st:
             for _ in range(max(3, min(args.steps, 10))):
                 step()
         stages = {k: (ms / n, n) for k, (ms, n) in st.result.items()}
-        dom = max(stages, key=lambda s: stages[s][0])
-        dom_ms = stages[dom][0]
-        dom_flops = stage_flops(dom, K, V) * B * T * H
-        dom_bytes = stage_bytes(dom, K, V) * B * T * H
-        hbm_bound = dom_flops / dom_bytes < MFMA_BF16_PEAK / HBM_PEAK
-        if hbm_bound:
-            roof = {"kernel": dom, "bound": "hbm", "achieved": round(dom_bytes / (dom_ms * 1e-3) / 1e9, 1),
-                    "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(dom_bytes / (dom_ms * 1e-3) / HBM_PEAK, 4)}
-        else:
-            roof = {"kernel": dom, "bound": "mfma", "achieved": round(dom_flops / (dom_ms * 1e-3) / 1e12, 2),
-                    "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
-                    "frac": round(dom_flops / (dom_ms * 1e-3) / MFMA_BF16_PEAK, 4)}
-        roof.update({"traffic": measured_traffic().get(dom, {}).get("bytes"), "algorithmic_bytes": dom_bytes,
-                     "flops_per_launch": dom_flops,
-                     "mfma_frac": round(dom_flops / (dom_ms * 1e-3) / MFMA_BF16_PEAK, 4),
-                     "avg_ms": round(dom_ms, 4)})
         call_flops = 3 * f_fwd(K, V) * B * T * H
+        algo_bytes = algo_bytes_step(K, V) * B * T * H
+        traffic_by_stage, mfma_by_stage = measured_traffic(), measured_mfma()
+        step_stages = ("factors", "fwd_stash", "bwd_state", "bwd_intra")
+        traffic = (sum(traffic_by_stage[k]["bytes"] for k in step_stages)
+                   if all(k in traffic_by_stage for k in step_stages) else None)
+        roof = {"kernel": "training step: chunk_factors + fwd_sweep<stash> + bwd_state + bwd_intra",
+                "bound": "hbm", "achieved": round(algo_bytes / sec_ev / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                "unit": "GB/s", "frac": round(algo_bytes / sec_ev / HBM_PEAK, 4), "traffic": traffic,
+                "algorithmic_bytes": algo_bytes,
+                "traffic_ratio": None if traffic is None else round(traffic / algo_bytes, 3),
+                "flops": call_flops, "intensity_flop_per_byte": round(call_flops / algo_bytes, 1),
+                "step_ms_events": round(sec_ev * 1e3, 4),
+                "mfma_frac": round(call_flops / sec_ev / MFMA_BF16_PEAK, 4),
+                "mfma_ceiling_frac": round(call_flops / algo_bytes * HBM_PEAK / MFMA_BF16_PEAK, 4)}
+        kernels = {}
+        for k in step_stages:
+            if k not in stages:
+                continue
+            ms = stages[k][0]
+            fl, by = stage_flops(k, K, V) * B * T * H, stage_bytes(k, K, V) * B * T * H
+            ent = {"ms": round(ms, 4), "design_flops": fl, "design_bytes": by,
+                   "design_GB_per_s": round(by / (ms * 1e-3) / 1e9, 1),
+                   "mfma_frac": round(fl / (ms * 1e-3) / MFMA_BF16_PEAK, 4)}
+            if k in traffic_by_stage:
+                tb = traffic_by_stage[k]["bytes"]
+                ent.update({"traffic": tb, "traffic_GB_per_s": round(tb / (ms * 1e-3) / 1e9, 1),
+                            "hbm_frac": round(tb / (ms * 1e-3) / HBM_PEAK, 4)})
+            if k in mfma_by_stage:
+                ent.update({kk: mfma_by_stage[k][kk] for kk in ("mfma_util", "executed_bf16_flops")
+                            if kk in mfma_by_stage[k]})
+            kernels[k] = ent
         out.update({
             "metric": METRIC, "value": round(tokens / sec, 1), "unit": "tokens/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4),
@@ -207,6 +275,7 @@ def main() -> int:
                        "scale": 1.0, "state": "fp32", "g_shift": 4.0},
             "mfma_frac": round(call_flops / sec / MFMA_BF16_PEAK, 4),
             "roofline": roof,
+            "kernels": kernels,
             "stages_ms": {k: round(v[0], 4) for k, v in stages.items()},
             "recompute_ms_per_step": round(sec_rc * 1e3, 4),
         })
@@ -215,7 +284,7 @@ def main() -> int:
         del x
         torch.cuda.empty_cache()
 
-    if args.only in ("all", "fwd"):
+    if want("fwd"):
         B, T, H, K, V = 8, 2048, 8, 128, 128
         log(f"forward only B={B} T={T} H={H} K={K} V={V} bf16")
         x = make_inputs(B, T, H, K, V, seed=0).to(dev, torch.bfloat16)
@@ -228,7 +297,34 @@ def main() -> int:
         del x
         torch.cuda.empty_cache()
 
-    if args.only in ("all", "decode"):
+    if want("long"):
+        B, T, H, K, V = 1, 16384, 16, 128, 256
+        log(f"long context fwd+bwd B={B} T={T} H={H} K={K} V={V} bf16, h0 ~ N(0, 0.1^2), g_shift 6")
+        x = make_inputs(B, T, H, K, V, seed=0, g_shift=6.0, h0_std=0.1, with_do=True).to(dev, torch.bfloat16)
+        dhT = torch.zeros(B, H, K, V, device=dev)
+
+        def long_step():
+            _, _, stash = ops.chunk_fwd_stash(x.q, x.k, x.v, x.g, x.beta, x.h0, 1.0)
+            ops.chunk_bwd_stashed(x.q, x.k, x.v, x.g, x.beta, x.h0, x.do, dhT, stash, 1.0)
+
+        n = max(5, min(args.steps, 20))
+        sec, sec_ev = timed_loop(long_step, n, 2, torch, events=True)
+        with _lib.StageTimer() as st:
+            for _ in range(3):
+                long_step()
+        fl = 3 * f_fwd(K, V) * B * T * H
+        out["long_context"] = {"workload": "gdn_chunk_fwd_bwd", "B": B, "T": T, "H": H, "K": K, "V": V,
+                               "h0": "N(0, 0.1^2)", "g_shift": 6.0, "steps": n, "ms_per_step": round(sec * 1e3, 4),
+                               "tokens_per_s": round(B * T / sec, 1),
+                               "mfma_frac": round(fl / sec_ev / MFMA_BF16_PEAK, 4),
+                               "stages_ms": {k: round(v[0] / v[1], 4) for k, v in st.result.items()}}
+        log(f"long context {sec * 1e3:.3f} ms/step, {B * T / sec:.3e} tokens/s, "
+            f"{out['long_context']['mfma_frac'] * 100:.1f}% of bf16 MFMA peak; "
+            f"stages {out['long_context']['stages_ms']}")
+        del x
+        torch.cuda.empty_cache()
+
+    if want("decode"):
         B, H, K, V = 256, 16, 128, 128
         log(f"decode step B={B} H={H} K={K} V={V} (fp32 state in place)")
         q, k, v, g, b, S = make_step_inputs(B, H, K, V)
@@ -249,7 +345,7 @@ def main() -> int:
                               "tokens_per_s": round(B / sec, 1)}
         log(f"decode kernel {kern_ms * 1e3:.2f} us, {out['decode_step']['GB_per_s']} GB/s")
 
-    if args.only in ("all", "conv"):
+    if want("conv"):
         B, T, D = 8, 4096, 2048
         log(f"short conv B={B} T={T} D={D} kernel 4 bf16")
         gen = torch.Generator(device=dev).manual_seed(0)
@@ -279,7 +375,7 @@ def main() -> int:
         del xc, dyc
         torch.cuda.empty_cache()
 
-    if args.only in ("all", "norm"):
+    if want("norm"):
         rows, dim, ntok, H = 8 * 4096 * 16, 128, 8 * 4096, 16
         log(f"gated RMSNorm rows={rows} dim={dim} and gates ntok={ntok} H={H}, bf16")
         gen = torch.Generator(device=dev).manual_seed(1)
@@ -315,7 +411,7 @@ def main() -> int:
         del xn, gn, dyn
         torch.cuda.empty_cache()
 
-    if args.only in ("all", "ce"):
+    if want("ce"):
         from archbench_amd import fused_ce
 
         N, Hd, Vv, nch = 8 * 4096, 1024, 50304, 1
@@ -347,7 +443,15 @@ def main() -> int:
         del xc, wc
         torch.cuda.empty_cache()
 
-    if args.only in ("all", "train") and not args.no_cpu_baseline:
+    if args.calibration_copy:
+        a = torch.ones(256 * 2 ** 20, dtype=torch.uint8, device=dev)
+        c = torch.empty_like(a)
+        for _ in range(2):
+            c.copy_(a)
+        torch.cuda.synchronize()
+        del a, c
+
+    if want("train") and not args.no_cpu_baseline:
         log(f"cpu baseline (oracle, T={args.cpu_sample_T})")
         out["cpu_baseline"] = cpu_baseline(args.cpu_sample_T)
         log(f"cpu {out['cpu_baseline']['value']} tokens/s")
