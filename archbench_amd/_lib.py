@@ -57,7 +57,7 @@ SIGNATURES = {
     "gdn_profile_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
     "gdn_profile_stage_name": (ctypes.c_char_p, [_i]),
 }
-PROFILE_STAGES = 16
+PROFILE_STAGES = 19
 
 _lock = threading.Lock()
 _lib = None

@@ -31,7 +31,8 @@ static bool misaligned(const P*... p) {
   return ((reinterpret_cast<uintptr_t>(p) & 15) | ...) != 0;
 }
 
-size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, ChunkWs* carve, void* base) {
+size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, ChunkWs* carve, void* base,
+                      int ns) {
   const size_t es = dtype == DT_BF16 ? 2 : 4;
   const size_t NT = (size_t)(T + CH_TOKENS - 1) / CH_TOKENS;
   const size_t BH = (size_t)B * H;
@@ -56,6 +57,16 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
     ws.dhs = take(BH * NT * (size_t)K * V * es);
     ws.dYs = take(BH * NT * CH_TOKENS * (size_t)V * es);
   }
+  const size_t seg_states = ns > 1 ? BH * (size_t)ns * K * V * 4 : 0;  // one fp32 state per segment and head
+  if ((parts & WS_SEGF) && ns > 1) {
+    ws.phi = static_cast<float*>(take(BH * (size_t)ns * K * K * 4));
+    ws.sloc = static_cast<float*>(take(seg_states));
+    ws.sin = static_cast<float*>(take(seg_states));
+  }
+  if ((parts & WS_SEGB) && ns > 1) {
+    ws.dsloc = static_cast<float*>(take(seg_states));
+    ws.dsend = static_cast<float*>(take(seg_states));
+  }
   if (carve) {
     if (parts & WS_FACT) {
       carve->Tm = ws.Tm; carve->P = ws.P; carve->Gc = ws.Gc;
@@ -66,8 +77,28 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
     if (parts & WS_GRAD) {
       carve->dhs = ws.dhs; carve->dYs = ws.dYs;
     }
+    if (parts & WS_SEGF) {
+      carve->phi = ws.phi; carve->sloc = ws.sloc; carve->sin = ws.sin;
+    }
+    if (parts & WS_SEGB) {
+      carve->dsloc = ws.dsloc; carve->dsend = ws.dsend;
+    }
   }
   return off;
+}
+
+int segment_count(int B, int T, int H, int K, int V) {
+  (void)K;
+  if (T <= 0 || T % CH_TOKENS) return 1;
+  const int NT = T / CH_TOKENS;
+  const int64_t blocks = (int64_t)(V / 64) * B * H;  // sweep workgroups of the unsegmented problem
+  const int cus = device_cu_count();
+  int ns = 1;
+  // double the segments while the sweeps still fit on the device and each segment keeps >= 16 chunks
+  while (blocks * ns * 2 <= cus && NT % (2 * ns) == 0 && NT / (2 * ns) >= 16) ns *= 2;
+  // the prefix pass and the scan cost about one and a half sweeps of a segment: below four segments they
+  // cost more than the parallelism gains
+  return ns >= 4 ? ns : 1;
 }
 
 int device_cu_count() {
@@ -119,11 +150,13 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
 // ---- per-stage event timing (diagnostic; off unless gdn_profile_enable(1) was called on this thread) ----
 enum Stage {
   ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_FACTORS, ST_CONV_FWD,
-  ST_CONV_BWD, ST_NORM_FWD, ST_NORM_BWD, ST_GATES_FWD, ST_GATES_BWD, ST_L2_FWD, ST_L2_BWD, ST_CE, ST_COUNT
+  ST_CONV_BWD, ST_NORM_FWD, ST_NORM_BWD, ST_GATES_FWD, ST_GATES_BWD, ST_L2_FWD, ST_L2_BWD, ST_CE, ST_PREFIX,
+  ST_SEGSCAN, ST_BWD_LOCAL, ST_COUNT
 };
 static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step", "fwd_stash",
                                             "factors", "conv_fwd", "conv_bwd", "norm_fwd", "norm_bwd", "gates_fwd", "gates_bwd",
-                                            "l2norm_fwd", "l2norm_bwd", "cross_entropy"};
+                                            "l2norm_fwd", "l2norm_bwd", "cross_entropy", "prefix", "seg_scan",
+                                            "bwd_local"};
 struct ProfRec { int stage; hipEvent_t a, b; };
 struct Prof {
   bool on = false;
@@ -231,7 +264,7 @@ int gdn_chunk_fwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t*
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
-  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT, nullptr, nullptr);
+  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT | WS_SEGF, nullptr, nullptr, segment_count(B, T, H, K, V));
   return GDN_OK;
 }
 
@@ -239,7 +272,8 @@ int gdn_chunk_bwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t*
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
-  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT | WS_STATE | WS_GRAD, nullptr, nullptr);
+  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT | WS_STATE | WS_GRAD | WS_SEGF | WS_SEGB, nullptr, nullptr,
+                          segment_count(B, T, H, K, V));
   return GDN_OK;
 }
 
@@ -248,8 +282,9 @@ int gdn_chunk_stash_bytes(int B, int T, int H, int K, int V, int dtype, size_t* 
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!stash_bytes || !bwd_ws_bytes) return fail(GDN_ERR_ARG, "stash_bytes or bwd_ws_bytes is NULL");
-  *stash_bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH, nullptr, nullptr);
-  *bwd_ws_bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_GRAD, nullptr, nullptr);
+  const int ns = segment_count(B, T, H, K, V);
+  *stash_bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH, nullptr, nullptr, ns);
+  *bwd_ws_bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_GRAD | WS_SEGB, nullptr, nullptr, ns);
   return GDN_OK;
 }
 
@@ -257,11 +292,30 @@ int gdn_chunk_stash_bytes(int B, int T, int H, int K, int V, int dtype, size_t* 
 
 namespace gdn {
 
+// Segmented forward, after the chunk factors of the segmented problem `a` (B*ns sequences of T/ns tokens):
+// the prefix pass (each segment's state from zero, and its transition), the scan across segments (the state
+// entering each segment; the final state to hT), and `a` set up for the main sweep to start every segment from
+// its entering state.
+static hipError_t seg_forward_prefix(ChunkArgs& a, const float* h0, float* hT, int B, int ns) {
+  ChunkArgs p = a;
+  p.h0 = nullptr;
+  p.hT = a.ws.sloc;
+  hipError_t e = timed(ST_PREFIX, a.stream, [&] { return launch_fwd(p, FWD_PREFIX); });
+  if (e == hipSuccess)
+    e = timed(ST_SEGSCAN, a.stream, [&] {
+      return launch_seg_scan(a.ws.phi, a.ws.sloc, h0, a.ws.sin, hT, B, ns, a.H, a.K, a.V, false, a.stream);
+    });
+  a.h0 = a.ws.sin;
+  a.hT = nullptr;
+  return e;
+}
+
 // Forward: o and hT, and with `stash` the per-chunk intermediates for gdn_chunk_bwd_stashed.  With write keys u
 // (non-null) beta may be null.
 static int chunk_fwd_impl(const void* q, const void* k, const void* u, const void* v, const float* g,
                           const float* beta, const float* h0, void* o, float* hT, void* ws, size_t ws_bytes, int B,
-                          int T, int H, int K, int V, float scale, int dtype, void* stream, bool stash) {
+                          int T, int H, int K, int V, float scale, int dtype, void* stream, bool stash,
+                          bool segments = true) {
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!chunk_shape_supported(K, V, dtype))
@@ -278,14 +332,16 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* u, const voi
   if (misaligned(q, k, u, v, g, beta, h0, o, hT, ws))
     return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   ChunkArgs a{};
-  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, stash ? WS_STASH : WS_FACT, &a.ws, ws);
+  const int ns = segments ? segment_count(B, T, H, K, V) : 1;
+  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, stash ? WS_STASH : (WS_FACT | WS_SEGF), &a.ws, ws, ns);
   if (!ws || ws_bytes < need)
     return fail(GDN_ERR_WORKSPACE, "%s of %zu bytes needed, %zu given", stash ? "stash" : "workspace", need,
                 ws ? ws_bytes : (size_t)0);
   a.q = q; a.k = k; a.u = u; a.v = v; a.g = g; a.beta = beta; a.h0 = h0; a.o = o; a.hT = hT;
-  a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
+  a.B = B * ns; a.T = T / ns; a.H = H; a.K = K; a.V = V; a.NT = (a.T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
   hipError_t e = timed(ST_FACTORS, st, [&] { return launch_factors(a); });
+  if (e == hipSuccess && ns > 1) e = seg_forward_prefix(a, h0, hT, B, ns);
   if (e == hipSuccess)
     e = stash ? timed(ST_FWD_STASH, st, [&] { return launch_fwd(a, FWD_STASH); })
               : timed(ST_FWD, st, [&] { return launch_fwd(a, FWD_OUT); });
@@ -318,27 +374,44 @@ static int chunk_bwd_impl(const void* q, const void* k, const void* u, const voi
   if (misaligned(q, k, u, v, g, beta, h0, dout, dhT, dq, dk, du, dv, dg, dbeta, dh0, stash, ws))
     return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   ChunkArgs a{};
+  const int ns = segment_count(B, T, H, K, V);  // as the forward that filled the stash chose
   if (stashed) {
     // the stash is only read (the kernels take it through the same carve-up as the recompute path's workspace)
-    const size_t sneed = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH, &a.ws, const_cast<void*>(stash));
+    const size_t sneed = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH, &a.ws, const_cast<void*>(stash), ns);
     if (!stash || stash_bytes < sneed)
       return fail(GDN_ERR_WORKSPACE, "stash of %zu bytes needed, %zu given", sneed,
                   stash ? stash_bytes : (size_t)0);
   }
-  const int parts = stashed ? WS_GRAD : (WS_FACT | WS_STATE | WS_GRAD);
-  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, parts, &a.ws, ws);
+  const int parts = stashed ? (WS_GRAD | WS_SEGB) : (WS_FACT | WS_STATE | WS_GRAD | WS_SEGF | WS_SEGB);
+  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, parts, &a.ws, ws, ns);
   if (!ws || ws_bytes < need)
     return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
   a.q = q; a.k = k; a.u = u; a.v = v; a.g = g; a.beta = beta; a.h0 = h0;
   a.dout = dout; a.dhT = dhT; a.dq = dq; a.dk = dk; a.du = du; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.dh0 = dh0;
-  a.B = B; a.T = T; a.H = H; a.K = K; a.V = V; a.NT = (T + CH_TOKENS - 1) / CH_TOKENS;
+  a.B = B * ns; a.T = T / ns; a.H = H; a.K = K; a.V = V; a.NT = (a.T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
   hipError_t e = hipSuccess;
   if (!stashed) {
     e = timed(ST_FACTORS, st, [&] { return launch_factors(a); });
-    if (e == hipSuccess) e = timed(ST_BWD_RECOMP, st, [&] { return launch_fwd(a, FWD_RECOMPUTE); });
+    ChunkArgs f = a;
+    if (e == hipSuccess && ns > 1) e = seg_forward_prefix(f, h0, nullptr, B, ns);
+    if (e == hipSuccess) e = timed(ST_BWD_RECOMP, st, [&] { return launch_fwd(f, FWD_RECOMPUTE); });
   }
-  if (e == hipSuccess) e = timed(ST_BWD_STATE, st, [&] { return launch_bwd_state(a); });
+  if (e == hipSuccess && ns > 1) {
+    // local reverse pass (each segment's entering-state gradient from a zero leaving gradient), then the scan
+    // backwards across segments: the gradient w.r.t. the state leaving each segment, and dh0
+    ChunkArgs l = a;
+    l.dhT = nullptr;
+    l.dh0 = a.ws.dsloc;
+    e = timed(ST_BWD_LOCAL, st, [&] { return launch_bwd_state(l, true); });
+    if (e == hipSuccess)
+      e = timed(ST_SEGSCAN, st, [&] {
+        return launch_seg_scan(a.ws.phi, a.ws.dsloc, dhT, a.ws.dsend, dh0, B, ns, H, K, V, true, st);
+      });
+    a.dhT = a.ws.dsend;
+    a.dh0 = nullptr;
+  }
+  if (e == hipSuccess) e = timed(ST_BWD_STATE, st, [&] { return launch_bwd_state(a, false); });
   if (e == hipSuccess) e = timed(ST_BWD_INTRA, st, [&] { return launch_bwd_intra(a); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "chunk backward launch: %s", hipGetErrorString(e));
   return GDN_OK;
@@ -397,7 +470,7 @@ int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const flo
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!chunk_shape_supported(K, V, dtype)) return shape_error(K, V, dtype);
   const size_t cap = GDN_NOALLOC_SCRATCH_BYTES;
-  const size_t one = chunk_ws_bytes(1, T, H, K, V, dtype, WS_FACT, nullptr, nullptr);
+  const size_t one = chunk_ws_bytes(1, T, H, K, V, dtype, WS_FACT, nullptr, nullptr, 1);
   if (one > cap)
     return fail(GDN_ERR_WORKSPACE, "one sequence needs %zu bytes of chunk factors (H * ceil(T/64) = %lld chunks), "
                 "more than the %zu-byte scratch of the allocation-free forward; use gdn_chunk_fwd", one,
@@ -408,18 +481,19 @@ int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const flo
   // scratch.  Splitting the batch moves every pointer by whole sequences, which keeps the 16-byte alignment the
   // kernels need as long as a sequence's g / beta rows (T * H fp32) are a multiple of 16 bytes.
   int nb = (int)std::min<size_t>((size_t)(B > 0 ? B : 1), cap / one);
-  while (nb > 1 && chunk_ws_bytes(nb, T, H, K, V, dtype, WS_FACT, nullptr, nullptr) > cap) --nb;
+  while (nb > 1 && chunk_ws_bytes(nb, T, H, K, V, dtype, WS_FACT, nullptr, nullptr, 1) > cap) --nb;
   if (nb < B && ((size_t)T * H * 4) % 16 != 0)
     return fail(GDN_ERR_WORKSPACE, "B=%d sequences need %zu bytes of chunk factors, more than the %zu-byte scratch, "
                 "and T * H = %lld is not a multiple of 4, so the batch cannot be split; use gdn_chunk_fwd", B,
-                chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT, nullptr, nullptr), cap, (long long)T * H);
+                chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT, nullptr, nullptr, 1), cap, (long long)T * H);
   const size_t es = dtype == DT_BF16 ? 2 : 4;
   const char* cq = static_cast<const char*>(q);
   const char* ck = static_cast<const char*>(k);
   const char* cv = static_cast<const char*>(v);
   char* co = static_cast<char*>(o);
   if (B == 0)  // nothing to compute; the shared checks still run
-    return chunk_fwd_impl(q, k, nullptr, v, g, beta, h0, o, hT, ws, cap, 0, T, H, K, V, scale, dtype, stream, false);
+    return chunk_fwd_impl(q, k, nullptr, v, g, beta, h0, o, hT, ws, cap, 0, T, H, K, V, scale, dtype, stream, false,
+                          false);
   for (int b0 = 0; b0 < B; b0 += nb) {
     const int n = B - b0 < nb ? B - b0 : nb;
     const int64_t tok = (int64_t)b0 * T * H;  // token rows before this group
@@ -428,7 +502,7 @@ int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const flo
                                  cv ? cv + tok * V * es : nullptr, g ? g + tok : nullptr,
                                  beta ? beta + tok : nullptr, h0 ? h0 + st : nullptr,
                                  co ? co + tok * V * es : nullptr, hT ? hT + st : nullptr, ws, cap, n, T, H, K, V,
-                                 scale, dtype, stream, false);
+                                 scale, dtype, stream, false, false);
     if (e != GDN_OK) return e;
   }
   return GDN_OK;

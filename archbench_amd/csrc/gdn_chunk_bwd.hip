@@ -45,7 +45,9 @@ constexpr int STH = 64 * SW;
 constexpr bool STATE_NT_LOAD = false, STATE_NT_STORE = true;
 constexpr bool INTRA_NT = true;  // every read and write of the gradient kernel is single-use
 
-template <typename T, int K, int BV, bool SEPU>
+// STORE: write dS_C and dY for every chunk (the gradient kernel reads them); without it (the local pass of a
+// segmented sweep) only dh0 is written.
+template <typename T, int K, int BV, bool SEPU, bool STORE>
 __global__ __launch_bounds__(STH) void bwd_state_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u, const T* __restrict__ dout,
     const float* __restrict__ beta,
@@ -142,7 +144,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
 #pragma unroll
     for (int s = 0; s < NSH; ++s) {
       dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
-      store_fragblk<T, STATE_NT_STORE>(wsdH + cidx * K * V, K, NSH * hf + s, cb, ncb, dSb[s]);
+      if constexpr (STORE) store_fragblk<T, STATE_NT_STORE>(wsdH + cidx * K * V, K, NSH * hf + s, cb, ncb, dSb[s]);
     }
     f32x4 kd[4];
 #pragma unroll
@@ -190,7 +192,8 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
       mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, 0), dR0);
       mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, 32), dR1);
     }
-    store_fragblk<T, STATE_NT_STORE>(wsdY + cidx * CH * V, CH, hf, cb, ncb, frag_acc2<T>(Z[0], Z[1]));
+    if constexpr (STORE)
+      store_fragblk<T, STATE_NT_STORE>(wsdY + cidx * CH * V, CH, hf, cb, ncb, frag_acc2<T>(Z[0], Z[1]));
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -632,15 +635,18 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 
 // ---------------------------------------------------------------------------------------------------------
 template <typename T, int K, bool SEPU>
-static hipError_t bwd_state_k(const ChunkArgs& a) {
+static hipError_t bwd_state_k(const ChunkArgs& a, bool local) {
   constexpr int BV = 64;
   dim3 grid(a.V / BV * a.B * a.H);
-  bwd_state_kernel<T, K, BV, SEPU><<<grid, STH, 0, a.stream>>>(
-      static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
-      static_cast<const T*>(a.dout), a.beta, static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P),
-      a.ws.Gc, a.dhT, a.dh0, static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dYs), a.T, a.H, a.V, a.NT,
-      a.scale);
-  return hipGetLastError();
+  auto go = [&](auto kern) {
+    kern<<<grid, STH, 0, a.stream>>>(
+        static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
+        static_cast<const T*>(a.dout), a.beta, static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P),
+        a.ws.Gc, a.dhT, a.dh0, static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dYs), a.T, a.H, a.V, a.NT,
+        a.scale);
+    return hipGetLastError();
+  };
+  return local ? go(bwd_state_kernel<T, K, BV, SEPU, false>) : go(bwd_state_kernel<T, K, BV, SEPU, true>);
 }
 
 template <typename T, int K, int V, bool SEPU>
@@ -667,12 +673,12 @@ static hipError_t bwd_intra_k(const ChunkArgs& a) {
 }
 
 template <bool SEPU>
-static hipError_t bwd_state_dispatch(const ChunkArgs& a) {
+static hipError_t bwd_state_dispatch(const ChunkArgs& a, bool local) {
   if (a.dtype == DT_BF16) {
-    if (a.K == 64) return bwd_state_k<bf16, 64, SEPU>(a);
-    if (a.K == 128) return bwd_state_k<bf16, 128, SEPU>(a);
+    if (a.K == 64) return bwd_state_k<bf16, 64, SEPU>(a, local);
+    if (a.K == 128) return bwd_state_k<bf16, 128, SEPU>(a, local);
   } else if constexpr (!SEPU) {  // separate write keys: bf16 only
-    if (a.K == 64) return bwd_state_k<float, 64, SEPU>(a);
+    if (a.K == 64) return bwd_state_k<float, 64, SEPU>(a, local);
   }
   return hipErrorInvalidValue;
 }
@@ -688,8 +694,8 @@ static hipError_t bwd_intra_dispatch(const ChunkArgs& a) {
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_bwd_state(const ChunkArgs& a) {
-  return a.u ? bwd_state_dispatch<true>(a) : bwd_state_dispatch<false>(a);
+hipError_t launch_bwd_state(const ChunkArgs& a, bool local) {
+  return a.u ? bwd_state_dispatch<true>(a, local) : bwd_state_dispatch<false>(a, local);
 }
 
 hipError_t launch_bwd_intra(const ChunkArgs& a) {

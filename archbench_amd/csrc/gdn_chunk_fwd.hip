@@ -11,6 +11,9 @@
 // prefetched into registers one chunk ahead.
 // MODE 0 writes O (and hT); MODE 1 (recompute for the backward) writes instead the state entering every chunk
 // and R, in the fragment layout straight from the accumulators; MODE 2 (training forward) writes both.
+// MODE 3 (the prefix pass of a segmented sweep) writes only the final state, and the grid carries K more columns
+// per head: those "identity" blocks start from S = I with V = 0, so their final state is the segment's transition
+// Phi = prod_c (gamma_C I - K^T diag(exp(G_C - G)) Tm diag(beta gamma) K), written to phi [BH][K][K].
 // SEPU (separate write keys u, nsgdn.py:240-249): the state update is S <- gamma_C S + U^T (exp(G_C - G) R) with
 // U loaded beside K; K keeps the read K S; beta may be absent (row scale 1).
 #include "gdn_chunk_common.h"
@@ -33,14 +36,14 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u, const T* __restrict__ v,
     const float* __restrict__ beta,
     const float* __restrict__ h0, const T* __restrict__ gTm, const T* __restrict__ gP,
-    const float* __restrict__ gGc, T* __restrict__ o, float* __restrict__ hT, T* __restrict__ wsH,
-    T* __restrict__ wsR, int T_, int H, int V, int NT, float scale) {
+    const float* __restrict__ gGc, T* __restrict__ o, float* __restrict__ hT, float* __restrict__ phi,
+    T* __restrict__ wsH, T* __restrict__ wsR, int T_, int H, int V, int NT, float scale) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
   constexpr int NKT = K / 16;  // row tiles of the state slab
   static_assert(BV / 16 / NWAVE == 1, "each wave pair owns one 16-column slab of the state");
-  constexpr bool OUT = MODE != 1;   // O is computed (needs Q and P)
-  constexpr bool SAVE = MODE != 0;  // per-chunk states and R are written
+  constexpr bool OUT = MODE == 0 || MODE == 2;   // O is computed (needs Q and P)
+  constexpr bool SAVE = MODE == 1 || MODE == 2;  // per-chunk states and R are written
   using F = typename Frag<T>::type;
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
   __shared__ __attribute__((aligned(16))) T sU_[SEPU ? CH * LK : 8];
@@ -54,9 +57,13 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
   __shared__ float sG[CH], sB[CH], sGam[CH];
 
   int vb, bh;
-  sweep_block(V / BV, gridDim.x * BV / V, vb, bh);
+  const int NVB = (V + (MODE == 3 ? K : 0)) / BV;  // column blocks per head
+  sweep_block(NVB, gridDim.x / NVB, vb, bh);
   const int b = bh / H, h = bh - b * H;
-  const int v0 = vb * BV;
+  // identity block (MODE 3): columns iv0 .. iv0 + BV - 1 of the transition; v reads nothing (no valid rows)
+  const bool ident = MODE == 3 && vb * BV >= V;
+  const int iv0 = vb * BV - V;
+  const int v0 = ident ? 0 : vb * BV;
   const int w = wave_id(), l = lane_id();
   const int ws = w & (NWAVE - 1), hf = w >> 2;        // column slab, token half
   const int c0 = 16 * ws;                             // the slab inside the V block
@@ -78,7 +85,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     rk.load(k + row0 * K, (int64_t)H * K, nv, tid);
     if constexpr (SEPU) ru.load(u + row0 * K, (int64_t)H * K, nv, tid);
     if constexpr (OUT) rq.load(q + row0 * K, (int64_t)H * K, nv, tid);
-    rv.load(v + row0 * V + v0, (int64_t)H * V, nv, tid);
+    rv.load(v + row0 * V + v0, (int64_t)H * V, ident ? 0 : nv, tid);
   };
   auto prefetch2 = [&](int c) {
     const int64_t row0 = row0_of(c), cidx = (int64_t)bh * NT + c;
@@ -108,8 +115,11 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
 #pragma unroll
   for (int t = 0; t < NKT; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      S[t][i] = h0 ? h0[sbase + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * t + acc_row(i);
+      S[t][i] = ident ? (row == iv0 + c0 + acc_col() ? 1.f : 0.f)
+                      : (h0 ? h0[sbase + (int64_t)row * V + v0 + c0 + acc_col()] : 0.f);
+    }
 
   auto chunk = [&](int c) {
     const int64_t cidx = (int64_t)bh * NT + c;
@@ -211,7 +221,13 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
   prefetch(0);
   prefetch2(0);
   for (int c = 0; c < NT; ++c) chunk(c);
-  if (hT && hf == 0) {
+  if (ident && hf == 0) {
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        phi[((int64_t)bh * K + 16 * t + acc_row(i)) * K + iv0 + c0 + acc_col()] = S[t][i];
+  } else if (hT && hf == 0) {
 #pragma unroll
     for (int t = 0; t < NKT; ++t)
 #pragma unroll
@@ -223,27 +239,29 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
 template <typename T, int K, int MODE, bool SEPU>
 static hipError_t fwd_sweep_k(const ChunkArgs& a) {
   constexpr int BV = 64;
-  dim3 grid(a.V / BV * a.B * a.H);
+  dim3 grid((a.V + (MODE == 3 ? K : 0)) / BV * a.B * a.H);
   fwd_sweep_kernel<T, K, BV, MODE, SEPU><<<grid, FTH, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
       static_cast<const T*>(a.v), a.beta, a.h0,
       static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P), a.ws.Gc, static_cast<T*>(a.o),
-      MODE == 1 ? nullptr : a.hT, static_cast<T*>(a.ws.hs), static_cast<T*>(a.ws.Rs), a.T, a.H, a.V, a.NT,
-      a.scale);
+      MODE == 1 ? nullptr : a.hT, a.ws.phi, static_cast<T*>(a.ws.hs), static_cast<T*>(a.ws.Rs), a.T, a.H, a.V,
+      a.NT, a.scale);
   return hipGetLastError();
 }
 
 template <typename T, int K>
 static hipError_t fwd_sweep_mode(const ChunkArgs& a, FwdMode mode) {
   if constexpr (sizeof(T) == 2) {
-    if (a.u) {  // separate write keys: the training pair only (stashing forward)
+    if (a.u) {  // separate write keys: the training pair only (stashing forward, and its prefix pass)
       if (mode == FWD_STASH) return fwd_sweep_k<T, K, 2, true>(a);
+      if (mode == FWD_PREFIX) return fwd_sweep_k<T, K, 3, true>(a);
       return hipErrorInvalidValue;
     }
   }
   switch (mode) {
     case FWD_OUT: return fwd_sweep_k<T, K, 0, false>(a);
     case FWD_RECOMPUTE: return fwd_sweep_k<T, K, 1, false>(a);
+    case FWD_PREFIX: return fwd_sweep_k<T, K, 3, false>(a);
     default: return fwd_sweep_k<T, K, 2, false>(a);
   }
 }

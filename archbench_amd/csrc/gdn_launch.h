@@ -34,6 +34,12 @@ struct ChunkWs {
   void* Rs;   // [BH][NT][64][V]    R = U - W S per chunk
   void* dhs;  // [BH][NT][K][V]     dL/d(state leaving each chunk)
   void* dYs;  // [BH][NT][64][V]    dY = Tm^T dL/dR per chunk (the gradient w.r.t. Y, R = Tm Y)
+  // segmented sweeps (WS_SEGF, WS_SEGB; see segment_count), fp32, in the segmented [B*NS, H, ...] layout:
+  float* phi;    // [B*NS][H][K][K]  transition of each segment
+  float* sloc;   // [B*NS][H][K][V]  state leaving each segment from a zero entering state
+  float* sin;    // [B*NS][H][K][V]  state entering each segment
+  float* dsloc;  // [B*NS][H][K][V]  gradient w.r.t. the entering state, from a zero leaving gradient
+  float* dsend;  // [B*NS][H][K][V]  gradient w.r.t. the state leaving each segment
 };
 
 // Separate read and write keys: with u non-null the write (state update, the column side of K K^T and Q K^T, the
@@ -62,8 +68,21 @@ struct ChunkArgs {
 
 // Returns the bytes of the requested parts laid out from `base` and, if `carve` is non-null, sets the pointers
 // of those parts (others untouched).
-enum WsPart { WS_FACT = 1, WS_STATE = 2, WS_GRAD = 4, WS_STASH = WS_FACT | WS_STATE };
-size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, ChunkWs* carve, void* base);
+// WS_SEGF = {phi, sloc, sin} and WS_SEGB = {dsloc, dsend} are empty unless ns > 1; the stash holds WS_SEGF (the
+// backward reads phi).
+enum WsPart { WS_FACT = 1, WS_STATE = 2, WS_GRAD = 4, WS_SEGF = 8, WS_SEGB = 16,
+              WS_STASH = WS_FACT | WS_STATE | WS_SEGF };
+size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, ChunkWs* carve, void* base, int ns);
+
+// Segmented sweeps: when the state sweeps would leave most compute units idle ((V/64) B H workgroups) and the
+// sequence is long, it is cut into NS equal segments of whole chunks, swept in parallel as the problem
+// [B*NS, T/NS, H] (the same memory: a segment of a token-major tensor is contiguous), with the states carried
+// across segments by a prefix pass and a small scan (gdn_segscan.hip).  Returns NS (1: not segmented); a pure
+// function of the shape and the device's CU count, so a forward and its backward agree.
+int segment_count(int B, int T, int H, int K, int V);
+// Carry states (reverse = false) or state gradients (reverse = true) across the segments of every (b, h).
+hipError_t launch_seg_scan(const float* phi, const float* loc, const float* init, float* outs, float* fin, int B,
+                           int NS, int H, int K, int V, bool reverse, hipStream_t stream);
 bool chunk_shape_supported(int K, int V, int dtype);
 bool step_shape_supported(int K, int V);
 
@@ -157,10 +176,12 @@ int device_cu_count();
 
 hipError_t launch_step(const StepArgs& a);
 hipError_t launch_factors(const ChunkArgs& a);                  // Tm, P, Gc
-// FWD_OUT: o, hT.  FWD_RECOMPUTE: hs, Rs, Tm, Gc.  FWD_STASH: both.
-enum FwdMode { FWD_OUT = 0, FWD_RECOMPUTE = 1, FWD_STASH = 2 };
+// FWD_OUT: o, hT.  FWD_RECOMPUTE: hs, Rs.  FWD_STASH: both.  FWD_PREFIX: hT from a zero state (into sloc) and
+// the transition into phi (the prefix pass of a segmented sweep).
+enum FwdMode { FWD_OUT = 0, FWD_RECOMPUTE = 1, FWD_STASH = 2, FWD_PREFIX = 3 };
 hipError_t launch_fwd(const ChunkArgs& a, FwdMode mode);
-hipError_t launch_bwd_state(const ChunkArgs& a);                 // dhs, dYs, dh0
+// dhs, dYs, dh0; local (the first pass of a segmented sweep): dh0 only
+hipError_t launch_bwd_state(const ChunkArgs& a, bool local);
 hipError_t launch_bwd_intra(const ChunkArgs& a);                 // dq, dk, dv, dg, dbeta
 
 }  // namespace gdn

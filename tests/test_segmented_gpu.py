@@ -1,0 +1,100 @@
+"""Segmented sweeps on the GPU: with few (b, h) and a long sequence the library cuts each sequence into segments
+of whole chunks (T = 4096 with one or two heads gives four segments of 1024 tokens), sweeps them in parallel from
+a prefix pass (each segment's state from zero and its transition) and a scan across segments, and mirrors this in
+the backward with the transposed transitions.  Every path that segments is checked against the fp64 oracle on
+the same rounded inputs: the training pair with initial state and final-state gradient (bf16, rel-L2 <= 1e-2),
+the recompute backward and the plain forward in fp32 (max-abs <= 1e-4), the separate-write-key variant, and the
+segmented forward against the unsegmented allocation-free forward.  The event timer confirms the prefix pass and
+the scans ran."""
+
+import ctypes
+
+import pytest
+import torch
+
+from archbench_amd import _lib, ops
+from oracle import gdn_oracle as O
+from oracle import nsgdn_oracle as NSO
+from tests.gpu_util import assert_fp32_close, banner, device_inputs, rel_l2
+
+pytestmark = pytest.mark.gpu
+NAMES = ["dq", "dk", "dv", "dg", "dbeta", "dh0"]
+
+
+@pytest.mark.parametrize("K,V", [(128, 128), (64, 256)])
+def test_training_pair_segmented(K, V):
+    B, T, H = 1, 4096, 2
+    banner(f"segmented training pair B={B} T={T} H={H} K={K} V={V} bf16")
+    host, dev = device_inputs(B, T, H, K, V, torch.bfloat16, seed=41, h0_std=0.1, with_do=True)
+    dhT = torch.randn(B, H, K, V, generator=torch.Generator().manual_seed(42)) * 0.1
+    with _lib.StageTimer() as st:
+        o, hT, stash = ops.chunk_fwd_stash(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, 0.8)
+        got = ops.chunk_bwd_stashed(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, dev.do, dhT.cuda(), stash, 0.8)
+    torch.cuda.synchronize()
+    assert {"prefix", "seg_scan", "bwd_local"} <= set(st.result), st.result
+    assert st.result["seg_scan"][1] == 2  # one scan forward, one backward
+    o_r, hT_r = O.chunk_fwd(host.q, host.k, host.v, host.g, host.beta, 0.8, host.h0)
+    ref = O.chunk_bwd(host.q, host.k, host.v, host.g, host.beta, host.do, 0.8, host.h0, dhT)
+    errs = {"o": rel_l2(o, o_r), "hT": rel_l2(hT, hT_r)}
+    errs.update({n: rel_l2(a, b) for n, a, b in zip(NAMES, got, ref)})
+    print(f"[segmented K={K} V={V}] rel-L2 " + ", ".join(f"{n} {e:.2e}" for n, e in errs.items()), flush=True)
+    assert all(e <= 1e-2 for e in errs.values()), errs
+
+
+def test_fp32_forward_and_recompute_backward_segmented():
+    B, T, H, K, V = 1, 4096, 1, 64, 64
+    banner(f"segmented fp32 forward + recompute backward B={B} T={T} H={H} K={K} V={V}")
+    host, dev = device_inputs(B, T, H, K, V, torch.float32, seed=43, h0_std=0.1, with_do=True)
+    dhT = torch.randn(B, H, K, V, generator=torch.Generator().manual_seed(44)) * 0.1
+    with _lib.StageTimer() as st:
+        o, hT = ops.chunk_fwd(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, 0.5)
+        got = ops.chunk_bwd(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, dev.do, dhT.cuda(), 0.5)
+    torch.cuda.synchronize()
+    assert st.result["prefix"][1] == 2 and st.result["seg_scan"][1] == 3, st.result
+    o_r, hT_r = O.chunk_fwd(host.q, host.k, host.v, host.g, host.beta, 0.5, host.h0)
+    ref = O.chunk_bwd(host.q, host.k, host.v, host.g, host.beta, host.do, 0.5, host.h0, dhT)
+    assert_fp32_close("segmented fp32", ["o", "hT", *NAMES], [o, hT, *got], [o_r, hT_r, *ref], 1e-4)
+
+
+def test_segmented_forward_matches_unsegmented():
+    """gdn_chunk_fwd segments this shape; the allocation-free forward never does: same result to the bf16 bar."""
+    B, T, H, K, V = 2, 4096, 1, 128, 128
+    banner(f"segmented vs unsegmented forward B={B} T={T} H={H} K={K} V={V} bf16")
+    _, dev = device_inputs(B, T, H, K, V, torch.bfloat16, seed=45, h0_std=0.1)
+    o, hT = ops.chunk_fwd(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, 1.0)
+    o2, hT2 = torch.empty_like(o), torch.empty_like(hT)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    rc = _lib.load().gdn_chunk_fwd_noalloc(p(dev.q), p(dev.k), p(dev.v), p(dev.g), p(dev.beta), p(dev.h0), p(o2),
+                                           p(hT2), B, T, H, K, V, 1.0, _lib.DTYPE_BF16, _lib.stream_ptr(o.device))
+    _lib.check(rc, "gdn_chunk_fwd_noalloc")
+    torch.cuda.synchronize()
+    assert rel_l2(o, o2) <= 1e-2 and rel_l2(hT, hT2) <= 1e-2, (rel_l2(o, o2), rel_l2(hT, hT2))
+
+
+def test_nsgdn_segmented():
+    B, T, H, K, V = 1, 4096, 2, 128, 128
+    banner(f"segmented nsgdn B={B} T={T} H={H} K={K} V={V} bf16")
+    gen = torch.Generator().manual_seed(46)
+    r = lambda *s: torch.randn(*s, generator=gen)
+    bf = torch.bfloat16
+    q = (torch.nn.functional.normalize(r(B, T, H, K), dim=-1) * K ** -0.5).to(bf).float()
+    k = torch.nn.functional.normalize(r(B, T, H, K), dim=-1).to(bf).float()
+    beta = torch.sigmoid(r(B, T, H))
+    u = (beta[..., None] * k + 0.05 * r(B, T, H, K)).to(bf).float()
+    v = r(B, T, H, V).to(bf).float()
+    la = torch.nn.functional.logsigmoid(r(B, T, H) + 4)
+    dy = r(B, T, H, V).to(bf).float()
+    S0, dS = 0.1 * r(B, H, K, V), 0.1 * r(B, H, K, V)
+    d = lambda t, dt=bf: t.to("cuda", dt)
+    with _lib.StageTimer() as st:
+        y, hT, stash = ops.nsgdn_chunk_fwd(d(q), d(k), d(u), d(v), d(la, torch.float32), d(S0, torch.float32), 1.0)
+        grads = ops.nsgdn_chunk_bwd(d(q), d(k), d(u), d(v), d(la, torch.float32), d(S0, torch.float32), d(dy),
+                                    d(dS, torch.float32), stash, 1.0)
+    torch.cuda.synchronize()
+    assert "prefix" in st.result and "bwd_local" in st.result, st.result
+    y_r, hT_r = NSO.chunk_fwd(q, k, u, v, la, 1.0, S0)
+    ref = NSO.recurrent_bwd(q, k, u, v, la, dy, 1.0, S0, dS)
+    errs = {"y": rel_l2(y, y_r), "hT": rel_l2(hT, hT_r)}
+    errs.update({n: rel_l2(g, rr) for n, g, rr in zip(("dq", "dk", "du", "dv", "dla", "dh0"), grads, ref)})
+    print("[segmented nsgdn] rel-L2 " + ", ".join(f"{n} {e:.2e}" for n, e in errs.items()), flush=True)
+    assert all(e <= 1e-2 for e in errs.values()), errs
