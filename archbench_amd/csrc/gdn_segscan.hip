@@ -9,11 +9,15 @@
 //     reverse:  G_NS = dhT,   out_s = G_{s+1}, G_s = Phi_s^T G_{s+1} + dloc_s,     fin = G_0    (= dh0)
 // (out_s: the state entering segment s, or the gradient w.r.t. the state leaving it).  All in fp32.
 //
-// One workgroup per (b*h, 64-column block of V), four waves: wave w carries rows w K/4 .. of the block, lane l
-// its column.  Phi_s is staged in LDS as it is stored (row-major, coalesced reads, no bank conflicts); the product
-// runs over k in blocks of four, so each 16-byte read of the staged Phi (the same address in every lane of the
-// wave: a broadcast) serves four multiply-adds: forward, Phi[r][k..k+3] per row r; reverse, Phi[k+j][r..r+3]
-// per j.  The carried block is staged as [k][c], one 4-byte read per lane per k.
+// One workgroup of 256 threads per (b*h, 16-column block of V): thread t carries column c = t & 15 of the block
+// and RPL = K/16 rows of it, row(i) = i*16 + (t >> 4) forward and (t >> 4)*RPL + i in reverse.  Phi_s is staged
+// row-major in LDS with a row pitch of K + 4 floats (coalesced 16-byte loads, prefetched into registers one segment
+// ahead so the global latency overlaps the previous segment's product); the carried block is staged as [k][c].
+//   forward  (out = Phi S):    lane reads Phi[row(i)][k .. k+3], one 16-byte read per row and block of four k;
+//                              the four row groups of a wave are one row apart: distinct banks with this pitch.
+//   reverse  (out = Phi^T G):  lane reads Phi[k][row(0) .. row(RPL-1)] (contiguous rows), RPL/4 16-byte reads per k;
+//                              the row groups are RPL floats apart in one LDS row: distinct banks.
+// The 16 lanes of a row group read the same LDS address (a broadcast).
 #include <hip/hip_runtime.h>
 
 #include "gdn_launch.h"
@@ -21,6 +25,19 @@
 namespace gdn {
 
 constexpr int SCAN_THREADS = 256;
+constexpr int SCAN_COLS = 16;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Loads segment `seg`'s Phi (16-byte pieces threadIdx.x + j * SCAN_THREADS) and the lane's rows of loc.
+template <int K, int NPH, int RPL, bool REVERSE>
+__device__ __forceinline__ void scan_fetch(const float* __restrict__ phi, const float* __restrict__ loc, int64_t seg,
+                                           int rg, int c, int V, f32x4 (&pf)[NPH], float (&lf)[RPL]) {
+  const f32x4* src = reinterpret_cast<const f32x4*>(phi + seg * K * K);
+#pragma unroll
+  for (int j = 0; j < NPH; ++j) pf[j] = src[threadIdx.x + j * SCAN_THREADS];
+#pragma unroll
+  for (int i = 0; i < RPL; ++i) lf[i] = loc[(seg * K + (REVERSE ? rg * RPL + i : i * 16 + rg)) * V + c];
+}
 
 template <int K, bool REVERSE>
 __global__ __launch_bounds__(SCAN_THREADS) void seg_scan_kernel(const float* __restrict__ phi,
@@ -28,71 +45,82 @@ __global__ __launch_bounds__(SCAN_THREADS) void seg_scan_kernel(const float* __r
                                                                const float* __restrict__ init,
                                                                float* __restrict__ outs, float* __restrict__ fin,
                                                                int NS, int H, int V) {
-  constexpr int RW = K / 4;  // rows per wave
-  __shared__ __attribute__((aligned(16))) float sM[K * K];   // Phi_s as stored: sM[r * K + k] = Phi(r, k)
-  __shared__ __attribute__((aligned(16))) float sS[K * 64];  // carried block, [k][c]
-  const int nvb = V / 64;
-  const int bh = blockIdx.x / nvb, vb = blockIdx.x - bh * nvb;
+  constexpr int LDM = K + 4;                           // staged row pitch (floats)
+  constexpr int RPL = K / 16;                          // rows per lane
+  constexpr int NPH = K * K / 4 / SCAN_THREADS;        // 16-byte pieces of Phi per thread
+  static_assert(NPH * 4 * SCAN_THREADS == K * K && RPL % 4 == 0, "scan tiling");
+  __shared__ __attribute__((aligned(16))) float sM[K * LDM];         // Phi_s[r][k]
+  __shared__ __attribute__((aligned(16))) float sS[K * SCAN_COLS];   // carried block, [k][c]
+  const int ncb = V / SCAN_COLS;
+  const int bh = blockIdx.x / ncb, cb = blockIdx.x - bh * ncb;
   const int b = bh / H, h = bh - b * H;
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int r0 = w * RW, c = vb * 64 + l;
-  float acc[RW];
+  const int cl = threadIdx.x & (SCAN_COLS - 1), rg = threadIdx.x >> 4;
+  const int c = cb * SCAN_COLS + cl;
+  auto row = [&](int i) { return REVERSE ? rg * RPL + i : i * 16 + rg; };
+  // (b, s, h) in the segmented [B*NS, H, ...] layout
+  auto seg_of = [&](int step) { return (int64_t)(b * NS + (REVERSE ? NS - 1 - step : step)) * H + h; };
+  f32x4 pf[NPH];
+  float lf[RPL], acc[RPL];
+  scan_fetch<K, NPH, RPL, REVERSE>(phi, loc, seg_of(0), rg, c, V, pf, lf);
 #pragma unroll
-  for (int i = 0; i < RW; ++i) acc[i] = init ? init[((int64_t)bh * K + r0 + i) * V + c] : 0.f;
+  for (int i = 0; i < RPL; ++i) acc[i] = init ? init[((int64_t)bh * K + row(i)) * V + c] : 0.f;
   for (int step = 0; step < NS; ++step) {
-    const int s = REVERSE ? NS - 1 - step : step;
-    const int64_t seg = (int64_t)(b * NS + s) * H + h;  // (b, s, h) in the segmented [B*NS, H, ...] layout
+    const int64_t seg = seg_of(step);
 #pragma unroll
-    for (int i = 0; i < RW; ++i) {
-      outs[(seg * K + r0 + i) * V + c] = acc[i];
-      sS[(r0 + i) * 64 + l] = acc[i];
+    for (int i = 0; i < RPL; ++i) {
+      outs[(seg * K + row(i)) * V + c] = acc[i];
+      sS[row(i) * SCAN_COLS + cl] = acc[i];
     }
-    for (int idx = threadIdx.x; idx < K * K / 4; idx += SCAN_THREADS)
-      reinterpret_cast<float4*>(sM)[idx] = reinterpret_cast<const float4*>(phi + seg * K * K)[idx];
-    __syncthreads();
-    float nxt[RW];
 #pragma unroll
-    for (int i = 0; i < RW; ++i) nxt[i] = loc[(seg * K + r0 + i) * V + c];
+    for (int j = 0; j < NPH; ++j) {
+      const int f = threadIdx.x + j * SCAN_THREADS;   // piece f of Phi: row f / (K/4), columns 4 (f % (K/4)) ..
+      *reinterpret_cast<f32x4*>(sM + (f / (K / 4)) * LDM + (f % (K / 4)) * 4) = pf[j];
+    }
+    float nxt[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) nxt[i] = lf[i];
+    // the next segment's Phi and loc (the last step reloads its own)
+    scan_fetch<K, NPH, RPL, REVERSE>(phi, loc, seg_of(step + 1 < NS ? step + 1 : step), rg, c, V, pf, lf);
+    __syncthreads();
 #pragma unroll 2
     for (int kb = 0; kb < K; kb += 4) {
       float sv[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sv[j] = sS[(kb + j) * 64 + l];
+      for (int j = 0; j < 4; ++j) sv[j] = sS[(kb + j) * SCAN_COLS + cl];
       if constexpr (!REVERSE) {
-        // nxt[r] += sum_j Phi[r][kb + j] S[kb + j]
 #pragma unroll
-        for (int i = 0; i < RW; ++i) {
-          const float4 m = *reinterpret_cast<const float4*>(sM + (r0 + i) * K + kb);
+        for (int i = 0; i < RPL; ++i) {
+          const float4 m = *reinterpret_cast<const float4*>(sM + row(i) * LDM + kb);
           nxt[i] += m.x * sv[0] + m.y * sv[1] + m.z * sv[2] + m.w * sv[3];
         }
       } else {
-        // nxt[r] += sum_j Phi[kb + j][r] G[kb + j]
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j) {
 #pragma unroll
-          for (int i4 = 0; i4 < RW / 4; ++i4) {
-            const float4 m = *reinterpret_cast<const float4*>(sM + (kb + j) * K + r0 + 4 * i4);
-            nxt[4 * i4 + 0] += m.x * sv[j];
-            nxt[4 * i4 + 1] += m.y * sv[j];
-            nxt[4 * i4 + 2] += m.z * sv[j];
-            nxt[4 * i4 + 3] += m.w * sv[j];
+          for (int q = 0; q < RPL / 4; ++q) {
+            const float4 m = *reinterpret_cast<const float4*>(sM + (kb + j) * LDM + rg * RPL + 4 * q);
+            nxt[4 * q] += m.x * sv[j];
+            nxt[4 * q + 1] += m.y * sv[j];
+            nxt[4 * q + 2] += m.z * sv[j];
+            nxt[4 * q + 3] += m.w * sv[j];
           }
+        }
       }
     }
 #pragma unroll
-    for (int i = 0; i < RW; ++i) acc[i] = nxt[i];
+    for (int i = 0; i < RPL; ++i) acc[i] = nxt[i];
     __syncthreads();  // every wave is done with sS and sM before the next segment overwrites them
   }
   if (fin) {
 #pragma unroll
-    for (int i = 0; i < RW; ++i) fin[((int64_t)bh * K + r0 + i) * V + c] = acc[i];
+    for (int i = 0; i < RPL; ++i) fin[((int64_t)bh * K + row(i)) * V + c] = acc[i];
   }
 }
 
 hipError_t launch_seg_scan(const float* phi, const float* loc, const float* init, float* outs, float* fin, int B,
                            int NS, int H, int K, int V, bool reverse, hipStream_t stream) {
-  if (V % 64 != 0) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((int64_t)B * H * (V / 64)));
+  if (V % SCAN_COLS != 0) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((int64_t)B * H * (V / SCAN_COLS)));
   auto go = [&](auto kern) {
     kern<<<grid, SCAN_THREADS, 0, stream>>>(phi, loc, init, outs, fin, NS, H, V);
     return hipGetLastError();
