@@ -14,13 +14,17 @@ zero-init rule for ``o_proj`` (archbench/model.py:14, :80-82) apply.  The forwar
                                                   q scale DK^-1/2 is the op's scale instead of a separate pass
     y = norm(y) * silu(g); o_proj              -> ops.gated_rmsnorm
 
-``scan_impl`` is accepted for config compatibility; every choice runs the HIP chunk kernels (there is no CPU or
-Triton path here).
+``scan_impl``: every choice runs the HIP chunk kernels in bf16 with fp32 state and accumulation, which is what
+the reference's default "chunk" (and "dplr") run (``nsgdn.py:404-405``).  The reference's "triton" and "ref"
+choices are exact fp32 token scans (``nsgdn.py:52-58``, ``:80-216``, ``:408-417``); there is no token-scan path
+here (its exact backward keeps a state per token), so selecting them warns once that the numerics are the chunk
+form's (relative L2 error within 1e-2 of the fp32 recurrence) rather than running silently.
 """
 
 from __future__ import annotations
 
 import math
+import warnings
 
 import torch
 import torch.nn as nn
@@ -59,6 +63,10 @@ class NStepGDN(nn.Module):
             raise ValueError("lam must be > 0")
         if scan_impl not in ("chunk", "dplr", "triton", "ref"):
             raise ValueError(f"unknown scan_impl {scan_impl!r}")
+        if scan_impl in ("triton", "ref"):
+            warnings.warn(f"NStepGDN(scan_impl={scan_impl!r}): the reference runs an exact fp32 token scan here; "
+                          "this build runs the bf16 chunk kernels for every scan_impl (fp32 state and "
+                          "accumulation, relative L2 within 1e-2 of the fp32 recurrence)", UserWarning, stacklevel=2)
         self.H, self.DK, self.DV, self.n_steps = num_heads, DK, DV, n_steps
         self.qk_dim, self.v_dim = num_heads * DK, num_heads * DV
         self.use_gate = use_gate

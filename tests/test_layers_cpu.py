@@ -99,3 +99,19 @@ def test_nsgdn_registered_and_no_cpu_fallback():
         m(torch.randn(1, 8, 128))
     with pytest.raises(ValueError):
         layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=48)
+
+
+def test_nsgdn_token_scan_choices_warn():
+    """The reference's "triton" and "ref" scan_impl are exact fp32 token scans; this build runs the chunk kernels
+    for every choice and says so for those two, while the reference's own default ("chunk") builds quietly."""
+    import warnings
+
+    for impl in ("triton", "ref"):
+        with pytest.warns(UserWarning, match="fp32 token scan"):
+            layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=64, scan_impl=impl)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        for impl in ("chunk", "dplr"):
+            layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=64, scan_impl=impl)
+    with pytest.raises(ValueError):
+        layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=64, scan_impl="cuda")
