@@ -7,7 +7,9 @@
 //     forward:  S_0 = h0,     out_s = S_s,   S_{s+1} = Phi_s S_s + loc_s,           fin = S_NS   (= hT)
 // and the state gradient backwards, with the transposed transitions:
 //     reverse:  G_NS = dhT,   out_s = G_{s+1}, G_s = Phi_s^T G_{s+1} + dloc_s,     fin = G_0    (= dh0)
-// (out_s: the state entering segment s, or the gradient w.r.t. the state leaving it).  All in fp32.
+// (out_s: the state entering segment s, or the gradient w.r.t. the state leaving it).  All in fp32.  Without
+// init the first product is skipped (its Phi need not exist), and without fin so is the last update: the main
+// sweeps produce hT (from the last segment) and dh0 (from the first) themselves.
 //
 // One workgroup of 256 threads per (b*h, 16-column block of V): thread t carries column c = t & 15 of the block
 // and RPL = K/16 rows of it, row(i) = i*16 + (t >> 4) forward and (t >> 4)*RPL + i in reverse.  Phi_s is staged
@@ -71,19 +73,23 @@ __global__ __launch_bounds__(SCAN_THREADS) void seg_scan_kernel(const float* __r
       outs[(seg * K + row(i)) * V + c] = acc[i];
       sS[row(i) * SCAN_COLS + cl] = acc[i];
     }
+    if (step == NS - 1 && !fin) break;  // uniform: nothing reads the state past the last segment
+    const bool prod = step > 0 || init;  // the carried block is zero before the first product without init
+    if (prod) {
 #pragma unroll
-    for (int j = 0; j < NPH; ++j) {
-      const int f = threadIdx.x + j * SCAN_THREADS;   // piece f of Phi: row f / (K/4), columns 4 (f % (K/4)) ..
-      *reinterpret_cast<f32x4*>(sM + (f / (K / 4)) * LDM + (f % (K / 4)) * 4) = pf[j];
+      for (int j = 0; j < NPH; ++j) {
+        const int f = threadIdx.x + j * SCAN_THREADS;   // piece f of Phi: row f / (K/4), columns 4 (f % (K/4)) ..
+        *reinterpret_cast<f32x4*>(sM + (f / (K / 4)) * LDM + (f % (K / 4)) * 4) = pf[j];
+      }
     }
     float nxt[RPL];
 #pragma unroll
     for (int i = 0; i < RPL; ++i) nxt[i] = lf[i];
     // the next segment's Phi and loc (the last step reloads its own)
     scan_fetch<K, NPH, RPL, REVERSE>(phi, loc, seg_of(step + 1 < NS ? step + 1 : step), rg, c, V, pf, lf);
-    __syncthreads();
+    if (prod) __syncthreads();
 #pragma unroll 2
-    for (int kb = 0; kb < K; kb += 4) {
+    for (int kb = 0; kb < (prod ? K : 0); kb += 4) {
       float sv[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) sv[j] = sS[(kb + j) * SCAN_COLS + cl];

@@ -98,3 +98,27 @@ def test_nsgdn_segmented():
     errs.update({n: rel_l2(g, rr) for n, g, rr in zip(("dq", "dk", "du", "dv", "dla", "dh0"), grads, ref)})
     print("[segmented nsgdn] rel-L2 " + ", ".join(f"{n} {e:.2e}" for n, e in errs.items()), flush=True)
     assert all(e <= 1e-2 for e in errs.values()), errs
+
+
+@pytest.mark.parametrize("with_h0, with_dhT", [(False, False), (False, True), (True, False)])
+def test_segmented_batch_without_states(with_h0, with_dhT):
+    """Two sequences of four segments each.  The main sweeps write hT from each sequence's last segment and dh0
+    from its first, at the sequence's own index; without h0 the first segment's transition is never built (the
+    scan starts from zero), and without dhT the reverse scan does.  Every output against the fp64 oracle."""
+    B, T, H, K, V = 2, 4096, 1, 128, 128
+    banner(f"segmented training pair B={B} T={T} H={H} K={K} V={V} bf16, h0={with_h0} dhT={with_dhT}")
+    host, dev = device_inputs(B, T, H, K, V, torch.bfloat16, seed=47, h0_std=0.1 if with_h0 else None,
+                              with_do=True)
+    dhT = torch.randn(B, H, K, V, generator=torch.Generator().manual_seed(48)) * 0.1 if with_dhT else None
+    with _lib.StageTimer() as st:
+        o, hT, stash = ops.chunk_fwd_stash(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, 1.0)
+        got = ops.chunk_bwd_stashed(dev.q, dev.k, dev.v, dev.g, dev.beta, dev.h0, dev.do,
+                                    None if dhT is None else dhT.cuda(), stash, 1.0)
+    torch.cuda.synchronize()
+    assert {"prefix", "seg_scan", "bwd_local"} <= set(st.result), st.result
+    o_r, hT_r = O.chunk_fwd(host.q, host.k, host.v, host.g, host.beta, 1.0, host.h0)
+    ref = O.chunk_bwd(host.q, host.k, host.v, host.g, host.beta, host.do, 1.0, host.h0, dhT)
+    errs = {"o": rel_l2(o, o_r), "hT": rel_l2(hT, hT_r)}
+    errs.update({n: rel_l2(a, b) for n, a, b in zip(NAMES, got, ref)})
+    print("[segmented batch] rel-L2 " + ", ".join(f"{n} {e:.2e}" for n, e in errs.items()), flush=True)
+    assert all(e <= 1e-2 for e in errs.values()), errs
