@@ -293,17 +293,14 @@ int gdn_chunk_stash_bytes(int B, int T, int H, int K, int V, int dtype, size_t* 
 namespace gdn {
 
 // Segmented forward, after the chunk factors of the segmented problem `a` (B*ns sequences of T/ns tokens):
-// the prefix pass (each segment's state from zero, and its transition), the scan across segments (the state
-// entering each segment), and `a` set up for the main sweep to start every segment from its entering state (it
-// writes hT, from each sequence's last segment).  Only what is read is computed: no local state for the last
-// segment, no transition for the first without h0, none for the last unless a backward will scan with it
-// (with_bwd).
-static hipError_t seg_forward_prefix(ChunkArgs& a, const float* h0, int B, int ns, bool with_bwd) {
+// the prefix pass (each segment's state from zero -- the first from h0 -- and the transitions of the middle
+// segments), the scan across segments (the state entering each segment), and `a` set up for the main sweep to
+// start every segment from its entering state (it writes hT, from each sequence's last segment).
+static hipError_t seg_forward_prefix(ChunkArgs& a, const float* h0, int B, int ns) {
   ChunkArgs p = a;
-  p.h0 = nullptr;
+  p.h0 = h0;
   p.hT = a.ws.sloc;
   p.ns = ns;
-  p.seg_flags = (h0 ? SEG_PHI_FIRST : 0) | (with_bwd ? SEG_PHI_LAST : 0);
   hipError_t e = timed(ST_PREFIX, a.stream, [&] { return launch_fwd(p, FWD_PREFIX); });
   if (e == hipSuccess)
     e = timed(ST_SEGSCAN, a.stream, [&] {
@@ -345,7 +342,7 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* u, const voi
   a.B = B * ns; a.T = T / ns; a.H = H; a.K = K; a.V = V; a.NT = (a.T + CH_TOKENS - 1) / CH_TOKENS;
   a.scale = scale; a.dtype = dtype; a.stream = st;
   hipError_t e = timed(ST_FACTORS, st, [&] { return launch_factors(a); });
-  if (e == hipSuccess && ns > 1) e = seg_forward_prefix(a, h0, B, ns, stash);
+  if (e == hipSuccess && ns > 1) e = seg_forward_prefix(a, h0, B, ns);
   if (e == hipSuccess)
     e = stash ? timed(ST_FWD_STASH, st, [&] { return launch_fwd(a, FWD_STASH); })
               : timed(ST_FWD, st, [&] { return launch_fwd(a, FWD_OUT); });
@@ -399,18 +396,18 @@ static int chunk_bwd_impl(const void* q, const void* k, const void* u, const voi
     e = timed(ST_FACTORS, st, [&] { return launch_factors(a); });
     ChunkArgs f = a;
     f.hT = nullptr;
-    if (e == hipSuccess && ns > 1) e = seg_forward_prefix(f, h0, B, ns, true);
+    if (e == hipSuccess && ns > 1) e = seg_forward_prefix(f, h0, B, ns);
     if (e == hipSuccess) e = timed(ST_BWD_RECOMP, st, [&] { return launch_fwd(f, FWD_RECOMPUTE); });
   }
   if (e == hipSuccess && ns > 1) {
-    // local reverse pass (each segment's entering-state gradient from a zero leaving gradient; not the first
-    // segment's, which only dh0 would need), then the scan backwards across segments: the gradient w.r.t. the
-    // state leaving each segment.  The main reverse sweep then writes dh0 from each sequence's first segment.
+    // local reverse pass (each segment's entering-state gradient from a zero leaving gradient -- the last from
+    // dhT; not the first segment's, which only dh0 would need), then the scan backwards across segments: the
+    // gradient w.r.t. the state leaving each segment.  The main reverse sweep then writes dh0 from each
+    // sequence's first segment.
     ChunkArgs l = a;
-    l.dhT = nullptr;
+    l.dhT = dhT;
     l.dh0 = a.ws.dsloc;
     l.ns = ns;
-    l.seg_flags = SEG_SKIP_FIRST;
     e = timed(ST_BWD_LOCAL, st, [&] { return launch_bwd_state(l, true); });
     if (e == hipSuccess)
       e = timed(ST_SEGSCAN, st, [&] {

@@ -53,7 +53,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     const float* __restrict__ beta,
     const T* __restrict__ gTm, const T* __restrict__ gP, const float* __restrict__ gGc,
     const float* __restrict__ dhT, float* __restrict__ dh0, T* __restrict__ wsdH, T* __restrict__ wsdY, int T_,
-    int H, int V, int NT, float scale, int ns, int seg_flags) {
+    int H, int V, int NT, float scale, int ns) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
   constexpr int NKH = K / 32;     // row tiles of dS per half
@@ -75,11 +75,15 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
   sweep_block(V / BV, gridDim.x * BV / V, vb, bh);
   const int b = bh / H, h = bh - b * H;
   const int seg = b % ns;  // segment of sequence b / ns (ns = 1: not segmented)
-  if ((seg_flags & SEG_SKIP_FIRST) && seg == 0) return;  // uniform over the workgroup, before any barrier
-  // dh0: per swept sequence in the local pass (STORE = false); otherwise, when segmented, only from the first
-  // segment of each sequence, at the sequence's index
+  // The local pass of a segmented sweep (STORE = false) skips each sequence's first segment (its entering-state
+  // gradient is the main sweep's dh0) and starts the last from the sequence's dhT, so that its result already
+  // carries dhT.  dh0: per swept sequence in the local pass; otherwise, when segmented, only from the first
+  // segment of each sequence, at the sequence's index.  dhT: per swept sequence in the main pass.
+  if (!STORE && seg == 0) return;  // uniform over the workgroup, before any barrier
   const bool put_dh0 = !STORE || seg == 0;
   const int64_t dh0_base = (!STORE ? (int64_t)bh : (int64_t)(b / ns) * H + h) * K * V;
+  const bool use_dhT = dhT && (STORE || seg == ns - 1);
+  const int64_t dhT_base = (STORE ? (int64_t)bh : (int64_t)(b / ns) * H + h) * K * V;
   const int v0 = vb * BV;
   const int w = wave_id(), l = lane_id();
   const int ws = w & (NWAVE - 1), hf = w >> 2;  // column slab; half of dS's rows and of the chunk's tokens
@@ -126,7 +130,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
   for (int t = 0; t < NKH; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      dS[t][i] = dhT ? dhT[sbase + (int64_t)(k0 + 16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
+      dS[t][i] = use_dhT ? dhT[dhT_base + (int64_t)(k0 + 16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] : 0.f;
 
   auto chunk = [&](int c) {
     const int64_t cidx = (int64_t)bh * NT + c;
@@ -649,7 +653,7 @@ static hipError_t bwd_state_k(const ChunkArgs& a, bool local) {
         static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
         static_cast<const T*>(a.dout), a.beta, static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P),
         a.ws.Gc, a.dhT, a.dh0, static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dYs), a.T, a.H, a.V, a.NT,
-        a.scale, a.ns, a.seg_flags);
+        a.scale, a.ns);
     return hipGetLastError();
   };
   return local ? go(bwd_state_kernel<T, K, BV, SEPU, false>) : go(bwd_state_kernel<T, K, BV, SEPU, true>);

@@ -13,9 +13,10 @@
 // and R, in the fragment layout straight from the accumulators; MODE 2 (training forward) writes both.
 // MODE 3 (the prefix pass of a segmented sweep) writes only the final state, and the grid carries K more columns
 // per head: those "identity" blocks start from S = I with V = 0, so their final state is the segment's transition
-// Phi = prod_c (gamma_C I - K^T diag(exp(G_C - G)) Tm diag(beta gamma) K), written to phi [BH][K][K].  Blocks
-// nothing reads return at once: the last segment's state (the main sweep writes hT), the first segment's Phi
-// without an initial state, the last segment's Phi without a backward (seg_flags).
+// Phi = prod_c (gamma_C I - K^T diag(exp(G_C - G)) Tm diag(beta gamma) K), written to phi [BH][K][K].  The
+// first segment of each sequence starts from h0 instead of zero, so its "local" state already carries h0 and its
+// Phi is never needed; nor is the last segment's state (the main sweep writes hT) or its Phi (the local reverse
+// pass starts that segment from dhT): those blocks return at once.
 // SEPU (separate write keys u, nsgdn.py:240-249): the state update is S <- gamma_C S + U^T (exp(G_C - G) R) with
 // U loaded beside K; K keeps the read K S; beta may be absent (row scale 1).
 #include "gdn_chunk_common.h"
@@ -39,7 +40,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     const float* __restrict__ beta,
     const float* __restrict__ h0, const T* __restrict__ gTm, const T* __restrict__ gP,
     const float* __restrict__ gGc, T* __restrict__ o, float* __restrict__ hT, float* __restrict__ phi,
-    T* __restrict__ wsH, T* __restrict__ wsR, int T_, int H, int V, int NT, float scale, int ns, int seg_flags) {
+    T* __restrict__ wsH, T* __restrict__ wsR, int T_, int H, int V, int NT, float scale, int ns) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
   constexpr int NKT = K / 16;  // row tiles of the state slab
@@ -68,15 +69,15 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
   const int v0 = ident ? 0 : vb * BV;
   const int seg = b % ns;  // segment of sequence b / ns (ns = 1: not segmented)
   if constexpr (MODE == 3) {
-    const bool need = ident ? (seg == 0 ? (seg_flags & SEG_PHI_FIRST) != 0
-                                        : seg < ns - 1 || (seg_flags & SEG_PHI_LAST) != 0)
-                            : seg < ns - 1;
-    if (!need) return;  // uniform over the workgroup, before any barrier
+    if (seg == ns - 1 || (ident && seg == 0)) return;  // uniform over the workgroup, before any barrier
   }
   // hT: per swept sequence in MODE 3 (the segments' local states); otherwise, when segmented, only from the last
-  // segment of each sequence, at the sequence's index
+  // segment of each sequence, at the sequence's index.  h0: in MODE 3 the sequence's own, for its first segment
+  // only; otherwise per swept sequence (the entering state of every segment).
   const bool put_hT = MODE == 3 || seg == ns - 1;
   const int64_t hT_base = (MODE == 3 ? (int64_t)bh : (int64_t)(b / ns) * H + h) * K * V;
+  const bool use_h0 = h0 && (MODE != 3 || seg == 0);
+  const int64_t h0_base = (MODE == 3 ? (int64_t)(b / ns) * H + h : (int64_t)bh) * K * V;
   const int w = wave_id(), l = lane_id();
   const int ws = w & (NWAVE - 1), hf = w >> 2;        // column slab, token half
   const int c0 = 16 * ws;                             // the slab inside the V block
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     for (int i = 0; i < 4; ++i) {
       const int row = 16 * t + acc_row(i);
       S[t][i] = ident ? (row == iv0 + c0 + acc_col() ? 1.f : 0.f)
-                      : (h0 ? h0[sbase + (int64_t)row * V + v0 + c0 + acc_col()] : 0.f);
+                      : (use_h0 ? h0[h0_base + (int64_t)row * V + v0 + c0 + acc_col()] : 0.f);
     }
 
   auto chunk = [&](int c) {
@@ -258,7 +259,7 @@ static hipError_t fwd_sweep_k(const ChunkArgs& a) {
       static_cast<const T*>(a.v), a.beta, a.h0,
       static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P), a.ws.Gc, static_cast<T*>(a.o),
       MODE == 1 ? nullptr : a.hT, a.ws.phi, static_cast<T*>(a.ws.hs), static_cast<T*>(a.ws.Rs), a.T, a.H, a.V,
-      a.NT, a.scale, a.ns, a.seg_flags);
+      a.NT, a.scale, a.ns);
   return hipGetLastError();
 }
 

@@ -65,15 +65,10 @@ struct ChunkArgs {
   int dtype;
   hipStream_t stream;
   // Segmented sweeps: B counts the segments (B = batch * ns, segment s of sequence b is b * ns + s).  With
-  // ns > 1 the main sweeps write hT only from each sequence's last segment and dh0 only from its first, at the
-  // sequence's own index; seg_flags selects the blocks of the prefix and local passes that are needed.
+  // ns > 1 the main sweeps write hT only from each sequence's last segment and dh0 only from its first, and the
+  // prefix pass (local reverse pass) starts each sequence's first (last) segment from h0 (dhT), all at the
+  // sequence's own index.
   int ns = 1;
-  int seg_flags = 0;
-};
-enum SegFlags {
-  SEG_PHI_FIRST = 1,   // prefix pass: the first segment's transition (an initial state is given)
-  SEG_PHI_LAST = 2,    // prefix pass: the last segment's transition (a backward will scan with it)
-  SEG_SKIP_FIRST = 4,  // local reverse pass: skip the first segment (its entering gradient is the main sweep's dh0)
 };
 
 // Returns the bytes of the requested parts laid out from `base` and, if `carve` is non-null, sets the pointers

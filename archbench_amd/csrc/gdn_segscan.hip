@@ -2,13 +2,15 @@
 //
 // A sequence of NS segments (the token-major tensors viewed as [B*NS, T/NS, H, .]) is swept in parallel: a
 // prefix pass gives, per segment s and head, the state the segment leaves from a zero entering state (loc_s,
-// [K][V]) and the segment's transition Phi_s ([K][K], so that leaving = Phi_s entering + loc_s).  This kernel
-// then carries the state across the segments in order, one small product per segment:
-//     forward:  S_0 = h0,     out_s = S_s,   S_{s+1} = Phi_s S_s + loc_s,           fin = S_NS   (= hT)
-// and the state gradient backwards, with the transposed transitions:
-//     reverse:  G_NS = dhT,   out_s = G_{s+1}, G_s = Phi_s^T G_{s+1} + dloc_s,     fin = G_0    (= dh0)
-// (out_s: the state entering segment s, or the gradient w.r.t. the state leaving it).  All in fp32.  Without
-// init the first product is skipped (its Phi need not exist), and without fin so is the last update: the main
+// [K][V]; for the first segment from h0, so loc_0 = Phi_0 h0 + its local state) and the segment's transition
+// Phi_s ([K][K], so that leaving = Phi_s entering + loc_s).  This kernel then carries the state across the
+// segments in order, one small product per segment:
+//     forward:  out_0 = S_0 = h0,  S_1 = loc_0,  S_{s+1} = Phi_s S_s + loc_s (s >= 1),  fin = S_NS   (= hT)
+// and the state gradient backwards, with the transposed transitions (dloc_{NS-1} likewise already carrying dhT):
+//     reverse:  out_{NS-1} = dhT,  G_{NS-1} = dloc_{NS-1},  G_s = Phi_s^T G_{s+1} + dloc_s,  out_s = G_{s+1},
+//               fin = G_0 (= dh0)
+// (out_s: the state entering segment s, or the gradient w.r.t. the state leaving it).  All in fp32.  Phi of the
+// first (forward) or last (reverse) segment is never read, and without fin neither is the other end's: the main
 // sweeps produce hT (from the last segment) and dh0 (from the first) themselves.
 //
 // One workgroup of 256 threads per (b*h, 16-column block of V): thread t carries column c = t & 15 of the block
@@ -74,7 +76,7 @@ __global__ __launch_bounds__(SCAN_THREADS) void seg_scan_kernel(const float* __r
       sS[row(i) * SCAN_COLS + cl] = acc[i];
     }
     if (step == NS - 1 && !fin) break;  // uniform: nothing reads the state past the last segment
-    const bool prod = step > 0 || init;  // the carried block is zero before the first product without init
+    const bool prod = step > 0;         // the first local state already carries init
     if (prod) {
 #pragma unroll
       for (int j = 0; j < NPH; ++j) {
