@@ -11,8 +11,9 @@
         -o profiles/mfma_counters.json --md profiles/X.md
 
 Kernels are grouped into the stage names the library's own event timer uses (factors, fwd, fwd_stash,
-bwd_recompute, bwd_state, bwd_intra, step, conv_fwd, conv_bwd, norm_fwd, norm_bwd, ...), so the numbers line up with
-bench.py's per-kernel table; a stage that ran at several grid sizes is split into stage@grid (threads).
+bwd_recompute, prefix, seg_scan, bwd_local, bwd_state, bwd_intra, step, conv_fwd, conv_bwd, norm_fwd, norm_bwd,
+...), so the numbers line up with bench.py's per-kernel table; a stage that ran at several grid sizes is split into
+stage@grid (threads).
 """
 
 from __future__ import annotations
@@ -37,8 +38,11 @@ def stage_of(name: str) -> str:
     if "fwd_sweep_kernel" in name:
         args = re.findall(r"Li(\d+)E", name)  # K, BV, MODE
         mode = int(args[2]) if len(args) >= 3 else -1
-        return {0: "fwd", 1: "bwd_recompute", 2: "fwd_stash"}.get(mode, "fwd_sweep")
-    for key, stage in (("bwd_state_kernel", "bwd_state"), ("bwd_intra_kernel", "bwd_intra"),
+        return {0: "fwd", 1: "bwd_recompute", 2: "fwd_stash", 3: "prefix"}.get(mode, "fwd_sweep")
+    if "bwd_state_kernel" in name:
+        flags = re.findall(r"Lb(\d)E", name)  # SEPU, STORE (STORE = 0: the local pass of a segmented sweep)
+        return "bwd_local" if len(flags) >= 2 and flags[1] == "0" else "bwd_state"
+    for key, stage in (("seg_scan_kernel", "seg_scan"), ("bwd_intra_kernel", "bwd_intra"),
                        ("step_kernel", "step"), ("conv_silu_fwd", "conv_fwd"), ("conv_silu_bwd", "conv_bwd"),
                        ("row_norm_fwd", "norm_fwd"), ("row_norm_bwd", "norm_bwd"), ("gates_fwd", "gates_fwd"),
                        ("gates_bwd", "gates_bwd"), ("ce_fwd_bwd", "cross_entropy"), ("column_sum", "column_sum"),
