@@ -446,8 +446,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   const int cnext = ci + (int)gridDim.x < nchunk ? ci + (int)gridDim.x : ci;
   T* sdq = slab;             // CH x LK   dq staging
   T* sdk = sdq + CH * LK;    // CH x LK   dk staging
-  T* sD = sdk + CH * LK;     // CH x LC   D = dA o beta_i E
-  T* sdPm = sD + CH * LC;    // CH x LC   dP o s E
+  T* sD = sdk + CH * LK;     // CH x LC   D = dA o beta_i E,  column-major (element (r, c) at c * LC + r)
+  T* sdPm = sD + CH * LC;    // CH x LC   dP o s E,         column-major
 
   const int lg = l >> 4;  // lane group: rows 4*lg .. 4*lg+3 of each tile
   float gam[4], dte[4], bet[4], Grow[4];
@@ -485,7 +485,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
     mma_blk<true, true, K>(kk, sK, LK, 16 * rb, sU, LK, 16 * n, l);
     mma_blk<true, true, K>(qk, sQ, LK, 16 * rb, sU, LK, 16 * n, l);
-    f32x4 z;
+    f32x4 z, Dt, Wt;
     const int cc = 16 * n + acc_col(l);
     const float Gc = sG[cc];
 #pragma unroll
@@ -498,11 +498,20 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       const float uu = r > cc ? -aDA[j][i] * e : 0.f;
       const float wv = aP[j][i] * (scale * e);
       const float Dv = uu * bet[i];
-      sD[r * LC + cc] = from_f<T>(Dv);
-      sdPm[r * LC + cc] = from_f<T>(wv);
+      Dt[i] = Dv;
+      Wt[i] = wv;
       dbA[i] += uu * kk[i];
       z[i] = wv * qk[i] + Dv * kk[i];
       rz[i] += z[i];
+    }
+    // the lane's four rows of column cc are contiguous in the column-major tiles: one vector store each
+    {
+      using V4 = typename std::conditional<sizeof(T) == 2, bf16x4, f32x4>::type;
+      const int r0 = 16 * rb + acc_row(0, l);
+      *reinterpret_cast<V4*>(sD + cc * LC + r0) = V4{from_f<T>(Dt[0]), from_f<T>(Dt[1]), from_f<T>(Dt[2]),
+                                                     from_f<T>(Dt[3])};
+      *reinterpret_cast<V4*>(sdPm + cc * LC + r0) = V4{from_f<T>(Wt[0]), from_f<T>(Wt[1]), from_f<T>(Wt[2]),
+                                                       from_f<T>(Wt[3])};
     }
     const float cs = colsum_tile(z);
     if (lg == 0) sColZ[rb][cc] = cs;
@@ -544,7 +553,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 #pragma unroll
     for (int j = 0; j < HK; ++j) {
       t[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      mma_blk<true, false, CH>(t[j], sdPm, LC, 16 * rb, sU, LK, 16 * (HK * hf + j), l);
+      mma_blk<false, false, CH>(t[j], sdPm, LC, 16 * rb, sU, LK, 16 * (HK * hf + j), l);
     }
 #pragma unroll
     for (int j = 0; j < HK; ++j)
@@ -561,9 +570,9 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     for (int j = 0; j < HK; ++j) {
       const int n = HK * hf + j;
       t[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      mma_blk<false, false, CH>(t[j], sdPm, LC, 16 * rb, sQ, LK, 16 * n, l);
-      mma_blk<true, false, CH>(t[j], sD, LC, 16 * rb, sK, LK, 16 * n, l);
+      mma_blk<true, false, CH>(t[j], sdPm, LC, 16 * rb, sQ, LK, 16 * n, l);
       mma_blk<false, false, CH>(t[j], sD, LC, 16 * rb, sK, LK, 16 * n, l);
+      mma_blk<true, false, CH>(t[j], sD, LC, 16 * rb, sK, LK, 16 * n, l);
     }
 #pragma unroll
     for (int j = 0; j < HK; ++j)
@@ -581,9 +590,9 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       const int n = HK * hf + j;
       f32x4 t2 = {0.f, 0.f, 0.f, 0.f};
       t[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      mma_blk<true, false, CH>(t[j], sD, LC, 16 * rb, sU, LK, 16 * n, l);
-      mma_blk<false, false, CH>(t2, sdPm, LC, 16 * rb, sQ, LK, 16 * n, l);
-      mma_blk<false, false, CH>(t2, sD, LC, 16 * rb, sK, LK, 16 * n, l);
+      mma_blk<false, false, CH>(t[j], sD, LC, 16 * rb, sU, LK, 16 * n, l);
+      mma_blk<true, false, CH>(t2, sdPm, LC, 16 * rb, sQ, LK, 16 * n, l);
+      mma_blk<true, false, CH>(t2, sD, LC, 16 * rb, sK, LK, 16 * n, l);
 #pragma unroll
       for (int i = 0; i < 4; ++i) aKd[j][i] = dte[i] * aKd[j][i] + t2[i];
     }
