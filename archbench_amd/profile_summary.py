@@ -153,6 +153,10 @@ def counters(args) -> None:
         for c, v in vals.items():
             per[st][c].append(v)
     names = sorted({c for st in per.values() for c in st})
+    # with SQ_WAVE_CYCLES present, every other SQ_ counter is also shown as a fraction of it (the share of the
+    # waves' cycles spent in that state; the SQ cycle counters share its unit)
+    frac_names = [c for c in names if c.startswith("SQ_") and c != "SQ_WAVE_CYCLES"] if "SQ_WAVE_CYCLES" in names \
+        else []
     per_launch, table = {}, []
     for st in sorted(per):
         if st.split("@")[0] == "copy" or st.startswith("other:"):
@@ -164,16 +168,21 @@ def counters(args) -> None:
         if "MfmaFlopsBF16" in avg:
             ent["executed_bf16_flops"] = round(avg["MfmaFlopsBF16"])
         ent.update({c: round(v, 1) for c, v in avg.items() if c not in ("MfmaUtil", "MfmaFlopsBF16")})
+        fr = [avg.get(c, float("nan")) / avg["SQ_WAVE_CYCLES"] for c in frac_names] if frac_names else []
+        if frac_names:
+            ent["per_wave_cycle"] = {c: round(f, 4) for c, f in zip(frac_names, fr)}
         per_launch[st] = ent
         table.append(f"| {st} | {ent['launches']} | " + " | ".join(f"{avg.get(c, float('nan')):.4g}" for c in names)
-                     + " |")
+                     + "".join(f" | {f:.3f}" for f in fr) + " |")
     json.dump({"workload": args.workload, "command": args.command, "per_launch": per_launch}, open(args.out, "w"),
               indent=1)
     print(f"wrote {args.out}")
     if args.md:
         lines = [f"# rocprofv3 counters per launch: {args.workload}", "", "Command (repo root, one MI355X):", "",
-                 "```", args.command, "```", "", "Averages over the launches of each stage.", "",
-                 "| stage | launches | " + " | ".join(names) + " |", "|---|---|" + "---|" * len(names), *table]
+                 "```", args.command, "```", "", "Averages over the launches of each stage" +
+                 ("; the last columns are the SQ counters over SQ_WAVE_CYCLES." if frac_names else "."), "",
+                 "| stage | launches | " + " | ".join(names) + "".join(f" | {c} / WAVE_CYCLES" for c in frac_names)
+                 + " |", "|---|---|" + "---|" * (len(names) + len(frac_names)), *table]
         open(args.md, "w").write("\n".join(lines) + "\n")
         print(f"wrote {args.md}")
 
