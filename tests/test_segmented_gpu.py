@@ -71,9 +71,10 @@ def test_segmented_forward_matches_unsegmented():
     assert rel_l2(o, o2) <= 1e-2 and rel_l2(hT, hT2) <= 1e-2, (rel_l2(o, o2), rel_l2(hT, hT2))
 
 
-def test_nsgdn_segmented():
+@pytest.mark.parametrize("with_states", [True, False])
+def test_nsgdn_segmented(with_states):
     B, T, H, K, V = 1, 4096, 2, 128, 128
-    banner(f"segmented nsgdn B={B} T={T} H={H} K={K} V={V} bf16")
+    banner(f"segmented nsgdn B={B} T={T} H={H} K={K} V={V} bf16, S0 and dS given: {with_states}")
     gen = torch.Generator().manual_seed(46)
     r = lambda *s: torch.randn(*s, generator=gen)
     bf = torch.bfloat16
@@ -85,7 +86,9 @@ def test_nsgdn_segmented():
     la = torch.nn.functional.logsigmoid(r(B, T, H) + 4)
     dy = r(B, T, H, V).to(bf).float()
     S0, dS = 0.1 * r(B, H, K, V), 0.1 * r(B, H, K, V)
-    d = lambda t, dt=bf: t.to("cuda", dt)
+    if not with_states:  # without them the prefix starts from zero and the reverse scan from a zero gradient
+        S0, dS = None, None
+    d = lambda t, dt=bf: None if t is None else t.to("cuda", dt)
     with _lib.StageTimer() as st:
         y, hT, stash = ops.nsgdn_chunk_fwd(d(q), d(k), d(u), d(v), d(la, torch.float32), d(S0, torch.float32), 1.0)
         grads = ops.nsgdn_chunk_bwd(d(q), d(k), d(u), d(v), d(la, torch.float32), d(S0, torch.float32), d(dy),
@@ -95,7 +98,8 @@ def test_nsgdn_segmented():
     y_r, hT_r = NSO.chunk_fwd(q, k, u, v, la, 1.0, S0)
     ref = NSO.recurrent_bwd(q, k, u, v, la, dy, 1.0, S0, dS)
     errs = {"y": rel_l2(y, y_r), "hT": rel_l2(hT, hT_r)}
-    errs.update({n: rel_l2(g, rr) for n, g, rr in zip(("dq", "dk", "du", "dv", "dla", "dh0"), grads, ref)})
+    errs.update({n: rel_l2(g, rr) for n, g, rr in zip(("dq", "dk", "du", "dv", "dla", "dh0"), grads, ref)
+                 if rr is not None})  # (the oracle gives no dh0 without an initial state)
     print("[segmented nsgdn] rel-L2 " + ", ".join(f"{n} {e:.2e}" for n, e in errs.items()), flush=True)
     assert all(e <= 1e-2 for e in errs.values()), errs
 
