@@ -27,6 +27,10 @@ Also reported in the same line:
   long_context  forward + backward at B=1, T=16384, H=16, K=128, V=256, nonzero initial state, slow decay
                 (g = logsigmoid(N(0,1) + 6)), the training pair with dh0; tokens/s and % of the bf16 MFMA peak at
                 3 * F_fwd(128, 256) per token-head;
+  nsgdn         the separate-write-key training pair (nsgdn_chunk_fwd + nsgdn_chunk_bwd: u != beta k, the n-step
+                family's write vectors) at archbench's nsgdn layer shape (head_dim 128, expand_v 2, 4 heads,
+                seq_len 1024: K=128, V=256, H=4, T=1024) with B=64; tokens/s and % of the bf16 MFMA peak at
+                3 * F_fwd(128, 256) per token-head;
   decode_step   one recurrent decode step at B=256, H=16, K=V=128 with the fp32 state updated in place
                 (HBM GB/s against 8 TB/s);
   short_conv    the causal depthwise conv (kernel 4) + SiLU in front of the op at the layer's shape, B=8, T=4096,
@@ -194,7 +198,7 @@ def main() -> int:
                          "FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     only = set(args.only.split(","))
-    known = {"all", "train", "fwd", "long", "decode", "conv", "norm", "ce"}
+    known = {"all", "train", "fwd", "long", "nsgdn", "decode", "conv", "norm", "ce"}
     if not only <= known:
         ap.error(f"--only: unknown workload(s) {sorted(only - known)}; choose from {sorted(known)}")
     want = lambda w: "all" in only or w in only
@@ -322,6 +326,35 @@ def main() -> int:
             f"{out['long_context']['mfma_frac'] * 100:.1f}% of bf16 MFMA peak; "
             f"stages {out['long_context']['stages_ms']}")
         del x
+        torch.cuda.empty_cache()
+
+    if want("nsgdn"):
+        B, T, H, K, V = 64, 1024, 4, 128, 256
+        log(f"nsgdn training pair B={B} T={T} H={H} K={K} V={V} bf16 (separate write keys)")
+        x = make_inputs(B, T, H, K, V, seed=0, with_do=True)
+        gen = torch.Generator().manual_seed(1)
+        u = (x.beta[..., None] * x.k + 0.05 * torch.randn(B, T, H, K, generator=gen)).to(dev, torch.bfloat16)
+        q, k, v, dy = (t.to(dev, torch.bfloat16) for t in (x.q, x.k, x.v, x.do))
+        la = x.g.to(dev)
+        sc = K ** -0.5
+
+        def nsgdn_step():
+            _, _, stash = ops.nsgdn_chunk_fwd(q, k, u, v, la, None, sc)
+            ops.nsgdn_chunk_bwd(q, k, u, v, la, None, dy, None, stash, sc)
+
+        n = max(5, min(args.steps, 20))
+        sec, sec_ev = timed_loop(nsgdn_step, n, 2, torch, events=True)
+        with _lib.StageTimer() as st:
+            for _ in range(3):
+                nsgdn_step()
+        fl = 3 * f_fwd(K, V) * B * T * H
+        out["nsgdn"] = {"workload": "nsgdn_chunk_fwd_bwd", "B": B, "T": T, "H": H, "K": K, "V": V, "steps": n,
+                        "ms_per_step": round(sec * 1e3, 4), "tokens_per_s": round(B * T / sec, 1),
+                        "mfma_frac": round(fl / sec_ev / MFMA_BF16_PEAK, 4),
+                        "stages_ms": {k_: round(v_[0] / v_[1], 4) for k_, v_ in st.result.items()}}
+        log(f"nsgdn {sec * 1e3:.3f} ms/step, {B * T / sec:.3e} tokens/s, "
+            f"{out['nsgdn']['mfma_frac'] * 100:.1f}% of bf16 MFMA peak; stages {out['nsgdn']['stages_ms']}")
+        del x, q, k, u, v, dy, la
         torch.cuda.empty_cache()
 
     if want("decode"):
