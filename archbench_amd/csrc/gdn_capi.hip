@@ -4,6 +4,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "../../include/gdn_mi355x.h"
@@ -147,7 +148,9 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
 }
 
 
-// ---- per-stage event timing (diagnostic; off unless gdn_profile_enable(1) was called on this thread) ----
+// ---- per-stage event timing (diagnostic; off unless gdn_profile_enable(1) was called) ----
+// Process-wide, so that launches from other host threads count too (PyTorch runs a backward pass on its
+// autograd thread): one mutex guards the record, taken only while profiling is on.
 enum Stage {
   ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_FACTORS, ST_CONV_FWD,
   ST_CONV_BWD, ST_NORM_FWD, ST_NORM_BWD, ST_GATES_FWD, ST_GATES_BWD, ST_L2_FWD, ST_L2_BWD, ST_CE, ST_PREFIX,
@@ -159,15 +162,16 @@ static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state",
                                             "bwd_local"};
 struct ProfRec { int stage; hipEvent_t a, b; };
 struct Prof {
-  bool on = false;
+  std::atomic<bool> on{false};
+  std::mutex mu;
   ProfRec rec[4096];
   int n = 0;
   hipEvent_t pool[8192];
   int pool_n = 0, pool_used = 0;
 };
-static thread_local Prof g_prof;
+static Prof g_prof;
 
-static hipEvent_t prof_event() {
+static hipEvent_t prof_event() {  // with g_prof.mu held
   if (g_prof.pool_used < g_prof.pool_n) return g_prof.pool[g_prof.pool_used++];
   hipEvent_t e = nullptr;
   if (g_prof.pool_n < 8192 && hipEventCreate(&e) == hipSuccess) {
@@ -180,7 +184,9 @@ static hipEvent_t prof_event() {
 // Runs `launch` and, when profiling is on, brackets it with events on `st`.
 template <typename F>
 static hipError_t timed(int stage, hipStream_t st, F&& launch) {
-  if (!g_prof.on || g_prof.n >= 4096) return launch();
+  if (!g_prof.on.load(std::memory_order_relaxed)) return launch();
+  std::lock_guard<std::mutex> lock(g_prof.mu);
+  if (!g_prof.on.load(std::memory_order_relaxed) || g_prof.n >= 4096) return launch();
   ProfRec r{stage, prof_event(), prof_event()};
   if (r.a) (void)hipEventRecord(r.a, st);
   const hipError_t e = launch();
@@ -222,7 +228,8 @@ extern "C" {
 int gdn_version(void) { return 100; }
 
 int gdn_profile_enable(int on) {
-  g_prof.on = on != 0;
+  std::lock_guard<std::mutex> lock(g_prof.mu);
+  g_prof.on.store(on != 0, std::memory_order_relaxed);
   g_prof.n = 0;
   g_prof.pool_used = 0;
   return GDN_OK;
@@ -235,6 +242,7 @@ int gdn_profile_read(double* ms_sum, int* launches, int n_stages) {
     ms_sum[i] = 0.0;
     launches[i] = 0;
   }
+  std::lock_guard<std::mutex> lock(g_prof.mu);
   for (int i = 0; i < g_prof.n; ++i) {
     const ProfRec& r = g_prof.rec[i];
     if (hipEventSynchronize(r.b) != hipSuccess) return fail(GDN_ERR_LAUNCH, "event synchronize failed");

@@ -10,7 +10,12 @@ g = -exp(A_log) softplus(a + dt_bias) (natural-log decay), fp32 state.  The outp
 
 The token mixing itself is always the HIP chunk op (training / prefill) or the HIP decode step (T = 1 with
 a recurrent state, no grad).  The short causal convolutions (with the q / k normalisation fused in), the gate
-functions and the output gated RMSNorm run on their own HIP kernels; the projections are PyTorch linears.
+functions and the output gated RMSNorm run on their own HIP kernels; the projections are PyTorch linears.  The
+six input projections (q, k, v, a, b and the gate) keep fla's separate ``nn.Linear`` parameters (names, shapes
+and initialisation, so checkpoints and the reference's init rules carry over) but run as one GEMM against their
+concatenated weights: one cast of the input under autocast instead of six, one input-gradient GEMM instead of
+six and their sum, and a weight-gradient GEMM wide enough to fill the GPU (the 4-wide a and b weight gradients,
+a 4 x hidden output reduced over every token, leave it nearly idle when computed apart).
 """
 
 from __future__ import annotations
@@ -93,6 +98,14 @@ class GatedDeltaNet(nn.Module):
         self.o_norm = GatedRMSNorm(self.head_v_dim, norm_eps)
         self.o_proj = nn.Linear(self.value_dim, hidden_size, bias=False)
 
+    def input_projections(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, ...]:
+        """(q, k, v, a, b[, gate]) = the six linears of ``hidden_states``, computed as one GEMM."""
+        mods = [self.q_proj, self.k_proj, self.v_proj, self.a_proj, self.b_proj]
+        if self.use_gate:
+            mods.append(self.g_proj)
+        y = F.linear(hidden_states, torch.cat([m.weight for m in mods], 0))
+        return torch.split(y, [m.out_features for m in mods], dim=-1)
+
     def forward(self, hidden_states: torch.Tensor, attention_mask: torch.Tensor | None = None,
                 past_key_values: dict | None = None, use_cache: bool = False, output_attentions: bool = False,
                 **kwargs):
@@ -106,7 +119,7 @@ class GatedDeltaNet(nn.Module):
         H, DK, DV = self.num_heads, self.head_k_dim, self.head_v_dim
         entry = None if past_key_values is None else past_key_values.get(self.layer_idx)
         conv_in = entry["conv_state"] if entry is not None else (None, None, None)
-        q, k, v = self.q_proj(hidden_states), self.k_proj(hidden_states), self.v_proj(hidden_states)
+        q, k, v, a, b, *gp = self.input_projections(hidden_states)
         conv_out = (None, None, None)
         if self.use_short_conv:
             (q, cq), (k, ck), (v, cv) = (self.q_conv1d(q, conv_in[0]), self.k_conv1d(k, conv_in[1]),
@@ -114,10 +127,10 @@ class GatedDeltaNet(nn.Module):
             conv_out = (cq, ck, cv)
         else:
             q, k, v = F.silu(q), F.silu(k), F.silu(v)
-        q, k, v = q.view(B, T, H, DK), k.view(B, T, H, DK), v.view(B, T, H, DV)
+        q, k, v = q.reshape(B, T, H, DK), k.reshape(B, T, H, DK), v.reshape(B, T, H, DV)
         # g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b) (x2 with negative eigenvalues), one HIP pass
-        g, beta = ops.gdn_gates(self.a_proj(hidden_states), self.b_proj(hidden_states), self.A_log, self.dt_bias,
-                                None, 2.0 if self.allow_neg_eigval else 1.0, float("-inf"))
+        g, beta = ops.gdn_gates(a, b, self.A_log, self.dt_bias, None, 2.0 if self.allow_neg_eigval else 1.0,
+                                float("-inf"))
         state = entry["recurrent_state"] if entry is not None else None
         # The op runs in the dtype the projections produced, as fla's layer passes them on: bf16 under the
         # trainer's bf16 autocast (archbench/trainer.py:66), even though the block hands the mixer fp32 hidden
@@ -138,6 +151,6 @@ class GatedDeltaNet(nn.Module):
             if past_key_values is None:
                 past_key_values = {}
             past_key_values[self.layer_idx] = {"recurrent_state": new_state, "conv_state": conv_out}
-        gate = self.g_proj(hidden_states).view(B, T, H, DV) if self.use_gate else None
+        gate = gp[0].reshape(B, T, H, DV) if self.use_gate else None
         o = self.o_norm(o, gate)
         return self.o_proj(o.reshape(B, T, -1)), None, past_key_values

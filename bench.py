@@ -31,6 +31,11 @@ Also reported in the same line:
                 family's write vectors) at archbench's nsgdn layer shape (head_dim 128, expand_v 2, 4 heads,
                 seq_len 1024: K=128, V=256, H=4, T=1024) with B=64; tokens/s and % of the bf16 MFMA peak at
                 3 * F_fwd(128, 256) per token-head;
+  gdn_layer     the drop-in `gdn` mixer as archbench's model builds it for configs/65m/gdn.yaml (d_model 512,
+                4 heads, head_dim 128, expand_v 2, gate, short conv 4), fed fp32 hidden states under bf16 autocast as
+                the trainer runs Block.forward, at B=64, T=1024: forward + backward of the whole layer (projections
+                on hipBLASLt, conv, gates, the op, gated RMSNorm, output projection), tokens/s, with the library's
+                kernels' share of the step;
   decode_step   one recurrent decode step at B=256, H=16, K=V=128 with the fp32 state updated in place
                 (HBM GB/s against 8 TB/s);
   short_conv    the causal depthwise conv (kernel 4) + SiLU in front of the op at the layer's shape, B=8, T=4096,
@@ -198,7 +203,7 @@ def main() -> int:
                          "FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     only = set(args.only.split(","))
-    known = {"all", "train", "fwd", "long", "nsgdn", "decode", "conv", "norm", "ce"}
+    known = {"all", "train", "fwd", "long", "nsgdn", "layer", "decode", "conv", "norm", "ce"}
     if not only <= known:
         ap.error(f"--only: unknown workload(s) {sorted(only - known)}; choose from {sorted(known)}")
     want = lambda w: "all" in only or w in only
@@ -355,6 +360,38 @@ def main() -> int:
         log(f"nsgdn {sec * 1e3:.3f} ms/step, {B * T / sec:.3e} tokens/s, "
             f"{out['nsgdn']['mfma_frac'] * 100:.1f}% of bf16 MFMA peak; stages {out['nsgdn']['stages_ms']}")
         del x, q, k, u, v, dy, la
+        torch.cuda.empty_cache()
+
+    if want("layer"):
+        from archbench_amd import layers
+
+        B, T, D, nh = 64, 1024, 512, 4
+        log(f"gdn layer (configs/65m/gdn.yaml: d_model {D}, {nh} heads, K=128, V=256) B={B} T={T}, fp32 input "
+            f"under bf16 autocast, forward + backward")
+        torch.manual_seed(0)
+        m = layers.build_mixer("gdn", D, 0, 10, num_heads=nh, head_dim=128, expand_v=2.0, use_gate=True,
+                               use_short_conv=True, conv_size=4).to(dev)
+        xin = torch.randn(B, T, D, device=dev, generator=torch.Generator(dev).manual_seed(1)).requires_grad_()
+        gy = torch.randn(B, T, D, device=dev, generator=torch.Generator(dev).manual_seed(2))
+
+        def layer_step():
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                y = m(xin)
+            y.backward(gy)
+
+        n = max(5, min(args.steps, 20))
+        sec = timed_loop(layer_step, n, 2, torch)
+        with _lib.StageTimer() as st:
+            for _ in range(3):
+                layer_step()
+        lib_ms = sum(v_[0] for v_ in st.result.values()) / 3
+        out["gdn_layer"] = {"workload": "gdn mixer fwd+bwd (configs/65m/gdn.yaml)", "B": B, "T": T, "d_model": D,
+                            "heads": nh, "K": 128, "V": 256, "steps": n, "ms_per_step": round(sec * 1e3, 4),
+                            "tokens_per_s": round(B * T / sec, 1), "library_kernels_ms": round(lib_ms, 4),
+                            "stages_ms": {k_: round(v_[0] / 3, 4) for k_, v_ in st.result.items()}}
+        log(f"gdn layer {sec * 1e3:.3f} ms/step, {B * T / sec:.3e} tokens/s; library kernels {lib_ms:.3f} ms "
+            f"per step {out['gdn_layer']['stages_ms']}")
+        del m, xin, gy
         torch.cuda.empty_cache()
 
     if want("decode"):

@@ -195,8 +195,8 @@ int gdn_cross_entropy_fwd_bwd(void* logits, const int64_t* target, float* loss, 
                               int64_t N, int V, int64_t ld, int64_t ignore_index, int dtype, void* stream);
 
 /* Per-stage kernel timing (diagnostic; no counterpart in the reference, which times whole phases with CUDA
- * events in archbench/logger.py:57-81).  While enabled on the calling thread, every kernel the calls above
- * enqueue is bracketed by hipEvents on the same stream.  gdn_profile_read synchronises on those events and
+ * events in archbench/logger.py:57-81).  While enabled (process-wide: launches from any host thread count), every
+ * kernel the calls above enqueue is bracketed by hipEvents on the same stream.  gdn_profile_read synchronises on those events and
  * returns, per stage, the summed milliseconds and the number of launches (arrays of at least
  * GDN_PROFILE_STAGES entries), then clears the record.  Stage names: gdn_profile_stage_name. */
 #define GDN_PROFILE_STAGES 19

@@ -115,3 +115,31 @@ def test_nsgdn_token_scan_choices_warn():
             layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=64, scan_impl=impl)
     with pytest.raises(ValueError):
         layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=64, scan_impl="cuda")
+
+
+@pytest.mark.parametrize("use_gate", [True, False])
+def test_fused_input_projections_equal_the_separate_linears(use_gate):
+    """The gdn mixer runs its six input linears as one GEMM on the concatenated weights: outputs and every
+    weight and input gradient equal those of the separate nn.Linear modules (fp64 on the CPU)."""
+    torch.manual_seed(0)
+    m = layers.build_mixer("gdn", 64, 0, 2, num_heads=2, head_dim=16, expand_v=2.0, use_gate=use_gate).double()
+    mods = [m.layer.q_proj, m.layer.k_proj, m.layer.v_proj, m.layer.a_proj, m.layer.b_proj]
+    if use_gate:
+        mods.append(m.layer.g_proj)
+    x = torch.randn(2, 5, 64, dtype=torch.float64, requires_grad=True)
+    outs = m.layer.input_projections(x)
+    assert [o.shape[-1] for o in outs] == [md.out_features for md in mods]
+    ws = [torch.randn(o.shape, dtype=torch.float64) for o in outs]
+    sum((o * w).sum() for o, w in zip(outs, ws)).backward()
+    g_fused = [md.weight.grad.clone() for md in mods]
+    gx = x.grad.clone()
+    for md in mods:
+        md.weight.grad = None
+    x.grad = None
+    ref = [md(x) for md in mods]
+    for o, r in zip(outs, ref):
+        torch.testing.assert_close(o, r, rtol=0, atol=1e-12)
+    sum((r * w).sum() for r, w in zip(ref, ws)).backward()
+    for gf, md in zip(g_fused, mods):
+        torch.testing.assert_close(gf, md.weight.grad, rtol=0, atol=1e-12)
+    torch.testing.assert_close(gx, x.grad, rtol=0, atol=1e-12)
