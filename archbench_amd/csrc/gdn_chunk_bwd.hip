@@ -492,9 +492,11 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rb + acc_row(i, l);
       // e = exp(G_r - G_c) on and below the diagonal, computed unconditionally (min(., 0) keeps it finite) and
-      // masked by a select: no branch around the exp.  With u = dA e (strictly below) and w = dP s e:
-      //   D = u beta_r,  dPm = w,  dbeta_A += u (K U^T),  z = dP P + dA A = w (Q U^T) + D (K U^T)
-      const float e = r >= cc ? __expf(fminf(Grow[i] - Gc, 0.f)) : 0.f;
+      // masked by a select: no branch around the exp (written as `cond ? exp : 0` it compiled into an exec-mask
+      // branch per element, each waiting for every LDS read in flight).  With u = dA e (strictly below) and
+      // w = dP s e:  D = u beta_r,  dPm = w,  dbeta_A += u (K U^T),  z = dP P + dA A = w (Q U^T) + D (K U^T)
+      const float ev = __expf(fminf(Grow[i] - Gc, 0.f));
+      const float e = r >= cc ? ev : 0.f;
       const float uu = r > cc ? -aDA[j][i] * e : 0.f;
       const float wv = aP[j][i] * (scale * e);
       const float Dv = uu * bet[i];

@@ -183,8 +183,15 @@ struct RegTile {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int idx = tid + i * NTH, row = idx / VPR, c = (idx - row * VPR) * E;
-      if constexpr (BUF) *reinterpret_cast<uint4*>(s + row * sld + c) = r[i];
-      else *reinterpret_cast<uint4*>(s + row * sld + c) = ((ok >> i) & 1u) ? r[i] : make_uint4(0, 0, 0, 0);
+      if constexpr (BUF) {
+        *reinterpret_cast<uint4*>(s + row * sld + c) = r[i];
+      } else {
+        // rows past the end zeroed by an AND with an all-ones / all-zeros mask; the empty asm hides that the mask
+        // comes from a condition (as a select it compiled into an exec-mask branch per vector)
+        uint32_t m = 0u - ((ok >> i) & 1u);
+        asm("" : "+v"(m));
+        *reinterpret_cast<uint4*>(s + row * sld + c) = make_uint4(r[i].x & m, r[i].y & m, r[i].z & m, r[i].w & m);
+      }
     }
   }
   __device__ __forceinline__ void load(const T* g, int64_t gld, int valid) { load(g, gld, valid, threadIdx.x); }
