@@ -113,6 +113,11 @@ int device_cu_count() {
   return cus;
 }
 
+bool narrow_sweep_blocks(const ChunkArgs& a, int blocks_per_head) {
+  // only when the narrow workgroups all run at once, one per CU (two per CU were measured slower than one wide)
+  return (int64_t)blocks_per_head * a.B * a.H <= (int64_t)device_cu_count();
+}
+
 bool chunk_shape_supported(int K, int V, int dtype) {
   const bool v_ok = V == 64 || V == 128 || V == 256;
   if (dtype == DT_BF16) return (K == 64 || K == 128) && v_ok;

@@ -34,12 +34,13 @@
 
 namespace gdn {
 
-// Eight waves, two per SIMD: waves w and w + 4 share the 16-column slab 16 (w & 3) of dS.  Half hf = w >> 2
-// holds rows 64 hf .. of dS (K = 128; rows K/2 hf .. in general) and computes dR and Z for the chunk's token
-// rows 32 hf .. 32 hf + 31.  Per chunk the halves swap through LDS: the partial K dS of the other half's token
-// rows (fp32), then the dR fragments, then the Z fragments (16 bytes per lane each).
-constexpr int SW = 2 * NWAVE;  // waves of the reverse sweep
-constexpr int STH = 64 * SW;
+// Two waves per 16-column slab of the V block (BV / 16 slabs: eight waves for BV = 64, four for BV = 32): waves
+// w and w + NSL share the slab 16 (w % NSL) of dS.  Half hf = w / NSL holds rows 64 hf .. of dS (K = 128; rows
+// K/2 hf .. in general) and computes dR and Z for the chunk's token rows 32 hf .. 32 hf + 31.  Per chunk the
+// halves swap through LDS: the partial K dS of the other half's token rows (fp32), then the dR fragments, then
+// the Z fragments (16 bytes per lane each).
+template <int BV>
+constexpr int state_threads() { return 128 * (BV / 16); }
 // the two V-block workgroups of a head read the same q, k, Tm and P (the second from L2): ordinary loads; dS_C and
 // dR are written once, nontemporal
 constexpr bool STATE_NT_LOAD = false, STATE_NT_STORE = true;
@@ -48,7 +49,7 @@ constexpr bool INTRA_NT = true;  // every read and write of the gradient kernel 
 // STORE: write dS_C and dY for every chunk (the gradient kernel reads them); without it (the local pass of a
 // segmented sweep) only dh0 is written.
 template <typename T, int K, int BV, bool SEPU, bool STORE>
-__global__ __launch_bounds__(STH) void bwd_state_kernel(
+__global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_per_eu(2))) void bwd_state_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u, const T* __restrict__ dout,
     const float* __restrict__ beta,
     const T* __restrict__ gTm, const T* __restrict__ gP, const float* __restrict__ gGc,
@@ -58,7 +59,8 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
   constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
   constexpr int NKH = K / 32;     // row tiles of dS per half
   constexpr int NSH = K / 64;     // 32-row fragments of dS per half
-  static_assert(BV / 16 / NWAVE == 1, "each wave pair owns one 16-column slab of dS");
+  constexpr int NSL = BV / 16, SW = 2 * NSL, STH = 64 * SW;  // slabs, waves, threads
+  static_assert(NSL == 2 || NSL == 4, "a wave pair per 16-column slab, two or four slabs");
   using F = typename Frag<T>::type;
   __shared__ __attribute__((aligned(16))) T sK[CH * LK];
   __shared__ __attribute__((aligned(16))) T sU_[SEPU ? CH * LK : 8];
@@ -86,7 +88,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
   const int64_t dhT_base = (STORE ? (int64_t)bh : (int64_t)(b / ns) * H + h) * K * V;
   const int v0 = vb * BV;
   const int w = wave_id(), l = lane_id();
-  const int ws = w & (NWAVE - 1), hf = w >> 2;  // column slab; half of dS's rows and of the chunk's tokens
+  const int ws = w & (NSL - 1), hf = w / NSL;  // column slab; half of dS's rows and of the chunk's tokens
   const int c0 = 16 * ws;
   const int ncb = V / 16, cb = vb * (BV / 16) + ws;  // fragment-layout column block of the slab
   const int k0 = (K / 2) * hf;                       // first dS row of this half
@@ -181,7 +183,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     for (int j = 0; j < 2; ++j) {
       const int rt_ = 2 * hf + j;
       const f32x4 mine = hf ? kd[2 + j] : kd[j];
-      const f32x4 other = xKd[w ^ NWAVE][j][l];
+      const f32x4 other = xKd[w ^ NSL][j][l];
 #pragma unroll
       for (int i = 0; i < 4; ++i) dR[j][i] = __expf(GC - sG[16 * rt_ + acc_row(i)]) * (mine[i] + other[i]);
 #pragma unroll
@@ -192,7 +194,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     xR[w][l] = dRmine;
     __syncthreads();
     if (c > 0) prefetch2(c - 1);
-    const F dRother = xR[w ^ NWAVE][l];
+    const F dRother = xR[w ^ NSL][l];
     const F dR0 = hf ? dRother : dRmine, dR1 = hf ? dRmine : dRother;
     f32x4 Z[2];
 #pragma unroll
@@ -214,7 +216,7 @@ __global__ __launch_bounds__(STH) void bwd_state_kernel(
     const F Zmine = frag_acc2<T>(Z[0], Z[1]);
     xZ[w][l] = Zmine;
     __syncthreads();
-    const F Zother = xZ[w ^ NWAVE][l];
+    const F Zother = xZ[w ^ NSL][l];
     const F Zb0 = hf ? Zother : Zmine, Zb1 = hf ? Zmine : Zother;
     // this half's rows of dS <- gamma_C dS + s Q^T (gamma dO) - K^T Z
     const float gC = __expf(GC);
@@ -655,12 +657,11 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------------------
-template <typename T, int K, bool SEPU>
-static hipError_t bwd_state_k(const ChunkArgs& a, bool local) {
-  constexpr int BV = 64;
+template <typename T, int K, bool SEPU, int BV>
+static hipError_t bwd_state_bv(const ChunkArgs& a, bool local) {
   dim3 grid(a.V / BV * a.B * a.H);
   auto go = [&](auto kern) {
-    kern<<<grid, STH, 0, a.stream>>>(
+    kern<<<grid, state_threads<BV>(), 0, a.stream>>>(
         static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
         static_cast<const T*>(a.dout), a.beta, static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P),
         a.ws.Gc, a.dhT, a.dh0, static_cast<T*>(a.ws.dhs), static_cast<T*>(a.ws.dYs), a.T, a.H, a.V, a.NT,
@@ -668,6 +669,14 @@ static hipError_t bwd_state_k(const ChunkArgs& a, bool local) {
     return hipGetLastError();
   };
   return local ? go(bwd_state_kernel<T, K, BV, SEPU, false>) : go(bwd_state_kernel<T, K, BV, SEPU, true>);
+}
+
+template <typename T, int K, bool SEPU>
+static hipError_t bwd_state_k(const ChunkArgs& a, bool local) {
+  if constexpr (sizeof(T) == 2 && !SEPU) {
+    if (narrow_sweep_blocks(a, a.V / 32)) return bwd_state_bv<T, K, SEPU, 32>(a, local);
+  }
+  return bwd_state_bv<T, K, SEPU, 64>(a, local);
 }
 
 template <typename T, int K, int V, bool SEPU>

@@ -24,18 +24,18 @@
 
 namespace gdn {
 
-// Eight waves, two per SIMD.  Waves w and w + 4 share the 16-column slab 16 (w & 3) and each holds all of S for
-// it; the chunk's token rows are split between them (half hf = w >> 2 takes rows 32 hf .. 32 hf + 31, i.e. the
-// permuted-k fragment hf of every token-indexed product).  Each half computes K S, Q S, Y, R, P R and O for its
-// rows; the Y and Rd fragments of the other half come through LDS (16 bytes per lane each), and both halves
-// apply the full state update.
-constexpr int FW = 2 * NWAVE;  // waves of the forward sweep
-constexpr int FTH = 64 * FW;
+// Two waves per 16-column slab of the V block (BV / 16 slabs: eight waves for BV = 64, four for BV = 32).  Waves
+// w and w + NSL share the slab 16 (w % NSL) and each holds all of S for it; the chunk's token rows are split
+// between them (half hf = w / NSL takes rows 32 hf .. 32 hf + 31, i.e. the permuted-k fragment hf of every
+// token-indexed product).  Each half computes K S, Q S, Y, R, P R and O for its rows; the Y and Rd fragments of
+// the other half come through LDS (16 bytes per lane each), and both halves apply the full state update.
+template <int BV>
+constexpr int fwd_threads() { return 128 * (BV / 16); }
 constexpr bool FWD_NT_LOAD = true;             // chunk inputs (measured faster with the hint)
 constexpr bool FWD_NT_STORE = true;            // O, and the stashed states and R: written once
 
 template <typename T, int K, int BV, int MODE, bool SEPU>
-__global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
+__global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_eu(2))) void fwd_sweep_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u, const T* __restrict__ v,
     const float* __restrict__ beta,
     const float* __restrict__ h0, const T* __restrict__ gTm, const T* __restrict__ gP,
@@ -44,7 +44,8 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
   constexpr int NKT = K / 16;  // row tiles of the state slab
-  static_assert(BV / 16 / NWAVE == 1, "each wave pair owns one 16-column slab of the state");
+  constexpr int NSL = BV / 16, FW = 2 * NSL, FTH = 64 * FW;  // slabs, waves, threads
+  static_assert(NSL == 2 || NSL == 4, "a wave pair per 16-column slab, two or four slabs");
   constexpr bool OUT = MODE == 0 || MODE == 2;   // O is computed (needs Q and P)
   constexpr bool SAVE = MODE == 1 || MODE == 2;  // per-chunk states and R are written
   using F = typename Frag<T>::type;
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
   const bool use_h0 = h0 && (MODE != 3 || seg == 0);
   const int64_t h0_base = (MODE == 3 ? (int64_t)(b / ns) * H + h : (int64_t)bh) * K * V;
   const int w = wave_id(), l = lane_id();
-  const int ws = w & (NWAVE - 1), hf = w >> 2;        // column slab, token half
+  const int ws = w & (NSL - 1), hf = w / NSL;        // column slab, token half
   const int c0 = 16 * ws;                             // the slab inside the V block
   const int ncb = V / 16, cb = vb * (BV / 16) + ws;  // its fragment-layout column block
   const int tid = threadIdx.x;
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     const F Ymine = frag_acc2<T>(Y[0], Y[1]);
     xY[w][l] = Ymine;
     __syncthreads();
-    const F Yother = xY[w ^ NWAVE][l];
+    const F Yother = xY[w ^ NSL][l];
     const F Yb0 = hf ? Yother : Ymine, Yb1 = hf ? Ymine : Yother;
 
     // R = Tm Y for the half's rows (saved if SAVE); Rd = exp(G_C - G) R; O = s gamma QS + P R staged
@@ -202,10 +203,10 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
     if constexpr (SAVE) store_fragblk<T, FWD_NT_STORE>(wsR + cidx * CH * V, CH, hf, cb, ncb, Rbmine);
     __syncthreads();  // R and Rd fragments of both halves exchanged
     if (c + 1 < NT) prefetch2(c + 1);
-    const F Rdother = xRd[w ^ NWAVE][l];
+    const F Rdother = xRd[w ^ NSL][l];
     const F Rd0 = hf ? Rdother : Rdmine, Rd1 = hf ? Rdmine : Rdother;
     if constexpr (OUT) {
-      const F Rbother = xR[w ^ NWAVE][l];
+      const F Rbother = xR[w ^ NSL][l];
       const F Rb0 = hf ? Rbother : Rbmine, Rb1 = hf ? Rbmine : Rbother;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -250,17 +251,24 @@ __global__ __launch_bounds__(FTH) void fwd_sweep_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------------------
-template <typename T, int K, int MODE, bool SEPU>
-static hipError_t fwd_sweep_k(const ChunkArgs& a) {
-  constexpr int BV = 64;
+template <typename T, int K, int MODE, bool SEPU, int BV>
+static hipError_t fwd_sweep_bv(const ChunkArgs& a) {
   dim3 grid((a.V + (MODE == 3 ? K : 0)) / BV * a.B * a.H);
-  fwd_sweep_kernel<T, K, BV, MODE, SEPU><<<grid, FTH, 0, a.stream>>>(
+  fwd_sweep_kernel<T, K, BV, MODE, SEPU><<<grid, fwd_threads<BV>(), 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
       static_cast<const T*>(a.v), a.beta, a.h0,
       static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P), a.ws.Gc, static_cast<T*>(a.o),
       MODE == 1 ? nullptr : a.hT, a.ws.phi, static_cast<T*>(a.ws.hs), static_cast<T*>(a.ws.Rs), a.T, a.H, a.V,
       a.NT, a.scale, a.ns);
   return hipGetLastError();
+}
+
+template <typename T, int K, int MODE, bool SEPU>
+static hipError_t fwd_sweep_k(const ChunkArgs& a) {
+  if constexpr (sizeof(T) == 2 && !SEPU) {
+    if (narrow_sweep_blocks(a, (a.V + (MODE == 3 ? K : 0)) / 32)) return fwd_sweep_bv<T, K, MODE, SEPU, 32>(a);
+  }
+  return fwd_sweep_bv<T, K, MODE, SEPU, 64>(a);
 }
 
 template <typename T, int K>

@@ -178,6 +178,10 @@ hipError_t launch_ce(const CeArgs& a);
 
 // Compute units of the current device (cached per device; 256 if the query fails).
 int device_cu_count();
+// Whether a state sweep with `blocks_per_head` 32-column blocks per (b, h) runs those narrow blocks (four waves
+// each, one wave per SIMD) rather than 64-wide blocks of eight waves: when the narrow grid still fits on the
+// device in one round, so that the wide grid would leave CUs idle.
+bool narrow_sweep_blocks(const ChunkArgs& a, int blocks_per_head);
 
 hipError_t launch_step(const StepArgs& a);
 hipError_t launch_factors(const ChunkArgs& a);                  // Tm, P, Gc
