@@ -41,12 +41,12 @@ SIGNATURES = {
     "gdn_nsgdn_chunk_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _sz,
                                  _i, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_recurrent_step": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i, _p]),
-    "gdn_short_conv_fwd": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
+    "gdn_short_conv_fwd": (_i, [_p, _i64, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "gdn_short_conv_bwd_ws_bytes": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
-    "gdn_short_conv_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _i, _p]),
-    "gdn_gated_rmsnorm_fwd": (_i, [_p, _p, _p, _p, _i64, _i, _f, _i, _p]),
+    "gdn_short_conv_bwd": (_i, [_p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _i, _p]),
+    "gdn_gated_rmsnorm_fwd": (_i, [_p, _p, _i64, _i, _p, _p, _i64, _i, _f, _i, _p]),
     "gdn_gated_rmsnorm_bwd_ws_bytes": (_i, [_i64, _i, ctypes.POINTER(_sz)]),
-    "gdn_gated_rmsnorm_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i, _f, _i, _p]),
+    "gdn_gated_rmsnorm_bwd": (_i, [_p, _p, _i64, _i, _p, _p, _p, _p, _p, _p, _sz, _i64, _i, _f, _i, _p]),
     "gdn_l2norm_fwd": (_i, [_p, _p, _i64, _i, _f, _f, _i, _p]),
     "gdn_l2norm_bwd": (_i, [_p, _p, _p, _i64, _i, _f, _f, _i, _p]),
     "gdn_gates_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i, _f, _f, _i, _p]),

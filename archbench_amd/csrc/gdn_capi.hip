@@ -581,22 +581,27 @@ int gdn_short_conv_bwd_ws_bytes(int B, int T, int D, int W, size_t* bytes) {
   return GDN_OK;
 }
 
-static int conv_check(int B, int T, int D, int W, int norm_group, int dtype) {
+static int conv_check(int B, int T, int D, int64_t ldx, int W, int norm_group, int dtype) {
   if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
   if (B < 0 || T < 0 || D <= 0 || W <= 0 || norm_group < 0)
     return fail(GDN_ERR_ARG, "invalid sizes B=%d T=%d D=%d W=%d norm_group=%d", B, T, D, W, norm_group);
-  if ((int64_t)T * D * (dtype == DT_BF16 ? 2 : 4) >= ((int64_t)1 << 31))
-    return fail(GDN_ERR_ARG, "T * D = %lld too large for the conv backward's 32-bit row offsets", (long long)T * D);
   if (!conv_shape_supported(D, W, norm_group))
     return fail(GDN_ERR_SHAPE, "short conv not compiled for D=%d W=%d norm_group=%d (D %% 4 == 0, W = 4, "
                 "norm_group in {0, 64, 128, 256} dividing D)", D, W, norm_group);
+  // each lane reads 4 consecutive channels of a token row: rows start on 4-channel boundaries
+  if (ldx < D || ldx % 4 != 0)
+    return fail(GDN_ERR_ARG, "ldx = %lld must be >= D = %d and a multiple of 4", (long long)ldx, D);
+  if ((int64_t)T * ldx * (dtype == DT_BF16 ? 2 : 4) >= ((int64_t)1 << 31))
+    return fail(GDN_ERR_ARG, "T * ldx = %lld too large for the conv backward's 32-bit row offsets",
+                (long long)T * ldx);
   return GDN_OK;
 }
 
-int gdn_short_conv_fwd(const void* x, const float* w, const float* bias, const void* state_in, void* y,
+int gdn_short_conv_fwd(const void* x, int64_t ldx, const float* w, const float* bias, const void* state_in, void* y,
                        void* state_out, int B, int T, int D, int W, int norm_group, int dtype, void* stream) {
   g_err[0] = 0;
-  if (int e = conv_check(B, T, D, W, norm_group, dtype)) return e;
+  if (ldx == 0) ldx = D;
+  if (int e = conv_check(B, T, D, ldx, W, norm_group, dtype)) return e;
   if (B == 0) return GDN_OK;
   if (T == 0) {
     if (state_out && state_out != state_in) {
@@ -611,18 +616,19 @@ int gdn_short_conv_fwd(const void* x, const float* w, const float* bias, const v
   if (misaligned(x, w, bias, state_in, y, state_out)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   ConvArgs a{};
   a.x = x; a.w = w; a.bias = bias; a.state_in = state_in; a.y = y; a.state_out = state_out;
-  a.B = B; a.T = T; a.D = D; a.norm_group = norm_group; a.dtype = dtype;
+  a.B = B; a.T = T; a.D = D; a.ldx = ldx; a.norm_group = norm_group; a.dtype = dtype;
   a.stream = static_cast<hipStream_t>(stream);
   const hipError_t e = timed(ST_CONV_FWD, a.stream, [&] { return launch_conv(a, false); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "short conv forward launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }
 
-int gdn_short_conv_bwd(const void* x, const float* w, const float* bias, const void* state_in, const void* dy,
-                       void* dx, float* dw, float* dbias, void* dstate_in, void* ws, size_t ws_bytes, int B, int T,
-                       int D, int W, int norm_group, int dtype, void* stream) {
+int gdn_short_conv_bwd(const void* x, int64_t ldx, const float* w, const float* bias, const void* state_in,
+                       const void* dy, void* dx, float* dw, float* dbias, void* dstate_in, void* ws, size_t ws_bytes,
+                       int B, int T, int D, int W, int norm_group, int dtype, void* stream) {
   g_err[0] = 0;
-  if (int e = conv_check(B, T, D, W, norm_group, dtype)) return e;
+  if (ldx == 0) ldx = D;
+  if (int e = conv_check(B, T, D, ldx, W, norm_group, dtype)) return e;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (B == 0 || T == 0) {
     hipError_t e = copy_or_zero_bytes(nullptr, dw, (size_t)D * W * 4, st);
@@ -641,7 +647,7 @@ int gdn_short_conv_bwd(const void* x, const float* w, const float* bias, const v
   ConvArgs a{};
   a.x = x; a.w = w; a.bias = bias; a.state_in = state_in; a.dy = dy; a.dx = dx; a.dstate_in = dstate_in;
   a.dw = dw; a.dbias = dbias; a.ws = ws;
-  a.B = B; a.T = T; a.D = D; a.norm_group = norm_group; a.dtype = dtype; a.stream = st;
+  a.B = B; a.T = T; a.D = D; a.ldx = ldx; a.norm_group = norm_group; a.dtype = dtype; a.stream = st;
   const hipError_t e = timed(ST_CONV_BWD, st, [&] { return launch_conv(a, true); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "short conv backward launch: %s", hipGetErrorString(e));
   return GDN_OK;
@@ -654,15 +660,27 @@ static int norm_check(int64_t rows, int dim, float eps, int dtype) {
   return GDN_OK;
 }
 
-int gdn_gated_rmsnorm_fwd(const void* x, const void* gate, const float* weight, void* y, int64_t rows, int dim,
-                          float eps, int dtype, void* stream) {
+// ldg = 0: contiguous gate rows; otherwise lines of gpl rows ldg elements apart (checked here)
+static int gate_layout_check(const void* gate, int64_t ldg, int gpl, int64_t rows, int dim, int dtype) {
+  if (!gate || ldg == 0) return GDN_OK;
+  const int esz = dtype == DT_BF16 ? 2 : 4;
+  if (gpl < 1 || rows % gpl != 0 || ldg < (int64_t)gpl * dim || (ldg * esz) % 16 != 0 || rows >= ((int64_t)1 << 32))
+    return fail(GDN_ERR_ARG, "gate layout: ldg = %lld elements must hold gpl = %d rows of %d (and be a multiple of "
+                "16 bytes), rows = %lld a multiple of gpl", (long long)ldg, gpl, dim, (long long)rows);
+  return GDN_OK;
+}
+
+int gdn_gated_rmsnorm_fwd(const void* x, const void* gate, int64_t ldg, int gpl, const float* weight, void* y,
+                          int64_t rows, int dim, float eps, int dtype, void* stream) {
   g_err[0] = 0;
   if (int e = norm_check(rows, dim, eps, dtype)) return e;
+  if (int e = gate_layout_check(gate, ldg, gpl, rows, dim, dtype)) return e;
   if (rows == 0) return GDN_OK;
   if (!x || !y) return fail(GDN_ERR_ARG, "null input/output pointer");
   if (misaligned(x, gate, y)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   NormArgs a{};
   a.x = x; a.gate = gate; a.w = weight; a.y = y; a.rows = rows; a.DV = dim; a.dtype = dtype; a.eps = eps;
+  a.ldg = ldg; a.gpl = gpl;
   a.stream = static_cast<hipStream_t>(stream);
   const hipError_t e = timed(ST_NORM_FWD, a.stream, [&] { return launch_norm(a, false); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "gated RMSNorm forward launch: %s", hipGetErrorString(e));
@@ -677,11 +695,12 @@ int gdn_gated_rmsnorm_bwd_ws_bytes(int64_t rows, int dim, size_t* bytes) {
   return GDN_OK;
 }
 
-int gdn_gated_rmsnorm_bwd(const void* x, const void* gate, const float* weight, const void* dy, void* dx,
-                          void* dgate, float* dweight, void* ws, size_t ws_bytes, int64_t rows, int dim, float eps,
-                          int dtype, void* stream) {
+int gdn_gated_rmsnorm_bwd(const void* x, const void* gate, int64_t ldg, int gpl, const float* weight,
+                          const void* dy, void* dx, void* dgate, float* dweight, void* ws, size_t ws_bytes,
+                          int64_t rows, int dim, float eps, int dtype, void* stream) {
   g_err[0] = 0;
   if (int e = norm_check(rows, dim, eps, dtype)) return e;
+  if (int e = gate_layout_check(gate, ldg, gpl, rows, dim, dtype)) return e;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (rows == 0) {
     if (copy_or_zero_bytes(nullptr, dweight, (size_t)dim * 4, st) != hipSuccess)
@@ -695,7 +714,7 @@ int gdn_gated_rmsnorm_bwd(const void* x, const void* gate, const float* weight, 
     return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
   NormArgs a{};
   a.x = x; a.gate = gate; a.w = weight; a.dy = dy; a.dx = dx; a.dgate = dgate; a.dw = dweight; a.ws = ws;
-  a.rows = rows; a.DV = dim; a.dtype = dtype; a.eps = eps; a.stream = st;
+  a.rows = rows; a.DV = dim; a.dtype = dtype; a.eps = eps; a.ldg = ldg; a.gpl = gpl; a.stream = st;
   const hipError_t e = timed(ST_NORM_BWD, st, [&] { return launch_norm(a, true); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "gated RMSNorm backward launch: %s", hipGetErrorString(e));
   return GDN_OK;

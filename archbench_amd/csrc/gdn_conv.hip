@@ -88,7 +88,7 @@ __device__ __forceinline__ float group_sum(float s) {
 constexpr float NORM_EPS = 1e-12f;  // F.normalize's eps
 
 template <typename T, int W>
-__device__ __forceinline__ void load_window(const T* xl, const T* state_in, int64_t srow, int D, int t0,
+__device__ __forceinline__ void load_window(const T* xl, const T* state_in, int64_t srow, int64_t ldx, int t0,
                                             float (&win)[W - 1][CONV_CPL]) {
   // inputs at t0 - (W-1) .. t0 - 1; negative positions from the conv state (zero if none)
 #pragma unroll
@@ -96,7 +96,7 @@ __device__ __forceinline__ void load_window(const T* xl, const T* state_in, int6
     const int t = t0 - (W - 1) + i;
     if (t >= 0) {
       Row4<T> r;
-      r.load(xl + (int64_t)t * D);
+      r.load(xl + (int64_t)t * ldx);
       r.get(win[i]);
     } else if (state_in) {
 #pragma unroll
@@ -116,7 +116,8 @@ template <typename T, int W, int NG>
 __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_fwd_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                            const float* __restrict__ bias,
                                                            const T* __restrict__ state_in, T* __restrict__ y,
-                                                           T* __restrict__ state_out, int Tn, int D, int nchunk) {
+                                                           T* __restrict__ state_out, int Tn, int D, int64_t ldx,
+                                                           int nchunk) {
   constexpr int CPL = CONV_CPL, U = CONV_UF;
   const int l = lane_id();
   const int ncg = (D + CONV_WAVES * CONV_CW - 1) / (CONV_WAVES * CONV_CW);
@@ -128,7 +129,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_fwd_kernel(const T*
   const int t0 = ch * CONV_L, t1 = min(Tn, t0 + CONV_L);
   const bool on = c < D;
   const int cc = on ? c : 0;  // clamped: lanes past D compute on channel 0 and store nothing
-  const T* xl = x + (int64_t)b * Tn * D + cc;
+  const T* xl = x + (int64_t)b * Tn * ldx + cc;  // token t of x at xl + t * ldx
   T* yl = y + (int64_t)b * Tn * D + cc;
   const int64_t srow = ((int64_t)b * D + cc) * (W - 1);
   float wk[CPL][W], bk[CPL];
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_fwd_kernel(const T*
     bk[j] = bias ? bias[cc + j] : 0.f;
   }
   float win[W - 1][CPL];
-  load_window<T, W>(xl, state_in, srow, D, t0, win);
+  load_window<T, W>(xl, state_in, srow, ldx, t0, win);
   auto step = [&](int t, const Row4<T>& row) {
     float xt[CPL], yt[CPL];
     row.get(xt);
@@ -170,28 +171,28 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_fwd_kernel(const T*
   if (nfull > 0) {
     Row4<T> buf[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) buf[u].load(xl + (int64_t)(t0 + u) * D);
+    for (int u = 0; u < U; ++u) buf[u].load(xl + (int64_t)(t0 + u) * ldx);
     for (int n = 0; n < nfull; ++n, t += U) {
       Row4<T> cur[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) cur[u] = buf[u];
       const int tn = min(t + U, t1 - U);
 #pragma unroll
-      for (int u = 0; u < U; ++u) buf[u].load(xl + (int64_t)(tn + u) * D);
+      for (int u = 0; u < U; ++u) buf[u].load(xl + (int64_t)(tn + u) * ldx);
 #pragma unroll
       for (int u = 0; u < U; ++u) step(t + u, cur[u]);
     }
   }
   for (; t < t1; ++t) {
     Row4<T> row;
-    row.load(xl + (int64_t)t * D);
+    row.load(xl + (int64_t)t * ldx);
     step(t, row);
   }
   // the last W-1 inputs become the new conv state (written by the chunk that holds the sequence end; for
   // Tn < W-1 part of it still comes from the old state, which must not be the same buffer)
   if (state_out && on && t1 == Tn) {
     float last[W - 1][CPL];
-    load_window<T, W>(xl, state_in, srow, D, Tn, last);
+    load_window<T, W>(xl, state_in, srow, ldx, Tn, last);
 #pragma unroll
     for (int i = 0; i < W - 1; ++i)
 #pragma unroll
@@ -208,7 +209,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
                                                            const T* __restrict__ state_in,
                                                            const T* __restrict__ dy, T* __restrict__ dx,
                                                            T* __restrict__ dstate_in, float* __restrict__ part_out,
-                                                           int Tn, int D, int nchunk) {
+                                                           int Tn, int D, int64_t ldx, int nchunk) {
   constexpr int CPL = CONV_CPL, U = CONV_UB;
   const int l = lane_id();
   const int ncg = (D + CONV_WAVES * CONV_CW - 1) / (CONV_WAVES * CONV_CW);
@@ -220,17 +221,19 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
   const int t0 = ch * CONV_L, t1 = min(Tn, t0 + CONV_L);
   const bool on = c < D;
   const int cc = on ? c : 0;
-  const int64_t off = (int64_t)b * Tn * D + cc;
-  const T* xl = x + off;
+  const T* xl = x + (int64_t)b * Tn * ldx + cc;
   const int64_t srow = ((int64_t)b * D + cc) * (W - 1);
-  // the batch element's [Tn][D] rows of x, dy and dx as buffer resources (uniform base, 32-bit offsets: the
-  // host keeps Tn * D * sizeof(T) under 2 GiB); token t, this lane's channels at byte offset boff(t)
+  // the batch element's rows of x ([Tn] rows ldx apart), dy and dx ([Tn][D]) as buffer resources (uniform base,
+  // 32-bit offsets: the host keeps Tn * ldx * sizeof(T) under 2 GiB); token t, this lane's channels at byte
+  // offset xoff(t) in x and boff(t) in dy and dx
   const int64_t bbase = (int64_t)b * Tn * D;
   const int bbytes = Tn * D * (int)sizeof(T);
-  const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(x + bbase), 0, bbytes, BUF_RSRC_WORD3);
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(x + (int64_t)b * Tn * ldx), 0,
+                                                    (int)(Tn * ldx * (int64_t)sizeof(T)), BUF_RSRC_WORD3);
   const auto rdy = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(dy + bbase), 0, bbytes, BUF_RSRC_WORD3);
   const auto rdx = __builtin_amdgcn_make_buffer_rsrc(dx + bbase, 0, bbytes, BUF_RSRC_WORD3);
   auto boff = [&](int t) { return (t * D + cc) * (int)sizeof(T); };
+  auto xoff = [&](int t) { return (int)((t * ldx + cc) * (int64_t)sizeof(T)); };
   float wk[CPL][W], bk[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -239,7 +242,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
     bk[j] = bias ? bias[cc + j] : 0.f;
   }
   float win[W - 1][CPL], dzw[W - 1][CPL], dwa[CPL][W], dba[CPL];
-  load_window<T, W>(xl, state_in, srow, D, t0, win);
+  load_window<T, W>(xl, state_in, srow, ldx, t0, win);
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     dba[j] = 0.f;
@@ -329,7 +332,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
     Row4<T> bx[U], bd[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      bx[u].load_buf_nt(rx, boff(t0 + u));
+      bx[u].load_buf_nt(rx, xoff(t0 + u));
       bd[u].load_buf_nt(rdy, boff(t0 + u));
     }
     for (int n = 0; n < nfull; ++n, s += U) {
@@ -342,7 +345,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
       const int sn = min(s + U, t1 - U);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        bx[u].load_buf_nt(rx, boff(sn + u));
+        bx[u].load_buf_nt(rx, xoff(sn + u));
         bd[u].load_buf_nt(rdy, boff(sn + u));
       }
 #pragma unroll
@@ -351,14 +354,14 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
   }
   for (; s < t1; ++s) {
     Row4<T> xr, dr;
-    xr.load_buf_nt(rx, boff(s));
+    xr.load_buf_nt(rx, xoff(s));
     dr.load_buf_nt(rdy, boff(s));
     step(s, xr, dr, Own{});
   }
   const int send = min(Tn, t1 + W - 1);
   for (; s < send; ++s) {
     Row4<T> xr, dr;
-    xr.load_buf_nt(rx, boff(s));
+    xr.load_buf_nt(rx, xoff(s));
     dr.load_buf_nt(rdy, boff(s));
     step(s, xr, dr, LookAhead{});
   }
@@ -403,7 +406,7 @@ static hipError_t conv_fwd_k(const ConvArgs& a) {
   dim3 grid((a.D + CONV_WG_CH - 1) / CONV_WG_CH * a.B * nchunk);
   conv_silu_fwd_kernel<T, 4, NG><<<grid, 64 * CONV_WAVES, 0, a.stream>>>(
       static_cast<const T*>(a.x), a.w, a.bias, static_cast<const T*>(a.state_in), static_cast<T*>(a.y),
-      static_cast<T*>(a.state_out), a.T, a.D, nchunk);
+      static_cast<T*>(a.state_out), a.T, a.D, a.ldx, nchunk);
   return hipGetLastError();
 }
 
@@ -415,7 +418,7 @@ static hipError_t conv_bwd_k(const ConvArgs& a) {
   dim3 grid((a.D + CONV_WG_CH - 1) / CONV_WG_CH * nparts);
   conv_silu_bwd_kernel<T, 4, NG><<<grid, 64 * CONV_WAVES, 0, a.stream>>>(
       static_cast<const T*>(a.x), a.w, a.bias, static_cast<const T*>(a.state_in), static_cast<const T*>(a.dy),
-      static_cast<T*>(a.dx), static_cast<T*>(a.dstate_in), part, a.T, a.D, nchunk);
+      static_cast<T*>(a.dx), static_cast<T*>(a.dstate_in), part, a.T, a.D, a.ldx, nchunk);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_column_sum(part, nparts, a.D * 4 + a.D, ColumnOut{{a.dw, a.dbias, nullptr}, {a.D * 4, a.D, 0}},

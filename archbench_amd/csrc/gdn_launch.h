@@ -93,7 +93,7 @@ bool step_shape_supported(int K, int V);
 
 // Short causal convolution + SiLU (+ per-group L2 normalisation), gdn_conv.hip.
 struct ConvArgs {
-  const void* x;          // [B, T, D]
+  const void* x;          // [B, T] rows of D channels, ldx elements apart (ldx >= D)
   const float* w;         // [D, W]
   const float* bias;      // [D] or null
   const void* state_in;   // [B, D, W-1] or null (zeros)
@@ -105,6 +105,7 @@ struct ConvArgs {
   float *dw, *dbias;      // dbias may be null
   void* ws;
   int B, T, D, norm_group, dtype;
+  int64_t ldx;
   hipStream_t stream;
 };
 size_t conv_ws_bytes(int B, int T, int D, int W);
@@ -125,6 +126,8 @@ hipError_t launch_column_sum(const float* part, int64_t nparts, int64_t ld, Colu
 struct NormArgs {
   const void* x;
   const void* gate;
+  int64_t ldg;     // 0: gate rows contiguous; else lines of gpl gate rows, ldg elements apart
+  int gpl;
   const float* w;  // [DV] or null (ones)
   void* y;         // forward
   const void* dy;  // backward

@@ -11,7 +11,9 @@
 //      beta = beta_scale * sigmoid(b + b_bias[h])
 //    forward and backward (da, db, dA_log, ddt_bias, db_bias).
 //
-// Rows of the norm: x, gate, y, dy, dx, dgate [rows, DV] contiguous; w [DV] fp32.  Each lane holds 8 consecutive
+// Rows of the norm: x, y, dy, dx, dgate [rows, DV] contiguous; w [DV] fp32; gate rows either contiguous too or
+// read in place from a wider tensor: lines of gpl rows (gpl * DV contiguous channels, e.g. the heads of one
+// token) ldg elements apart, row r at (r / gpl) * ldg + (r % gpl) * DV (gate_row below).  Each lane holds 8 consecutive
 // channels (one 16-byte bf16 access), a row spans DV/8 lanes and its sums run on DPP; a wave takes 64/(DV/8)
 // rows per access group and NORM_U groups per batch of loads.  HBM-bound: forward reads x and gate and writes y;
 // the backward reads x, gate and dy and writes dx and dgate.  dw is summed per workgroup in a fixed order and the
@@ -31,12 +33,20 @@ constexpr int NORM_WAVES = 4;  // waves per workgroup
 // what a row pass computes
 enum NormMode { RMS = 0, RMS_GATE = 1, L2 = 2 };
 
+// element offset of gate row r (gpl = 1: r * ldg; the host keeps rows below 2^32 otherwise)
+template <int DV>
+__device__ __forceinline__ int64_t gate_row(int64_t r, int64_t ldg, int gpl) {
+  if (gpl == 1) return r * ldg;
+  const uint32_t line = (uint32_t)r / (uint32_t)gpl;
+  return (int64_t)line * ldg + (int64_t)((uint32_t)r - line * (uint32_t)gpl) * DV;
+}
+
 template <typename T, int DV, int MODE>
 __global__ __launch_bounds__(64 * NORM_WAVES) void row_norm_fwd_kernel(const T* __restrict__ x,
                                                                        const T* __restrict__ gate,
                                                                        const float* __restrict__ w,
                                                                        T* __restrict__ y, int64_t rows, float eps,
-                                                                       float scale) {
+                                                                       float scale, int64_t ldg, int gpl) {
   constexpr int LPR = DV / 8, RPW = 64 / LPR, U = NORM_U;
   constexpr bool GATE = MODE == RMS_GATE;
   const int l = lane_id();
@@ -51,7 +61,7 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void row_norm_fwd_kernel(const T* 
   for (int u = 0; u < U; ++u) {
     const int64_t r = min(row0 + u * RPW + sub, rows - 1);  // clamped: rows past the end are loaded, not stored
     xr[u].load(x + r * DV + c0);
-    if constexpr (GATE) gr[u].load(gate + r * DV + c0);
+    if constexpr (GATE) gr[u].load(gate + gate_row<DV>(r, ldg, gpl) + c0);
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -82,7 +92,8 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void row_norm_fwd_kernel(const T* 
 template <typename T, int DV, int MODE>
 __global__ __launch_bounds__(64 * NORM_WAVES) void row_norm_bwd_kernel(
     const T* __restrict__ x, const T* __restrict__ gate, const float* __restrict__ w, const T* __restrict__ dy,
-    T* __restrict__ dx, T* __restrict__ dgate, float* __restrict__ dw_part, int64_t rows, float eps, float scale) {
+    T* __restrict__ dx, T* __restrict__ dgate, float* __restrict__ dw_part, int64_t rows, float eps, float scale,
+    int64_t ldg, int gpl) {
   constexpr int LPR = DV / 8, RPW = 64 / LPR, U = NORM_U;
   constexpr bool GATE = MODE == RMS_GATE;
   __shared__ float red[NORM_WAVES][DV];
@@ -102,7 +113,7 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void row_norm_bwd_kernel(
       const int64_t r = min(row0 + u * RPW + sub, rows - 1);
       xr[u].load(x + r * DV + c0);
       dr[u].load(dy + r * DV + c0);
-      if constexpr (GATE) gr[u].load(gate + r * DV + c0);
+      if constexpr (GATE) gr[u].load(gate + gate_row<DV>(r, ldg, gpl) + c0);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -251,14 +262,15 @@ static hipError_t norm_k(const NormArgs& a, bool backward) {
   if (!backward) {
     row_norm_fwd_kernel<T, DV, MODE><<<dim3(norm_grid_fwd(a.rows, DV)), 64 * NORM_WAVES, 0, a.stream>>>(
         static_cast<const T*>(a.x), static_cast<const T*>(a.gate), a.w, static_cast<T*>(a.y), a.rows, a.eps,
-        a.scale);
+        a.scale, a.ldg ? a.ldg : DV, a.ldg ? a.gpl : 1);
     return hipGetLastError();
   }
   const int nwg = norm_bwd_workgroups(a.rows, DV);
   float* part = static_cast<float*>(a.ws);
   row_norm_bwd_kernel<T, DV, MODE><<<dim3(nwg), 64 * NORM_WAVES, 0, a.stream>>>(
       static_cast<const T*>(a.x), static_cast<const T*>(a.gate), a.w, static_cast<const T*>(a.dy),
-      static_cast<T*>(a.dx), static_cast<T*>(a.dgate), part, a.rows, a.eps, a.scale);
+      static_cast<T*>(a.dx), static_cast<T*>(a.dgate), part, a.rows, a.eps, a.scale, a.ldg ? a.ldg : DV,
+      a.ldg ? a.gpl : 1);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || MODE == L2 || !a.dw) return e;
   return launch_column_sum(part, nwg, DV, ColumnOut{{a.dw, nullptr, nullptr}, {DV, 0, 0}}, a.stream);

@@ -12,10 +12,11 @@ The token mixing itself is always the HIP chunk op (training / prefill) or the H
 a recurrent state, no grad).  The short causal convolutions (with the q / k normalisation fused in), the gate
 functions and the output gated RMSNorm run on their own HIP kernels; the projections are PyTorch linears.  The
 six input projections (q, k, v, a, b and the gate) keep fla's separate ``nn.Linear`` parameters (names, shapes
-and initialisation, so checkpoints and the reference's init rules carry over) but run as one GEMM against their
-concatenated weights: one cast of the input under autocast instead of six, one input-gradient GEMM instead of
-six and their sum, and a weight-gradient GEMM wide enough to fill the GPU (the 4-wide a and b weight gradients,
-a 4 x hidden output reduced over every token, leave it nearly idle when computed apart).
+and initialisation, so checkpoints and the reference's init rules carry over) but run as two GEMMs against
+concatenated weights: q, k, v and the gate as one (2 key_dim + 2 value_dim columns: a multiple of 256 at the
+reference configs, which hipBLASLt's 256-wide tiles cover exactly; with the eight a and b columns added the
+forward GEMM ran 1.6x longer), a and b as the other.  One input-gradient GEMM per group instead of one per
+projection, and a weight-gradient GEMM wide enough to fill the GPU for the big group.
 """
 
 from __future__ import annotations
@@ -99,12 +100,14 @@ class GatedDeltaNet(nn.Module):
         self.o_proj = nn.Linear(self.value_dim, hidden_size, bias=False)
 
     def input_projections(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, ...]:
-        """(q, k, v, a, b[, gate]) = the six linears of ``hidden_states``, computed as one GEMM."""
-        mods = [self.q_proj, self.k_proj, self.v_proj, self.a_proj, self.b_proj]
-        if self.use_gate:
-            mods.append(self.g_proj)
-        y = F.linear(hidden_states, torch.cat([m.weight for m in mods], 0))
-        return torch.split(y, [m.out_features for m in mods], dim=-1)
+        """(q, k, v, a, b[, gate]) = the six linears of ``hidden_states``, computed as two GEMMs: q, k, v (and
+        the gate) against their concatenated weights, a and b against theirs."""
+        wide = [self.q_proj, self.k_proj, self.v_proj] + ([self.g_proj] if self.use_gate else [])
+        y = F.linear(hidden_states, torch.cat([m.weight for m in wide], 0))
+        q, k, v, *gate = torch.split(y, [m.out_features for m in wide], dim=-1)
+        a, b = torch.split(F.linear(hidden_states, torch.cat([self.a_proj.weight, self.b_proj.weight], 0)),
+                           [self.a_proj.out_features, self.b_proj.out_features], dim=-1)
+        return (q, k, v, a, b, *gate)
 
     def forward(self, hidden_states: torch.Tensor, attention_mask: torch.Tensor | None = None,
                 past_key_values: dict | None = None, use_cache: bool = False, output_attentions: bool = False,

@@ -62,6 +62,37 @@ def _arg(t: Optional[Tensor], dtype: Optional[torch.dtype] = None) -> Optional[T
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+def _token_rows(x: Tensor) -> tuple[Tensor, int]:
+    """A [B, T, D] kernel argument as (tensor, ld): read in place when its channels are contiguous and its tokens
+    lie ld elements apart with one stride throughout (e.g. a column slice of a fused projection's output, whose
+    tokens are the projection's width apart), ld a multiple of 4 and the base 16-byte aligned; otherwise a
+    contiguous copy (ld = D)."""
+    B, T, D = x.shape
+    ld = x.stride(1) if T > 1 else (x.stride(0) if B > 1 else D)
+    if (x.stride(2) == 1 and ld >= D and (B <= 1 or x.stride(0) == T * ld) and ld % 4 == 0
+            and x.data_ptr() % 16 == 0):
+        return x, ld
+    return _arg(x), D
+
+
+def _gate_lines(gate: Tensor, dim: int) -> tuple[Tensor, int, int]:
+    """A gate of rows of `dim` channels as (tensor, ldg, gpl): ldg = 0 for contiguous rows; otherwise read in place
+    as lines of gpl rows (its second-to-last dimension, gpl * dim contiguous channels) ldg elements apart with one
+    stride over the leading dimensions, such as [B, T, H, dim] heads sliced from a fused projection's output."""
+    if gate.is_contiguous() and gate.data_ptr() % 16 == 0:
+        return gate, 0, 1
+    if gate.dim() >= 3 and gate.stride(-1) == 1 and gate.stride(-2) == dim and gate.data_ptr() % 16 == 0:
+        gpl, lead = gate.shape[-2], gate.shape[:-2]
+        ldg = gate.stride(-3) if lead[-1] > 1 else gpl * dim
+        ok, expect = ldg >= gpl * dim and (ldg * gate.element_size()) % 16 == 0, ldg
+        for i in range(len(lead) - 1, -1, -1):
+            ok = ok and (lead[i] <= 1 or gate.stride(i) == expect)
+            expect *= lead[i]
+        if ok:
+            return gate, ldg, gpl
+    return _arg(gate), 0, 1
+
+
 def _shapes(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, h0: Optional[Tensor]):
     if q.dim() != 4 or k.shape != q.shape:
         raise ValueError(f"q and k must be [B, T, H, K] with equal shapes, got {tuple(q.shape)} and {tuple(k.shape)}")
@@ -375,11 +406,11 @@ def short_conv(x: Tensor, w: Tensor, bias: Optional[Tensor], state: Optional[Ten
     _require_gpu(x, w, bias, state)
     B, T, D, W = _conv_shapes(x, w, bias, state)
     lib = _lib.load()
-    x = _arg(x)
+    x, ldx = _token_rows(x)
     w, bias, state = _arg(w, torch.float32), _arg(bias, torch.float32), _arg(state, x.dtype)
-    y = torch.empty_like(x)
+    y = x.new_empty(B, T, D)
     new_state = torch.empty(B, D, W - 1, dtype=x.dtype, device=x.device)
-    rc = lib.gdn_short_conv_fwd(_lib.ptr(x), _lib.ptr(w), _lib.ptr(bias), _lib.ptr(state), _lib.ptr(y),
+    rc = lib.gdn_short_conv_fwd(_lib.ptr(x), ldx, _lib.ptr(w), _lib.ptr(bias), _lib.ptr(state), _lib.ptr(y),
                                 _lib.ptr(new_state), B, T, D, W, int(norm_group), _lib.dtype_code(x.dtype),
                                 _lib.stream_ptr(x.device))
     _lib.check(rc, "gdn_short_conv_fwd")
@@ -389,7 +420,7 @@ def short_conv(x: Tensor, w: Tensor, bias: Optional[Tensor], state: Optional[Ten
 @short_conv.register_fake
 def _(x, w, bias, state, norm_group):
     B, T, D = x.shape
-    return torch.empty_like(x), x.new_empty(B, D, w.shape[1] - 1)
+    return x.new_empty(B, T, D), x.new_empty(B, D, w.shape[1] - 1)
 
 
 @torch.library.custom_op("archbench_amd::short_conv_bwd", mutates_args=())
@@ -399,14 +430,15 @@ def short_conv_bwd(x: Tensor, w: Tensor, bias: Optional[Tensor], state: Optional
     _require_gpu(x, w, bias, state, dy)
     B, T, D, W = _conv_shapes(x, w, bias, state)
     lib = _lib.load()
-    x, dy = _arg(x), _arg(dy, x.dtype)
+    dy = _arg(dy, x.dtype)
+    x, ldx = _token_rows(x)
     w, bias, state = _arg(w, torch.float32), _arg(bias, torch.float32), _arg(state, x.dtype)
-    dx = torch.empty_like(x)
+    dx = x.new_empty(B, T, D)
     dw = torch.empty(D, W, dtype=torch.float32, device=x.device)
     db = torch.empty(D, dtype=torch.float32, device=x.device)
     dstate = torch.empty(B, D, W - 1, dtype=x.dtype, device=x.device)
     ws = torch.empty(_lib.conv_ws_bytes(B, T, D, W), dtype=torch.uint8, device=x.device)
-    rc = lib.gdn_short_conv_bwd(_lib.ptr(x), _lib.ptr(w), _lib.ptr(bias), _lib.ptr(state), _lib.ptr(dy),
+    rc = lib.gdn_short_conv_bwd(_lib.ptr(x), ldx, _lib.ptr(w), _lib.ptr(bias), _lib.ptr(state), _lib.ptr(dy),
                                 _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(dstate), _lib.ptr(ws), ws.numel(),
                                 B, T, D, W, int(norm_group), _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device))
     _lib.check(rc, "gdn_short_conv_bwd")
@@ -418,7 +450,7 @@ def _(x, w, bias, state, dy, norm_group):
     B, T, D = x.shape
     W = w.shape[1]
     f32 = dict(dtype=torch.float32)
-    return torch.empty_like(x), w.new_empty(D, W, **f32), w.new_empty(D, **f32), x.new_empty(B, D, W - 1)
+    return x.new_empty(B, T, D), w.new_empty(D, W, **f32), w.new_empty(D, **f32), x.new_empty(B, D, W - 1)
 
 
 def _conv_setup(ctx, inputs, output):
@@ -470,10 +502,11 @@ def gated_rmsnorm(x: Tensor, gate: Optional[Tensor], weight: Optional[Tensor], e
     _require_gpu(x, gate, weight)
     rows, dim = _norm_rows(x, gate, weight)
     lib = _lib.load()
-    x, gate, weight = _arg(x), _arg(gate, x.dtype), _arg(weight, torch.float32)
+    x, weight = _arg(x), _arg(weight, torch.float32)
+    gate, ldg, gpl = _gate_lines(gate.to(x.dtype), dim) if gate is not None else (None, 0, 1)
     y = torch.empty_like(x)
-    rc = lib.gdn_gated_rmsnorm_fwd(_lib.ptr(x), _lib.ptr(gate), _lib.ptr(weight), _lib.ptr(y), rows, dim,
-                                   float(eps), _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device))
+    rc = lib.gdn_gated_rmsnorm_fwd(_lib.ptr(x), _lib.ptr(gate), ldg, gpl, _lib.ptr(weight), _lib.ptr(y), rows,
+                                   dim, float(eps), _lib.dtype_code(x.dtype), _lib.stream_ptr(x.device))
     _lib.check(rc, "gdn_gated_rmsnorm_fwd")
     return y
 
@@ -490,14 +523,15 @@ def gated_rmsnorm_bwd(x: Tensor, gate: Optional[Tensor], weight: Optional[Tensor
     _require_gpu(x, gate, weight, dy)
     rows, dim = _norm_rows(x, gate, weight)
     lib = _lib.load()
-    x, gate, weight, dy = _arg(x), _arg(gate, x.dtype), _arg(weight, torch.float32), _arg(dy, x.dtype)
+    x, weight, dy = _arg(x), _arg(weight, torch.float32), _arg(dy, x.dtype)
+    gate, ldg, gpl = _gate_lines(gate.to(x.dtype), dim) if gate is not None else (None, 0, 1)
     dx = torch.empty_like(x)
     dgate = torch.empty_like(x) if gate is not None else x.new_empty(0)
     dw = torch.empty(dim, dtype=torch.float32, device=x.device)
     ws = torch.empty(_lib.norm_ws_bytes(rows, dim), dtype=torch.uint8, device=x.device)
-    rc = lib.gdn_gated_rmsnorm_bwd(_lib.ptr(x), _lib.ptr(gate), _lib.ptr(weight), _lib.ptr(dy), _lib.ptr(dx),
-                                   _lib.ptr(dgate) if gate is not None else None, _lib.ptr(dw), _lib.ptr(ws),
-                                   ws.numel(), rows, dim, float(eps), _lib.dtype_code(x.dtype),
+    rc = lib.gdn_gated_rmsnorm_bwd(_lib.ptr(x), _lib.ptr(gate), ldg, gpl, _lib.ptr(weight), _lib.ptr(dy),
+                                   _lib.ptr(dx), _lib.ptr(dgate) if gate is not None else None, _lib.ptr(dw),
+                                   _lib.ptr(ws), ws.numel(), rows, dim, float(eps), _lib.dtype_code(x.dtype),
                                    _lib.stream_ptr(x.device))
     _lib.check(rc, "gdn_gated_rmsnorm_bwd")
     return dx, dgate, dw

@@ -134,31 +134,37 @@ int gdn_recurrent_step(const void* q, const void* k, const void* v, const float*
  *   z[t,c] = bias[c] + sum_i w[c,i] x[t-(W-1)+i, c],   y = silu(z),   y <- y / max(||y||_group, 1e-12).
  * Replaces the ShortConv + causal_conv1d custom ops archbench::causal_conv_silu / _bwd
  * (archbench/layers/nsgdn.py:420-470; fla's ShortConvolution in GatedDeltaNet) and the per-head normalisation
- * of q and k (nsgdn.py:527-528).  x, y, dy, dx [B, T, D] token-major in dtype; w [D, W] and bias [D] fp32 (bias
- * may be NULL); conv states [B, D, W-1] in dtype, the previous W-1 inputs oldest first (state_in NULL = zeros;
- * state_out NULL = not returned; it must not alias state_in).  Compiled for W = 4, D % 4 == 0, norm_group in {0 (none), 64, 128, 256}.
+ * of q and k (nsgdn.py:527-528).  y, dy, dx [B, T, D] token-major in dtype; x [B, T] rows of D channels ldx
+ * elements apart (ldx = D, or 0, for a contiguous x; a larger ldx reads x in place as a column slice of a wider
+ * [B, T, ldx] tensor, such as one output of a fused input projection; ldx a multiple of 4);
+ * w [D, W] and bias [D] fp32 (bias may be NULL); conv states [B, D, W-1] in dtype, the previous W-1 inputs oldest
+ * first (state_in NULL = zeros; state_out NULL = not returned; it must not alias state_in).  Compiled for W = 4,
+ * D % 4 == 0, norm_group in {0 (none), 64, 128, 256}.
  * The backward writes dx, dw [D, W] fp32, dbias [D] fp32 (if non-NULL) and dstate_in (if non-NULL); its
  * workspace holds per-chunk partial sums of dw, reduced in a fixed order (deterministic). */
-int gdn_short_conv_fwd(const void* x, const float* w, const float* bias, const void* state_in, void* y,
+int gdn_short_conv_fwd(const void* x, int64_t ldx, const float* w, const float* bias, const void* state_in, void* y,
                        void* state_out, int B, int T, int D, int W, int norm_group, int dtype, void* stream);
 int gdn_short_conv_bwd_ws_bytes(int B, int T, int D, int W, size_t* bytes);
-int gdn_short_conv_bwd(const void* x, const float* w, const float* bias, const void* state_in, const void* dy,
-                       void* dx, float* dw, float* dbias, void* dstate_in, void* ws, size_t ws_bytes, int B, int T,
-                       int D, int W, int norm_group, int dtype, void* stream);
+int gdn_short_conv_bwd(const void* x, int64_t ldx, const float* w, const float* bias, const void* state_in,
+                       const void* dy, void* dx, float* dw, float* dbias, void* dstate_in, void* ws, size_t ws_bytes,
+                       int B, int T, int D, int W, int norm_group, int dtype, void* stream);
 
 /* Gated RMSNorm of the op's output, per row of `dim` channels (one head of one token):
  *   y = x * rsqrt(mean(x^2) + eps) * weight * silu(gate)
  * Replaces the output normalisation of the mixer: fla's FusedRMSNormGated in GatedDeltaNet and the reference's
  * self.norm(y) followed by y * F.silu(g) (archbench/layers/nsgdn.py:539-541), as one pass (fp32 arithmetic).
- * x, gate, y, dy, dx, dgate [rows, dim] in dtype; gate may be NULL (plain RMSNorm; dgate unused); weight [dim]
- * fp32 or NULL (ones).  dim in {64, 128, 256}.  The backward writes dx, dgate and dweight (if non-NULL; summed
- * over rows in a fixed order through the workspace). */
-int gdn_gated_rmsnorm_fwd(const void* x, const void* gate, const float* weight, void* y, int64_t rows, int dim,
-                          float eps, int dtype, void* stream);
+ * x, y, dy, dx, dgate [rows, dim] in dtype; gate may be NULL (plain RMSNorm; dgate unused); weight [dim]
+ * fp32 or NULL (ones).  dim in {64, 128, 256}.  Gate rows are contiguous when ldg = 0; otherwise the gate is read
+ * in place from a wider tensor as lines of gpl rows (gpl * dim contiguous channels, e.g. the heads of one token)
+ * ldg elements apart: row r at (r / gpl) * ldg + (r % gpl) * dim (rows a multiple of gpl, ldg * sizeof(dtype) a
+ * multiple of 16, such as the gate columns of a fused input projection).  The backward writes dx, dgate (rows
+ * contiguous) and dweight (if non-NULL; summed over rows in a fixed order through the workspace). */
+int gdn_gated_rmsnorm_fwd(const void* x, const void* gate, int64_t ldg, int gpl, const float* weight, void* y,
+                          int64_t rows, int dim, float eps, int dtype, void* stream);
 int gdn_gated_rmsnorm_bwd_ws_bytes(int64_t rows, int dim, size_t* bytes);
-int gdn_gated_rmsnorm_bwd(const void* x, const void* gate, const float* weight, const void* dy, void* dx,
-                          void* dgate, float* dweight, void* ws, size_t ws_bytes, int64_t rows, int dim, float eps,
-                          int dtype, void* stream);
+int gdn_gated_rmsnorm_bwd(const void* x, const void* gate, int64_t ldg, int gpl, const float* weight,
+                          const void* dy, void* dx, void* dgate, float* dweight, void* ws, size_t ws_bytes,
+                          int64_t rows, int dim, float eps, int dtype, void* stream);
 
 /* L2 normalisation with a scale over rows of `dim` channels (one head of q or k):
  *   y = scale * x / max(||x||, eps)

@@ -111,3 +111,22 @@ def test_fp32_head_size_error_names_the_bf16_route():
                            _lib.DTYPE_F32, None)
     assert rc == _lib.GDN_ERR_SHAPE
     assert b"bf16" in lib.gdn_last_error() and b"K=64" in lib.gdn_last_error()
+
+
+def test_strided_input_layouts_are_validated_before_any_launch():
+    """The conv's x row stride and the norm's gate line layout are checked on the host: a stride below the row
+    width or off a 4-channel (conv) or 16-byte (gate) multiple, or a row count that is not a whole number of gate
+    lines, is refused."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rc = lib.gdn_short_conv_fwd(p, 100, p, None, None, p, None, 1, 8, 128, 4, 0, _lib.DTYPE_BF16, None)
+    assert rc == _lib.GDN_ERR_ARG and b"ldx" in lib.gdn_last_error()
+    rc = lib.gdn_short_conv_fwd(p, 130, p, None, None, p, None, 1, 8, 128, 4, 0, _lib.DTYPE_BF16, None)
+    assert rc == _lib.GDN_ERR_ARG and b"multiple of 4" in lib.gdn_last_error()
+    rc = lib.gdn_short_conv_bwd(p, 64, p, None, None, p, p, p, None, None, p, 1 << 20, 1, 8, 128, 4, 0,
+                                _lib.DTYPE_BF16, None)
+    assert rc == _lib.GDN_ERR_ARG and b"ldx" in lib.gdn_last_error()
+    rc = lib.gdn_gated_rmsnorm_fwd(p, p, 3072, 4, None, p, 10, 256, 1e-5, _lib.DTYPE_BF16, None)
+    assert rc == _lib.GDN_ERR_ARG and b"gate layout" in lib.gdn_last_error()
+    rc = lib.gdn_gated_rmsnorm_fwd(p, p, 512, 4, None, p, 8, 256, 1e-5, _lib.DTYPE_BF16, None)
+    assert rc == _lib.GDN_ERR_ARG and b"gate layout" in lib.gdn_last_error()

@@ -144,3 +144,33 @@ def test_conv_large_deterministic():
     _, dw_ref, _, _ = CO.short_conv_bwd(x[..., sl], w[sl], None, None, dy[..., sl], 128, dtype=torch.float32)
     assert rel_l2(r1[1][sl], dw_ref) <= 1e-2
     assert _lib.conv_ws_bytes(B, T, D, W) >= B * (T // 64) * D * W * 4
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,ng", [(200, 128), (65, 0), (3, 64)])
+def test_conv_reads_a_column_slice_in_place(dtype, T, ng):
+    """x as a column slice of a wider [B, T, L] tensor (the q, k or v part of a fused projection's output): read in
+    place with its token stride, bit-identical to the same values made contiguous, forward and backward, and the
+    autograd path leaves the slice's storage untouched."""
+    banner(f"conv column slice dtype={dtype} T={T} ng={ng}")
+    B, D, L, off = 2, 256, 768, 128
+    gen = torch.Generator().manual_seed(5)
+    wide = torch.randn(B, T, L, generator=gen).to("cuda", dtype)
+    w = (torch.randn(D, W, generator=gen) * 0.5).cuda()
+    dy = torch.randn(B, T, D, generator=gen).to("cuda", dtype)
+    xs = wide[..., off:off + D]
+    assert not xs.is_contiguous() and ops._token_rows(xs)[1] == L
+    xc = xs.contiguous()
+    y_s, st_s = ops.short_conv(xs, w, None, None, ng)
+    y_c, st_c = ops.short_conv(xc, w, None, None, ng)
+    assert torch.equal(y_s, y_c) and torch.equal(st_s, st_c)
+    g_s = ops.short_conv_bwd(xs, w, None, None, dy, ng)
+    g_c = ops.short_conv_bwd(xc, w, None, None, dy, ng)
+    for a, b in zip(g_s, g_c):
+        assert torch.equal(a, b)
+    before = wide.clone()
+    xa = wide[..., off:off + D].detach().requires_grad_()
+    y, _ = ops.short_conv(xa, w, None, None, ng)
+    y.float().sum().backward()
+    assert torch.equal(xa.grad, ops.short_conv_bwd(xc, w, None, None, torch.ones_like(dy), ng)[0])
+    assert torch.equal(wide, before)

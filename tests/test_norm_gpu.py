@@ -176,3 +176,25 @@ def test_op_l2norm_in_kernel_path():
     o2.backward(do.cuda())
     assert max_abs(o1, o2) <= 1e-4
     assert max_abs(lq.grad, rq.grad) <= 1e-4 and max_abs(lk.grad, rk.grad) <= 1e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("H,dim", [(4, 256), (16, 128), (3, 64)])
+def test_norm_reads_gate_heads_in_place(dtype, H, dim):
+    """The gate as [B, T, H, dim] heads sliced from a wider [B, T, L] tensor (the gate part of a fused projection):
+    read in place as lines of H rows, bit-identical to the contiguous gate, forward and backward."""
+    banner(f"norm strided gate dtype={dtype} H={H} dim={dim}")
+    B, T, off = 2, 37, 64
+    L = off + H * dim + 64
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn(B, T, H, dim, generator=gen).to("cuda", dtype)
+    wide = torch.randn(B, T, L, generator=gen).to("cuda", dtype)
+    wt = (1 + 0.1 * torch.randn(dim, generator=gen)).cuda()
+    dy = torch.randn(B, T, H, dim, generator=gen).to("cuda", dtype)
+    gs = wide[..., off:off + H * dim].reshape(B, T, H, dim)
+    _, ldg, gpl = ops._gate_lines(gs, dim)
+    assert (ldg, gpl) == (L, H)
+    gc = gs.contiguous()
+    assert torch.equal(ops.gated_rmsnorm(x, gs, wt, 1e-5), ops.gated_rmsnorm(x, gc, wt, 1e-5))
+    for a, b in zip(ops.gated_rmsnorm_bwd(x, gs, wt, dy, 1e-5), ops.gated_rmsnorm_bwd(x, gc, wt, dy, 1e-5)):
+        assert torch.equal(a, b)
