@@ -5,7 +5,8 @@
 //   z[t,c] = bias[c] + sum_i w[c,i] x[t - (W-1) + i, c]      (x at t < 0 comes from the conv state)
 //   y[t,c] = silu(z[t,c]);  with normalisation over each group of NG channels: y / max(||y||_group, 1e-12)
 //
-// Layout: x, y, dy, dx [B, T, D] token-major (channel-last), w [D, W] fp32, bias [D] fp32, conv states
+// Layout: y, dy, dx [B, T, D] token-major (channel-last); x [B, T] rows of D channels ldx elements apart (ldx = D,
+// or larger to read a column slice of a wider tensor in place); w [D, W] fp32, bias [D] fp32, conv states
 // [B, D, W-1] in the activation dtype (the previous W-1 inputs, oldest first).
 // Mapping: one wave per (256 channels, 64-token chunk, b); each lane holds 4 consecutive channels, so every token
 // row is one 8-byte (bf16) or 16-byte (fp32) access per lane and a wave covers 512 B / 1 KB contiguous.  The W-1
@@ -88,7 +89,7 @@ __device__ __forceinline__ float group_sum(float s) {
 constexpr float NORM_EPS = 1e-12f;  // F.normalize's eps
 
 template <typename T, int W>
-__device__ __forceinline__ void load_window(const T* xl, const T* state_in, int64_t srow, int64_t ldx, int t0,
+__device__ __forceinline__ void load_window(const T* xl, const T* state_in, int64_t srow, int ldx, int t0,
                                             float (&win)[W - 1][CONV_CPL]) {
   // inputs at t0 - (W-1) .. t0 - 1; negative positions from the conv state (zero if none)
 #pragma unroll
@@ -108,22 +109,29 @@ __device__ __forceinline__ void load_window(const T* xl, const T* state_in, int6
   }
 }
 
-// grid B * nchunk * ceil(D / (CONV_WAVES * CONV_CW)) (channel groups fastest), CONV_WAVES waves, each
-// independent: consecutive workgroups cover adjacent channels of the same token rows.  Rows are loaded in batches of CONV_UF with the next batch in
-// flight while the current one is computed; the prefetch of the last batch re-reads it (start clamped to
-// t1 - CONV_UF) so every load stays inside the chunk.
+// Work items: (part = b * nchunk + chunk, 256-channel block), blocks fastest; wave w of workgroup x takes item
+// x * CONV_WAVES + w, so the waves of a workgroup, each independent, cover adjacent channel blocks of the same
+// token rows (and, when D has fewer than CONV_WAVES blocks, the next chunk's: no wave idles at D = 256 or 512).
+__device__ __forceinline__ bool conv_wave_item(int D, int nparts, int& part, int& cw0) {
+  const int ncb = (D + CONV_CW - 1) / CONV_CW;
+  const int item = (int)blockIdx.x * CONV_WAVES + __builtin_amdgcn_readfirstlane(wave_id());  // uniform: scalar
+  part = item / ncb;
+  cw0 = (item - part * ncb) * CONV_CW;
+  return part < nparts;
+}
+// Forward: grid ceil(B * nchunk * ceil(D / CONV_CW) / CONV_WAVES), CONV_WAVES waves.  Rows are loaded in batches
+// of CONV_UF with the next batch in flight while the current one is computed; the prefetch of the last batch
+// re-reads it (start clamped to t1 - CONV_UF) so every load stays inside the chunk.
 template <typename T, int W, int NG>
 __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_fwd_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                            const float* __restrict__ bias,
                                                            const T* __restrict__ state_in, T* __restrict__ y,
-                                                           T* __restrict__ state_out, int Tn, int D, int64_t ldx,
-                                                           int nchunk) {
+                                                           T* __restrict__ state_out, int Tn, int D, int ldx,
+                                                           int nchunk, int nparts) {
   constexpr int CPL = CONV_CPL, U = CONV_UF;
   const int l = lane_id();
-  const int ncg = (D + CONV_WAVES * CONV_CW - 1) / (CONV_WAVES * CONV_CW);
-  const int part = blockIdx.x / ncg, cg = blockIdx.x - part * ncg;  // part = b * nchunk + chunk
-  const int cw0 = (cg * CONV_WAVES + wave_id()) * CONV_CW;
-  if (cw0 >= D) return;  // a wave wholly past the channels (waves never synchronise)
+  int part, cw0;
+  if (!conv_wave_item(D, nparts, part, cw0)) return;  // past the last item (waves never synchronise)
   const int c = cw0 + CPL * l;
   const int b = part / nchunk, ch = part - b * nchunk;
   const int t0 = ch * CONV_L, t1 = min(Tn, t0 + CONV_L);
@@ -209,13 +217,11 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
                                                            const T* __restrict__ state_in,
                                                            const T* __restrict__ dy, T* __restrict__ dx,
                                                            T* __restrict__ dstate_in, float* __restrict__ part_out,
-                                                           int Tn, int D, int64_t ldx, int nchunk) {
+                                                           int Tn, int D, int ldx, int nchunk, int nparts) {
   constexpr int CPL = CONV_CPL, U = CONV_UB;
   const int l = lane_id();
-  const int ncg = (D + CONV_WAVES * CONV_CW - 1) / (CONV_WAVES * CONV_CW);
-  const int part = blockIdx.x / ncg, cg = blockIdx.x - part * ncg;  // part = b * nchunk + chunk
-  const int cw0 = (cg * CONV_WAVES + wave_id()) * CONV_CW;
-  if (cw0 >= D) return;  // a wave wholly past the channels (waves never synchronise)
+  int part, cw0;
+  if (!conv_wave_item(D, nparts, part, cw0)) return;  // past the last item (waves never synchronise)
   const int c = cw0 + CPL * l;
   const int b = part / nchunk, ch = part - b * nchunk;
   const int t0 = ch * CONV_L, t1 = min(Tn, t0 + CONV_L);
@@ -229,11 +235,11 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
   const int64_t bbase = (int64_t)b * Tn * D;
   const int bbytes = Tn * D * (int)sizeof(T);
   const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(x + (int64_t)b * Tn * ldx), 0,
-                                                    (int)(Tn * ldx * (int64_t)sizeof(T)), BUF_RSRC_WORD3);
+                                                    Tn * ldx * (int)sizeof(T), BUF_RSRC_WORD3);
   const auto rdy = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(dy + bbase), 0, bbytes, BUF_RSRC_WORD3);
   const auto rdx = __builtin_amdgcn_make_buffer_rsrc(dx + bbase, 0, bbytes, BUF_RSRC_WORD3);
   auto boff = [&](int t) { return (t * D + cc) * (int)sizeof(T); };
-  auto xoff = [&](int t) { return (int)((t * ldx + cc) * (int64_t)sizeof(T)); };
+  auto xoff = [&](int t) { return (t * ldx + cc) * (int)sizeof(T); };
   float wk[CPL][W], bk[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -398,15 +404,19 @@ bool conv_shape_supported(int D, int W, int norm_group) {
          (norm_group == 0 || ((norm_group == 64 || norm_group == 128 || norm_group == 256) && D % norm_group == 0));
 }
 
-constexpr int CONV_WG_CH = CONV_WAVES * CONV_CW;
+// workgroups for every (part, 256-channel block) item, CONV_WAVES items each
+static dim3 conv_grid(int D, int nparts) {
+  const int64_t items = (int64_t)(D + CONV_CW - 1) / CONV_CW * nparts;
+  return dim3((unsigned)((items + CONV_WAVES - 1) / CONV_WAVES));
+}
 
 template <typename T, int NG>
 static hipError_t conv_fwd_k(const ConvArgs& a) {
   const int nchunk = (a.T + CONV_L - 1) / CONV_L;
-  dim3 grid((a.D + CONV_WG_CH - 1) / CONV_WG_CH * a.B * nchunk);
-  conv_silu_fwd_kernel<T, 4, NG><<<grid, 64 * CONV_WAVES, 0, a.stream>>>(
+  const int nparts = a.B * nchunk;
+  conv_silu_fwd_kernel<T, 4, NG><<<conv_grid(a.D, nparts), 64 * CONV_WAVES, 0, a.stream>>>(
       static_cast<const T*>(a.x), a.w, a.bias, static_cast<const T*>(a.state_in), static_cast<T*>(a.y),
-      static_cast<T*>(a.state_out), a.T, a.D, a.ldx, nchunk);
+      static_cast<T*>(a.state_out), a.T, a.D, (int)a.ldx, nchunk, nparts);
   return hipGetLastError();
 }
 
@@ -415,10 +425,9 @@ static hipError_t conv_bwd_k(const ConvArgs& a) {
   const int nchunk = (a.T + CONV_L - 1) / CONV_L;
   const int nparts = a.B * nchunk;
   float* part = static_cast<float*>(a.ws);
-  dim3 grid((a.D + CONV_WG_CH - 1) / CONV_WG_CH * nparts);
-  conv_silu_bwd_kernel<T, 4, NG><<<grid, 64 * CONV_WAVES, 0, a.stream>>>(
+  conv_silu_bwd_kernel<T, 4, NG><<<conv_grid(a.D, nparts), 64 * CONV_WAVES, 0, a.stream>>>(
       static_cast<const T*>(a.x), a.w, a.bias, static_cast<const T*>(a.state_in), static_cast<const T*>(a.dy),
-      static_cast<T*>(a.dx), static_cast<T*>(a.dstate_in), part, a.T, a.D, a.ldx, nchunk);
+      static_cast<T*>(a.dx), static_cast<T*>(a.dstate_in), part, a.T, a.D, (int)a.ldx, nchunk, nparts);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_column_sum(part, nparts, a.D * 4 + a.D, ColumnOut{{a.dw, a.dbias, nullptr}, {a.D * 4, a.D, 0}},
