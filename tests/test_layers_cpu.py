@@ -143,3 +143,32 @@ def test_fused_input_projections_equal_the_separate_linears(use_gate):
     for gf, md in zip(g_fused, mods):
         torch.testing.assert_close(gf, md.weight.grad, rtol=0, atol=1e-12)
     torch.testing.assert_close(gx, x.grad, rtol=0, atol=1e-12)
+
+
+def test_in_place_row_layouts_of_projection_slices():
+    """The conv and norm ops read column slices of a fused projection's output in place: the token stride and the
+    gate's line layout are derived from the view's strides, and anything they cannot express (a transposed view, a
+    stride off the kernels' alignment) falls back to a contiguous copy."""
+    from archbench_amd import ops
+    B, T, L = 2, 5, 3072
+    y = torch.zeros(B, T, L, dtype=torch.bfloat16)
+    x, ld = ops._token_rows(y[..., 512:1024])
+    assert ld == L and x.data_ptr() == y[..., 512:1024].data_ptr()       # read in place
+    x, ld = ops._token_rows(y[..., :512].contiguous())
+    assert ld == 512
+    x, ld = ops._token_rows(y[..., 2:514])                                # 2 elements in: stride fine, base 4 B off
+    assert ld == 512 and x.is_contiguous()
+    x, ld = ops._token_rows(y[:1, ::2, :512])                            # every other token of one sequence
+    assert ld == 2 * L and not x.is_contiguous()
+    x, ld = ops._token_rows(y[:, ::2, :512])                             # ... of two: batch stride != T * ld
+    assert ld == 512 and x.is_contiguous()
+    x, ld = ops._token_rows(torch.zeros(B, 512, T, dtype=torch.bfloat16).transpose(1, 2))  # channels strided
+    assert ld == 512 and x.is_contiguous()
+    H, dim = 4, 256
+    gate = y[..., 2048:2048 + H * dim].reshape(B, T, H, dim)
+    g, ldg, gpl = ops._gate_lines(gate, dim)
+    assert (ldg, gpl) == (L, H) and g.data_ptr() == gate.data_ptr()
+    g, ldg, gpl = ops._gate_lines(gate.contiguous(), dim)
+    assert (ldg, gpl) == (0, 1)
+    g, ldg, gpl = ops._gate_lines(gate.transpose(2, 3).contiguous().transpose(2, 3), dim)  # dim not contiguous
+    assert (ldg, gpl) == (0, 1) and g.is_contiguous()
