@@ -230,7 +230,7 @@ using namespace gdn;
 
 extern "C" {
 
-int gdn_version(void) { return 100; }
+int gdn_version(void) { return 200; }  // 0.2.0: row strides in the conv and norm entry points
 
 int gdn_profile_enable(int on) {
   std::lock_guard<std::mutex> lock(g_prof.mu);
