@@ -3,8 +3,8 @@
 // The backward takes the chunk factors (Tm, P, G) and the state entering every chunk with R from the stashing
 // forward, or rebuilds them first (chunk factors kernel, then the forward sweep in recompute mode), then runs:
 //
-// bwd_state: one workgroup per (64-wide V block, b*h), reverse over chunks, reading the chunk factors; each
-//   wave carries a 16-column slab of dS in MFMA accumulators.
+// bwd_state: one workgroup per (V block of 64 columns, or 32 when the grid fits the device, b*h), reverse over
+//   chunks, reading the chunk factors; each wave carries a 16-column slab of dS in MFMA accumulators.
 //     dR  = P^T dO + Kd dS_C                         Kd = diag(exp(G_C - G)) K
 //     dY  = Tm^T dR                                  (the gradient w.r.t. Y, where R = Tm Y, Y = beta (V - gamma K S0))
 //     dS0 = gamma_C dS_C + s (diag(gamma) Q)^T dO - K^T diag(beta gamma) dY

@@ -1,6 +1,6 @@
-// Chunkwise gated delta rule, forward state sweep: one workgroup per (64-wide V block, b*h), sequential over the
-// 64-token chunks of the sequence, after the chunk factors (Tm, P, G) have been built for all chunks in
-// parallel (gdn_chunk_factors.hip).
+// Chunkwise gated delta rule, forward state sweep: one workgroup per (V block of 64 columns, or 32 when the grid
+// fits the device, b*h), sequential over the 64-token chunks of the sequence, after the chunk factors (Tm, P, G)
+// have been built for all chunks in parallel (gdn_chunk_factors.hip).
 //
 // Per chunk (archbench/layers/nsgdn.py:240-249 algebra; fla GDN call order cumsum -> WY -> state -> output,
 // nsgdn.py:357-362), each wave holds one 16-column slab of S in fp32 MFMA accumulators for the whole sweep:
