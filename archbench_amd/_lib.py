@@ -43,7 +43,8 @@ SIGNATURES = {
     "gdn_recurrent_step": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_short_conv_fwd": (_i, [_p, _i64, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "gdn_short_conv_bwd_ws_bytes": (_i, [_i, _i, _i, _i, ctypes.POINTER(_sz)]),
-    "gdn_short_conv_bwd": (_i, [_p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _i, _p]),
+    "gdn_short_conv_bwd": (_i, [_p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _i,
+                                _p]),
     "gdn_gated_rmsnorm_fwd": (_i, [_p, _p, _i64, _i, _p, _p, _i64, _i, _f, _i, _p]),
     "gdn_gated_rmsnorm_bwd_ws_bytes": (_i, [_i64, _i, ctypes.POINTER(_sz)]),
     "gdn_gated_rmsnorm_bwd": (_i, [_p, _p, _i64, _i, _p, _p, _p, _p, _p, _p, _sz, _i64, _i, _f, _i, _p]),

@@ -581,7 +581,7 @@ int gdn_short_conv_bwd_ws_bytes(int B, int T, int D, int W, size_t* bytes) {
   return GDN_OK;
 }
 
-static int conv_check(int B, int T, int D, int64_t ldx, int W, int norm_group, int dtype) {
+static int conv_check(int B, int T, int D, int64_t ldx, int W, int norm_group, int dtype, const char* ld_name = "ldx") {
   if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
   if (B < 0 || T < 0 || D <= 0 || W <= 0 || norm_group < 0)
     return fail(GDN_ERR_ARG, "invalid sizes B=%d T=%d D=%d W=%d norm_group=%d", B, T, D, W, norm_group);
@@ -590,9 +590,9 @@ static int conv_check(int B, int T, int D, int64_t ldx, int W, int norm_group, i
                 "norm_group in {0, 64, 128, 256} dividing D)", D, W, norm_group);
   // each lane reads 4 consecutive channels of a token row: rows start on 4-channel boundaries
   if (ldx < D || ldx % 4 != 0)
-    return fail(GDN_ERR_ARG, "ldx = %lld must be >= D = %d and a multiple of 4", (long long)ldx, D);
+    return fail(GDN_ERR_ARG, "%s = %lld must be >= D = %d and a multiple of 4", ld_name, (long long)ldx, D);
   if ((int64_t)T * ldx * (dtype == DT_BF16 ? 2 : 4) >= ((int64_t)1 << 31))
-    return fail(GDN_ERR_ARG, "T * ldx = %lld too large for the conv backward's 32-bit row offsets",
+    return fail(GDN_ERR_ARG, "T * %s = %lld too large for the conv backward's 32-bit row offsets", ld_name,
                 (long long)T * ldx);
   return GDN_OK;
 }
@@ -624,11 +624,13 @@ int gdn_short_conv_fwd(const void* x, int64_t ldx, const float* w, const float* 
 }
 
 int gdn_short_conv_bwd(const void* x, int64_t ldx, const float* w, const float* bias, const void* state_in,
-                       const void* dy, void* dx, float* dw, float* dbias, void* dstate_in, void* ws, size_t ws_bytes,
-                       int B, int T, int D, int W, int norm_group, int dtype, void* stream) {
+                       const void* dy, void* dx, int64_t lddx, float* dw, float* dbias, void* dstate_in, void* ws,
+                       size_t ws_bytes, int B, int T, int D, int W, int norm_group, int dtype, void* stream) {
   g_err[0] = 0;
   if (ldx == 0) ldx = D;
+  if (lddx == 0) lddx = D;
   if (int e = conv_check(B, T, D, ldx, W, norm_group, dtype)) return e;
+  if (int e = conv_check(B, T, D, lddx, W, norm_group, dtype, "lddx")) return e;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (B == 0 || T == 0) {
     hipError_t e = copy_or_zero_bytes(nullptr, dw, (size_t)D * W * 4, st);
@@ -647,7 +649,7 @@ int gdn_short_conv_bwd(const void* x, int64_t ldx, const float* w, const float* 
   ConvArgs a{};
   a.x = x; a.w = w; a.bias = bias; a.state_in = state_in; a.dy = dy; a.dx = dx; a.dstate_in = dstate_in;
   a.dw = dw; a.dbias = dbias; a.ws = ws;
-  a.B = B; a.T = T; a.D = D; a.ldx = ldx; a.norm_group = norm_group; a.dtype = dtype; a.stream = st;
+  a.B = B; a.T = T; a.D = D; a.ldx = ldx; a.lddx = lddx; a.norm_group = norm_group; a.dtype = dtype; a.stream = st;
   const hipError_t e = timed(ST_CONV_BWD, st, [&] { return launch_conv(a, true); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "short conv backward launch: %s", hipGetErrorString(e));
   return GDN_OK;

@@ -5,8 +5,8 @@
 //   z[t,c] = bias[c] + sum_i w[c,i] x[t - (W-1) + i, c]      (x at t < 0 comes from the conv state)
 //   y[t,c] = silu(z[t,c]);  with normalisation over each group of NG channels: y / max(||y||_group, 1e-12)
 //
-// Layout: y, dy, dx [B, T, D] token-major (channel-last); x [B, T] rows of D channels ldx elements apart (ldx = D,
-// or larger to read a column slice of a wider tensor in place); w [D, W] fp32, bias [D] fp32, conv states
+// Layout: y, dy [B, T, D] token-major (channel-last); x and dx [B, T] rows of D channels ldx / lddx elements apart
+// (= D, or larger to read or write a column slice of a wider tensor in place); w [D, W] fp32, bias [D] fp32, conv states
 // [B, D, W-1] in the activation dtype (the previous W-1 inputs, oldest first).
 // Mapping: one wave per (256 channels, 64-token chunk, b); each lane holds 4 consecutive channels, so every token
 // row is one 8-byte (bf16) or 16-byte (fp32) access per lane and a wave covers 512 B / 1 KB contiguous.  The W-1
@@ -217,7 +217,8 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
                                                            const T* __restrict__ state_in,
                                                            const T* __restrict__ dy, T* __restrict__ dx,
                                                            T* __restrict__ dstate_in, float* __restrict__ part_out,
-                                                           int Tn, int D, int ldx, int nchunk, int nparts) {
+                                                           int Tn, int D, int ldx, int lddx, int nchunk,
+                                                           int nparts) {
   constexpr int CPL = CONV_CPL, U = CONV_UB;
   const int l = lane_id();
   int part, cw0;
@@ -237,9 +238,11 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
   const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(x + (int64_t)b * Tn * ldx), 0,
                                                     Tn * ldx * (int)sizeof(T), BUF_RSRC_WORD3);
   const auto rdy = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(dy + bbase), 0, bbytes, BUF_RSRC_WORD3);
-  const auto rdx = __builtin_amdgcn_make_buffer_rsrc(dx + bbase, 0, bbytes, BUF_RSRC_WORD3);
+  const auto rdx = __builtin_amdgcn_make_buffer_rsrc(dx + (int64_t)b * Tn * lddx, 0, Tn * lddx * (int)sizeof(T),
+                                                     BUF_RSRC_WORD3);
   auto boff = [&](int t) { return (t * D + cc) * (int)sizeof(T); };
   auto xoff = [&](int t) { return (t * ldx + cc) * (int)sizeof(T); };
+  auto dxoff = [&](int t) { return (t * lddx + cc) * (int)sizeof(T); };
   float wk[CPL][W], bk[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -271,7 +274,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
       }
       if (on) {
         if (p >= 0) {
-          store4_buf_nt<T>(rdx, boff(p), o);
+          store4_buf_nt<T>(rdx, dxoff(p), o);
         } else if (dstate_in) {
 #pragma unroll
           for (int j = 0; j < CPL; ++j) dstate_in[srow + (int64_t)j * (W - 1) + (W - 1) + p] = from_f<T>(o[j]);
@@ -427,7 +430,8 @@ static hipError_t conv_bwd_k(const ConvArgs& a) {
   float* part = static_cast<float*>(a.ws);
   conv_silu_bwd_kernel<T, 4, NG><<<conv_grid(a.D, nparts), 64 * CONV_WAVES, 0, a.stream>>>(
       static_cast<const T*>(a.x), a.w, a.bias, static_cast<const T*>(a.state_in), static_cast<const T*>(a.dy),
-      static_cast<T*>(a.dx), static_cast<T*>(a.dstate_in), part, a.T, a.D, (int)a.ldx, nchunk, nparts);
+      static_cast<T*>(a.dx), static_cast<T*>(a.dstate_in), part, a.T, a.D, (int)a.ldx, (int)a.lddx, nchunk,
+      nparts);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_column_sum(part, nparts, a.D * 4 + a.D, ColumnOut{{a.dw, a.dbias, nullptr}, {a.D * 4, a.D, 0}},

@@ -100,12 +100,12 @@ struct ConvArgs {
   void* y;                // [B, T, D] (forward)
   void* state_out;        // [B, D, W-1] or null (forward)
   const void* dy;         // backward
-  void* dx;
+  void* dx;               // [B, T] rows of D channels, lddx elements apart
   void* dstate_in;        // or null
   float *dw, *dbias;      // dbias may be null
   void* ws;
   int B, T, D, norm_group, dtype;
-  int64_t ldx;
+  int64_t ldx, lddx;  // row strides of x and dx (>= D)
   hipStream_t stream;
 };
 size_t conv_ws_bytes(int B, int T, int D, int W);

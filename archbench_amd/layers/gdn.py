@@ -99,15 +99,22 @@ class GatedDeltaNet(nn.Module):
         self.o_norm = GatedRMSNorm(self.head_v_dim, norm_eps)
         self.o_proj = nn.Linear(self.value_dim, hidden_size, bias=False)
 
+    def _wide_projection(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        """[q | k | v (| gate)] = hidden_states against the concatenated weights of those linears, one GEMM."""
+        wide = [self.q_proj, self.k_proj, self.v_proj] + ([self.g_proj] if self.use_gate else [])
+        return F.linear(hidden_states, torch.cat([m.weight for m in wide], 0))
+
+    def _ab_projection(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        ab = F.linear(hidden_states, torch.cat([self.a_proj.weight, self.b_proj.weight], 0))
+        return torch.split(ab, [self.a_proj.out_features, self.b_proj.out_features], dim=-1)
+
     def input_projections(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, ...]:
         """(q, k, v, a, b[, gate]) = the six linears of ``hidden_states``, computed as two GEMMs: q, k, v (and
         the gate) against their concatenated weights, a and b against theirs."""
-        wide = [self.q_proj, self.k_proj, self.v_proj] + ([self.g_proj] if self.use_gate else [])
-        y = F.linear(hidden_states, torch.cat([m.weight for m in wide], 0))
-        q, k, v, *gate = torch.split(y, [m.out_features for m in wide], dim=-1)
-        a, b = torch.split(F.linear(hidden_states, torch.cat([self.a_proj.weight, self.b_proj.weight], 0)),
-                           [self.a_proj.out_features, self.b_proj.out_features], dim=-1)
-        return (q, k, v, a, b, *gate)
+        q, k, v, *gate = torch.split(self._wide_projection(hidden_states),
+                                     [self.key_dim, self.key_dim, self.value_dim] + [self.value_dim] * self.use_gate,
+                                     dim=-1)
+        return (q, k, v, *self._ab_projection(hidden_states), *gate)
 
     def forward(self, hidden_states: torch.Tensor, attention_mask: torch.Tensor | None = None,
                 past_key_values: dict | None = None, use_cache: bool = False, output_attentions: bool = False,
@@ -122,14 +129,25 @@ class GatedDeltaNet(nn.Module):
         H, DK, DV = self.num_heads, self.head_k_dim, self.head_v_dim
         entry = None if past_key_values is None else past_key_values.get(self.layer_idx)
         conv_in = entry["conv_state"] if entry is not None else (None, None, None)
-        q, k, v, a, b, *gp = self.input_projections(hidden_states)
         conv_out = (None, None, None)
-        if self.use_short_conv:
-            (q, cq), (k, ck), (v, cv) = (self.q_conv1d(q, conv_in[0]), self.k_conv1d(k, conv_in[1]),
-                                         self.v_conv1d(v, conv_in[2]))
-            conv_out = (cq, ck, cv)
+        convs = (self.q_conv1d, self.k_conv1d, self.v_conv1d) if self.use_short_conv else ()
+        if convs and entry is None and not use_cache and all(c.bias is None for c in convs):
+            # training / prefill without a cache: the convolutions read q, k, v straight out of the projection's
+            # output and their backward writes into one gradient of it (ops.mixer_input_stage); the weights are
+            # rounded to the activation dtype first, as ShortConvolution does
+            y = self._wide_projection(hidden_states)
+            a, b = self._ab_projection(hidden_states)
+            wq, wk, wv = (c.weight.squeeze(1).to(y.dtype).float() for c in convs)
+            q, k, v, gcols = ops.mixer_input_stage(y, wq, wk, wv, self.key_dim, self.value_dim, DK)
+            gp = [gcols] if self.use_gate else []
         else:
-            q, k, v = F.silu(q), F.silu(k), F.silu(v)
+            q, k, v, a, b, *gp = self.input_projections(hidden_states)
+            if convs:
+                (q, cq), (k, ck), (v, cv) = (self.q_conv1d(q, conv_in[0]), self.k_conv1d(k, conv_in[1]),
+                                             self.v_conv1d(v, conv_in[2]))
+                conv_out = (cq, ck, cv)
+            else:
+                q, k, v = F.silu(q), F.silu(k), F.silu(v)
         q, k, v = q.reshape(B, T, H, DK), k.reshape(B, T, H, DK), v.reshape(B, T, H, DV)
         # g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b) (x2 with negative eigenvalues), one HIP pass
         g, beta = ops.gdn_gates(a, b, self.A_log, self.dt_bias, None, 2.0 if self.allow_neg_eigval else 1.0,

@@ -134,9 +134,9 @@ int gdn_recurrent_step(const void* q, const void* k, const void* v, const float*
  *   z[t,c] = bias[c] + sum_i w[c,i] x[t-(W-1)+i, c],   y = silu(z),   y <- y / max(||y||_group, 1e-12).
  * Replaces the ShortConv + causal_conv1d custom ops archbench::causal_conv_silu / _bwd
  * (archbench/layers/nsgdn.py:420-470; fla's ShortConvolution in GatedDeltaNet) and the per-head normalisation
- * of q and k (nsgdn.py:527-528).  y, dy, dx [B, T, D] token-major in dtype; x [B, T] rows of D channels ldx
- * elements apart (ldx = D, or 0, for a contiguous x; a larger ldx reads x in place as a column slice of a wider
- * [B, T, ldx] tensor, such as one output of a fused input projection; ldx a multiple of 4);
+ * of q and k (nsgdn.py:527-528).  y, dy [B, T, D] token-major in dtype; x and dx [B, T] rows of D channels ldx /
+ * lddx elements apart (D, or 0, when contiguous; larger to read x from, or write dx into, a column slice of a
+ * wider [B, T, ld] tensor such as the output of a fused input projection or its gradient; a multiple of 4);
  * w [D, W] and bias [D] fp32 (bias may be NULL); conv states [B, D, W-1] in dtype, the previous W-1 inputs oldest
  * first (state_in NULL = zeros; state_out NULL = not returned; it must not alias state_in).  Compiled for W = 4,
  * D % 4 == 0, norm_group in {0 (none), 64, 128, 256}.
@@ -146,8 +146,8 @@ int gdn_short_conv_fwd(const void* x, int64_t ldx, const float* w, const float* 
                        void* state_out, int B, int T, int D, int W, int norm_group, int dtype, void* stream);
 int gdn_short_conv_bwd_ws_bytes(int B, int T, int D, int W, size_t* bytes);
 int gdn_short_conv_bwd(const void* x, int64_t ldx, const float* w, const float* bias, const void* state_in,
-                       const void* dy, void* dx, float* dw, float* dbias, void* dstate_in, void* ws, size_t ws_bytes,
-                       int B, int T, int D, int W, int norm_group, int dtype, void* stream);
+                       const void* dy, void* dx, int64_t lddx, float* dw, float* dbias, void* dstate_in, void* ws,
+                       size_t ws_bytes, int B, int T, int D, int W, int norm_group, int dtype, void* stream);
 
 /* Gated RMSNorm of the op's output, per row of `dim` channels (one head of one token):
  *   y = x * rsqrt(mean(x^2) + eps) * weight * silu(gate)

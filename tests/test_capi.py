@@ -123,9 +123,12 @@ def test_strided_input_layouts_are_validated_before_any_launch():
     assert rc == _lib.GDN_ERR_ARG and b"ldx" in lib.gdn_last_error()
     rc = lib.gdn_short_conv_fwd(p, 130, p, None, None, p, None, 1, 8, 128, 4, 0, _lib.DTYPE_BF16, None)
     assert rc == _lib.GDN_ERR_ARG and b"multiple of 4" in lib.gdn_last_error()
-    rc = lib.gdn_short_conv_bwd(p, 64, p, None, None, p, p, p, None, None, p, 1 << 20, 1, 8, 128, 4, 0,
+    rc = lib.gdn_short_conv_bwd(p, 64, p, None, None, p, p, 0, p, None, None, p, 1 << 20, 1, 8, 128, 4, 0,
                                 _lib.DTYPE_BF16, None)
     assert rc == _lib.GDN_ERR_ARG and b"ldx" in lib.gdn_last_error()
+    rc = lib.gdn_short_conv_bwd(p, 0, p, None, None, p, p, 126, p, None, None, p, 1 << 20, 1, 8, 128, 4, 0,
+                                _lib.DTYPE_BF16, None)
+    assert rc == _lib.GDN_ERR_ARG and b"lddx" in lib.gdn_last_error()
     rc = lib.gdn_gated_rmsnorm_fwd(p, p, 3072, 4, None, p, 10, 256, 1e-5, _lib.DTYPE_BF16, None)
     assert rc == _lib.GDN_ERR_ARG and b"gate layout" in lib.gdn_last_error()
     rc = lib.gdn_gated_rmsnorm_fwd(p, p, 512, 4, None, p, 8, 256, 1e-5, _lib.DTYPE_BF16, None)

@@ -174,3 +174,34 @@ def test_conv_reads_a_column_slice_in_place(dtype, T, ng):
     y.float().sum().backward()
     assert torch.equal(xa.grad, ops.short_conv_bwd(xc, w, None, None, torch.ones_like(dy), ng)[0])
     assert torch.equal(wide, before)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("gate_dim", [0, 256])
+def test_mixer_input_stage_equals_separate_convs(dtype, gate_dim):
+    """The fused input stage (q, k, v convolved out of one projection output, the gate passed on) gives exactly
+    the separate short convs' outputs, and its backward exactly their input gradients written into the column
+    slices of one dy (the concatenation autograd would otherwise build) plus the gate's gradient."""
+    banner(f"mixer input stage dtype={dtype} gate_dim={gate_dim}")
+    B, T, kd, vd, ng = 2, 130, 256, 512, 128
+    L = 2 * kd + vd + gate_dim
+    gen = torch.Generator().manual_seed(11)
+    y = torch.randn(B, T, L, generator=gen).to("cuda", dtype)
+    ws = [(torch.randn(d, W, generator=gen) * 0.5).cuda() for d in (kd, kd, vd)]
+    outs = ops.mixer_input_stage(y, *ws, kd, vd, ng)
+    cols = [(0, kd, ng), (kd, kd, ng), (2 * kd, vd, 0)]
+    for o, w, (c0, d, g) in zip(outs[:3], ws, cols):
+        assert torch.equal(o, ops.short_conv(y[..., c0:c0 + d].contiguous(), w, None, None, g)[0])
+    assert torch.equal(outs[3], y[..., 2 * kd + vd:])
+    grads = [torch.randn(o.shape, generator=gen).to("cuda", dtype) for o in outs]
+    dy, *dws = ops.mixer_input_stage_bwd(y, *ws, *grads, kd, vd, ng)
+    for (c0, d, g), w, gr, dw in zip(cols, ws, grads, dws):
+        dx_ref, dw_ref, _, _ = ops.short_conv_bwd(y[..., c0:c0 + d].contiguous(), w, None, None, gr, g)
+        assert torch.equal(dy[..., c0:c0 + d], dx_ref) and torch.equal(dw, dw_ref)
+    assert torch.equal(dy[..., 2 * kd + vd:], grads[3])
+    # through autograd: every input gradient of the stage at once
+    ya = y.detach().requires_grad_()
+    wa = [w.detach().requires_grad_() for w in ws]
+    out = ops.mixer_input_stage(ya, *wa, kd, vd, ng)
+    torch.autograd.backward(out, grads)
+    assert torch.equal(ya.grad, dy) and all(torch.equal(w.grad, d) for w, d in zip(wa, dws))

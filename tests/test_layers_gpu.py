@@ -202,3 +202,26 @@ def test_decode_shapes_without_step_kernel(K, V):
                                                      output_final_state=True, inplace_final_state=True)
     assert S1 is S
     assert rel_l2(o[:, 0], o_ref) <= 1e-2 and rel_l2(S, S_ref) <= 1e-2
+
+
+def test_layer_under_torch_compile():
+    """The mixer compiled as the reference trainer compiles the model (torch.compile(dynamic=False), bf16
+    autocast): forward and backward match eager, through the custom ops' fake implementations."""
+    banner("layer under torch.compile(dynamic=False)")
+    m = _layer()
+    x = torch.randn(2, 128, 256, device="cuda", generator=torch.Generator("cuda").manual_seed(3))
+
+    def run(fn):
+        for p in m.parameters():
+            p.grad = None
+        xi = x.clone().requires_grad_()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = fn(xi)
+        y.float().square().sum().backward()
+        return y.float(), xi.grad, {n: p.grad.clone() for n, p in m.named_parameters()}
+
+    y0, gx0, gp0 = run(m)
+    y1, gx1, gp1 = run(torch.compile(m, dynamic=False))
+    assert rel_l2(y1, y0) <= 1e-2 and rel_l2(gx1, gx0) <= 1e-2
+    for n in gp0:
+        assert rel_l2(gp1[n], gp0[n]) <= 2e-2, n
