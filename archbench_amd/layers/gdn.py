@@ -127,6 +127,11 @@ class GatedDeltaNet(nn.Module):
             raise ValueError("padding masks are not supported by the gated DeltaNet layer")
         B, T, _ = hidden_states.shape
         H, DK, DV = self.num_heads, self.head_k_dim, self.head_v_dim
+        dev_type = hidden_states.device.type
+        if torch.is_autocast_enabled(dev_type) and hidden_states.dtype == torch.float32:
+            # the cast autocast would make in front of each projection GEMM, made once for both (and one cast of
+            # the input gradient back in the backward instead of two and their fp32 sum)
+            hidden_states = hidden_states.to(torch.get_autocast_dtype(dev_type))
         entry = None if past_key_values is None else past_key_values.get(self.layer_idx)
         conv_in = entry["conv_state"] if entry is not None else (None, None, None)
         conv_out = (None, None, None)

@@ -178,11 +178,17 @@ def _chunk_setup(ctx, inputs, output):
     ctx.scale = scale
     ctx.has_h0 = h0 is not None
     ctx.g_dtype, ctx.beta_dtype = g.dtype, beta.dtype
+    # an unused final state gets no zero-filled gradient (the kernels take dhT = NULL)
+    ctx.set_materialize_grads(False)
+
+
+def _zero_do(do: Optional[Tensor], q: Tensor, v: Tensor) -> Tensor:
+    return do if do is not None else torch.zeros(*q.shape[:3], v.shape[-1], dtype=q.dtype, device=q.device)
 
 
 def _chunk_backward(ctx, do, dhT):
     q, k, v, g, beta, h0 = ctx.saved_tensors
-    dq, dk, dv, dg, db, dh0 = chunk_bwd(q, k, v, g, beta, h0, do.contiguous(),
+    dq, dk, dv, dg, db, dh0 = chunk_bwd(q, k, v, g, beta, h0, _zero_do(do, q, v).contiguous(),
                                         None if dhT is None else dhT.contiguous(), ctx.scale)
     return dq, dk, dv, dg.to(ctx.g_dtype), db.to(ctx.beta_dtype), (dh0 if ctx.has_h0 else None), None
 
@@ -263,11 +269,14 @@ def _stash_setup(ctx, inputs, output):
     ctx.scale = scale
     ctx.has_h0 = h0 is not None
     ctx.g_dtype, ctx.beta_dtype = g.dtype, beta.dtype
+    # no zero-filled gradients for the unused final state or the (integer) stash: the stash of a long sequence
+    # is hundreds of MB, and autograd would otherwise fill a zero gradient of it every step
+    ctx.set_materialize_grads(False)
 
 
 def _stash_backward(ctx, do, dhT, _dstash):
     q, k, v, g, beta, h0, stash = ctx.saved_tensors
-    dq, dk, dv, dg, db, dh0 = chunk_bwd_stashed(q, k, v, g, beta, h0, do.contiguous(),
+    dq, dk, dv, dg, db, dh0 = chunk_bwd_stashed(q, k, v, g, beta, h0, _zero_do(do, q, v).contiguous(),
                                                 None if dhT is None else dhT.contiguous(), stash, ctx.scale)
     return dq, dk, dv, dg.to(ctx.g_dtype), db.to(ctx.beta_dtype), (dh0 if ctx.has_h0 else None), None
 
@@ -358,6 +367,7 @@ def _nsgdn_setup(ctx, inputs, output):
     ctx.scale = scale
     ctx.has_h0 = h0 is not None
     ctx.la_dtype = la.dtype
+    ctx.set_materialize_grads(False)  # as for the gated delta rule's stash pair
 
 
 def _nsgdn_backward(ctx, dy, dhT, _dstash):
