@@ -30,6 +30,52 @@ import torch.nn.functional as F
 from .. import ops
 
 
+def _weight_grad(dy: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """dW = dy^T x (dy [M, N], x [M, K]) in fp32, split over the M tokens: a batch of chunk products summed in fp32.
+    A weight gradient reduces over every token into a small N x K output; as one GEMM it has too few output tiles
+    to fill the GPU (hipBLASLt at B64 T1024: 131 us for N = 8, K = 512; 248 us for N = 512, K = 1024; 400 us for
+    N = 3072, K = 512), split 8 or 16 ways 34, 211 and 322 us.  The smaller operand is transposed into contiguous
+    chunks, so neither product operand is a transposed view."""
+    M, N = dy.shape
+    K = x.shape[1]
+    C = 16 if N <= K else 8
+    if dy.dtype == torch.float32:
+        return dy.t() @ x
+    if M % C or M // C < 1024:
+        return torch.mm(dy.t(), x, out_dtype=torch.float32)
+    if N <= K:
+        dyt = dy.view(C, M // C, N).transpose(1, 2).contiguous()
+        return torch.bmm(dyt, x.view(C, M // C, K), out_dtype=torch.float32).sum(0)
+    xt = x.view(C, M // C, K).transpose(1, 2).contiguous()
+    return torch.bmm(xt, dy.view(C, M // C, N), out_dtype=torch.float32).sum(0).t()
+
+
+class _Linear(torch.autograd.Function):
+    """y = x W^T with W cast to x's dtype (as autocast casts it); the backward's weight gradient split over the
+    tokens (_weight_grad) and returned in W's dtype."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        wc = w.to(x.dtype)
+        ctx.save_for_backward(x, wc)
+        ctx.w_dtype = w.dtype
+        return F.linear(x, wc)
+
+    @staticmethod
+    def backward(ctx, dy: torch.Tensor):
+        x, wc = ctx.saved_tensors
+        lead = dy.shape[:-1]
+        dy2 = dy.reshape(-1, dy.shape[-1])
+        dx = (dy2 @ wc).view(*lead, wc.shape[1]) if ctx.needs_input_grad[0] else None
+        dw = _weight_grad(dy2, x.reshape(-1, x.shape[-1])).to(ctx.w_dtype) if ctx.needs_input_grad[1] else None
+        return dx, dw
+
+
+def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """F.linear for a bf16 (or fp32) activation under the layer's own cast; the split-K weight gradient on GPUs."""
+    return _Linear.apply(x, w) if x.is_cuda else F.linear(x, w.to(x.dtype))
+
+
 class ShortConvolution(nn.Module):
     """Depthwise causal conv1d (kernel ``size``) + SiLU over [B, T, D] (the ShortConv of nsgdn.py:457-470), on
     the HIP kernel (``ops.short_conv``).  With ``state`` ([B, D, size-1], the previous inputs) it continues a
@@ -102,10 +148,10 @@ class GatedDeltaNet(nn.Module):
     def _wide_projection(self, hidden_states: torch.Tensor) -> torch.Tensor:
         """[q | k | v (| gate)] = hidden_states against the concatenated weights of those linears, one GEMM."""
         wide = [self.q_proj, self.k_proj, self.v_proj] + ([self.g_proj] if self.use_gate else [])
-        return F.linear(hidden_states, torch.cat([m.weight for m in wide], 0))
+        return _linear(hidden_states, torch.cat([m.weight for m in wide], 0))
 
     def _ab_projection(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        ab = F.linear(hidden_states, torch.cat([self.a_proj.weight, self.b_proj.weight], 0))
+        ab = _linear(hidden_states, torch.cat([self.a_proj.weight, self.b_proj.weight], 0))
         return torch.split(ab, [self.a_proj.out_features, self.b_proj.out_features], dim=-1)
 
     def input_projections(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, ...]:
@@ -179,4 +225,4 @@ class GatedDeltaNet(nn.Module):
             past_key_values[self.layer_idx] = {"recurrent_state": new_state, "conv_state": conv_out}
         gate = gp[0].reshape(B, T, H, DV) if self.use_gate else None
         o = self.o_norm(o, gate)
-        return self.o_proj(o.reshape(B, T, -1)), None, past_key_values
+        return _linear(o.reshape(B, T, -1), self.o_proj.weight), None, past_key_values

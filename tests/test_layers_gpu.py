@@ -225,3 +225,27 @@ def test_layer_under_torch_compile():
     assert rel_l2(y1, y0) <= 1e-2 and rel_l2(gx1, gx0) <= 1e-2
     for n in gp0:
         assert rel_l2(gp1[n], gp0[n]) <= 2e-2, n
+
+
+@pytest.mark.parametrize("N,K", [(8, 512), (512, 1024), (3072, 512), (24, 40)])
+def test_split_weight_gradient(N, K):
+    """The layer's weight gradient split over the tokens equals dy^T x to fp32 accumulation (both operand orders,
+    and the single-product fallback for short inputs), and the layer's linear backward returns it in the
+    weight's dtype."""
+    from archbench_amd.layers.gdn import _linear, _weight_grad
+    banner(f"split weight gradient N={N} K={K}")
+    M = 16384 if N != 24 else 1000
+    gen = torch.Generator("cuda").manual_seed(7)
+    dy = torch.randn(M, N, device="cuda", generator=gen).to(torch.bfloat16)
+    x = torch.randn(M, K, device="cuda", generator=gen).to(torch.bfloat16)
+    ref = dy.double().t() @ x.double()
+    got = _weight_grad(dy, x)
+    assert got.dtype == torch.float32 and got.shape == (N, K)
+    assert rel_l2(got.double(), ref) <= 1e-5
+    w = torch.randn(N, K, device="cuda", generator=gen).requires_grad_()
+    xa = x.clone().requires_grad_()
+    y = _linear(xa, w)
+    assert torch.equal(y, torch.nn.functional.linear(x, w.to(torch.bfloat16)))
+    y.backward(dy)
+    assert w.grad.dtype == torch.float32 and rel_l2(w.grad.double(), ref) <= 1e-5
+    assert torch.equal(xa.grad, dy @ w.detach().to(torch.bfloat16))
