@@ -32,6 +32,7 @@ import torch.nn.functional as F
 
 from .. import ops
 from . import register
+from .gdn import _linear
 
 
 def write_direction(k: torch.Tensor, p: torch.Tensor, beta: torch.Tensor, lam: torch.Tensor,
@@ -87,17 +88,23 @@ class NStepGDN(nn.Module):
         B, T, _ = x.shape
         H, DK, DV = self.H, self.DK, self.DV
         n_qkv = 2 * self.qk_dim + self.v_dim
-        proj = self.in_proj(x)
-        qkv = proj[..., :n_qkv]
-        g = proj[..., n_qkv:n_qkv + self.n_gate]
-        ab = proj[..., n_qkv + self.n_gate:n_qkv + self.n_gate + 2 * H]
-        qs, ks, vs = qkv[..., :self.qk_dim], qkv[..., self.qk_dim:2 * self.qk_dim], qkv[..., 2 * self.qk_dim:]
+        n_main = n_qkv + self.n_gate
+        dev_type = x.device.type
+        xp = x
+        if torch.is_autocast_enabled(dev_type) and x.dtype == torch.float32:
+            xp = x.to(torch.get_autocast_dtype(dev_type))  # autocast's cast, made once for both GEMMs below
+        # in_proj's rows [q k v | gate] and [a b] as two GEMMs (the first a multiple of 256 wide at the reference
+        # shapes); the rows past them pad the projection and are not computed (their gradient is zero)
+        w_in = self.in_proj.weight
+        y = _linear(xp, w_in[:n_main])
+        ab = _linear(xp, w_in[n_main:n_main + 2 * H])
         if self.conv is not None:
-            w = self.conv.weight.squeeze(1).to(qkv.dtype).float()  # rounded as the reference's conv runs it
-            q, _ = ops.short_conv(qs, w[:self.qk_dim], None, None, DK)
-            k, _ = ops.short_conv(ks, w[self.qk_dim:2 * self.qk_dim], None, None, DK)
-            v, _ = ops.short_conv(vs, w[2 * self.qk_dim:], None, None, 0)
+            w = self.conv.weight.squeeze(1).to(y.dtype).float()  # rounded as the reference's conv runs it
+            # q, k, v convolved straight out of y; the gate columns passed on (ops.mixer_input_stage)
+            q, k, v, g = ops.mixer_input_stage(y, w[:self.qk_dim], w[self.qk_dim:2 * self.qk_dim],
+                                               w[2 * self.qk_dim:], self.qk_dim, self.v_dim, DK)
         else:
+            qs, ks, vs, g = torch.split(y, [self.qk_dim, self.qk_dim, self.v_dim, self.n_gate], dim=-1)
             q, k, v = ops.l2norm(qs, 1e-12, 1.0), ops.l2norm(ks, 1e-12, 1.0), vs
         q, k, v = q.view(B, T, H, DK), k.view(B, T, H, DK), v.reshape(B, T, H, DV)
         la, beta = ops.gdn_gates(ab[..., :H], ab[..., H:], self.A_log, self.dt_bias, self.b_bias, 1.0,
@@ -106,9 +113,9 @@ class NStepGDN(nn.Module):
         p = F.pad(kf[:, :-1], (0, 0, 0, 0, 1, 0))
         u = write_direction(kf, p, beta, F.softplus(self.lam.float()), self.n_steps)
         y = ops.nsgdn_scan_chunk(q, k, u, v, la, scale=DK ** -0.5)
-        gate = g.view(B, T, H, DV) if self.use_gate else None
-        y = ops.gated_rmsnorm(y.to(x.dtype), gate, self.norm.weight, self.norm.eps or 1e-5)
-        return self.o_proj(y.reshape(B, T, -1))
+        gate = g.reshape(B, T, H, DV) if self.use_gate else None
+        y = ops.gated_rmsnorm(y.to(xp.dtype), gate, self.norm.weight, self.norm.eps or 1e-5)
+        return _linear(y.reshape(B, T, -1), self.o_proj.weight)
 
 
 class _ConvWeight(nn.Module):
