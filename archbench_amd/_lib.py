@@ -54,11 +54,13 @@ SIGNATURES = {
     "gdn_gates_bwd_ws_bytes": (_i, [_i64, _i, ctypes.POINTER(_sz)]),
     "gdn_gates_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i, _f, _f, _i, _p]),
     "gdn_cross_entropy_fwd_bwd": (_i, [_p, _p, _p, _p, _p, _i64, _i, _i64, _i64, _i, _p]),
+    "gdn_write_direction_fwd": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
+    "gdn_write_direction_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "gdn_profile_enable": (_i, [_i]),
     "gdn_profile_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
     "gdn_profile_stage_name": (ctypes.c_char_p, [_i]),
 }
-PROFILE_STAGES = 19
+PROFILE_STAGES = 21
 
 _lock = threading.Lock()
 _lib = None

@@ -159,12 +159,12 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
 enum Stage {
   ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_FACTORS, ST_CONV_FWD,
   ST_CONV_BWD, ST_NORM_FWD, ST_NORM_BWD, ST_GATES_FWD, ST_GATES_BWD, ST_L2_FWD, ST_L2_BWD, ST_CE, ST_PREFIX,
-  ST_SEGSCAN, ST_BWD_LOCAL, ST_COUNT
+  ST_SEGSCAN, ST_BWD_LOCAL, ST_WD_FWD, ST_WD_BWD, ST_COUNT
 };
 static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step", "fwd_stash",
                                             "factors", "conv_fwd", "conv_bwd", "norm_fwd", "norm_bwd", "gates_fwd", "gates_bwd",
                                             "l2norm_fwd", "l2norm_bwd", "cross_entropy", "prefix", "seg_scan",
-                                            "bwd_local"};
+                                            "bwd_local", "write_dir_fwd", "write_dir_bwd"};
 struct ProfRec { int stage; hipEvent_t a, b; };
 struct Prof {
   std::atomic<bool> on{false};
@@ -768,6 +768,48 @@ int gdn_cross_entropy_fwd_bwd(void* logits, const int64_t* target, float* loss, 
   a.stream = static_cast<hipStream_t>(stream);
   const hipError_t e = timed(ST_CE, a.stream, [&] { return launch_ce(a); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "cross entropy launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+static int write_dir_check(int B, int T, int H, int K, int n_steps, int dtype) {
+  if (dtype != DT_F32 && dtype != DT_BF16) return fail(GDN_ERR_ARG, "dtype code %d is not GDN_DTYPE_F32/BF16", dtype);
+  if (B < 0 || T < 0 || H <= 0 || K <= 0) return fail(GDN_ERR_ARG, "invalid sizes B=%d T=%d H=%d K=%d", B, T, H, K);
+  if (!write_dir_supported(K, n_steps))
+    return fail(GDN_ERR_SHAPE, "write direction not compiled for K=%d n_steps=%d (K in {64, 128, 256}, "
+                "1 <= n_steps <= 8)", K, n_steps);
+  return GDN_OK;
+}
+
+int gdn_write_direction_fwd(const void* k, const float* beta, const float* lam, void* u, int B, int T, int H, int K,
+                            int n_steps, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (int e = write_dir_check(B, T, H, K, n_steps, dtype)) return e;
+  if ((int64_t)B * T == 0) return GDN_OK;
+  if (!k || !beta || !lam || !u) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(k, u)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
+  WriteDirArgs a{};
+  a.k = k; a.beta = beta; a.lam = lam; a.u = u;
+  a.B = B; a.T = T; a.H = H; a.K = K; a.n_steps = n_steps; a.dtype = dtype;
+  a.stream = static_cast<hipStream_t>(stream);
+  const hipError_t e = timed(ST_WD_FWD, a.stream, [&] { return launch_write_dir(a, false); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "write direction forward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+int gdn_write_direction_bwd(const void* k, const float* beta, const float* lam, const void* du, void* dk,
+                            float* dbeta, float* dlam, int B, int T, int H, int K, int n_steps, int dtype,
+                            void* stream) {
+  g_err[0] = 0;
+  if (int e = write_dir_check(B, T, H, K, n_steps, dtype)) return e;
+  if ((int64_t)B * T == 0) return GDN_OK;
+  if (!k || !beta || !lam || !du || !dk || !dbeta || !dlam) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(k, du, dk)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
+  WriteDirArgs a{};
+  a.k = k; a.beta = beta; a.lam = lam; a.du = du; a.dk = dk; a.dbeta = dbeta; a.dlam = dlam;
+  a.B = B; a.T = T; a.H = H; a.K = K; a.n_steps = n_steps; a.dtype = dtype;
+  a.stream = static_cast<hipStream_t>(stream);
+  const hipError_t e = timed(ST_WD_BWD, a.stream, [&] { return launch_write_dir(a, true); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "write direction backward launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }
 

@@ -179,6 +179,21 @@ struct CeArgs {
 bool ce_shape_supported(int V, int64_t ld);
 hipError_t launch_ce(const CeArgs& a);
 
+// Write direction of the n-step family (gdn_writedir.hip): k [B,T,H,K] -> u, and the backward.
+struct WriteDirArgs {
+  const void* k;
+  const float* beta;  // [B, T, H]
+  const float* lam;   // [H], the effective lam (after the module's softplus)
+  void* u;            // forward
+  const void* du;     // backward
+  void* dk;
+  float *dbeta, *dlam;  // [B, T, H]; dlam per row (summed over rows by the caller)
+  int B, T, H, K, n_steps, dtype;
+  hipStream_t stream;
+};
+bool write_dir_supported(int K, int n_steps);
+hipError_t launch_write_dir(const WriteDirArgs& a, bool backward);
+
 // Compute units of the current device (cached per device; 256 if the query fails).
 int device_cu_count();
 // Whether a state sweep with `blocks_per_head` 32-column blocks per (b, h) runs those narrow blocks (four waves

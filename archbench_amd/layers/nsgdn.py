@@ -9,7 +9,8 @@ zero-init rule for ``o_proj`` (archbench/model.py:14, :80-82) apply.  The forwar
     qkv = conv(in_proj(x)) with SiLU           -> ops.short_conv, three calls on the weight's row slices, q and k
                                                   L2-normalised per head inside the conv (nsgdn.py:527-528)
     la, beta from ab                           -> ops.gdn_gates (nsgdn.py:531-534, optional la_min clamp)
-    u = write_direction(k, p, beta, lam, n)    -> PyTorch elementwise (nsgdn.py:61-75, :535-536)
+    u = write_direction(k, p, beta, lam, n)    -> ops.write_direction, one HIP pass each way with p = the previous
+                                                  token's k (nsgdn.py:61-75, :535-536)
     y = scan(q, k, u, v, la)                   -> ops.nsgdn_scan_chunk, the chunk kernels with write keys u; the
                                                   q scale DK^-1/2 is the op's scale instead of a separate pass
     y = norm(y) * silu(g); o_proj              -> ops.gated_rmsnorm
@@ -38,7 +39,8 @@ from .gdn import _linear
 def write_direction(k: torch.Tensor, p: torch.Tensor, beta: torch.Tensor, lam: torch.Tensor,
                     n_steps: int) -> torch.Tensor:
     """u_1 = beta k; then n_steps - 1 steps u <- u - lam beta (p . u) p_perp, p_perp = p - (p . k) k
-    (nsgdn.py:61-75).  k, p [B,T,H,K]; beta [B,T,H]; lam [H]."""
+    (nsgdn.py:61-75).  k, p [B,T,H,K]; beta [B,T,H]; lam [H].  The reference's function with an explicit p, in
+    PyTorch (any device); the mixer runs ops.write_direction, which takes p as the previous token's k."""
     b = beta[..., None]
     u = b * k
     if n_steps > 1:
@@ -109,9 +111,9 @@ class NStepGDN(nn.Module):
         q, k, v = q.view(B, T, H, DK), k.view(B, T, H, DK), v.reshape(B, T, H, DV)
         la, beta = ops.gdn_gates(ab[..., :H], ab[..., H:], self.A_log, self.dt_bias, self.b_bias, 1.0,
                                  float("-inf") if self.la_min is None else float(self.la_min))
-        kf = k.float()
-        p = F.pad(kf[:, :-1], (0, 0, 0, 0, 1, 0))
-        u = write_direction(kf, p, beta, F.softplus(self.lam.float()), self.n_steps)
+        # u from k, the previous token's k and beta in one HIP pass (fp32 arithmetic, written in k's dtype, which
+        # the scan takes u in)
+        u = ops.write_direction(k, beta, F.softplus(self.lam.float()), self.n_steps)
         y = ops.nsgdn_scan_chunk(q, k, u, v, la, scale=DK ** -0.5)
         gate = g.reshape(B, T, H, DV) if self.use_gate else None
         y = ops.gated_rmsnorm(y.to(xp.dtype), gate, self.norm.weight, self.norm.eps or 1e-5)

@@ -41,7 +41,7 @@ from torch import Tensor
 from . import _lib
 
 __all__ = ["chunk_gated_delta_rule", "fused_recurrent_gated_delta_rule", "recurrent_step", "chunk_fwd",
-           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "nsgdn_scan_chunk", "short_conv", "mixer_input_stage",
+           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "nsgdn_scan_chunk", "short_conv", "mixer_input_stage", "write_direction",
            "gated_rmsnorm", "l2norm", "gdn_gates", "cross_entropy_fwd_bwd_"]
 
 
@@ -380,6 +380,79 @@ def _nsgdn_backward(ctx, dy, dhT, _dstash):
 
 
 nsgdn_chunk_fwd.register_autograd(_nsgdn_backward, setup_context=_nsgdn_setup)
+
+
+# The n-step family's write direction (nsgdn.py:61-75 with the shift of k at :535): u from k (p = the previous
+# token's key of the same sequence), beta and the effective lam, one HIP pass each way (gdn_writedir.hip).
+@torch.library.custom_op("archbench_amd::write_direction", mutates_args=())
+def write_direction(k: Tensor, beta: Tensor, lam: Tensor, n_steps: int) -> Tensor:
+    """u [B,T,H,K] in k's dtype: u_1 = beta k, u_{i+1} = u_i - lam beta (p . u_i) (p - (p . k) k), p = k[:, t-1]
+    (zero at t = 0).  n_steps <= 1 is u = beta k, as in the reference; at most 8 steps are compiled."""
+    _require_gpu(k, beta, lam)
+    B, T, H, K = _wd_shapes(k, beta, lam)
+    lib = _lib.load()
+    k, beta, lam = _arg(k), _arg(beta, torch.float32), _arg(lam, torch.float32)
+    u = torch.empty_like(k)
+    rc = lib.gdn_write_direction_fwd(_lib.ptr(k), _lib.ptr(beta), _lib.ptr(lam), _lib.ptr(u), B, T, H, K,
+                                     max(int(n_steps), 1), _lib.dtype_code(k.dtype), _lib.stream_ptr(k.device))
+    _lib.check(rc, "gdn_write_direction_fwd")
+    return u
+
+
+def _wd_shapes(k: Tensor, beta: Tensor, lam: Tensor):
+    if k.dim() != 4:
+        raise ValueError(f"k must be [B, T, H, K], got {tuple(k.shape)}")
+    B, T, H, K = k.shape
+    if tuple(beta.shape) != (B, T, H) or tuple(lam.shape) != (H,):
+        raise ValueError(f"beta must be [B, T, H] = {(B, T, H)} and lam [H] = [{H}], got {tuple(beta.shape)} and "
+                         f"{tuple(lam.shape)}")
+    return B, T, H, K
+
+
+@write_direction.register_fake
+def _(k, beta, lam, n_steps):
+    return torch.empty_like(k)
+
+
+@torch.library.custom_op("archbench_amd::write_direction_bwd", mutates_args=())
+def write_direction_bwd(k: Tensor, beta: Tensor, lam: Tensor, du: Tensor,
+                        n_steps: int) -> tuple[Tensor, Tensor, Tensor]:
+    """(dk in k's dtype, dbeta [B,T,H] fp32, dlam [H] fp32)."""
+    _require_gpu(k, beta, lam, du)
+    B, T, H, K = _wd_shapes(k, beta, lam)
+    lib = _lib.load()
+    k, beta, lam, du = _arg(k), _arg(beta, torch.float32), _arg(lam, torch.float32), _arg(du, k.dtype)
+    dk = torch.empty_like(k)
+    dbeta = torch.empty(B, T, H, dtype=torch.float32, device=k.device)
+    dlam_rows = torch.empty(B, T, H, dtype=torch.float32, device=k.device)
+    rc = lib.gdn_write_direction_bwd(_lib.ptr(k), _lib.ptr(beta), _lib.ptr(lam), _lib.ptr(du), _lib.ptr(dk),
+                                     _lib.ptr(dbeta), _lib.ptr(dlam_rows), B, T, H, K, max(int(n_steps), 1),
+                                     _lib.dtype_code(k.dtype), _lib.stream_ptr(k.device))
+    _lib.check(rc, "gdn_write_direction_bwd")
+    return dk, dbeta, dlam_rows.sum((0, 1))
+
+
+@write_direction_bwd.register_fake
+def _(k, beta, lam, du, n_steps):
+    B, T, H, K = k.shape
+    f32 = dict(dtype=torch.float32)
+    return torch.empty_like(k), k.new_empty(B, T, H, **f32), k.new_empty(H, **f32)
+
+
+def _wd_setup(ctx, inputs, output):
+    k, beta, lam, n_steps = inputs
+    ctx.save_for_backward(k, beta, lam)
+    ctx.n_steps = n_steps
+    ctx.dtypes = (beta.dtype, lam.dtype)
+
+
+def _wd_backward(ctx, du):
+    k, beta, lam = ctx.saved_tensors
+    dk, dbeta, dlam = write_direction_bwd(k, beta, lam, du.contiguous(), ctx.n_steps)
+    return dk, dbeta.to(ctx.dtypes[0]), dlam.to(ctx.dtypes[1]), None
+
+
+write_direction.register_autograd(_wd_backward, setup_context=_wd_setup)
 
 
 def nsgdn_scan_chunk(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor, scale: float = 1.0,

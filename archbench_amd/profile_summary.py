@@ -46,6 +46,7 @@ def stage_of(name: str) -> str:
                        ("step_kernel", "step"), ("conv_silu_fwd", "conv_fwd"), ("conv_silu_bwd", "conv_bwd"),
                        ("row_norm_fwd", "norm_fwd"), ("row_norm_bwd", "norm_bwd"), ("gates_fwd", "gates_fwd"),
                        ("gates_bwd", "gates_bwd"), ("ce_fwd_bwd", "cross_entropy"), ("column_sum", "column_sum"),
+                       ("write_dir_fwd", "write_dir_fwd"), ("write_dir_bwd", "write_dir_bwd"),
                        ("copyBuffer", "copy"), ("copy_kernel", "copy")):
         if key in name:
             return stage

@@ -36,6 +36,8 @@ Also reported in the same line:
                 the trainer runs Block.forward, at B=64, T=1024: forward + backward of the whole layer (projections
                 on hipBLASLt, conv, gates, the op, gated RMSNorm, output projection), tokens/s, with the library's
                 kernels' share of the step;
+  nsgdn_layer   the same for archbench's `nsgdn` mixer (configs/65m/nsgdn.yaml: n_steps 2, lam 1, the same
+                projections, conv and norm around the separate-write-key chunk kernels, plus the write direction);
   decode_step   one recurrent decode step at B=256, H=16, K=V=128 with the fp32 state updated in place
                 (HBM GB/s against 8 TB/s);
   short_conv    the causal depthwise conv (kernel 4) + SiLU in front of the op at the layer's shape, B=8, T=4096,
@@ -203,7 +205,7 @@ def main() -> int:
                          "FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     only = set(args.only.split(","))
-    known = {"all", "train", "fwd", "long", "nsgdn", "layer", "decode", "conv", "norm", "ce"}
+    known = {"all", "train", "fwd", "long", "nsgdn", "layer", "nsgdn_layer", "decode", "conv", "norm", "ce"}
     if not only <= known:
         ap.error(f"--only: unknown workload(s) {sorted(only - known)}; choose from {sorted(known)}")
     want = lambda w: "all" in only or w in only
@@ -362,37 +364,44 @@ def main() -> int:
         del x, q, k, u, v, dy, la
         torch.cuda.empty_cache()
 
-    if want("layer"):
+    if want("layer") or want("nsgdn_layer"):
         from archbench_amd import layers
 
         B, T, D, nh = 64, 1024, 512, 4
-        log(f"gdn layer (configs/65m/gdn.yaml: d_model {D}, {nh} heads, K=128, V=256) B={B} T={T}, fp32 input "
-            f"under bf16 autocast, forward + backward")
-        torch.manual_seed(0)
-        m = layers.build_mixer("gdn", D, 0, 10, num_heads=nh, head_dim=128, expand_v=2.0, use_gate=True,
-                               use_short_conv=True, conv_size=4).to(dev)
-        xin = torch.randn(B, T, D, device=dev, generator=torch.Generator(dev).manual_seed(1)).requires_grad_()
-        gy = torch.randn(B, T, D, device=dev, generator=torch.Generator(dev).manual_seed(2))
+        mixers = []
+        if want("layer"):
+            mixers.append(("gdn", "gdn_layer", dict(use_gate=True, use_short_conv=True, conv_size=4)))
+        if want("nsgdn_layer"):
+            mixers.append(("nsgdn", "nsgdn_layer",
+                           dict(n_steps=2, lam=1.0, use_gate=True, use_short_conv=True, conv_size=4)))
+        for arch, key, cfg in mixers:
+            log(f"{arch} layer (configs/65m/{arch}.yaml: d_model {D}, {nh} heads, K=128, V=256) B={B} T={T}, fp32 "
+                f"input under bf16 autocast, forward + backward")
+            torch.manual_seed(0)
+            m = layers.build_mixer(arch, D, 0, 10, num_heads=nh, head_dim=128, expand_v=2.0, **cfg).to(dev)
+            xin = torch.randn(B, T, D, device=dev, generator=torch.Generator(dev).manual_seed(1)).requires_grad_()
+            gy = torch.randn(B, T, D, device=dev, generator=torch.Generator(dev).manual_seed(2))
 
-        def layer_step():
-            with torch.autocast("cuda", dtype=torch.bfloat16):
-                y = m(xin)
-            y.backward(gy)
+            def layer_step():
+                with torch.autocast("cuda", dtype=torch.bfloat16):
+                    y = m(xin)
+                y.backward(gy)
 
-        n = max(5, min(args.steps, 20))
-        sec = timed_loop(layer_step, n, 2, torch)
-        with _lib.StageTimer() as st:
-            for _ in range(3):
-                layer_step()
-        lib_ms = sum(v_[0] for v_ in st.result.values()) / 3
-        out["gdn_layer"] = {"workload": "gdn mixer fwd+bwd (configs/65m/gdn.yaml)", "B": B, "T": T, "d_model": D,
-                            "heads": nh, "K": 128, "V": 256, "steps": n, "ms_per_step": round(sec * 1e3, 4),
-                            "tokens_per_s": round(B * T / sec, 1), "library_kernels_ms": round(lib_ms, 4),
-                            "stages_ms": {k_: round(v_[0] / 3, 4) for k_, v_ in st.result.items()}}
-        log(f"gdn layer {sec * 1e3:.3f} ms/step, {B * T / sec:.3e} tokens/s; library kernels {lib_ms:.3f} ms "
-            f"per step {out['gdn_layer']['stages_ms']}")
-        del m, xin, gy
-        torch.cuda.empty_cache()
+            n = max(5, min(args.steps, 20))
+            sec = timed_loop(layer_step, n, 2, torch)
+            with _lib.StageTimer() as st:
+                for _ in range(3):
+                    layer_step()
+            lib_ms = sum(v_[0] for v_ in st.result.values()) / 3
+            out[key] = {"workload": f"{arch} mixer fwd+bwd (configs/65m/{arch}.yaml)", "B": B, "T": T,
+                        "d_model": D, "heads": nh, "K": 128, "V": 256, "steps": n,
+                        "ms_per_step": round(sec * 1e3, 4), "tokens_per_s": round(B * T / sec, 1),
+                        "library_kernels_ms": round(lib_ms, 4),
+                        "stages_ms": {k_: round(v_[0] / 3, 4) for k_, v_ in st.result.items()}}
+            log(f"{arch} layer {sec * 1e3:.3f} ms/step, {B * T / sec:.3e} tokens/s; library kernels {lib_ms:.3f} "
+                f"ms per step {out[key]['stages_ms']}")
+            del m, xin, gy
+            torch.cuda.empty_cache()
 
     if want("decode"):
         B, H, K, V = 256, 16, 128, 128

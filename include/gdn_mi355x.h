@@ -200,12 +200,25 @@ int gdn_gates_bwd(const void* a, const void* b, const float* A_log, const float*
 int gdn_cross_entropy_fwd_bwd(void* logits, const int64_t* target, float* loss, float* lse, const float* dloss,
                               int64_t N, int V, int64_t ld, int64_t ignore_index, int dtype, void* stream);
 
+/* Write direction of the n-step family: per token row of K channels (one head of one token), with p the previous
+ * token's key in the same sequence (zero at t = 0),
+ *   u_1 = beta k,  u_{i+1} = u_i - lam beta (p . u_i) (p - (p . k) k)   for i < n_steps.
+ * Replaces write_direction (archbench/layers/nsgdn.py:61-75) and the shift of k that feeds it (:535-536).  k, u, du,
+ * dk [B, T, H, K] in dtype; beta, dbeta, dlam [B, T, H] fp32; lam [H] fp32 (the module's softplus(lam)).  The
+ * backward writes dk (through both k and the next token's p), dbeta and dlam per row (the caller sums dlam over
+ * B and T).  K in {64, 128, 256}, 1 <= n_steps <= 8; fp32 arithmetic. */
+int gdn_write_direction_fwd(const void* k, const float* beta, const float* lam, void* u, int B, int T, int H, int K,
+                            int n_steps, int dtype, void* stream);
+int gdn_write_direction_bwd(const void* k, const float* beta, const float* lam, const void* du, void* dk,
+                            float* dbeta, float* dlam, int B, int T, int H, int K, int n_steps, int dtype,
+                            void* stream);
+
 /* Per-stage kernel timing (diagnostic; no counterpart in the reference, which times whole phases with CUDA
  * events in archbench/logger.py:57-81).  While enabled (process-wide: launches from any host thread count), every
  * kernel the calls above enqueue is bracketed by hipEvents on the same stream.  gdn_profile_read synchronises on those events and
  * returns, per stage, the summed milliseconds and the number of launches (arrays of at least
  * GDN_PROFILE_STAGES entries), then clears the record.  Stage names: gdn_profile_stage_name. */
-#define GDN_PROFILE_STAGES 19
+#define GDN_PROFILE_STAGES 21
 int gdn_profile_enable(int on);
 int gdn_profile_read(double* ms_sum, int* launches, int n_stages);
 const char* gdn_profile_stage_name(int stage);
