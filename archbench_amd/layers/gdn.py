@@ -12,11 +12,12 @@ The token mixing itself is always the HIP chunk op (training / prefill) or the H
 a recurrent state, no grad).  The short causal convolutions (with the q / k normalisation fused in), the gate
 functions and the output gated RMSNorm run on their own HIP kernels; the projections are PyTorch linears.  The
 six input projections (q, k, v, a, b and the gate) keep fla's separate ``nn.Linear`` parameters (names, shapes
-and initialisation, so checkpoints and the reference's init rules carry over) but run as two GEMMs against
-concatenated weights: q, k, v and the gate as one (2 key_dim + 2 value_dim columns: a multiple of 256 at the
-reference configs, which hipBLASLt's 256-wide tiles cover exactly; with the eight a and b columns added the
-forward GEMM ran 1.6x longer), a and b as the other.  One input-gradient GEMM per group instead of one per
-projection, and a weight-gradient GEMM wide enough to fill the GPU for the big group.
+and initialisation, so checkpoints and the reference's init rules carry over) but run as three GEMMs against
+their concatenated weights: q, k, v as one (2 key_dim + value_dim columns: a multiple of 256 at the reference
+configs, which hipBLASLt's 256-wide tiles cover exactly; with the eight a and b columns added the forward GEMM ran
+1.6x longer), the gate (its own contiguous output, which the output norm reads as it is), and a and b.  The
+backward accumulates the groups' input gradients inside their GEMMs and splits each weight gradient over the
+tokens (_GroupedLinear).
 """
 
 from __future__ import annotations
@@ -33,47 +34,71 @@ from .. import ops
 def _weight_grad(dy: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     """dW = dy^T x (dy [M, N], x [M, K]) in fp32, split over the M tokens: a batch of chunk products summed in fp32.
     A weight gradient reduces over every token into a small N x K output; as one GEMM it has too few output tiles
-    to fill the GPU (hipBLASLt at B64 T1024: 131 us for N = 8, K = 512; 248 us for N = 512, K = 1024; 400 us for
-    N = 3072, K = 512), split 8 or 16 ways 34, 211 and 322 us.  The smaller operand is transposed into contiguous
-    chunks, so neither product operand is a transposed view."""
+    to fill the GPU (hipBLASLt at M = 65536: 131 us for N = 8, K = 512; 248 us for N = 512, K = 1024; 400 us for
+    N = 3072, K = 512), split 8 or 16 ways 27, 77 and 211 us.  The smaller operand's chunks enter the batched
+    product as the transposed left operand (a layout the GEMM reads directly; copying them transposed first cost
+    140 us at these sizes); the right operand is always contiguous."""
     M, N = dy.shape
     K = x.shape[1]
-    C = 16 if N <= K else 8
+    C = 16 if N * K <= 1 << 20 else 8
     if dy.dtype == torch.float32:
         return dy.t() @ x
     if M % C or M // C < 1024:
         return torch.mm(dy.t(), x, out_dtype=torch.float32)
     if N <= K:
-        dyt = dy.view(C, M // C, N).transpose(1, 2).contiguous()
-        return torch.bmm(dyt, x.view(C, M // C, K), out_dtype=torch.float32).sum(0)
-    xt = x.view(C, M // C, K).transpose(1, 2).contiguous()
-    return torch.bmm(xt, dy.view(C, M // C, N), out_dtype=torch.float32).sum(0).t()
+        return torch.bmm(dy.view(C, M // C, N).transpose(1, 2), x.view(C, M // C, K), out_dtype=torch.float32).sum(0)
+    return torch.bmm(x.view(C, M // C, K).transpose(1, 2), dy.view(C, M // C, N), out_dtype=torch.float32).sum(0).t()
 
 
-class _Linear(torch.autograd.Function):
-    """y = x W^T with W cast to x's dtype (as autocast casts it); the backward's weight gradient split over the
-    tokens (_weight_grad) and returned in W's dtype."""
+class _GroupedLinear(torch.autograd.Function):
+    """y_g = x W[r_g:r_{g+1}]^T for consecutive row groups of one weight: one GEMM per group, each output its own
+    contiguous tensor, W cast to x's dtype once (as autocast casts it).  Backward: the groups' input gradients
+    accumulated in place into the first (dx += dy_g W_g in the GEMM, no separate sum), and each group's weight
+    gradient split over the tokens (_weight_grad) written into its rows of one fp32 gradient (rows outside every
+    group: zero), returned in W's dtype."""
 
     @staticmethod
-    def forward(ctx, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    def forward(ctx, x: torch.Tensor, w: torch.Tensor, bounds: tuple):
         wc = w.to(x.dtype)
         ctx.save_for_backward(x, wc)
-        ctx.w_dtype = w.dtype
-        return F.linear(x, wc)
+        ctx.bounds, ctx.w_dtype = bounds, w.dtype
+        return tuple(F.linear(x, wc[r0:r1]) for r0, r1 in zip(bounds[:-1], bounds[1:]))
 
     @staticmethod
-    def backward(ctx, dy: torch.Tensor):
+    def backward(ctx, *dys):
         x, wc = ctx.saved_tensors
-        lead = dy.shape[:-1]
-        dy2 = dy.reshape(-1, dy.shape[-1])
-        dx = (dy2 @ wc).view(*lead, wc.shape[1]) if ctx.needs_input_grad[0] else None
-        dw = _weight_grad(dy2, x.reshape(-1, x.shape[-1])).to(ctx.w_dtype) if ctx.needs_input_grad[1] else None
-        return dx, dw
+        groups = [(r0, r1, None if dy is None else dy.reshape(-1, dy.shape[-1]))
+                  for r0, r1, dy in zip(ctx.bounds[:-1], ctx.bounds[1:], dys)]
+        x2 = x.reshape(-1, x.shape[-1])
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            for r0, r1, dy in groups:
+                if dy is not None:
+                    dx = dy @ wc[r0:r1] if dx is None else dx.addmm_(dy, wc[r0:r1])
+            dx = torch.zeros_like(x) if dx is None else dx.view(x.shape)
+        if ctx.needs_input_grad[1]:
+            whole = ctx.bounds[0] == 0 and ctx.bounds[-1] == wc.shape[0] and all(g[2] is not None for g in groups)
+            dw = (torch.empty if whole else torch.zeros)(wc.shape, dtype=torch.float32, device=wc.device)
+            for r0, r1, dy in groups:
+                if dy is not None:
+                    dw[r0:r1] = _weight_grad(dy, x2)
+            dw = dw.to(ctx.w_dtype)
+        return dx, dw, None
+
+
+def _grouped_linear(x: torch.Tensor, w: torch.Tensor, bounds) -> tuple[torch.Tensor, ...]:
+    """(x W[r_0:r_1]^T, x W[r_1:r_2]^T, ...) for row bounds r_0 < r_1 < ...; on GPUs one GEMM per group with the
+    backward of _GroupedLinear."""
+    bounds = tuple(int(r) for r in bounds)
+    if x.is_cuda:
+        return _GroupedLinear.apply(x, w, bounds)
+    wc = w.to(x.dtype)
+    return tuple(F.linear(x, wc[r0:r1]) for r0, r1 in zip(bounds[:-1], bounds[1:]))
 
 
 def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """F.linear for a bf16 (or fp32) activation under the layer's own cast; the split-K weight gradient on GPUs."""
-    return _Linear.apply(x, w) if x.is_cuda else F.linear(x, w.to(x.dtype))
+    return _grouped_linear(x, w, (0, w.shape[0]))[0]
 
 
 class ShortConvolution(nn.Module):
@@ -145,22 +170,24 @@ class GatedDeltaNet(nn.Module):
         self.o_norm = GatedRMSNorm(self.head_v_dim, norm_eps)
         self.o_proj = nn.Linear(self.value_dim, hidden_size, bias=False)
 
-    def _wide_projection(self, hidden_states: torch.Tensor) -> torch.Tensor:
-        """[q | k | v (| gate)] = hidden_states against the concatenated weights of those linears, one GEMM."""
-        wide = [self.q_proj, self.k_proj, self.v_proj] + ([self.g_proj] if self.use_gate else [])
-        return _linear(hidden_states, torch.cat([m.weight for m in wide], 0))
-
-    def _ab_projection(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        ab = _linear(hidden_states, torch.cat([self.a_proj.weight, self.b_proj.weight], 0))
-        return torch.split(ab, [self.a_proj.out_features, self.b_proj.out_features], dim=-1)
+    def _grouped_projections(self, hidden_states: torch.Tensor):
+        """([q | k | v], gate or None, [a | b]): the six input linears against their concatenated weights, one GEMM
+        per group."""
+        mods = [self.q_proj, self.k_proj, self.v_proj] + ([self.g_proj] if self.use_gate else [])
+        mods += [self.a_proj, self.b_proj]
+        n_qkv = 2 * self.key_dim + self.value_dim
+        bounds = [0, n_qkv] + ([n_qkv + self.value_dim] if self.use_gate else [])
+        bounds.append(bounds[-1] + self.a_proj.out_features + self.b_proj.out_features)
+        outs = _grouped_linear(hidden_states, torch.cat([m.weight for m in mods], 0), bounds)
+        return outs[0], (outs[1] if self.use_gate else None), outs[-1]
 
     def input_projections(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, ...]:
-        """(q, k, v, a, b[, gate]) = the six linears of ``hidden_states``, computed as two GEMMs: q, k, v (and
-        the gate) against their concatenated weights, a and b against theirs."""
-        q, k, v, *gate = torch.split(self._wide_projection(hidden_states),
-                                     [self.key_dim, self.key_dim, self.value_dim] + [self.value_dim] * self.use_gate,
-                                     dim=-1)
-        return (q, k, v, *self._ab_projection(hidden_states), *gate)
+        """(q, k, v, a, b[, gate]) = the six linears of ``hidden_states``, computed as three GEMMs: q, k, v against
+        their concatenated weights, the gate, and a and b against theirs."""
+        y, gate, ab = self._grouped_projections(hidden_states)
+        q, k, v = torch.split(y, [self.key_dim, self.key_dim, self.value_dim], dim=-1)
+        a, b = torch.split(ab, [self.a_proj.out_features, self.b_proj.out_features], dim=-1)
+        return (q, k, v, a, b) + ((gate,) if self.use_gate else ())
 
     def forward(self, hidden_states: torch.Tensor, attention_mask: torch.Tensor | None = None,
                 past_key_values: dict | None = None, use_cache: bool = False, output_attentions: bool = False,
@@ -186,11 +213,11 @@ class GatedDeltaNet(nn.Module):
             # training / prefill without a cache: the convolutions read q, k, v straight out of the projection's
             # output and their backward writes into one gradient of it (ops.mixer_input_stage); the weights are
             # rounded to the activation dtype first, as ShortConvolution does
-            y = self._wide_projection(hidden_states)
-            a, b = self._ab_projection(hidden_states)
+            y, gate, ab = self._grouped_projections(hidden_states)
+            a, b = torch.split(ab, [self.a_proj.out_features, self.b_proj.out_features], dim=-1)
             wq, wk, wv = (c.weight.squeeze(1).to(y.dtype).float() for c in convs)
-            q, k, v, gcols = ops.mixer_input_stage(y, wq, wk, wv, self.key_dim, self.value_dim, DK)
-            gp = [gcols] if self.use_gate else []
+            q, k, v, _ = ops.mixer_input_stage(y, wq, wk, wv, self.key_dim, self.value_dim, DK)
+            gp = [gate] if self.use_gate else []
         else:
             q, k, v, a, b, *gp = self.input_projections(hidden_states)
             if convs:

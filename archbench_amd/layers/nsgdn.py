@@ -33,7 +33,7 @@ import torch.nn.functional as F
 
 from .. import ops
 from . import register
-from .gdn import _linear
+from .gdn import _grouped_linear, _linear
 
 
 def write_direction(k: torch.Tensor, p: torch.Tensor, beta: torch.Tensor, lam: torch.Tensor,
@@ -95,18 +95,18 @@ class NStepGDN(nn.Module):
         xp = x
         if torch.is_autocast_enabled(dev_type) and x.dtype == torch.float32:
             xp = x.to(torch.get_autocast_dtype(dev_type))  # autocast's cast, made once for both GEMMs below
-        # in_proj's rows [q k v | gate] and [a b] as two GEMMs (the first a multiple of 256 wide at the reference
-        # shapes); the rows past them pad the projection and are not computed (their gradient is zero)
-        w_in = self.in_proj.weight
-        y = _linear(xp, w_in[:n_main])
-        ab = _linear(xp, w_in[n_main:n_main + 2 * H])
+        # in_proj's rows [q k v], [gate] and [a b] as one GEMM each (the first a multiple of 256 wide at the
+        # reference shapes); the rows past them pad the projection and are not computed (their gradient is zero)
+        bounds = [0, n_qkv] + ([n_main] if self.n_gate else []) + [n_main + 2 * H]
+        y, *g, ab = _grouped_linear(xp, self.in_proj.weight, bounds)
+        g = g[0] if g else None
         if self.conv is not None:
             w = self.conv.weight.squeeze(1).to(y.dtype).float()  # rounded as the reference's conv runs it
-            # q, k, v convolved straight out of y; the gate columns passed on (ops.mixer_input_stage)
-            q, k, v, g = ops.mixer_input_stage(y, w[:self.qk_dim], w[self.qk_dim:2 * self.qk_dim],
+            # q, k, v convolved straight out of y (ops.mixer_input_stage)
+            q, k, v, _ = ops.mixer_input_stage(y, w[:self.qk_dim], w[self.qk_dim:2 * self.qk_dim],
                                                w[2 * self.qk_dim:], self.qk_dim, self.v_dim, DK)
         else:
-            qs, ks, vs, g = torch.split(y, [self.qk_dim, self.qk_dim, self.v_dim, self.n_gate], dim=-1)
+            qs, ks, vs = torch.split(y, [self.qk_dim, self.qk_dim, self.v_dim], dim=-1)
             q, k, v = ops.l2norm(qs, 1e-12, 1.0), ops.l2norm(ks, 1e-12, 1.0), vs
         q, k, v = q.view(B, T, H, DK), k.view(B, T, H, DK), v.reshape(B, T, H, DV)
         la, beta = ops.gdn_gates(ab[..., :H], ab[..., H:], self.A_log, self.dt_bias, self.b_bias, 1.0,

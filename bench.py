@@ -34,8 +34,8 @@ Also reported in the same line:
   gdn_layer     the drop-in `gdn` mixer as archbench's model builds it for configs/65m/gdn.yaml (d_model 512,
                 4 heads, head_dim 128, expand_v 2, gate, short conv 4), fed fp32 hidden states under bf16 autocast as
                 the trainer runs Block.forward, at B=64, T=1024: forward + backward of the whole layer (projections
-                on hipBLASLt, conv, gates, the op, gated RMSNorm, output projection), tokens/s, with the library's
-                kernels' share of the step;
+                on hipBLASLt, conv, gates, the op, gated RMSNorm, output projection; gradients unset before each
+                step, as after zero_grad(set_to_none=True)), tokens/s, with the library's kernels' share of the step;
   nsgdn_layer   the same for archbench's `nsgdn` mixer (configs/65m/nsgdn.yaml: n_steps 2, lam 1, the same
                 projections, conv and norm around the separate-write-key chunk kernels, plus the write direction);
   decode_step   one recurrent decode step at B=256, H=16, K=V=128 with the fp32 state updated in place
@@ -382,7 +382,14 @@ def main() -> int:
             xin = torch.randn(B, T, D, device=dev, generator=torch.Generator(dev).manual_seed(1)).requires_grad_()
             gy = torch.randn(B, T, D, device=dev, generator=torch.Generator(dev).manual_seed(2))
 
+            params = list(m.parameters())
+
             def layer_step():
+                # gradients start unset, as after the trainer's zero_grad(set_to_none=True); the input's stands
+                # for the gradient the block passes on, which the model does not accumulate across steps
+                xin.grad = None
+                for p_ in params:
+                    p_.grad = None
                 with torch.autocast("cuda", dtype=torch.bfloat16):
                     y = m(xin)
                 y.backward(gy)

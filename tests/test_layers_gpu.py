@@ -249,3 +249,29 @@ def test_split_weight_gradient(N, K):
     y.backward(dy)
     assert w.grad.dtype == torch.float32 and rel_l2(w.grad.double(), ref) <= 1e-5
     assert torch.equal(xa.grad, dy @ w.detach().to(torch.bfloat16))
+
+
+def test_grouped_linear_groups_and_gradients():
+    """The layers' grouped projection: one output per row group of one weight (each equal to F.linear against
+    those rows), the input gradient summed over the groups inside their GEMMs, each group's weight gradient in its
+    rows and zero in rows no group covers (the padding rows of nsgdn's in_proj)."""
+    from archbench_amd.layers.gdn import _grouped_linear
+    banner("grouped linear: three groups and padding rows")
+    M, K = 16384, 512
+    bounds = (0, 2048, 3072, 3080)
+    gen = torch.Generator("cuda").manual_seed(11)
+    x = torch.randn(M, K, device="cuda", generator=gen).to(torch.bfloat16).requires_grad_()
+    w = (torch.randn(3088, K, device="cuda", generator=gen) * 0.05).requires_grad_()
+    outs = _grouped_linear(x, w, bounds)
+    wb = w.detach().to(torch.bfloat16)
+    dys = []
+    for (r0, r1), y in zip(zip(bounds[:-1], bounds[1:]), outs):
+        assert y.is_contiguous() and torch.equal(y, torch.nn.functional.linear(x.detach(), wb[r0:r1]))
+        dys.append(torch.randn(y.shape, device="cuda", generator=gen).to(torch.bfloat16))
+    torch.autograd.backward(outs, dys)
+    dx_ref = sum(dy.double() @ wb[r0:r1].double() for dy, r0, r1 in zip(dys, bounds[:-1], bounds[1:]))
+    assert x.grad.dtype == torch.bfloat16 and rel_l2(x.grad.double(), dx_ref) <= 5e-3
+    for dy, r0, r1 in zip(dys, bounds[:-1], bounds[1:]):
+        ref = dy.double().t() @ x.detach().double()
+        assert rel_l2(w.grad[r0:r1].double(), ref) <= 1e-5, (r0, r1)
+    assert torch.count_nonzero(w.grad[bounds[-1]:]) == 0
