@@ -47,11 +47,12 @@ def test_ce_invalid_target_and_shapes():
                                                                                     device="cuda"), None, -100)
 
 
-@pytest.mark.parametrize("num_chunks", [1, 3, 8])
-def test_fused_linear_ce_matches_oracle(num_chunks):
-    banner(f"fused linear CE chunks={num_chunks}")
+@pytest.mark.parametrize("num_chunks,V", [(1, 4096), (3, 4096), (8, 4096), (1, 4000), (3, 4000)])
+def test_fused_linear_ce_matches_oracle(num_chunks, V):
+    """The whole LCE against the oracle, at a vocabulary of whole 256-wide GEMM tiles and one that is not."""
+    banner(f"fused linear CE chunks={num_chunks} V={V}")
     gen = torch.Generator().manual_seed(num_chunks)
-    B, T, H, V = 2, 300, 256, 4096
+    B, T, H = 2, 300, 256
     x = torch.randn(B, T, H, generator=gen).bfloat16()
     w = (torch.randn(V, H, generator=gen) * 0.05).bfloat16()
     t = torch.randint(0, V, (B, T), generator=gen)
@@ -63,3 +64,4 @@ def test_fused_linear_ce_matches_oracle(num_chunks):
     assert abs(loss.item() - l_r.item()) <= 1e-3 * abs(l_r.item())
     assert rel_l2(xd.grad.reshape(-1, H), dx_r) <= 1e-2
     assert rel_l2(wd.grad, dw_r) <= 1e-2
+    assert wd.grad.shape == w.shape and xd.grad.shape == x.shape
