@@ -1,6 +1,6 @@
 """The gdn mixer layer and the op boundary on the GPU: layer output/gradients against the same layer whose
-token mixing runs in the CPU oracle, prefill + decode through the cache, torch.compile(dynamic=False) and
-torch.library.opcheck."""
+token mixing runs in the CPU oracle and against an fp64 restatement of fla's GatedDeltaNet, prefill + decode
+through the cache, torch.compile(dynamic=False) and torch.library.opcheck."""
 
 import pytest
 import torch
@@ -275,3 +275,66 @@ def test_grouped_linear_groups_and_gradients():
         ref = dy.double().t() @ x.detach().double()
         assert rel_l2(w.grad[r0:r1].double(), ref) <= 1e-5, (r0, r1)
     assert torch.count_nonzero(w.grad[bounds[-1]:]) == 0
+
+
+def _gdn_restatement(P, x, H, DK, DV, use_gate, eps, bf16_op):
+    """fla's GatedDeltaNet.forward as the gdn arch builds it (separate q/k/v/a/b/g linears; causal depthwise conv
+    + SiLU; q, k L2-normalised per head; g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b); the chunk rule
+    at scale DK^-1/2; RMSNorm(o) * silu(gate); o_proj), restated on the CPU in fp64 from the module's parameters
+    P.  With bf16_op the op's inputs and output are rounded to bf16, where the layer under autocast hands them
+    over."""
+    F = torch.nn.functional
+    B, T, _ = x.shape
+    lin = lambda n: x @ P[n + ".weight"].T
+    bf = (lambda t: t.to(torch.bfloat16).to(torch.float64)) if bf16_op else (lambda t: t)
+
+    def conv(y, n):
+        w = P[n + ".weight"]
+        z = F.conv1d(y.transpose(1, 2), w, padding=w.shape[-1] - 1, groups=y.shape[-1])[..., :T]
+        return F.silu(z.transpose(1, 2))
+    q = F.normalize(conv(lin("layer.q_proj"), "layer.q_conv1d").reshape(B, T, H, DK), dim=-1)
+    k = F.normalize(conv(lin("layer.k_proj"), "layer.k_conv1d").reshape(B, T, H, DK), dim=-1)
+    v = conv(lin("layer.v_proj"), "layer.v_conv1d").reshape(B, T, H, DV)
+    g = -P["layer.A_log"].exp() * F.softplus(lin("layer.a_proj") + P["layer.dt_bias"])
+    beta = torch.sigmoid(lin("layer.b_proj"))
+    o, _ = O.chunk_fwd(bf(q), bf(k), bf(v), g, beta, DK ** -0.5)
+    o = F.rms_norm(bf(o), (DV,), P["layer.o_norm.weight"], eps)
+    if use_gate:
+        o = o * F.silu(lin("layer.g_proj").reshape(B, T, H, DV))
+    return o.reshape(B, T, -1) @ P["layer.o_proj.weight"].T
+
+
+@pytest.mark.parametrize("use_gate", [True, False])
+def test_gdn_layer_matches_restatement(use_gate):
+    """The whole gdn mixer under bf16 autocast (grouped projection GEMMs, the fused input stage, gates, the chunk
+    kernels, gated RMSNorm) against an fp64 CPU restatement of fla's GatedDeltaNet with the same parameters:
+    output and input gradient within rel-L2 2e-2, every parameter gradient within 3e-2 plus four times the
+    restatement's own movement when only the op's bf16 rounding point changes (the per-head vectors' gradients
+    are cancelling sums over every token)."""
+    banner(f"gdn layer vs fp64 restatement, use_gate={use_gate}")
+    torch.manual_seed(7)
+    H, DK, DV, d = 2, 64, 128, 192
+    m = layers.build_mixer("gdn", d, 0, 2, num_heads=H, head_dim=DK, expand_v=2.0, use_gate=use_gate).cuda()
+    for p in m.parameters():
+        if p.dim() == 2:
+            torch.nn.init.normal_(p, std=0.05)
+    x = torch.randn(2, 100, d, generator=torch.Generator().manual_seed(8))
+    xd = x.cuda().requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = m(xd)
+    dy = torch.randn(*y.shape, generator=torch.Generator().manual_seed(9))
+    y.float().backward(dy.cuda())
+    refs = []
+    for bf16_op in (True, False):
+        P = {n: p.detach().cpu().double().requires_grad_() for n, p in m.named_parameters()}
+        xr = x.double().requires_grad_()
+        yr = _gdn_restatement(P, xr, H, DK, DV, use_gate, m.layer.o_norm.eps, bf16_op)
+        yr.backward(dy.double())
+        refs.append((yr.detach(), xr.grad, {n: t.grad for n, t in P.items()}))
+    (yr, dxr, gr), (_, _, gr_exact) = refs
+    errs = {"y": rel_l2(y.float(), yr), "dx": rel_l2(xd.grad, dxr)}
+    print("rel-L2 vs restatement:", {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    assert errs["y"] <= 2e-2 and errs["dx"] <= 2e-2, errs
+    for n, p in m.named_parameters():
+        noise = rel_l2(gr_exact[n], gr[n])
+        assert rel_l2(p.grad, gr[n]) <= 3e-2 + 4 * noise, (n, rel_l2(p.grad, gr[n]), noise)
