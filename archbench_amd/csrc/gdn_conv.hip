@@ -27,7 +27,10 @@ constexpr int CONV_CPL = 4;  // consecutive channels per lane
 constexpr int CONV_CW = 64 * CONV_CPL;  // channels per wave
 constexpr int CONV_WAVES = 4;  // waves per workgroup, on adjacent channel blocks of the same chunk
 constexpr int CONV_UF = 8;  // token rows per load batch, forward
-constexpr int CONV_UB = 8;  // token rows of x and of dy per load batch, backward
+// token rows of x and of dy per load batch, backward: with the per-group normalisation the smaller batch measured
+// faster (fewer registers in flight beside the group sums' longer chain: 109 -> 102 us at B8 T4096 D2048), without
+// it the larger one (95 against 102 us)
+constexpr int CONV_UB = 8, CONV_UB_NORM = 4;
 
 // CONV_CPL = 4 consecutive channels of one token row as loaded (8 B in bf16, 16 B in fp32), converted at use so
 // that a whole batch of loads is in flight at once.  The backward reads x and dy and writes dx once each through
@@ -210,7 +213,8 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_fwd_kernel(const T*
 
 // grid and waves as in the forward; partial sums of dw and dbias per (b, chunk) = part.
 // Each wave recomputes z over its chunk plus W-1 tokens of look-ahead, forms dz, and emits dx with a W-1 token
-// delay; rows of x and dy are loaded in double-buffered batches of CONV_UB as in the forward.
+// delay; rows of x and dy are loaded in double-buffered batches (CONV_UB, or CONV_UB_NORM with the normalisation) as
+// in the forward.
 template <typename T, int W, int NG>
 __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                            const float* __restrict__ bias,
@@ -219,7 +223,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
                                                            T* __restrict__ dstate_in, float* __restrict__ part_out,
                                                            int Tn, int D, int ldx, int lddx, int nchunk,
                                                            int nparts) {
-  constexpr int CPL = CONV_CPL, U = CONV_UB;
+  constexpr int CPL = CONV_CPL, U = NG > 0 ? CONV_UB_NORM : CONV_UB;
   const int l = lane_id();
   int part, cw0;
   if (!conv_wave_item(D, nparts, part, cw0)) return;  // past the last item (waves never synchronise)
