@@ -22,7 +22,13 @@
 
 namespace gdn {
 
-constexpr int CONV_L = 64;  // tokens per wave
+constexpr int CONV_L = 64;  // tokens per wave (the backward without normalisation may take CONV_L_LONG)
+// Tokens per wave of the backward without the normalisation when the grid stays large (at least
+// CONV_LONG_MIN_WAVES_PER_CU waves per CU): each wave's set-up, look-ahead recompute and dw partial are then
+// amortised over twice the tokens (96 -> 86 us at B8 T4096 D2048, 99 -> 91 us at B64 T1024 D1024); on small grids
+// the shorter chunks' parallelism wins (23 against 39 us at B2 T200 D512).  With the normalisation 64 throughout
+// (at the 65m layer's D = 512, 61 against 70 us with 128).
+constexpr int CONV_L_LONG = 128, CONV_LONG_MIN_WAVES_PER_CU = 4;
 constexpr int CONV_CPL = 4;  // consecutive channels per lane
 constexpr int CONV_CW = 64 * CONV_CPL;  // channels per wave
 constexpr int CONV_WAVES = 4;  // waves per workgroup, on adjacent channel blocks of the same chunk
@@ -215,7 +221,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_fwd_kernel(const T*
 // Each wave recomputes z over its chunk plus W-1 tokens of look-ahead, forms dz, and emits dx with a W-1 token
 // delay; rows of x and dy are loaded in double-buffered batches (CONV_UB, or CONV_UB_NORM with the normalisation) as
 // in the forward.
-template <typename T, int W, int NG>
+template <typename T, int W, int NG, int L>
 __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T* __restrict__ x, const float* __restrict__ w,
                                                            const float* __restrict__ bias,
                                                            const T* __restrict__ state_in,
@@ -229,7 +235,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
   if (!conv_wave_item(D, nparts, part, cw0)) return;  // past the last item (waves never synchronise)
   const int c = cw0 + CPL * l;
   const int b = part / nchunk, ch = part - b * nchunk;
-  const int t0 = ch * CONV_L, t1 = min(Tn, t0 + CONV_L);
+  const int t0 = ch * L, t1 = min(Tn, t0 + L);
   const bool on = c < D;
   const int cc = on ? c : 0;
   const T* xl = x + (int64_t)b * Tn * ldx + cc;
@@ -402,6 +408,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
 
 // ---------------------------------------------------------------------------------------------------------
 size_t conv_ws_bytes(int B, int T, int D, int W) {
+  // partial rows of the backward: one per (b, chunk of CONV_L or CONV_L_LONG tokens), at most this many
   const size_t nparts = (size_t)B * ((T + CONV_L - 1) / CONV_L);
   return (nparts * (size_t)(D * W + D) * 4 + 255) & ~size_t(255);
 }
@@ -427,12 +434,12 @@ static hipError_t conv_fwd_k(const ConvArgs& a) {
   return hipGetLastError();
 }
 
-template <typename T, int NG>
-static hipError_t conv_bwd_k(const ConvArgs& a) {
-  const int nchunk = (a.T + CONV_L - 1) / CONV_L;
+template <typename T, int NG, int L>
+static hipError_t conv_bwd_len(const ConvArgs& a) {
+  const int nchunk = (a.T + L - 1) / L;
   const int nparts = a.B * nchunk;
   float* part = static_cast<float*>(a.ws);
-  conv_silu_bwd_kernel<T, 4, NG><<<conv_grid(a.D, nparts), 64 * CONV_WAVES, 0, a.stream>>>(
+  conv_silu_bwd_kernel<T, 4, NG, L><<<conv_grid(a.D, nparts), 64 * CONV_WAVES, 0, a.stream>>>(
       static_cast<const T*>(a.x), a.w, a.bias, static_cast<const T*>(a.state_in), static_cast<const T*>(a.dy),
       static_cast<T*>(a.dx), static_cast<T*>(a.dstate_in), part, a.T, a.D, (int)a.ldx, (int)a.lddx, nchunk,
       nparts);
@@ -440,6 +447,17 @@ static hipError_t conv_bwd_k(const ConvArgs& a) {
   if (e != hipSuccess) return e;
   return launch_column_sum(part, nparts, a.D * 4 + a.D, ColumnOut{{a.dw, a.dbias, nullptr}, {a.D * 4, a.D, 0}},
                            a.stream);
+}
+
+template <typename T, int NG>
+static hipError_t conv_bwd_k(const ConvArgs& a) {
+  if constexpr (NG == 0) {
+    const int64_t long_waves =
+        (int64_t)((a.D + CONV_CW - 1) / CONV_CW) * a.B * ((a.T + CONV_L_LONG - 1) / CONV_L_LONG);
+    if (long_waves >= (int64_t)CONV_LONG_MIN_WAVES_PER_CU * device_cu_count())
+      return conv_bwd_len<T, NG, CONV_L_LONG>(a);
+  }
+  return conv_bwd_len<T, NG, CONV_L>(a);
 }
 
 template <typename T>

@@ -205,3 +205,23 @@ def test_mixer_input_stage_equals_separate_convs(dtype, gate_dim):
     out = ops.mixer_input_stage(ya, *wa, kd, vd, ng)
     torch.autograd.backward(out, grads)
     assert torch.equal(ya.grad, dy) and all(torch.equal(w.grad, d) for w, d in zip(wa, dws))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_conv_backward_long_chunks_match_oracle(dtype):
+    """Without normalisation a large grid takes the backward's 128-token waves (at least four waves per CU): a
+    ragged last chunk (T = 4000 = 31 * 128 + 32), bias and conv state, against the oracle."""
+    B, T, D = 4, 4000, 2048
+    waves_long = (D // 256) * B * -(-T // 128)
+    if waves_long < 4 * torch.cuda.get_device_properties(0).multi_processor_count:
+        pytest.skip("device has too many CUs for this grid to take the long-chunk backward")
+    banner(f"short conv backward, 128-token waves: B={B} T={T} D={D} {dtype}")
+    x, w, bias, state, dy = _inputs(B, T, D, dtype, 11, True, True)
+    dx, dw, db, dst = ops.short_conv_bwd(_dev(x, dtype), w.cuda(), _dev(bias, torch.float32), _dev(state, dtype),
+                                         _dev(dy, dtype), 0)
+    torch.cuda.synchronize()
+    dx_ref, dw_ref, db_ref, dst_ref = CO.short_conv_bwd(x, w, bias, state, dy, 0)
+    _check(dx, dx_ref, dtype, "dx")
+    _check(dw, dw_ref, dtype, "dw")
+    _check(db, db_ref, dtype, "dbias")
+    _check(dst, dst_ref, dtype, "dstate")
