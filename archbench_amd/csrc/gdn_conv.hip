@@ -6,7 +6,8 @@
 //   y[t,c] = silu(z[t,c]);  with normalisation over each group of NG channels: y / max(||y||_group, 1e-12)
 //
 // Layout: y, dy [B, T, D] token-major (channel-last); x and dx [B, T] rows of D channels ldx / lddx elements apart
-// (= D, or larger to read or write a column slice of a wider tensor in place); w [D, W] fp32, bias [D] fp32, conv states
+// (= D, or larger to read or write a column slice of a wider tensor in place); w [D, W] fp32 (used rounded to the
+// activation dtype; dw is the fp32 gradient of those rounded taps), bias [D] fp32, conv states
 // [B, D, W-1] in the activation dtype (the previous W-1 inputs, oldest first).
 // Mapping: one wave per (256 channels, 64-token chunk, b); each lane holds 4 consecutive channels, so every token
 // row is one 8-byte (bf16) or 16-byte (fp32) access per lane and a wave covers 512 B / 1 KB contiguous.  The W-1
@@ -90,6 +91,13 @@ __device__ __forceinline__ void store4_buf_nt(__amdgpu_buffer_rsrc_t rs, int off
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]}), rs, off, 0, 2);
   }
 }
+// A tap weight at the activation dtype's precision: the reference's conv runs under bf16 autocast, which casts its
+// fp32 weight to bf16 (archbench/layers/nsgdn.py:464); rounding here spares the caller two cast passes each way.
+template <typename T>
+__device__ __forceinline__ float act_round(float x) {
+  if constexpr (sizeof(T) == 2) return static_cast<float>(static_cast<bf16>(x));
+  return x;
+}
 // sum over the NG / CONV_CPL lanes of a normalisation group (aligned runs of lanes), the same value in every lane
 template <int NG>
 __device__ __forceinline__ float group_sum(float s) {
@@ -153,7 +161,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_fwd_kernel(const T*
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
 #pragma unroll
-    for (int i = 0; i < W; ++i) wk[j][i] = w[(cc + j) * W + i];
+    for (int i = 0; i < W; ++i) wk[j][i] = act_round<T>(w[(cc + j) * W + i]);
     bk[j] = bias ? bias[cc + j] : 0.f;
   }
   float win[W - 1][CPL];
@@ -257,7 +265,7 @@ __global__ __launch_bounds__(64 * CONV_WAVES) void conv_silu_bwd_kernel(const T*
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
 #pragma unroll
-    for (int i = 0; i < W; ++i) wk[j][i] = w[(cc + j) * W + i];
+    for (int i = 0; i < W; ++i) wk[j][i] = act_round<T>(w[(cc + j) * W + i]);
     bk[j] = bias ? bias[cc + j] : 0.f;
   }
   float win[W - 1][CPL], dzw[W - 1][CPL], dwa[CPL][W], dba[CPL];

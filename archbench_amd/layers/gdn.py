@@ -114,10 +114,10 @@ class ShortConvolution(nn.Module):
         self.bias = nn.Parameter(torch.zeros(dim)) if bias else None
 
     def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
-        # the weight is rounded to the activation dtype first, as the reference's conv runs it (nsgdn.py:464)
-        w = self.weight.squeeze(1).to(x.dtype).float()
+        # the kernel uses the taps rounded to the activation dtype, as the reference's conv runs its weight
+        # (nsgdn.py:464); the bias is rounded here
         b = None if self.bias is None else self.bias.to(x.dtype).float()
-        return ops.short_conv(x, w, b, state, self.norm_group)
+        return ops.short_conv(x, self.weight.squeeze(1), b, state, self.norm_group)
 
 
 class GatedRMSNorm(nn.Module):
@@ -211,12 +211,11 @@ class GatedDeltaNet(nn.Module):
         convs = (self.q_conv1d, self.k_conv1d, self.v_conv1d) if self.use_short_conv else ()
         if convs and entry is None and not use_cache and all(c.bias is None for c in convs):
             # training / prefill without a cache: the convolutions read q, k, v straight out of the projection's
-            # output and their backward writes into one gradient of it (ops.mixer_input_stage); the weights are
-            # rounded to the activation dtype first, as ShortConvolution does
+            # output and their backward writes into one gradient of it (ops.mixer_input_stage)
             y, gate, ab = self._grouped_projections(hidden_states)
             a, b = torch.split(ab, [self.a_proj.out_features, self.b_proj.out_features], dim=-1)
-            wq, wk, wv = (c.weight.squeeze(1).to(y.dtype).float() for c in convs)
-            q, k, v, _ = ops.mixer_input_stage(y, wq, wk, wv, self.key_dim, self.value_dim, DK)
+            w = torch.cat([c.weight.squeeze(1) for c in convs], 0)
+            q, k, v = ops.mixer_input_stage(y, w, self.key_dim, self.value_dim, DK)
             gp = [gate] if self.use_gate else []
         else:
             q, k, v, a, b, *gp = self.input_projections(hidden_states)

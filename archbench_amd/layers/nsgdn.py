@@ -6,7 +6,7 @@ gate, and the a / b gate inputs in one projection), ``conv.weight`` [2*H*DK + H*
 zero-init rule for ``o_proj`` (archbench/model.py:14, :80-82) apply.  The forward computes what
 ``NStepGDN.forward`` does (nsgdn.py:518-542):
 
-    qkv = conv(in_proj(x)) with SiLU           -> ops.short_conv, three calls on the weight's row slices, q and k
+    qkv = conv(in_proj(x)) with SiLU           -> ops.mixer_input_stage, three conv launches on the weight's rows, q and k
                                                   L2-normalised per head inside the conv (nsgdn.py:527-528)
     la, beta from ab                           -> ops.gdn_gates (nsgdn.py:531-534, optional la_min clamp)
     u = write_direction(k, p, beta, lam, n)    -> ops.write_direction, one HIP pass each way with p = the previous
@@ -101,10 +101,9 @@ class NStepGDN(nn.Module):
         y, *g, ab = _grouped_linear(xp, self.in_proj.weight, bounds)
         g = g[0] if g else None
         if self.conv is not None:
-            w = self.conv.weight.squeeze(1).to(y.dtype).float()  # rounded as the reference's conv runs it
-            # q, k, v convolved straight out of y (ops.mixer_input_stage)
-            q, k, v, _ = ops.mixer_input_stage(y, w[:self.qk_dim], w[self.qk_dim:2 * self.qk_dim],
-                                               w[2 * self.qk_dim:], self.qk_dim, self.v_dim, DK)
+            # q, k, v convolved straight out of y (ops.mixer_input_stage; the taps used rounded to y's dtype, as
+            # the reference's conv runs them)
+            q, k, v = ops.mixer_input_stage(y, self.conv.weight.squeeze(1), self.qk_dim, self.v_dim, DK)
         else:
             qs, ks, vs = torch.split(y, [self.qk_dim, self.qk_dim, self.v_dim], dim=-1)
             q, k, v = ops.l2norm(qs, 1e-12, 1.0), ops.l2norm(ks, 1e-12, 1.0), vs

@@ -519,15 +519,19 @@ def short_conv_bwd(x: Tensor, w: Tensor, bias: Optional[Tensor], state: Optional
 
 
 def _conv_bwd_launch(x: Tensor, w: Tensor, bias: Optional[Tensor], state: Optional[Tensor], dy: Tensor, dx: Tensor,
-                     lddx: int, norm_group: int) -> tuple[Tensor, Tensor, Tensor]:
+                     lddx: int, norm_group: int, dw: Optional[Tensor] = None) -> tuple[Tensor, Tensor, Tensor]:
     """The conv backward into dx, whose tokens lie lddx elements apart (dx may be a column slice of a wider
-    gradient); returns (dw, dbias, dstate)."""
+    gradient), and into dw when given (contiguous fp32 [D, W], e.g. a row slice of a larger weight gradient);
+    returns (dw, dbias, dstate)."""
     B, T, D, W = _conv_shapes(x, w, bias, state)
     lib = _lib.load()
     dy = _arg(dy, x.dtype)
     x, ldx = _token_rows(x)
     w, bias, state = _arg(w, torch.float32), _arg(bias, torch.float32), _arg(state, x.dtype)
-    dw = torch.empty(D, W, dtype=torch.float32, device=x.device)
+    if dw is None:
+        dw = torch.empty(D, W, dtype=torch.float32, device=x.device)
+    elif dw.shape != (D, W) or dw.dtype != torch.float32 or not dw.is_contiguous() or dw.data_ptr() % 16:
+        raise ValueError(f"dw must be a contiguous 16-byte aligned fp32 [{D}, {W}] tensor")
     db = torch.empty(D, dtype=torch.float32, device=x.device)
     dstate = torch.empty(B, D, W - 1, dtype=x.dtype, device=x.device)
     ws = torch.empty(_lib.conv_ws_bytes(B, T, D, W), dtype=torch.uint8, device=x.device)
@@ -577,74 +581,68 @@ def _conv_backward(ctx, dy, dstate_out):
 short_conv.register_autograd(_conv_backward, setup_context=_conv_setup)
 
 
-# The mixer's input stage in one op: q, k and v convolved straight out of the fused input projection's output y
-# [B, T, 2 key_dim + value_dim + gate_dim] (its column groups, read in place), and the gate columns passed on.
-# The backward writes dq, dk, dv and the gate's gradient into the column slices of one dy, so no gradient of a
-# split has to be concatenated (the conv backward takes dx's row stride).
-def _stage_dims(y: Tensor, key_dim: int, value_dim: int):
-    if y.dim() != 3 or y.shape[-1] < 2 * key_dim + value_dim:
-        raise ValueError(f"y must be [B, T, >= 2 key_dim + value_dim = {2 * key_dim + value_dim}], got "
-                         f"{tuple(y.shape)}")
-    return (0, key_dim), (key_dim, key_dim), (2 * key_dim, value_dim), 2 * key_dim + value_dim
+# The mixer's input stage in one op: q, k and v convolved straight out of the q/k/v input projection's output y
+# [B, T, 2 key_dim + value_dim] (its column groups, read in place), with one weight [2 key_dim + value_dim, W] for
+# the three convolutions (q's rows, then k's, then v's).  The backward writes dq, dk, dv's input gradients into the
+# column slices of one dy and the three weight gradients into the row slices of one dw, so no gradient of a split
+# or of a concatenation costs a pass (the conv backward takes dx's row stride).
+def _stage_dims(y: Tensor, w: Tensor, key_dim: int, value_dim: int):
+    n = 2 * key_dim + value_dim
+    if y.dim() != 3 or y.shape[-1] != n:
+        raise ValueError(f"y must be [B, T, 2 key_dim + value_dim = {n}], got {tuple(y.shape)}")
+    if w.dim() != 2 or w.shape[0] != n:
+        raise ValueError(f"w must be [2 key_dim + value_dim = {n}, W], got {tuple(w.shape)}")
+    return (0, key_dim), (key_dim, key_dim), (2 * key_dim, value_dim)
 
 
 @torch.library.custom_op("archbench_amd::mixer_input_stage", mutates_args=())
-def mixer_input_stage(y: Tensor, wq: Tensor, wk: Tensor, wv: Tensor, key_dim: int, value_dim: int,
-                      norm_group: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """(q, k, v, gate): silu(causal conv(.)) of y's q, k and v columns (q and k L2-normalised per norm_group
-    channels; conv weights [D, W] fp32, no bias, no state) and y's remaining columns as a contiguous tensor."""
-    _require_gpu(y, wq, wk, wv)
-    (q0, dq_), (k0, dk_), (v0, dv_), g0 = _stage_dims(y, key_dim, value_dim)
-    outs = [short_conv(y[..., c0:c0 + d], w, None, None, ng)[0]
-            for (c0, d), w, ng in (((q0, dq_), wq, norm_group), ((k0, dk_), wk, norm_group), ((v0, dv_), wv, 0))]
-    return (*outs, y[..., g0:].clone(memory_format=torch.contiguous_format))  # a copy even when empty
+def mixer_input_stage(y: Tensor, w: Tensor, key_dim: int, value_dim: int,
+                      norm_group: int) -> tuple[Tensor, Tensor, Tensor]:
+    """(q, k, v): silu(causal conv(.)) of y's q, k and v columns (q and k L2-normalised per norm_group channels;
+    conv weights fp32, used rounded to y's dtype; no bias, no state)."""
+    _require_gpu(y, w)
+    cols = _stage_dims(y, w, key_dim, value_dim)
+    w = _arg(w, torch.float32)
+    return tuple(short_conv(y[..., c0:c0 + d], w[c0:c0 + d], None, None, ng)[0]
+                 for (c0, d), ng in zip(cols, (norm_group, norm_group, 0)))
 
 
 @mixer_input_stage.register_fake
-def _(y, wq, wk, wv, key_dim, value_dim, norm_group):
-    B, T, L = y.shape
-    g = L - 2 * key_dim - value_dim
-    return y.new_empty(B, T, key_dim), y.new_empty(B, T, key_dim), y.new_empty(B, T, value_dim), y.new_empty(B, T, g)
+def _(y, w, key_dim, value_dim, norm_group):
+    B, T, _ = y.shape
+    return y.new_empty(B, T, key_dim), y.new_empty(B, T, key_dim), y.new_empty(B, T, value_dim)
 
 
 @torch.library.custom_op("archbench_amd::mixer_input_stage_bwd", mutates_args=())
-def mixer_input_stage_bwd(y: Tensor, wq: Tensor, wk: Tensor, wv: Tensor, dq: Tensor, dk: Tensor, dv: Tensor,
-                          dgate: Tensor, key_dim: int, value_dim: int,
-                          norm_group: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """(dy, dwq, dwk, dwv): the three conv backwards written into dy's column slices, the gate's gradient copied
-    into the rest."""
-    _require_gpu(y, wq, wk, wv, dq, dk, dv, dgate)
-    (q0, dq_), (k0, dk_), (v0, dv_), g0 = _stage_dims(y, key_dim, value_dim)
+def mixer_input_stage_bwd(y: Tensor, w: Tensor, dq: Tensor, dk: Tensor, dv: Tensor, key_dim: int, value_dim: int,
+                          norm_group: int) -> tuple[Tensor, Tensor]:
+    """(dy, dw): the three conv backwards written into dy's column slices and dw's row slices (dw fp32)."""
+    _require_gpu(y, w, dq, dk, dv)
+    cols = _stage_dims(y, w, key_dim, value_dim)
+    w = _arg(w, torch.float32)
     B, T, L = y.shape
     dy = y.new_empty(B, T, L)
-    dws = []
-    for (c0, d), w, g, ng in (((q0, dq_), wq, dq, norm_group), ((k0, dk_), wk, dk, norm_group),
-                              ((v0, dv_), wv, dv, 0)):
-        dws.append(_conv_bwd_launch(y[..., c0:c0 + d], w, None, None, g, dy[..., c0:c0 + d], L, ng)[0])
-    if L > g0:
-        dy[..., g0:].copy_(dgate)
-    return (dy, *dws)
+    dw = torch.empty(w.shape, dtype=torch.float32, device=w.device)
+    for (c0, d), g, ng in zip(cols, (dq, dk, dv), (norm_group, norm_group, 0)):
+        _conv_bwd_launch(y[..., c0:c0 + d], w[c0:c0 + d], None, None, g, dy[..., c0:c0 + d], L, ng, dw[c0:c0 + d])
+    return dy, dw
 
 
 @mixer_input_stage_bwd.register_fake
-def _(y, wq, wk, wv, dq, dk, dv, dgate, key_dim, value_dim, norm_group):
-    f32 = dict(dtype=torch.float32)
-    return (torch.empty_like(y), wq.new_empty(wq.shape, **f32), wk.new_empty(wk.shape, **f32),
-            wv.new_empty(wv.shape, **f32))
+def _(y, w, dq, dk, dv, key_dim, value_dim, norm_group):
+    return torch.empty_like(y), w.new_empty(w.shape, dtype=torch.float32)
 
 
 def _stage_setup(ctx, inputs, output):
-    y, wq, wk, wv, key_dim, value_dim, norm_group = inputs
-    ctx.save_for_backward(y, wq, wk, wv)
+    y, w, key_dim, value_dim, norm_group = inputs
+    ctx.save_for_backward(y, w)
     ctx.dims = (key_dim, value_dim, norm_group)
-    ctx.w_dtypes = (wq.dtype, wk.dtype, wv.dtype)
 
 
-def _stage_backward(ctx, dq, dk, dv, dgate):
-    y, wq, wk, wv = ctx.saved_tensors
-    dy, dwq, dwk, dwv = mixer_input_stage_bwd(y, wq, wk, wv, dq.contiguous(), dk.contiguous(), dv.contiguous(),
-                                              dgate.contiguous(), *ctx.dims)
-    return (dy, dwq.to(ctx.w_dtypes[0]), dwk.to(ctx.w_dtypes[1]), dwv.to(ctx.w_dtypes[2]), None, None, None)
+def _stage_backward(ctx, dq, dk, dv):
+    y, w = ctx.saved_tensors
+    dy, dw = mixer_input_stage_bwd(y, w, dq.contiguous(), dk.contiguous(), dv.contiguous(), *ctx.dims)
+    return dy, dw.to(w.dtype), None, None, None
 
 
 mixer_input_stage.register_autograd(_stage_backward, setup_context=_stage_setup)

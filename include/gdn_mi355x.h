@@ -137,7 +137,9 @@ int gdn_recurrent_step(const void* q, const void* k, const void* v, const float*
  * of q and k (nsgdn.py:527-528).  y, dy [B, T, D] token-major in dtype; x and dx [B, T] rows of D channels ldx /
  * lddx elements apart (D, or 0, when contiguous; larger to read x from, or write dx into, a column slice of a
  * wider [B, T, ld] tensor such as the output of a fused input projection or its gradient; a multiple of 4);
- * w [D, W] and bias [D] fp32 (bias may be NULL); conv states [B, D, W-1] in dtype, the previous W-1 inputs oldest
+ * w [D, W] and bias [D] fp32 (bias may be NULL); the taps are used rounded to dtype, as the reference's conv runs
+ * its weight under bf16 autocast (nsgdn.py:464), and dw is the fp32 gradient of the rounded taps; conv states
+ * [B, D, W-1] in dtype, the previous W-1 inputs oldest
  * first (state_in NULL = zeros; state_out NULL = not returned; it must not alias state_in).  Compiled for W = 4,
  * D % 4 == 0, norm_group in {0 (none), 64, 128, 256}.
  * The backward writes dx, dw [D, W] fp32, dbias [D] fp32 (if non-NULL) and dstate_in (if non-NULL); its

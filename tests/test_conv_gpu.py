@@ -177,34 +177,53 @@ def test_conv_reads_a_column_slice_in_place(dtype, T, ng):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("gate_dim", [0, 256])
-def test_mixer_input_stage_equals_separate_convs(dtype, gate_dim):
-    """The fused input stage (q, k, v convolved out of one projection output, the gate passed on) gives exactly
-    the separate short convs' outputs, and its backward exactly their input gradients written into the column
-    slices of one dy (the concatenation autograd would otherwise build) plus the gate's gradient."""
-    banner(f"mixer input stage dtype={dtype} gate_dim={gate_dim}")
+def test_mixer_input_stage_equals_separate_convs(dtype):
+    """The fused input stage (q, k, v convolved out of one projection output with one weight for the three) gives
+    exactly the separate short convs' outputs, and its backward exactly their input gradients written into the
+    column slices of one dy and their weight gradients into the row slices of one dw."""
+    banner(f"mixer input stage dtype={dtype}")
     B, T, kd, vd, ng = 2, 130, 256, 512, 128
-    L = 2 * kd + vd + gate_dim
+    L = 2 * kd + vd
     gen = torch.Generator().manual_seed(11)
     y = torch.randn(B, T, L, generator=gen).to("cuda", dtype)
-    ws = [(torch.randn(d, W, generator=gen) * 0.5).cuda() for d in (kd, kd, vd)]
-    outs = ops.mixer_input_stage(y, *ws, kd, vd, ng)
+    w = (torch.randn(L, W, generator=gen) * 0.5).cuda()
+    outs = ops.mixer_input_stage(y, w, kd, vd, ng)
     cols = [(0, kd, ng), (kd, kd, ng), (2 * kd, vd, 0)]
-    for o, w, (c0, d, g) in zip(outs[:3], ws, cols):
-        assert torch.equal(o, ops.short_conv(y[..., c0:c0 + d].contiguous(), w, None, None, g)[0])
-    assert torch.equal(outs[3], y[..., 2 * kd + vd:])
+    for o, (c0, d, g) in zip(outs, cols):
+        assert torch.equal(o, ops.short_conv(y[..., c0:c0 + d].contiguous(), w[c0:c0 + d], None, None, g)[0])
     grads = [torch.randn(o.shape, generator=gen).to("cuda", dtype) for o in outs]
-    dy, *dws = ops.mixer_input_stage_bwd(y, *ws, *grads, kd, vd, ng)
-    for (c0, d, g), w, gr, dw in zip(cols, ws, grads, dws):
-        dx_ref, dw_ref, _, _ = ops.short_conv_bwd(y[..., c0:c0 + d].contiguous(), w, None, None, gr, g)
-        assert torch.equal(dy[..., c0:c0 + d], dx_ref) and torch.equal(dw, dw_ref)
-    assert torch.equal(dy[..., 2 * kd + vd:], grads[3])
+    dy, dw = ops.mixer_input_stage_bwd(y, w, *grads, kd, vd, ng)
+    for (c0, d, g), gr in zip(cols, grads):
+        dx_ref, dw_ref, _, _ = ops.short_conv_bwd(y[..., c0:c0 + d].contiguous(), w[c0:c0 + d], None, None, gr, g)
+        assert torch.equal(dy[..., c0:c0 + d], dx_ref) and torch.equal(dw[c0:c0 + d], dw_ref)
     # through autograd: every input gradient of the stage at once
-    ya = y.detach().requires_grad_()
-    wa = [w.detach().requires_grad_() for w in ws]
-    out = ops.mixer_input_stage(ya, *wa, kd, vd, ng)
+    ya, wa = y.detach().requires_grad_(), w.detach().requires_grad_()
+    out = ops.mixer_input_stage(ya, wa, kd, vd, ng)
     torch.autograd.backward(out, grads)
-    assert torch.equal(ya.grad, dy) and all(torch.equal(w.grad, d) for w, d in zip(wa, dws))
+    assert torch.equal(ya.grad, dy) and torch.equal(wa.grad, dw)
+    with pytest.raises(ValueError, match="2 key_dim"):
+        ops.mixer_input_stage(y[..., :-4], w, kd, vd, ng)
+
+
+def test_conv_taps_rounded_to_activation_dtype():
+    """With bf16 activations the kernels use the taps rounded to bf16 (as the reference's conv runs its fp32
+    weight under bf16 autocast): an fp32 weight gives bit for bit what its bf16-rounded copy gives, forward and
+    backward; with fp32 activations the taps are used as they are."""
+    banner("short conv taps rounded to the activation dtype")
+    B, T, D = 2, 100, 256
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(B, T, D, generator=gen).cuda()
+    dy = torch.randn(B, T, D, generator=gen).cuda()
+    w = (torch.randn(D, W, generator=gen) * 0.5).cuda()
+    wr = w.bfloat16().float()
+    assert not torch.equal(w, wr)
+    for ng in (0, 128):
+        xb, dyb = x.bfloat16(), dy.bfloat16()
+        assert torch.equal(ops.short_conv(xb, w, None, None, ng)[0], ops.short_conv(xb, wr, None, None, ng)[0])
+        a = ops.short_conv_bwd(xb, w, None, None, dyb, ng)
+        b = ops.short_conv_bwd(xb, wr, None, None, dyb, ng)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+        assert not torch.equal(ops.short_conv(x, w, None, None, ng)[0], ops.short_conv(x, wr, None, None, ng)[0])
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
