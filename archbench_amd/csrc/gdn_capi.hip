@@ -159,12 +159,13 @@ static hipError_t copy_or_zero(const float* src, float* dst, int64_t n, hipStrea
 enum Stage {
   ST_FWD = 0, ST_BWD_RECOMP, ST_BWD_STATE, ST_BWD_INTRA, ST_STEP, ST_FWD_STASH, ST_FACTORS, ST_CONV_FWD,
   ST_CONV_BWD, ST_NORM_FWD, ST_NORM_BWD, ST_GATES_FWD, ST_GATES_BWD, ST_L2_FWD, ST_L2_BWD, ST_CE, ST_PREFIX,
-  ST_SEGSCAN, ST_BWD_LOCAL, ST_WD_FWD, ST_WD_BWD, ST_COUNT
+  ST_SEGSCAN, ST_BWD_LOCAL, ST_WD_FWD, ST_WD_BWD, ST_TSCAN_FWD, ST_TSCAN_BWD, ST_COUNT
 };
 static const char* kStageNames[ST_COUNT] = {"fwd", "bwd_recompute", "bwd_state", "bwd_intra", "step", "fwd_stash",
                                             "factors", "conv_fwd", "conv_bwd", "norm_fwd", "norm_bwd", "gates_fwd", "gates_bwd",
                                             "l2norm_fwd", "l2norm_bwd", "cross_entropy", "prefix", "seg_scan",
-                                            "bwd_local", "write_dir_fwd", "write_dir_bwd"};
+                                            "bwd_local", "write_dir_fwd", "write_dir_bwd", "token_scan_fwd",
+                                            "token_scan_bwd"};
 struct ProfRec { int stage; hipEvent_t a, b; };
 struct Prof {
   std::atomic<bool> on{false};
@@ -810,6 +811,67 @@ int gdn_write_direction_bwd(const void* k, const float* beta, const float* lam, 
   a.stream = static_cast<hipStream_t>(stream);
   const hipError_t e = timed(ST_WD_BWD, a.stream, [&] { return launch_write_dir(a, true); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "write direction backward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+static int token_scan_check(int B, int T, int H, int K, int V) {
+  if (B < 0 || T < 0 || H <= 0 || V <= 0) return fail(GDN_ERR_ARG, "invalid sizes B=%d T=%d H=%d V=%d", B, T, H, V);
+  if (!token_scan_supported(K)) return fail(GDN_ERR_SHAPE, "token scan not compiled for K=%d (K in {64, 128})", K);
+  if ((int64_t)B * H * ((V + 63) / 64) > INT32_MAX) return fail(GDN_ERR_ARG, "grid too large");
+  return GDN_OK;
+}
+
+int gdn_token_scan_sizes(int B, int T, int H, int K, int V, size_t* st_bytes, size_t* scratch_bytes,
+                         int* n_partials) {
+  g_err[0] = 0;
+  if (int e = token_scan_check(B, T, H, K, V)) return e;
+  if (!st_bytes || !scratch_bytes || !n_partials) return fail(GDN_ERR_ARG, "null output pointer");
+  const size_t NB = (size_t)(V + 63) / 64, NCH = (size_t)(T + token_scan_ct() - 1) / token_scan_ct();
+  *st_bytes = (size_t)B * H * NCH * K * V * 4;
+  *scratch_bytes = (size_t)B * H * NB * token_scan_ct() * K * 64 * 4;
+  *n_partials = (int)NB;
+  return GDN_OK;
+}
+
+int gdn_token_scan_fwd(const float* q, const float* k, const float* u, const float* v, const float* la, float* y,
+                       float* r, float* st, size_t st_bytes, int B, int T, int H, int K, int V, void* stream) {
+  size_t need_st = 0, need_sc = 0;
+  int nb = 0;
+  if (int e = gdn_token_scan_sizes(B, T, H, K, V, &need_st, &need_sc, &nb)) return e;
+  if ((int64_t)B * T == 0) return GDN_OK;
+  if (!q || !k || !u || !v || !la || !y || !r || !st) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (st_bytes < need_st) return fail(GDN_ERR_WORKSPACE, "checkpoint buffer %zu bytes, need %zu", st_bytes, need_st);
+  TokenScanArgs a{};
+  a.q = q; a.k = k; a.u = u; a.v = v; a.la = la; a.y = y; a.r = r; a.st = st;
+  a.B = B; a.T = T; a.H = H; a.K = K; a.V = V;
+  a.stream = static_cast<hipStream_t>(stream);
+  const hipError_t e = timed(ST_TSCAN_FWD, a.stream, [&] { return launch_token_scan(a, false); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "token scan forward launch: %s", hipGetErrorString(e));
+  return GDN_OK;
+}
+
+int gdn_token_scan_bwd(const float* q, const float* k, const float* u, const float* la, const float* r,
+                       const float* st, size_t st_bytes, const float* dy, float* dv, float* dq_part, float* du_part,
+                       float* dk_part, float* dla_part, float* scratch, size_t scratch_bytes, int B, int T, int H,
+                       int K, int V, void* stream) {
+  size_t need_st = 0, need_sc = 0;
+  int nb = 0;
+  if (int e = gdn_token_scan_sizes(B, T, H, K, V, &need_st, &need_sc, &nb)) return e;
+  if ((int64_t)B * T == 0) return GDN_OK;
+  if (!q || !k || !u || !la || !r || !st || !dy || !dv || !dq_part || !du_part || !dk_part || !dla_part || !scratch)
+    return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (st_bytes < need_st) return fail(GDN_ERR_WORKSPACE, "checkpoint buffer %zu bytes, need %zu", st_bytes, need_st);
+  if (scratch_bytes < need_sc)
+    return fail(GDN_ERR_WORKSPACE, "scratch %zu bytes, need %zu", scratch_bytes, need_sc);
+  TokenScanArgs a{};
+  a.q = q; a.k = k; a.u = u; a.la = la; a.dy = dy; a.dv = dv;
+  a.r = const_cast<float*>(r);  // read only here (the forward writes them)
+  a.st = const_cast<float*>(st);
+  a.dq_part = dq_part; a.du_part = du_part; a.dk_part = dk_part; a.dla_part = dla_part; a.scratch = scratch;
+  a.B = B; a.T = T; a.H = H; a.K = K; a.V = V;
+  a.stream = static_cast<hipStream_t>(stream);
+  const hipError_t e = timed(ST_TSCAN_BWD, a.stream, [&] { return launch_token_scan(a, true); });
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "token scan backward launch: %s", hipGetErrorString(e));
   return GDN_OK;
 }
 

@@ -194,6 +194,19 @@ struct WriteDirArgs {
 bool write_dir_supported(int K, int n_steps);
 hipError_t launch_write_dir(const WriteDirArgs& a, bool backward);
 
+// Exact fp32 token scan of the n-step family (gdn_tokenscan.hip)
+struct TokenScanArgs {
+  const float *q, *k, *u, *v, *la;  // [B, T, H, K] x3, [B, T, H, V], [B, T, H]
+  float *y, *r, *st;                // forward: y, r [B, T, H, V]; st [B H][ceil(T / ct)][K][V] checkpoints
+  const float* dy;                  // backward
+  float *dv, *dq_part, *du_part, *dk_part, *dla_part, *scratch;  // partials [NB][B T H][K] ([NB][B T H] for dla)
+  int B, T, H, K, V;
+  hipStream_t stream;
+};
+bool token_scan_supported(int K);
+int token_scan_ct();
+hipError_t launch_token_scan(const TokenScanArgs& a, bool backward);
+
 // Compute units of the current device (cached per device; 256 if the query fails).
 int device_cu_count();
 // Whether a state sweep with `blocks_per_head` 32-column blocks per (b, h) runs those narrow blocks (four waves

@@ -15,11 +15,12 @@ zero-init rule for ``o_proj`` (archbench/model.py:14, :80-82) apply.  The forwar
                                                   q scale DK^-1/2 is the op's scale instead of a separate pass
     y = norm(y) * silu(g); o_proj              -> ops.gated_rmsnorm
 
-``scan_impl``: every choice runs the HIP chunk kernels in bf16 with fp32 state and accumulation, which is what
-the reference's default "chunk" (and "dplr") run (``nsgdn.py:404-405``).  The reference's "triton" and "ref"
-choices are exact fp32 token scans (``nsgdn.py:52-58``, ``:80-216``, ``:408-417``); there is no token-scan path
-here (its exact backward keeps a state per token), so selecting them warns once that the numerics are the chunk
-form's (relative L2 error within 1e-2 of the fp32 recurrence) rather than running silently.
+``scan_impl``: "chunk" and "dplr" run the HIP chunk kernels in bf16 with fp32 state and accumulation, which is
+what the reference's "chunk" (its default) and "dplr" run (``nsgdn.py:404-405``).  "triton" and "ref" are the
+reference's exact fp32 token scan (``nsgdn.py:52-58``, ``:80-216``, ``:408-417``), here ``ops.nsgdn_scan`` (the HIP
+token scan with its checkpointed reverse-time backward): fp32 q, k, u, v, the write direction computed in fp32, and
+y kept in fp32 through the output norm, as the reference's module keeps them.  That scan is compiled for head_dim
+64 and 128; other head sizes fall back to the chunk kernels with a warning.
 """
 
 from __future__ import annotations
@@ -66,10 +67,10 @@ class NStepGDN(nn.Module):
             raise ValueError("lam must be > 0")
         if scan_impl not in ("chunk", "dplr", "triton", "ref"):
             raise ValueError(f"unknown scan_impl {scan_impl!r}")
-        if scan_impl in ("triton", "ref"):
-            warnings.warn(f"NStepGDN(scan_impl={scan_impl!r}): the reference runs an exact fp32 token scan here; "
-                          "this build runs the bf16 chunk kernels for every scan_impl (fp32 state and "
-                          "accumulation, relative L2 within 1e-2 of the fp32 recurrence)", UserWarning, stacklevel=2)
+        if scan_impl in ("triton", "ref") and DK not in (64, 128):
+            warnings.warn(f"NStepGDN(scan_impl={scan_impl!r}): the exact fp32 token scan is compiled for head_dim 64 "
+                          f"and 128; head_dim {DK} runs the bf16 chunk kernels (fp32 state and accumulation, relative "
+                          "L2 within 1e-2 of the fp32 recurrence)", UserWarning, stacklevel=2)
         self.H, self.DK, self.DV, self.n_steps = num_heads, DK, DV, n_steps
         self.qk_dim, self.v_dim = num_heads * DK, num_heads * DV
         self.use_gate = use_gate
@@ -110,12 +111,22 @@ class NStepGDN(nn.Module):
         q, k, v = q.view(B, T, H, DK), k.view(B, T, H, DK), v.reshape(B, T, H, DV)
         la, beta = ops.gdn_gates(ab[..., :H], ab[..., H:], self.A_log, self.dt_bias, self.b_bias, 1.0,
                                  float("-inf") if self.la_min is None else float(self.la_min))
+        gate = g.reshape(B, T, H, DV) if self.use_gate else None
+        lam = F.softplus(self.lam.float())
+        eps = self.norm.eps or 1e-5
+        if self.scan_impl in ("triton", "ref") and DK in (64, 128):
+            # the reference's exact fp32 token scan (nsgdn.py:525-536 with its "triton" / "ref" scan): u from fp32
+            # k, y fp32 through the norm, cast for o_proj as autocast casts the projection's input
+            kf = k.float()
+            u = ops.write_direction(kf, beta, lam, self.n_steps)
+            y = ops.nsgdn_scan(q.float() * DK ** -0.5, kf, u, v.float(), la)
+            y = ops.gated_rmsnorm(y, None if gate is None else gate.float(), self.norm.weight, eps)
+            return _linear(y.reshape(B, T, -1).to(xp.dtype), self.o_proj.weight)
         # u from k, the previous token's k and beta in one HIP pass (fp32 arithmetic, written in k's dtype, which
         # the scan takes u in)
-        u = ops.write_direction(k, beta, F.softplus(self.lam.float()), self.n_steps)
+        u = ops.write_direction(k, beta, lam, self.n_steps)
         y = ops.nsgdn_scan_chunk(q, k, u, v, la, scale=DK ** -0.5)
-        gate = g.reshape(B, T, H, DV) if self.use_gate else None
-        y = ops.gated_rmsnorm(y.to(xp.dtype), gate, self.norm.weight, self.norm.eps or 1e-5)
+        y = ops.gated_rmsnorm(y.to(xp.dtype), gate, self.norm.weight, eps)
         return _linear(y.reshape(B, T, -1), self.o_proj.weight)
 
 

@@ -32,6 +32,7 @@ a launch failure raises RuntimeError.
 
 from __future__ import annotations
 
+import ctypes
 import os
 from typing import Optional
 
@@ -41,7 +42,7 @@ from torch import Tensor
 from . import _lib
 
 __all__ = ["chunk_gated_delta_rule", "fused_recurrent_gated_delta_rule", "recurrent_step", "chunk_fwd",
-           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "nsgdn_scan_chunk", "short_conv", "mixer_input_stage", "write_direction",
+           "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "nsgdn_scan", "nsgdn_scan_chunk", "short_conv", "mixer_input_stage", "write_direction",
            "gated_rmsnorm", "l2norm", "gdn_gates", "cross_entropy_fwd_bwd_"]
 
 
@@ -453,6 +454,114 @@ def _wd_backward(ctx, du):
 
 
 write_direction.register_autograd(_wd_backward, setup_context=_wd_setup)
+
+
+# The exact fp32 token scan of the n-step family (the reference's "triton" / "ref" scan_impl): archbench::nsgdn_fwd
+# and nsgdn_bwd (nsgdn.py:162-216) on gdn_tokenscan.hip.  The forward returns y, the residuals r and the state
+# checkpoints, which its backward restarts from; the backward's dq, du, dk and dla come as per-wave-row-block
+# partials that are added here in a fixed order.
+TOKEN_SCAN_CT = 32  # tokens between the forward's checkpoints (gdn_tokenscan.hip)
+
+
+def _token_shapes(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor):
+    if q.dim() != 4 or k.shape != q.shape or u.shape != q.shape:
+        raise ValueError(f"q, k, u must be [B, T, H, K] alike, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(u.shape)}")
+    B, T, H, K = q.shape
+    if v.dim() != 4 or tuple(v.shape[:3]) != (B, T, H) or tuple(la.shape) != (B, T, H):
+        raise ValueError(f"v must be [B, T, H, V] and la [B, T, H] with (B, T, H) = {(B, T, H)}, got "
+                         f"{tuple(v.shape)}, {tuple(la.shape)}")
+    return B, T, H, K, v.shape[-1]
+
+
+def _token_sizes(lib, B, T, H, K, V):
+    st, sc, nb = ctypes.c_size_t(0), ctypes.c_size_t(0), ctypes.c_int(0)
+    _lib.check(lib.gdn_token_scan_sizes(B, T, H, K, V, ctypes.byref(st), ctypes.byref(sc), ctypes.byref(nb)),
+               "gdn_token_scan_sizes")
+    return st.value, sc.value, nb.value
+
+
+@torch.library.custom_op("archbench_amd::nsgdn_token_fwd", mutates_args=())
+def nsgdn_token_fwd(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """(y, r, st), fp32: the scan's output, its residuals r = v - (e^la S) k and the state checkpoints."""
+    _require_gpu(q, k, u, v, la)
+    B, T, H, K, V = _token_shapes(q, k, u, v, la)
+    lib = _lib.load()
+    q, k, u, v, la = (_arg(t, torch.float32) for t in (q, k, u, v, la))
+    st_bytes, _, _ = _token_sizes(lib, B, T, H, K, V)
+    y, r = torch.empty_like(v), torch.empty_like(v)
+    st = torch.empty(st_bytes // 4, dtype=torch.float32, device=q.device)
+    rc = lib.gdn_token_scan_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(u), _lib.ptr(v), _lib.ptr(la), _lib.ptr(y),
+                                _lib.ptr(r), _lib.ptr(st), st_bytes, B, T, H, K, V, _lib.stream_ptr(q.device))
+    _lib.check(rc, "gdn_token_scan_fwd")
+    return y, r, st
+
+
+@nsgdn_token_fwd.register_fake
+def _(q, k, u, v, la):
+    B, T, H, K = q.shape
+    V = v.shape[-1]
+    nch = -(-T // TOKEN_SCAN_CT)
+    f32 = dict(dtype=torch.float32)
+    return v.new_empty(v.shape, **f32), v.new_empty(v.shape, **f32), v.new_empty(B * H * nch * K * V, **f32)
+
+
+@torch.library.custom_op("archbench_amd::nsgdn_token_bwd", mutates_args=())
+def nsgdn_token_bwd(q: Tensor, k: Tensor, u: Tensor, la: Tensor, r: Tensor, st: Tensor,
+                    dy: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(dq, dk, du, dv, dla), fp32."""
+    _require_gpu(q, k, u, la, r, st, dy)
+    B, T, H, K, V = _token_shapes(q, k, u, r, la)
+    lib = _lib.load()
+    q, k, u, la, r, dy = (_arg(t, torch.float32) for t in (q, k, u, la, r, dy))
+    st_bytes, sc_bytes, nb = _token_sizes(lib, B, T, H, K, V)
+    if st.numel() * 4 < st_bytes:
+        raise ValueError("st is not this shape's checkpoint buffer")
+    dev = q.device
+    parts = [torch.empty(nb, B, T, H, K, dtype=torch.float32, device=dev) for _ in range(3)]
+    dla_p = torch.empty(nb, B, T, H, dtype=torch.float32, device=dev)
+    dv = torch.empty_like(r)
+    sc = torch.empty(max(sc_bytes // 4, 1), dtype=torch.float32, device=dev)
+    rc = lib.gdn_token_scan_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(u), _lib.ptr(la), _lib.ptr(r), _lib.ptr(st),
+                                st.numel() * 4, _lib.ptr(dy), _lib.ptr(dv), _lib.ptr(parts[0]), _lib.ptr(parts[1]),
+                                _lib.ptr(parts[2]), _lib.ptr(dla_p), _lib.ptr(sc), sc.numel() * 4, B, T, H, K, V,
+                                _lib.stream_ptr(dev))
+    _lib.check(rc, "gdn_token_scan_bwd")
+    dq, du, dk = (p[0] if nb == 1 else p.sum(0) for p in parts)
+    return dq, dk, du, dv, (dla_p[0] if nb == 1 else dla_p.sum(0))
+
+
+@nsgdn_token_bwd.register_fake
+def _(q, k, u, la, r, st, dy):
+    f32 = dict(dtype=torch.float32)
+    return (q.new_empty(q.shape, **f32), q.new_empty(q.shape, **f32), q.new_empty(q.shape, **f32),
+            r.new_empty(r.shape, **f32), la.new_empty(la.shape, **f32))
+
+
+def _token_setup(ctx, inputs, output):
+    q, k, u, v, la = inputs
+    _, r, st = output
+    ctx.save_for_backward(q, k, u, la, r, st)
+    ctx.dtypes = tuple(t.dtype for t in inputs)
+    ctx.set_materialize_grads(False)  # r and st take no gradient: no zero-filled buffers for them
+
+
+def _token_backward(ctx, dy, dr, dst):
+    q, k, u, la, r, st = ctx.saved_tensors
+    if dy is None:
+        return None, None, None, None, None
+    grads = nsgdn_token_bwd(q, k, u, la, r, st, dy.contiguous())
+    dq, dk, du, dv, dla = grads
+    return tuple(g.to(dt) for g, dt in zip((dq, dk, du, dv, dla), ctx.dtypes))
+
+
+nsgdn_token_fwd.register_autograd(_token_backward, setup_context=_token_setup)
+
+
+def nsgdn_scan(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor) -> Tensor:
+    """archbench's nsgdn_scan (nsgdn.py:219-221): y [B, T, H, V] fp32 from the exact fp32 token scan, for q, k, u
+    [B, T, H, K] (q already scaled), v [B, T, H, V] and log-retention la [B, T, H].  Differentiable w.r.t. every
+    input; K in {64, 128}."""
+    return nsgdn_token_fwd(q.float(), k.float(), u.float(), v.float(), la.float())[0]
 
 
 def nsgdn_scan_chunk(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor, scale: float = 1.0,

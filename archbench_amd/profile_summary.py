@@ -47,6 +47,7 @@ def stage_of(name: str) -> str:
                        ("row_norm_fwd", "norm_fwd"), ("row_norm_bwd", "norm_bwd"), ("gates_fwd", "gates_fwd"),
                        ("gates_bwd", "gates_bwd"), ("ce_fwd_bwd", "cross_entropy"), ("column_sum", "column_sum"),
                        ("write_dir_fwd", "write_dir_fwd"), ("write_dir_bwd", "write_dir_bwd"),
+                       ("token_scan_fwd", "token_scan_fwd"), ("token_scan_bwd", "token_scan_bwd"),
                        ("copyBuffer", "copy"), ("copy_kernel", "copy")):
         if key in name:
             return stage

@@ -215,12 +215,29 @@ int gdn_write_direction_bwd(const void* k, const float* beta, const float* lam, 
                             float* dbeta, float* dlam, int B, int T, int H, int K, int n_steps, int dtype,
                             void* stream);
 
+/* Exact fp32 token scan of the n-step family: the reference's "triton" / "ref" scan, archbench::nsgdn_fwd and
+ * archbench::nsgdn_bwd (archbench/layers/nsgdn.py:80-154, ops :162-216, the recurrence of nsgdn_ref :408-417).
+ * Per token, with the state S [V, K] from zero: S <- e^{la} S, r = v - S k, S <- S + r u^T, y = S q.  q, k, u
+ * [B, T, H, K], v, y, r [B, T, H, V], la [B, T, H], all fp32 (q already scaled, as the reference's module does).
+ * The forward writes y, the residuals r and the state every ct tokens into st (the backward's checkpoints); the
+ * backward writes dv directly and dq, du, dk, dla as n_partials row blocks each ([n_partials][B*T*H][K],
+ * [n_partials][B*T*H]) that the caller sums over the first index (the reference adds them with atomics).  Sizes
+ * of st, of the backward's scratch and n_partials from gdn_token_scan_sizes.  K in {64, 128}, any V. */
+int gdn_token_scan_sizes(int B, int T, int H, int K, int V, size_t* st_bytes, size_t* scratch_bytes,
+                         int* n_partials);
+int gdn_token_scan_fwd(const float* q, const float* k, const float* u, const float* v, const float* la, float* y,
+                       float* r, float* st, size_t st_bytes, int B, int T, int H, int K, int V, void* stream);
+int gdn_token_scan_bwd(const float* q, const float* k, const float* u, const float* la, const float* r,
+                       const float* st, size_t st_bytes, const float* dy, float* dv, float* dq_part, float* du_part,
+                       float* dk_part, float* dla_part, float* scratch, size_t scratch_bytes, int B, int T, int H,
+                       int K, int V, void* stream);
+
 /* Per-stage kernel timing (diagnostic; no counterpart in the reference, which times whole phases with CUDA
  * events in archbench/logger.py:57-81).  While enabled (process-wide: launches from any host thread count), every
  * kernel the calls above enqueue is bracketed by hipEvents on the same stream.  gdn_profile_read synchronises on those events and
  * returns, per stage, the summed milliseconds and the number of launches (arrays of at least
  * GDN_PROFILE_STAGES entries), then clears the record.  Stage names: gdn_profile_stage_name. */
-#define GDN_PROFILE_STAGES 21
+#define GDN_PROFILE_STAGES 23
 int gdn_profile_enable(int on);
 int gdn_profile_read(double* ms_sum, int* launches, int n_stages);
 const char* gdn_profile_stage_name(int stage);

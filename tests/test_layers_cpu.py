@@ -101,18 +101,21 @@ def test_nsgdn_registered_and_no_cpu_fallback():
         layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=48)
 
 
-def test_nsgdn_token_scan_choices_warn():
-    """The reference's "triton" and "ref" scan_impl are exact fp32 token scans; this build runs the chunk kernels
-    for every choice and says so for those two, while the reference's own default ("chunk") builds quietly."""
+def test_nsgdn_token_scan_choices():
+    """The reference's "triton" and "ref" scan_impl are its exact fp32 token scan, which this build runs for
+    head_dim 64 and 128 (quietly, as for "chunk" and "dplr"); other head sizes fall back to the chunk kernels and
+    say so."""
     import warnings
 
-    for impl in ("triton", "ref"):
-        with pytest.warns(UserWarning, match="fp32 token scan"):
-            layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=64, scan_impl=impl)
     with warnings.catch_warnings():
         warnings.simplefilter("error")
-        for impl in ("chunk", "dplr"):
-            layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=64, scan_impl=impl)
+        for impl in ("chunk", "dplr", "triton", "ref"):
+            for hd in (64, 128):
+                m = layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=hd, scan_impl=impl)
+                assert m.scan_impl == impl
+    for impl in ("triton", "ref"):
+        with pytest.warns(UserWarning, match="fp32 token scan"):
+            layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=32, scan_impl=impl)
     with pytest.raises(ValueError):
         layers.build_mixer("nsgdn", 128, 0, 2, num_heads=2, head_dim=64, scan_impl="cuda")
 

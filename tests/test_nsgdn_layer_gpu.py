@@ -67,3 +67,35 @@ def test_nsgdn_layer_matches_reference_forward_backward():
         # so that sensitivity widens the bound
         noise = rel_l2(gr_exact[n], gr[n])
         assert rel_l2(p.grad, gr[n]) <= 3e-2 + 4 * noise, (n, noise)
+
+
+@pytest.mark.parametrize("impl,DK", [("triton", 64), ("ref", 128)])
+def test_nsgdn_layer_exact_scan_matches_in_fp32(impl, DK):
+    """scan_impl "triton" / "ref" run the reference's exact fp32 token scan (ops.nsgdn_scan).  Without autocast
+    every pass of the layer is fp32 (projections, conv, gates, write direction, scan, norm), so the whole mixer
+    must match the fp64 restatement of NStepGDN.forward to fp32 accuracy: output and input gradient rel-L2
+    <= 1e-5, every parameter gradient <= 1e-4 (the per-head vectors' are cancelling sums over every token)."""
+    banner(f"nsgdn layer, scan_impl={impl}, fp32 vs fp64 restatement")
+    torch.manual_seed(3)
+    H, DV, d = 2, 2 * DK, 192
+    m = layers.build_mixer("nsgdn", d, 0, 2, num_heads=H, head_dim=DK, expand_v=2.0, n_steps=2, lam=1.0,
+                           scan_impl=impl).cuda()
+    for n, p in m.named_parameters():
+        if p.dim() == 2:
+            torch.nn.init.normal_(p, std=0.05)
+    x = torch.randn(2, 70, d, generator=torch.Generator().manual_seed(4))
+    xd = x.cuda().requires_grad_()
+    y = m(xd)
+    assert y.dtype == torch.float32
+    dy = torch.randn(*y.shape, generator=torch.Generator().manual_seed(5))
+    y.backward(dy.cuda())
+    P = {n: p.detach().cpu().double().requires_grad_() for n, p in m.named_parameters()}
+    xr = x.double().requires_grad_()
+    yr = _reference_forward(P, xr, H, DK, DV, 2, 4, m.norm.eps or 1e-5, bf16_scan=False)
+    yr.backward(dy.double())
+    errs = {"y": rel_l2(y, yr), "dx": rel_l2(xd.grad, xr.grad)}
+    errs.update({n: rel_l2(p.grad, P[n].grad) for n, p in m.named_parameters()})
+    print("rel-L2:", {n: f"{e:.1e}" for n, e in errs.items()}, flush=True)
+    assert errs["y"] <= 1e-5 and errs["dx"] <= 1e-5, errs
+    for n, _ in m.named_parameters():
+        assert errs[n] <= 1e-4, (n, errs[n])
