@@ -149,6 +149,18 @@ def test_opcheck():
             b.requires_grad_(), h0.requires_grad_(), 0.5)
     torch.library.opcheck(torch.ops.archbench_amd.gdn_chunk_fwd.default, args,
                           test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
+    # the ops added around the chunk op: write direction, fp32 token scan, mixer input stage
+    utils = ("test_schema", "test_faketensor", "test_autograd_registration")
+    k = torch.nn.functional.normalize(torch.randn(1, 70, 2, 64, device="cuda"), dim=-1).requires_grad_()
+    beta, lam = torch.rand(1, 70, 2, device="cuda").requires_grad_(), torch.rand(2, device="cuda").requires_grad_()
+    torch.library.opcheck(torch.ops.archbench_amd.write_direction.default, (k, beta, lam, 2), test_utils=utils)
+    la = (-torch.rand(1, 70, 2, device="cuda")).requires_grad_()
+    qs = [torch.randn(1, 70, 2, 64, device="cuda").requires_grad_() for _ in range(3)]
+    torch.library.opcheck(torch.ops.archbench_amd.nsgdn_token_fwd.default, (*qs, v.detach().requires_grad_(), la),
+                          test_utils=utils)
+    y = torch.randn(1, 70, 512, device="cuda", dtype=torch.bfloat16).requires_grad_()
+    w = (torch.randn(512, 4, device="cuda") * 0.5).requires_grad_()
+    torch.library.opcheck(torch.ops.archbench_amd.mixer_input_stage.default, (y, w, 128, 256, 64), test_utils=utils)
 
 
 def test_decode_advances_cache_state_in_place(monkeypatch):
