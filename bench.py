@@ -38,6 +38,9 @@ Also reported in the same line:
                 step, as after zero_grad(set_to_none=True)), tokens/s, with the library's kernels' share of the step;
   nsgdn_layer   the same for archbench's `nsgdn` mixer (configs/65m/nsgdn.yaml: n_steps 2, lam 1, the same
                 projections, conv and norm around the separate-write-key chunk kernels, plus the write direction);
+  token_scan    the exact fp32 token scan of the n-step family (the reference's scan_impl "triton" / "ref") at
+                B=16, T=1024, H=4, K=128, V=256: forward and backward kernel times (an exactness path, not a fast
+                one: the chunk pair does the same tokens in a fraction of the time);
   decode_step   one recurrent decode step at B=256, H=16, K=V=128 with the fp32 state updated in place
                 (HBM GB/s against 8 TB/s);
   short_conv    the causal depthwise conv (kernel 4) + SiLU in front of the op at the layer's shape, B=8, T=4096,
@@ -205,7 +208,8 @@ def main() -> int:
                          "FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     only = set(args.only.split(","))
-    known = {"all", "train", "fwd", "long", "nsgdn", "layer", "nsgdn_layer", "decode", "conv", "norm", "ce"}
+    known = {"all", "train", "fwd", "long", "nsgdn", "layer", "nsgdn_layer", "token_scan", "decode", "conv", "norm",
+             "ce"}
     if not only <= known:
         ap.error(f"--only: unknown workload(s) {sorted(only - known)}; choose from {sorted(known)}")
     want = lambda w: "all" in only or w in only
@@ -409,6 +413,31 @@ def main() -> int:
                 f"ms per step {out[key]['stages_ms']}")
             del m, xin, gy
             torch.cuda.empty_cache()
+
+    if want("token_scan"):
+        B, T, H, K, V = 16, 1024, 4, 128, 256
+        log(f"exact fp32 token scan B={B} T={T} H={H} K={K} V={V}")
+        gen = torch.Generator(device=dev).manual_seed(0)
+        qt = torch.nn.functional.normalize(torch.randn(B, T, H, K, device=dev, generator=gen), dim=-1) * K ** -0.5
+        kt = torch.nn.functional.normalize(torch.randn(B, T, H, K, device=dev, generator=gen), dim=-1)
+        ut, vt = kt * 0.5, torch.randn(B, T, H, V, device=dev, generator=gen)
+        lat = -torch.nn.functional.softplus(torch.randn(B, T, H, device=dev, generator=gen))
+        dyt = torch.randn(B, T, H, V, device=dev, generator=gen)
+        y_, r_, st_ = ops.nsgdn_token_fwd(qt, kt, ut, vt, lat)
+        ops.nsgdn_token_bwd(qt, kt, ut, lat, r_, st_, dyt)
+        torch.cuda.synchronize()
+        with _lib.StageTimer() as st:
+            for _ in range(2):
+                y_, r_, st_ = ops.nsgdn_token_fwd(qt, kt, ut, vt, lat)
+                ops.nsgdn_token_bwd(qt, kt, ut, lat, r_, st_, dyt)
+        f_ms = st.result["token_scan_fwd"][0] / 2
+        b_ms = st.result["token_scan_bwd"][0] / 2
+        out["token_scan"] = {"workload": "nsgdn exact fp32 token scan (scan_impl triton/ref)", "B": B, "T": T, "H": H,
+                             "K": K, "V": V, "fwd_ms": round(f_ms, 3), "bwd_ms": round(b_ms, 3),
+                             "tokens_per_s": round(B * T / ((f_ms + b_ms) * 1e-3), 1)}
+        log(f"token scan fwd {f_ms:.3f} ms, bwd {b_ms:.3f} ms")
+        del qt, kt, ut, vt, lat, dyt, y_, r_, st_
+        torch.cuda.empty_cache()
 
     if want("decode"):
         B, H, K, V = 256, 16, 128, 128
