@@ -99,3 +99,33 @@ def test_nsgdn_layer_exact_scan_matches_in_fp32(impl, DK):
     assert errs["y"] <= 1e-5 and errs["dx"] <= 1e-5, errs
     for n, _ in m.named_parameters():
         assert errs[n] <= 1e-4, (n, errs[n])
+
+
+@pytest.mark.parametrize("impl", ["chunk", "triton"])
+def test_nsgdn_layer_under_torch_compile(impl):
+    """The n-step mixer compiled as the reference trainer compiles the model (torch.compile(dynamic=False), bf16
+    autocast): forward and backward match eager through the custom ops' fake implementations (write direction,
+    input stage, gates, the chunk op or the exact token scan, gated RMSNorm)."""
+    banner(f"nsgdn layer under torch.compile(dynamic=False), scan_impl={impl}")
+    torch.manual_seed(6)
+    m = layers.build_mixer("nsgdn", 192, 0, 2, num_heads=2, head_dim=64, expand_v=2.0, n_steps=2, lam=1.0,
+                           scan_impl=impl).cuda()
+    for p in m.parameters():
+        if p.dim() == 2:
+            torch.nn.init.normal_(p, std=0.05)
+    x = torch.randn(2, 96, 192, device="cuda", generator=torch.Generator("cuda").manual_seed(7))
+
+    def run(fn):
+        for p in m.parameters():
+            p.grad = None
+        xi = x.clone().requires_grad_()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = fn(xi)
+        y.float().square().sum().backward()
+        return y.float(), xi.grad, {n: p.grad.clone() for n, p in m.named_parameters()}
+
+    y0, gx0, gp0 = run(m)
+    y1, gx1, gp1 = run(torch.compile(m, dynamic=False))
+    assert rel_l2(y1, y0) <= 1e-2 and rel_l2(gx1, gx0) <= 1e-2
+    for n in gp0:
+        assert rel_l2(gp1[n], gp0[n]) <= 2e-2, n
