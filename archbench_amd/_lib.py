@@ -57,9 +57,9 @@ SIGNATURES = {
     "gdn_write_direction_fwd": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "gdn_write_direction_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "gdn_token_scan_sizes": (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(_i)]),
-    "gdn_token_scan_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _p]),
-    "gdn_token_scan_bwd": (_i, [_p, _p, _p, _p, _p, _p, _sz, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i,
-                                _p]),
+    "gdn_token_scan_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _i, _i, _i, _i, _i, _p]),
+    "gdn_token_scan_bwd": (_i, [_p, _p, _p, _p, _p, _p, _sz, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i,
+                                _i, _i, _p]),
     "gdn_profile_enable": (_i, [_i]),
     "gdn_profile_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i), _i]),
     "gdn_profile_stage_name": (ctypes.c_char_p, [_i]),

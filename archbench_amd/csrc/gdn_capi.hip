@@ -833,16 +833,18 @@ int gdn_token_scan_sizes(int B, int T, int H, int K, int V, size_t* st_bytes, si
   return GDN_OK;
 }
 
-int gdn_token_scan_fwd(const float* q, const float* k, const float* u, const float* v, const float* la, float* y,
-                       float* r, float* st, size_t st_bytes, int B, int T, int H, int K, int V, void* stream) {
+int gdn_token_scan_fwd(const float* q, const float* k, const float* u, const float* v, const float* la,
+                       const float* h0, float* y, float* r, float* st, size_t st_bytes, float* hT, int B, int T, int H,
+                       int K, int V, void* stream) {
   size_t need_st = 0, need_sc = 0;
   int nb = 0;
   if (int e = gdn_token_scan_sizes(B, T, H, K, V, &need_st, &need_sc, &nb)) return e;
   if ((int64_t)B * T == 0) return GDN_OK;
   if (!q || !k || !u || !v || !la || !y || !r || !st) return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(h0, hT)) return fail(GDN_ERR_ARG, "state pointer not 16-byte aligned");
   if (st_bytes < need_st) return fail(GDN_ERR_WORKSPACE, "checkpoint buffer %zu bytes, need %zu", st_bytes, need_st);
   TokenScanArgs a{};
-  a.q = q; a.k = k; a.u = u; a.v = v; a.la = la; a.y = y; a.r = r; a.st = st;
+  a.q = q; a.k = k; a.u = u; a.v = v; a.la = la; a.h0 = h0; a.y = y; a.r = r; a.st = st; a.hT = hT;
   a.B = B; a.T = T; a.H = H; a.K = K; a.V = V;
   a.stream = static_cast<hipStream_t>(stream);
   const hipError_t e = timed(ST_TSCAN_FWD, a.stream, [&] { return launch_token_scan(a, false); });
@@ -851,20 +853,21 @@ int gdn_token_scan_fwd(const float* q, const float* k, const float* u, const flo
 }
 
 int gdn_token_scan_bwd(const float* q, const float* k, const float* u, const float* la, const float* r,
-                       const float* st, size_t st_bytes, const float* dy, float* dv, float* dq_part, float* du_part,
-                       float* dk_part, float* dla_part, float* scratch, size_t scratch_bytes, int B, int T, int H,
-                       int K, int V, void* stream) {
+                       const float* st, size_t st_bytes, const float* dy, const float* dhT, float* dv, float* dq_part,
+                       float* du_part, float* dk_part, float* dla_part, float* dh0, float* scratch,
+                       size_t scratch_bytes, int B, int T, int H, int K, int V, void* stream) {
   size_t need_st = 0, need_sc = 0;
   int nb = 0;
   if (int e = gdn_token_scan_sizes(B, T, H, K, V, &need_st, &need_sc, &nb)) return e;
   if ((int64_t)B * T == 0) return GDN_OK;
   if (!q || !k || !u || !la || !r || !st || !dy || !dv || !dq_part || !du_part || !dk_part || !dla_part || !scratch)
     return fail(GDN_ERR_ARG, "null input/output pointer");
+  if (misaligned(dhT, dh0)) return fail(GDN_ERR_ARG, "state pointer not 16-byte aligned");
   if (st_bytes < need_st) return fail(GDN_ERR_WORKSPACE, "checkpoint buffer %zu bytes, need %zu", st_bytes, need_st);
   if (scratch_bytes < need_sc)
     return fail(GDN_ERR_WORKSPACE, "scratch %zu bytes, need %zu", scratch_bytes, need_sc);
   TokenScanArgs a{};
-  a.q = q; a.k = k; a.u = u; a.la = la; a.dy = dy; a.dv = dv;
+  a.q = q; a.k = k; a.u = u; a.la = la; a.dy = dy; a.dhT = dhT; a.dv = dv; a.dh0 = dh0;
   a.r = const_cast<float*>(r);  // read only here (the forward writes them)
   a.st = const_cast<float*>(st);
   a.dq_part = dq_part; a.du_part = du_part; a.dk_part = dk_part; a.dla_part = dla_part; a.scratch = scratch;

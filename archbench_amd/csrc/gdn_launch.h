@@ -197,9 +197,10 @@ hipError_t launch_write_dir(const WriteDirArgs& a, bool backward);
 // Exact fp32 token scan of the n-step family (gdn_tokenscan.hip)
 struct TokenScanArgs {
   const float *q, *k, *u, *v, *la;  // [B, T, H, K] x3, [B, T, H, V], [B, T, H]
-  float *y, *r, *st;                // forward: y, r [B, T, H, V]; st [B H][ceil(T / ct)][K][V] checkpoints
-  const float* dy;                  // backward
-  float *dv, *dq_part, *du_part, *dk_part, *dla_part, *scratch;  // partials [NB][B T H][K] ([NB][B T H] for dla)
+  const float* h0;                  // [B, H, K, V] or NULL (zero)
+  float *y, *r, *st, *hT;           // forward: y, r [B, T, H, V]; st [B H][ceil(T / ct)][K][V]; hT or NULL
+  const float *dy, *dhT;            // backward (dhT NULL: zero)
+  float *dv, *dq_part, *du_part, *dk_part, *dla_part, *dh0, *scratch;  // partials [NB][B T H][K] ([NB][B T H])
   int B, T, H, K, V;
   hipStream_t stream;
 };

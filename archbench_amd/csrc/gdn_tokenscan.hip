@@ -1,6 +1,6 @@
 // Exact fp32 token scan of the n-step gated DeltaNet, forward and reverse-time backward: the reference's
 // "triton" / "ref" scan (archbench/layers/nsgdn.py:80-154, ops :162-216; the recurrence of nsgdn_ref, :408-417).
-// Per token t of a (b, h) sequence, with the state S [V, K] fp32 from zero:
+// Per token t of a (b, h) sequence, with the state S [V, K] fp32 from zero (or from an initial state):
 //     S <- e^{la_t} S;   r_t = v_t - S k_t;   S <- S + r_t u_t^T;   y_t = S q_t.
 // Rows of S are independent given the token stream, so each lane of a wave owns one row (its K entries in
 // registers) and the wave walks the tokens; k, u, q and la of a token are wave-uniform (staged through LDS).  Every CT
@@ -103,8 +103,9 @@ struct TokVecs {
 template <int K>
 __global__ __launch_bounds__(64) void token_scan_fwd_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                             const float* __restrict__ u, const float* __restrict__ v,
-                                                            const float* __restrict__ la, float* __restrict__ y,
-                                                            float* __restrict__ r, float* __restrict__ st, int T_,
+                                                            const float* __restrict__ la, const float* __restrict__ h0,
+                                                            float* __restrict__ y, float* __restrict__ r,
+                                                            float* __restrict__ st, float* __restrict__ hT, int T_,
                                                             int H, int V, int NCH, int NB) {
   __shared__ __attribute__((aligned(16))) float sv[3][K];  // the token's k, u, q
   const int pid = blockIdx.x, bh = pid / NB, vb = pid - bh * NB;
@@ -112,9 +113,11 @@ __global__ __launch_bounds__(64) void token_scan_fwd_kernel(const float* __restr
   const int l = lane_id(), vi = vb * 64 + l;
   const bool on = vi < V;
   const int vc = on ? vi : V - 1;  // lanes past V compute on row V-1 and store nothing
+  // states [B, H, K, V] (fla's layout): row vi of S is column vi of the head's [K, V] block
+  const int64_t hbase = (int64_t)bh * K * V + vi;
   float S[K];
 #pragma unroll
-  for (int j = 0; j < K; ++j) S[j] = 0.f;
+  for (int j = 0; j < K; ++j) S[j] = h0 && on ? h0[hbase + (int64_t)j * V] : 0.f;
   float* stb = st + (int64_t)bh * NCH * K * V;
   const int64_t tok_first = (int64_t)b * T_ * H + h;
   TokVecs<K> nx;
@@ -156,15 +159,20 @@ __global__ __launch_bounds__(64) void token_scan_fwd_kernel(const float* __restr
       __syncthreads();  // every lane done reading this token's vectors before the next are staged
     }
   }
+  if (hT && on) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) hT[hbase + (int64_t)j * V] = S[j];
+  }
 }
 
 // Partials: gqp, gup, gkp [NB][B*T*H][K], glap [NB][B*T*H]; sc [B*H*NB][TS_CT][K][64] scratch.
 template <int K>
 __global__ __launch_bounds__(64) void token_scan_bwd_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ u, const float* __restrict__ la,
-    const float* __restrict__ r, const float* __restrict__ st, const float* __restrict__ gy, float* __restrict__ gv,
-    float* __restrict__ gqp, float* __restrict__ gup, float* __restrict__ gkp, float* __restrict__ glap,
-    float* __restrict__ sc, int T_, int H, int V, int NCH, int NB, int64_t ntok) {
+    const float* __restrict__ r, const float* __restrict__ st, const float* __restrict__ gy,
+    const float* __restrict__ dhT, float* __restrict__ gv, float* __restrict__ gqp, float* __restrict__ gup,
+    float* __restrict__ gkp, float* __restrict__ glap, float* __restrict__ dh0, float* __restrict__ sc, int T_, int H,
+    int V, int NCH, int NB, int64_t ntok) {
   __shared__ float sG[K * 64];  // G, column-major by lane, while the recompute phase holds S
   __shared__ __attribute__((aligned(16))) float sv[3][K];  // the token's k, u, q
   const int pid = blockIdx.x, bh = pid / NB, vb = pid - bh * NB;
@@ -185,8 +193,9 @@ __global__ __launch_bounds__(64) void token_scan_bwd_kernel(
     nr = on ? r[t * V + vi] : 0.f;
     ngy = on ? gy[t * V + vi] : 0.f;
   };
+  const int64_t hbase = (int64_t)bh * K * V + vi;  // [B, H, K, V] states, as in the forward
 #pragma unroll
-  for (int j = 0; j < K; ++j) sG[j * 64 + l] = 0.f;
+  for (int j = 0; j < K; ++j) sG[j * 64 + l] = dhT && on ? dhT[hbase + (int64_t)j * V] : 0.f;
   for (int c = NCH - 1; c >= 0; --c) {
     const int n = min(TS_CT, T_ - c * TS_CT);
     const int64_t tok0 = ((int64_t)b * T_ + (int64_t)c * TS_CT) * H + h;
@@ -245,6 +254,11 @@ __global__ __launch_bounds__(64) void token_scan_bwd_kernel(
 #pragma unroll
     for (int j = 0; j < K; ++j) sG[j * 64 + l] = G[j];
   }
+  // G is now the gradient of the state before the first token: the initial state's
+  if (dh0 && on) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) dh0[hbase + (int64_t)j * V] = sG[j * 64 + l];
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -256,12 +270,12 @@ static hipError_t token_scan_k(const TokenScanArgs& a, bool backward) {
   const int NB = (a.V + 63) / 64, NCH = (a.T + TS_CT - 1) / TS_CT;
   const dim3 grid((unsigned)(a.B * a.H * NB));
   if (!backward) {
-    token_scan_fwd_kernel<K><<<grid, 64, 0, a.stream>>>(a.q, a.k, a.u, a.v, a.la, a.y, a.r, a.st, a.T, a.H, a.V,
-                                                        NCH, NB);
+    token_scan_fwd_kernel<K><<<grid, 64, 0, a.stream>>>(a.q, a.k, a.u, a.v, a.la, a.h0, a.y, a.r, a.st, a.hT, a.T,
+                                                        a.H, a.V, NCH, NB);
   } else {
-    token_scan_bwd_kernel<K><<<grid, 64, 0, a.stream>>>(a.q, a.k, a.u, a.la, a.r, a.st, a.dy, a.dv, a.dq_part,
-                                                        a.du_part, a.dk_part, a.dla_part, a.scratch, a.T, a.H, a.V,
-                                                        NCH, NB, (int64_t)a.B * a.T * a.H);
+    token_scan_bwd_kernel<K><<<grid, 64, 0, a.stream>>>(a.q, a.k, a.u, a.la, a.r, a.st, a.dy, a.dhT, a.dv,
+                                                        a.dq_part, a.du_part, a.dk_part, a.dla_part, a.dh0, a.scratch,
+                                                        a.T, a.H, a.V, NCH, NB, (int64_t)a.B * a.T * a.H);
   }
   return hipGetLastError();
 }

@@ -34,6 +34,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import warnings
 from typing import Optional
 
 import torch
@@ -480,39 +481,60 @@ def _token_sizes(lib, B, T, H, K, V):
     return st.value, sc.value, nb.value
 
 
+def _state_arg(t: Optional[Tensor], B: int, H: int, K: int, V: int, what: str) -> Optional[Tensor]:
+    if t is None:
+        return None
+    if tuple(t.shape) != (B, H, K, V):
+        raise ValueError(f"{what} must be [B, H, K, V] = {(B, H, K, V)}, got {tuple(t.shape)}")
+    return _arg(t, torch.float32)
+
+
 @torch.library.custom_op("archbench_amd::nsgdn_token_fwd", mutates_args=())
-def nsgdn_token_fwd(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor) -> tuple[Tensor, Tensor, Tensor]:
-    """(y, r, st), fp32: the scan's output, its residuals r = v - (e^la S) k and the state checkpoints."""
-    _require_gpu(q, k, u, v, la)
+def nsgdn_token_fwd(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor, h0: Optional[Tensor],
+                    output_final_state: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(y, r, st, hT), fp32: the scan's output, its residuals r = v - (e^la S) k, the state checkpoints and the
+    final state [B, H, K, V] (empty unless output_final_state).  h0: an initial state [B, H, K, V] or None."""
+    _require_gpu(q, k, u, v, la, h0)
     B, T, H, K, V = _token_shapes(q, k, u, v, la)
     lib = _lib.load()
     q, k, u, v, la = (_arg(t, torch.float32) for t in (q, k, u, v, la))
+    h0 = _state_arg(h0, B, H, K, V, "h0")
     st_bytes, _, _ = _token_sizes(lib, B, T, H, K, V)
     y, r = torch.empty_like(v), torch.empty_like(v)
     st = torch.empty(st_bytes // 4, dtype=torch.float32, device=q.device)
-    rc = lib.gdn_token_scan_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(u), _lib.ptr(v), _lib.ptr(la), _lib.ptr(y),
-                                _lib.ptr(r), _lib.ptr(st), st_bytes, B, T, H, K, V, _lib.stream_ptr(q.device))
+    hT = torch.empty((B, H, K, V) if output_final_state else (0,), dtype=torch.float32, device=q.device)
+    if B * T == 0:  # no token: the final state is the initial one
+        if output_final_state:
+            hT.copy_(h0) if h0 is not None else hT.zero_()
+        return y, r, st, hT
+    rc = lib.gdn_token_scan_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(u), _lib.ptr(v), _lib.ptr(la), _lib.ptr(h0),
+                                _lib.ptr(y), _lib.ptr(r), _lib.ptr(st), st_bytes,
+                                _lib.ptr(hT) if output_final_state else None, B, T, H, K, V,
+                                _lib.stream_ptr(q.device))
     _lib.check(rc, "gdn_token_scan_fwd")
-    return y, r, st
+    return y, r, st, hT
 
 
 @nsgdn_token_fwd.register_fake
-def _(q, k, u, v, la):
+def _(q, k, u, v, la, h0, output_final_state):
     B, T, H, K = q.shape
     V = v.shape[-1]
     nch = -(-T // TOKEN_SCAN_CT)
     f32 = dict(dtype=torch.float32)
-    return v.new_empty(v.shape, **f32), v.new_empty(v.shape, **f32), v.new_empty(B * H * nch * K * V, **f32)
+    return (v.new_empty(v.shape, **f32), v.new_empty(v.shape, **f32), v.new_empty(B * H * nch * K * V, **f32),
+            v.new_empty((B, H, K, V) if output_final_state else (0,), **f32))
 
 
 @torch.library.custom_op("archbench_amd::nsgdn_token_bwd", mutates_args=())
-def nsgdn_token_bwd(q: Tensor, k: Tensor, u: Tensor, la: Tensor, r: Tensor, st: Tensor,
-                    dy: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """(dq, dk, du, dv, dla), fp32."""
-    _require_gpu(q, k, u, la, r, st, dy)
+def nsgdn_token_bwd(q: Tensor, k: Tensor, u: Tensor, la: Tensor, r: Tensor, st: Tensor, dy: Tensor,
+                    dhT: Optional[Tensor], need_dh0: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(dq, dk, du, dv, dla, dh0), fp32; dh0 [B, H, K, V] when need_dh0, else empty.  dhT: the final state's
+    gradient or None."""
+    _require_gpu(q, k, u, la, r, st, dy, dhT)
     B, T, H, K, V = _token_shapes(q, k, u, r, la)
     lib = _lib.load()
     q, k, u, la, r, dy = (_arg(t, torch.float32) for t in (q, k, u, la, r, dy))
+    dhT = _state_arg(dhT, B, H, K, V, "dhT")
     st_bytes, sc_bytes, nb = _token_sizes(lib, B, T, H, K, V)
     if st.numel() * 4 < st_bytes:
         raise ValueError("st is not this shape's checkpoint buffer")
@@ -520,38 +542,53 @@ def nsgdn_token_bwd(q: Tensor, k: Tensor, u: Tensor, la: Tensor, r: Tensor, st: 
     parts = [torch.empty(nb, B, T, H, K, dtype=torch.float32, device=dev) for _ in range(3)]
     dla_p = torch.empty(nb, B, T, H, dtype=torch.float32, device=dev)
     dv = torch.empty_like(r)
+    dh0 = torch.empty((B, H, K, V) if need_dh0 else (0,), dtype=torch.float32, device=dev)
+    if B * T == 0:  # no token: the initial state's gradient is the final state's
+        if need_dh0:
+            dh0.copy_(dhT) if dhT is not None else dh0.zero_()
+        z = torch.zeros(B, T, H, K, dtype=torch.float32, device=dev)
+        return z, z.clone(), z.clone(), dv, torch.zeros(B, T, H, dtype=torch.float32, device=dev), dh0
     sc = torch.empty(max(sc_bytes // 4, 1), dtype=torch.float32, device=dev)
     rc = lib.gdn_token_scan_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(u), _lib.ptr(la), _lib.ptr(r), _lib.ptr(st),
-                                st.numel() * 4, _lib.ptr(dy), _lib.ptr(dv), _lib.ptr(parts[0]), _lib.ptr(parts[1]),
-                                _lib.ptr(parts[2]), _lib.ptr(dla_p), _lib.ptr(sc), sc.numel() * 4, B, T, H, K, V,
+                                st.numel() * 4, _lib.ptr(dy), _lib.ptr(dhT), _lib.ptr(dv), _lib.ptr(parts[0]),
+                                _lib.ptr(parts[1]), _lib.ptr(parts[2]), _lib.ptr(dla_p),
+                                _lib.ptr(dh0) if need_dh0 else None, _lib.ptr(sc), sc.numel() * 4, B, T, H, K, V,
                                 _lib.stream_ptr(dev))
     _lib.check(rc, "gdn_token_scan_bwd")
     dq, du, dk = (p[0] if nb == 1 else p.sum(0) for p in parts)
-    return dq, dk, du, dv, (dla_p[0] if nb == 1 else dla_p.sum(0))
+    return dq, dk, du, dv, (dla_p[0] if nb == 1 else dla_p.sum(0)), dh0
 
 
 @nsgdn_token_bwd.register_fake
-def _(q, k, u, la, r, st, dy):
+def _(q, k, u, la, r, st, dy, dhT, need_dh0):
+    B, T, H, K = q.shape
+    V = r.shape[-1]
     f32 = dict(dtype=torch.float32)
     return (q.new_empty(q.shape, **f32), q.new_empty(q.shape, **f32), q.new_empty(q.shape, **f32),
-            r.new_empty(r.shape, **f32), la.new_empty(la.shape, **f32))
+            r.new_empty(r.shape, **f32), la.new_empty(la.shape, **f32),
+            q.new_empty((B, H, K, V) if need_dh0 else (0,), **f32))
 
 
 def _token_setup(ctx, inputs, output):
-    q, k, u, v, la = inputs
-    _, r, st = output
+    q, k, u, v, la, h0, output_final_state = inputs
+    _, r, st, _ = output
     ctx.save_for_backward(q, k, u, la, r, st)
-    ctx.dtypes = tuple(t.dtype for t in inputs)
+    ctx.dtypes = tuple(t.dtype for t in (q, k, u, v, la))
+    ctx.h0_dtype = None if h0 is None else h0.dtype
     ctx.set_materialize_grads(False)  # r and st take no gradient: no zero-filled buffers for them
 
 
-def _token_backward(ctx, dy, dr, dst):
+def _token_backward(ctx, dy, dr, dst, dhT):
     q, k, u, la, r, st = ctx.saved_tensors
+    if dy is None and dhT is None:
+        return None, None, None, None, None, None, None
     if dy is None:
-        return None, None, None, None, None
-    grads = nsgdn_token_bwd(q, k, u, la, r, st, dy.contiguous())
-    dq, dk, du, dv, dla = grads
-    return tuple(g.to(dt) for g, dt in zip((dq, dk, du, dv, dla), ctx.dtypes))
+        dy = torch.zeros_like(r)
+    need_dh0 = ctx.h0_dtype is not None
+    dq, dk, du, dv, dla, dh0 = nsgdn_token_bwd(q, k, u, la, r, st, dy.contiguous(),
+                                               None if dhT is None else dhT.contiguous(), need_dh0)
+    grads = tuple(g.to(dt) for g, dt in zip((dq, dk, du, dv, dla), ctx.dtypes))
+    return (*grads, dh0.to(ctx.h0_dtype) if need_dh0 else None, None)
 
 
 nsgdn_token_fwd.register_autograd(_token_backward, setup_context=_token_setup)
@@ -561,7 +598,7 @@ def nsgdn_scan(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor) -> Tensor
     """archbench's nsgdn_scan (nsgdn.py:219-221): y [B, T, H, V] fp32 from the exact fp32 token scan, for q, k, u
     [B, T, H, K] (q already scaled), v [B, T, H, V] and log-retention la [B, T, H].  Differentiable w.r.t. every
     input; K in {64, 128}."""
-    return nsgdn_token_fwd(q.float(), k.float(), u.float(), v.float(), la.float())[0]
+    return nsgdn_token_fwd(q.float(), k.float(), u.float(), v.float(), la.float(), None, False)[0]
 
 
 def nsgdn_scan_chunk(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor, scale: float = 1.0,
@@ -1059,11 +1096,39 @@ def chunk_gated_delta_rule(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Ten
         q, k = _l2norm(q), _l2norm(k)
     if scale is None:
         scale = q.shape[-1] ** -0.5
+    if _fp32_token_route(q, v):
+        return _gdn_token_scan(q, k, v, g, beta, float(scale), initial_state, output_final_state)
     if _use_stash(q, k, v, g, beta, initial_state):
         o, hT, _ = chunk_fwd_stash(q, k, v, g, beta, initial_state, float(scale))
     else:
         o, hT = chunk_fwd(q, k, v, g, beta, initial_state, float(scale))
     return o, (hT if output_final_state else None)
+
+
+_TOKEN_ROUTE_WARNED = [False]
+
+
+def _fp32_token_route(q: Tensor, v: Tensor) -> bool:
+    """fp32 inputs at a head size the fp32 chunk kernels are not compiled for, which the exact token scan covers."""
+    if q.dtype != torch.float32 or not q.is_cuda or q.dim() != 4 or v.dim() != 4:
+        return False
+    K, V = q.shape[-1], v.shape[-1]
+    return not _lib.supported("chunk", K, V, torch.float32) and K in (64, 128)
+
+
+def _gdn_token_scan(q, k, v, g, beta, scale, initial_state, output_final_state):
+    """The gated delta rule in fp32 where no fp32 chunk kernel is compiled: the exact token scan with write vector
+    u = beta k and log-decay g (S <- e^g S + beta (v - e^g S k) k^T is the scan's recurrence at that u); exact to
+    fp32 rounding and much slower than the bf16 chunk kernels, which the trainer's bf16 autocast selects."""
+    if not _TOKEN_ROUTE_WARNED[0]:
+        _TOKEN_ROUTE_WARNED[0] = True
+        warnings.warn(f"chunk_gated_delta_rule: fp32 q/k/v at K={q.shape[-1]}, V={v.shape[-1]} run the exact fp32 "
+                      "token scan (no fp32 chunk kernels at this size); bf16 inputs (e.g. under "
+                      "torch.autocast(dtype=torch.bfloat16)) run the chunk kernels, many times faster",
+                      UserWarning, stacklevel=3)
+    u = beta.float()[..., None] * k
+    y, _, _, hT = nsgdn_token_fwd(q * scale, k, u, v, g.float(), initial_state, bool(output_final_state))
+    return y, (hT if output_final_state else None)
 
 
 def recurrent_step(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, state: Tensor,

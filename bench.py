@@ -423,13 +423,13 @@ def main() -> int:
         ut, vt = kt * 0.5, torch.randn(B, T, H, V, device=dev, generator=gen)
         lat = -torch.nn.functional.softplus(torch.randn(B, T, H, device=dev, generator=gen))
         dyt = torch.randn(B, T, H, V, device=dev, generator=gen)
-        y_, r_, st_ = ops.nsgdn_token_fwd(qt, kt, ut, vt, lat)
-        ops.nsgdn_token_bwd(qt, kt, ut, lat, r_, st_, dyt)
+        y_, r_, st_, _ = ops.nsgdn_token_fwd(qt, kt, ut, vt, lat, None, False)
+        ops.nsgdn_token_bwd(qt, kt, ut, lat, r_, st_, dyt, None, False)
         torch.cuda.synchronize()
         with _lib.StageTimer() as st:
             for _ in range(2):
-                y_, r_, st_ = ops.nsgdn_token_fwd(qt, kt, ut, vt, lat)
-                ops.nsgdn_token_bwd(qt, kt, ut, lat, r_, st_, dyt)
+                y_, r_, st_, _ = ops.nsgdn_token_fwd(qt, kt, ut, vt, lat, None, False)
+                ops.nsgdn_token_bwd(qt, kt, ut, lat, r_, st_, dyt, None, False)
         f_ms = st.result["token_scan_fwd"][0] / 2
         b_ms = st.result["token_scan_bwd"][0] / 2
         out["token_scan"] = {"workload": "nsgdn exact fp32 token scan (scan_impl triton/ref)", "B": B, "T": T, "H": H,

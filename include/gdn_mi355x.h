@@ -222,15 +222,19 @@ int gdn_write_direction_bwd(const void* k, const float* beta, const float* lam, 
  * The forward writes y, the residuals r and the state every ct tokens into st (the backward's checkpoints); the
  * backward writes dv directly and dq, du, dk, dla as n_partials row blocks each ([n_partials][B*T*H][K],
  * [n_partials][B*T*H]) that the caller sums over the first index (the reference adds them with atomics).  Sizes
- * of st, of the backward's scratch and n_partials from gdn_token_scan_sizes.  K in {64, 128}, any V. */
+ * of st, of the backward's scratch and n_partials from gdn_token_scan_sizes.  K in {64, 128}, any V.
+ * Optional states, an extension of the reference's zero-initialised scan (NULL: none), in fla's [B, H, K, V] fp32
+ * layout: h0 (initial) and hT (final) in the forward, dhT and dh0 in the backward; B * T == 0 returns at once
+ * without touching them. */
 int gdn_token_scan_sizes(int B, int T, int H, int K, int V, size_t* st_bytes, size_t* scratch_bytes,
                          int* n_partials);
-int gdn_token_scan_fwd(const float* q, const float* k, const float* u, const float* v, const float* la, float* y,
-                       float* r, float* st, size_t st_bytes, int B, int T, int H, int K, int V, void* stream);
-int gdn_token_scan_bwd(const float* q, const float* k, const float* u, const float* la, const float* r,
-                       const float* st, size_t st_bytes, const float* dy, float* dv, float* dq_part, float* du_part,
-                       float* dk_part, float* dla_part, float* scratch, size_t scratch_bytes, int B, int T, int H,
+int gdn_token_scan_fwd(const float* q, const float* k, const float* u, const float* v, const float* la,
+                       const float* h0, float* y, float* r, float* st, size_t st_bytes, float* hT, int B, int T, int H,
                        int K, int V, void* stream);
+int gdn_token_scan_bwd(const float* q, const float* k, const float* u, const float* la, const float* r,
+                       const float* st, size_t st_bytes, const float* dy, const float* dhT, float* dv, float* dq_part,
+                       float* du_part, float* dk_part, float* dla_part, float* dh0, float* scratch,
+                       size_t scratch_bytes, int B, int T, int H, int K, int V, void* stream);
 
 /* Per-stage kernel timing (diagnostic; no counterpart in the reference, which times whole phases with CUDA
  * events in archbench/logger.py:57-81).  While enabled (process-wide: launches from any host thread count), every

@@ -99,12 +99,34 @@ def test_reference_config_under_autocast(monkeypatch):
         assert errs[n] <= 2e-2, (n, errs[n])
 
 
-def test_fp32_layer_at_k128_raises_with_bf16_hint():
-    """Without autocast the projections are fp32; the fp32 kernels exist for K = 64 only, so the reference
-    config's K = 128 is refused with a message naming the bf16 route (no silent precision change)."""
+def test_fp32_layer_at_k128_runs_the_exact_scan(monkeypatch):
+    """Without autocast the projections are fp32; the fp32 chunk kernels exist for K = 64 only, so at the reference
+    config's K = 128 the op runs the exact fp32 token scan (saying so once, with the bf16 route named) and the
+    layer matches its oracle-backed copy to fp32 accuracy."""
+    banner("fp32 layer at K = 128 through the exact token scan")
+    monkeypatch.setattr(ops, "_TOKEN_ROUTE_WARNED", [False])
+    torch.manual_seed(9)
     m = layers.build_mixer("gdn", 256, 0, 2, num_heads=2, **GDN_YAML).cuda()
-    with pytest.raises(ValueError, match="bf16"):
-        m(torch.randn(1, 64, 256, device="cuda"))
+    for p in m.parameters():
+        if p.dim() == 2:
+            torch.nn.init.normal_(p, std=0.05)
+    x = torch.randn(2, 80, 256, device="cuda", generator=torch.Generator("cuda").manual_seed(10))
+    x1 = x.clone().requires_grad_()
+    with pytest.warns(UserWarning, match="bf16"):
+        y1 = m(x1)
+    assert y1.dtype == torch.float32
+    y1.square().sum().backward()
+    g1 = {n: p.grad.clone() for n, p in m.named_parameters()}
+    m.zero_grad()
+    monkeypatch.setattr("archbench_amd.layers.gdn.ops.chunk_gated_delta_rule", _oracle_op)
+    x2 = x.clone().requires_grad_()
+    y2 = m(x2)
+    y2.square().sum().backward()
+    errs = {"y": rel_l2(y1, y2), "dx": rel_l2(x1.grad, x2.grad)}
+    errs.update({n: rel_l2(g1[n], p.grad) for n, p in m.named_parameters()})
+    print("rel-L2 vs oracle-backed layer:", {n: f"{e:.1e}" for n, e in errs.items()}, flush=True)
+    for n, e in errs.items():
+        assert e <= 1e-5, (n, e)
 
 
 def test_prefill_then_decode_matches_full_sequence():
@@ -156,8 +178,10 @@ def test_opcheck():
     torch.library.opcheck(torch.ops.archbench_amd.write_direction.default, (k, beta, lam, 2), test_utils=utils)
     la = (-torch.rand(1, 70, 2, device="cuda")).requires_grad_()
     qs = [torch.randn(1, 70, 2, 64, device="cuda").requires_grad_() for _ in range(3)]
-    torch.library.opcheck(torch.ops.archbench_amd.nsgdn_token_fwd.default, (*qs, v.detach().requires_grad_(), la),
-                          test_utils=utils)
+    h0t = (torch.randn(1, 2, 64, 64, device="cuda") * 0.1).requires_grad_()
+    for h0a, fin in ((None, False), (h0t, True)):
+        torch.library.opcheck(torch.ops.archbench_amd.nsgdn_token_fwd.default,
+                              (*qs, v.detach().requires_grad_(), la, h0a, fin), test_utils=utils)
     y = torch.randn(1, 70, 512, device="cuda", dtype=torch.bfloat16).requires_grad_()
     w = (torch.randn(512, 4, device="cuda") * 0.5).requires_grad_()
     torch.library.opcheck(torch.ops.archbench_amd.mixer_input_stage.default, (y, w, 128, 256, 64), test_utils=utils)

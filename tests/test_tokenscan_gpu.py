@@ -66,3 +66,37 @@ def test_token_scan_edges():
         ops.nsgdn_scan(z, z, z, d[3], d[4])
     with pytest.raises(ValueError, match="la"):
         ops.nsgdn_scan(d[0], d[1], d[2], d[3], d[4][:, :4])
+
+
+def test_gdn_op_fp32_k128_runs_exact_token_scan(monkeypatch):
+    """chunk_gated_delta_rule with fp32 inputs at K = 128 (no fp32 chunk kernels there) runs the token scan with
+    u = beta k: o, the final state and every gradient including dh0 (with a final-state gradient) against the gated
+    delta rule oracle (fp64), rel-L2 <= 1e-6; T = 0 returns the initial state."""
+    from oracle import gdn_oracle as O
+    banner("gdn op fp32 K=128 V=256 through the token scan, with h0 / hT")
+    monkeypatch.setattr(ops, "_TOKEN_ROUTE_WARNED", [False])
+    B, T, H, K, V = 2, 70, 2, 128, 256
+    g_ = torch.Generator().manual_seed(12)
+    q = F.normalize(torch.randn(B, T, H, K, generator=g_), dim=-1)
+    k = F.normalize(torch.randn(B, T, H, K, generator=g_), dim=-1)
+    v = torch.randn(B, T, H, V, generator=g_)
+    g = F.logsigmoid(torch.randn(B, T, H, generator=g_) + 3)
+    beta = torch.rand(B, T, H, generator=g_)
+    h0 = torch.randn(B, H, K, V, generator=g_) * 0.1
+    do = torch.randn(B, T, H, V, generator=g_)
+    dhT = torch.randn(B, H, K, V, generator=g_) * 0.1
+    leaves = [t.cuda().requires_grad_() for t in (q, k, v, g, beta, h0)]
+    with pytest.warns(UserWarning, match="token scan"):
+        o, hT = ops.chunk_gated_delta_rule(*leaves[:5], scale=0.5, initial_state=leaves[5], output_final_state=True)
+    torch.autograd.backward((o, hT), (do.cuda(), dhT.cuda()))
+    o_ref, hT_ref = O.chunk_fwd(q, k, v, g, beta, 0.5, h0)
+    grads_ref = O.chunk_bwd(q, k, v, g, beta, do, 0.5, h0, dhT)
+    errs = {"o": rel_l2(o, o_ref), "hT": rel_l2(hT, hT_ref)}
+    for n, t, gr in zip(("dq", "dk", "dv", "dg", "dbeta", "dh0"), leaves, grads_ref):
+        errs[n] = rel_l2(t.grad, gr)
+    print("[rel-L2] " + ", ".join(f"{n} {e:.1e}" for n, e in errs.items()), flush=True)
+    for n, e in errs.items():
+        assert e <= 1e-6, (n, e)
+    o0, hT0 = ops.chunk_gated_delta_rule(*(t[:, :0].detach() for t in leaves[:5]), scale=0.5,
+                                         initial_state=leaves[5].detach(), output_final_state=True)
+    assert o0.shape == (B, 0, H, V) and torch.equal(hT0, leaves[5].detach())
