@@ -22,9 +22,9 @@ namespace gdn {
 
 constexpr int TS_CT = 32;  // tokens between checkpoints
 
-// The previous 16 lanes' worth of DPP reduce-scatter: values a[0 .. 2N) -> a[0 .. N).  The lane whose bit `hi`
-// is clear keeps a[k] and sends a[k + N], its DPP partner (pattern CTRL, which pairs lanes with opposite bits)
-// the reverse; each adds the value it receives.
+// One reduce-scatter round inside a 16-lane DPP row: values a[0 .. 2N) -> a[0 .. N).  The lane whose bit `hi` is
+// clear keeps a[k] and sends a[k + N], its DPP partner (pattern CTRL, which pairs lanes with opposite bits) the
+// reverse; each adds the value it receives.
 template <int N, int CTRL>
 __device__ __forceinline__ void ts_rs_dpp(float* a, int hi) {
 #pragma unroll
@@ -33,6 +33,7 @@ __device__ __forceinline__ void ts_rs_dpp(float* a, int hi) {
     a[k] = keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), CTRL, 0xf, 0xf, false));
   }
 }
+// The same round between lanes l and l ^ 16 (a lane shuffle: the pair sits in different DPP rows)
 template <int N>
 __device__ __forceinline__ void ts_rs_xor16(float* a, int hi) {
 #pragma unroll
