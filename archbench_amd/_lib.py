@@ -50,9 +50,10 @@ SIGNATURES = {
     "gdn_gated_rmsnorm_bwd": (_i, [_p, _p, _i64, _i, _p, _p, _p, _p, _p, _p, _sz, _i64, _i, _f, _i, _p]),
     "gdn_l2norm_fwd": (_i, [_p, _p, _i64, _i, _f, _f, _i, _p]),
     "gdn_l2norm_bwd": (_i, [_p, _p, _p, _i64, _i, _f, _f, _i, _p]),
-    "gdn_gates_fwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i, _f, _f, _i, _p]),
+    "gdn_gates_fwd": (_i, [_p, _p, _i64, _p, _p, _p, _p, _p, _i64, _i, _f, _f, _i, _p]),
     "gdn_gates_bwd_ws_bytes": (_i, [_i64, _i, ctypes.POINTER(_sz)]),
-    "gdn_gates_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i64, _i, _f, _f, _i, _p]),
+    "gdn_gates_bwd": (_i, [_p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _sz, _i64, _i, _f, _f,
+                           _i, _p]),
     "gdn_cross_entropy_fwd_bwd": (_i, [_p, _p, _p, _p, _p, _i64, _i, _i64, _i64, _i, _p]),
     "gdn_write_direction_fwd": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
     "gdn_write_direction_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),

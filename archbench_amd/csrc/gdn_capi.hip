@@ -886,16 +886,17 @@ static int gates_check(int64_t ntok, int H, int dtype, bool backward = false) {
   return GDN_OK;
 }
 
-int gdn_gates_fwd(const void* a, const void* b, const float* A_log, const float* dt_bias, const float* b_bias,
-                  float* g, float* beta, int64_t ntok, int H, float beta_scale, float g_min, int dtype,
-                  void* stream) {
+int gdn_gates_fwd(const void* a, const void* b, int64_t lda, const float* A_log, const float* dt_bias,
+                  const float* b_bias, float* g, float* beta, int64_t ntok, int H, float beta_scale, float g_min,
+                  int dtype, void* stream) {
   g_err[0] = 0;
   if (int e = gates_check(ntok, H, dtype)) return e;
+  if (lda != 0 && lda < H) return fail(GDN_ERR_ARG, "lda = %lld is below H = %d", (long long)lda, H);
   if (ntok == 0) return GDN_OK;
   if (!a || !b || !A_log || !g || !beta) return fail(GDN_ERR_ARG, "null input/output pointer");
   GateArgs ga{};
-  ga.a = a; ga.b = b; ga.A_log = A_log; ga.dt_bias = dt_bias; ga.b_bias = b_bias; ga.g = g; ga.beta = beta;
-  ga.ntok = ntok; ga.H = H; ga.dtype = dtype; ga.beta_scale = beta_scale; ga.g_min = g_min;
+  ga.a = a; ga.b = b; ga.lda = lda; ga.A_log = A_log; ga.dt_bias = dt_bias; ga.b_bias = b_bias; ga.g = g;
+  ga.beta = beta; ga.ntok = ntok; ga.H = H; ga.dtype = dtype; ga.beta_scale = beta_scale; ga.g_min = g_min;
   ga.stream = static_cast<hipStream_t>(stream);
   const hipError_t e = timed(ST_GATES_FWD, ga.stream, [&] { return launch_gates(ga, false); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "gates forward launch: %s", hipGetErrorString(e));
@@ -910,12 +911,14 @@ int gdn_gates_bwd_ws_bytes(int64_t ntok, int H, size_t* bytes) {
   return GDN_OK;
 }
 
-int gdn_gates_bwd(const void* a, const void* b, const float* A_log, const float* dt_bias, const float* b_bias,
-                  const float* dg, const float* dbeta, void* da, void* db, float* dA_log, float* ddt_bias,
-                  float* db_bias, void* ws, size_t ws_bytes, int64_t ntok, int H, float beta_scale, float g_min,
-                  int dtype, void* stream) {
+int gdn_gates_bwd(const void* a, const void* b, int64_t lda, const float* A_log, const float* dt_bias,
+                  const float* b_bias, const float* dg, const float* dbeta, void* da, void* db, int64_t ldd,
+                  float* dA_log, float* ddt_bias, float* db_bias, void* ws, size_t ws_bytes, int64_t ntok, int H,
+                  float beta_scale, float g_min, int dtype, void* stream) {
   g_err[0] = 0;
   if (int e = gates_check(ntok, H, dtype, true)) return e;
+  if ((lda != 0 && lda < H) || (ldd != 0 && ldd < H))
+    return fail(GDN_ERR_ARG, "lda = %lld / ldd = %lld below H = %d", (long long)lda, (long long)ldd, H);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (ntok == 0) {
     hipError_t e = copy_or_zero_bytes(nullptr, dA_log, (size_t)H * 4, st);
@@ -929,8 +932,8 @@ int gdn_gates_bwd(const void* a, const void* b, const float* A_log, const float*
   if (!ws || ws_bytes < need)
     return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
   GateArgs ga{};
-  ga.a = a; ga.b = b; ga.A_log = A_log; ga.dt_bias = dt_bias; ga.b_bias = b_bias; ga.dg = dg; ga.dbeta = dbeta;
-  ga.da = da; ga.db = db; ga.dA_log = dA_log; ga.ddt_bias = ddt_bias; ga.db_bias = db_bias; ga.ws = ws;
+  ga.a = a; ga.b = b; ga.lda = lda; ga.ldd = ldd; ga.A_log = A_log; ga.dt_bias = dt_bias; ga.b_bias = b_bias;
+  ga.dg = dg; ga.dbeta = dbeta; ga.da = da; ga.db = db; ga.dA_log = dA_log; ga.ddt_bias = ddt_bias; ga.db_bias = db_bias; ga.ws = ws;
   ga.ntok = ntok; ga.H = H; ga.dtype = dtype; ga.beta_scale = beta_scale; ga.g_min = g_min; ga.stream = st;
   const hipError_t e = timed(ST_GATES_BWD, st, [&] { return launch_gates(ga, true); });
   if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "gates backward launch: %s", hipGetErrorString(e));

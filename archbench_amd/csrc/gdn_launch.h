@@ -148,6 +148,7 @@ hipError_t launch_norm(const NormArgs& a, bool backward);
 // Gate functions over [ntok, H] (a, b, da, db in dtype; g, beta, dg, dbeta fp32).
 struct GateArgs {
   const void *a, *b;
+  int64_t lda, ldd;                       // elements between token rows of a, b / of da, db (0: H, contiguous)
   const float *A_log, *dt_bias, *b_bias;  // [H]; dt_bias, b_bias may be null (zero)
   float *g, *beta;                        // forward
   const float *dg, *dbeta;                // backward

@@ -185,13 +185,14 @@ __global__ __launch_bounds__(256) void gates_fwd_kernel(const T* __restrict__ a,
                                                         const float* __restrict__ A_log,
                                                         const float* __restrict__ dt_bias,
                                                         const float* __restrict__ b_bias, float* __restrict__ g,
-                                                        float* __restrict__ beta, int64_t n, int H, float beta_scale,
-                                                        float g_min) {
+                                                        float* __restrict__ beta, int64_t n, int H, int64_t lda,
+                                                        float beta_scale, float g_min) {
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
-    const int h = (int)(e % H);
-    const float xa = to_f(a[e]) + (dt_bias ? dt_bias[h] : 0.f);
+    const int64_t t = e / H;
+    const int h = (int)(e - t * H);
+    const float xa = to_f(a[t * lda + h]) + (dt_bias ? dt_bias[h] : 0.f);
     g[e] = fmaxf(-expf(A_log[h]) * softplus_f(xa), g_min);
-    const float xb = to_f(b[e]) + (b_bias ? b_bias[h] : 0.f);
+    const float xb = to_f(b[t * lda + h]) + (b_bias ? b_bias[h] : 0.f);
     beta[e] = beta_scale * (1.f / (1.f + expf(-xb)));
   }
 }
@@ -208,24 +209,25 @@ __global__ __launch_bounds__(256) void gates_bwd_kernel(const T* __restrict__ a,
                                                         const float* __restrict__ dg, const float* __restrict__ dbeta,
                                                         T* __restrict__ da, T* __restrict__ db,
                                                         float* __restrict__ part, int64_t ntok, int H, int TN,
-                                                        float beta_scale, float g_min) {
+                                                        int64_t lda, int64_t ldd, float beta_scale, float g_min) {
   __shared__ float sA[GATE_TILE], sX[GATE_TILE], sY[GATE_TILE];
   const int64_t tok0 = (int64_t)blockIdx.x * TN;
   const int ntile = (int)min((int64_t)TN, ntok - tok0) * H;
   const int64_t e0 = tok0 * H;
   for (int i = threadIdx.x; i < ntile; i += 256) {
     const int64_t e = e0 + i;
-    const int h = i % H;
-    const float xa = to_f(a[e]) + (dt_bias ? dt_bias[h] : 0.f);
+    const int tl = i / H, h = i - tl * H;
+    const int64_t ia = (tok0 + tl) * lda + h, id = (tok0 + tl) * ldd + h;  // a, b and da, db rows lda, ldd apart
+    const float xa = to_f(a[ia]) + (dt_bias ? dt_bias[h] : 0.f);
     const float eA = expf(A_log[h]);
     const float gu = -eA * softplus_f(xa);  // before the clamp
     const float dgu = gu >= g_min ? dg[e] : 0.f;  // clamp_min passes the gradient where the input is >= g_min
     const float dxa = dgu * -eA * (xa > 20.f ? 1.f : 1.f / (1.f + expf(-xa)));
-    const float xb = to_f(b[e]) + (b_bias ? b_bias[h] : 0.f);
+    const float xb = to_f(b[ia]) + (b_bias ? b_bias[h] : 0.f);
     const float s = 1.f / (1.f + expf(-xb));
     const float dxb = dbeta[e] * beta_scale * s * (1.f - s);
-    da[e] = from_f<T>(dxa);
-    db[e] = from_f<T>(dxb);
+    da[id] = from_f<T>(dxa);
+    db[id] = from_f<T>(dxb);
     sA[i] = dgu * gu;  // d/dA_log of -exp(A_log) softplus(.) is the value itself
     sX[i] = dxa;
     sY[i] = dxb;
@@ -312,7 +314,7 @@ static hipError_t gates_k(const GateArgs& a, bool backward) {
     const int64_t nb = std::min<int64_t>((n + 255) / 256, 8 * (int64_t)device_cu_count());
     gates_fwd_kernel<T><<<dim3((int)nb), 256, 0, a.stream>>>(static_cast<const T*>(a.a), static_cast<const T*>(a.b),
                                                               a.A_log, a.dt_bias, a.b_bias, a.g, a.beta, n, a.H,
-                                                              a.beta_scale, a.g_min);
+                                                              a.lda ? a.lda : a.H, a.beta_scale, a.g_min);
     return hipGetLastError();
   }
   const int TN = gates_tile_tokens(a.H);
@@ -320,7 +322,8 @@ static hipError_t gates_k(const GateArgs& a, bool backward) {
   float* part = static_cast<float*>(a.ws);
   gates_bwd_kernel<T><<<dim3((int)nwg), 256, 0, a.stream>>>(
       static_cast<const T*>(a.a), static_cast<const T*>(a.b), a.A_log, a.dt_bias, a.b_bias, a.dg, a.dbeta,
-      static_cast<T*>(a.da), static_cast<T*>(a.db), part, a.ntok, a.H, TN, a.beta_scale, a.g_min);
+      static_cast<T*>(a.da), static_cast<T*>(a.db), part, a.ntok, a.H, TN, a.lda ? a.lda : a.H,
+      a.ldd ? a.ldd : a.H, a.beta_scale, a.g_min);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // each partial row is [dA_log (H) | ddt_bias (H) | db_bias (H)]

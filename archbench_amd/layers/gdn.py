@@ -213,11 +213,11 @@ class GatedDeltaNet(nn.Module):
             # training / prefill without a cache: the convolutions read q, k, v straight out of the projection's
             # output and their backward writes into one gradient of it (ops.mixer_input_stage)
             y, gate, ab = self._grouped_projections(hidden_states)
-            a, b = torch.split(ab, [self.a_proj.out_features, self.b_proj.out_features], dim=-1)
             w = torch.cat([c.weight.squeeze(1) for c in convs], 0)
             q, k, v = ops.mixer_input_stage(y, w, self.key_dim, self.value_dim, DK)
             gp = [gate] if self.use_gate else []
         else:
+            ab = None
             q, k, v, a, b, *gp = self.input_projections(hidden_states)
             if convs:
                 (q, cq), (k, ck), (v, cv) = (self.q_conv1d(q, conv_in[0]), self.k_conv1d(k, conv_in[1]),
@@ -226,9 +226,13 @@ class GatedDeltaNet(nn.Module):
             else:
                 q, k, v = F.silu(q), F.silu(k), F.silu(v)
         q, k, v = q.reshape(B, T, H, DK), k.reshape(B, T, H, DK), v.reshape(B, T, H, DV)
-        # g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b) (x2 with negative eigenvalues), one HIP pass
-        g, beta = ops.gdn_gates(a, b, self.A_log, self.dt_bias, None, 2.0 if self.allow_neg_eigval else 1.0,
-                                float("-inf"))
+        # g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b) (x2 with negative eigenvalues), one HIP pass;
+        # from the [a | b] projection output in place when there is one
+        scale_b = 2.0 if self.allow_neg_eigval else 1.0
+        if ab is not None:
+            g, beta = ops.gdn_gates_ab(ab, self.A_log, self.dt_bias, None, scale_b, float("-inf"))
+        else:
+            g, beta = ops.gdn_gates(a, b, self.A_log, self.dt_bias, None, scale_b, float("-inf"))
         state = entry["recurrent_state"] if entry is not None else None
         # The op runs in the dtype the projections produced, as fla's layer passes them on: bf16 under the
         # trainer's bf16 autocast (archbench/trainer.py:66), even though the block hands the mixer fp32 hidden

@@ -109,7 +109,7 @@ class NStepGDN(nn.Module):
             qs, ks, vs = torch.split(y, [self.qk_dim, self.qk_dim, self.v_dim], dim=-1)
             q, k, v = ops.l2norm(qs, 1e-12, 1.0), ops.l2norm(ks, 1e-12, 1.0), vs
         q, k, v = q.view(B, T, H, DK), k.view(B, T, H, DK), v.reshape(B, T, H, DV)
-        la, beta = ops.gdn_gates(ab[..., :H], ab[..., H:], self.A_log, self.dt_bias, self.b_bias, 1.0,
+        la, beta = ops.gdn_gates_ab(ab, self.A_log, self.dt_bias, self.b_bias, 1.0,
                                  float("-inf") if self.la_min is None else float(self.la_min))
         gate = g.reshape(B, T, H, DV) if self.use_gate else None
         lam = F.softplus(self.lam.float())

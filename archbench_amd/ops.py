@@ -44,7 +44,7 @@ from . import _lib
 
 __all__ = ["chunk_gated_delta_rule", "fused_recurrent_gated_delta_rule", "recurrent_step", "chunk_fwd",
            "chunk_bwd", "chunk_fwd_stash", "chunk_bwd_stashed", "nsgdn_scan", "nsgdn_scan_chunk", "short_conv", "mixer_input_stage", "write_direction",
-           "gated_rmsnorm", "l2norm", "gdn_gates", "cross_entropy_fwd_bwd_"]
+           "gated_rmsnorm", "l2norm", "gdn_gates", "gdn_gates_ab", "cross_entropy_fwd_bwd_"]
 
 
 def _require_gpu(*ts: Optional[Tensor]) -> None:
@@ -950,7 +950,7 @@ def gdn_gates(a: Tensor, b: Tensor, A_log: Tensor, dt_bias: Optional[Tensor], b_
     A_log, dt_bias, b_bias = _arg(A_log, torch.float32), _arg(dt_bias, torch.float32), _arg(b_bias, torch.float32)
     g = torch.empty(a.shape, dtype=torch.float32, device=a.device)
     beta = torch.empty(a.shape, dtype=torch.float32, device=a.device)
-    rc = lib.gdn_gates_fwd(_lib.ptr(a), _lib.ptr(b), _lib.ptr(A_log), _lib.ptr(dt_bias), _lib.ptr(b_bias),
+    rc = lib.gdn_gates_fwd(_lib.ptr(a), _lib.ptr(b), 0, _lib.ptr(A_log), _lib.ptr(dt_bias), _lib.ptr(b_bias),
                            _lib.ptr(g), _lib.ptr(beta), ntok, H, float(beta_scale), float(g_min),
                            _lib.dtype_code(a.dtype), _lib.stream_ptr(a.device))
     _lib.check(rc, "gdn_gates_fwd")
@@ -976,8 +976,8 @@ def gdn_gates_bwd(a: Tensor, b: Tensor, A_log: Tensor, dt_bias: Optional[Tensor]
     da, db = torch.empty_like(a), torch.empty_like(a)
     dA, ddt, dbb = (torch.empty(H, dtype=torch.float32, device=a.device) for _ in range(3))
     ws = torch.empty(_lib.gates_ws_bytes(ntok, H), dtype=torch.uint8, device=a.device)
-    rc = lib.gdn_gates_bwd(_lib.ptr(a), _lib.ptr(b), _lib.ptr(A_log), _lib.ptr(dt_bias), _lib.ptr(b_bias),
-                           _lib.ptr(dg), _lib.ptr(dbeta), _lib.ptr(da), _lib.ptr(db), _lib.ptr(dA), _lib.ptr(ddt),
+    rc = lib.gdn_gates_bwd(_lib.ptr(a), _lib.ptr(b), 0, _lib.ptr(A_log), _lib.ptr(dt_bias), _lib.ptr(b_bias),
+                           _lib.ptr(dg), _lib.ptr(dbeta), _lib.ptr(da), _lib.ptr(db), 0, _lib.ptr(dA), _lib.ptr(ddt),
                            _lib.ptr(dbb), _lib.ptr(ws), ws.numel(), ntok, H, float(beta_scale), float(g_min),
                            _lib.dtype_code(a.dtype), _lib.stream_ptr(a.device))
     _lib.check(rc, "gdn_gates_bwd")
@@ -1007,6 +1007,91 @@ def _gates_backward(ctx, dg, dbeta):
 
 
 gdn_gates.register_autograd(_gates_backward, setup_context=_gates_setup)
+
+
+# The same gates from the two halves of one [..., 2H] projection output ab = [a | b] (nsgdn.py:522, :531-534 slice
+# ab this way), read in place; the backward writes d(ab) as one tensor, so no gradient of the two slices has to be
+# zero-filled and copied back into a full-width one.
+def _ab_halves(ab: Tensor):
+    if ab.dim() < 1 or ab.shape[-1] % 2 or ab.shape[-1] == 0:
+        raise ValueError(f"ab must be [..., 2H], got {tuple(ab.shape)}")
+    return ab.shape[-1] // 2
+
+
+def _half_ptr(t: Tensor, H: int):
+    return ctypes.c_void_p(t.data_ptr() + H * t.element_size())
+
+
+@torch.library.custom_op("archbench_amd::gdn_gates_ab", mutates_args=())
+def gdn_gates_ab(ab: Tensor, A_log: Tensor, dt_bias: Optional[Tensor], b_bias: Optional[Tensor], beta_scale: float,
+                 g_min: float) -> tuple[Tensor, Tensor]:
+    """(g, beta), fp32 [..., H], from ab [..., 2H] = [a | b]."""
+    _require_gpu(ab, A_log, dt_bias, b_bias)
+    H = _ab_halves(ab)
+    ntok, _ = _gate_shapes(ab[..., :H], ab[..., H:], A_log, dt_bias, b_bias)
+    lib = _lib.load()
+    ab = _arg(ab)
+    A_log, dt_bias, b_bias = _arg(A_log, torch.float32), _arg(dt_bias, torch.float32), _arg(b_bias, torch.float32)
+    shape = (*ab.shape[:-1], H)
+    g = torch.empty(shape, dtype=torch.float32, device=ab.device)
+    beta = torch.empty(shape, dtype=torch.float32, device=ab.device)
+    rc = lib.gdn_gates_fwd(_lib.ptr(ab), _half_ptr(ab, H), 2 * H, _lib.ptr(A_log), _lib.ptr(dt_bias),
+                           _lib.ptr(b_bias), _lib.ptr(g), _lib.ptr(beta), ntok, H, float(beta_scale), float(g_min),
+                           _lib.dtype_code(ab.dtype), _lib.stream_ptr(ab.device))
+    _lib.check(rc, "gdn_gates_fwd")
+    return g, beta
+
+
+@gdn_gates_ab.register_fake
+def _(ab, A_log, dt_bias, b_bias, beta_scale, g_min):
+    shape = (*ab.shape[:-1], ab.shape[-1] // 2)
+    return ab.new_empty(shape, dtype=torch.float32), ab.new_empty(shape, dtype=torch.float32)
+
+
+@torch.library.custom_op("archbench_amd::gdn_gates_ab_bwd", mutates_args=())
+def gdn_gates_ab_bwd(ab: Tensor, A_log: Tensor, dt_bias: Optional[Tensor], b_bias: Optional[Tensor], dg: Tensor,
+                     dbeta: Tensor, beta_scale: float, g_min: float) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(d ab [..., 2H] in ab's dtype, dA_log, ddt_bias, db_bias fp32)."""
+    _require_gpu(ab, A_log, dt_bias, b_bias, dg, dbeta)
+    H = _ab_halves(ab)
+    ntok, _ = _gate_shapes(ab[..., :H], ab[..., H:], A_log, dt_bias, b_bias)
+    lib = _lib.load()
+    ab = _arg(ab)
+    A_log, dt_bias, b_bias = _arg(A_log, torch.float32), _arg(dt_bias, torch.float32), _arg(b_bias, torch.float32)
+    dg, dbeta = _arg(dg, torch.float32), _arg(dbeta, torch.float32)
+    dab = torch.empty_like(ab)
+    dA, ddt, dbb = (torch.empty(H, dtype=torch.float32, device=ab.device) for _ in range(3))
+    ws = torch.empty(_lib.gates_ws_bytes(ntok, H), dtype=torch.uint8, device=ab.device)
+    rc = lib.gdn_gates_bwd(_lib.ptr(ab), _half_ptr(ab, H), 2 * H, _lib.ptr(A_log), _lib.ptr(dt_bias),
+                           _lib.ptr(b_bias), _lib.ptr(dg), _lib.ptr(dbeta), _lib.ptr(dab), _half_ptr(dab, H), 2 * H,
+                           _lib.ptr(dA), _lib.ptr(ddt), _lib.ptr(dbb), _lib.ptr(ws), ws.numel(), ntok, H,
+                           float(beta_scale), float(g_min), _lib.dtype_code(ab.dtype), _lib.stream_ptr(ab.device))
+    _lib.check(rc, "gdn_gates_bwd")
+    return dab, dA, ddt, dbb
+
+
+@gdn_gates_ab_bwd.register_fake
+def _(ab, A_log, dt_bias, b_bias, dg, dbeta, beta_scale, g_min):
+    H = ab.shape[-1] // 2
+    f32 = dict(dtype=torch.float32)
+    return torch.empty_like(ab), ab.new_empty(H, **f32), ab.new_empty(H, **f32), ab.new_empty(H, **f32)
+
+
+def _gates_ab_setup(ctx, inputs, output):
+    ab, A_log, dt_bias, b_bias, beta_scale, g_min = inputs
+    ctx.save_for_backward(ab, A_log, dt_bias, b_bias)
+    ctx.beta_scale, ctx.g_min = beta_scale, g_min
+    ctx.set_materialize_grads(True)
+
+
+def _gates_ab_backward(ctx, dg, dbeta):
+    ab, A_log, dt_bias, b_bias = ctx.saved_tensors
+    dab, dA, ddt, dbb = gdn_gates_ab_bwd(ab, A_log, dt_bias, b_bias, dg, dbeta, ctx.beta_scale, ctx.g_min)
+    return (dab, dA.to(A_log.dtype), None if dt_bias is None else ddt.to(dt_bias.dtype),
+            None if b_bias is None else dbb.to(b_bias.dtype), None, None)
+
+
+gdn_gates_ab.register_autograd(_gates_ab_backward, setup_context=_gates_ab_setup)
 
 
 # ------------------------------------------------------------------------------------------- cross entropy

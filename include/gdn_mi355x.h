@@ -182,16 +182,19 @@ int gdn_l2norm_bwd(const void* x, const void* dy, void* dx, int64_t rows, int di
  *   beta = beta_scale * sigmoid(b + b_bias[h])
  * Replaces nsgdn.py:531-533 (la = -softplus(ab[:H] + dt_bias) * exp(A_log), clamp_min(la_min), beta =
  * sigmoid(ab[H:] + b_bias)) and fla GatedDeltaNet's g / beta (beta_scale 2 for allow_neg_eigval).  a, b, da, db
- * [ntok, H] in dtype; A_log, dt_bias, b_bias [H] fp32 (dt_bias, b_bias may be NULL = 0); g, beta, dg, dbeta
+ * [ntok] rows of H in dtype, the rows of a and b lda elements apart, of da and db ldd apart (0 = H, contiguous;
+ * 2H reads a and b as the halves of one [ntok, 2H] projection, as the reference slices ab, and writes its gradient
+ * in place); A_log, dt_bias, b_bias [H] fp32 (dt_bias, b_bias may be NULL = 0); g, beta, dg, dbeta
  * [ntok, H] fp32.  The backward writes da, db and, where non-NULL, dA_log, ddt_bias, db_bias (summed over tokens
  * in a fixed order through the workspace). */
-int gdn_gates_fwd(const void* a, const void* b, const float* A_log, const float* dt_bias, const float* b_bias,
-                  float* g, float* beta, int64_t ntok, int H, float beta_scale, float g_min, int dtype, void* stream);
-int gdn_gates_bwd_ws_bytes(int64_t ntok, int H, size_t* bytes);
-int gdn_gates_bwd(const void* a, const void* b, const float* A_log, const float* dt_bias, const float* b_bias,
-                  const float* dg, const float* dbeta, void* da, void* db, float* dA_log, float* ddt_bias,
-                  float* db_bias, void* ws, size_t ws_bytes, int64_t ntok, int H, float beta_scale, float g_min,
+int gdn_gates_fwd(const void* a, const void* b, int64_t lda, const float* A_log, const float* dt_bias,
+                  const float* b_bias, float* g, float* beta, int64_t ntok, int H, float beta_scale, float g_min,
                   int dtype, void* stream);
+int gdn_gates_bwd_ws_bytes(int64_t ntok, int H, size_t* bytes);
+int gdn_gates_bwd(const void* a, const void* b, int64_t lda, const float* A_log, const float* dt_bias,
+                  const float* b_bias, const float* dg, const float* dbeta, void* da, void* db, int64_t ldd,
+                  float* dA_log, float* ddt_bias, float* db_bias, void* ws, size_t ws_bytes, int64_t ntok, int H,
+                  float beta_scale, float g_min, int dtype, void* stream);
 
 /* Cross-entropy forward and backward in one pass, in place on a chunk of logits [N, ld] (dtype; V classes,
  * V % 8 == 0, ld % 8 == 0, V <= 65536): loss[i] = logsumexp(x_i) - x_i,target[i] (0 where target == ignore_index,

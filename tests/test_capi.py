@@ -99,9 +99,12 @@ def test_gates_backward_rejects_too_many_heads():
     assert lib.gdn_gates_bwd_ws_bytes(4, 1025, ctypes.byref(n)) == _lib.GDN_ERR_SHAPE
     assert b"1024" in lib.gdn_last_error()
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    rc = lib.gdn_gates_bwd(p, p, p, None, None, p, p, p, p, None, None, None, p, 1 << 30, 4, 2000, 1.0,
+    rc = lib.gdn_gates_bwd(p, p, 0, p, None, None, p, p, p, p, 0, None, None, None, p, 1 << 30, 4, 2000, 1.0,
                            float("-inf"), 1, None)
     assert rc == _lib.GDN_ERR_SHAPE
+    # row strides below H are refused
+    rc = lib.gdn_gates_fwd(p, p, 3, p, None, None, p, p, 4, 4, 1.0, float("-inf"), 1, None)
+    assert rc == _lib.GDN_ERR_ARG and b"lda" in lib.gdn_last_error()
 
 
 def test_fp32_head_size_error_names_the_bf16_route():

@@ -130,6 +130,32 @@ def test_gates_autograd():
         assert max_abs(leaf.grad, r) <= 1e-4 * max(1.0, r.abs().max().item())
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_gates_from_one_ab_projection(dtype):
+    """gdn_gates_ab reads a and b as the halves of one [..., 2H] tensor in place and writes its gradient as one
+    tensor: bit for bit what gdn_gates gives on the two slices, forward and through autograd."""
+    banner(f"gates from one ab projection {dtype}")
+    H = 4
+    ab = (torch.randn(2, 300, 2 * H, generator=_g(20)) * 2).to("cuda", dtype)
+    A_log, dt_bias, b_bias = (torch.rand(H, generator=_g(21)) * 2).cuda(), torch.randn(H, generator=_g(22)).cuda(), \
+        torch.randn(H, generator=_g(23)).cuda()
+    dg, dbeta = torch.randn(2, 300, H, generator=_g(24)).cuda(), torch.randn(2, 300, H, generator=_g(25)).cuda()
+    for g_min in (float("-inf"), -0.5):
+        leaves1 = [ab.clone().requires_grad_(), A_log.clone().requires_grad_(), dt_bias.clone().requires_grad_(),
+                   b_bias.clone().requires_grad_()]
+        g1, beta1 = ops.gdn_gates_ab(*leaves1, 1.0, g_min)
+        ((g1 * dg).sum() + (beta1 * dbeta).sum()).backward()
+        leaves2 = [ab.clone().requires_grad_(), A_log.clone().requires_grad_(), dt_bias.clone().requires_grad_(),
+                   b_bias.clone().requires_grad_()]
+        g2, beta2 = ops.gdn_gates(leaves2[0][..., :H], leaves2[0][..., H:], *leaves2[1:], 1.0, g_min)
+        ((g2 * dg).sum() + (beta2 * dbeta).sum()).backward()
+        assert torch.equal(g1, g2) and torch.equal(beta1, beta2)
+        for l1, l2 in zip(leaves1, leaves2):
+            assert torch.equal(l1.grad, l2.grad)
+    with pytest.raises(ValueError, match="2H"):
+        ops.gdn_gates_ab(torch.randn(3, 7, device="cuda"), A_log, None, None, 1.0, float("-inf"))
+
+
 def test_norm_and_gates_shape_errors():
     banner("norm / gates shape errors")
     x = torch.randn(4, 96, device="cuda")
