@@ -828,7 +828,7 @@ int gdn_token_scan_sizes(int B, int T, int H, int K, int V, size_t* st_bytes, si
   if (!st_bytes || !scratch_bytes || !n_partials) return fail(GDN_ERR_ARG, "null output pointer");
   const size_t NB = (size_t)(V + 63) / 64, NCH = (size_t)(T + token_scan_ct() - 1) / token_scan_ct();
   *st_bytes = (size_t)B * H * NCH * K * V * 4;
-  *scratch_bytes = (size_t)B * H * NB * token_scan_ct() * K * 64 * 4;
+  *scratch_bytes = (size_t)B * H * NB * token_scan_scratch_floats(K) * 4;
   *n_partials = (int)NB;
   return GDN_OK;
 }

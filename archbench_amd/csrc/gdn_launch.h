@@ -207,6 +207,7 @@ struct TokenScanArgs {
 };
 bool token_scan_supported(int K);
 int token_scan_ct();
+size_t token_scan_scratch_floats(int K);  // backward scratch per (b, h, 64-row block)
 hipError_t launch_token_scan(const TokenScanArgs& a, bool backward);
 
 // Compute units of the current device (cached per device; 256 if the query fails).

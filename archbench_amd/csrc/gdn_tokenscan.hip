@@ -2,18 +2,19 @@
 // "triton" / "ref" scan (archbench/layers/nsgdn.py:80-154, ops :162-216; the recurrence of nsgdn_ref, :408-417).
 // Per token t of a (b, h) sequence, with the state S [V, K] fp32 from zero (or from an initial state):
 //     S <- e^{la_t} S;   r_t = v_t - S k_t;   S <- S + r_t u_t^T;   y_t = S q_t.
-// Rows of S are independent given the token stream.  A workgroup of four waves owns 64 rows; four lanes share a
-// row, lane quarter l & 3 holding K / 4 of its entries in registers, so a row's dot products (S k, S q, G u) are a
-// partial sum per lane and two DPP steps inside the quad.  k, u, q of a token are workgroup-uniform and reach the
+// Rows of S are independent given the token stream.  A workgroup of eight waves owns 64 rows; eight lanes share a
+// row, lane part l & 7 holding K / 8 of its entries in registers, so a row's dot products (S k, S q, G u) are a
+// partial sum per lane and three DPP steps inside the 8-lane group.  k, u, q of a token are workgroup-uniform and reach the
 // lanes through LDS (double-buffered: a token is staged while the one before it computes, one barrier per token).
 // Every CT tokens the forward stores S (the checkpoint the backward restarts from) in [K][V] order.
-// The backward walks the checkpoints in reverse: it recomputes the chunk's states forward from the checkpoint
-// (keeping e^{la} S before each token's update in a per-workgroup scratch) and accumulates dq = sum_rows S_t^T dy_t,
-// then runs the chunk's tokens backward with the state gradient G [V, K] in registers beside S:
+// The backward walks the checkpoints in reverse and each chunk in groups of four tokens, last first: it recomputes
+// a group's states forward from the state entering the group (stored by a forward pass over the chunk from its
+// checkpoint), keeping e^{la} S before each token's update in registers and accumulating dq = sum_rows S_t^T dy_t,
+// then runs the group's tokens backward with the state gradient G [V, K] in registers beside S:
 //     G += dy_t q_t^T;  dv_t = G u_t;  du_t = sum_rows G r_t;  G -= dv_t k_t^T;
 //     dk_t = -sum_rows (e^{la} S_{t-1}) dv_t;  dla_t = sum (G o e^{la} S_{t-1});  G <- e^{la_t} G.
-// Sums over rows are a reduce-scatter over the wave's 16 rows (lane swaps and DPP, no LDS crossbar), then over the
-// four waves through LDS (a fixed order, no atomics), then over a head's V / 64 workgroups through partial rows that
+// Sums over rows are a reduce-scatter over the wave's 8 rows (lane swaps and DPP, no LDS crossbar), then over the
+// eight waves through LDS (a fixed order, no atomics), then over a head's V / 64 workgroups through partial rows that
 // the host adds.
 #include <hip/hip_runtime.h>
 
@@ -22,17 +23,39 @@
 
 namespace gdn {
 
-constexpr int TS_CT = 32;                  // tokens between checkpoints
-constexpr int TS_ROWS = 64;                // state rows per workgroup
-constexpr int TS_THREADS = 4 * TS_ROWS;    // four lanes per row
-constexpr int TS_WAVES = TS_THREADS / 64;  // each wave holds 16 rows
+constexpr int TS_CT = 32;                    // tokens between checkpoints
+constexpr int TS_GS = 4;                     // tokens per group of the backward (decayed states held in registers)
+constexpr int TS_PF = 4;                     // tokens in flight: a token's loads are issued TS_PF tokens ahead
+constexpr int TS_ROWS = 64;                  // state rows per workgroup
+constexpr int TS_LPR = 8;                    // lanes per row
+constexpr int TS_LB = 3;                     // log2 TS_LPR
+constexpr int TS_THREADS = TS_LPR * TS_ROWS;
+constexpr int TS_WAVES = TS_THREADS / 64;    // each wave holds 64 / TS_LPR rows
 
-// sum over the four lanes of a row (a quad), left in each of them
-__device__ __forceinline__ float ts_quad_sum(float x) { return dpp_sum_step<0x4e>(dpp_sum_step<0xb1>(x)); }
+// The per-token barrier orders LDS only (the staged vectors and the row sums): __syncthreads() would also wait for
+// every global load in flight, the tokens prefetched ahead included, and so expose a memory latency per token.
+__device__ __forceinline__ void ts_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+// A zero the compiler cannot see through, added to a workgroup-uniform index so that the load is a vector load: a
+// scalar load would be waited for at the next barrier (scalar loads and LDS share one wait counter).
+__device__ __forceinline__ int ts_vector_zero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
 
-// Reduce-scatter over a wave's 16 rows: N values per lane (its quarter's local columns), summed over the 16 lanes
-// that share l & 3 (lane bits 2..5).  Lane l ends with the sums of local columns m + (N / 16) (l >> 2), m < N / 16,
-// in a[0 .. N / 16).  Each round pairs lanes that differ in one bit and hold the same column set: one keeps the lower
+// sum over the eight lanes of a row, left in each of them: quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror
+// (lane p <- 7 - p) adds the other quad
+__device__ __forceinline__ float ts_row_sum(float x) {
+  return dpp_sum_step<0x141>(dpp_sum_step<0x4e>(dpp_sum_step<0xb1>(x)));
+}
+
+// Reduce-scatter over a wave's 8 rows: N values per lane (its part's local columns), summed over the 8 lanes that
+// share l & 7 (lane bits 3..5).  Lane l ends with the sums of local columns m + (N / 8) (l >> 3), m < N / 8, in
+// a[0 .. N / 8).  Each round pairs lanes that differ in one bit and hold the same column set: one keeps the lower
 // half of its set, the other the upper half, and each adds what its partner sends.
 template <int N>
 __device__ __forceinline__ void ts_rows_rs(float (&a)[N], int l) {
@@ -56,33 +79,26 @@ __device__ __forceinline__ void ts_rows_rs(float (&a)[N], int l) {
     const float keep = b3 ? a[m + N / 8] : a[m], send = b3 ? a[m] : a[m + N / 8];
     a[m] = keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0x128, 0xf, 0xf, false));
   }
-  // bit 2: lanes l and l ^ 4
-  const int b2 = (l >> 2) & 1;
-#pragma unroll
-  for (int m = 0; m < N / 16; ++m) {
-    const float keep = b2 ? a[m + N / 16] : a[m], send = b2 ? a[m] : a[m + N / 16];
-    a[m] = keep + __shfl_xor(send, 4);
-  }
 }
 
-// A token's k, u, q in LDS: per vector four quarter blocks of K / 4 floats, each padded by 4 so that the four lanes
-// of a quad (one per block) read different banks with 16-byte reads.  Threads below 3 K / 4 (or the K / 4 of u alone)
-// each load one float4 of the next token while the current one computes and store it here when it is done.
+// A token's k, u, q in LDS: per vector eight blocks of K / 8 floats, each padded by 4 so that the eight lanes of a
+// row (one per block) read different banks with 16-byte reads.  Threads below 3 K / 4 (or the K / 4 of u alone)
+// each load one float4 of a token TS_PF tokens ahead of the one computing (a ring of registers, so that a load has
+// TS_PF tokens' time to arrive) and store it here one token ahead.
 template <int K>
 struct TokStage {
-  static constexpr int KQ = K / 4, LD = KQ + 4, VEC = 4 * LD, SIZE = 3 * VEC;
-  f32x4 x;
-  __device__ __forceinline__ void load(const float* kp, const float* up, const float* qp, int64_t t, int tid,
-                                       bool kq) {
-    const int vec = tid / KQ, e4 = tid - vec * KQ;
-    if (kq ? tid < 3 * KQ : vec == 1) {
+  static constexpr int KQ = K / TS_LPR, K4 = K / 4, LD = KQ + 4, VEC = TS_LPR * LD, SIZE = 3 * VEC;
+  static __device__ __forceinline__ void load(const float* kp, const float* up, const float* qp, int64_t t, int tid,
+                                              bool kq, f32x4& x) {
+    const int vec = tid / K4, e4 = tid - vec * K4;
+    if (kq ? tid < 3 * K4 : vec == 1) {
       const float* src = vec == 0 ? kp : vec == 1 ? up : qp;
       x = *reinterpret_cast<const f32x4*>(src + t * K + 4 * e4);
     }
   }
-  __device__ __forceinline__ void stage(float* sv, int tid, bool kq) const {
-    const int vec = tid / KQ, c = 4 * (tid - vec * KQ), qd = c / KQ;
-    if (kq ? tid < 3 * KQ : vec == 1) *reinterpret_cast<f32x4*>(sv + vec * VEC + qd * LD + c - qd * KQ) = x;
+  static __device__ __forceinline__ void stage(float* sv, int tid, bool kq, const f32x4& x) {
+    const int vec = tid / K4, c = 4 * (tid - vec * K4), qd = c / KQ;
+    if (kq ? tid < 3 * K4 : vec == 1) *reinterpret_cast<f32x4*>(sv + vec * VEC + qd * LD + c - qd * KQ) = x;
   }
 };
 
@@ -97,7 +113,7 @@ __device__ __forceinline__ void ts_read(const float* p, float (&o)[KQ]) {
   }
 }
 
-// grid B * H * NB (NB = ceil(V / 64)) workgroups of 256 threads: workgroup x -> (b h, row block vb)
+// grid B * H * NB (NB = ceil(V / 64)) workgroups of 512 threads: workgroup x -> (b h, row block vb)
 template <int K>
 __global__ __launch_bounds__(TS_THREADS) void token_scan_fwd_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ u, const float* __restrict__ v,
@@ -106,10 +122,10 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_fwd_kernel(
   using TS = TokStage<K>;
   constexpr int KQ = TS::KQ;
   __shared__ __attribute__((aligned(16))) float sv[2][TS::SIZE];
-  const int tid = threadIdx.x, l = lane_id(), qd = l & 3;
+  const int tid = threadIdx.x, l = lane_id(), qd = l & (TS_LPR - 1);
   const int pid = blockIdx.x, bh = pid / NB, vb = pid - bh * NB;
   const int b = bh / H, h = bh - b * H;
-  const int vi = vb * TS_ROWS + (tid >> 2);
+  const int vi = vb * TS_ROWS + (tid >> TS_LB);
   const bool on = vi < V;
   const int vc = on ? vi : V - 1;  // rows past V compute on row V-1 and store nothing
   // states [B, H, K, V] (fla's layout): entry (row vi, column qd KQ + j) at cb + j V
@@ -119,49 +135,66 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_fwd_kernel(
   for (int j = 0; j < KQ; ++j) S[j] = h0 && on ? h0[cb + (int64_t)j * V] : 0.f;
   float* stb = st + (int64_t)bh * NCH * K * V + (int64_t)qd * KQ * V + vi;
   const int64_t tok_first = (int64_t)b * T_ * H + h;
-  TS nx;
-  nx.load(k, u, q, tok_first, tid, true);  // T_ >= 1 here (the host returns before launching an empty scan)
-  nx.stage(sv[0], tid, true);
-  float nv = v[tok_first * V + vc], nla = la[tok_first];
-  if (T_ > 1) nx.load(k, u, q, tok_first + H, tid, true);
-  __syncthreads();
-  int64_t tok = tok_first;
-  for (int t = 0; t < T_; ++t, tok += H) {
-    if (t % TS_CT == 0 && on) {
-      const int64_t c = t / TS_CT;
+  // token t's vectors and row values in ring slot t % TS_PF
+  f32x4 xr[TS_PF];
+  float vr[TS_PF], lr[TS_PF];
+  const int zv = ts_vector_zero();
+  auto load_tok = [&](int t, int sl) {
+    const int64_t tk = tok_first + (int64_t)t * H;
+    TS::load(k, u, q, tk, tid, true, xr[sl]);
+    vr[sl] = v[tk * V + vc];
+    lr[sl] = la[tk + zv];
+  };
 #pragma unroll
-      for (int j = 0; j < KQ; ++j) stb[(c * K + j) * V] = S[j];
-    }
-    const float vcur = nv, a = expf(nla);
-    if (t + 1 < T_) {  // stage the next token (loaded one token ago), load the one after it
-      nx.stage(sv[(t + 1) & 1], tid, true);
-      nv = v[(tok + H) * V + vc];
-      nla = la[tok + H];
-      if (t + 2 < T_) nx.load(k, u, q, tok + 2 * H, tid, true);
-    }
-    const float* sk = sv[t & 1] + qd * TS::LD;
-    float kk[KQ];
-    ts_read<KQ>(sk, kk);
-    float d[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < TS_PF; ++s)
+    if (s < T_) load_tok(s, s);  // T_ >= 1 here (the host returns before launching an empty scan)
+  TS::stage(sv[0], tid, true, xr[0]);
+  float nv = vr[0], nla = lr[0];
+  if (TS_PF < T_) load_tok(TS_PF, 0);
+  ts_barrier();
+  for (int t0 = 0; t0 < T_; t0 += TS_PF) {
 #pragma unroll
-    for (int j = 0; j < KQ; ++j) {
-      S[j] *= a;
-      d[j & 3] = fmaf(S[j], kk[j], d[j & 3]);
-    }
-    const float rr = vcur - ts_quad_sum((d[0] + d[1]) + (d[2] + d[3]));
-    float uu[KQ], qq[KQ];
-    ts_read<KQ>(sk + TS::VEC, uu);
-    ts_read<KQ>(sk + 2 * TS::VEC, qq);
-    float e[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < TS_PF; ++s) {
+      const int t = t0 + s;
+      if (t >= T_) break;
+      const int64_t tok = tok_first + (int64_t)t * H;
+      if (t % TS_CT == 0 && on) {
+        const int64_t c = t / TS_CT;
 #pragma unroll
-    for (int j = 0; j < KQ; ++j) {
-      S[j] = fmaf(rr, uu[j], S[j]);
-      e[j & 3] = fmaf(S[j], qq[j], e[j & 3]);
+        for (int j = 0; j < KQ; ++j) stb[(c * K + j) * V] = S[j];
+      }
+      const float vcur = nv, a = expf(nla);
+      if (t + 1 < T_) {  // stage the next token from its slot, and load the token TS_PF after it there
+        const int sl = (s + 1) % TS_PF;
+        TS::stage(sv[(t + 1) & 1], tid, true, xr[sl]);
+        nv = vr[sl];
+        nla = lr[sl];
+        if (t + 1 + TS_PF < T_) load_tok(t + 1 + TS_PF, sl);
+      }
+      const float* sk = sv[t & 1] + qd * TS::LD;
+      float kk[KQ];
+      ts_read<KQ>(sk, kk);
+      float d[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KQ; ++j) {
+        S[j] *= a;
+        d[j & 3] = fmaf(S[j], kk[j], d[j & 3]);
+      }
+      const float rr = vcur - ts_row_sum((d[0] + d[1]) + (d[2] + d[3]));
+      float uu[KQ], qq[KQ];
+      ts_read<KQ>(sk + TS::VEC, uu);
+      ts_read<KQ>(sk + 2 * TS::VEC, qq);
+      float e[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KQ; ++j) {
+        S[j] = fmaf(rr, uu[j], S[j]);
+        e[j & 3] = fmaf(S[j], qq[j], e[j & 3]);
+      }
+      const float yy = ts_row_sum((e[0] + e[1]) + (e[2] + e[3]));
+      if (on && qd == 0) r[tok * V + vi] = rr;
+      if (on && qd == 1) y[tok * V + vi] = yy;
+      ts_barrier();  // this token's vectors read by every lane; the next token's staged
     }
-    const float yy = ts_quad_sum((e[0] + e[1]) + (e[2] + e[3]));
-    if (on && qd == 0) r[tok * V + vi] = rr;
-    if (on && qd == 1) y[tok * V + vi] = yy;
-    __syncthreads();  // this token's vectors read by every lane; the next token's staged
   }
   if (hT && on) {
 #pragma unroll
@@ -178,21 +211,29 @@ struct TokSums {
   // this wave's reduce-scattered sums of local columns (quarter qd) into vector slot s
   template <int KQ>
   __device__ __forceinline__ void put(int par, int s, const float (&a)[KQ], int l) {
-    const int w = wave_id(), c0 = (l & 3) * KQ + (KQ / 16) * (l >> 2);
+    const int w = wave_id(), c0 = (l & (TS_LPR - 1)) * KQ + (KQ / 8) * (l >> TS_LB);
 #pragma unroll
-    for (int m = 0; m < KQ / 16; ++m) col[par][s][w][c0 + m] = a[m];
+    for (int m = 0; m < KQ / 8; ++m) col[par][s][w][c0 + m] = a[m];
   }
   __device__ __forceinline__ float col_sum(int par, int s, int c) const {
     const float(&x)[TS_WAVES][K] = col[par][s];
-    return (x[0][c] + x[1][c]) + (x[2][c] + x[3][c]);
+    return ((x[0][c] + x[1][c]) + (x[2][c] + x[3][c])) + ((x[4][c] + x[5][c]) + (x[6][c] + x[7][c]));
   }
   __device__ __forceinline__ float sca_sum(int par) const {
-    return (sca[par][0] + sca[par][1]) + (sca[par][2] + sca[par][3]);
+    return ((sca[par][0] + sca[par][1]) + (sca[par][2] + sca[par][3])) +
+           ((sca[par][4] + sca[par][5]) + (sca[par][6] + sca[par][7]));
   }
 };
-static_assert(TS_WAVES == 4, "the LDS sums add four waves");
+static_assert(TS_WAVES == 8 && TS_LPR == 1 << TS_LB, "the LDS sums add eight waves");
+static_assert(TS_GS % TS_PF == 0, "a backward pass's steps come in whole rings");
 
-// Partials: gqp, gup, gkp [NB][B*T*H][K], glap [NB][B*T*H]; sc [B*H*NB][TS_CT][K / 4][256] scratch.
+// Partials: gqp, gup, gkp [NB][B*T*H][K], glap [NB][B*T*H]; sc [B*H*NB][TS_CT / TS_GS][K / 8][512] scratch of the
+// chunk's group-start states.
+// Per chunk (last first), in groups of TS_GS tokens: a forward pass from the checkpoint stores the state entering each
+// group but the first and last (the last stays in registers); then, group by group from the last, the group's tokens
+// are recomputed forward from its start state with each decayed state e^{la} S_{t-1} kept in registers (and dq
+// accumulated), and walked backward.  A short last group is padded with identity tokens (la = 0, zero vectors and
+// row values), which change neither S nor G, and whose sums are not stored.
 template <int K>
 __global__ __launch_bounds__(TS_THREADS) void token_scan_bwd_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ u, const float* __restrict__ la,
@@ -201,128 +242,175 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_bwd_kernel(
     float* __restrict__ gkp, float* __restrict__ glap, float* __restrict__ dh0, float* __restrict__ sc, int T_, int H,
     int V, int NCH, int NB, int64_t ntok) {
   using TS = TokStage<K>;
-  constexpr int KQ = TS::KQ;
+  constexpr int KQ = TS::KQ, NGS = TS_CT / TS_GS;
   __shared__ __attribute__((aligned(16))) float sv[2][TS::SIZE];
   __shared__ TokSums<K> sums;
-  const int tid = threadIdx.x, l = lane_id(), qd = l & 3;
+  const int tid = threadIdx.x, l = lane_id(), qd = l & (TS_LPR - 1);
   const int pid = blockIdx.x, bh = pid / NB, vb = pid - bh * NB;
   const int b = bh / H, h = bh - b * H;
-  const int vi = vb * TS_ROWS + (tid >> 2);
+  const int vi = vb * TS_ROWS + (tid >> TS_LB);
   const bool on = vi < V;
   const float* stb = st + (int64_t)bh * NCH * K * V + (int64_t)qd * KQ * V + vi;
-  float* scw = sc + (int64_t)pid * TS_CT * KQ * TS_THREADS + tid;
+  float* scw = sc + (int64_t)pid * NGS * KQ * TS_THREADS + tid;
   float* gq_b = gqp + (int64_t)vb * ntok * K;
   float* gu_b = gup + (int64_t)vb * ntok * K;
   float* gk_b = gkp + (int64_t)vb * ntok * K;
   float* gl_b = glap + (int64_t)vb * ntok;
-  TS nx;
-  float nla = 0.f, nr = 0.f, ngy = 0.f;
-  auto fetch_row = [&](int64_t t) {
-    nla = la[t];
-    nr = on ? r[t * V + vi] : 0.f;
-    ngy = on ? gy[t * V + vi] : 0.f;
+  // a step's vectors and row values in ring slot f % TS_PF (f: the step within its pass)
+  f32x4 xr[TS_PF];
+  float lr[TS_PF], rr[TS_PF], yr[TS_PF];
+  float nla = 0.f, nr = 0.f, ngy = 0.f;  // the next step's row values
+  const int zv = ts_vector_zero();
+  // token tok, or an identity token (tok < 0: zero vectors and row values, la = 0), into slot sl
+  auto ld = [&](int64_t tok, int sl, bool kq) {
+    if (tok >= 0) TS::load(k, u, q, tok, tid, kq, xr[sl]);
+    else xr[sl] = f32x4{0.f, 0.f, 0.f, 0.f};
+    lr[sl] = tok >= 0 ? la[tok + zv] : 0.f;
+    rr[sl] = tok >= 0 && on ? r[tok * V + vi] : 0.f;
+    yr[sl] = tok >= 0 && on ? gy[tok * V + vi] : 0.f;
   };
-  // one pass over the tokens tok_at(0 .. n) with the vectors (u alone unless kq) staged a token ahead; body(i, tok,
-  // parity) computes token i from sv[parity] with its row scalars in the registers taken before the staging
-  int par = 0;
-  auto pass = [&](int n, bool kq, auto&& tok_at, auto&& body) {
-    nx.load(k, u, q, tok_at(0), tid, kq);
-    nx.stage(sv[par & 1], tid, kq);
-    fetch_row(tok_at(0));
-    if (n > 1) nx.load(k, u, q, tok_at(1), tid, kq);
-    __syncthreads();
-    for (int i = 0; i < n; ++i, ++par) {
-      const float a = expf(nla), rc = nr, gyc = ngy;
-      const int64_t tok = tok_at(i);
-      if (i + 1 < n) {
-        nx.stage(sv[(par + 1) & 1], tid, kq);
-        fetch_row(tok_at(i + 1));
-        if (i + 2 < n) nx.load(k, u, q, tok_at(i + 2), tid, kq);
-      }
-      body(i, tok, a, rc, gyc);
-      __syncthreads();  // this token's vectors and sums complete; the next token's staged
+  int par = 0;  // parity of the step: sv[par & 1] holds its vectors, sums[par & 1] takes its row sums
+  // Steps f = 0 .. nf of a pass over tokens tok_at(f): the first TS_PF loaded and the first staged before the first
+  // barrier; then each step stages step f + 1 from its slot (sl = (f + 1) % TS_PF) and loads step f + 1 + TS_PF there.
+  auto prologue = [&](int nf, bool kq, auto&& tok_at) {
+#pragma unroll
+    for (int s = 0; s < TS_PF; ++s)
+      if (s < nf) ld(tok_at(s), s, kq);
+    TS::stage(sv[par & 1], tid, kq, xr[0]);
+    nla = lr[0], nr = rr[0], ngy = yr[0];
+    if (TS_PF < nf) ld(tok_at(TS_PF), 0, kq);
+    ts_barrier();
+  };
+  auto advance = [&](int f, int sl, int nf, bool kq, auto&& tok_at) {
+    if (f + 1 < nf) {
+      TS::stage(sv[(par + 1) & 1], tid, kq, xr[sl]);
+      nla = lr[sl], nr = rr[sl], ngy = yr[sl];
+      if (f + 1 + TS_PF < nf) ld(tok_at(f + 1 + TS_PF), sl, kq);
     }
   };
   const int64_t cb = (int64_t)bh * K * V + (int64_t)qd * KQ * V + vi;  // [B, H, K, V] states, as in the forward
-  float G[KQ];
+  float G[KQ], S[KQ];
 #pragma unroll
   for (int j = 0; j < KQ; ++j) G[j] = dhT && on ? dhT[cb + (int64_t)j * V] : 0.f;
   for (int c = NCH - 1; c >= 0; --c) {
-    const int n = min(TS_CT, T_ - c * TS_CT);
+    const int n = min(TS_CT, T_ - c * TS_CT), ng = (n + TS_GS - 1) / TS_GS;
     const int64_t tok0 = ((int64_t)b * T_ + (int64_t)c * TS_CT) * H + h;
-    {  // recompute the chunk's states from its checkpoint; dq
-      float S[KQ];
 #pragma unroll
-      for (int j = 0; j < KQ; ++j) S[j] = on ? stb[((int64_t)c * K + j) * V] : 0.f;
-      int64_t prev = -1;  // the token whose dq sums wait in LDS
-      pass(n, false, [&](int i) { return tok0 + (int64_t)i * H; },
-           [&](int i, int64_t tok, float a, float rc, float gyc) {
-             const int p = par & 1;
-             if (prev >= 0 && tid < K) gq_b[prev * K + tid] = sums.col_sum(p ^ 1, 0, tid);
-             float uu[KQ];
-             ts_read<KQ>(sv[p] + TS::VEC + qd * TS::LD, uu);
-             float t[KQ];
+    for (int j = 0; j < KQ; ++j) S[j] = on ? stb[((int64_t)c * K + j) * V] : 0.f;
+    // forward from the checkpoint to the last group's start, storing the start states of groups 1 .. ng - 2
+    const int na = (ng - 1) * TS_GS;
+    if (na > 0) {
+      auto tok_a = [&](int f) { return tok0 + (int64_t)f * H; };
+      prologue(na, false, tok_a);
+      for (int f0 = 0; f0 < na; f0 += TS_PF) {
 #pragma unroll
-             for (int j = 0; j < KQ; ++j) {
-               S[j] *= a;
-               scw[((int64_t)i * KQ + j) * TS_THREADS] = S[j];
-               S[j] = fmaf(rc, uu[j], S[j]);
-               t[j] = S[j] * gyc;
-             }
-             ts_rows_rs<KQ>(t, l);
-             sums.put(p, 0, t, l);
-             prev = tok;
-           });
-      if (tid < K) gq_b[prev * K + tid] = sums.col_sum((par - 1) & 1, 0, tid);
+        for (int s = 0; s < TS_PF; ++s, ++par) {
+          const int f = f0 + s;
+          const float a = expf(nla), rc = nr;
+          advance(f, (s + 1) % TS_PF, na, false, tok_a);
+          float uu[KQ];
+          ts_read<KQ>(sv[par & 1] + TS::VEC + qd * TS::LD, uu);
+#pragma unroll
+          for (int j = 0; j < KQ; ++j) S[j] = fmaf(rc, uu[j], S[j] * a);
+          if ((f + 1) % TS_GS == 0 && f + 1 < na) {
+#pragma unroll
+            for (int j = 0; j < KQ; ++j) scw[((int64_t)((f + 1) / TS_GS) * KQ + j) * TS_THREADS] = S[j];
+          }
+          ts_barrier();
+        }
+      }
     }
-    int64_t prev = -1;  // the token whose du, dk, dla sums wait in LDS
-    auto flush = [&](int p) {
+    // groups last to first: TS_GS forward steps (tokens 0 .. TS_GS - 1 of the group), then TS_GS backward steps
+    const int nf = 2 * TS_GS * ng;
+    auto tok_b = [&](int f) -> int64_t {
+      const int g = ng - 1 - f / (2 * TS_GS), s = f % (2 * TS_GS);
+      const int i = g * TS_GS + (s < TS_GS ? s : 2 * TS_GS - 1 - s);
+      return i < n ? tok0 + (int64_t)i * H : -1;
+    };
+    prologue(nf, true, tok_b);
+    int64_t prev = -1;  // the token whose row sums wait in LDS (-1: none, or an identity token)
+    for (int g = ng - 1; g >= 0; --g) {
+      if (g < ng - 1) {
+        if (g == 0) {
+#pragma unroll
+          for (int j = 0; j < KQ; ++j) S[j] = on ? stb[((int64_t)c * K + j) * V] : 0.f;
+        } else {
+#pragma unroll
+          for (int j = 0; j < KQ; ++j) S[j] = scw[((int64_t)g * KQ + j) * TS_THREADS];
+        }
+      }
+      float Sd[TS_GS][KQ];  // e^{la} S_{t-1} of the group's tokens
+#pragma unroll
+      for (int s = 0; s < 2 * TS_GS; ++s, ++par) {
+        const int f = (ng - 1 - g) * 2 * TS_GS + s, p = par & 1;
+        const int64_t tok = tok_b(f);
+        const float a = expf(nla), rc = nr, gyc = ngy;
+        advance(f, (s + 1) % TS_PF, nf, true, tok_b);
+        // the previous step's sums: dq after a forward step, du, dk, dla after a backward one
+        if (prev >= 0) {
+          if (s >= 1 && s <= TS_GS) {
+            if (tid < K) gq_b[prev * K + tid] = sums.col_sum(p ^ 1, 0, tid);
+          } else {
+            if (tid < K) gu_b[prev * K + tid] = sums.col_sum(p ^ 1, 0, tid);
+            else if (tid < 2 * K) gk_b[prev * K + tid - K] = sums.col_sum(p ^ 1, 1, tid - K);
+            if (tid == 0) gl_b[prev] = sums.sca_sum(p ^ 1);
+          }
+        }
+        const float* sb = sv[p] + qd * TS::LD;
+        float uu[KQ], t[KQ];
+        ts_read<KQ>(sb + TS::VEC, uu);
+        if (s < TS_GS) {
+#pragma unroll
+          for (int j = 0; j < KQ; ++j) {
+            S[j] *= a;
+            Sd[s][j] = S[j];
+            S[j] = fmaf(rc, uu[j], S[j]);
+            t[j] = S[j] * gyc;
+          }
+          ts_rows_rs<KQ>(t, l);
+          sums.put(p, 0, t, l);
+        } else {
+          const int i = 2 * TS_GS - 1 - s;
+          float qq[KQ], kk[KQ];
+          ts_read<KQ>(sb + 2 * TS::VEC, qq);
+          float d[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < KQ; ++j) {
+            G[j] = fmaf(gyc, qq[j], G[j]);
+            d[j & 3] = fmaf(G[j], uu[j], d[j & 3]);
+          }
+          const float gr = ts_row_sum((d[0] + d[1]) + (d[2] + d[3]));
+          if (on && qd == 0 && tok >= 0) gv[tok * V + vi] = gr;
+#pragma unroll
+          for (int j = 0; j < KQ; ++j) t[j] = G[j] * rc;
+          ts_rows_rs<KQ>(t, l);
+          sums.put(p, 0, t, l);
+          ts_read<KQ>(sb, kk);
+#pragma unroll
+          for (int j = 0; j < KQ; ++j) {
+            G[j] = fmaf(-gr, kk[j], G[j]);
+            t[j] = -Sd[i][j] * gr;
+          }
+          ts_rows_rs<KQ>(t, l);
+          sums.put(p, 1, t, l);
+          float e[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < KQ; ++j) e[j & 3] = fmaf(G[j], Sd[i][j], e[j & 3]);
+          const float gl = wave_sum64((e[0] + e[1]) + (e[2] + e[3]));
+          if (l == 0) sums.sca[p][wave_id()] = gl;
+#pragma unroll
+          for (int j = 0; j < KQ; ++j) G[j] *= a;
+        }
+        prev = tok;
+        ts_barrier();  // this step's vectors read and sums written; the next step's vectors staged
+      }
+    }
+    if (prev >= 0) {  // the chunk's first token (a backward step)
+      const int p = (par - 1) & 1;
       if (tid < K) gu_b[prev * K + tid] = sums.col_sum(p, 0, tid);
       else if (tid < 2 * K) gk_b[prev * K + tid - K] = sums.col_sum(p, 1, tid - K);
       if (tid == 0) gl_b[prev] = sums.sca_sum(p);
-    };
-    pass(n, true, [&](int i) { return tok0 + (int64_t)(n - 1 - i) * H; },
-         [&](int i, int64_t tok, float a, float rc, float gyc) {
-           const int p = par & 1;
-           if (prev >= 0) flush(p ^ 1);
-           const float* sb = sv[p] + qd * TS::LD;
-           float qq[KQ], uu[KQ];
-           ts_read<KQ>(sb + 2 * TS::VEC, qq);
-           ts_read<KQ>(sb + TS::VEC, uu);
-           float d[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-           for (int j = 0; j < KQ; ++j) {
-             G[j] = fmaf(gyc, qq[j], G[j]);
-             d[j & 3] = fmaf(G[j], uu[j], d[j & 3]);
-           }
-           const float gr = ts_quad_sum((d[0] + d[1]) + (d[2] + d[3]));
-           if (on && qd == 0) gv[tok * V + vi] = gr;
-           float t[KQ];
-#pragma unroll
-           for (int j = 0; j < KQ; ++j) t[j] = G[j] * rc;
-           ts_rows_rs<KQ>(t, l);
-           sums.put(p, 0, t, l);
-           float kk[KQ], sp[KQ];
-           ts_read<KQ>(sb, kk);
-           const int ic = n - 1 - i;  // the token's place in the chunk
-#pragma unroll
-           for (int j = 0; j < KQ; ++j) {
-             sp[j] = scw[((int64_t)ic * KQ + j) * TS_THREADS];
-             G[j] = fmaf(-gr, kk[j], G[j]);
-             t[j] = -sp[j] * gr;
-           }
-           ts_rows_rs<KQ>(t, l);
-           sums.put(p, 1, t, l);
-           float e[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-           for (int j = 0; j < KQ; ++j) e[j & 3] = fmaf(G[j], sp[j], e[j & 3]);
-           const float gl = wave_sum64((e[0] + e[1]) + (e[2] + e[3]));
-           if (l == 0) sums.sca[p][wave_id()] = gl;
-#pragma unroll
-           for (int j = 0; j < KQ; ++j) G[j] *= a;
-           prev = tok;
-         });
-    flush((par - 1) & 1);
+    }
   }
   // G is now the gradient of the state before the first token: the initial state's
   if (dh0 && on) {
@@ -334,6 +422,7 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_bwd_kernel(
 // ---------------------------------------------------------------------------------------------------------
 bool token_scan_supported(int K) { return K == 64 || K == 128; }
 int token_scan_ct() { return TS_CT; }
+size_t token_scan_scratch_floats(int K) { return (size_t)(TS_CT / TS_GS) * K * TS_ROWS; }
 
 template <int K>
 static hipError_t token_scan_k(const TokenScanArgs& a, bool backward) {
