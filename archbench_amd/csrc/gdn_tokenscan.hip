@@ -27,8 +27,8 @@ constexpr int TS_CT = 32;                    // tokens between checkpoints
 constexpr int TS_GS = 4;                     // tokens per group of the backward (decayed states held in registers)
 constexpr int TS_PF = 4;                     // tokens in flight: a token's loads are issued TS_PF tokens ahead
 constexpr int TS_ROWS = 64;                  // state rows per workgroup
-constexpr int TS_LPR = 8;                    // lanes per row
-constexpr int TS_LB = 3;                     // log2 TS_LPR
+constexpr int TS_LB = 3;                     // log2 of the lanes per row (16 lanes: slower, spills)
+constexpr int TS_LPR = 1 << TS_LB;          // lanes per row
 constexpr int TS_THREADS = TS_LPR * TS_ROWS;
 constexpr int TS_WAVES = TS_THREADS / 64;    // each wave holds 64 / TS_LPR rows
 
@@ -47,15 +47,18 @@ __device__ __forceinline__ int ts_vector_zero() {
   return z;
 }
 
-// sum over the eight lanes of a row, left in each of them: quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror
-// (lane p <- 7 - p) adds the other quad
+// sum over the lanes of a row, left in each of them: quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror (lane
+// p <- 7 - p) adds the other quad of an 8-lane group and row_mirror (p <- 15 - p) the other half of a 16-lane row
 __device__ __forceinline__ float ts_row_sum(float x) {
-  return dpp_sum_step<0x141>(dpp_sum_step<0x4e>(dpp_sum_step<0xb1>(x)));
+  x = dpp_sum_step<0x4e>(dpp_sum_step<0xb1>(x));
+  if constexpr (TS_LB >= 3) x = dpp_sum_step<0x141>(x);
+  if constexpr (TS_LB >= 4) x = dpp_sum_step<0x140>(x);
+  return x;
 }
 
-// Reduce-scatter over a wave's 8 rows: N values per lane (its part's local columns), summed over the 8 lanes that
-// share l & 7 (lane bits 3..5).  Lane l ends with the sums of local columns m + (N / 8) (l >> 3), m < N / 8, in
-// a[0 .. N / 8).  Each round pairs lanes that differ in one bit and hold the same column set: one keeps the lower
+// Reduce-scatter over a wave's 64 / TS_LPR rows: N values per lane (its part's local columns), summed over the lanes
+// that share l & (TS_LPR - 1) (lane bits TS_LB .. 5).  With R = N TS_LPR / 64, lane l ends with the sums of local
+// columns m + R (l >> TS_LB), m < R, in a[0 .. R).  Each round pairs lanes that differ in one bit and hold the same column set: one keeps the lower
 // half of its set, the other the upper half, and each adds what its partner sends.
 template <int N>
 __device__ __forceinline__ void ts_rows_rs(float (&a)[N], int l) {
@@ -66,12 +69,14 @@ __device__ __forceinline__ void ts_rows_rs(float (&a)[N], int l) {
     const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[m]), __float_as_uint(a[m + N / 2]), false, false);
     a[m] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
   }
+  if constexpr (TS_LB > 4) return;
   // bit 4: the same with v_permlane16_swap between even and odd 16-lane rows
 #pragma unroll
   for (int m = 0; m < N / 4; ++m) {
     const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[m]), __float_as_uint(a[m + N / 4]), false, false);
     a[m] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
   }
+  if constexpr (TS_LB > 3) return;
   // bit 3: row_ror:8 pairs lanes p and p ^ 8 of a 16-lane row
   const int b3 = (l >> 3) & 1;
 #pragma unroll
@@ -113,7 +118,7 @@ __device__ __forceinline__ void ts_read(const float* p, float (&o)[KQ]) {
   }
 }
 
-// grid B * H * NB (NB = ceil(V / 64)) workgroups of 512 threads: workgroup x -> (b h, row block vb)
+// grid B * H * NB (NB = ceil(V / 64)) workgroups of TS_THREADS (512) threads: workgroup x -> (b h, row block vb)
 template <int K>
 __global__ __launch_bounds__(TS_THREADS) void token_scan_fwd_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ u, const float* __restrict__ v,
@@ -211,23 +216,35 @@ struct TokSums {
   // this wave's reduce-scattered sums of local columns (quarter qd) into vector slot s
   template <int KQ>
   __device__ __forceinline__ void put(int par, int s, const float (&a)[KQ], int l) {
-    const int w = wave_id(), c0 = (l & (TS_LPR - 1)) * KQ + (KQ / 8) * (l >> TS_LB);
+    constexpr int R = KQ * TS_LPR / 64;
+    const int w = wave_id(), c0 = (l & (TS_LPR - 1)) * KQ + R * (l >> TS_LB);
 #pragma unroll
-    for (int m = 0; m < KQ / 8; ++m) col[par][s][w][c0 + m] = a[m];
+    for (int m = 0; m < R; ++m) col[par][s][w][c0 + m] = a[m];
+  }
+  // the waves' values added as a pairwise tree (a fixed order)
+  template <typename F>
+  static __device__ __forceinline__ float tree(F&& x) {
+    float a[TS_WAVES];
+#pragma unroll
+    for (int w = 0; w < TS_WAVES; ++w) a[w] = x(w);
+#pragma unroll
+    for (int h = TS_WAVES / 2; h >= 1; h /= 2) {
+#pragma unroll
+      for (int w = 0; w < h; ++w) a[w] = a[2 * w] + a[2 * w + 1];
+    }
+    return a[0];
   }
   __device__ __forceinline__ float col_sum(int par, int s, int c) const {
-    const float(&x)[TS_WAVES][K] = col[par][s];
-    return ((x[0][c] + x[1][c]) + (x[2][c] + x[3][c])) + ((x[4][c] + x[5][c]) + (x[6][c] + x[7][c]));
+    return tree([&](int w) { return col[par][s][w][c]; });
   }
   __device__ __forceinline__ float sca_sum(int par) const {
-    return ((sca[par][0] + sca[par][1]) + (sca[par][2] + sca[par][3])) +
-           ((sca[par][4] + sca[par][5]) + (sca[par][6] + sca[par][7]));
+    return tree([&](int w) { return sca[par][w]; });
   }
 };
-static_assert(TS_WAVES == 8 && TS_LPR == 1 << TS_LB, "the LDS sums add eight waves");
+static_assert(TS_LB >= 3 && TS_LB <= 4, "row sums and reduce-scatter rounds cover 8 or 16 lanes per row");
 static_assert(TS_GS % TS_PF == 0, "a backward pass's steps come in whole rings");
 
-// Partials: gqp, gup, gkp [NB][B*T*H][K], glap [NB][B*T*H]; sc [B*H*NB][TS_CT / TS_GS][K / 8][512] scratch of the
+// Partials: gqp, gup, gkp [NB][B*T*H][K], glap [NB][B*T*H]; sc [B*H*NB][TS_CT / TS_GS][K / TS_LPR][TS_THREADS] scratch of the
 // chunk's group-start states.
 // Per chunk (last first), in groups of TS_GS tokens: a forward pass from the checkpoint stores the state entering each
 // group but the first and last (the last stays in registers); then, group by group from the last, the group's tokens
