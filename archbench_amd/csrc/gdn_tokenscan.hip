@@ -87,14 +87,13 @@ __device__ __forceinline__ void ts_rows_rs(float (&a)[N], int l) {
 }
 
 // A token's k, u, q in LDS: per vector eight blocks of K / 8 floats, each padded by 4 so that the eight lanes of a
-// row (one per block) read different banks with 16-byte reads.  Threads below 3 K / 4 (or the K / 4 of u alone)
-// each load one float4 of a token TS_PF tokens ahead of the one computing (a ring of registers, so that a load has
-// TS_PF tokens' time to arrive) and store it here one token ahead.
+// row (one per block) read different banks with 16-byte reads.  Piece p < 3 K / 4 of a token (or one of the K / 4
+// pieces of u alone) is one float4, loaded into a register well ahead of its token and stored here before it.
 template <int K>
 struct TokStage {
   static constexpr int KQ = K / TS_LPR, K4 = K / 4, LD = KQ + 4, VEC = TS_LPR * LD, SIZE = 3 * VEC;
   static __device__ __forceinline__ void load(const float* kp, const float* up, const float* qp, int64_t t, int tid,
-                                              bool kq, f32x4& x) {
+                                              bool kq, f32x4& x) {  // tid: the piece
     const int vec = tid / K4, e4 = tid - vec * K4;
     if (kq ? tid < 3 * K4 : vec == 1) {
       const float* src = vec == 0 ? kp : vec == 1 ? up : qp;
@@ -118,6 +117,11 @@ __device__ __forceinline__ void ts_read(const float* p, float (&o)[KQ]) {
   }
 }
 
+// Tokens per block of the forward: a block's k, u, q are staged through LDS together (loaded a block ahead), so the
+// workgroup meets at one barrier per block and its waves run through the block's tokens unsynchronised.
+constexpr int TS_TB = 8;
+static_assert(TS_CT % TS_TB == 0, "checkpoints fall on block starts");
+
 // grid B * H * NB (NB = ceil(V / 64)) workgroups of TS_THREADS (512) threads: workgroup x -> (b h, row block vb)
 template <int K>
 __global__ __launch_bounds__(TS_THREADS) void token_scan_fwd_kernel(
@@ -125,8 +129,8 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_fwd_kernel(
     const float* __restrict__ la, const float* __restrict__ h0, float* __restrict__ y, float* __restrict__ r,
     float* __restrict__ st, float* __restrict__ hT, int T_, int H, int V, int NCH, int NB) {
   using TS = TokStage<K>;
-  constexpr int KQ = TS::KQ;
-  __shared__ __attribute__((aligned(16))) float sv[2][TS::SIZE];
+  constexpr int KQ = TS::KQ, PER = 3 * TS::K4, NL = (TS_TB * PER + TS_THREADS - 1) / TS_THREADS;
+  __shared__ __attribute__((aligned(16))) float sv[2][TS_TB][TS::SIZE];
   const int tid = threadIdx.x, l = lane_id(), qd = l & (TS_LPR - 1);
   const int pid = blockIdx.x, bh = pid / NB, vb = pid - bh * NB;
   const int b = bh / H, h = bh - b * H;
@@ -140,43 +144,49 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_fwd_kernel(
   for (int j = 0; j < KQ; ++j) S[j] = h0 && on ? h0[cb + (int64_t)j * V] : 0.f;
   float* stb = st + (int64_t)bh * NCH * K * V + (int64_t)qd * KQ * V + vi;
   const int64_t tok_first = (int64_t)b * T_ * H + h;
-  // token t's vectors and row values in ring slot t % TS_PF
-  f32x4 xr[TS_PF];
-  float vr[TS_PF], lr[TS_PF];
+  // block t0's vectors: thread piece e < TS_TB * PER is float4 e % PER (k, u, q in order) of token t0 + e / PER
+  f32x4 xr[NL];
+  float vn[TS_TB], ln[TS_TB];  // the next block's v (this row) and la, loaded a block ahead
   const int zv = ts_vector_zero();
-  auto load_tok = [&](int t, int sl) {
-    const int64_t tk = tok_first + (int64_t)t * H;
-    TS::load(k, u, q, tk, tid, true, xr[sl]);
-    vr[sl] = v[tk * V + vc];
-    lr[sl] = la[tk + zv];
+  auto load_block = [&](int t0) {
+#pragma unroll
+    for (int m = 0; m < NL; ++m) {
+      const int e = tid + m * TS_THREADS, i = e / PER, rem = e - i * PER;
+      if (e < TS_TB * PER && t0 + i < T_) TS::load(k, u, q, tok_first + (int64_t)(t0 + i) * H, rem, true, xr[m]);
+    }
+#pragma unroll
+    for (int i = 0; i < TS_TB; ++i) {
+      const int64_t tk = tok_first + (int64_t)min(t0 + i, T_ - 1) * H;
+      vn[i] = v[tk * V + vc];
+      ln[i] = la[tk + zv];
+    }
   };
+  auto stage_block = [&](float (*dst)[TS::SIZE]) {
 #pragma unroll
-  for (int s = 0; s < TS_PF; ++s)
-    if (s < T_) load_tok(s, s);  // T_ >= 1 here (the host returns before launching an empty scan)
-  TS::stage(sv[0], tid, true, xr[0]);
-  float nv = vr[0], nla = lr[0];
-  if (TS_PF < T_) load_tok(TS_PF, 0);
+    for (int m = 0; m < NL; ++m) {
+      const int e = tid + m * TS_THREADS, i = e / PER, rem = e - i * PER;
+      if (e < TS_TB * PER) TS::stage(dst[i], rem, true, xr[m]);
+    }
+  };
+  float vcur[TS_TB], lcur[TS_TB];
+  load_block(0);  // T_ >= 1 here (the host returns before launching an empty scan)
+  stage_block(sv[0]);
+#pragma unroll
+  for (int i = 0; i < TS_TB; ++i) vcur[i] = vn[i], lcur[i] = ln[i];
+  if (TS_TB < T_) load_block(TS_TB);
   ts_barrier();
-  for (int t0 = 0; t0 < T_; t0 += TS_PF) {
+  for (int t0 = 0, blk = 0; t0 < T_; t0 += TS_TB, ++blk) {
+    if (t0 % TS_CT == 0 && on) {
+      const int64_t c = t0 / TS_CT;
 #pragma unroll
-    for (int s = 0; s < TS_PF; ++s) {
-      const int t = t0 + s;
-      if (t >= T_) break;
-      const int64_t tok = tok_first + (int64_t)t * H;
-      if (t % TS_CT == 0 && on) {
-        const int64_t c = t / TS_CT;
+      for (int j = 0; j < KQ; ++j) stb[(c * K + j) * V] = S[j];
+    }
 #pragma unroll
-        for (int j = 0; j < KQ; ++j) stb[(c * K + j) * V] = S[j];
-      }
-      const float vcur = nv, a = expf(nla);
-      if (t + 1 < T_) {  // stage the next token from its slot, and load the token TS_PF after it there
-        const int sl = (s + 1) % TS_PF;
-        TS::stage(sv[(t + 1) & 1], tid, true, xr[sl]);
-        nv = vr[sl];
-        nla = lr[sl];
-        if (t + 1 + TS_PF < T_) load_tok(t + 1 + TS_PF, sl);
-      }
-      const float* sk = sv[t & 1] + qd * TS::LD;
+    for (int i = 0; i < TS_TB; ++i) {
+      if (t0 + i >= T_) break;
+      const int64_t tok = tok_first + (int64_t)(t0 + i) * H;
+      const float a = expf(lcur[i]);
+      const float* sk = sv[blk & 1][i] + qd * TS::LD;
       float kk[KQ];
       ts_read<KQ>(sk, kk);
       float d[4] = {0.f, 0.f, 0.f, 0.f};
@@ -185,7 +195,7 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_fwd_kernel(
         S[j] *= a;
         d[j & 3] = fmaf(S[j], kk[j], d[j & 3]);
       }
-      const float rr = vcur - ts_row_sum((d[0] + d[1]) + (d[2] + d[3]));
+      const float rr = vcur[i] - ts_row_sum((d[0] + d[1]) + (d[2] + d[3]));
       float uu[KQ], qq[KQ];
       ts_read<KQ>(sk + TS::VEC, uu);
       ts_read<KQ>(sk + 2 * TS::VEC, qq);
@@ -198,8 +208,14 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_fwd_kernel(
       const float yy = ts_row_sum((e[0] + e[1]) + (e[2] + e[3]));
       if (on && qd == 0) r[tok * V + vi] = rr;
       if (on && qd == 1) y[tok * V + vi] = yy;
-      ts_barrier();  // this token's vectors read by every lane; the next token's staged
     }
+    if (t0 + TS_TB < T_) {  // stage the next block (loaded a block ago), load the one after it
+      stage_block(sv[(blk + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < TS_TB; ++i) vcur[i] = vn[i], lcur[i] = ln[i];
+      if (t0 + 2 * TS_TB < T_) load_block(t0 + 2 * TS_TB);
+    }
+    ts_barrier();  // the block's vectors read by every lane; the next block's staged
   }
   if (hT && on) {
 #pragma unroll
