@@ -25,7 +25,6 @@ namespace gdn {
 
 constexpr int TS_CT = 32;                    // tokens between checkpoints
 constexpr int TS_GS = 4;                     // tokens per group of the backward (decayed states held in registers)
-constexpr int TS_PF = 4;                     // tokens in flight: a token's loads are issued TS_PF tokens ahead
 constexpr int TS_ROWS = 64;                  // state rows per workgroup
 constexpr int TS_LB = 3;                     // log2 of the lanes per row (16 lanes: slower, spills)
 constexpr int TS_LPR = 1 << TS_LB;          // lanes per row
@@ -223,19 +222,20 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_fwd_kernel(
   }
 }
 
-// The per-token sums over the workgroup's rows: each wave's column sums (after ts_rows_rs) and its dla go to LDS,
-// and the step after (behind the token's barrier) adds the four waves in order and stores the partial row.
+// The row sums of a group's steps: each wave's column sums (after ts_rows_rs) and its dla go to LDS slots of their
+// own (vector, token), and after the group's barrier the eight waves are added in a fixed order and stored as the
+// workgroup's partial rows (double-buffered by group parity).
 template <int K>
 struct TokSums {
-  float col[2][2][TS_WAVES][K];  // [parity][vector][wave][column]
-  float sca[2][TS_WAVES];        // [parity][wave]
-  // this wave's reduce-scattered sums of local columns (quarter qd) into vector slot s
+  float col[2][3][TS_GS][TS_WAVES][K];  // [parity][dq, du, dk][token][wave][column]
+  float sca[2][TS_GS][TS_WAVES];        // [parity][token][wave]: dla
+  // this wave's reduce-scattered sums of local columns (part l & (TS_LPR - 1)) into slot (vec, i)
   template <int KQ>
-  __device__ __forceinline__ void put(int par, int s, const float (&a)[KQ], int l) {
+  __device__ __forceinline__ void put(int par, int vec, int i, const float (&a)[KQ], int l) {
     constexpr int R = KQ * TS_LPR / 64;
     const int w = wave_id(), c0 = (l & (TS_LPR - 1)) * KQ + R * (l >> TS_LB);
 #pragma unroll
-    for (int m = 0; m < R; ++m) col[par][s][w][c0 + m] = a[m];
+    for (int m = 0; m < R; ++m) col[par][vec][i][w][c0 + m] = a[m];
   }
   // the waves' values added as a pairwise tree (a fixed order)
   template <typename F>
@@ -250,23 +250,23 @@ struct TokSums {
     }
     return a[0];
   }
-  __device__ __forceinline__ float col_sum(int par, int s, int c) const {
-    return tree([&](int w) { return col[par][s][w][c]; });
+  __device__ __forceinline__ float col_sum(int par, int vec, int i, int c) const {
+    return tree([&](int w) { return col[par][vec][i][w][c]; });
   }
-  __device__ __forceinline__ float sca_sum(int par) const {
-    return tree([&](int w) { return sca[par][w]; });
+  __device__ __forceinline__ float sca_sum(int par, int i) const {
+    return tree([&](int w) { return sca[par][i][w]; });
   }
 };
 static_assert(TS_LB >= 3 && TS_LB <= 4, "row sums and reduce-scatter rounds cover 8 or 16 lanes per row");
-static_assert(TS_GS % TS_PF == 0, "a backward pass's steps come in whole rings");
 
-// Partials: gqp, gup, gkp [NB][B*T*H][K], glap [NB][B*T*H]; sc [B*H*NB][TS_CT / TS_GS][K / TS_LPR][TS_THREADS] scratch of the
-// chunk's group-start states.
+// Partials: gqp, gup, gkp [NB][B*T*H][K], glap [NB][B*T*H]; sc [B*H*NB][TS_CT / TS_GS][K / TS_LPR][TS_THREADS] scratch of
+// the chunk's group-start states.
 // Per chunk (last first), in groups of TS_GS tokens: a forward pass from the checkpoint stores the state entering each
 // group but the first and last (the last stays in registers); then, group by group from the last, the group's tokens
 // are recomputed forward from its start state with each decayed state e^{la} S_{t-1} kept in registers (and dq
 // accumulated), and walked backward.  A short last group is padded with identity tokens (la = 0, zero vectors and
-// row values), which change neither S nor G, and whose sums are not stored.
+// row values), which change neither S nor G, and whose sums are not stored.  Both passes stage a group's vectors
+// through LDS (and load its row values) a group ahead: one barrier per group.
 template <int K>
 __global__ __launch_bounds__(TS_THREADS) void token_scan_bwd_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ u, const float* __restrict__ la,
@@ -275,8 +275,9 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_bwd_kernel(
     float* __restrict__ gkp, float* __restrict__ glap, float* __restrict__ dh0, float* __restrict__ sc, int T_, int H,
     int V, int NCH, int NB, int64_t ntok) {
   using TS = TokStage<K>;
-  constexpr int KQ = TS::KQ, NGS = TS_CT / TS_GS;
-  __shared__ __attribute__((aligned(16))) float sv[2][TS::SIZE];
+  constexpr int KQ = TS::KQ, NGS = TS_CT / TS_GS, PER = 3 * TS::K4;
+  static_assert(TS_GS * PER <= TS_THREADS, "one piece of a group's vectors per thread");
+  __shared__ __attribute__((aligned(16))) float sv[2][TS_GS][TS::SIZE];
   __shared__ TokSums<K> sums;
   const int tid = threadIdx.x, l = lane_id(), qd = l & (TS_LPR - 1);
   const int pid = blockIdx.x, bh = pid / NB, vb = pid - bh * NB;
@@ -285,42 +286,34 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_bwd_kernel(
   const bool on = vi < V;
   const float* stb = st + (int64_t)bh * NCH * K * V + (int64_t)qd * KQ * V + vi;
   float* scw = sc + (int64_t)pid * NGS * KQ * TS_THREADS + tid;
-  float* gq_b = gqp + (int64_t)vb * ntok * K;
-  float* gu_b = gup + (int64_t)vb * ntok * K;
-  float* gk_b = gkp + (int64_t)vb * ntok * K;
+  float* const gout[3] = {gqp + (int64_t)vb * ntok * K, gup + (int64_t)vb * ntok * K, gkp + (int64_t)vb * ntok * K};
   float* gl_b = glap + (int64_t)vb * ntok;
-  // a step's vectors and row values in ring slot f % TS_PF (f: the step within its pass)
-  f32x4 xr[TS_PF];
-  float lr[TS_PF], rr[TS_PF], yr[TS_PF];
-  float nla = 0.f, nr = 0.f, ngy = 0.f;  // the next step's row values
   const int zv = ts_vector_zero();
-  // token tok, or an identity token (tok < 0: zero vectors and row values, la = 0), into slot sl
-  auto ld = [&](int64_t tok, int sl, bool kq) {
-    if (tok >= 0) TS::load(k, u, q, tok, tid, kq, xr[sl]);
-    else xr[sl] = f32x4{0.f, 0.f, 0.f, 0.f};
-    lr[sl] = tok >= 0 ? la[tok + zv] : 0.f;
-    rr[sl] = tok >= 0 && on ? r[tok * V + vi] : 0.f;
-    yr[sl] = tok >= 0 && on ? gy[tok * V + vi] : 0.f;
-  };
-  int par = 0;  // parity of the step: sv[par & 1] holds its vectors, sums[par & 1] takes its row sums
-  // Steps f = 0 .. nf of a pass over tokens tok_at(f): the first TS_PF loaded and the first staged before the first
-  // barrier; then each step stages step f + 1 from its slot (sl = (f + 1) % TS_PF) and loads step f + 1 + TS_PF there.
-  auto prologue = [&](int nf, bool kq, auto&& tok_at) {
+  const int pi = tid / PER, prem = tid - pi * PER;  // this thread's piece of a group's vectors: token pi, piece prem
+  f32x4 xr;                                         // ... of the next group, loaded a group ahead
+  float nla[TS_GS], nr[TS_GS], ngy[TS_GS];          // the next group's row values
+  float cla[TS_GS], cr[TS_GS], cgy[TS_GS];          // the current group's
+  // a group's tokens tok_at(i), i < TS_GS (tok < 0: an identity token); kq: k, q and dy too (else u and r alone)
+  auto load_grp = [&](auto&& tok_at, bool kq) {
+    if (pi < TS_GS) {
+      const int64_t tk = tok_at(pi);
+      if (tk >= 0) TS::load(k, u, q, tk, prem, kq, xr);
+      else xr = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
-    for (int s = 0; s < TS_PF; ++s)
-      if (s < nf) ld(tok_at(s), s, kq);
-    TS::stage(sv[par & 1], tid, kq, xr[0]);
-    nla = lr[0], nr = rr[0], ngy = yr[0];
-    if (TS_PF < nf) ld(tok_at(TS_PF), 0, kq);
-    ts_barrier();
-  };
-  auto advance = [&](int f, int sl, int nf, bool kq, auto&& tok_at) {
-    if (f + 1 < nf) {
-      TS::stage(sv[(par + 1) & 1], tid, kq, xr[sl]);
-      nla = lr[sl], nr = rr[sl], ngy = yr[sl];
-      if (f + 1 + TS_PF < nf) ld(tok_at(f + 1 + TS_PF), sl, kq);
+    for (int i = 0; i < TS_GS; ++i) {
+      const int64_t tk = tok_at(i);
+      nla[i] = tk >= 0 ? la[tk + zv] : 0.f;
+      nr[i] = tk >= 0 && on ? r[tk * V + vi] : 0.f;
+      ngy[i] = tk >= 0 && on && kq ? gy[tk * V + vi] : 0.f;
     }
   };
+  auto stage_grp = [&](int buf, bool kq) {
+    if (pi < TS_GS) TS::stage(sv[buf][pi], prem, kq, xr);
+#pragma unroll
+    for (int i = 0; i < TS_GS; ++i) cla[i] = nla[i], cr[i] = nr[i], cgy[i] = ngy[i];
+  };
+  int par = 0;  // parity of the group: sv[par & 1] holds its vectors, sums[par & 1] takes its row sums
   const int64_t cb = (int64_t)bh * K * V + (int64_t)qd * KQ * V + vi;  // [B, H, K, V] states, as in the forward
   float G[KQ], S[KQ];
 #pragma unroll
@@ -328,42 +321,63 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_bwd_kernel(
   for (int c = NCH - 1; c >= 0; --c) {
     const int n = min(TS_CT, T_ - c * TS_CT), ng = (n + TS_GS - 1) / TS_GS;
     const int64_t tok0 = ((int64_t)b * T_ + (int64_t)c * TS_CT) * H + h;
+    auto tok_in = [&](int g, int i) -> int64_t {
+      const int t = g * TS_GS + i;
+      return t < n ? tok0 + (int64_t)t * H : -1;
+    };
 #pragma unroll
     for (int j = 0; j < KQ; ++j) S[j] = on ? stb[((int64_t)c * K + j) * V] : 0.f;
     // forward from the checkpoint to the last group's start, storing the start states of groups 1 .. ng - 2
-    const int na = (ng - 1) * TS_GS;
-    if (na > 0) {
-      auto tok_a = [&](int f) { return tok0 + (int64_t)f * H; };
-      prologue(na, false, tok_a);
-      for (int f0 = 0; f0 < na; f0 += TS_PF) {
+    if (ng > 1) {
+      load_grp([&](int i) { return tok_in(0, i); }, false);
+      stage_grp(par & 1, false);
+      if (ng > 2) load_grp([&](int i) { return tok_in(1, i); }, false);
+      ts_barrier();
+      for (int g = 0; g < ng - 1; ++g, ++par) {
+        const int p = par & 1;
+        if (g > 0) {
 #pragma unroll
-        for (int s = 0; s < TS_PF; ++s, ++par) {
-          const int f = f0 + s;
-          const float a = expf(nla), rc = nr;
-          advance(f, (s + 1) % TS_PF, na, false, tok_a);
-          float uu[KQ];
-          ts_read<KQ>(sv[par & 1] + TS::VEC + qd * TS::LD, uu);
-#pragma unroll
-          for (int j = 0; j < KQ; ++j) S[j] = fmaf(rc, uu[j], S[j] * a);
-          if ((f + 1) % TS_GS == 0 && f + 1 < na) {
-#pragma unroll
-            for (int j = 0; j < KQ; ++j) scw[((int64_t)((f + 1) / TS_GS) * KQ + j) * TS_THREADS] = S[j];
-          }
-          ts_barrier();
+          for (int j = 0; j < KQ; ++j) scw[((int64_t)g * KQ + j) * TS_THREADS] = S[j];
         }
+#pragma unroll
+        for (int i = 0; i < TS_GS; ++i) {
+          float uu[KQ];
+          ts_read<KQ>(sv[p][i] + TS::VEC + qd * TS::LD, uu);
+          const float a = expf(cla[i]);
+#pragma unroll
+          for (int j = 0; j < KQ; ++j) S[j] = fmaf(cr[i], uu[j], S[j] * a);
+        }
+        if (g + 1 < ng - 1) {
+          stage_grp((par + 1) & 1, false);
+          if (g + 2 < ng - 1) load_grp([&](int i) { return tok_in(g + 2, i); }, false);
+        }
+        ts_barrier();
       }
     }
     // groups last to first: TS_GS forward steps (tokens 0 .. TS_GS - 1 of the group), then TS_GS backward steps
-    const int nf = 2 * TS_GS * ng;
-    auto tok_b = [&](int f) -> int64_t {
-      const int g = ng - 1 - f / (2 * TS_GS), s = f % (2 * TS_GS);
-      const int i = g * TS_GS + (s < TS_GS ? s : 2 * TS_GS - 1 - s);
-      return i < n ? tok0 + (int64_t)i * H : -1;
+    auto flush = [&](int g, int pb) {  // the group's row sums, from LDS slots of parity pb
+#pragma unroll
+      for (int m = 0; m < (3 * TS_GS * K + TS_THREADS - 1) / TS_THREADS; ++m) {
+        const int o = tid + m * TS_THREADS;
+        if (o < 3 * TS_GS * K) {
+          const int vec = o / (TS_GS * K), rem = o - vec * TS_GS * K, i = rem / K, cc = rem - i * K;
+          const int64_t tk = tok_in(g, i);
+          if (tk >= 0) gout[vec][tk * K + cc] = sums.col_sum(pb, vec, i, cc);
+        }
+      }
+      if (tid < TS_GS) {
+        const int64_t tk = tok_in(g, tid);
+        if (tk >= 0) gl_b[tk] = sums.sca_sum(pb, tid);
+      }
     };
-    prologue(nf, true, tok_b);
-    int64_t prev = -1;  // the token whose row sums wait in LDS (-1: none, or an identity token)
-    for (int g = ng - 1; g >= 0; --g) {
+    load_grp([&](int i) { return tok_in(ng - 1, i); }, true);
+    stage_grp(par & 1, true);
+    if (ng > 1) load_grp([&](int i) { return tok_in(ng - 2, i); }, true);
+    ts_barrier();
+    for (int g = ng - 1; g >= 0; --g, ++par) {
+      const int p = par & 1;
       if (g < ng - 1) {
+        flush(g + 1, p ^ 1);
         if (g == 0) {
 #pragma unroll
           for (int j = 0; j < KQ; ++j) S[j] = on ? stb[((int64_t)c * K + j) * V] : 0.f;
@@ -374,36 +388,23 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_bwd_kernel(
       }
       float Sd[TS_GS][KQ];  // e^{la} S_{t-1} of the group's tokens
 #pragma unroll
-      for (int s = 0; s < 2 * TS_GS; ++s, ++par) {
-        const int f = (ng - 1 - g) * 2 * TS_GS + s, p = par & 1;
-        const int64_t tok = tok_b(f);
-        const float a = expf(nla), rc = nr, gyc = ngy;
-        advance(f, (s + 1) % TS_PF, nf, true, tok_b);
-        // the previous step's sums: dq after a forward step, du, dk, dla after a backward one
-        if (prev >= 0) {
-          if (s >= 1 && s <= TS_GS) {
-            if (tid < K) gq_b[prev * K + tid] = sums.col_sum(p ^ 1, 0, tid);
-          } else {
-            if (tid < K) gu_b[prev * K + tid] = sums.col_sum(p ^ 1, 0, tid);
-            else if (tid < 2 * K) gk_b[prev * K + tid - K] = sums.col_sum(p ^ 1, 1, tid - K);
-            if (tid == 0) gl_b[prev] = sums.sca_sum(p ^ 1);
-          }
-        }
-        const float* sb = sv[p] + qd * TS::LD;
+      for (int s = 0; s < 2 * TS_GS; ++s) {
+        const int i = s < TS_GS ? s : 2 * TS_GS - 1 - s;
+        const float a = expf(cla[i]), rc = cr[i], gyc = cgy[i];
+        const float* sb = sv[p][i] + qd * TS::LD;
         float uu[KQ], t[KQ];
         ts_read<KQ>(sb + TS::VEC, uu);
         if (s < TS_GS) {
 #pragma unroll
           for (int j = 0; j < KQ; ++j) {
             S[j] *= a;
-            Sd[s][j] = S[j];
+            Sd[i][j] = S[j];
             S[j] = fmaf(rc, uu[j], S[j]);
             t[j] = S[j] * gyc;
           }
           ts_rows_rs<KQ>(t, l);
-          sums.put(p, 0, t, l);
+          sums.put(p, 0, i, t, l);
         } else {
-          const int i = 2 * TS_GS - 1 - s;
           float qq[KQ], kk[KQ];
           ts_read<KQ>(sb + 2 * TS::VEC, qq);
           float d[4] = {0.f, 0.f, 0.f, 0.f};
@@ -413,11 +414,12 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_bwd_kernel(
             d[j & 3] = fmaf(G[j], uu[j], d[j & 3]);
           }
           const float gr = ts_row_sum((d[0] + d[1]) + (d[2] + d[3]));
+          const int64_t tok = tok_in(g, i);
           if (on && qd == 0 && tok >= 0) gv[tok * V + vi] = gr;
 #pragma unroll
           for (int j = 0; j < KQ; ++j) t[j] = G[j] * rc;
           ts_rows_rs<KQ>(t, l);
-          sums.put(p, 0, t, l);
+          sums.put(p, 1, i, t, l);
           ts_read<KQ>(sb, kk);
 #pragma unroll
           for (int j = 0; j < KQ; ++j) {
@@ -425,25 +427,23 @@ __global__ __launch_bounds__(TS_THREADS) void token_scan_bwd_kernel(
             t[j] = -Sd[i][j] * gr;
           }
           ts_rows_rs<KQ>(t, l);
-          sums.put(p, 1, t, l);
+          sums.put(p, 2, i, t, l);
           float e[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int j = 0; j < KQ; ++j) e[j & 3] = fmaf(G[j], Sd[i][j], e[j & 3]);
           const float gl = wave_sum64((e[0] + e[1]) + (e[2] + e[3]));
-          if (l == 0) sums.sca[p][wave_id()] = gl;
+          if (l == 0) sums.sca[p][i][wave_id()] = gl;
 #pragma unroll
           for (int j = 0; j < KQ; ++j) G[j] *= a;
         }
-        prev = tok;
-        ts_barrier();  // this step's vectors read and sums written; the next step's vectors staged
       }
+      if (g > 0) {  // stage the group before (loaded a group ago), load the one before it
+        stage_grp((par + 1) & 1, true);
+        if (g > 1) load_grp([&](int i) { return tok_in(g - 2, i); }, true);
+      }
+      ts_barrier();  // the group's vectors read and sums written; the group before staged
     }
-    if (prev >= 0) {  // the chunk's first token (a backward step)
-      const int p = (par - 1) & 1;
-      if (tid < K) gu_b[prev * K + tid] = sums.col_sum(p, 0, tid);
-      else if (tid < 2 * K) gk_b[prev * K + tid - K] = sums.col_sum(p, 1, tid - K);
-      if (tid == 0) gl_b[prev] = sums.sca_sum(p);
-    }
+    flush(0, (par - 1) & 1);
   }
   // G is now the gradient of the state before the first token: the initial state's
   if (dh0 && on) {
