@@ -2,8 +2,8 @@
 oracle's token recurrence (oracle/nsgdn_oracle.py::recurrent_fwd / recurrent_bwd, fp64 on the CPU): y and every
 gradient (dq, dk, du, dv, dla) at fp32 accuracy -- max-abs error <= 1e-4 for y and rel-L2 <= 1e-6 for y and each
 gradient, the achieved errors printed -- over K in {64, 128}, V below, at and above one 64-row block (96: a
-partial block), T around the 32-token checkpoint interval and the backward's 4-token groups (1, 31, 32, 33, 45, 100),
-B and H > 1."""
+partial block), T around the 32-token checkpoint interval and the backward's 4-token groups (1, 31, 32, 33, 45, 100)
+and over 32 checkpoint chunks (1024), B and H > 1."""
 
 import pytest
 import torch
@@ -34,6 +34,7 @@ CASES = [  # B, T, H, K, V
     (1, 31, 2, 64, 96),
     (3, 1, 2, 128, 64),
     (1, 45, 2, 64, 64),
+    (1, 1024, 1, 128, 64),
 ]
 
 
