@@ -4,9 +4,10 @@
 //     S <- e^{la_t} S;   r_t = v_t - S k_t;   S <- S + r_t u_t^T;   y_t = S q_t.
 // Rows of S are independent given the token stream.  A workgroup of eight waves owns 64 rows; eight lanes share a
 // row, lane part l & 7 holding K / 8 of its entries in registers, so a row's dot products (S k, S q, G u) are a
-// partial sum per lane and three DPP steps inside the 8-lane group.  k, u, q of a token are workgroup-uniform and reach the
-// lanes through LDS (double-buffered: a token is staged while the one before it computes, one barrier per token).
-// Every CT tokens the forward stores S (the checkpoint the backward restarts from) in [K][V] order.
+// partial sum per lane and three DPP steps inside the 8-lane group.  k, u, q of a token are workgroup-uniform and
+// reach the lanes through LDS, staged a block of tokens at a time (double-buffered: the next block is staged while
+// one computes, one barrier per block).  Every CT tokens the forward stores S (the checkpoint the backward restarts
+// from) in [K][V] order.
 // The backward walks the checkpoints in reverse and each chunk in groups of four tokens, last first: it recomputes
 // a group's states forward from the state entering the group (stored by a forward pass over the chunk from its
 // checkpoint), keeping e^{la} S before each token's update in registers and accumulating dq = sum_rows S_t^T dy_t,
@@ -27,12 +28,12 @@ constexpr int TS_CT = 32;                    // tokens between checkpoints
 constexpr int TS_GS = 4;                     // tokens per group of the backward (decayed states held in registers)
 constexpr int TS_ROWS = 64;                  // state rows per workgroup
 constexpr int TS_LB = 3;                     // log2 of the lanes per row (16 lanes: slower, spills)
-constexpr int TS_LPR = 1 << TS_LB;          // lanes per row
+constexpr int TS_LPR = 1 << TS_LB;           // lanes per row
 constexpr int TS_THREADS = TS_LPR * TS_ROWS;
 constexpr int TS_WAVES = TS_THREADS / 64;    // each wave holds 64 / TS_LPR rows
 
-// The per-token barrier orders LDS only (the staged vectors and the row sums): __syncthreads() would also wait for
-// every global load in flight, the tokens prefetched ahead included, and so expose a memory latency per token.
+// The block / group barrier orders LDS only (the staged vectors and the row sums): __syncthreads() would also wait
+// for every global load in flight, the next block's included, and so expose a memory latency per barrier.
 __device__ __forceinline__ void ts_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
