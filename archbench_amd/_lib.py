@@ -6,6 +6,7 @@ The library is the only compute path: if it is missing, every op raises instead 
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import threading
 
@@ -112,26 +113,75 @@ def dtype_code(dt: torch.dtype) -> int:
 
 
 def ptr(t: torch.Tensor | None):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    # the argtypes are c_void_p: ctypes converts the integer address (and None -> NULL) itself
+    return None if t is None else t.data_ptr()
 
 
 def stream_ptr(device: torch.device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+# Workspaces (scratch that lives only for one call's kernels) are kept per (device, stream) and reused while large
+# enough, instead of a torch.empty per call: the library's kernels on one stream run in order, so a later call on
+# the same stream cannot overlap an earlier one's use.  A buffer that is too small is replaced (the caching
+# allocator reuses the old block on that stream only after the work queued there).  Under CUDA / HIP graph capture
+# every call allocates its own workspace from the graph's pool as before, so a captured graph never holds the
+# address of a cached buffer that a later call could replace.  The cache holds, per stream, the largest workspace
+# requested so far until the process ends (or release_workspaces()).
+_ws_cache: dict = {}
+_ws_lock = threading.Lock()
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A uint8 device buffer of at least nbytes for one call's kernels on the current stream of `device`."""
+    stream = torch.cuda.current_stream(device)
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+    key = (stream.device_index, stream.cuda_stream)
+    with _ws_lock:
+        buf = _ws_cache.get(key)
+        if buf is None or buf.numel() < nbytes:
+            _ws_cache.pop(key, None)
+            buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+            _ws_cache[key] = buf
+        return buf
+
+
+def release_workspaces() -> None:
+    """Drop the cached workspaces (their memory returns to PyTorch's caching allocator)."""
+    with _ws_lock:
+        _ws_cache.clear()
 
 
 def supported(op: str, K: int, V: int, dtype: torch.dtype) -> bool:
     return bool(load().gdn_supported({"chunk": 0, "step": 1}[op], K, V, dtype_code(dtype)))
 
 
-def ws_bytes(kind: str, B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype) -> int:
+# The size queries are pure functions of the shape and the device (the C side reads its CU count), so their results
+# are cached per device.
+@functools.lru_cache(maxsize=1024)
+def _ws_bytes(kind: str, B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype, dev: int) -> int:
     out = _sz(0)
     fn = load().gdn_chunk_fwd_ws_bytes if kind == "fwd" else load().gdn_chunk_bwd_ws_bytes
     check(fn(B, T, H, K, V, dtype_code(dtype), ctypes.byref(out)), f"gdn_chunk_{kind}_ws_bytes")
     return out.value
 
 
+def ws_bytes(kind: str, B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype) -> int:
+    return _ws_bytes(kind, B, T, H, K, V, dtype, _device_index())
+
+
+def _device_index() -> int:
+    return torch.cuda.current_device() if torch.cuda.is_available() else -1
+
+
 def stash_bytes(B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype) -> tuple[int, int]:
     """(stash bytes for gdn_chunk_fwd_stash, workspace bytes for gdn_chunk_bwd_stashed)."""
+    return _stash_bytes(B, T, H, K, V, dtype, _device_index())
+
+
+@functools.lru_cache(maxsize=1024)
+def _stash_bytes(B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype, dev: int) -> tuple[int, int]:
     st, ws = _sz(0), _sz(0)
     check(load().gdn_chunk_stash_bytes(B, T, H, K, V, dtype_code(dtype), ctypes.byref(st), ctypes.byref(ws)),
           "gdn_chunk_stash_bytes")

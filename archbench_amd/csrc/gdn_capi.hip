@@ -777,7 +777,7 @@ static int write_dir_check(int B, int T, int H, int K, int n_steps, int dtype) {
   if (B < 0 || T < 0 || H <= 0 || K <= 0) return fail(GDN_ERR_ARG, "invalid sizes B=%d T=%d H=%d K=%d", B, T, H, K);
   if (!write_dir_supported(K, n_steps))
     return fail(GDN_ERR_SHAPE, "write direction not compiled for K=%d n_steps=%d (K in {64, 128, 256}, "
-                "1 <= n_steps <= 8)", K, n_steps);
+                "n_steps >= 1)", K, n_steps);
   return GDN_OK;
 }
 
@@ -841,7 +841,8 @@ int gdn_token_scan_fwd(const float* q, const float* k, const float* u, const flo
   if (int e = gdn_token_scan_sizes(B, T, H, K, V, &need_st, &need_sc, &nb)) return e;
   if ((int64_t)B * T == 0) return GDN_OK;
   if (!q || !k || !u || !v || !la || !y || !r || !st) return fail(GDN_ERR_ARG, "null input/output pointer");
-  if (misaligned(h0, hT)) return fail(GDN_ERR_ARG, "state pointer not 16-byte aligned");
+  // q, k, u are read as 16-byte vectors, and so are the states
+  if (misaligned(q, k, u, h0, hT)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   if (st_bytes < need_st) return fail(GDN_ERR_WORKSPACE, "checkpoint buffer %zu bytes, need %zu", st_bytes, need_st);
   TokenScanArgs a{};
   a.q = q; a.k = k; a.u = u; a.v = v; a.la = la; a.h0 = h0; a.y = y; a.r = r; a.st = st; a.hT = hT;
@@ -862,7 +863,7 @@ int gdn_token_scan_bwd(const float* q, const float* k, const float* u, const flo
   if ((int64_t)B * T == 0) return GDN_OK;
   if (!q || !k || !u || !la || !r || !st || !dy || !dv || !dq_part || !du_part || !dk_part || !dla_part || !scratch)
     return fail(GDN_ERR_ARG, "null input/output pointer");
-  if (misaligned(dhT, dh0)) return fail(GDN_ERR_ARG, "state pointer not 16-byte aligned");
+  if (misaligned(q, k, u, dhT, dh0)) return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   if (st_bytes < need_st) return fail(GDN_ERR_WORKSPACE, "checkpoint buffer %zu bytes, need %zu", st_bytes, need_st);
   if (scratch_bytes < need_sc)
     return fail(GDN_ERR_WORKSPACE, "scratch %zu bytes, need %zu", scratch_bytes, need_sc);

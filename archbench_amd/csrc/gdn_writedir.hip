@@ -18,43 +18,40 @@
 namespace gdn {
 
 constexpr int WD_WAVES = 4;  // waves per workgroup
-constexpr int WD_NMAX = 8;   // largest n_steps compiled
 
-// Scalars of one row from its (k, p) dot products: a, b with u = a k + b p, and the recursion's c_i.
+// Scalars of one row from its (k, p) dot products: a, b with u = a k + b p, and what the backward needs of the
+// recursion.  With rho = 1 - x m the recursion is affine, c_{i+1} = rho c_i + x y, so the reverse-mode sums over
+// its n - 1 steps -- g_rho = gc F and g_xy = gc E with F = sum_{i=2..n} rho^(n-i) c_{i-1} and
+// E = sum_{i=2..n} rho^(n-i) -- are accumulated in the same forward loop (F <- rho F + c, E <- rho E + 1) that
+// builds c_n: any n_steps, no per-step storage.
 struct WdRow {
-  float s, m, x, y, c[WD_NMAX], a, b;
+  float s, m, x, y, c, F, E, a, b;
   __device__ __forceinline__ void build(float s_, float pp, float beta, float lam, int n) {
     s = s_;
     m = pp - s * s;
     x = lam * beta;
     y = beta * s;
-    c[0] = 0.f;
-#pragma unroll
-    for (int i = 1; i < WD_NMAX; ++i) c[i] = i < n ? c[i - 1] + x * (y - c[i - 1] * m) : c[i - 1];
-    const float cn = c[WD_NMAX - 1];
-    a = beta + cn * s;
-    b = -cn;
+    const float rho = 1.f - x * m;
+    c = 0.f;
+    F = 0.f;
+    E = 0.f;
+    for (int i = 1; i < n; ++i) {  // step c_{i+1} = c_i + x (y - c_i m)
+      F = rho * F + c;
+      E = rho * E + 1.f;
+      c = c + x * (y - c * m);
+    }
+    a = beta + c * s;
+    b = -c;
   }
   // Reverse pass from da = du . k, db = du . p: gradients w.r.t. beta, lam and the row's two dot products
-  __device__ __forceinline__ void grad(float da, float db, float beta, float lam, int n, float& dbeta, float& dlam,
+  __device__ __forceinline__ void grad(float da, float db, float beta, float lam, float& dbeta, float& dlam,
                                        float& ds, float& dpp) const {
-    const float cn = c[WD_NMAX - 1];
-    float gc = s * da - db, gx = 0.f, gy = 0.f, gm = 0.f;
-    ds = cn * da;
-    dbeta = da;
-#pragma unroll
-    for (int i = WD_NMAX - 1; i >= 1; --i) {
-      if (i < n) {  // step c_i = c_{i-1} + x (y - c_{i-1} m)
-        const float cp = c[i - 1];
-        gx += gc * (y - cp * m);
-        gy += gc * x;
-        gm -= gc * x * cp;
-        gc *= 1.f - x * m;
-      }
-    }
+    const float gc = s * da - db;           // dL/dc_n
+    const float grho = gc * F, gxy = gc * E;  // through rho = 1 - x m and the constant term x y
+    const float gx = y * gxy - m * grho, gy = x * gxy, gm = -x * grho;
     dlam = gx * beta;
-    dbeta += gx * lam + gy * s;
-    ds += gy * beta - 2.f * s * gm;
+    dbeta = da + gx * lam + gy * s;
+    ds = c * da + gy * beta - 2.f * s * gm;
     dpp = gm;
   }
 };
@@ -135,7 +132,7 @@ __global__ __launch_bounds__(64 * WD_WAVES) void write_dir_bwd_kernel(
   WdRow w;
   w.build(lane_group_sum<LPR>(s1), lane_group_sum<LPR>(s2), bt, lm, n);
   float db_, dl_, ds, dpp;
-  w.grad(lane_group_sum<LPR>(s3), lane_group_sum<LPR>(s4), bt, lm, n, db_, dl_, ds, dpp);
+  w.grad(lane_group_sum<LPR>(s3), lane_group_sum<LPR>(s4), bt, lm, db_, dl_, ds, dpp);
   float o[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) o[j] = w.a * gv[j] + ds * pv[j];
@@ -153,7 +150,7 @@ __global__ __launch_bounds__(64 * WD_WAVES) void write_dir_bwd_kernel(
     WdRow wn;
     wn.build(lane_group_sum<LPR>(n1), lane_group_sum<LPR>(n2), btn, lm, n);
     float dbn, dln, dsn, dppn;
-    wn.grad(lane_group_sum<LPR>(n3), lane_group_sum<LPR>(n4), btn, lm, n, dbn, dln, dsn, dppn);
+    wn.grad(lane_group_sum<LPR>(n3), lane_group_sum<LPR>(n4), btn, lm, dbn, dln, dsn, dppn);
     if (has_next) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[j] += wn.b * gn[j] + dsn * kn[j] + 2.f * dppn * kv[j];
@@ -170,7 +167,7 @@ __global__ __launch_bounds__(64 * WD_WAVES) void write_dir_bwd_kernel(
 
 // ---------------------------------------------------------------------------------------------------------
 bool write_dir_supported(int K, int n_steps) {
-  return (K == 64 || K == 128 || K == 256) && n_steps >= 1 && n_steps <= WD_NMAX;
+  return (K == 64 || K == 128 || K == 256) && n_steps >= 1;
 }
 
 template <typename T, int K>

@@ -37,21 +37,6 @@ from . import register
 from .gdn import _grouped_linear, _linear
 
 
-def write_direction(k: torch.Tensor, p: torch.Tensor, beta: torch.Tensor, lam: torch.Tensor,
-                    n_steps: int) -> torch.Tensor:
-    """u_1 = beta k; then n_steps - 1 steps u <- u - lam beta (p . u) p_perp, p_perp = p - (p . k) k
-    (nsgdn.py:61-75).  k, p [B,T,H,K]; beta [B,T,H]; lam [H].  The reference's function with an explicit p, in
-    PyTorch (any device); the mixer runs ops.write_direction, which takes p as the previous token's k."""
-    b = beta[..., None]
-    u = b * k
-    if n_steps > 1:
-        lb = lam[None, None, :, None] * b
-        p_perp = p - (p * k).sum(-1, keepdim=True) * k
-        for _ in range(n_steps - 1):
-            u = u - lb * (p * u).sum(-1, keepdim=True) * p_perp
-    return u
-
-
 class NStepGDN(nn.Module):
     def __init__(self, d_model: int, num_heads: int = 8, head_dim: int = 128, expand_v: float = 2.0,
                  n_steps: int = 2, lam: float = 1.0, use_gate: bool = True, use_short_conv: bool = True,
@@ -101,25 +86,32 @@ class NStepGDN(nn.Module):
         bounds = [0, n_qkv] + ([n_main] if self.n_gate else []) + [n_main + 2 * H]
         y, *g, ab = _grouped_linear(xp, self.in_proj.weight, bounds)
         g = g[0] if g else None
+        # the exact token scan takes fp32 q and k normalised after the conv, as the reference normalises the fp32
+        # copies of the conv output (nsgdn.py:525-528); the chunk path gets them normalised inside the conv
+        exact = self.scan_impl in ("triton", "ref") and DK in (64, 128)
         if self.conv is not None:
             # q, k, v convolved straight out of y (ops.mixer_input_stage; the taps used rounded to y's dtype, as
             # the reference's conv runs them)
-            q, k, v = ops.mixer_input_stage(y, self.conv.weight.squeeze(1), self.qk_dim, self.v_dim, DK)
+            q, k, v = ops.mixer_input_stage(y, self.conv.weight.squeeze(1), self.qk_dim, self.v_dim,
+                                            0 if exact else DK)
         else:
-            qs, ks, vs = torch.split(y, [self.qk_dim, self.qk_dim, self.v_dim], dim=-1)
-            q, k, v = ops.l2norm(qs, 1e-12, 1.0), ops.l2norm(ks, 1e-12, 1.0), vs
-        q, k, v = q.view(B, T, H, DK), k.view(B, T, H, DK), v.reshape(B, T, H, DV)
+            q, k, v = torch.split(y, [self.qk_dim, self.qk_dim, self.v_dim], dim=-1)
+        q, k, v = q.reshape(B, T, H, DK), k.reshape(B, T, H, DK), v.reshape(B, T, H, DV)
+        if not exact and self.conv is None:
+            q, k = ops.l2norm(q, 1e-12, 1.0), ops.l2norm(k, 1e-12, 1.0)
         la, beta = ops.gdn_gates_ab(ab, self.A_log, self.dt_bias, self.b_bias, 1.0,
                                  float("-inf") if self.la_min is None else float(self.la_min))
         gate = g.reshape(B, T, H, DV) if self.use_gate else None
         lam = F.softplus(self.lam.float())
         eps = self.norm.eps or 1e-5
-        if self.scan_impl in ("triton", "ref") and DK in (64, 128):
-            # the reference's exact fp32 token scan (nsgdn.py:525-536 with its "triton" / "ref" scan): u from fp32
-            # k, y fp32 through the norm, cast for o_proj as autocast casts the projection's input
-            kf = k.float()
+        if exact:
+            # the reference's exact fp32 token scan (nsgdn.py:525-536 with its "triton" / "ref" scan): q and k
+            # normalised in fp32 (q with the DK^-1/2 scale), u from fp32 k, y fp32 through the norm, cast for
+            # o_proj as autocast casts the projection's input
+            qf = ops.l2norm(q.float(), 1e-12, DK ** -0.5)
+            kf = ops.l2norm(k.float(), 1e-12, 1.0)
             u = ops.write_direction(kf, beta, lam, self.n_steps)
-            y = ops.nsgdn_scan(q.float() * DK ** -0.5, kf, u, v.float(), la)
+            y = ops.nsgdn_scan(qf, kf, u, v.float(), la)
             y = ops.gated_rmsnorm(y, None if gate is None else gate.float(), self.norm.weight, eps)
             return _linear(y.reshape(B, T, -1).to(xp.dtype), self.o_proj.weight)
         # u from k, the previous token's k and beta in one HIP pass (fp32 arithmetic, written in k's dtype, which

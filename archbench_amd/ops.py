@@ -124,7 +124,7 @@ def chunk_fwd(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, h0: Opti
     g, beta, h0 = _arg(g, torch.float32), _arg(beta, torch.float32), _arg(h0, torch.float32)
     o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
     hT = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
-    ws = torch.empty(_lib.ws_bytes("fwd", B, T, H, K, V, q.dtype), dtype=torch.uint8, device=q.device)
+    ws = _lib.workspace(q.device, _lib.ws_bytes("fwd", B, T, H, K, V, q.dtype))
     rc = lib.gdn_chunk_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta), _lib.ptr(h0),
                            _lib.ptr(o), _lib.ptr(hT), _lib.ptr(ws), ws.numel(), B, T, H, K, V, float(scale), dt,
                            _lib.stream_ptr(q.device))
@@ -156,7 +156,7 @@ def chunk_bwd(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, h0: Opti
     dg = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
     db = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
     dh0 = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
-    ws = torch.empty(_lib.ws_bytes("bwd", B, T, H, K, V, q.dtype), dtype=torch.uint8, device=q.device)
+    ws = _lib.workspace(q.device, _lib.ws_bytes("bwd", B, T, H, K, V, q.dtype))
     rc = lib.gdn_chunk_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta), _lib.ptr(h0),
                            _lib.ptr(do), _lib.ptr(dhT), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg),
                            _lib.ptr(db), _lib.ptr(dh0), _lib.ptr(ws), ws.numel(), B, T, H, K, V, float(scale), dt,
@@ -246,7 +246,7 @@ def chunk_bwd_stashed(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor, 
     dg = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
     db = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
     dh0 = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
-    ws = torch.empty(_lib.stash_bytes(B, T, H, K, V, q.dtype)[1], dtype=torch.uint8, device=q.device)
+    ws = _lib.workspace(q.device, _lib.stash_bytes(B, T, H, K, V, q.dtype)[1])
     rc = lib.gdn_chunk_bwd_stashed(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
                                    _lib.ptr(h0), _lib.ptr(do), _lib.ptr(dhT), _lib.ptr(dq), _lib.ptr(dk),
                                    _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(db), _lib.ptr(dh0), _lib.ptr(stash),
@@ -344,7 +344,7 @@ def nsgdn_chunk_bwd(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor, h0: 
     dq, dk, du, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(u), torch.empty_like(v)
     dla = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
     dh0 = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
-    ws = torch.empty(_lib.stash_bytes(B, T, H, K, V, q.dtype)[1], dtype=torch.uint8, device=q.device)
+    ws = _lib.workspace(q.device, _lib.stash_bytes(B, T, H, K, V, q.dtype)[1])
     rc = lib.gdn_nsgdn_chunk_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(u), _lib.ptr(v), _lib.ptr(la), _lib.ptr(h0),
                                  _lib.ptr(dy), _lib.ptr(dhT), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(du),
                                  _lib.ptr(dv), _lib.ptr(dla), _lib.ptr(dh0), _lib.ptr(stash), stash.numel(),
@@ -389,7 +389,7 @@ nsgdn_chunk_fwd.register_autograd(_nsgdn_backward, setup_context=_nsgdn_setup)
 @torch.library.custom_op("archbench_amd::write_direction", mutates_args=())
 def write_direction(k: Tensor, beta: Tensor, lam: Tensor, n_steps: int) -> Tensor:
     """u [B,T,H,K] in k's dtype: u_1 = beta k, u_{i+1} = u_i - lam beta (p . u_i) (p - (p . k) k), p = k[:, t-1]
-    (zero at t = 0).  n_steps <= 1 is u = beta k, as in the reference; at most 8 steps are compiled."""
+    (zero at t = 0).  n_steps <= 1 is u = beta k, as in the reference; any number of steps."""
     _require_gpu(k, beta, lam)
     B, T, H, K = _wd_shapes(k, beta, lam)
     lib = _lib.load()
@@ -680,7 +680,7 @@ def _conv_bwd_launch(x: Tensor, w: Tensor, bias: Optional[Tensor], state: Option
         raise ValueError(f"dw must be a contiguous 16-byte aligned fp32 [{D}, {W}] tensor")
     db = torch.empty(D, dtype=torch.float32, device=x.device)
     dstate = torch.empty(B, D, W - 1, dtype=x.dtype, device=x.device)
-    ws = torch.empty(_lib.conv_ws_bytes(B, T, D, W), dtype=torch.uint8, device=x.device)
+    ws = _lib.workspace(x.device, _lib.conv_ws_bytes(B, T, D, W))
     rc = lib.gdn_short_conv_bwd(_lib.ptr(x), ldx, _lib.ptr(w), _lib.ptr(bias), _lib.ptr(state), _lib.ptr(dy),
                                 _lib.ptr(dx), lddx, _lib.ptr(dw), _lib.ptr(db), _lib.ptr(dstate), _lib.ptr(ws),
                                 ws.numel(), B, T, D, W, int(norm_group), _lib.dtype_code(x.dtype),
@@ -839,7 +839,7 @@ def gated_rmsnorm_bwd(x: Tensor, gate: Optional[Tensor], weight: Optional[Tensor
     dx = torch.empty_like(x)
     dgate = torch.empty_like(x) if gate is not None else x.new_empty(0)
     dw = torch.empty(dim, dtype=torch.float32, device=x.device)
-    ws = torch.empty(_lib.norm_ws_bytes(rows, dim), dtype=torch.uint8, device=x.device)
+    ws = _lib.workspace(x.device, _lib.norm_ws_bytes(rows, dim))
     rc = lib.gdn_gated_rmsnorm_bwd(_lib.ptr(x), _lib.ptr(gate), ldg, gpl, _lib.ptr(weight), _lib.ptr(dy),
                                    _lib.ptr(dx), _lib.ptr(dgate) if gate is not None else None, _lib.ptr(dw),
                                    _lib.ptr(ws), ws.numel(), rows, dim, float(eps), _lib.dtype_code(x.dtype),
@@ -975,7 +975,7 @@ def gdn_gates_bwd(a: Tensor, b: Tensor, A_log: Tensor, dt_bias: Optional[Tensor]
     dg, dbeta = _arg(dg, torch.float32), _arg(dbeta, torch.float32)
     da, db = torch.empty_like(a), torch.empty_like(a)
     dA, ddt, dbb = (torch.empty(H, dtype=torch.float32, device=a.device) for _ in range(3))
-    ws = torch.empty(_lib.gates_ws_bytes(ntok, H), dtype=torch.uint8, device=a.device)
+    ws = _lib.workspace(a.device, _lib.gates_ws_bytes(ntok, H))
     rc = lib.gdn_gates_bwd(_lib.ptr(a), _lib.ptr(b), 0, _lib.ptr(A_log), _lib.ptr(dt_bias), _lib.ptr(b_bias),
                            _lib.ptr(dg), _lib.ptr(dbeta), _lib.ptr(da), _lib.ptr(db), 0, _lib.ptr(dA), _lib.ptr(ddt),
                            _lib.ptr(dbb), _lib.ptr(ws), ws.numel(), ntok, H, float(beta_scale), float(g_min),
@@ -1061,7 +1061,7 @@ def gdn_gates_ab_bwd(ab: Tensor, A_log: Tensor, dt_bias: Optional[Tensor], b_bia
     dg, dbeta = _arg(dg, torch.float32), _arg(dbeta, torch.float32)
     dab = torch.empty_like(ab)
     dA, ddt, dbb = (torch.empty(H, dtype=torch.float32, device=ab.device) for _ in range(3))
-    ws = torch.empty(_lib.gates_ws_bytes(ntok, H), dtype=torch.uint8, device=ab.device)
+    ws = _lib.workspace(ab.device, _lib.gates_ws_bytes(ntok, H))
     rc = lib.gdn_gates_bwd(_lib.ptr(ab), _half_ptr(ab, H), 2 * H, _lib.ptr(A_log), _lib.ptr(dt_bias),
                            _lib.ptr(b_bias), _lib.ptr(dg), _lib.ptr(dbeta), _lib.ptr(dab), _half_ptr(dab, H), 2 * H,
                            _lib.ptr(dA), _lib.ptr(ddt), _lib.ptr(dbb), _lib.ptr(ws), ws.numel(), ntok, H,

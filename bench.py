@@ -35,12 +35,15 @@ Also reported in the same line:
                 4 heads, head_dim 128, expand_v 2, gate, short conv 4), fed fp32 hidden states under bf16 autocast as
                 the trainer runs Block.forward, at B=64, T=1024: forward + backward of the whole layer (projections
                 on hipBLASLt, conv, gates, the op, gated RMSNorm, output projection; gradients unset before each
-                step, as after zero_grad(set_to_none=True)), tokens/s, with the library's kernels' share of the step;
+                step, as after zero_grad(set_to_none=True)), tokens/s by the host clock and the step's GPU span by
+                events, with the library's kernels' share of that span (the rest: PyTorch's kernels, mostly the
+                projection GEMMs, and any time the GPU waits for the host);
   nsgdn_layer   the same for archbench's `nsgdn` mixer (configs/65m/nsgdn.yaml: n_steps 2, lam 1, the same
                 projections, conv and norm around the separate-write-key chunk kernels, plus the write direction);
   token_scan    the exact fp32 token scan of the n-step family (the reference's scan_impl "triton" / "ref") at
-                B=16, T=1024, H=4, K=128, V=256: forward and backward kernel times (an exactness path, not a fast
-                one: the chunk pair does the same tokens in a fraction of the time);
+                B=16, T=1024, H=4, K=128, V=256: the forward + backward op pair by the host clock (tokens/s), and
+                its two scan kernels by events (an exactness path, not a fast one: the chunk pair does the same
+                tokens in a fraction of the time);
   decode_step   one recurrent decode step at B=256, H=16, K=V=128 with the fp32 state updated in place
                 (HBM GB/s against 8 TB/s);
   short_conv    the causal depthwise conv (kernel 4) + SiLU in front of the op at the layer's shape, B=8, T=4096,
@@ -303,12 +306,13 @@ def main() -> int:
         B, T, H, K, V = 8, 2048, 8, 128, 128
         log(f"forward only B={B} T={T} H={H} K={K} V={V} bf16")
         x = make_inputs(B, T, H, K, V, seed=0).to(dev, torch.bfloat16)
-        sec = timed_loop(lambda: ops.chunk_fwd(x.q, x.k, x.v, x.g, x.beta, None, 1.0), args.steps, args.warmup,
-                         torch)
+        sec, sec_ev = timed_loop(lambda: ops.chunk_fwd(x.q, x.k, x.v, x.g, x.beta, None, 1.0), args.steps,
+                                 args.warmup, torch, events=True)
         out["fwd_only"] = {"workload": "gdn_chunk_fwd", "B": B, "T": T, "H": H, "K": K, "V": V,
-                           "ms": round(sec * 1e3, 4), "tokens_per_s": round(B * T / sec, 1),
-                           "mfma_frac": round(f_fwd(K, V) * B * T * H / sec / MFMA_BF16_PEAK, 4)}
-        log(f"fwd {sec * 1e3:.3f} ms")
+                           "ms": round(sec * 1e3, 4), "ms_events": round(sec_ev * 1e3, 4),
+                           "tokens_per_s": round(B * T / sec, 1),
+                           "mfma_frac": round(f_fwd(K, V) * B * T * H / sec_ev / MFMA_BF16_PEAK, 4)}
+        log(f"fwd {sec * 1e3:.3f} ms by the host clock, {sec_ev * 1e3:.3f} ms by events")
         del x
         torch.cuda.empty_cache()
 
@@ -399,18 +403,26 @@ def main() -> int:
                 y.backward(gy)
 
             n = max(5, min(args.steps, 20))
-            sec = timed_loop(layer_step, n, 2, torch)
+            # warmup >= 5: the first steps of a mixer pay one-time costs (hipBLASLt's first calls at each GEMM
+            # shape, the caching allocator's growth) that are not the step's
+            sec, sec_ev = timed_loop(layer_step, n, max(5, args.warmup), torch, events=True)
             with _lib.StageTimer() as st:
                 for _ in range(3):
                     layer_step()
             lib_ms = sum(v_[0] for v_ in st.result.values()) / 3
+            ev_ms = sec_ev * 1e3
             out[key] = {"workload": f"{arch} mixer fwd+bwd (configs/65m/{arch}.yaml)", "B": B, "T": T,
                         "d_model": D, "heads": nh, "K": 128, "V": 256, "steps": n,
-                        "ms_per_step": round(sec * 1e3, 4), "tokens_per_s": round(B * T / sec, 1),
+                        "ms_per_step": round(sec * 1e3, 4), "ms_per_step_events": round(ev_ms, 4),
+                        "tokens_per_s": round(B * T / sec, 1),
                         "library_kernels_ms": round(lib_ms, 4),
+                        # the GPU span of a step less this library's kernels: PyTorch's kernels (the projection
+                        # GEMMs on hipBLASLt, casts, gradient sums) and any time the GPU waits for the host
+                        "other_ms": round(ev_ms - lib_ms, 4),
+                        "library_share": round(lib_ms / ev_ms, 4),
                         "stages_ms": {k_: round(v_[0] / 3, 4) for k_, v_ in st.result.items()}}
-            log(f"{arch} layer {sec * 1e3:.3f} ms/step, {B * T / sec:.3e} tokens/s; library kernels {lib_ms:.3f} "
-                f"ms per step {out[key]['stages_ms']}")
+            log(f"{arch} layer {sec * 1e3:.3f} ms/step by the host clock, {ev_ms:.3f} ms by events, "
+                f"{B * T / sec:.3e} tokens/s; library kernels {lib_ms:.3f} ms per step {out[key]['stages_ms']}")
             del m, xin, gy
             torch.cuda.empty_cache()
 
@@ -423,19 +435,22 @@ def main() -> int:
         ut, vt = kt * 0.5, torch.randn(B, T, H, V, device=dev, generator=gen)
         lat = -torch.nn.functional.softplus(torch.randn(B, T, H, device=dev, generator=gen))
         dyt = torch.randn(B, T, H, V, device=dev, generator=gen)
-        y_, r_, st_, _ = ops.nsgdn_token_fwd(qt, kt, ut, vt, lat, None, False)
-        ops.nsgdn_token_bwd(qt, kt, ut, lat, r_, st_, dyt, None, False)
-        torch.cuda.synchronize()
+        def scan_pair():
+            _, r1, st1, _ = ops.nsgdn_token_fwd(qt, kt, ut, vt, lat, None, False)
+            ops.nsgdn_token_bwd(qt, kt, ut, lat, r1, st1, dyt, None, False)
+
+        # the op pair as called (the backward's host side also sums the per-block partial rows of dq, du, dk
+        # and dla): host clock over whole calls; the two scan kernels by events beside it
+        sec = timed_loop(scan_pair, 5, 1, torch)
         with _lib.StageTimer() as st:
             for _ in range(2):
-                y_, r_, st_, _ = ops.nsgdn_token_fwd(qt, kt, ut, vt, lat, None, False)
-                ops.nsgdn_token_bwd(qt, kt, ut, lat, r_, st_, dyt, None, False)
+                scan_pair()
         f_ms = st.result["token_scan_fwd"][0] / 2
         b_ms = st.result["token_scan_bwd"][0] / 2
         out["token_scan"] = {"workload": "nsgdn exact fp32 token scan (scan_impl triton/ref)", "B": B, "T": T, "H": H,
-                             "K": K, "V": V, "fwd_ms": round(f_ms, 3), "bwd_ms": round(b_ms, 3),
-                             "tokens_per_s": round(B * T / ((f_ms + b_ms) * 1e-3), 1)}
-        log(f"token scan fwd {f_ms:.3f} ms, bwd {b_ms:.3f} ms")
+                             "K": K, "V": V, "ms_per_step": round(sec * 1e3, 3), "fwd_kernel_ms": round(f_ms, 3),
+                             "bwd_kernel_ms": round(b_ms, 3), "tokens_per_s": round(B * T / sec, 1)}
+        log(f"token scan fwd+bwd {sec * 1e3:.3f} ms per call pair; kernels fwd {f_ms:.3f} ms, bwd {b_ms:.3f} ms")
         del qt, kt, ut, vt, lat, dyt, y_, r_, st_
         torch.cuda.empty_cache()
 

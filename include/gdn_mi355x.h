@@ -73,9 +73,11 @@ int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, c
 
 /* Allocation-free chunkwise forward.  No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It computes
- * exactly what gdn_chunk_fwd computes, with the same kernels, but takes no workspace: the chunk factors go to a
+ * what gdn_chunk_fwd computes, with the same kernels, but takes no workspace: the chunk factors go to a
  * scratch array of GDN_NOALLOC_SCRATCH_BYTES that the library keeps in device memory on each GPU it runs on
- * (until the process ends).  The call allocates and frees nothing.  Limit: one sequence's factors,
+ * (until the process ends).  The results equal gdn_chunk_fwd's bit for bit where gdn_chunk_fwd does not segment
+ * its sweeps (long T with few B * H: there it splits each sequence into segments and this entry point does not,
+ * and the two agree within rounding).  The call allocates and frees nothing.  Limit: one sequence's factors,
  * H * ceil(T/64) chunks of 16,640 bytes (bf16; 33,024 in fp32), must fit in the scratch; larger batches run as
  * consecutive groups of sequences on `stream` (this needs T * H to be a multiple of 4), otherwise
  * GDN_ERR_WORKSPACE.  Every call on one GPU shares that GPU's scratch, so calls that overlap in time on one GPU
@@ -211,7 +213,7 @@ int gdn_cross_entropy_fwd_bwd(void* logits, const int64_t* target, float* loss, 
  * Replaces write_direction (archbench/layers/nsgdn.py:61-75) and the shift of k that feeds it (:535-536).  k, u, du,
  * dk [B, T, H, K] in dtype; beta, dbeta, dlam [B, T, H] fp32; lam [H] fp32 (the module's softplus(lam)).  The
  * backward writes dk (through both k and the next token's p), dbeta and dlam per row (the caller sums dlam over
- * B and T).  K in {64, 128, 256}, 1 <= n_steps <= 8; fp32 arithmetic. */
+ * B and T).  K in {64, 128, 256}, n_steps >= 1; fp32 arithmetic. */
 int gdn_write_direction_fwd(const void* k, const float* beta, const float* lam, void* u, int B, int T, int H, int K,
                             int n_steps, int dtype, void* stream);
 int gdn_write_direction_bwd(const void* k, const float* beta, const float* lam, const void* du, void* dk,

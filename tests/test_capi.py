@@ -136,3 +136,19 @@ def test_strided_input_layouts_are_validated_before_any_launch():
     assert rc == _lib.GDN_ERR_ARG and b"gate layout" in lib.gdn_last_error()
     rc = lib.gdn_gated_rmsnorm_fwd(p, p, 512, 4, None, p, 8, 256, 1e-5, _lib.DTYPE_BF16, None)
     assert rc == _lib.GDN_ERR_ARG and b"gate layout" in lib.gdn_last_error()
+
+
+def test_token_scan_rejects_misaligned_vector_arrays():
+    """The token scan reads q, k and u (and the states) as 16-byte vectors: a pointer off a 16-byte boundary (an
+    offset view handed straight to the C ABI) is refused before anything is launched, forward and backward."""
+    lib = _lib.load()
+    ok, off = ctypes.c_void_p(1 << 12), ctypes.c_void_p((1 << 12) + 4)  # never dereferenced: validation fails first
+    big = 1 << 40
+    for which in range(3):  # q, k, u misaligned in turn
+        qku = [ok, ok, ok]
+        qku[which] = off
+        rc = lib.gdn_token_scan_fwd(*qku, ok, ok, None, ok, ok, ok, big, None, 1, 64, 1, 64, 64, None)
+        assert rc == _lib.GDN_ERR_ARG and b"16-byte" in lib.gdn_last_error(), which
+        rc = lib.gdn_token_scan_bwd(*qku, ok, ok, ok, big, ok, None, ok, ok, ok, ok, ok, None, ok, big,
+                                    1, 64, 1, 64, 64, None)
+        assert rc == _lib.GDN_ERR_ARG and b"16-byte" in lib.gdn_last_error(), which

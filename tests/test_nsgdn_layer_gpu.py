@@ -1,7 +1,8 @@
 """The nsgdn mixer (archbench_amd/layers/nsgdn.py) on the GPU against a CPU fp64 restatement of the reference's
 NStepGDN.forward (archbench/layers/nsgdn.py:518-542: conv1d + SiLU, F.normalize, softplus / sigmoid gates,
 write_direction, the token scan with its bf16 boundary, RMSNorm * silu(g), o_proj) with the same parameters:
-output, input gradient and every parameter gradient within rel-L2 2e-2 (3e-2 for parameter gradients)."""
+output and input gradient within rel-L2 1e-2, every parameter gradient within 3e-2; and the mixer at each of
+archbench's model sizes under bf16 autocast against the same mixer with its scan in the fp64 oracle."""
 
 import pytest
 import torch
@@ -14,15 +15,19 @@ from tests.gpu_util import banner, rel_l2
 pytestmark = pytest.mark.gpu
 
 
-def _reference_forward(P, x, H, DK, DV, n_steps, size, eps, bf16_scan=True):
+def _reference_forward(P, x, H, DK, DV, n_steps, size, eps, bf16_scan=True, autocast=False):
     """NStepGDN.forward restated on CPU fp64 from the module's parameters P (name -> tensor); with bf16_scan the
-    scan's inputs and output are rounded to bf16 as the reference's nsgdn_scan_chunk does (nsgdn.py:404)."""
+    scan's inputs and output are rounded to bf16 as the reference's nsgdn_scan_chunk does (nsgdn.py:404).  With
+    autocast the values are rounded to bf16 where bf16 autocast rounds them in the reference: the projections'
+    inputs, weights and outputs, and the conv's output, which the reference then normalises in fp32
+    (nsgdn.py:520-528); o_proj's input and weight."""
     B, T, _ = x.shape
     qk, vd = H * DK, H * DV
-    proj = x @ P["in_proj.weight"].T
+    r = (lambda t: t.to(torch.bfloat16).to(torch.float64)) if autocast else (lambda t: t)
+    proj = r(r(x) @ r(P["in_proj.weight"]).T)
     qkv, g, ab = proj[..., :2 * qk + vd], proj[..., 2 * qk + vd:2 * qk + 2 * vd], proj[..., 2 * qk + 2 * vd:]
-    y = F.conv1d(qkv.transpose(1, 2), P["conv.weight"], padding=size - 1, groups=qkv.shape[-1])
-    qkv = F.silu(y[..., :T].transpose(1, 2))
+    y = F.conv1d(qkv.transpose(1, 2), r(P["conv.weight"]), padding=size - 1, groups=qkv.shape[-1])
+    qkv = r(F.silu(y[..., :T].transpose(1, 2)))
     q = F.normalize(qkv[..., :qk].reshape(B, T, H, DK), dim=-1) * DK ** -0.5
     k = F.normalize(qkv[..., qk:2 * qk].reshape(B, T, H, DK), dim=-1)
     v = qkv[..., 2 * qk:].reshape(B, T, H, DV)
@@ -35,7 +40,7 @@ def _reference_forward(P, x, H, DK, DV, n_steps, size, eps, bf16_scan=True):
     yk, _ = NS.chunk_fwd(bf(q), bf(k), bf(u), bf(v), la, 1.0)
     yk = bf(yk)
     yk = F.rms_norm(yk, (DV,), P["norm.weight"], eps) * F.silu(g.reshape(B, T, H, DV))
-    return yk.reshape(B, T, -1) @ P["o_proj.weight"].T
+    return r(yk.reshape(B, T, -1)) @ r(P["o_proj.weight"]).T
 
 
 def test_nsgdn_layer_matches_reference_forward_backward():
@@ -59,8 +64,9 @@ def test_nsgdn_layer_matches_reference_forward_backward():
         yr.backward(dy.double())
         refs.append((yr.detach(), xr.grad, {n: t.grad for n, t in P.items()}))
     (yr, dxr, gr), (_, _, gr_exact) = refs
-    assert rel_l2(y, yr) <= 2e-2
-    assert rel_l2(xd.grad, dxr) <= 2e-2
+    errs = {"y": rel_l2(y, yr), "dx": rel_l2(xd.grad, dxr)}
+    print("rel-L2 vs restatement:", {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    assert errs["y"] <= 1e-2 and errs["dx"] <= 1e-2, errs
     for n, p in m.named_parameters():
         # the per-head vectors' gradients (A_log, dt_bias, b_bias, lam) are sums over every token that largely
         # cancel; the reference itself moves by rel_l2(exact, bf16) when only the bf16 rounding point changes,
@@ -69,13 +75,15 @@ def test_nsgdn_layer_matches_reference_forward_backward():
         assert rel_l2(p.grad, gr[n]) <= 3e-2 + 4 * noise, (n, noise)
 
 
-@pytest.mark.parametrize("impl,DK", [("triton", 64), ("ref", 128)])
-def test_nsgdn_layer_exact_scan_matches_in_fp32(impl, DK):
+@pytest.mark.parametrize("impl,DK,autocast", [("triton", 64, False), ("ref", 128, False), ("triton", 128, True)])
+def test_nsgdn_layer_exact_scan_matches_in_fp32(impl, DK, autocast):
     """scan_impl "triton" / "ref" run the reference's exact fp32 token scan (ops.nsgdn_scan).  Without autocast
     every pass of the layer is fp32 (projections, conv, gates, write direction, scan, norm), so the whole mixer
     must match the fp64 restatement of NStepGDN.forward to fp32 accuracy: output and input gradient rel-L2
-    <= 1e-5, every parameter gradient <= 1e-4 (the per-head vectors' are cancelling sums over every token)."""
-    banner(f"nsgdn layer, scan_impl={impl}, fp32 vs fp64 restatement")
+    <= 1e-5, every parameter gradient <= 1e-4 (the per-head vectors' are cancelling sums over every token).
+    Under bf16 autocast the projections and the conv output are bf16 and q, k are normalised afterwards in fp32,
+    as in the reference; against the restatement rounded at the same points: output and input gradient <= 1e-2."""
+    banner(f"nsgdn layer, scan_impl={impl}, autocast={autocast}, vs fp64 restatement")
     torch.manual_seed(3)
     H, DV, d = 2, 2 * DK, 192
     m = layers.build_mixer("nsgdn", d, 0, 2, num_heads=H, head_dim=DK, expand_v=2.0, n_steps=2, lam=1.0,
@@ -85,17 +93,21 @@ def test_nsgdn_layer_exact_scan_matches_in_fp32(impl, DK):
             torch.nn.init.normal_(p, std=0.05)
     x = torch.randn(2, 70, d, generator=torch.Generator().manual_seed(4))
     xd = x.cuda().requires_grad_()
-    y = m(xd)
-    assert y.dtype == torch.float32
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        y = m(xd)
+    assert y.dtype == (torch.bfloat16 if autocast else torch.float32)
     dy = torch.randn(*y.shape, generator=torch.Generator().manual_seed(5))
-    y.backward(dy.cuda())
+    y.float().backward(dy.cuda())
     P = {n: p.detach().cpu().double().requires_grad_() for n, p in m.named_parameters()}
     xr = x.double().requires_grad_()
-    yr = _reference_forward(P, xr, H, DK, DV, 2, 4, m.norm.eps or 1e-5, bf16_scan=False)
+    yr = _reference_forward(P, xr, H, DK, DV, 2, 4, m.norm.eps or 1e-5, bf16_scan=False, autocast=autocast)
     yr.backward(dy.double())
-    errs = {"y": rel_l2(y, yr), "dx": rel_l2(xd.grad, xr.grad)}
+    errs = {"y": rel_l2(y.float(), yr), "dx": rel_l2(xd.grad, xr.grad)}
     errs.update({n: rel_l2(p.grad, P[n].grad) for n, p in m.named_parameters()})
     print("rel-L2:", {n: f"{e:.1e}" for n, e in errs.items()}, flush=True)
+    if autocast:
+        assert errs["y"] <= 1e-2 and errs["dx"] <= 1e-2, errs
+        return
     assert errs["y"] <= 1e-5 and errs["dx"] <= 1e-5, errs
     for n, _ in m.named_parameters():
         assert errs[n] <= 1e-4, (n, errs[n])
@@ -129,3 +141,48 @@ def test_nsgdn_layer_under_torch_compile(impl):
     assert rel_l2(y1, y0) <= 1e-2 and rel_l2(gx1, gx0) <= 1e-2
     for n in gp0:
         assert rel_l2(gp1[n], gp0[n]) <= 2e-2, n
+
+
+def _oracle_scan_chunk(q, k, u, v, la, scale=1.0, **kw):
+    """The oracle (fp64, CPU, differentiable) in place of ops.nsgdn_scan_chunk: test infrastructure only."""
+    dev, dt = q.device, q.dtype
+    y, _ = NS.chunk_fwd(*(t.cpu().double() for t in (q, k, u, v, la)), scale)
+    return y.to(dev, dt)
+
+
+# archbench's model sizes (configs/{40m,65m,130m,380m}/nsgdn.yaml): d_model and num_heads, with head_dim 128,
+# expand_v 2, n_steps 2, lam 1 (configs/arch/nsgdn.yaml); n_steps 9 at the 65m size as well (any n_steps runs)
+@pytest.mark.parametrize("size,d_model,heads,n_steps", [("40m", 384, 3, 2), ("65m", 512, 4, 2), ("65m", 512, 4, 9),
+                                                        ("130m", 768, 6, 2), ("380m", 1024, 8, 2)])
+def test_nsgdn_reference_configs_under_autocast(monkeypatch, size, d_model, heads, n_steps):
+    """The mixer as archbench builds it for configs/<size>/nsgdn.yaml (K = 128, V = 256), fed fp32 hidden states
+    under bf16 autocast as the trainer runs it: output, input gradient and every parameter gradient match the same
+    mixer with its chunk scan in the fp64 oracle within rel-L2 1e-2."""
+    banner(f"nsgdn layer at configs/{size}/nsgdn.yaml (d_model {d_model}, {heads} heads, n_steps {n_steps}) "
+           "under bf16 autocast vs oracle-backed layer")
+    torch.manual_seed(11)
+    m = layers.build_mixer("nsgdn", d_model, 0, 10, num_heads=heads, head_dim=128, expand_v=2.0, n_steps=n_steps,
+                           lam=1.0, use_gate=True, use_short_conv=True, conv_size=4).cuda()
+    for p in m.parameters():
+        if p.dim() == 2:
+            torch.nn.init.normal_(p, std=0.03)
+    x = torch.randn(2, 200, d_model, device="cuda", generator=torch.Generator("cuda").manual_seed(12))
+    dy = torch.randn(2, 200, d_model, device="cuda", generator=torch.Generator("cuda").manual_seed(13))
+
+    def run():
+        for p in m.parameters():
+            p.grad = None
+        xi = x.clone().requires_grad_()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = m(xi)
+        (y.float() * dy).sum().backward()
+        return y.float(), xi.grad, {n: p.grad.clone() for n, p in m.named_parameters()}
+
+    y1, dx1, g1 = run()
+    monkeypatch.setattr("archbench_amd.layers.nsgdn.ops.nsgdn_scan_chunk", _oracle_scan_chunk)
+    y2, dx2, g2 = run()
+    errs = {"y": rel_l2(y1, y2), "dx": rel_l2(dx1, dx2)}
+    errs.update({n: rel_l2(g1[n], g2[n]) for n in g1})
+    print("rel-L2 vs oracle-backed layer:", {n: f"{e:.2e}" for n, e in errs.items()}, flush=True)
+    for n, e in errs.items():
+        assert e <= 1e-2, (n, e)

@@ -1,6 +1,7 @@
 """Pins oracle/nsgdn_oracle.py (separate read / write vectors) on the CPU: reduction to the pinned gated delta
 rule oracle at u = beta k, chunk form = token recurrence, brute-force affine-map products, the T = 1 closed
-form, fp64 gradcheck and the write_direction invariant (nsgdn.py:61-75, :240-249, :408-417)."""
+form, fp64 gradcheck, and write_direction's invariant, per-step contraction and two-step closed form, with planted
+mistakes that the pins must catch (nsgdn.py:61-75, :240-249, :408-417)."""
 
 import torch
 import torch.nn.functional as F
@@ -81,3 +82,59 @@ def test_write_direction():
     u3 = NS.write_direction(k, p, beta, lam, 3)
     torch.testing.assert_close((u3 * k).sum(-1), beta)  # the current-key gain is kept for unit k
     assert not torch.allclose(u3, beta[..., None] * k)
+
+
+def _wd_case(T=20):
+    q, k, _, _, la, _ = _inputs(T=T, K=8)
+    gen = torch.Generator().manual_seed(5)
+    beta = torch.rand(*la.shape, generator=gen, dtype=torch.float64)
+    lam = torch.tensor([0.7, 1.8], dtype=torch.float64)
+    p = torch.randn(*k.shape, generator=gen, dtype=torch.float64)  # any p (the layer passes the previous key)
+    return k, p, beta, lam
+
+
+def _wd_pins(wd) -> None:
+    """Properties that fix write_direction's step coefficient (the reference states the first at nsgdn.py:64-66):
+    * contraction: for unit k each step scales p . u by (1 - lam beta |p_perp|^2), so
+      p . u_n = beta (p . k) (1 - lam beta |p_perp|^2)^(n-1);
+    * the n = 2 closed form u_2 = beta k - lam beta^2 (p . k) p_perp;
+    * u_n - beta k lies along p_perp (every step moves u along p_perp only)."""
+    k, p, beta, lam = _wd_case()
+    b, lm = beta[..., None], lam[None, None, :, None]
+    pk = (p * k).sum(-1, keepdim=True)
+    p_perp = p - pk * k
+    shrink = 1 - lm * b * (p_perp * p_perp).sum(-1, keepdim=True)
+    for n in (2, 3, 4):
+        u = wd(k, p, beta, lam, n)
+        torch.testing.assert_close((p * u).sum(-1, keepdim=True), b * pk * shrink ** (n - 1))
+        resid = u - b * k
+        along = (resid * p_perp).sum(-1, keepdim=True) / (p_perp * p_perp).sum(-1, keepdim=True)
+        torch.testing.assert_close(resid, along * p_perp)
+    torch.testing.assert_close(wd(k, p, beta, lam, 2), b * k - lm * b * b * pk * p_perp)
+
+
+def test_write_direction_pinned_for_several_steps():
+    _wd_pins(NS.write_direction)
+
+
+def test_write_direction_pins_catch_planted_mistakes():
+    """Restatements with a flipped step sign, a dropped lam, a dropped beta (all three keep the k . u = beta
+    invariant of test_write_direction) or p in place of p_perp must each fail the pins."""
+    def mutant(kind):
+        def wd(k, p, beta, lam, n_steps):
+            b, lm = beta[..., None], lam[None, None, :, None]
+            u = b * k
+            p_perp = p - (p * k).sum(-1, keepdim=True) * k
+            for _ in range(n_steps - 1):
+                c = {"sign": -lm * b, "lam": b, "beta": lm, "p": lm * b}[kind]
+                d = p if kind == "p" else p_perp
+                u = u - c * (p * u).sum(-1, keepdim=True) * d
+            return u
+        return wd
+
+    for kind in ("sign", "lam", "beta", "p"):
+        try:
+            _wd_pins(mutant(kind))
+        except AssertionError:
+            continue
+        raise AssertionError(f"planted write_direction mistake {kind!r} passed the pins")

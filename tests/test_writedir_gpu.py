@@ -50,6 +50,9 @@ CASES = [  # B, T, H, K, n_steps, unit-norm keys
     (2, 100, 2, 256, 4, False),
     (1, 50, 5, 128, 8, False),
     (2, 33, 2, 64, 1, True),
+    (2, 40, 3, 64, 9, True),  # past the unrolled range the earlier kernel had: any n_steps runs
+    (1, 33, 2, 128, 16, True),
+    (2, 20, 2, 64, 9, False),
 ]
 
 
@@ -89,7 +92,5 @@ def test_write_direction_one_step_and_edges():
     assert e.shape == (0, 20, 2, 64)
     with pytest.raises(ValueError, match="K=96"):
         ops.write_direction(torch.randn(1, 4, 2, 96, device="cuda"), beta[:1, :4].cuda(), lam.cuda(), 2)
-    with pytest.raises(ValueError, match="n_steps=9"):
-        ops.write_direction(k.cuda(), beta.cuda(), lam.cuda(), 9)
     with pytest.raises(ValueError, match="beta must be"):
         ops.write_direction(k.cuda(), beta[:, :3].cuda(), lam.cuda(), 2)
