@@ -107,8 +107,8 @@ __device__ __forceinline__ void mma_blk(f32x4& c, const T* A, int lda, int m0, c
 // its B operand without leaving registers; the other operand is then read with the same slot order.
 // k contiguous (element (o, k) at p[o*ld + k]), permuted slots: two 4-element reads.
 template <typename T>
-__device__ __forceinline__ typename Frag<T>::type frag_kc_perm(const T* p, int ld, int o0, int k0) {
-  const int l = lane_id();
+__device__ __forceinline__ typename Frag<T>::type frag_kc_perm(const T* p, int ld, int o0, int k0,
+                                                              int l = lane_id()) {
   const T* s = p + (o0 + (l & 15)) * ld + k0 + 4 * (l >> 4);
   if constexpr (sizeof(T) == 2) {
     const bf16x4 a = *reinterpret_cast<const bf16x4*>(s);
@@ -123,8 +123,8 @@ __device__ __forceinline__ typename Frag<T>::type frag_kc_perm(const T* p, int l
 
 // outer index contiguous (element (o, k) at p[k*ld + o]), permuted slots.
 template <typename T>
-__device__ __forceinline__ typename Frag<T>::type frag_oc_perm(const T* p, int ld, int o0, int k0) {
-  const int l = lane_id();
+__device__ __forceinline__ typename Frag<T>::type frag_oc_perm(const T* p, int ld, int o0, int k0,
+                                                              int l = lane_id()) {
   const T* s = p + (k0 + 4 * (l >> 4)) * ld + o0 + (l & 15);
   typename Frag<T>::type f;
 #pragma unroll
@@ -163,16 +163,14 @@ __device__ __forceinline__ typename Frag<T>::type frag_oct(const T* p, int ld, i
   }
 }
 template <typename T>
-__device__ __forceinline__ typename Frag<T>::type frag_oct_perm(const T* p, int ld, int o0, int k0);
-
-template <typename T>
-__device__ __forceinline__ typename Frag<T>::type frag_oct_perm(const T* p, int ld, int o0, int k0) {
+__device__ __forceinline__ typename Frag<T>::type frag_oct_perm(const T* p, int ld, int o0, int k0,
+                                                               int l = lane_id()) {
   if constexpr (sizeof(T) == 2) {
-    const int g = lane_id() >> 4;
-    const bf16x4 a = ld_tr4(p, ld, o0, k0 + 4 * g), b = ld_tr4(p, ld, o0, k0 + 16 + 4 * g);
+    const int g = l >> 4;
+    const bf16x4 a = ld_tr4(p, ld, o0, k0 + 4 * g, l), b = ld_tr4(p, ld, o0, k0 + 16 + 4 * g, l);
     return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   } else {
-    return frag_oc_perm(p, ld, o0, k0);
+    return frag_oc_perm(p, ld, o0, k0, l);
   }
 }
 
