@@ -50,14 +50,13 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
     ws.P = take(BH * NT * CH_TOKENS * CH_TOKENS * es);
     ws.Gc = static_cast<float*>(take(BH * NT * CH_TOKENS * 4));
   }
-  const bool lean = rebuilds_r_dy(dtype);  // no R / dY buffers: the gradient kernel rebuilds them
   if (parts & WS_STATE) {
     ws.hs = take(BH * NT * (size_t)K * V * es);
-    if (!lean) ws.Rs = take(BH * NT * CH_TOKENS * (size_t)V * es);
+    ws.Rs = take(BH * NT * CH_TOKENS * (size_t)V * es);
   }
   if (parts & WS_GRAD) {
     ws.dhs = take(BH * NT * (size_t)K * V * es);
-    if (!lean) ws.dYs = take(BH * NT * CH_TOKENS * (size_t)V * es);
+    ws.dYs = take(BH * NT * CH_TOKENS * (size_t)V * es);
   }
   const size_t seg_states = ns > 1 ? BH * (size_t)ns * K * V * 4 : 0;  // one fp32 state per segment and head
   if ((parts & WS_SEGF) && ns > 1) {

@@ -204,7 +204,7 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
       mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, 0), dR0);
       mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, 32), dR1);
     }
-    if constexpr (STORE && !rebuilds_r_dy<T>())
+    if constexpr (STORE)
       store_fragblk<T, STATE_NT_STORE>(wsdY + cidx * CH * V, CH, hf, cb, ncb, frag_acc2<T>(Z[0], Z[1]));
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -270,7 +270,6 @@ template <typename T, int K, int V, int VS, bool SEPU>
 __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u, const T* __restrict__ v,
     const float* __restrict__ beta, const T* __restrict__ dout, const float* __restrict__ wsGc,
-    const T* __restrict__ gTm, const T* __restrict__ gP,
     const T* __restrict__ wsH, const T* __restrict__ wsR, const T* __restrict__ wsdH, const T* __restrict__ wsdY,
     T* __restrict__ dq, T* __restrict__ dk, T* __restrict__ du, T* __restrict__ dv, float* __restrict__ dg,
     float* __restrict__ dbeta, int T_, int H, int NT, int BH, float scale) {
@@ -292,11 +291,6 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   __shared__ __attribute__((aligned(16))) T sdv[CH * LS];  // dv of the current slab, for the coalesced store
   __shared__ float sG[CH], sB[CH], sdG[CH], sLast[CH], sColZ[NWAVE][CH], sRed[IW];
   __shared__ float sRow[2][6][CH];  // per-half row sums: rq, rk, dbV, rx, dbA, rz
-  // RB (rebuilds_r_dy): the chunk factors Tm and P, and exp(G) and exp(G_C - G) per row, for rebuilding R and dY
-  constexpr bool RB = rebuilds_r_dy<T>();
-  __shared__ __attribute__((aligned(16))) T sTm[RB ? CH * LC : 8];
-  __shared__ __attribute__((aligned(16))) T sP[RB ? CH * LC : 8];
-  __shared__ float sGam[RB ? CH : 1], sDte[RB ? CH : 1];
 
   T* sdO = slab;
   T* sV = sdO + CH * LS;
@@ -327,22 +321,11 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   RegTile<T, CH, VS, ITH, INTRA_NT> rdo, rv;
   FragTile<T, CH, VS, ITH, INTRA_NT> rr, rdy;
   FragTile<T, K, VS, ITH, INTRA_NT> rs0, rdsc;
-  RegTile<T, CH, CH, ITH, INTRA_NT> rtm, rp;
   auto load_a = [&](int64_t ci, int64_t r0, int nv, int vs) {
     rdo.load(dout + r0 * V + vs, (int64_t)H * V, nv, tid);
     rv.load(v + r0 * V + vs, (int64_t)H * V, nv, tid);
-    if constexpr (!RB) {
-      rr.load(wsR + ci * CH * V, V / 16, vs / 16, tid);
-      rdy.load(wsdY + ci * CH * V, V / 16, vs / 16, tid);
-    }
-  };
-  // Q, K (and U) of chunk ci; with RB also issued one chunk ahead (the rebuild needs K in the first slab)
-  auto load_qk = [&](int ci) {
-    int nv;
-    const int64_t r0 = chunk_rows(ci, nv);
-    tq.load(q + r0 * K, (int64_t)H * K, nv, tid);
-    tk.load(k + r0 * K, (int64_t)H * K, nv, tid);
-    if constexpr (SEPU) tu.load(u + r0 * K, (int64_t)H * K, nv, tid);
+    rr.load(wsR + ci * CH * V, V / 16, vs / 16, tid);
+    rdy.load(wsdY + ci * CH * V, V / 16, vs / 16, tid);
   };
   auto load_b = [&](int64_t ci, int vs) {
     rs0.load(wsH + ci * K * V, V / 16, vs / 16, tid);
@@ -358,10 +341,6 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     const int64_t r0 = chunk_rows(ci, nv);
     pg = wsGc[(int64_t)ci * CH + (tid & (CH - 1))];
     pb = beta ? beta[r0 + (int64_t)((tid & (CH - 1)) < nv ? (tid & (CH - 1)) : 0) * H] : 1.f;
-    if constexpr (RB) {
-      rtm.load(gTm + (int64_t)ci * CH * CH, (int64_t)CH, CH, tid);
-      rp.load(gP + (int64_t)ci * CH * CH, (int64_t)CH, CH, tid);
-    }
     load_a(ci, r0, nv, 0);
     if (order) {
       // A bare barrier (no fence: nothing waits for the loads) so that every wave has issued group A before any
@@ -374,10 +353,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     }
     if (with_b) load_b(ci, 0);
   };
-  if ((int)blockIdx.x < nchunk) {
-    load_first(blockIdx.x, true, true);
-    if constexpr (RB) load_qk(blockIdx.x);
-  }
+  if ((int)blockIdx.x < nchunk) load_first(blockIdx.x, true, true);
 
 #pragma unroll 1
   for (int ci = blockIdx.x; ci < nchunk; ci += gridDim.x) {
@@ -386,23 +362,12 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   int nvalid;
   const int64_t row0 = chunk_rows(ci, nvalid);
   const int64_t cidx = ci;
-  if constexpr (!RB) load_qk(ci);
+  tq.load(q + row0 * K, (int64_t)H * K, nvalid, tid);
+  tk.load(k + row0 * K, (int64_t)H * K, nvalid, tid);
+  if constexpr (SEPU) tu.load(u + row0 * K, (int64_t)H * K, nvalid, tid);
   if (tid < CH) {
     sG[tid] = pg;
     sB[tid] = tid < nvalid ? pb : 0.f;
-    if constexpr (RB) {
-      const float gl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pg), CH - 1));  // G_C (wave 0)
-      sGam[tid] = __expf(pg);
-      sDte[tid] = __expf(gl - pg);
-    }
-  }
-  if constexpr (RB) {
-    // the rebuild reads Q, K (U), Tm and P from the first slab on
-    tq.store(sQ, LK, tid);
-    tk.store(sK, LK, tid);
-    if constexpr (SEPU) tu.store(sU, LK, tid);
-    rtm.store(sTm, LC, tid);
-    rp.store(sP, LC, tid);
   }
 
   // ---- V phase: contractions over V, slab by slab -------------------------------------------------------
@@ -419,161 +384,56 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   // flight exactly (four slabs unrolled would spill).
 #pragma unroll(V / VS <= 2 ? V / VS : 1)
   for (int vs = 0; vs < V; vs += VS) {
-    if constexpr (RB) {
-      // groups A (dO, V) and B (S0, dS_C; <dS_C, S0> from the registers: each thread holds the same elements of
-      // both tiles) together: R and dY are rebuilt from them before any product that reads R or dY
-      rdo.store(sdO, LS, tid);
-      rv.store(sV, LS, tid);
-      rs0.store_t(sS0t, LK, tid);
-      rdsc.store_t(sdSCt, LK, tid);
+    // group A: dO R^T, dY R^T; dv = beta dY and dbeta += dY . v
+    rdo.store(sdO, LS, tid);
+    rv.store(sV, LS, tid);
+    rr.store_t(sRt, LC, tid);
+    rdy.store_t(sdYt, LC, tid);
+    __syncthreads();
+    if (vs + VS < V) load_a(cidx, row0, nvalid, vs + VS);
 #pragma unroll
-      for (int i = 0; i < decltype(rs0)::N; ++i)
-        if (decltype(rs0)::NVEC % ITH == 0 || tid + i * ITH < decltype(rs0)::NVEC)  // loaded by this thread
-#pragma unroll
-          for (int e = 0; e < 8; ++e) sdot += to_f(rdsc.r[i][e]) * to_f(rs0.r[i][e]);
-      __syncthreads();
-      if (vs + VS < V) load_a(cidx, row0, nvalid, vs + VS);
-      {
-        // wave w rebuilds column tile ct = w & 3 of the slab: Y = diag(beta) (V - diag(gamma) K S0) and
-        // dR = P^T dO + diag(exp(G_C - G)) U dS_C over all 64 token rows, then, for the rows of half th = w >> 2,
-        // R = Tm Y and dY = Tm^T dR with Y and dR as B operands straight from the accumulators (permuted-k
-        // fragments); R^T and dY^T go to LDS for the products below and dv = beta dY to the staging tile
-        using V4 = typename std::conditional<sizeof(T) == 2, bf16x4, f32x4>::type;
-        using F = typename Frag<T>::type;
-        const int ct = w & 3, th = w >> 2, cc0 = 16 * ct;
-        F Yb[2], dRb[2];
-        {
-          f32x4 ks[4], kd[4];
-#pragma unroll
-          for (int rt = 0; rt < 4; ++rt) ks[rt] = kd[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int s = 0; s < K / 32; ++s) {
-            const F bs = frag_kc(sS0t, LK, cc0, 32 * s, l), bd = frag_kc(sdSCt, LK, cc0, 32 * s, l);
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-              mma(ks[rt], frag_kc(sK, LK, 16 * rt, 32 * s, l), bs);
-              mma(kd[rt], frag_kc(sU, LK, 16 * rt, 32 * s, l), bd);
-            }
-          }
-          f32x4 y[4];
-#pragma unroll
-          for (int rt = 0; rt < 4; ++rt) {
-            float vv[4];
-            acc_vals(sV, LS, 16 * rt, cc0, vv, l);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int r = 16 * rt + acc_row(i, l);
-              y[rt][i] = sB[r] * (vv[i] - sGam[r] * ks[rt][i]);
-              kd[rt][i] *= sDte[r];
-            }
-          }
-#pragma unroll
-          for (int ib = 0; ib < 2; ++ib) {
-            const F bo = frag_oct(sdO, LS, cc0, 32 * ib, l);
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) mma(kd[rt], frag_oct(sP, LC, 16 * rt, 32 * ib, l), bo);
-          }
-          Yb[0] = frag_acc2<T>(y[0], y[1]);
-          Yb[1] = frag_acc2<T>(y[2], y[3]);
-          dRb[0] = frag_acc2<T>(kd[0], kd[1]);
-          dRb[1] = frag_acc2<T>(kd[2], kd[3]);
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int rt = 2 * th + j;
-          f32x4 R = {0.f, 0.f, 0.f, 0.f}, D = {0.f, 0.f, 0.f, 0.f};
-          mma(R, frag_kc_perm(sTm, LC, 16 * rt, 0, l), Yb[0]);
-          mma(R, frag_kc_perm(sTm, LC, 16 * rt, 32, l), Yb[1]);
-          mma(D, frag_oct_perm(sTm, LC, 16 * rt, 0, l), dRb[0]);
-          mma(D, frag_oct_perm(sTm, LC, 16 * rt, 32, l), dRb[1]);
-          // the lane's four rows of column cc are contiguous in the column-major tiles: one vector store each
-          const int r0 = 16 * rt + 4 * (l >> 4), cc = cc0 + (l & 15);
-          *reinterpret_cast<V4*>(sRt + cc * LC + r0) = V4{from_f<T>(R[0]), from_f<T>(R[1]), from_f<T>(R[2]),
-                                                          from_f<T>(R[3])};
-          *reinterpret_cast<V4*>(sdYt + cc * LC + r0) = V4{from_f<T>(D[0]), from_f<T>(D[1]), from_f<T>(D[2]),
-                                                           from_f<T>(D[3])};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sdv[(r0 + i) * LS + cc] = from_f<T>(sB[r0 + i] * D[i]);
-        }
-      }
-      __syncthreads();
-      if (vs + VS < V) load_b(cidx, vs + VS);
-      s2g_rows<T, CH, VS, ITH, INTRA_NT>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, nvalid, tid);
-#pragma unroll
-      for (int j = 0; j < HC; ++j) {
-        const int n = HC * hf + j;
-        mma_blk<true, false, VS>(aP[j], sdO, LS, 16 * rb, sRt, LC, 16 * n, l);
-        mma_blk<false, false, VS>(aDA[j], sdYt, LC, 16 * rb, sRt, LC, 16 * n, l);
-      }
-#pragma unroll
-      for (int j = 0; j < HV; ++j) {
-        const int vc = 16 * (HV * hf + j) + acc_col(l), r0 = 16 * rb + 4 * (l >> 4);
-        float dy[4], vv[4];
-        run4(sdYt, LC, vc, r0, dy);
-        acc_vals(sV, LS, 16 * rb, 16 * (HV * hf + j), vv, l);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dbV[i] += dy[i] * vv[i];
-      }
-#pragma unroll
-      for (int j = 0; j < HK; ++j) {
-        const int n = HK * hf + j;
-        mma_blk<true, false, VS>(aQg[j], sdO, LS, 16 * rb, sS0t, LK, 16 * n, l);
-        mma_blk<false, false, VS>(aKd[j], sRt, LC, 16 * rb, sdSCt, LK, 16 * n, l);
-        mma_blk<false, false, VS>(aKY[j], sdYt, LC, 16 * rb, sS0t, LK, 16 * n, l);
-      }
-      __syncthreads();
-    } else {
-      // group A: dO R^T, dY R^T; dv = beta dY and dbeta += dY . v
-      rdo.store(sdO, LS, tid);
-      rv.store(sV, LS, tid);
-      rr.store_t(sRt, LC, tid);
-      rdy.store_t(sdYt, LC, tid);
-      __syncthreads();
-      if (vs + VS < V) load_a(cidx, row0, nvalid, vs + VS);
-  #pragma unroll
-      for (int j = 0; j < HC; ++j) {
-        const int n = HC * hf + j;
-        mma_blk<true, false, VS>(aP[j], sdO, LS, 16 * rb, sRt, LC, 16 * n, l);
-        mma_blk<false, false, VS>(aDA[j], sdYt, LC, 16 * rb, sRt, LC, 16 * n, l);
-      }
-  #pragma unroll
-      for (int j = 0; j < HV; ++j) {
-        const int vc = 16 * (HV * hf + j) + acc_col(l), r0 = 16 * rb + 4 * (l >> 4);
-        float dy[4], vv[4];
-        run4(sdYt, LC, vc, r0, dy);
-        acc_vals(sV, LS, 16 * rb, 16 * (HV * hf + j), vv, l);
-  #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          dbV[i] += dy[i] * vv[i];
-          sdv[(r0 + i) * LS + vc] = from_f<T>(sB[r0 + i] * dy[i]);
-        }
-      }
-      // group B: dO S0^T, R dS_C^T, dY S0^T, <dS_C, S0> (the last from the registers: each thread holds the same
-      // elements of both tiles)
-      rs0.store_t(sS0t, LK, tid);
-      rdsc.store_t(sdSCt, LK, tid);
-  #pragma unroll
-      for (int i = 0; i < decltype(rs0)::N; ++i)
-        if (decltype(rs0)::NVEC % ITH == 0 || tid + i * ITH < decltype(rs0)::NVEC)  // loaded by this thread
-  #pragma unroll
-          for (int e = 0; e < 8; ++e) sdot += to_f(rdsc.r[i][e]) * to_f(rs0.r[i][e]);
-      if (vs == 0) {
-        tq.store(sQ, LK, tid);
-        tk.store(sK, LK, tid);
-        if constexpr (SEPU) tu.store(sU, LK, tid);
-      }
-      __syncthreads();
-      if (vs + VS < V) load_b(cidx, vs + VS);
-      s2g_rows<T, CH, VS, ITH, INTRA_NT>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, nvalid, tid);
-  #pragma unroll
-      for (int j = 0; j < HK; ++j) {
-        const int n = HK * hf + j;
-        mma_blk<true, false, VS>(aQg[j], sdO, LS, 16 * rb, sS0t, LK, 16 * n, l);
-        mma_blk<false, false, VS>(aKd[j], sRt, LC, 16 * rb, sdSCt, LK, 16 * n, l);
-        mma_blk<false, false, VS>(aKY[j], sdYt, LC, 16 * rb, sS0t, LK, 16 * n, l);
-      }
-      __syncthreads();
+    for (int j = 0; j < HC; ++j) {
+      const int n = HC * hf + j;
+      mma_blk<true, false, VS>(aP[j], sdO, LS, 16 * rb, sRt, LC, 16 * n, l);
+      mma_blk<false, false, VS>(aDA[j], sdYt, LC, 16 * rb, sRt, LC, 16 * n, l);
     }
+#pragma unroll
+    for (int j = 0; j < HV; ++j) {
+      const int vc = 16 * (HV * hf + j) + acc_col(l), r0 = 16 * rb + 4 * (l >> 4);
+      float dy[4], vv[4];
+      run4(sdYt, LC, vc, r0, dy);
+      acc_vals(sV, LS, 16 * rb, 16 * (HV * hf + j), vv, l);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dbV[i] += dy[i] * vv[i];
+        sdv[(r0 + i) * LS + vc] = from_f<T>(sB[r0 + i] * dy[i]);
+      }
+    }
+    // group B: dO S0^T, R dS_C^T, dY S0^T, <dS_C, S0> (the last from the registers: each thread holds the same
+    // elements of both tiles)
+    rs0.store_t(sS0t, LK, tid);
+    rdsc.store_t(sdSCt, LK, tid);
+#pragma unroll
+    for (int i = 0; i < decltype(rs0)::N; ++i)
+      if (decltype(rs0)::NVEC % ITH == 0 || tid + i * ITH < decltype(rs0)::NVEC)  // loaded by this thread
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sdot += to_f(rdsc.r[i][e]) * to_f(rs0.r[i][e]);
+    if (vs == 0) {
+      tq.store(sQ, LK, tid);
+      tk.store(sK, LK, tid);
+      if constexpr (SEPU) tu.store(sU, LK, tid);
+    }
+    __syncthreads();
+    if (vs + VS < V) load_b(cidx, vs + VS);
+    s2g_rows<T, CH, VS, ITH, INTRA_NT>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, nvalid, tid);
+#pragma unroll
+    for (int j = 0; j < HK; ++j) {
+      const int n = HK * hf + j;
+      mma_blk<true, false, VS>(aQg[j], sdO, LS, 16 * rb, sS0t, LK, 16 * n, l);
+      mma_blk<false, false, VS>(aKd[j], sRt, LC, 16 * rb, sdSCt, LK, 16 * n, l);
+      mma_blk<false, false, VS>(aKY[j], sdYt, LC, 16 * rb, sS0t, LK, 16 * n, l);
+    }
+    __syncthreads();
   }
   // block reduce <dS_C, S0>
   {
@@ -625,10 +485,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   for (int j = 0; j < HC; ++j) {
     const int n = HC * hf + j;
     f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
-    float pv[4] = {0.f, 0.f, 0.f, 0.f};  // RB: P from LDS (P_rc = s (q_r . u_c) e), so w (Q U^T) = dP P
     mma_blk<true, true, K>(kk, sK, LK, 16 * rb, sU, LK, 16 * n, l);
-    if constexpr (RB) acc_vals(sP, LC, 16 * rb, 16 * n, pv, l);
-    else mma_blk<true, true, K>(qk, sQ, LK, 16 * rb, sU, LK, 16 * n, l);
+    mma_blk<true, true, K>(qk, sQ, LK, 16 * rb, sU, LK, 16 * n, l);
     f32x4 z, Dt, Wt;
     const int cc = 16 * n + acc_col(l);
     const float Gc = sG[cc];
@@ -647,7 +505,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       Dt[i] = Dv;
       Wt[i] = wv;
       dbA[i] += uu * kk[i];
-      z[i] = (RB ? aP[j][i] * pv[i] : wv * qk[i]) + Dv * kk[i];
+      z[i] = wv * qk[i] + Dv * kk[i];
       rz[i] += z[i];
     }
     // the lane's four rows of column cc are contiguous in the column-major tiles: one vector store each
@@ -750,9 +608,6 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
         sdk[r * LK + d] = from_f<T>(t[j][i] - bet[i] * gam[i] * aKY[j][i]);
       }
   }
-  // RB: the next chunk's Q, K (U) go out now, their registers free since the chunk start (the rebuild in its
-  // first slab needs them in LDS)
-  if constexpr (RB) load_qk(cnext);
   // dbeta and the per-row part of dG (first half, one lane per row)
   if (hf == 0 && (l & 15) == 0) {
 #pragma unroll
@@ -833,8 +688,7 @@ static hipError_t bwd_intra_kv(const ChunkArgs& a) {
   bwd_intra_kernel<T, K, V, VS, SEPU><<<grid, ITH, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
       static_cast<const T*>(a.v), a.beta, static_cast<const T*>(a.dout),
-      a.ws.Gc, static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P),
-      static_cast<const T*>(a.ws.hs), static_cast<const T*>(a.ws.Rs), static_cast<const T*>(a.ws.dhs),
+      a.ws.Gc, static_cast<const T*>(a.ws.hs), static_cast<const T*>(a.ws.Rs), static_cast<const T*>(a.ws.dhs),
       static_cast<const T*>(a.ws.dYs), static_cast<T*>(a.dq), static_cast<T*>(a.dk), static_cast<T*>(a.du),
       static_cast<T*>(a.dv), a.dg, a.dbeta, a.T, a.H, a.NT, a.B * a.H, a.scale);
   return hipGetLastError();

@@ -10,8 +10,7 @@
 // waves never exchange state; only the chunk inputs are shared through LDS.  The next chunk's inputs are
 // prefetched into registers one chunk ahead.
 // MODE 0 writes O (and hT); MODE 1 (recompute for the backward) writes instead the state entering every chunk
-// (and, in fp32, R), in the fragment layout straight from the accumulators; MODE 2 (training forward) writes both
-// O and those.  (bf16 stores no R: the gradient kernel rebuilds it, see rebuilds_r_dy.)
+// and R, in the fragment layout straight from the accumulators; MODE 2 (training forward) writes both.
 // MODE 3 (the prefix pass of a segmented sweep) writes only the final state, and the grid carries K more columns
 // per head: those "identity" blocks start from S = I with V = 0, so their final state is the segment's transition
 // Phi = prod_c (gamma_C I - K^T diag(exp(G_C - G)) Tm diag(beta gamma) K), written to phi [BH][K][K].  The
@@ -201,8 +200,7 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
     }
     const F Rbmine = frag_acc2<T>(R[0], R[1]);
     if constexpr (OUT) xR[w][l] = Rbmine;
-    if constexpr (SAVE && !rebuilds_r_dy<T>())
-      store_fragblk<T, FWD_NT_STORE>(wsR + cidx * CH * V, CH, hf, cb, ncb, Rbmine);
+    if constexpr (SAVE) store_fragblk<T, FWD_NT_STORE>(wsR + cidx * CH * V, CH, hf, cb, ncb, Rbmine);
     __syncthreads();  // R and Rd fragments of both halves exchanged
     if (c + 1 < NT) prefetch2(c + 1);
     const F Rdother = xRd[w ^ NSL][l];

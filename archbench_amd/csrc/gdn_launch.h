@@ -22,13 +22,6 @@ struct StepArgs {
   hipStream_t stream;
 };
 
-// The bf16 gradient kernel rebuilds R and dY itself from tiles it stages anyway (K, the entering state, the leaving
-// state's gradient, V, dO) and the chunk factors Tm and P, so in bf16 the forward sweep stores no R, the reverse
-// sweep no dY, and neither is in the stash or the backward workspace.  The fp32 kernels keep both.
-template <typename T>
-constexpr bool rebuilds_r_dy() { return sizeof(T) == 2; }
-inline bool rebuilds_r_dy(int dtype) { return dtype == DT_BF16; }
-
 // Chunk workspace carve-up (chunk-major: [B*H][NT][...]).  All offsets are 256-byte aligned.
 // Parts: WS_FACT = {Tm, P, Gc} (the chunk factors kernel), WS_STATE = {hs, Rs} (the stashing forward or the
 // recompute sweep), WS_GRAD = {dhs, dYs} (the reverse sweep); the gradient kernel reads Gc, hs, Rs, dhs, dYs.
@@ -38,9 +31,9 @@ struct ChunkWs {
   void* P;    // [BH][NT][64][64]   s (Q K^T) o exp(G_i - G_j), lower triangle incl. diagonal, input dtype
   float* Gc;  // [BH][NT][64]       chunk-local cumulative log-decay
   void* hs;   // [BH][NT][K][V]     state entering each chunk
-  void* Rs;   // [BH][NT][64][V]    R = U - W S per chunk (fp32 only; see rebuilds_r_dy)
+  void* Rs;   // [BH][NT][64][V]    R = U - W S per chunk
   void* dhs;  // [BH][NT][K][V]     dL/d(state leaving each chunk)
-  void* dYs;  // [BH][NT][64][V]    dY = Tm^T dL/dR per chunk (the gradient w.r.t. Y, R = Tm Y; fp32 only)
+  void* dYs;  // [BH][NT][64][V]    dY = Tm^T dL/dR per chunk (the gradient w.r.t. Y, R = Tm Y)
   // segmented sweeps (WS_SEGF, WS_SEGB; see segment_count), fp32, in the segmented [B*NS, H, ...] layout:
   float* phi;    // [B*NS][H][K][K]  transition of each segment
   float* sloc;   // [B*NS][H][K][V]  state leaving each segment from a zero entering state

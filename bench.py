@@ -89,26 +89,24 @@ def stage_flops(stage: str, K: int, V: int) -> int:
         "fwd_stash": 6 * K * V + 4 * C * V,                  # the same, states and R also written
         "bwd_recompute": 4 * K * V + 2 * C * V,              # K S, K^T R; Tm Y
         "bwd_state": 6 * K * V + 4 * C * V,                  # K dS, Q^T dO, K^T Z; P^T dO, Tm^T dR
-        "bwd_intra": 10 * K * V + 10 * C * V + 10 * C * K,   # rebuild: K S0, U dSC, P^T dO, Tm Y, Tm^T dR;
-                                                             # dO S0^T, R dSC^T, dY S0^T; dO R^T, dY R^T;
-                                                             # K K^T, dPm K, dPm^T Q, D K, D^T K
+        "bwd_intra": 6 * K * V + 4 * C * V + 12 * C * K,     # dO S0^T, R dSC^T, dY S0^T; dO R^T, dY R^T;
+                                                             # K K^T, Q K^T, dPm K, dPm^T Q, D K, D^T K
     }.get(stage, 0)
 
 
 def stage_bytes(stage: str, K: int, V: int, es: int = 2) -> int:
-    """Design HBM bytes per token-head of each kernel (bf16: the gradient kernel rebuilds R and dY, so neither
-    is stored or read): every input and workspace buffer read once, every output written once (q, k: es*K; v, o,
-    dO, dv: es*V; g, beta, G, dg, dbeta: 4; Tm, P: es*C per token; a chunk's state or state gradient: es*K*V/C
-    per token).  The second V-block workgroup's reads of q, k, Tm and P in the sweeps, which hit L2, count
-    once."""
+    """Design HBM bytes per token-head of each kernel: every input and workspace buffer read once, every output
+    written once (q, k: es*K; v, o, dO, dv, R, dY: es*V; g, beta, G, dg, dbeta: 4; Tm, P: es*C per token; a
+    chunk's state or state gradient: es*K*V/C per token).  The second V-block workgroup's reads of q, k, Tm
+    and P in the sweeps, which hit L2, count once."""
     qk, vv, st, tm = es * K, es * V, es * K * V // C, es * C
     return {
         "factors": 2 * qk + 8 + 2 * tm + 4,                  # q k g beta -> Tm P G
         "fwd": 2 * qk + vv + 8 + 2 * tm + vv,                # q k v beta G Tm P -> o
-        "fwd_stash": 2 * qk + vv + 8 + 2 * tm + vv + st,     # ... -> o, states
-        "bwd_recompute": qk + vv + 8 + tm + st,              # k v beta G Tm -> states
-        "bwd_state": 2 * qk + vv + 8 + 2 * tm + st,          # q k dO beta G Tm P -> dstates
-        "bwd_intra": 2 * qk + 2 * vv + 8 + 2 * st + 2 * tm + 2 * qk + vv + 8,  # q k v dO beta G S0 dSC Tm P ->
+        "fwd_stash": 2 * qk + vv + 8 + 2 * tm + vv + st + vv,  # ... -> o, states, R
+        "bwd_recompute": qk + vv + 8 + tm + st + vv,         # k v beta G Tm -> states, R
+        "bwd_state": 2 * qk + vv + 8 + 2 * tm + st + vv,     # q k dO beta G Tm P -> dstates, dY
+        "bwd_intra": 2 * qk + 2 * vv + 8 + 2 * st + 2 * vv + 2 * qk + vv + 8,  # q k v dO beta G S0 dSC R dY ->
                                                                              # dq dk dv dg dbeta
     }.get(stage, 0)
 

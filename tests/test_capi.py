@@ -49,12 +49,8 @@ def test_workspace_sizes():
     BH, NT = 8 * 16, 64
     # the forward's workspace holds the chunk factors: Tm and P (64x64 each), G (64 fp32) per chunk
     assert fwd == BH * NT * (2 * 64 * 64 * 2 + 64 * 4)
-    # the backward adds the entering and leaving state (K x V) per chunk (in bf16 the gradient kernel rebuilds R
-    # and dY itself, so neither is stored)
-    assert bwd == fwd + BH * NT * (2 * 128 * 128 * 2)
-    # fp32 keeps R and dY (64 x V each) per chunk too
-    f32 = _lib.ws_bytes("fwd", 2, 256, 2, 64, 64, torch.float32)
-    assert _lib.ws_bytes("bwd", 2, 256, 2, 64, 64, torch.float32) == f32 + 4 * 4 * (2 * 64 * 64 * 4 + 2 * 64 * 64 * 4)
+    # the backward adds the entering and leaving state (K x V), R and dR (64 x V) per chunk
+    assert bwd == fwd + BH * NT * (2 * 128 * 128 * 2 + 2 * 64 * 128 * 2)
     # ragged T rounds up to whole chunks
     assert _lib.ws_bytes("bwd", 1, 65, 1, 64, 64, torch.float32) == 2 * _lib.ws_bytes("bwd", 1, 64, 1, 64, 64,
                                                                                         torch.float32)
@@ -67,8 +63,8 @@ def test_stash_sizes_split_the_backward_workspace():
         assert stash + grad == _lib.ws_bytes("bwd", *args)
     B, T, H, K, V = 8, 4096, 16, 128, 128
     stash, grad = _lib.stash_bytes(B, T, H, K, V, torch.bfloat16)
-    # per chunk: Tm and P (64x64 bf16 each), G (64 fp32), entering state (K x V bf16)
-    assert stash == B * H * 64 * (2 * 64 * 64 * 2 + 64 * 4 + K * V * 2)
+    # per chunk: Tm and P (64x64 bf16 each), G (64 fp32), entering state (K x V bf16), R (64 x V bf16)
+    assert stash == B * H * 64 * (2 * 64 * 64 * 2 + 64 * 4 + K * V * 2 + 64 * V * 2)
 
 
 def test_stashed_backward_rejects_missing_stash():
