@@ -35,6 +35,7 @@ SIGNATURES = {
                            _i, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_chunk_fwd_noalloc": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_chunk_stash_bytes": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
+    "gdn_nsgdn_stash_bytes": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "gdn_chunk_fwd_stash": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _i, _i, _i, _i, _i, _f, _i, _p]),
     "gdn_chunk_bwd_stashed": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p, _sz,
                                    _i, _i, _i, _i, _i, _f, _i, _p]),
@@ -175,16 +176,19 @@ def _device_index() -> int:
     return torch.cuda.current_device() if torch.cuda.is_available() else -1
 
 
-def stash_bytes(B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype) -> tuple[int, int]:
-    """(stash bytes for gdn_chunk_fwd_stash, workspace bytes for gdn_chunk_bwd_stashed)."""
-    return _stash_bytes(B, T, H, K, V, dtype, _device_index())
+def stash_bytes(B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype, nsgdn: bool = False) -> tuple[int, int]:
+    """(stash bytes for gdn_chunk_fwd_stash, workspace bytes for gdn_chunk_bwd_stashed); with nsgdn, the sizes of
+    the separate-write-key pair gdn_nsgdn_chunk_fwd / _bwd."""
+    return _stash_bytes(B, T, H, K, V, dtype, nsgdn, _device_index())
 
 
 @functools.lru_cache(maxsize=1024)
-def _stash_bytes(B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype, dev: int) -> tuple[int, int]:
+def _stash_bytes(B: int, T: int, H: int, K: int, V: int, dtype: torch.dtype, nsgdn: bool,
+                 dev: int) -> tuple[int, int]:
     st, ws = _sz(0), _sz(0)
-    check(load().gdn_chunk_stash_bytes(B, T, H, K, V, dtype_code(dtype), ctypes.byref(st), ctypes.byref(ws)),
-          "gdn_chunk_stash_bytes")
+    fn = load().gdn_nsgdn_stash_bytes if nsgdn else load().gdn_chunk_stash_bytes
+    check(fn(B, T, H, K, V, dtype_code(dtype), ctypes.byref(st), ctypes.byref(ws)),
+          "gdn_nsgdn_stash_bytes" if nsgdn else "gdn_chunk_stash_bytes")
     return st.value, ws.value
 
 

@@ -33,7 +33,7 @@ static bool misaligned(const P*... p) {
 }
 
 size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, ChunkWs* carve, void* base,
-                      int ns) {
+                      int ns, int hstride) {
   const size_t es = dtype == DT_BF16 ? 2 : 4;
   const size_t NT = (size_t)(T + CH_TOKENS - 1) / CH_TOKENS;
   const size_t BH = (size_t)B * H;
@@ -51,7 +51,9 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
     ws.Gc = static_cast<float*>(take(BH * NT * CH_TOKENS * 4));
   }
   if (parts & WS_STATE) {
-    ws.hs = take(BH * NT * (size_t)K * V * es);
+    // states of every hstride-th chunk of each swept sequence (a segment when ns > 1; segments hold whole pairs)
+    const size_t nts = ns > 1 ? NT / ns : NT;
+    ws.hs = take(BH * (size_t)(ns > 1 ? ns : 1) * ((nts + hstride - 1) / hstride) * (size_t)K * V * es);
     ws.Rs = take(BH * NT * CH_TOKENS * (size_t)V * es);
   }
   if (parts & WS_GRAD) {
@@ -278,7 +280,7 @@ int gdn_chunk_fwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t*
   g_err[0] = 0;
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
-  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT | WS_SEGF, nullptr, nullptr, segment_count(B, T, H, K, V));
+  *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT | WS_SEGF, nullptr, nullptr, segment_count(B, T, H, K, V), 1);
   return GDN_OK;
 }
 
@@ -287,19 +289,29 @@ int gdn_chunk_bwd_ws_bytes(int B, int T, int H, int K, int V, int dtype, size_t*
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!bytes) return fail(GDN_ERR_ARG, "bytes is NULL");
   *bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT | WS_STATE | WS_GRAD | WS_SEGF | WS_SEGB, nullptr, nullptr,
-                          segment_count(B, T, H, K, V));
+                          segment_count(B, T, H, K, V), state_stride(V, dtype, false));
+  return GDN_OK;
+}
+
+static int stash_sizes(int B, int T, int H, int K, int V, int dtype, bool sepu, size_t* stash_bytes,
+                       size_t* bwd_ws_bytes) {
+  g_err[0] = 0;
+  if (int e = check_common(B, T, H, K, V, dtype)) return e;
+  if (!stash_bytes || !bwd_ws_bytes) return fail(GDN_ERR_ARG, "stash_bytes or bwd_ws_bytes is NULL");
+  const int ns = segment_count(B, T, H, K, V), hs = state_stride(V, dtype, sepu);
+  *stash_bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH, nullptr, nullptr, ns, hs);
+  *bwd_ws_bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_GRAD | WS_SEGB, nullptr, nullptr, ns, hs);
   return GDN_OK;
 }
 
 int gdn_chunk_stash_bytes(int B, int T, int H, int K, int V, int dtype, size_t* stash_bytes,
                           size_t* bwd_ws_bytes) {
-  g_err[0] = 0;
-  if (int e = check_common(B, T, H, K, V, dtype)) return e;
-  if (!stash_bytes || !bwd_ws_bytes) return fail(GDN_ERR_ARG, "stash_bytes or bwd_ws_bytes is NULL");
-  const int ns = segment_count(B, T, H, K, V);
-  *stash_bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH, nullptr, nullptr, ns);
-  *bwd_ws_bytes = chunk_ws_bytes(B, T, H, K, V, dtype, WS_GRAD | WS_SEGB, nullptr, nullptr, ns);
-  return GDN_OK;
+  return stash_sizes(B, T, H, K, V, dtype, false, stash_bytes, bwd_ws_bytes);
+}
+
+int gdn_nsgdn_stash_bytes(int B, int T, int H, int K, int V, int dtype, size_t* stash_bytes,
+                          size_t* bwd_ws_bytes) {
+  return stash_sizes(B, T, H, K, V, dtype, true, stash_bytes, bwd_ws_bytes);
 }
 
 }  // extern "C"
@@ -348,7 +360,9 @@ static int chunk_fwd_impl(const void* q, const void* k, const void* u, const voi
     return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   ChunkArgs a{};
   const int ns = segments ? segment_count(B, T, H, K, V) : 1;
-  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, stash ? WS_STASH : (WS_FACT | WS_SEGF), &a.ws, ws, ns);
+  a.hstride = state_stride(V, dtype, u != nullptr);
+  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, stash ? WS_STASH : (WS_FACT | WS_SEGF), &a.ws, ws, ns,
+                                     a.hstride);
   if (!ws || ws_bytes < need)
     return fail(GDN_ERR_WORKSPACE, "%s of %zu bytes needed, %zu given", stash ? "stash" : "workspace", need,
                 ws ? ws_bytes : (size_t)0);
@@ -390,15 +404,17 @@ static int chunk_bwd_impl(const void* q, const void* k, const void* u, const voi
     return fail(GDN_ERR_ARG, "array pointer not 16-byte aligned");
   ChunkArgs a{};
   const int ns = segment_count(B, T, H, K, V);  // as the forward that filled the stash chose
+  a.hstride = state_stride(V, dtype, u != nullptr);
   if (stashed) {
     // the stash is only read (the kernels take it through the same carve-up as the recompute path's workspace)
-    const size_t sneed = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH, &a.ws, const_cast<void*>(stash), ns);
+    const size_t sneed = chunk_ws_bytes(B, T, H, K, V, dtype, WS_STASH, &a.ws, const_cast<void*>(stash), ns,
+                                        a.hstride);
     if (!stash || stash_bytes < sneed)
       return fail(GDN_ERR_WORKSPACE, "stash of %zu bytes needed, %zu given", sneed,
                   stash ? stash_bytes : (size_t)0);
   }
   const int parts = stashed ? (WS_GRAD | WS_SEGB) : (WS_FACT | WS_STATE | WS_GRAD | WS_SEGF | WS_SEGB);
-  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, parts, &a.ws, ws, ns);
+  const size_t need = chunk_ws_bytes(B, T, H, K, V, dtype, parts, &a.ws, ws, ns, a.hstride);
   if (!ws || ws_bytes < need)
     return fail(GDN_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws ? ws_bytes : (size_t)0);
   a.q = q; a.k = k; a.u = u; a.v = v; a.g = g; a.beta = beta; a.h0 = h0;
@@ -489,7 +505,7 @@ int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const flo
   if (int e = check_common(B, T, H, K, V, dtype)) return e;
   if (!chunk_shape_supported(K, V, dtype)) return shape_error(K, V, dtype);
   const size_t cap = GDN_NOALLOC_SCRATCH_BYTES;
-  const size_t one = chunk_ws_bytes(1, T, H, K, V, dtype, WS_FACT, nullptr, nullptr, 1);
+  const size_t one = chunk_ws_bytes(1, T, H, K, V, dtype, WS_FACT, nullptr, nullptr, 1, 1);
   if (one > cap)
     return fail(GDN_ERR_WORKSPACE, "one sequence needs %zu bytes of chunk factors (H * ceil(T/64) = %lld chunks), "
                 "more than the %zu-byte scratch of the allocation-free forward; use gdn_chunk_fwd", one,
@@ -500,11 +516,11 @@ int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const flo
   // scratch.  Splitting the batch moves every pointer by whole sequences, which keeps the 16-byte alignment the
   // kernels need as long as a sequence's g / beta rows (T * H fp32) are a multiple of 16 bytes.
   int nb = (int)std::min<size_t>((size_t)(B > 0 ? B : 1), cap / one);
-  while (nb > 1 && chunk_ws_bytes(nb, T, H, K, V, dtype, WS_FACT, nullptr, nullptr, 1) > cap) --nb;
+  while (nb > 1 && chunk_ws_bytes(nb, T, H, K, V, dtype, WS_FACT, nullptr, nullptr, 1, 1) > cap) --nb;
   if (nb < B && ((size_t)T * H * 4) % 16 != 0)
     return fail(GDN_ERR_WORKSPACE, "B=%d sequences need %zu bytes of chunk factors, more than the %zu-byte scratch, "
                 "and T * H = %lld is not a multiple of 4, so the batch cannot be split; use gdn_chunk_fwd", B,
-                chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT, nullptr, nullptr, 1), cap, (long long)T * H);
+                chunk_ws_bytes(B, T, H, K, V, dtype, WS_FACT, nullptr, nullptr, 1, 1), cap, (long long)T * H);
   const size_t es = dtype == DT_BF16 ? 2 : 4;
   const char* cq = static_cast<const char*>(q);
   const char* ck = static_cast<const char*>(k);

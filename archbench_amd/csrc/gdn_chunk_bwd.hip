@@ -266,7 +266,7 @@ __device__ __forceinline__ float colsum_tile(const f32x4& x) {
 constexpr int IW = 2 * NWAVE;  // waves of the intra kernel
 constexpr int ITH = IW * 64;   // its threads
 
-template <typename T, int K, int V, int VS, bool SEPU>
+template <typename T, int K, int V, int VS, bool SEPU, bool HALF>
 __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u, const T* __restrict__ v,
     const float* __restrict__ beta, const T* __restrict__ dout, const float* __restrict__ wsGc,
@@ -291,6 +291,11 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   __shared__ __attribute__((aligned(16))) T sdv[CH * LS];  // dv of the current slab, for the coalesced store
   __shared__ float sG[CH], sB[CH], sdG[CH], sLast[CH], sColZ[NWAVE][CH], sRed[IW];
   __shared__ float sRow[2][6][CH];  // per-half row sums: rq, rk, dbV, rx, dbA, rz
+  // HALF (state stride 2): the stash holds the state entering even chunks only; an even chunk advances it through
+  // itself into sS1t (the odd chunk's entering state, S1^T [V][LK]) with exp(G_C - G) per row from sDte
+  static_assert(!HALF || (sizeof(T) == 2 && !SEPU), "state stride 2: bf16 without separate write keys");
+  __shared__ __attribute__((aligned(16))) T sS1t[HALF ? V * LK : 8];
+  __shared__ float sDte[HALF ? CH : 1];
 
   T* sdO = slab;
   T* sV = sdO + CH * LS;
@@ -301,7 +306,27 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
   const int rb = w & (NWAVE - 1), hf = w >> 2;
-  const int nchunk = BH * NT;
+  // work items: chunks, or (HALF) pairs of chunks (2 j, 2 j + 1) of one sequence, the second if it exists
+  const int NT2 = HALF ? (NT + 1) / 2 : NT;
+  const int nitem = BH * NT2;
+  auto item_chunk = [&](int it) {  // the first chunk of work item it
+    if constexpr (HALF) {
+      const int bh_ = (int)((unsigned)it / (unsigned)NT2);
+      return bh_ * NT + 2 * (it - bh_ * NT2);
+    } else {
+      return it;
+    }
+  };
+  auto chunk_pos = [&](int ci_) { return ci_ - (int)((unsigned)ci_ / (unsigned)NT) * NT; };  // chunk in sequence
+  // the stash slot of chunk ci's entering state (HALF: even chunks only)
+  auto state_slot = [&](int ci_) -> int64_t {
+    if constexpr (HALF) {
+      const int bh_ = (int)((unsigned)ci_ / (unsigned)NT);
+      return (int64_t)bh_ * NT2 + (ci_ - bh_ * NT) / 2;
+    } else {
+      return ci_;
+    }
+  };
   // thread index and lane, re-derived opaquely in every chunk iteration (see the lane-dependent helpers)
   int tid = threadIdx.x, l = tid & 63;
 
@@ -327,8 +352,10 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     rr.load(wsR + ci * CH * V, V / 16, vs / 16, tid);
     rdy.load(wsdY + ci * CH * V, V / 16, vs / 16, tid);
   };
-  auto load_b = [&](int64_t ci, int vs) {
-    rs0.load(wsH + ci * K * V, V / 16, vs / 16, tid);
+  // group B: the entering state (not read for the odd chunk of a HALF pair: s0 false) and the leaving state's
+  // gradient
+  auto load_b = [&](int64_t ci, int vs, bool s0) {
+    rs0.load(wsH + state_slot((int)ci) * K * V, V / 16, vs / 16, tid, s0);
     rdsc.load(wsdH + ci * K * V, V / 16, vs / 16, tid);
   };
   // The reads a chunk needs first: G, beta and the first slab's groups.  The workgroups are persistent (one per
@@ -336,6 +363,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   // no global memory: the loads are served while the K phase computes (group A at the K phase's start, group B
   // after its first barrier: issued together, the waves stalled on the memory queue instead of computing).
   float pg, pb;
+  auto is_odd = [&](int ci_) { return HALF && (chunk_pos(ci_) & 1); };
   auto load_first = [&](int ci, bool order, bool with_b) {
     int nv;
     const int64_t r0 = chunk_rows(ci, nv);
@@ -351,23 +379,35 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (with_b) load_b(ci, 0);
+    if (with_b) load_b(ci, 0, !is_odd(ci));
   };
-  if ((int)blockIdx.x < nchunk) load_first(blockIdx.x, true, true);
+  if ((int)blockIdx.x < nitem) load_first(item_chunk(blockIdx.x), true, true);
 
 #pragma unroll 1
-  for (int ci = blockIdx.x; ci < nchunk; ci += gridDim.x) {
+  for (int it = blockIdx.x, ci = item_chunk(it); it < nitem;) {
   asm volatile("" : "+v"(tid));
   l = tid & 63;
   int nvalid;
   const int64_t row0 = chunk_rows(ci, nvalid);
   const int64_t cidx = ci;
+  // HALF: odd chunks take their entering state from sS1t; an even chunk with an odd partner fills it
+  const bool odd = is_odd(ci);
+  const bool advance = HALF && !odd && chunk_pos(ci) + 1 < NT;
+  // the next chunk: this pair's odd one, else the next item's first (or this chunk again after the last item:
+  // the prefetch stays unconditional)
+  const bool in_pair = advance;
+  const int it_next = in_pair ? it : it + (int)gridDim.x;
+  const int cnext = in_pair ? ci + 1 : (it_next < nitem ? item_chunk(it_next) : ci);
   tq.load(q + row0 * K, (int64_t)H * K, nvalid, tid);
   tk.load(k + row0 * K, (int64_t)H * K, nvalid, tid);
   if constexpr (SEPU) tu.load(u + row0 * K, (int64_t)H * K, nvalid, tid);
   if (tid < CH) {
     sG[tid] = pg;
     sB[tid] = tid < nvalid ? pb : 0.f;
+    if constexpr (HALF) {
+      const float gl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pg), CH - 1));  // G_C (wave 0)
+      sDte[tid] = __expf(gl - pg);
+    }
   }
 
   // ---- V phase: contractions over V, slab by slab -------------------------------------------------------
@@ -411,27 +451,62 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     }
     // group B: dO S0^T, R dS_C^T, dY S0^T, <dS_C, S0> (the last from the registers: each thread holds the same
     // elements of both tiles)
-    rs0.store_t(sS0t, LK, tid);
     rdsc.store_t(sdSCt, LK, tid);
+    if (HALF && odd) {  // the entering state is the even chunk's advance in sS1t (rs0 loaded nothing)
+      sdot += rdsc.dot_t(sS1t + vs * LK, LK, tid);
+    } else {
+      rs0.store_t(sS0t, LK, tid);
 #pragma unroll
-    for (int i = 0; i < decltype(rs0)::N; ++i)
-      if (decltype(rs0)::NVEC % ITH == 0 || tid + i * ITH < decltype(rs0)::NVEC)  // loaded by this thread
+      for (int i = 0; i < decltype(rs0)::N; ++i)
+        if (decltype(rs0)::NVEC % ITH == 0 || tid + i * ITH < decltype(rs0)::NVEC)  // loaded by this thread
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sdot += to_f(rdsc.r[i][e]) * to_f(rs0.r[i][e]);
+          for (int e = 0; e < 8; ++e) sdot += to_f(rdsc.r[i][e]) * to_f(rs0.r[i][e]);
+    }
     if (vs == 0) {
       tq.store(sQ, LK, tid);
       tk.store(sK, LK, tid);
       if constexpr (SEPU) tu.store(sU, LK, tid);
     }
     __syncthreads();
-    if (vs + VS < V) load_b(cidx, vs + VS);
+    if (vs + VS < V) load_b(cidx, vs + VS, !odd);
     s2g_rows<T, CH, VS, ITH, INTRA_NT>(dv + row0 * V + vs, (int64_t)H * V, sdv, LS, nvalid, tid);
+    const T* s0t = HALF && odd ? sS1t + vs * LK : sS0t;  // S0^T of this slab
 #pragma unroll
     for (int j = 0; j < HK; ++j) {
       const int n = HK * hf + j;
-      mma_blk<true, false, VS>(aQg[j], sdO, LS, 16 * rb, sS0t, LK, 16 * n, l);
+      mma_blk<true, false, VS>(aQg[j], sdO, LS, 16 * rb, s0t, LK, 16 * n, l);
       mma_blk<false, false, VS>(aKd[j], sRt, LC, 16 * rb, sdSCt, LK, 16 * n, l);
-      mma_blk<false, false, VS>(aKY[j], sdYt, LC, 16 * rb, sS0t, LK, 16 * n, l);
+      mma_blk<false, false, VS>(aKY[j], sdYt, LC, 16 * rb, s0t, LK, 16 * n, l);
+    }
+    if constexpr (HALF) {
+      if (advance) {
+        // S1 = gamma_C S0 + (diag(exp(G_C - G)) K)^T R over this slab's columns, the odd chunk's entering state
+        // (the forward sweep's update, nsgdn.py:240-249): [K] x [VS] in 16 x 16 tiles, wave w taking NA tiles of
+        // one row tile so that one A operand serves them all; S1^T to sS1t in the column-major layout of sS0t
+        constexpr int NA = NKT * NVT / IW;
+        static_assert(NA >= 1 && NVT % NA == 0, "whole runs of column tiles per wave");
+        using V4 = typename std::conditional<sizeof(T) == 2, bf16x4, f32x4>::type;
+        const int rt = (w * NA) / NVT, ct0 = w * NA - rt * NVT;
+        const float gC = __expf(sG[CH - 1]);
+        typename Frag<T>::type a[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          a[kb] = frag_oct(sK, LK, 16 * rt, 32 * kb, l);  // (row d of K^T, token t) = K[t][d], scaled by exp(G_C - G_t)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[kb][e] = from_f<T>(to_f(a[kb][e]) * sDte[32 * kb + 8 * (l >> 4) + e]);
+        }
+#pragma unroll
+        for (int m = 0; m < NA; ++m) {
+          const int ct = ct0 + m, d0 = 16 * rt + 4 * (l >> 4), vc = 16 * ct + (l & 15);
+          float s0[4];
+          run4(sS0t, LK, vc, d0, s0);
+          f32x4 acc = {gC * s0[0], gC * s0[1], gC * s0[2], gC * s0[3]};
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) mma(acc, a[kb], frag_kc(sRt, LC, 16 * ct, 32 * kb, l));
+          *reinterpret_cast<V4*>(sS1t + (vs + vc) * LK + d0) =
+              V4{from_f<T>(acc[0]), from_f<T>(acc[1]), from_f<T>(acc[2]), from_f<T>(acc[3])};
+        }
+      }
     }
     __syncthreads();
   }
@@ -445,7 +520,6 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   // The next chunk's reads are issued unconditionally (the last chunk of a workgroup reads its own chunk again,
   // 0.3% of the traffic): after a conditional block the compiler could not count the loads in flight and would
   // wait for all of them at the first reuse of a register of the chunk's earlier reads.
-  const int cnext = ci + (int)gridDim.x < nchunk ? ci + (int)gridDim.x : ci;
   T* sdq = slab;             // CH x LK   dq staging
   T* sdk = sdq + CH * LK;    // CH x LK   dk staging
   T* sD = sdk + CH * LK;     // CH x LC   D = dA o beta_i E,  column-major (element (r, c) at c * LC + r)
@@ -549,7 +623,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     if ((p & 1) == 0) sRow[hf][f1 >> 2][16 * rb + 4 * lg + (f1 & 3)] = z1;
   }
   __syncthreads();
-  load_b(cnext, 0);
+  load_b(cnext, 0, !is_odd(cnext));
   // dq = s gamma dQg + dPm U.  (Here and below every tile of a product is computed before any is stored: with no
   // LDS store in between, the row block's A fragments are read once for all column tiles.)
   {
@@ -653,6 +727,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     const float total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), 63));
     if (l < nvalid) dg[row0 + (int64_t)l * H] = total - incl + x;
   }
+  it = it_next;
+  ci = cnext;
   }
 }
 
@@ -679,19 +755,28 @@ static hipError_t bwd_state_k(const ChunkArgs& a, bool local) {
   return bwd_state_bv<T, K, SEPU, 64>(a, local);
 }
 
-template <typename T, int K, int V, bool SEPU>
-static hipError_t bwd_intra_kv(const ChunkArgs& a) {
+template <typename T, int K, int V, bool SEPU, bool HALF>
+static hipError_t bwd_intra_launch(const ChunkArgs& a) {
   constexpr int VS = sizeof(T) == 2 ? 64 : 32;
-  // persistent: one workgroup per CU (the LDS use allows no more), each looping over chunks
-  const int nchunk = a.NT * a.B * a.H;
-  dim3 grid(std::min(nchunk, device_cu_count()));
-  bwd_intra_kernel<T, K, V, VS, SEPU><<<grid, ITH, 0, a.stream>>>(
+  // persistent: one workgroup per CU (the LDS use allows no more), each looping over chunks (HALF: chunk pairs)
+  const int nitem = (HALF ? (a.NT + 1) / 2 : a.NT) * a.B * a.H;
+  dim3 grid(std::min(nitem, device_cu_count()));
+  bwd_intra_kernel<T, K, V, VS, SEPU, HALF><<<grid, ITH, 0, a.stream>>>(
       static_cast<const T*>(a.q), static_cast<const T*>(a.k), static_cast<const T*>(a.u),
       static_cast<const T*>(a.v), a.beta, static_cast<const T*>(a.dout),
       a.ws.Gc, static_cast<const T*>(a.ws.hs), static_cast<const T*>(a.ws.Rs), static_cast<const T*>(a.ws.dhs),
       static_cast<const T*>(a.ws.dYs), static_cast<T*>(a.dq), static_cast<T*>(a.dk), static_cast<T*>(a.du),
       static_cast<T*>(a.dv), a.dg, a.dbeta, a.T, a.H, a.NT, a.B * a.H, a.scale);
   return hipGetLastError();
+}
+
+template <typename T, int K, int V, bool SEPU>
+static hipError_t bwd_intra_kv(const ChunkArgs& a) {
+  if constexpr (sizeof(T) == 2 && !SEPU && V <= 128) {
+    if (a.hstride == 2) return bwd_intra_launch<T, K, V, SEPU, true>(a);
+  }
+  if (a.hstride != 1) return hipErrorInvalidValue;  // the stash layout this build's forward would not write
+  return bwd_intra_launch<T, K, V, SEPU, false>(a);
 }
 
 template <typename T, int K, bool SEPU>

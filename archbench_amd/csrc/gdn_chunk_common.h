@@ -244,10 +244,12 @@ struct FragTile {
   static constexpr int NCBS = VS / 16;
   static_assert(R % 32 == 0 && VS % 16 == 0 && NVEC % 64 == 0, "whole fragment blocks only");
   F r[N];
-  // base: the chunk's [R][16 ncb] matrix; bf16 reads go through a buffer resource over it (32-bit offsets)
-  __device__ __forceinline__ void load(const T* base, int ncb, int cb0, int tid) {
-    [[maybe_unused]] const auto rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), 0, R * ncb * 16 * (int)sizeof(T), BUF_RSRC_WORD3);
+  // base: the chunk's [R][16 ncb] matrix; bf16 reads go through a buffer resource over it (32-bit offsets).  With
+  // live false (bf16 only) the resource's range is empty: the loads return zeros and fetch nothing, and the
+  // instruction stream stays the same.
+  __device__ __forceinline__ void load(const T* base, int ncb, int cb0, int tid, bool live = true) {
+    [[maybe_unused]] const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(base), 0, live ? R * ncb * 16 * (int)sizeof(T) : 0, BUF_RSRC_WORD3);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int idx = tid + i * NTH;
@@ -275,6 +277,22 @@ struct FragTile {
         for (int p = 0; p < 8; ++p) dst[fragblk_row(ln >> 4, p) * ld] = r[i][p];
       }
     }
+  }
+  // sum over this thread's elements of r times the same elements of a column-major LDS tile laid out as store_t
+  // writes one (bf16)
+  __device__ __forceinline__ float dot_t(const T* lds, int ldt, int tid) const {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int idx = tid + i * NTH;
+      if (NVEC % NTH == 0 || idx < NVEC) {
+        const int blk = idx >> 6, ln = idx & 63, s = blk / NCBS, cbl = blk - s * NCBS;
+        const T* src = lds + (16 * cbl + (ln & 15)) * ldt + 32 * s + 4 * (ln >> 4);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) acc += to_f(r[i][p]) * to_f(src[p]) + to_f(r[i][4 + p]) * to_f(src[16 + p]);
+      }
+    }
+    return acc;
   }
   // Column-major LDS tile [VS][ldt] (element (row, col) at col * ldt + row): the lane's rows 4g..4g+3 and
   // 16+4g..16+4g+3 are two contiguous runs of 4, written as two vectors.  ldt must be a multiple of 4.

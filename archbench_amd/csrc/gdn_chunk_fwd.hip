@@ -40,7 +40,7 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
     const float* __restrict__ beta,
     const float* __restrict__ h0, const T* __restrict__ gTm, const T* __restrict__ gP,
     const float* __restrict__ gGc, T* __restrict__ o, float* __restrict__ hT, float* __restrict__ phi,
-    T* __restrict__ wsH, T* __restrict__ wsR, int T_, int H, int V, int NT, float scale, int ns) {
+    T* __restrict__ wsH, T* __restrict__ wsR, int T_, int H, int V, int NT, float scale, int ns, int hstride) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
   constexpr int NKT = K / 16;  // row tiles of the state slab
@@ -144,11 +144,17 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
 
     // rows 32 hf .. 32 hf + 31: K S, Q S and Y = diag(beta) (V - diag(gamma) K S)
     F Sb[K / 32];
+    // the state entering every hstride-th chunk goes to the stash (slot c / hstride of the sequence); the branch is
+    // uniform and the stored values come from the accumulators, not from loads in flight
+    const bool keep = (c & (hstride - 1)) == 0;
+    const int64_t hidx = (int64_t)bh * ((NT + hstride - 1) / hstride) + c / hstride;
 #pragma unroll
-    for (int s = 0; s < K / 32; ++s) {
-      Sb[s] = frag_acc2<T>(S[2 * s], S[2 * s + 1]);
-      if constexpr (SAVE) {
-        if ((s & 1) == hf) store_fragblk<T, FWD_NT_STORE>(wsH + cidx * K * V, K, s, cb, ncb, Sb[s]);
+    for (int s = 0; s < K / 32; ++s) Sb[s] = frag_acc2<T>(S[2 * s], S[2 * s + 1]);
+    if constexpr (SAVE) {
+      if (keep) {
+#pragma unroll
+        for (int s = 0; s < K / 32; ++s)
+          if ((s & 1) == hf) store_fragblk<T, FWD_NT_STORE>(wsH + hidx * K * V, K, s, cb, ncb, Sb[s]);
       }
     }
     f32x4 Y[2], QS[2];
@@ -259,7 +265,7 @@ static hipError_t fwd_sweep_bv(const ChunkArgs& a) {
       static_cast<const T*>(a.v), a.beta, a.h0,
       static_cast<const T*>(a.ws.Tm), static_cast<const T*>(a.ws.P), a.ws.Gc, static_cast<T*>(a.o),
       MODE == 1 ? nullptr : a.hT, a.ws.phi, static_cast<T*>(a.ws.hs), static_cast<T*>(a.ws.Rs), a.T, a.H, a.V,
-      a.NT, a.scale, a.ns);
+      a.NT, a.scale, a.ns, a.hstride);
   return hipGetLastError();
 }
 

@@ -22,6 +22,12 @@ struct StepArgs {
   hipStream_t stream;
 };
 
+// The stash keeps the state entering every chunk (stride 1), or entering every even chunk only (stride 2): then the
+// gradient kernel advances each even chunk's state through that chunk itself, S' = gamma_C S + (Kd)^T R, from tiles
+// it already holds, for the odd chunk that follows.  Stride 2 needs one more K x V bf16 tile of LDS in the gradient
+// kernel, which fits for bf16 with V <= 128 and without separate write keys.
+inline int state_stride(int V, int dtype, bool sepu) { return dtype == DT_BF16 && !sepu && V <= 128 ? 2 : 1; }
+
 // Chunk workspace carve-up (chunk-major: [B*H][NT][...]).  All offsets are 256-byte aligned.
 // Parts: WS_FACT = {Tm, P, Gc} (the chunk factors kernel), WS_STATE = {hs, Rs} (the stashing forward or the
 // recompute sweep), WS_GRAD = {dhs, dYs} (the reverse sweep); the gradient kernel reads Gc, hs, Rs, dhs, dYs.
@@ -30,7 +36,7 @@ struct ChunkWs {
   void* Tm;   // [BH][NT][64][64]   (I + A)^-1 per chunk, input dtype
   void* P;    // [BH][NT][64][64]   s (Q K^T) o exp(G_i - G_j), lower triangle incl. diagonal, input dtype
   float* Gc;  // [BH][NT][64]       chunk-local cumulative log-decay
-  void* hs;   // [BH][NT][K][V]     state entering each chunk
+  void* hs;   // [BH][ceil(NT / hstride)][K][V]  state entering each chunk (hstride 2: each even chunk)
   void* Rs;   // [BH][NT][64][V]    R = U - W S per chunk
   void* dhs;  // [BH][NT][K][V]     dL/d(state leaving each chunk)
   void* dYs;  // [BH][NT][64][V]    dY = Tm^T dL/dR per chunk (the gradient w.r.t. Y, R = Tm Y)
@@ -69,6 +75,7 @@ struct ChunkArgs {
   // prefix pass (local reverse pass) starts each sequence's first (last) segment from h0 (dhT), all at the
   // sequence's own index.
   int ns = 1;
+  int hstride = 1;  // state_stride(): the stash holds the state entering every hstride-th chunk
 };
 
 // Returns the bytes of the requested parts laid out from `base` and, if `carve` is non-null, sets the pointers
@@ -77,7 +84,8 @@ struct ChunkArgs {
 // backward reads phi).
 enum WsPart { WS_FACT = 1, WS_STATE = 2, WS_GRAD = 4, WS_SEGF = 8, WS_SEGB = 16,
               WS_STASH = WS_FACT | WS_STATE | WS_SEGF };
-size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, ChunkWs* carve, void* base, int ns);
+size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, ChunkWs* carve, void* base, int ns,
+                      int hstride);
 
 // Segmented sweeps: when the state sweeps would leave most compute units idle ((V/64) B H workgroups) and the
 // sequence is long, it is cut into NS equal segments of whole chunks, swept in parallel as the problem

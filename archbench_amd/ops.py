@@ -314,7 +314,7 @@ def nsgdn_chunk_fwd(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor, h0: 
     q, k, u, v, la, h0 = _arg(q), _arg(k), _arg(u), _arg(v), _arg(la, torch.float32), _arg(h0, torch.float32)
     y = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
     hT = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
-    stash = torch.empty(_lib.stash_bytes(B, T, H, K, V, q.dtype)[0], dtype=torch.uint8, device=q.device)
+    stash = torch.empty(_lib.stash_bytes(B, T, H, K, V, q.dtype, nsgdn=True)[0], dtype=torch.uint8, device=q.device)
     rc = lib.gdn_nsgdn_chunk_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(u), _lib.ptr(v), _lib.ptr(la), _lib.ptr(h0),
                                  _lib.ptr(y), _lib.ptr(hT), _lib.ptr(stash), stash.numel(), B, T, H, K, V,
                                  float(scale), _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
@@ -326,7 +326,7 @@ def nsgdn_chunk_fwd(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor, h0: 
 def _(q, k, u, v, la, h0, scale):
     B, T, H, K = q.shape
     V = v.shape[-1]
-    n = _lib.stash_bytes(B, T, H, K, V, q.dtype)[0]
+    n = _lib.stash_bytes(B, T, H, K, V, q.dtype, nsgdn=True)[0]
     return (q.new_empty(B, T, H, V), q.new_empty(B, H, K, V, dtype=torch.float32),
             q.new_empty(n, dtype=torch.uint8))
 
@@ -344,7 +344,7 @@ def nsgdn_chunk_bwd(q: Tensor, k: Tensor, u: Tensor, v: Tensor, la: Tensor, h0: 
     dq, dk, du, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(u), torch.empty_like(v)
     dla = torch.empty(B, T, H, dtype=torch.float32, device=q.device)
     dh0 = torch.empty(B, H, K, V, dtype=torch.float32, device=q.device)
-    ws = _lib.workspace(q.device, _lib.stash_bytes(B, T, H, K, V, q.dtype)[1])
+    ws = _lib.workspace(q.device, _lib.stash_bytes(B, T, H, K, V, q.dtype, nsgdn=True)[1])
     rc = lib.gdn_nsgdn_chunk_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(u), _lib.ptr(v), _lib.ptr(la), _lib.ptr(h0),
                                  _lib.ptr(dy), _lib.ptr(dhT), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(du),
                                  _lib.ptr(dv), _lib.ptr(dla), _lib.ptr(dh0), _lib.ptr(stash), stash.numel(),

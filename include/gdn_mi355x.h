@@ -89,12 +89,14 @@ int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const flo
                           int dtype, void* stream);
 
 /* Training pair.  gdn_chunk_fwd_stash computes what gdn_chunk_fwd computes and also writes into `stash` the
- * per-chunk intermediates the backward needs (chunk factors, chunk-local decay, the state entering every chunk
- * and R = U - W S); gdn_chunk_bwd_stashed, called later with the same inputs and the same stash (unchanged in
- * between; it is only read), is gdn_chunk_bwd without its recompute sweep, with `ws` holding only the
- * gradient part of the workspace.  gdn_chunk_stash_bytes gives both sizes.  The reference's forward likewise
- * returns its chunk factor A and cumulative decay g for the backward to reuse (nsgdn.py:352-363, saved at
- * :385-388); keeping the states too trades stash_bytes of device memory for one sweep over the sequence. */
+ * per-chunk intermediates the backward needs (chunk factors, chunk-local decay, R = U - W S, and the state
+ * entering chunks: in bf16 with V <= 128 only every second chunk's, the backward advancing the state through the
+ * chunk between itself; otherwise every chunk's); gdn_chunk_bwd_stashed, called later with the same inputs and the
+ * same stash (unchanged in between; it is only read), is gdn_chunk_bwd without its recompute sweep, with `ws`
+ * holding only the gradient part of the workspace.  gdn_chunk_stash_bytes gives both sizes.  The reference's
+ * forward likewise returns its chunk factor A and cumulative decay g for the backward to reuse
+ * (nsgdn.py:352-363, saved at :385-388); keeping states too trades stash_bytes of device memory for one sweep
+ * over the sequence. */
 int gdn_chunk_stash_bytes(int B, int T, int H, int K, int V, int dtype, size_t* stash_bytes, size_t* bwd_ws_bytes);
 int gdn_chunk_fwd_stash(const void* q, const void* k, const void* v, const float* g, const float* beta,
                         const float* h0, void* o, float* hT, void* stash, size_t stash_bytes, int B, int T, int H,
@@ -110,11 +112,13 @@ int gdn_chunk_bwd_stashed(const void* q, const void* k, const void* v, const flo
  *   S~ = e^la S,   r = v - S~^T k,   S = S~ + u r^T,   y = S^T (scale q)
  * (nsgdn_ref, archbench/layers/nsgdn.py:408-417; the chunked form nsgdn.py:240-249 with
  * L_ij = (k_i . u_j) gamma_i / gamma_j).  Replaces the custom ops archbench::nsgdn_chunk_fwd / _bwd
- * (nsgdn.py:352-397): the reference's forward returns (y, g, A) for its backward, this one fills the stash of
- * gdn_chunk_stash_bytes (same sizes); the backward reads it and writes dq, dk, du, dv, dla (and dh0).  u has
+ * (nsgdn.py:352-397): the reference's forward returns (y, g, A) for its backward, this one fills a stash of
+ * gdn_nsgdn_stash_bytes (the state entering every chunk is kept); the backward reads it and writes dq, dk, du,
+ * dv, dla (and dh0), with a workspace of the second size gdn_nsgdn_stash_bytes gives.  u has
  * q's shape and dtype; la (natural-log decay) [B,T,H] fp32; h0, hT, dhT, dh0 as for the chunk op (optional);
  * the reference calls it with scale 1 (q pre-scaled) and no states.  bf16 only (as the reference's op, which
  * casts to bf16, nsgdn.py:400-405); K and V as for the chunk op. */
+int gdn_nsgdn_stash_bytes(int B, int T, int H, int K, int V, int dtype, size_t* stash_bytes, size_t* bwd_ws_bytes);
 int gdn_nsgdn_chunk_fwd(const void* q, const void* k, const void* u, const void* v, const float* la,
                         const float* h0, void* y, float* hT, void* stash, size_t stash_bytes, int B, int T, int H,
                         int K, int V, float scale, int dtype, void* stream);
