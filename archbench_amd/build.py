@@ -33,6 +33,21 @@ def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
+def source_digest() -> str:
+    """SHA-256 (first 16 hex digits) over the kernel sources (csrc/*.hip and *.h, names and contents): the build a
+    profile under profiles/ was measured on is recorded by it, so that bench.py uses a profile only with the
+    sources it was taken from."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in sorted(os.listdir(CSRC)):
+        if f.endswith((".hip", ".h")):
+            h.update(f.encode() + b"\0")
+            with open(os.path.join(CSRC, f), "rb") as fh:
+                h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> str:
     cc = hipcc()
     srcs = sources()

@@ -31,6 +31,13 @@ from collections import defaultdict
 COPY_BYTES = 256 * 2 ** 20  # bench.py --calibration-copy: two copies of this many bytes
 
 
+def _digest() -> str:
+    """The kernel-source digest of this tree (bench.py reads a profile only if it matches its own sources)."""
+    from archbench_amd.build import source_digest
+
+    return source_digest()
+
+
 def stage_of(name: str) -> str:
     """Stage name of a kernel (the library's mangled template names carry the forward sweep's mode)."""
     if "chunk_factors_kernel" in name:
@@ -129,7 +136,7 @@ def traffic(args) -> None:
                           "launches": len(sums["fetch"][st])}
         table.append(f"| {st} | {len(sums['fetch'][st])} | {rf:.0f} | {rw:.0f} | {rf * ff / 1e6:.1f} | "
                      f"{rw * fw / 1e6:.1f} | {(rf * ff + rw * fw) / 1e6:.1f} |")
-    doc = {"workload": args.workload, "command": args.command,
+    doc = {"workload": args.workload, "command": args.command, "sources": _digest(),
            "calibration": {"fetch_bytes_per_unit": round(ff, 4), "write_bytes_per_unit": round(fw, 4),
                            "copy": "two device copies of 256 MiB (bench.py --calibration-copy)"},
            "per_launch": per_launch}
@@ -176,7 +183,8 @@ def counters(args) -> None:
         per_launch[st] = ent
         table.append(f"| {st} | {ent['launches']} | " + " | ".join(f"{avg.get(c, float('nan')):.4g}" for c in names)
                      + "".join(f" | {f:.3f}" for f in fr) + " |")
-    json.dump({"workload": args.workload, "command": args.command, "per_launch": per_launch}, open(args.out, "w"),
+    json.dump({"workload": args.workload, "command": args.command, "sources": _digest(), "per_launch": per_launch},
+              open(args.out, "w"),
               indent=1)
     print(f"wrote {args.out}")
     if args.md:

@@ -63,6 +63,7 @@ Also reported in the same line:
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -121,12 +122,20 @@ def algo_bytes_step(K: int, V: int, es: int = 2) -> int:
 
 
 def _profile_json(name: str) -> dict:
+    """A profiles/ summary, if it was measured on these kernel sources (its "sources" digest equals this tree's);
+    otherwise empty, so that no figure measured on other kernels is reported as this build's."""
+    from archbench_amd.build import source_digest
+
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
     try:
         with open(path) as f:
-            return json.load(f)
+            doc = json.load(f)
     except (OSError, ValueError):
         return {}
+    if doc.get("sources") != source_digest():
+        log(f"profiles/{name} was measured on other kernel sources ({doc.get('sources')}); not used")
+        return {}
+    return doc
 
 
 def measured_traffic() -> dict:
@@ -154,18 +163,27 @@ def cpu_model() -> str:
 def timed_loop(fn, steps: int, warmup: int, torch, events: bool = False):
     """Seconds per call of fn over `steps` calls after `warmup` untimed ones, by the host clock between two
     synchronisations; with events, also the GPU time between HIP events recorded on the current stream (the
-    stream the library launches on) around the same calls: (host_s, event_s)."""
+    stream the library launches on) around the same calls: (host_s, event_s).
+
+    Python's garbage collector is run before and kept off inside the timed region, as timeit does: a full
+    collection late in this process takes about 80 ms (measured), and one falling among 20 steps of a 2.6 ms layer
+    step read as 6.3 ms per step."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(steps):
-        fn()
-    e1.record()
-    torch.cuda.synchronize()
-    host = (time.perf_counter() - t0) / steps
+    gc.collect()
+    gc.disable()
+    try:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        host = (time.perf_counter() - t0) / steps
+    finally:
+        gc.enable()
     return (host, e0.elapsed_time(e1) * 1e-3 / steps) if events else host
 
 
@@ -451,7 +469,7 @@ def main() -> int:
                              "K": K, "V": V, "ms_per_step": round(sec * 1e3, 3), "fwd_kernel_ms": round(f_ms, 3),
                              "bwd_kernel_ms": round(b_ms, 3), "tokens_per_s": round(B * T / sec, 1)}
         log(f"token scan fwd+bwd {sec * 1e3:.3f} ms per call pair; kernels fwd {f_ms:.3f} ms, bwd {b_ms:.3f} ms")
-        del qt, kt, ut, vt, lat, dyt, y_, r_, st_
+        del qt, kt, ut, vt, lat, dyt
         torch.cuda.empty_cache()
 
     if want("decode"):
