@@ -95,20 +95,22 @@ def stage_flops(stage: str, K: int, V: int) -> int:
     }.get(stage, 0)
 
 
-def stage_bytes(stage: str, K: int, V: int, es: int = 2) -> int:
+def stage_bytes(stage: str, K: int, V: int, es: int = 2, hstride: int = 2) -> int:
     """Design HBM bytes per token-head of each kernel: every input and workspace buffer read once, every output
     written once (q, k: es*K; v, o, dO, dv, R, dY: es*V; g, beta, G, dg, dbeta: 4; Tm, P: es*C per token; a
-    chunk's state or state gradient: es*K*V/C per token).  The second V-block workgroup's reads of q, k, Tm
-    and P in the sweeps, which hit L2, count once."""
+    chunk's state or state gradient: es*K*V/C per token, the stash keeping the state entering every hstride-th
+    chunk: every second one in bf16 at V <= 128).  The second V-block workgroup's reads of q, k, Tm and P in the
+    sweeps, which hit L2, count once."""
     qk, vv, st, tm = es * K, es * V, es * K * V // C, es * C
+    sh = st // hstride
     return {
         "factors": 2 * qk + 8 + 2 * tm + 4,                  # q k g beta -> Tm P G
         "fwd": 2 * qk + vv + 8 + 2 * tm + vv,                # q k v beta G Tm P -> o
-        "fwd_stash": 2 * qk + vv + 8 + 2 * tm + vv + st + vv,  # ... -> o, states, R
-        "bwd_recompute": qk + vv + 8 + tm + st + vv,         # k v beta G Tm -> states, R
+        "fwd_stash": 2 * qk + vv + 8 + 2 * tm + vv + sh + vv,  # ... -> o, states, R
+        "bwd_recompute": qk + vv + 8 + tm + sh + vv,         # k v beta G Tm -> states, R
         "bwd_state": 2 * qk + vv + 8 + 2 * tm + st + vv,     # q k dO beta G Tm P -> dstates, dY
-        "bwd_intra": 2 * qk + 2 * vv + 8 + 2 * st + 2 * vv + 2 * qk + vv + 8,  # q k v dO beta G S0 dSC R dY ->
-                                                                             # dq dk dv dg dbeta
+        "bwd_intra": 2 * qk + 2 * vv + 8 + sh + st + 2 * vv + 2 * qk + vv + 8,  # q k v dO beta G S0 dSC R dY ->
+                                                                               # dq dk dv dg dbeta
     }.get(stage, 0)
 
 
