@@ -93,7 +93,6 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
   const int ncb = V / 16, cb = vb * (BV / 16) + ws;  // fragment-layout column block of the slab
   const int k0 = (K / 2) * hf;                       // first dS row of this half
   const int tid = threadIdx.x;
-  const int64_t sbase = (int64_t)bh * K * V;
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
@@ -422,7 +421,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 
   // Unrolled up to two slabs: with the slab tests resolved at compile time the compiler counts the loads in
   // flight exactly (four slabs unrolled would spill).
-#pragma unroll(V / VS <= 2 ? V / VS : 1)
+  constexpr int SLAB_UNROLL = V / VS <= 2 ? V / VS : 1;
+#pragma unroll SLAB_UNROLL
   for (int vs = 0; vs < V; vs += VS) {
     // group A: dO R^T, dY R^T; dv = beta dY and dbeta += dY . v
     rdo.store(sdO, LS, tid);

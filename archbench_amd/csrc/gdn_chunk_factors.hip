@@ -29,7 +29,7 @@ template <typename T, int K>
 constexpr bool factors_a_on_q() { return (K + 16 / (int)sizeof(T)) * (int)sizeof(T) == (CH + 4) * 4; }
 
 template <typename T, int K, bool SEPU>
-__global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && !SEPU ? 3 : 2)))
 void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ u,
                           const float* __restrict__ g, const float* __restrict__ beta, T* __restrict__ gTm,
                           T* __restrict__ gP, float* __restrict__ gGc, int T_, int H, int NT, int nitems,

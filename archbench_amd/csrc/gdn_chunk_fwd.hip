@@ -84,7 +84,6 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
   const int c0 = 16 * ws;                             // the slab inside the V block
   const int ncb = V / 16, cb = vb * (BV / 16) + ws;  // its fragment-layout column block
   const int tid = threadIdx.x;
-  const int64_t sbase = (int64_t)bh * K * V;
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
