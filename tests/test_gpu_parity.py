@@ -123,10 +123,13 @@ def test_autograd_recompute_path(monkeypatch):
 
 
 @pytest.mark.parametrize("dtype,T,K,V", [(torch.float32, 130, 64, 64), (torch.bfloat16, 200, 128, 128),
-                                         (torch.bfloat16, 64, 64, 256)])
+                                         (torch.bfloat16, 64, 64, 256), (torch.bfloat16, 64, 128, 128),
+                                         (torch.bfloat16, 130, 128, 128), (torch.bfloat16, 190, 64, 128)])
 def test_stash_pair_equals_plain_and_recompute(dtype, T, K, V):
     """fwd_stash gives the plain forward's o and hT bit for bit, and bwd_stashed the recompute backward's
-    gradients bit for bit (the stash holds exactly what the recompute sweep rebuilds); both against the oracle."""
+    gradients bit for bit (the stash holds exactly what the recompute sweep rebuilds); both against the oracle.
+    bf16 at V <= 128 keeps every second state: one chunk (no pair), and three chunks (the last one unpaired,
+    ragged at T = 190) walk the pairs' edge cases."""
     banner(f"stash pair {dtype} T={T} K={K} V={V}")
     host, dev = device_inputs(2, T, 2, K, V, dtype, h0_std=0.1, with_do=True, seed=3)
     dhT = (torch.randn(2, 2, K, V, generator=torch.Generator().manual_seed(9)) * 0.1).cuda()
