@@ -46,8 +46,8 @@ size_t chunk_ws_bytes(int B, int T, int H, int K, int V, int dtype, int parts, C
   };
   ChunkWs ws{};
   if (parts & WS_FACT) {
-    ws.Tm = take(BH * NT * CH_TOKENS * CH_TOKENS * es);
-    ws.P = take(BH * NT * CH_TOKENS * CH_TOKENS * es);
+    ws.Tm = take(BH * NT * CH_TRI_ELEMS * es);
+    ws.P = take(BH * NT * CH_TRI_ELEMS * es);
     ws.Gc = static_cast<float*>(take(BH * NT * CH_TOKENS * 4));
   }
   if (parts & WS_STATE) {

@@ -98,7 +98,7 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
 
   RegTile<T, CH, K, STH, STATE_NT_LOAD> rk, rq, ru;
   RegTile<T, CH, BV, STH, STATE_NT_LOAD> rdo;
-  RegTile<T, CH, CH, STH, STATE_NT_LOAD> rtm, rp;
+  TriTile<T, STH, STATE_NT_LOAD> rtm, rp;  // packed lower blocks
   float pG = 0.f, pB = 0.f;
   // The next chunk's reads go out in three batches (k, q after the first barrier, dO after the second; Tm, P,
   // G, beta after the dR exchange), so that no wave stalls on a full memory queue for the whole set at once
@@ -118,8 +118,8 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
   auto prefetch2 = [&](int c) {
     const int64_t row0 = row0_of(c), cidx = (int64_t)bh * NT + c;
     const int nv = nvalid_of(c);
-    rtm.load(gTm + cidx * CH * CH, (int64_t)CH, CH, tid);
-    rp.load(gP + cidx * CH * CH, (int64_t)CH, CH, tid);
+    rtm.load(gTm + cidx * CH_TRI_ELEMS, tid);
+    rp.load(gP + cidx * CH_TRI_ELEMS, tid);
     if (w == 0) {
       pG = gGc[cidx * CH + l];
       pB = l < nv ? (beta ? beta[row0 + (int64_t)l * H] : 1.f) : 0.f;
@@ -230,6 +230,10 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
     }
     __syncthreads();  // every wave done with this chunk's inputs
   };
+  // the blocks of Tm and P above the diagonal stay zero (the packed loads write the others); ordered before any
+  // read by the first chunk's first barrier
+  tri_zero_upper<T, STH>(sTm, LC, tid);
+  tri_zero_upper<T, STH>(sP, LC, tid);
   prefetch(NT - 1, 0);
   prefetch2(NT - 1);
   for (int c = NT - 1; c >= 0; --c) chunk(c);

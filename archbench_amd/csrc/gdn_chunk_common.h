@@ -13,6 +13,7 @@
 #include <type_traits>
 
 #include "gdn_common.h"
+#include "gdn_launch.h"
 
 namespace gdn {
 
@@ -329,6 +330,77 @@ __device__ __forceinline__ void s2g_rows(T* g, int64_t gld, const T* s, int sld,
       const int r = idx / VPR, c = (idx - r * VPR) * E;
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, *reinterpret_cast<const uint4*>(s + r * sld + c)),
                                              rs, (r * (int)gld + c) * (int)sizeof(T), 0, NT ? 2 : 0);
+    }
+  }
+}
+
+// ---- lower block-triangular 64 x 64 matrices (Tm, P) in HBM ----------------------------------------------------
+// Only the blocks (bi, bj), bj <= bi, of 16 x 16 are stored, block bi (bi + 1) / 2 + bj of CH_TRI_ELEMS elements
+// (5 KB instead of 8 KB in bf16); in LDS the matrices keep the full row-major layout, with the six blocks above the
+// diagonal written as zeros once per workgroup.
+// (row, first column) in the 64 x 64 matrix of 16-byte vector vi of the packed layout
+template <typename T>
+__device__ __forceinline__ void tri_vec_pos(int vi, int& row, int& col) {
+  constexpr int E = 16 / sizeof(T), VPR = 16 / E, VPB = 16 * VPR;  // elements per vector; vectors per block row, block
+  const int b = vi / VPB, wv = vi - b * VPB;
+  const int bi = b >= 6 ? 3 : (b >= 3 ? 2 : (b >= 1 ? 1 : 0));
+  const int rr = wv / VPR;
+  row = 16 * bi + rr;
+  col = 16 * (b - bi * (bi + 1) / 2) + (wv - rr * VPR) * E;
+}
+
+// A packed matrix held in registers as 16-byte vectors, to prefetch the next chunk's Tm or P as RegTile does.  The
+// loads are unconditional -- threads past the last vector reload an earlier one and do not store it -- so the
+// compiler counts the loads in flight exactly.
+template <typename T, int NTH, bool NT>
+struct TriTile {
+  static constexpr int E = 16 / sizeof(T), NV = CH_TRI_ELEMS / E, N = (NV + NTH - 1) / NTH;
+  static_assert(N * NTH <= 2 * NV, "a thread's spare vectors reload the first NV");
+  uint4 r[N];
+  __device__ __forceinline__ void load(const T* g, int tid) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int vi = tid + i * NTH;
+      r[i] = ld16<NT>(g + (NV % NTH == 0 || vi < NV ? vi : vi - NV) * E);
+    }
+  }
+  __device__ __forceinline__ void store(T* s, int ld, int tid) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int vi = tid + i * NTH;
+      if (NV % NTH == 0 || vi < NV) {
+        int row, col;
+        tri_vec_pos<T>(vi, row, col);
+        *reinterpret_cast<uint4*>(s + row * ld + col) = r[i];
+      }
+    }
+  }
+};
+
+// The six zero blocks above the diagonal of a 64 x 64 LDS tile (ld elements per row), which packed stores never write
+template <typename T, int NTH>
+__device__ __forceinline__ void tri_zero_upper(T* s, int ld, int tid) {
+  constexpr int E = 16 / sizeof(T), VPR = 16 / E, VPB = 16 * VPR;
+  for (int vi = tid; vi < 6 * VPB; vi += NTH) {
+    const int u = vi / VPB, wv = vi - u * VPB;  // upper block u: (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+    const int bi = u >= 5 ? 2 : (u >= 3 ? 1 : 0);
+    const int bj = u + (bi == 0 ? 1 : (bi == 1 ? -1 : -2));
+    const int rr = wv / VPR;
+    *reinterpret_cast<uint4*>(s + (16 * bi + rr) * ld + 16 * bj + (wv - rr * VPR) * E) = make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+// Packed store of the lower blocks of a 64 x 64 LDS tile (ld elements per row) to global memory
+template <typename T, int NTH, bool NT>
+__device__ __forceinline__ void s2g_tri(T* g, const T* s, int ld, int tid) {
+  constexpr int E = 16 / sizeof(T), NV = CH_TRI_ELEMS / E, N = (NV + NTH - 1) / NTH;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int vi = tid + i * NTH;
+    if (NV % NTH == 0 || vi < NV) {
+      int row, col;
+      tri_vec_pos<T>(vi, row, col);
+      st16<NT>(g + vi * E, *reinterpret_cast<const uint4*>(s + row * ld + col));
     }
   }
 }

@@ -5,8 +5,9 @@
 //   G    chunk-local inclusive cumsum of g                                            -> Gc [BH][NT][64] fp32
 //   A    beta_i (k_i . u_j) exp(G_i - G_j), strictly lower, on MFMA (fp32 in LDS)
 //   Tm   (I + A)^-1: diagonal 16x16 blocks by Neumann products, blocks below by column chains (bf16x3 MFMA)
-//                                                                                     -> Tm [BH][NT][64][64]
-//   P    s (q_i . u_j) exp(G_i - G_j) for i >= j                                      -> P  [BH][NT][64][64]
+//                                                                                     -> Tm [BH][NT][packed]
+//   P    s (q_i . u_j) exp(G_i - G_j) for i >= j                                      -> P  [BH][NT][packed]
+// (packed: the ten 16 x 16 blocks on and below the diagonal, the rest being zero; gdn_chunk_common.h)
 // u is the write key: u = k for the gated delta rule (SEPU false); with separate write keys (SEPU, the n-step
 // family, archbench/layers/nsgdn.py:240-249 with L_ij = (k_i . u_j) gamma_i / gamma_j) u is loaded too and
 // beta may be absent (row scale 1).
@@ -88,8 +89,8 @@ void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, cons
     __syncthreads();
     factors_merge<T>(D, sA, sD, sTm, nullptr, sOne, w);
     __syncthreads();
-    s2g_rows<T, CH, CH, NTHR, true>(gTm + (int64_t)it * CH * CH, (int64_t)CH, sTm, LC, CH);
-    s2g_rows<T, CH, CH, NTHR, true>(gP + (int64_t)it * CH * CH, (int64_t)CH, sP, LC, CH);
+    s2g_tri<T, NTHR, true>(gTm + (int64_t)it * CH_TRI_ELEMS, sTm, LC, threadIdx.x);
+    s2g_tri<T, NTHR, true>(gP + (int64_t)it * CH_TRI_ELEMS, sP, LC, threadIdx.x);
     __syncthreads();  // LDS free for the next item
   }
 }

@@ -89,7 +89,7 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
 
   RegTile<T, CH, K, FTH, FWD_NT_LOAD, false> rk, rq, ru;
   RegTile<T, CH, BV, FTH, FWD_NT_LOAD, false> rv;
-  RegTile<T, CH, CH, FTH, FWD_NT_LOAD, false> rtm, rp;
+  TriTile<T, FTH, FWD_NT_LOAD> rtm, rp;  // packed lower blocks
   float pG = 0.f, pB = 0.f;  // wave 0: G and beta of lane l's token
   // The next chunk's reads go out in two batches (k, q, v after the first barrier; Tm, P, G, beta after the
   // second exchange), so that no wave stalls on a full memory queue for the whole set at once.
@@ -104,8 +104,8 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
   auto prefetch2 = [&](int c) {
     const int64_t row0 = row0_of(c), cidx = (int64_t)bh * NT + c;
     const int nv = nvalid_of(c);
-    rtm.load(gTm + cidx * CH * CH, (int64_t)CH, CH, tid);
-    if constexpr (OUT) rp.load(gP + cidx * CH * CH, (int64_t)CH, CH, tid);
+    rtm.load(gTm + cidx * CH_TRI_ELEMS, tid);
+    if constexpr (OUT) rp.load(gP + cidx * CH_TRI_ELEMS, tid);
     if (w == 0) {
       pG = gGc[cidx * CH + l];
       pB = l < nv ? (beta ? beta[row0 + (int64_t)l * H] : 1.f) : 0.f;
@@ -238,6 +238,10 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
     if constexpr (OUT)
       s2g_rows<T, CH, BV, FTH, FWD_NT_STORE>(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, nvalid_of(c));
   };
+  // the blocks of Tm and P above the diagonal stay zero (the packed loads write the others); ordered before any
+  // read by the first chunk's first barrier
+  tri_zero_upper<T, FTH>(sTm, LC, tid);
+  if constexpr (OUT) tri_zero_upper<T, FTH>(sP, LC, tid);
   prefetch(0);
   prefetch2(0);
   for (int c = 0; c < NT; ++c) chunk(c);

@@ -10,6 +10,9 @@ namespace gdn {
 enum DType { DT_F32 = 0, DT_BF16 = 1 };
 
 constexpr int CH_TOKENS = 64;  // tokens per chunk (the kernels' CH)
+// Tm and P per chunk in HBM: the ten 16 x 16 blocks on and below the diagonal of the 64 x 64 matrix (the six above
+// are zero), packed row-block-major, each block 16 rows x 16 columns row-major
+constexpr int CH_TRI_ELEMS = 10 * 256;
 
 struct StepArgs {
   const void *q, *k, *v;
@@ -33,8 +36,8 @@ inline int state_stride(int V, int dtype, bool sepu) { return dtype == DT_BF16 &
 // recompute sweep), WS_GRAD = {dhs, dYs} (the reverse sweep); the gradient kernel reads Gc, hs, Rs, dhs, dYs.
 // hs, Rs, dhs and dYs use the fragment layout of the sweeps' accumulators (store_fragblk).
 struct ChunkWs {
-  void* Tm;   // [BH][NT][64][64]   (I + A)^-1 per chunk, input dtype
-  void* P;    // [BH][NT][64][64]   s (Q K^T) o exp(G_i - G_j), lower triangle incl. diagonal, input dtype
+  void* Tm;   // [BH][NT][CH_TRI_ELEMS]  (I + A)^-1 per chunk (lower blocks, packed), input dtype
+  void* P;    // [BH][NT][CH_TRI_ELEMS]  s (Q K^T) o exp(G_i - G_j), lower triangle incl. diagonal (packed)
   float* Gc;  // [BH][NT][64]       chunk-local cumulative log-decay
   void* hs;   // [BH][ceil(NT / hstride)][K][V]  state entering each chunk (hstride 2: each even chunk)
   void* Rs;   // [BH][NT][64][V]    R = U - W S per chunk

@@ -97,11 +97,12 @@ def stage_flops(stage: str, K: int, V: int) -> int:
 
 def stage_bytes(stage: str, K: int, V: int, es: int = 2, hstride: int = 2) -> int:
     """Design HBM bytes per token-head of each kernel: every input and workspace buffer read once, every output
-    written once (q, k: es*K; v, o, dO, dv, R, dY: es*V; g, beta, G, dg, dbeta: 4; Tm, P: es*C per token; a
+    written once (q, k: es*K; v, o, dO, dv, R, dY: es*V; g, beta, G, dg, dbeta: 4; Tm, P: es*40 per token, their
+    ten 16 x 16 blocks on and below the diagonal per 64 tokens; a
     chunk's state or state gradient: es*K*V/C per token, the stash keeping the state entering every hstride-th
     chunk: every second one in bf16 at V <= 128).  The second V-block workgroup's reads of q, k, Tm and P in the
     sweeps, which hit L2, count once."""
-    qk, vv, st, tm = es * K, es * V, es * K * V // C, es * C
+    qk, vv, st, tm = es * K, es * V, es * K * V // C, es * 10 * 256 // C
     sh = st // hstride
     return {
         "factors": 2 * qk + 8 + 2 * tm + 4,                  # q k g beta -> Tm P G

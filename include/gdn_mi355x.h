@@ -78,7 +78,7 @@ int gdn_chunk_bwd(const void* q, const void* k, const void* v, const float* g, c
  * (until the process ends).  The results equal gdn_chunk_fwd's bit for bit where gdn_chunk_fwd does not segment
  * its sweeps (long T with few B * H: there it splits each sequence into segments and this entry point does not,
  * and the two agree within rounding).  The call allocates and frees nothing.  Limit: one sequence's factors,
- * H * ceil(T/64) chunks of 16,640 bytes (bf16; 33,024 in fp32), must fit in the scratch; larger batches run as
+ * H * ceil(T/64) chunks of 10,496 bytes (bf16; 20,736 in fp32), must fit in the scratch; larger batches run as
  * consecutive groups of sequences on `stream` (this needs T * H to be a multiple of 4), otherwise
  * GDN_ERR_WORKSPACE.  Every call on one GPU shares that GPU's scratch, so calls that overlap in time on one GPU
  * (concurrent streams, or several host threads) race and give wrong results: serialise them.  The stream must

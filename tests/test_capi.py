@@ -47,8 +47,9 @@ def test_workspace_sizes():
     fwd = _lib.ws_bytes("fwd", 8, 4096, 16, 128, 128, torch.bfloat16)
     bwd = _lib.ws_bytes("bwd", 8, 4096, 16, 128, 128, torch.bfloat16)
     BH, NT = 8 * 16, 64
-    # the forward's workspace holds the chunk factors: Tm and P (64x64 each), G (64 fp32) per chunk
-    assert fwd == BH * NT * (2 * 64 * 64 * 2 + 64 * 4)
+    # the forward's workspace holds the chunk factors: Tm and P (their ten 16x16 blocks on and below the diagonal,
+    # packed), G (64 fp32) per chunk
+    assert fwd == BH * NT * (2 * 10 * 256 * 2 + 64 * 4)
     # the backward adds the leaving state's gradient (K x V), R and dY (64 x V) per chunk, and the entering state of
     # every second chunk (bf16 at V <= 128: the gradient kernel advances it through the chunk between)
     assert bwd == fwd + BH * NT * (128 * 128 * 2 + 2 * 64 * 128 * 2) + BH * (NT // 2) * 128 * 128 * 2
@@ -64,17 +65,17 @@ def test_stash_sizes_split_the_backward_workspace():
         assert stash + grad == _lib.ws_bytes("bwd", *args)
     B, T, H, K, V = 8, 4096, 16, 128, 128
     stash, grad = _lib.stash_bytes(B, T, H, K, V, torch.bfloat16)
-    # per chunk: Tm and P (64x64 bf16 each), G (64 fp32), R (64 x V bf16); per pair of chunks: the entering state
-    # (K x V bf16)
-    assert stash == B * H * 64 * (2 * 64 * 64 * 2 + 64 * 4 + 64 * V * 2) + B * H * 32 * K * V * 2
+    # per chunk: Tm and P (ten 16x16 bf16 blocks each), G (64 fp32), R (64 x V bf16); per pair of chunks: the
+    # entering state (K x V bf16)
+    assert stash == B * H * 64 * (2 * 10 * 256 * 2 + 64 * 4 + 64 * V * 2) + B * H * 32 * K * V * 2
     # the n-step pair keeps every entering state; so do V = 256 and fp32
     ns_stash, ns_grad = _lib.stash_bytes(B, T, H, K, V, torch.bfloat16, nsgdn=True)
     assert ns_stash == stash + B * H * 32 * K * V * 2 and ns_grad == grad
     s256, _ = _lib.stash_bytes(8, 4096, 16, 128, 256, torch.bfloat16)
-    assert s256 == 8 * 16 * 64 * (2 * 64 * 64 * 2 + 64 * 4 + 64 * 256 * 2 + 128 * 256 * 2)
+    assert s256 == 8 * 16 * 64 * (2 * 10 * 256 * 2 + 64 * 4 + 64 * 256 * 2 + 128 * 256 * 2)
     # odd chunk counts keep the last (unpaired) chunk's state: ceil(NT / 2) states per sequence
     s3, _ = _lib.stash_bytes(1, 130, 1, 64, 64, torch.bfloat16)
-    assert s3 == 3 * (2 * 64 * 64 * 2 + 64 * 4 + 64 * 64 * 2) + 2 * 64 * 64 * 2
+    assert s3 == 3 * (2 * 10 * 256 * 2 + 64 * 4 + 64 * 64 * 2) + 2 * 64 * 64 * 2
 
 
 def test_stashed_backward_rejects_missing_stash():

@@ -50,7 +50,7 @@ def test_fp32_call():
 
 
 def test_batch_in_sequence_groups():
-    """B=8, T=4096, H=16 bf16 needs 136 MB of factors: more than the scratch, so the call runs as consecutive
+    """B=8, T=4096, H=16 bf16 needs 86 MB of factors: more than the scratch, so the call runs as consecutive
     groups of sequences, each reusing the scratch."""
     _both(8, 4096, 16, 128, 128, torch.bfloat16, None, 14, 1.0)
 
