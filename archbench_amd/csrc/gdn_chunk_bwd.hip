@@ -1,7 +1,7 @@
 // Chunkwise gated delta rule, backward.
 //
-// The backward takes the chunk factors (Tm, P, G) and the state entering every chunk with R from the stashing
-// forward, or rebuilds them first (chunk factors kernel, then the forward sweep in recompute mode), then runs:
+// The backward takes the chunk factors (Tm, P, G), R and the state entering every chunk (every second one:
+// state_stride) from the stashing forward, or rebuilds them first (chunk factors kernel, then the forward sweep in recompute mode), then runs:
 //
 // bwd_state: one workgroup per (V block of 64 columns, or 32 when the grid fits the device, b*h), reverse over
 //   chunks, reading the chunk factors; each wave carries a 16-column slab of dS in MFMA accumulators.

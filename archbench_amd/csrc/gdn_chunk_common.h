@@ -89,19 +89,13 @@ __device__ __forceinline__ f32x4 inv_diag16(const float* Lp) {
   return D;
 }
 
-// Writes block (bi, bj) of Tm (accumulator x) as TmB = Tm diag(beta) into LDS (stride LC) and, if gTm is
-// non-null, the unscaled block to global memory (64 x 64 row-major).
+// Writes block (bi, bj) of Tm (accumulator x) into LDS (row-major, stride LC).
 template <typename T, int LC>
-__device__ __forceinline__ void put_tm_block(T* sTmB, T* gTm, const float* sB, int bi, int bj, const f32x4& x) {
+__device__ __forceinline__ void put_tm_block(T* sTm, int bi, int bj, const f32x4& x) {
   const int l = lane_id();
   const int col = 16 * bj + (l & 15);
-  const float bc = sB[col];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * bi + 4 * (l >> 4) + i;
-    sTmB[r * LC + col] = from_f<T>(x[i] * bc);
-    if (gTm) gTm[r * CH + col] = from_f<T>(x[i]);
-  }
+  for (int i = 0; i < 4; ++i) sTm[(16 * bi + 4 * (l >> 4) + i) * LC + col] = from_f<T>(x[i]);
 }
 
 // Compact store of the four 16x16 diagonal blocks of the inverse (fp32): block b at sD + b * DBLK, stride LDD.
@@ -111,8 +105,7 @@ constexpr int DBLK = 16 * LDD;
 // Column block J of Tm for blocks below the diagonal: X_iJ = -D_i sum_{k=J}^{i-1} A_ik X_kJ, X_JJ = D_J.
 // A in sA (fp32, stride LF), the diagonal blocks D_i compact in sD (see LDD).  Blocks above the diagonal are zero.
 template <typename T, int J, int LF, int LC>
-__device__ __forceinline__ void tm_column(const float* sA, const float* sD, const f32x4& DJ, T* sTmB, T* gTm,
-                                          const float* sB) {
+__device__ __forceinline__ void tm_column(const float* sA, const float* sD, const f32x4& DJ, T* sTm) {
   f32x4 X[4];
   X[J] = DJ;
 #pragma unroll
@@ -122,10 +115,10 @@ __device__ __forceinline__ void tm_column(const float* sA, const float* sD, cons
     for (int k = J; k < i; ++k) mm16<T>(Y, ld_aslice<LF>(sA + 16 * i * LF + 16 * k), X[k]);
     mm16<T>(Xi, ld_aslice<LDD>(sD + i * DBLK), Y);
     X[i] = -Xi;
-    put_tm_block<T, LC>(sTmB, gTm, sB, i, J, X[i]);
+    put_tm_block<T, LC>(sTm, i, J, X[i]);
   }
 #pragma unroll
-  for (int i = 0; i < J; ++i) put_tm_block<T, LC>(sTmB, gTm, sB, i, J, zero4());
+  for (int i = 0; i < J; ++i) put_tm_block<T, LC>(sTm, i, J, zero4());
 }
 
 // Global accesses with the nontemporal hint (NT) stream past the caches' normal replacement: every kernel that
@@ -488,31 +481,30 @@ __device__ __forceinline__ void factors_kq(const T* sK, const T* sU, const T* sQ
 }
 
 // factors_diag (after factors_kq; it reads only the row block of A that the same wave wrote, so no barrier is
-// needed in between): wave w inverts diagonal block w of I + A, writes it to sD and to its TmB block
-// (TmB = Tm diag(beta), row-major, and the unscaled block to gTm if non-null) and returns it for factors_merge.
+// needed in between): wave w inverts diagonal block w of I + A, writes it to sD and to its Tm block (row-major) and
+// returns it for factors_merge.
 template <typename T>
-__device__ __forceinline__ f32x4 factors_diag(const float* sA, float* sD, T* sTmB, T* gTm, const float* sB, int w) {
+__device__ __forceinline__ f32x4 factors_diag(const float* sA, float* sD, T* sTm, int w) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LC = CH + PT, LF = CH + 4;
   const f32x4 D = inv_diag16<T, LF>(sA + 16 * w * LF + 16 * w);
 #pragma unroll
   for (int i = 0; i < 4; ++i) sD[w * DBLK + acc_row(i) * LDD + acc_col()] = D[i];
-  put_tm_block<T, LC>(sTmB, gTm, sB, w, w, D);
+  put_tm_block<T, LC>(sTm, w, w, D);
   return D;
 }
 
 // factors_merge (after a barrier following factors_diag): the blocks of Tm below the diagonal, column block =
-// wave w, straight into TmB (and gTm).  TmB is complete once every wave has returned (caller's barrier).
+// wave w, straight into sTm.  Tm is complete once every wave has returned (caller's barrier).
 template <typename T>
-__device__ __forceinline__ void factors_merge(const f32x4& D, const float* sA, const float* sD, T* sTmB, T* gTm,
-                                              const float* sB, int w) {
+__device__ __forceinline__ void factors_merge(const f32x4& D, const float* sA, const float* sD, T* sTm, int w) {
   constexpr int PT = 16 / sizeof(T);
   constexpr int LC = CH + PT, LF = CH + 4;
   switch (w) {
-    case 0: tm_column<T, 0, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
-    case 1: tm_column<T, 1, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
-    case 2: tm_column<T, 2, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
-    default: tm_column<T, 3, LF, LC>(sA, sD, D, sTmB, gTm, sB); break;
+    case 0: tm_column<T, 0, LF, LC>(sA, sD, D, sTm); break;
+    case 1: tm_column<T, 1, LF, LC>(sA, sD, D, sTm); break;
+    case 2: tm_column<T, 2, LF, LC>(sA, sD, D, sTm); break;
+    default: tm_column<T, 3, LF, LC>(sA, sD, D, sTm); break;
   }
 }
 

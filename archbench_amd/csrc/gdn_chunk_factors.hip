@@ -12,7 +12,7 @@
 // family, archbench/layers/nsgdn.py:240-249 with L_ij = (k_i . u_j) gamma_i / gamma_j) u is loaded too and
 // beta may be absent (row scale 1).
 // The sweeps over the sequence (forward, recompute, reverse) read these instead of rebuilding them for every
-// 64-wide V block, and the gradient kernel reads Tm and G.  Rows past the end of the sequence hold zero k, q
+// 64-wide V block, and the gradient kernel reads G.  Rows past the end of the sequence hold zero k, q
 // and beta, which makes Tm the identity and P zero there.
 #include <algorithm>
 
@@ -48,7 +48,7 @@ void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, cons
   __shared__ __attribute__((aligned(16))) float sD[4 * DBLK];
   __shared__ __attribute__((aligned(16))) T sP[CH * LC];
   T* sTm = sK;
-  __shared__ float sG[CH], sB[CH], sOne[CH];
+  __shared__ float sG[CH], sB[CH];
 
   const int w = wave_id(), l = lane_id();
   RegTile<T, CH, K, NTHR, true> rk, rq, ru;  // k, q, u are read once here: nontemporal
@@ -67,7 +67,6 @@ void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, cons
       if (w == 0) rt.load(g, beta, row0, H, nvalid);
     }
   };
-  if (w == 0) sOne[l] = 1.f;
   if ((int)blockIdx.x < nitems) prefetch(blockIdx.x, 0);
   for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
     rk.store(sK, LK);
@@ -85,9 +84,9 @@ void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, cons
     factors_kq<T, K, 1>(sK, sU, sQ, sG, sB, scale, sA, sP, w);
     __syncthreads();  // every wave done with K (Tm overwrites it); A written
     if (itn < nitems) prefetch(itn, 2);
-    const f32x4 D = factors_diag<T>(sA, sD, sTm, nullptr, sOne, w);
+    const f32x4 D = factors_diag<T>(sA, sD, sTm, w);
     __syncthreads();
-    factors_merge<T>(D, sA, sD, sTm, nullptr, sOne, w);
+    factors_merge<T>(D, sA, sD, sTm, w);
     __syncthreads();
     s2g_tri<T, NTHR, true>(gTm + (int64_t)it * CH_TRI_ELEMS, sTm, LC, threadIdx.x);
     s2g_tri<T, NTHR, true>(gP + (int64_t)it * CH_TRI_ELEMS, sP, LC, threadIdx.x);

@@ -10,7 +10,8 @@
 // waves never exchange state; only the chunk inputs are shared through LDS.  The next chunk's inputs are
 // prefetched into registers one chunk ahead.
 // MODE 0 writes O (and hT); MODE 1 (recompute for the backward) writes instead the state entering every chunk
-// and R, in the fragment layout straight from the accumulators; MODE 2 (training forward) writes both.
+// (every hstride-th) and R, in the fragment layout straight from the accumulators; MODE 2 (training forward)
+// writes both.
 // MODE 3 (the prefix pass of a segmented sweep) writes only the final state, and the grid carries K more columns
 // per head: those "identity" blocks start from S = I with V = 0, so their final state is the segment's transition
 // Phi = prod_c (gamma_C I - K^T diag(exp(G_C - G)) Tm diag(beta gamma) K), written to phi [BH][K][K].  The
