@@ -6,9 +6,9 @@
 // nsgdn.py:357-362), each wave holds one 16-column slab of S in fp32 MFMA accumulators for the whole sweep:
 //     Y = diag(beta) (V - diag(gamma) K S)          R = Tm Y            (= U - W S)
 //     O = s diag(gamma) Q S + P R                   S <- gamma_C S + K^T (exp(G_C - G) R)
-// S, Y and R reach the next product as B operands straight from the accumulators (permuted-k fragments), so
-// waves never exchange state; only the chunk inputs are shared through LDS.  The next chunk's inputs are
-// prefetched into registers one chunk ahead.
+// S, Y and R reach the next product as B operands straight from the accumulators (permuted-k fragments); the
+// chunk inputs are shared through LDS, and so is half of each wave's state slab (below).  The next chunk's
+// inputs are prefetched into registers one chunk ahead.
 // MODE 0 writes O (and hT); MODE 1 (recompute for the backward) writes instead the state entering every chunk
 // (every hstride-th) and R, in the fragment layout straight from the accumulators; MODE 2 (training forward)
 // writes both.
@@ -26,10 +26,12 @@
 namespace gdn {
 
 // Two waves per 16-column slab of the V block (BV / 16 slabs: eight waves for BV = 64, four for BV = 32).  Waves
-// w and w + NSL share the slab 16 (w % NSL) and each holds all of S for it; the chunk's token rows are split
-// between them (half hf = w / NSL takes rows 32 hf .. 32 hf + 31, i.e. the permuted-k fragment hf of every
-// token-indexed product).  Each half computes K S, Q S, Y, R, P R and O for its rows; the Y and Rd fragments of
-// the other half come through LDS (16 bytes per lane each), and both halves apply the full state update.
+// w and w + NSL share the slab 16 (w % NSL); the chunk's token rows are split between them (half hf = w / NSL
+// takes rows 32 hf .. 32 hf + 31, i.e. the permuted-k fragment hf of every token-indexed product), and so are
+// the state's K rows (wave hf holds and updates rows K/2 hf .. K/2 hf + K/2 - 1 of the slab).  Each half computes
+// K S, Q S, Y, R, P R and O for its token rows; the Y and Rd fragments of the other half come through LDS (16
+// bytes per lane each), and so do the bf16 fragments of the other half's state rows, written after the update
+// and read after the next chunk's first barrier (no barrier of their own).
 template <int BV>
 constexpr int fwd_threads() { return 128 * (BV / 16); }
 constexpr bool FWD_NT_LOAD = true;             // chunk inputs (measured faster with the hint)
@@ -45,6 +47,7 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
   constexpr int PT = 16 / sizeof(T);
   constexpr int LK = K + PT, LC = CH + PT, LV = BV + PT;
   constexpr int NKT = K / 16;  // row tiles of the state slab
+  constexpr int NKH = NKT / 2, NSB = K / 64;  // row tiles and 32-row fragments held by each wave of the pair
   constexpr int NSL = BV / 16, FW = 2 * NSL, FTH = 64 * FW;  // slabs, waves, threads
   static_assert(NSL == 2 || NSL == 4, "a wave pair per 16-column slab, two or four slabs");
   constexpr bool OUT = MODE == 0 || MODE == 2;   // O is computed (needs Q and P)
@@ -59,6 +62,15 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
   __shared__ __attribute__((aligned(16))) T sP[OUT ? CH * LC : 8];
   __shared__ __attribute__((aligned(16))) T stage[OUT ? CH * LV : 8];  // O, for the coalesced store
   __shared__ __attribute__((aligned(16))) F xY[FW][64], xR[FW][64], xRd[FW][64];  // exchange between halves
+  // the other half's state fragments, in the reading wave's slot; fp32 (K = 64: one fragment) reuses the reader's
+  // Y slot, which the reader overwrites only after reading them and its partner reads only in the next phase
+  constexpr bool S_ON_Y = sizeof(T) == 4;
+  static_assert(!S_ON_Y || NSB == 1, "the state fragments fit one exchange slot");
+  __shared__ __attribute__((aligned(16))) F xS_[S_ON_Y ? 1 : FW][NSB][64];
+  auto xS = [&](int wr, int s) -> F& {
+    if constexpr (S_ON_Y) return xY[wr][lane_id()];
+    else return xS_[wr][s][lane_id()];
+  };
   __shared__ float sG[CH], sB[CH], sGam[CH];
 
   int vb, bh;
@@ -126,15 +138,23 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
     }
   };
 
-  f32x4 S[NKT];
+  f32x4 S[NKH];  // state rows 16 (NKH hf + t) .. + 15 of the slab
 #pragma unroll
-  for (int t = 0; t < NKT; ++t)
+  for (int t = 0; t < NKH; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = 16 * t + acc_row(i);
+      const int row = 16 * (NKH * hf + t) + acc_row(i);
       S[t][i] = ident ? (row == iv0 + c0 + acc_col() ? 1.f : 0.f)
                       : (use_h0 ? h0[h0_base + (int64_t)row * V + v0 + c0 + acc_col()] : 0.f);
     }
+  F Smine[NSB];  // bf16 fragments of the wave's state rows (32-row blocks NSB hf ..), also written to xS
+  auto publish_state = [&]() {
+#pragma unroll
+    for (int s = 0; s < NSB; ++s) {
+      Smine[s] = frag_acc2<T>(S[2 * s], S[2 * s + 1]);
+      xS(w ^ NSL, s) = Smine[s];
+    }
+  };
 
   auto chunk = [&](int c) {
     const int64_t cidx = (int64_t)bh * NT + c;
@@ -142,19 +162,24 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
     __syncthreads();
     if (c + 1 < NT) prefetch(c + 1);
 
-    // rows 32 hf .. 32 hf + 31: K S, Q S and Y = diag(beta) (V - diag(gamma) K S)
+    // rows 32 hf .. 32 hf + 31: K S, Q S and Y = diag(beta) (V - diag(gamma) K S); the state's fragments are the
+    // wave's own and, for the other half of the K rows, the partner's from xS (written before the last barrier)
     F Sb[K / 32];
-    // the state entering every hstride-th chunk goes to the stash (slot c / hstride of the sequence); the branch is
-    // uniform and the stored values come from the accumulators, not from loads in flight
+#pragma unroll
+    for (int s = 0; s < NSB; ++s) {
+      const F Sother = xS(w, s);
+      Sb[s] = hf ? Sother : Smine[s];
+      Sb[NSB + s] = hf ? Smine[s] : Sother;
+    }
+    // the state entering every hstride-th chunk goes to the stash (slot c / hstride of the sequence), each wave
+    // its own rows; the branch is uniform and the stored values come from registers, not from loads in flight
     const bool keep = (c & (hstride - 1)) == 0;
     const int64_t hidx = (int64_t)bh * ((NT + hstride - 1) / hstride) + c / hstride;
-#pragma unroll
-    for (int s = 0; s < K / 32; ++s) Sb[s] = frag_acc2<T>(S[2 * s], S[2 * s + 1]);
     if constexpr (SAVE) {
       if (keep) {
 #pragma unroll
-        for (int s = 0; s < K / 32; ++s)
-          if ((s & 1) == hf) store_fragblk<T, FWD_NT_STORE>(wsH + hidx * K * V, K, s, cb, ncb, Sb[s]);
+        for (int s = 0; s < NSB; ++s)
+          store_fragblk<T, FWD_NT_STORE>(wsH + hidx * K * V, K, NSB * hf + s, cb, ncb, Smine[s]);
       }
     }
     f32x4 Y[2], QS[2];
@@ -227,14 +252,15 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
         }
       }
     }
-    // S <- gamma_C S + U^T Rd (all rows of U, both halves of the chunk)
+    // S <- gamma_C S + U^T Rd for the wave's state rows (both halves of the chunk's tokens)
     const float gC = __expf(GC);
 #pragma unroll
-    for (int t = 0; t < NKT; ++t) {
+    for (int t = 0; t < NKH; ++t) {
       S[t] *= gC;
-      mma(S[t], frag_oct_perm(sU, LK, 16 * t, 0), Rd0);
-      mma(S[t], frag_oct_perm(sU, LK, 16 * t, 32), Rd1);
+      mma(S[t], frag_oct_perm(sU, LK, 16 * (NKH * hf + t), 0), Rd0);
+      mma(S[t], frag_oct_perm(sU, LK, 16 * (NKH * hf + t), 32), Rd1);
     }
+    publish_state();  // the partner read the previous fragments before the exchange barriers above
     __syncthreads();  // O staged; every wave done with this chunk's inputs
     if constexpr (OUT)
       s2g_rows<T, CH, BV, FTH, FWD_NT_STORE>(o + row0_of(c) * V + v0, (int64_t)H * V, stage, LV, nvalid_of(c));
@@ -243,20 +269,22 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
   // read by the first chunk's first barrier
   tri_zero_upper<T, FTH>(sTm, LC, tid);
   if constexpr (OUT) tri_zero_upper<T, FTH>(sP, LC, tid);
+  publish_state();  // read after the first chunk's first barrier
   prefetch(0);
   prefetch2(0);
   for (int c = 0; c < NT; ++c) chunk(c);
-  if (ident && hf == 0) {
+  if (ident) {
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
+    for (int t = 0; t < NKH; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        phi[((int64_t)bh * K + 16 * t + acc_row(i)) * K + iv0 + c0 + acc_col()] = S[t][i];
-  } else if (hT && hf == 0 && put_hT) {
+        phi[((int64_t)bh * K + 16 * (NKH * hf + t) + acc_row(i)) * K + iv0 + c0 + acc_col()] = S[t][i];
+  } else if (hT && put_hT) {
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
+    for (int t = 0; t < NKH; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) hT[hT_base + (int64_t)(16 * t + acc_row(i)) * V + v0 + c0 + acc_col()] = S[t][i];
+      for (int i = 0; i < 4; ++i)
+        hT[hT_base + (int64_t)(16 * (NKH * hf + t) + acc_row(i)) * V + v0 + c0 + acc_col()] = S[t][i];
   }
 }
 
