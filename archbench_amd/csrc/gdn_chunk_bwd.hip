@@ -422,6 +422,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   for (int j = 0; j < HK; ++j) aQg[j] = aKd[j] = aKY[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float dbV[4] = {0.f, 0.f, 0.f, 0.f};
   float sdot = 0.f;  // partial <dS_C, S0>
+  typename Frag<T>::type adv_a[2];  // HALF: the state advance's first operand, formed in the first slab
 
   // Unrolled up to two slabs: with the slab tests resolved at compile time the compiler counts the loads in
   // flight exactly (four slabs unrolled would spill).
@@ -464,7 +465,8 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
       for (int i = 0; i < decltype(rs0)::N; ++i)
         if (decltype(rs0)::NVEC % ITH == 0 || tid + i * ITH < decltype(rs0)::NVEC)  // loaded by this thread
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sdot += to_f(rdsc.r[i][e]) * to_f(rs0.r[i][e]);
+          for (int e = 0; e < 8; e += 2)
+            sdot = dot2(rdsc.r[i][e], rdsc.r[i][e + 1], rs0.r[i][e], rs0.r[i][e + 1], sdot);
     }
     if (vs == 0) {
       tq.store(sQ, LK, tid);
@@ -492,12 +494,15 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
         using V4 = typename std::conditional<sizeof(T) == 2, bf16x4, f32x4>::type;
         const int rt = (w * NA) / NVT, ct0 = w * NA - rt * NVT;
         const float gC = __expf(sG[CH - 1]);
-        typename Frag<T>::type a[2];
+        if (vs == 0) {  // the same for every slab (K is staged by then)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          a[kb] = frag_oct(sK, LK, 16 * rt, 32 * kb, l);  // (row d of K^T, token t) = K[t][d], scaled by exp(G_C - G_t)
+          for (int kb = 0; kb < 2; ++kb) {
+            // (row d of K^T, token t) = K[t][d], scaled by exp(G_C - G_t)
+            adv_a[kb] = frag_oct(sK, LK, 16 * rt, 32 * kb, l);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) a[kb][e] = from_f<T>(to_f(a[kb][e]) * sDte[32 * kb + 8 * (l >> 4) + e]);
+            for (int e = 0; e < 8; ++e)
+              adv_a[kb][e] = from_f<T>(to_f(adv_a[kb][e]) * sDte[32 * kb + 8 * (l >> 4) + e]);
+          }
         }
 #pragma unroll
         for (int m = 0; m < NA; ++m) {
@@ -506,7 +511,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
           run4(sS0t, LK, vc, d0, s0);
           f32x4 acc = {gC * s0[0], gC * s0[1], gC * s0[2], gC * s0[3]};
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb) mma(acc, a[kb], frag_kc(sRt, LC, 16 * ct, 32 * kb, l));
+          for (int kb = 0; kb < 2; ++kb) mma(acc, adv_a[kb], frag_kc(sRt, LC, 16 * ct, 32 * kb, l));
           *reinterpret_cast<V4*>(sS1t + (vs + vc) * LK + d0) =
               V4{from_f<T>(acc[0]), from_f<T>(acc[1]), from_f<T>(acc[2]), from_f<T>(acc[3])};
         }

@@ -283,7 +283,10 @@ struct FragTile {
         const int blk = idx >> 6, ln = idx & 63, s = blk / NCBS, cbl = blk - s * NCBS;
         const T* src = lds + (16 * cbl + (ln & 15)) * ldt + 32 * s + 4 * (ln >> 4);
 #pragma unroll
-        for (int p = 0; p < 4; ++p) acc += to_f(r[i][p]) * to_f(src[p]) + to_f(r[i][4 + p]) * to_f(src[16 + p]);
+        for (int p = 0; p < 4; p += 2) {
+          acc = dot2(r[i][p], r[i][p + 1], src[p], src[p + 1], acc);
+          acc = dot2(r[i][4 + p], r[i][5 + p], src[16 + p], src[17 + p], acc);
+        }
       }
     }
     return acc;

@@ -41,6 +41,15 @@ __device__ __forceinline__ float to_f(bf16 x) { return static_cast<float>(x); }
 template <typename T> __device__ __forceinline__ T from_f(float x);
 template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
 template <> __device__ __forceinline__ bf16 from_f<bf16>(float x) { return static_cast<bf16>(x); }
+// a0 b0 + a1 b1 + c: for bf16 one v_dot2c_f32_bf16 (exact bf16 products, fp32 sum) in place of four conversions
+// and two FMAs
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2(bf16 a0, bf16 a1, bf16 b0, bf16 b1, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(bf16x2{a0, a1}, bf16x2{b0, b1}, c, false);
+}
+__device__ __forceinline__ float dot2(float a0, float a1, float b0, float b1, float c) {
+  return fmaf(a1, b1, fmaf(a0, b0, c));
+}
 
 __device__ __forceinline__ void mma(f32x4& c, const bf16x8& a, const bf16x8& b) {
   c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
