@@ -157,16 +157,19 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
       dSb[s] = frag_acc2<T>(dS[2 * s], dS[2 * s + 1]);
       if constexpr (STORE) store_fragblk<T, STATE_NT_STORE>(wsdH + cidx * K * V, K, NSH * hf + s, cb, ncb, dSb[s]);
     }
+    // kd[j]: this half's token rows 32 hf + 16 j (first), kd[2 + j]: the other half's (to the partner); the rows
+    // are chosen by address, so no value is selected by the half
+    const int tmine = 32 * hf, tother = 32 - tmine;  // first token of each half
     f32x4 kd[4];
 #pragma unroll
-    for (int rt_ = 0; rt_ < 4; ++rt_) {
-      kd[rt_] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int jj = 0; jj < 4; ++jj) {
+      kd[jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int r0 = (jj < 2 ? tmine : tother) + 16 * (jj & 1);
 #pragma unroll
-      for (int s = 0; s < NSH; ++s) mma(kd[rt_], frag_kc_perm(sU, LK, 16 * rt_, k0 + 32 * s), dSb[s]);
+      for (int s = 0; s < NSH; ++s) mma(kd[jj], frag_kc_perm(sU, LK, r0, k0 + 32 * s), dSb[s]);
     }
-    // (values are selected by the half, never indexed by it: registers cannot be indexed at run time)
-    xKd[w][0][l] = hf ? kd[0] : kd[2];  // the other half's token rows
-    xKd[w][1][l] = hf ? kd[1] : kd[3];
+    xKd[w][0][l] = kd[2];
+    xKd[w][1][l] = kd[3];
     F dOb[2], dOg[2];
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib) {
@@ -181,7 +184,7 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int rt_ = 2 * hf + j;
-      const f32x4 mine = hf ? kd[2 + j] : kd[j];
+      const f32x4 mine = kd[j];
       const f32x4 other = xKd[w ^ NSL][j][l];
 #pragma unroll
       for (int i = 0; i < 4; ++i) dR[j][i] = __expf(GC - sG[16 * rt_ + acc_row(i)]) * (mine[i] + other[i]);
@@ -194,14 +197,13 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
     __syncthreads();
     if (c > 0) prefetch2(c - 1);
     const F dRother = xR[w ^ NSL][l];
-    const F dR0 = hf ? dRother : dRmine, dR1 = hf ? dRmine : dRother;
     f32x4 Z[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int rt_ = 2 * hf + j;
       Z[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, 0), dR0);
-      mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, 32), dR1);
+      mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, tmine), dRmine);
+      mma(Z[j], frag_oct_perm(sTm, LC, 16 * rt_, tother), dRother);
     }
     if constexpr (STORE)
       store_fragblk<T, STATE_NT_STORE>(wsdY + cidx * CH * V, CH, hf, cb, ncb, frag_acc2<T>(Z[0], Z[1]));
@@ -216,7 +218,6 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
     xZ[w][l] = Zmine;
     __syncthreads();
     const F Zother = xZ[w ^ NSL][l];
-    const F Zb0 = hf ? Zother : Zmine, Zb1 = hf ? Zmine : Zother;
     // this half's rows of dS <- gamma_C dS + s Q^T (gamma dO) - K^T Z
     const float gC = __expf(GC);
 #pragma unroll
@@ -224,8 +225,8 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
       f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib) mma(a1, frag_oct(sQ, LK, k0 + 16 * t, 32 * ib), dOg[ib]);
-      mma(a2, frag_oct_perm(sK, LK, k0 + 16 * t, 0), Zb0);
-      mma(a2, frag_oct_perm(sK, LK, k0 + 16 * t, 32), Zb1);
+      mma(a2, frag_oct_perm(sK, LK, k0 + 16 * t, tmine), Zmine);
+      mma(a2, frag_oct_perm(sK, LK, k0 + 16 * t, tother), Zother);
       dS[t] = gC * dS[t] + scale * a1 - a2;
     }
     __syncthreads();  // every wave done with this chunk's inputs

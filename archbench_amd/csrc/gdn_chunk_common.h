@@ -137,62 +137,40 @@ __device__ __forceinline__ void st16(void* p, const uint4& v) {
 
 // A ROWS x COLS tile of T held in registers as 16-byte vectors (ROWS*COLS*sizeof(T)/16 split over the NTH
 // threads of a group; tid = thread index inside the group), used to prefetch the next chunk while the
-// current one is computed.  Rows past the end of the sequence must arrive as zeros, by one of two routes:
-//  * BUF: the rows are read through a buffer resource whose range ends with the last valid row, so the
-//    hardware range check returns zeros past it (no select, no access outside the valid rows) and the per-lane
-//    offsets are 32-bit (the host keeps a chunk's row span of 64 * gld elements under 2 GiB);
-//  * otherwise, global loads: rows past the end read row 0 instead (always in bounds) and are zeroed only when
-//    the tile is stored, so no wait for the data is forced at load time.
-// (Measured: BUF is 4% faster in the reverse sweep and 2% slower in the forward sweep.)
-template <typename T, int ROWS, int COLS, int NTH = NTHR, bool NT = false, bool BUF = true>
+// current one is computed.  The rows are read through a buffer resource whose range ends with the last valid
+// row, so the hardware range check returns zeros for rows past the end of the sequence (no select, no access
+// outside the valid rows); the per-lane offsets are 32-bit (the host keeps a chunk's row span of 64 * gld
+// elements under 2 GiB).
+template <typename T, int ROWS, int COLS, int NTH = NTHR, bool NT = false>
 struct RegTile {
   static constexpr int E = 16 / sizeof(T);
   static constexpr int VPR = COLS / E;
   static constexpr int N = ROWS * VPR / NTH;
   static_assert(N * NTH == ROWS * VPR && N >= 1 && N <= 32, "tile must split evenly over the thread group");
   uint4 r[N];
-  uint32_t ok;  // global-load route: bit i set if vector i lies in a valid row
   __device__ __forceinline__ void load(const T* g, int64_t gld, int valid, int tid) {
-    if constexpr (BUF) {
-      const int nbytes = valid > 0 ? ((valid - 1) * (int)gld + COLS) * (int)sizeof(T) : 0;
-      const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(g), 0, nbytes, BUF_RSRC_WORD3);
+    const int nbytes = valid > 0 ? ((valid - 1) * (int)gld + COLS) * (int)sizeof(T) : 0;
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(g), 0, nbytes, BUF_RSRC_WORD3);
 #pragma unroll
-      for (int i = 0; i < N; ++i) {
-        const int idx = tid + i * NTH, row = idx / VPR, c = (idx - row * VPR) * E;
-        r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             rs, (row * (int)gld + c) * (int)sizeof(T), 0, NT ? 2 : 0));
-      }
-    } else {
-      ok = 0;
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        const int idx = tid + i * NTH, row = idx / VPR, c = (idx - row * VPR) * E;
-        const bool in = row < valid;
-        ok |= (in ? 1u : 0u) << i;
-        r[i] = ld16<NT>(g + (in ? row : 0) * gld + c);
-      }
+    for (int i = 0; i < N; ++i) {
+      const int idx = tid + i * NTH, row = idx / VPR, c = (idx - row * VPR) * E;
+      r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rs, (row * (int)gld + c) * (int)sizeof(T), 0, NT ? 2 : 0));
     }
   }
   __device__ __forceinline__ void store(T* s, int sld, int tid) const {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int idx = tid + i * NTH, row = idx / VPR, c = (idx - row * VPR) * E;
-      if constexpr (BUF) {
-        *reinterpret_cast<uint4*>(s + row * sld + c) = r[i];
-      } else {
-        // rows past the end zeroed by an AND with an all-ones / all-zeros mask; the empty asm hides that the mask
-        // comes from a condition (as a select it compiled into an exec-mask branch per vector)
-        uint32_t m = 0u - ((ok >> i) & 1u);
-        asm("" : "+v"(m));
-        *reinterpret_cast<uint4*>(s + row * sld + c) = make_uint4(r[i].x & m, r[i].y & m, r[i].z & m, r[i].w & m);
-      }
+      *reinterpret_cast<uint4*>(s + row * sld + c) = r[i];
     }
   }
   __device__ __forceinline__ void load(const T* g, int64_t gld, int valid) { load(g, gld, valid, threadIdx.x); }
   __device__ __forceinline__ void store(T* s, int sld) const { store(s, sld, threadIdx.x); }
 };
 
-// Per-token scalars (g, beta) of a chunk for the first wave: same unconditional-load scheme.
+// Per-token scalars (g, beta) of a chunk for the first wave: lanes past the end read token 0 instead (always in
+// bounds) and report ok = false, so no wait for the data is forced at load time.
 struct RegTok {
   float g, b;
   bool ok;

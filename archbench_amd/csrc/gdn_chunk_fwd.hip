@@ -100,8 +100,8 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
   auto row0_of = [&](int c) { return ((int64_t)b * T_ + (int64_t)c * CH) * H + h; };
   auto nvalid_of = [&](int c) { return min(CH, T_ - c * CH); };
 
-  RegTile<T, CH, K, FTH, FWD_NT_LOAD, false> rk, rq, ru;
-  RegTile<T, CH, BV, FTH, FWD_NT_LOAD, false> rv;
+  RegTile<T, CH, K, FTH, FWD_NT_LOAD> rk, rq, ru;
+  RegTile<T, CH, BV, FTH, FWD_NT_LOAD> rv;
   TriTile<T, FTH, FWD_NT_LOAD> rtm, rp;  // packed lower blocks
   float pG = 0.f, pB = 0.f;  // wave 0: G and beta of lane l's token
   // The next chunk's reads go out in two batches (k, q, v after the first barrier; Tm, P, G, beta after the
@@ -163,14 +163,13 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
     if (c + 1 < NT) prefetch(c + 1);
 
     // rows 32 hf .. 32 hf + 31: K S, Q S and Y = diag(beta) (V - diag(gamma) K S); the state's fragments are the
-    // wave's own and, for the other half of the K rows, the partner's from xS (written before the last barrier)
-    F Sb[K / 32];
+    // wave's own and, for the other half of the K rows, the partner's from xS (written before the last barrier).
+    // Here and below a product over both halves pairs each fragment with the other operand's columns for its half
+    // (offsets by hf), so no fragment is selected by the half.
+    F Sother[NSB];
 #pragma unroll
-    for (int s = 0; s < NSB; ++s) {
-      const F Sother = xS(w, s);
-      Sb[s] = hf ? Sother : Smine[s];
-      Sb[NSB + s] = hf ? Smine[s] : Sother;
-    }
+    for (int s = 0; s < NSB; ++s) Sother[s] = xS(w, s);
+    const int kmine = (K / 2) * hf, kother = (K / 2) - kmine;  // first K column of each half
     // the state entering every hstride-th chunk goes to the stash (slot c / hstride of the sequence), each wave
     // its own rows; the branch is uniform and the stored values come from registers, not from loads in flight
     const bool keep = (c & (hstride - 1)) == 0;
@@ -188,11 +187,15 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
       const int rt_ = 2 * hf + j;
       f32x4 ks = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < K / 32; ++s) mma(ks, frag_kc_perm(sK, LK, 16 * rt_, 32 * s), Sb[s]);
+      for (int s = 0; s < NSB; ++s) mma(ks, frag_kc_perm(sK, LK, 16 * rt_, kmine + 32 * s), Smine[s]);
+#pragma unroll
+      for (int s = 0; s < NSB; ++s) mma(ks, frag_kc_perm(sK, LK, 16 * rt_, kother + 32 * s), Sother[s]);
       if constexpr (OUT) {
         QS[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < K / 32; ++s) mma(QS[j], frag_kc_perm(sQ, LK, 16 * rt_, 32 * s), Sb[s]);
+        for (int s = 0; s < NSB; ++s) mma(QS[j], frag_kc_perm(sQ, LK, 16 * rt_, kmine + 32 * s), Smine[s]);
+#pragma unroll
+        for (int s = 0; s < NSB; ++s) mma(QS[j], frag_kc_perm(sQ, LK, 16 * rt_, kother + 32 * s), Sother[s]);
       }
       float vv[4];
       acc_vals(sV, LV, 16 * rt_, c0, vv);
@@ -202,20 +205,19 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
         Y[j][i] = sB[r] * (vv[i] - sGam[r] * ks[i]);
       }
     }
-    // (fragments are selected by value, never indexed by the half: registers cannot be indexed at run time)
     const F Ymine = frag_acc2<T>(Y[0], Y[1]);
     xY[w][l] = Ymine;
     __syncthreads();
     const F Yother = xY[w ^ NSL][l];
-    const F Yb0 = hf ? Yother : Ymine, Yb1 = hf ? Ymine : Yother;
+    const int tmine = 32 * hf, tother = 32 - tmine;  // first token of each half
 
     // R = Tm Y for the half's rows (saved if SAVE); Rd = exp(G_C - G) R; O = s gamma QS + P R staged
     f32x4 R[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       R[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      mma(R[j], frag_kc_perm(sTm, LC, 16 * (2 * hf + j), 0), Yb0);
-      mma(R[j], frag_kc_perm(sTm, LC, 16 * (2 * hf + j), 32), Yb1);
+      mma(R[j], frag_kc_perm(sTm, LC, 16 * (2 * hf + j), tmine), Ymine);
+      mma(R[j], frag_kc_perm(sTm, LC, 16 * (2 * hf + j), tother), Yother);
     }
     const float GC = sG[CH - 1];
     F Rdmine;
@@ -235,16 +237,14 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
     __syncthreads();  // R and Rd fragments of both halves exchanged
     if (c + 1 < NT) prefetch2(c + 1);
     const F Rdother = xRd[w ^ NSL][l];
-    const F Rd0 = hf ? Rdother : Rdmine, Rd1 = hf ? Rdmine : Rdother;
     if constexpr (OUT) {
       const F Rbother = xR[w ^ NSL][l];
-      const F Rb0 = hf ? Rbother : Rbmine, Rb1 = hf ? Rbmine : Rbother;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int rt_ = 2 * hf + j;
         f32x4 pr = {0.f, 0.f, 0.f, 0.f};
-        mma(pr, frag_kc_perm(sP, LC, 16 * rt_, 0), Rb0);
-        mma(pr, frag_kc_perm(sP, LC, 16 * rt_, 32), Rb1);
+        mma(pr, frag_kc_perm(sP, LC, 16 * rt_, tmine), Rbmine);
+        mma(pr, frag_kc_perm(sP, LC, 16 * rt_, tother), Rbother);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = 16 * rt_ + acc_row(i);
@@ -257,8 +257,8 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
 #pragma unroll
     for (int t = 0; t < NKH; ++t) {
       S[t] *= gC;
-      mma(S[t], frag_oct_perm(sU, LK, 16 * (NKH * hf + t), 0), Rd0);
-      mma(S[t], frag_oct_perm(sU, LK, 16 * (NKH * hf + t), 32), Rd1);
+      mma(S[t], frag_oct_perm(sU, LK, 16 * (NKH * hf + t), tmine), Rdmine);
+      mma(S[t], frag_oct_perm(sU, LK, 16 * (NKH * hf + t), tother), Rdother);
     }
     publish_state();  // the partner read the previous fragments before the exchange barriers above
     __syncthreads();  // O staged; every wave done with this chunk's inputs
