@@ -71,7 +71,8 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
   __shared__ __attribute__((aligned(16))) T sP[CH * LC];
   __shared__ __attribute__((aligned(16))) f32x4 xKd[SW][2][64];      // partial K dS for the other half's rows
   __shared__ __attribute__((aligned(16))) F xR[SW][64], xZ[SW][64];  // dR and Z fragments
-  __shared__ float sG[CH], sB[CH], sGam[CH];
+  // per token: G, exp(G), exp(G_C - G) and -beta exp(G) (formed once per chunk by the first wave)
+  __shared__ float sG[CH], sGam[CH], sDte[CH], sBGn[CH];
 
   int vb, bh;
   sweep_block(V / BV, gridDim.x * BV / V, vb, bh);
@@ -142,9 +143,11 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
     rtm.store(sTm, LC, tid);
     rp.store(sP, LC, tid);
     if (w == 0) {
+      const float gam = __expf(pG), GCl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pG), CH - 1));
       sG[l] = pG;
-      sB[l] = pB;
-      sGam[l] = __expf(pG);
+      sDte[l] = __expf(GCl - pG);
+      sGam[l] = gam;
+      sBGn[l] = -pB * gam;
     }
     __syncthreads();
     if (c > 0) prefetch(c - 1, 1);
@@ -187,11 +190,11 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
       const f32x4 mine = kd[j];
       const f32x4 other = xKd[w ^ NSL][j][l];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dR[j][i] = __expf(GC - sG[16 * rt_ + acc_row(i)]) * (mine[i] + other[i]);
+      for (int i = 0; i < 4; ++i) dR[j][i] = sDte[16 * rt_ + acc_row(i)] * (mine[i] + other[i]);
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib) mma(dR[j], frag_oct(sP, LC, 16 * rt_, 32 * ib), dOb[ib]);
     }
-    // dR to the other half; dY (this half's token rows) = Tm^T dR -> global; Z = diag(beta gamma) dY
+    // dR to the other half; dY (this half's token rows) = Tm^T dR -> global; Z = -diag(beta gamma) dY
     const F dRmine = frag_acc2<T>(dR[0], dR[1]);
     xR[w][l] = dRmine;
     __syncthreads();
@@ -211,23 +214,23 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * (2 * hf + j) + acc_row(i);
-        Z[j][i] *= sB[r] * sGam[r];
+        Z[j][i] *= sBGn[16 * (2 * hf + j) + acc_row(i)];
       }
     const F Zmine = frag_acc2<T>(Z[0], Z[1]);
     xZ[w][l] = Zmine;
     __syncthreads();
     const F Zother = xZ[w ^ NSL][l];
-    // this half's rows of dS <- gamma_C dS + s Q^T (gamma dO) - K^T Z
+    // this half's rows of dS <- gamma_C dS + K^T Z (accumulated in place) + s Q^T (gamma dO)
     const float gC = __expf(GC);
 #pragma unroll
     for (int t = 0; t < NKH; ++t) {
-      f32x4 a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
+      f32x4 a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib) mma(a1, frag_oct(sQ, LK, k0 + 16 * t, 32 * ib), dOg[ib]);
-      mma(a2, frag_oct_perm(sK, LK, k0 + 16 * t, tmine), Zmine);
-      mma(a2, frag_oct_perm(sK, LK, k0 + 16 * t, tother), Zother);
-      dS[t] = gC * dS[t] + scale * a1 - a2;
+      dS[t] *= gC;
+      mma(dS[t], frag_oct_perm(sK, LK, k0 + 16 * t, tmine), Zmine);
+      mma(dS[t], frag_oct_perm(sK, LK, k0 + 16 * t, tother), Zother);
+      dS[t] += scale * a1;
     }
     __syncthreads();  // every wave done with this chunk's inputs
   };

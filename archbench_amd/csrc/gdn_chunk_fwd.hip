@@ -71,7 +71,8 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
     if constexpr (S_ON_Y) return xY[wr][lane_id()];
     else return xS_[wr][s][lane_id()];
   };
-  __shared__ float sG[CH], sB[CH], sGam[CH];
+  // per token: G, beta, exp(G), exp(G_C - G), s exp(G) (formed once per chunk by the first wave)
+  __shared__ float sG[CH], sB[CH], sGam[CH], sDte[CH], sGs[CH];
 
   int vb, bh;
   const int NVB = (V + (MODE == 3 ? K : 0)) / BV;  // column blocks per head
@@ -132,9 +133,12 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
     rtm.store(sTm, LC, tid);
     if constexpr (OUT) rp.store(sP, LC, tid);
     if (w == 0) {
+      const float gam = __expf(pG), GCl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pG), CH - 1));
       sG[l] = pG;
       sB[l] = pB;
-      sGam[l] = __expf(pG);
+      sGam[l] = gam;
+      sDte[l] = __expf(GCl - pG);
+      sGs[l] = scale * gam;
     }
   };
 
@@ -225,8 +229,8 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
       f32x4 d0, d1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        d0[i] = R[0][i] * __expf(GC - sG[32 * hf + acc_row(i)]);
-        d1[i] = R[1][i] * __expf(GC - sG[32 * hf + 16 + acc_row(i)]);
+        d0[i] = R[0][i] * sDte[32 * hf + acc_row(i)];
+        d1[i] = R[1][i] * sDte[32 * hf + 16 + acc_row(i)];
       }
       Rdmine = frag_acc2<T>(d0, d1);
       xRd[w][l] = Rdmine;
@@ -248,7 +252,7 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = 16 * rt_ + acc_row(i);
-          stage[r * LV + c0 + acc_col()] = from_f<T>(scale * sGam[r] * QS[j][i] + pr[i]);
+          stage[r * LV + c0 + acc_col()] = from_f<T>(sGs[r] * QS[j][i] + pr[i]);
         }
       }
     }
