@@ -259,7 +259,7 @@ __device__ __forceinline__ void rs_round(float* a, int hi) {
 #pragma unroll
   for (int k = 0; k < N; ++k) {
     const float keep = hi ? a[k + N] : a[k], send = hi ? a[k] : a[k + N];
-    a[k] = keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), CTRL, 0xf, 0xf, false));
+    a[k] = keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), CTRL, 0xf, 0xf, true));
   }
 }
 
@@ -297,12 +297,12 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   __shared__ __attribute__((aligned(16))) T slab[SLAB];
   __shared__ __attribute__((aligned(16))) T sdv[CH * LS];  // dv of the current slab, for the coalesced store
   __shared__ float sG[CH], sB[CH], sdG[CH], sLast[CH], sColZ[NWAVE][CH], sRed[IW];
+  __shared__ float sGam[CH], sDte[CH];  // exp(G) and exp(G_C - G) per token (formed once per chunk by wave 0)
   __shared__ float sRow[2][6][CH];  // per-half row sums: rq, rk, dbV, rx, dbA, rz
   // HALF (state stride 2): the stash holds the state entering even chunks only; an even chunk advances it through
   // itself into sS1t (the odd chunk's entering state, S1^T [V][LK]) with exp(G_C - G) per row from sDte
   static_assert(!HALF || (sizeof(T) == 2 && !SEPU), "state stride 2: bf16 without separate write keys");
   __shared__ __attribute__((aligned(16))) T sS1t[HALF ? V * LK : 8];
-  __shared__ float sDte[HALF ? CH : 1];
 
   T* sdO = slab;
   T* sV = sdO + CH * LS;
@@ -411,10 +411,9 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   if (tid < CH) {
     sG[tid] = pg;
     sB[tid] = tid < nvalid ? pb : 0.f;
-    if constexpr (HALF) {
-      const float gl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pg), CH - 1));  // G_C (wave 0)
-      sDte[tid] = __expf(gl - pg);
-    }
+    const float gl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pg), CH - 1));  // G_C (wave 0)
+    sGam[tid] = __expf(pg);
+    sDte[tid] = __expf(gl - pg);
   }
 
   // ---- V phase: contractions over V, slab by slab -------------------------------------------------------
@@ -497,7 +496,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
         static_assert(NA >= 1 && NVT % NA == 0, "whole runs of column tiles per wave");
         using V4 = typename std::conditional<sizeof(T) == 2, bf16x4, f32x4>::type;
         const int rt = (w * NA) / NVT, ct0 = w * NA - rt * NVT;
-        const float gC = __expf(sG[CH - 1]);
+        const float gC = sGam[CH - 1];
         if (vs == 0) {  // the same for every slab (K is staged by then)
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb) {
@@ -540,13 +539,12 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
 
   const int lg = l >> 4;  // lane group: rows 4*lg .. 4*lg+3 of each tile
   float gam[4], dte[4], bet[4], Grow[4];
-  const float GC = sG[CH - 1];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 16 * rb + acc_row(i, l);
     Grow[i] = sG[r];
-    gam[i] = __expf(Grow[i]);
-    dte[i] = __expf(GC - Grow[i]);
+    gam[i] = sGam[r];
+    dte[i] = sDte[r];
     bet[i] = sB[r];
   }
   // row dots from the V-phase accumulators (this half's columns); dX = -dY S0^T, so rx = dX . k = -aKY . k
@@ -734,7 +732,7 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
     float red = 0.f;
 #pragma unroll
     for (int i = 0; i < IW; ++i) red += sRed[i];
-    last += __expf(GC) * red;
+    last += sGam[CH - 1] * red;
     if (l == CH - 1) x += last;
     const float incl = wave_inclusive_scan(x);
     const float total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), 63));

@@ -260,10 +260,12 @@ struct FragTile {
       if (NVEC % NTH == 0 || idx < NVEC) {
         const int blk = idx >> 6, ln = idx & 63, s = blk / NCBS, cbl = blk - s * NCBS;
         const T* src = lds + (16 * cbl + (ln & 15)) * ldt + 32 * s + 4 * (ln >> 4);
+        using V4 = typename std::conditional<sizeof(T) == 2, bf16x4, f32x4>::type;  // two 4-element runs
+        const V4 a = *reinterpret_cast<const V4*>(src), b = *reinterpret_cast<const V4*>(src + 16);
 #pragma unroll
         for (int p = 0; p < 4; p += 2) {
-          acc = dot2(r[i][p], r[i][p + 1], src[p], src[p + 1], acc);
-          acc = dot2(r[i][4 + p], r[i][5 + p], src[16 + p], src[17 + p], acc);
+          acc = dot2(r[i][p], r[i][p + 1], a[p], a[p + 1], acc);
+          acc = dot2(r[i][4 + p], r[i][5 + p], b[p], b[p + 1], acc);
         }
       }
     }

@@ -218,9 +218,11 @@ __device__ __forceinline__ void sweep_block(int NV, int BH, int& vb, int& bh) {
 // Sum over the 16 lanes of a DPP row (the columns of one accumulator tile row set), left in every lane of the
 // row: butterfly on DPP, no LDS crossbar.  quad_perm [1,0,3,2] and [2,3,0,1] sum each quad, row_half_mirror
 // (lane i <- 7 - i) adds the other quad of the half-row, row_mirror (lane i <- 15 - i) the other half-row.
+// Every DPP move here reads a lane of its own row, all of which are active, so bound_ctrl (zero for a source
+// lane that is not there) changes no value; it lets the compiler fold the move into the add (v_add_f32_dpp).
 template <int CTRL>
 __device__ __forceinline__ float dpp_sum_step(float x) {
-  return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+  return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, true));
 }
 __device__ __forceinline__ float sum16(float x) {
   x = dpp_sum_step<0xb1>(x);   // quad_perm [1,0,3,2]
@@ -302,7 +304,7 @@ __device__ __forceinline__ float xor8_sum(float x) { return dpp_sum_step<0x128>(
 __device__ __forceinline__ float wave_sum64(float x) { return xor32_sum(xor16_sum(sum16(x))); }
 template <int CTRL>
 __device__ __forceinline__ float dpp_max_step(float x) {
-  return fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false)));
+  return fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, true)));
 }
 __device__ __forceinline__ float wave_max64(float x) {
   x = dpp_max_step<0xb1>(x);

@@ -82,7 +82,7 @@ __device__ __forceinline__ void ts_rows_rs(float (&a)[N], int l) {
 #pragma unroll
   for (int m = 0; m < N / 8; ++m) {
     const float keep = b3 ? a[m + N / 8] : a[m], send = b3 ? a[m] : a[m + N / 8];
-    a[m] = keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0x128, 0xf, 0xf, false));
+    a[m] = keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0x128, 0xf, 0xf, true));
   }
 }
 
