@@ -168,15 +168,17 @@ def timed_loop(fn, steps: int, warmup: int, torch, events: bool = False):
     synchronisations; with events, also the GPU time between HIP events recorded on the current stream (the
     stream the library launches on) around the same calls: (host_s, event_s).
 
-    Python's garbage collector is run before and kept off inside the timed region, as timeit does: a full
-    collection late in this process takes about 80 ms (measured), and one falling among 20 steps of a 2.6 ms layer
-    step read as 6.3 ms per step."""
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
+    Python's garbage collector is run before the warmup and kept off through the warmup and the timed region, as
+    timeit does: a full collection late in this process takes about 80 ms (measured), and one falling among 20
+    steps of a 2.6 ms layer step read as 6.3 ms per step.  Collecting before the warmup rather than between it and
+    the timed steps also keeps the GPU from idling there: after some tens of milliseconds idle its clocks start
+    from their idle state again, and the first 25 ms or so of a heavy load then run up to 30% slower."""
     gc.collect()
     gc.disable()
     try:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record()
@@ -265,9 +267,13 @@ def main() -> int:
             ops.chunk_fwd(x.q, x.k, x.v, x.g, x.beta, None, 1.0)
             ops.chunk_bwd(x.q, x.k, x.v, x.g, x.beta, None, x.do, None, 1.0)
 
-        log(f"timing {args.steps} steps after {args.warmup} warmup")
-        sec, sec_ev = timed_loop(step, args.steps, args.warmup, torch, events=True)
+        # The recompute path is timed first and the headline right after it, with no idle time in between: the
+        # inputs are generated on the host, during which the GPU idles, and for about 25 ms after it goes from idle
+        # to this load its clocks dip (per step 0.88 -> 1.09 -> 0.83 ms over the first 40 steps, by HIP events),
+        # so the headline's timed steps would otherwise measure that transient rather than the sustained rate.
+        log(f"timing {args.steps} steps after {args.warmup} warmup (recompute path first)")
         sec_rc = timed_loop(step_recompute, max(3, args.steps // 2), 1, torch)
+        sec, sec_ev = timed_loop(step, args.steps, args.warmup, torch, events=True)
         tokens = B * T
         with _lib.StageTimer() as st:
             for _ in range(max(3, min(args.steps, 10))):
