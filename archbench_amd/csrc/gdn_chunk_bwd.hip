@@ -71,8 +71,8 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
   __shared__ __attribute__((aligned(16))) T sP[CH * LC];
   __shared__ __attribute__((aligned(16))) f32x4 xKd[SW][2][64];      // partial K dS for the other half's rows
   __shared__ __attribute__((aligned(16))) F xR[SW][64], xZ[SW][64];  // dR and Z fragments
-  // per token: G, exp(G), exp(G_C - G) and -beta exp(G) (formed once per chunk by the first wave)
-  __shared__ float sG[CH], sGam[CH], sDte[CH], sBGn[CH];
+  // per token: exp(G), exp(G_C - G) and -beta exp(G) (formed once per chunk by the first wave)
+  __shared__ float sGam[CH], sDte[CH], sBGn[CH];
 
   int vb, bh;
   sweep_block(V / BV, gridDim.x * BV / V, vb, bh);
@@ -144,7 +144,6 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
     rp.store(sP, LC, tid);
     if (w == 0) {
       const float gam = __expf(pG), GCl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pG), CH - 1));
-      sG[l] = pG;
       sDte[l] = __expf(GCl - pG);
       sGam[l] = gam;
       sBGn[l] = -pB * gam;
@@ -153,7 +152,6 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
     if (c > 0) prefetch(c - 1, 1);
 
     // dS leaving the chunk -> dh (fragment layout); partial U dS over this half's rows, for all tokens
-    const float GC = sG[CH - 1];
     F dSb[NSH];
 #pragma unroll
     for (int s = 0; s < NSH; ++s) {
@@ -221,7 +219,7 @@ __global__ __launch_bounds__(state_threads<BV>()) __attribute__((amdgpu_waves_pe
     __syncthreads();
     const F Zother = xZ[w ^ NSL][l];
     // this half's rows of dS <- gamma_C dS + K^T Z (accumulated in place) + s Q^T (gamma dO)
-    const float gC = __expf(GC);
+    const float gC = sGam[CH - 1];  // exp(G_C)
 #pragma unroll
     for (int t = 0; t < NKH; ++t) {
       f32x4 a1 = {0.f, 0.f, 0.f, 0.f};

@@ -62,8 +62,9 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
   __shared__ __attribute__((aligned(16))) T sP[OUT ? CH * LC : 8];
   __shared__ __attribute__((aligned(16))) T stage[OUT ? CH * LV : 8];  // O, for the coalesced store
   __shared__ __attribute__((aligned(16))) F xY[FW][64], xR[FW][64], xRd[FW][64];  // exchange between halves
-  // the other half's state fragments, in the reading wave's slot; fp32 (K = 64: one fragment) reuses the reader's
-  // Y slot, which the reader overwrites only after reading them and its partner reads only in the next phase
+  // the other half's state fragments, in the reading wave's slot.  fp32 (K = 64: one fragment) uses the reader's Y
+  // slot: the writer reads the reader's Y there (after the Y exchange barrier) before it writes the state after the
+  // update, and the reader writes its next Y there only after it has read the state.
   constexpr bool S_ON_Y = sizeof(T) == 4;
   static_assert(!S_ON_Y || NSB == 1, "the state fragments fit one exchange slot");
   __shared__ __attribute__((aligned(16))) F xS_[S_ON_Y ? 1 : FW][NSB][64];
@@ -71,8 +72,8 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
     if constexpr (S_ON_Y) return xY[wr][lane_id()];
     else return xS_[wr][s][lane_id()];
   };
-  // per token: G, beta, exp(G), exp(G_C - G), s exp(G) (formed once per chunk by the first wave)
-  __shared__ float sG[CH], sB[CH], sGam[CH], sDte[CH], sGs[CH];
+  // per token: beta, exp(G), exp(G_C - G), s exp(G) (formed once per chunk by the first wave)
+  __shared__ float sB[CH], sGam[CH], sDte[CH], sGs[CH];
 
   int vb, bh;
   const int NVB = (V + (MODE == 3 ? K : 0)) / BV;  // column blocks per head
@@ -134,7 +135,6 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
     if constexpr (OUT) rp.store(sP, LC, tid);
     if (w == 0) {
       const float gam = __expf(pG), GCl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pG), CH - 1));
-      sG[l] = pG;
       sB[l] = pB;
       sGam[l] = gam;
       sDte[l] = __expf(GCl - pG);
@@ -223,7 +223,6 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
       mma(R[j], frag_kc_perm(sTm, LC, 16 * (2 * hf + j), tmine), Ymine);
       mma(R[j], frag_kc_perm(sTm, LC, 16 * (2 * hf + j), tother), Yother);
     }
-    const float GC = sG[CH - 1];
     F Rdmine;
     {
       f32x4 d0, d1;
@@ -257,7 +256,7 @@ __global__ __launch_bounds__(fwd_threads<BV>()) __attribute__((amdgpu_waves_per_
       }
     }
     // S <- gamma_C S + U^T Rd for the wave's state rows (both halves of the chunk's tokens)
-    const float gC = __expf(GC);
+    const float gC = sGam[CH - 1];  // exp(G_C)
 #pragma unroll
     for (int t = 0; t < NKH; ++t) {
       S[t] *= gC;
