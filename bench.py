@@ -163,7 +163,8 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def timed_loop(fn, steps: int, warmup: int, torch, events: bool = False):
+def timed_loop(fn, steps: int, warmup: int, torch, events: bool = False, collect: bool = True,
+               settle_ms: float = 40.0):
     """Seconds per call of fn over `steps` calls after `warmup` untimed ones, by the host clock between two
     synchronisations; with events, also the GPU time between HIP events recorded on the current stream (the
     stream the library launches on) around the same calls: (host_s, event_s).
@@ -172,10 +173,22 @@ def timed_loop(fn, steps: int, warmup: int, torch, events: bool = False):
     timeit does: a full collection late in this process takes about 80 ms (measured), and one falling among 20
     steps of a 2.6 ms layer step read as 6.3 ms per step.  Collecting before the warmup rather than between it and
     the timed steps also keeps the GPU from idling there: after some tens of milliseconds idle its clocks start
-    from their idle state again, and the first 25 ms or so of a heavy load then run up to 30% slower."""
-    gc.collect()
-    gc.disable()
+    from their idle state again, and the first 25 ms or so of a heavy load then run up to 30% slower.  With
+    collect false the caller has already collected and disabled the collector (loops timed back to back).
+
+    Before the warmup, fn is run untimed for about settle_ms of GPU time (0: not at all), so that a short step's
+    timed calls fall after that transient rather than inside it."""
+    if collect:
+        gc.collect()
+        gc.disable()
     try:
+        if settle_ms > 0:
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            one = max(time.perf_counter() - t0, 1e-5)
+            for _ in range(min(int(settle_ms * 1e-3 / one), 20000)):
+                fn()
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
@@ -188,7 +201,8 @@ def timed_loop(fn, steps: int, warmup: int, torch, events: bool = False):
         torch.cuda.synchronize()
         host = (time.perf_counter() - t0) / steps
     finally:
-        gc.enable()
+        if collect:
+            gc.enable()
     return (host, e0.elapsed_time(e1) * 1e-3 / steps) if events else host
 
 
@@ -267,17 +281,25 @@ def main() -> int:
             ops.chunk_fwd(x.q, x.k, x.v, x.g, x.beta, None, 1.0)
             ops.chunk_bwd(x.q, x.k, x.v, x.g, x.beta, None, x.do, None, 1.0)
 
-        # The recompute path is timed first and the headline right after it, with no idle time in between: the
-        # inputs are generated on the host, during which the GPU idles, and for about 25 ms after it goes from idle
-        # to this load its clocks dip (per step 0.88 -> 1.09 -> 0.83 ms over the first 40 steps, by HIP events),
-        # so the headline's timed steps would otherwise measure that transient rather than the sustained rate.
+        # The recompute path is timed first (same step counts) and the headline right after it, with no idle time in
+        # between: the inputs are generated on the host, during which the GPU idles, and for about 25-30 ms after it
+        # goes from idle to this load its clocks dip (per step 0.88 -> 1.09 -> 0.83 ms over the first 40 steps, by
+        # HIP events), so the headline's timed steps would otherwise measure that transient rather than the
+        # sustained rate.
         log(f"timing {args.steps} steps after {args.warmup} warmup (recompute path first)")
-        sec_rc = timed_loop(step_recompute, max(3, args.steps // 2), 1, torch)
-        sec, sec_ev = timed_loop(step, args.steps, args.warmup, torch, events=True)
+        # Collected once, before all three loops (the per-kernel stage timing follows at once too): a collection
+        # between them would leave the GPU idle.
+        gc.collect()
+        gc.disable()
+        try:
+            sec_rc = timed_loop(step_recompute, args.steps, args.warmup, torch, collect=False, settle_ms=0)
+            sec, sec_ev = timed_loop(step, args.steps, args.warmup, torch, events=True, collect=False, settle_ms=0)
+            with _lib.StageTimer() as st:
+                for _ in range(max(3, min(args.steps, 10))):
+                    step()
+        finally:
+            gc.enable()
         tokens = B * T
-        with _lib.StageTimer() as st:
-            for _ in range(max(3, min(args.steps, 10))):
-                step()
         stages = {k: (ms / n, n) for k, (ms, n) in st.result.items()}
         call_flops = 3 * f_fwd(K, V) * B * T * H
         algo_bytes = algo_bytes_step(K, V) * B * T * H
