@@ -314,13 +314,11 @@ __global__ __launch_bounds__(ITH) void bwd_intra_kernel(
   // work items: chunks, or (HALF) pairs of chunks (2 j, 2 j + 1) of one sequence, the second if it exists
   const int NT2 = HALF ? (NT + 1) / 2 : NT;
   const int nitem = BH * NT2;
+  // items in chunk-position-major order (item = position * BH + b*h): the workgroups in flight together read the
+  // same token rows of every head, so each row of q, k, v and dO is fetched by all its heads at about the same time
   auto item_chunk = [&](int it) {  // the first chunk of work item it
-    if constexpr (HALF) {
-      const int bh_ = (int)((unsigned)it / (unsigned)NT2);
-      return bh_ * NT + 2 * (it - bh_ * NT2);
-    } else {
-      return it;
-    }
+    const int pos = (int)((unsigned)it / (unsigned)BH), bh_ = it - pos * BH;
+    return bh_ * NT + (HALF ? 2 * pos : pos);
   };
   auto chunk_pos = [&](int ci_) { return ci_ - (int)((unsigned)ci_ / (unsigned)NT) * NT; };  // chunk in sequence
   // the stash slot of chunk ci's entering state (HALF: even chunks only)
