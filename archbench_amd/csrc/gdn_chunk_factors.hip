@@ -21,7 +21,7 @@
 
 namespace gdn {
 
-// Persistent: workgroup x handles items x, x + gridDim.x, ... of the (chunk, b*h) grid (item = c * BH + bh), with
+// Persistent: workgroup x handles items x, x + gridDim.x, ... of the (b*h, chunk) grid (item = bh * NT + c), with
 // the next item's k, q, g and beta prefetched into registers while the current one is factored, in two batches
 // (k after the first barrier, q, g, beta after the second: 6% faster than all at once).
 // LDS overlays keep a workgroup at about 50 KB (bf16, K = 128), so three share a CU: A (fp32) overlays Q row for
@@ -53,11 +53,8 @@ void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, cons
   const int w = wave_id(), l = lane_id();
   RegTile<T, CH, K, NTHR, true> rk, rq, ru;  // k, q, u are read once here: nontemporal
   RegTok rt;
-  // items in chunk-position-major order (item = c * BH + b*h), so that the workgroups in flight together read the
-  // same token rows of every head; outputs are indexed by chunk, bh * NT + c
-  const int BH = nitems / NT;
   auto prefetch = [&](int it, int part) {
-    const int c = it / BH, bh = it - c * BH;
+    const int bh = it / NT, c = it - bh * NT;
     const int b = bh / H, h = bh - b * H;
     const int nvalid = min(CH, T_ - c * CH);
     const int64_t row0 = ((int64_t)b * T_ + (int64_t)c * CH) * H + h;
@@ -72,7 +69,6 @@ void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, cons
   };
   if ((int)blockIdx.x < nitems) prefetch(blockIdx.x, 0);
   for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
-    const int64_t cidx = (int64_t)(it - (it / BH) * BH) * NT + it / BH;  // chunk index of the item
     rk.store(sK, LK);
     rq.store(sQ, LK);
     if constexpr (SEPU) ru.store(sU, LK);
@@ -80,7 +76,7 @@ void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, cons
       const float G = wave_inclusive_scan(rt.ok ? rt.g : 0.f);
       sG[l] = G;
       sB[l] = rt.ok ? rt.b : 0.f;
-      gGc[cidx * CH + l] = G;
+      gGc[(int64_t)it * CH + l] = G;
     }
     __syncthreads();
     const int itn = it + (int)gridDim.x;
@@ -92,8 +88,8 @@ void chunk_factors_kernel(const T* __restrict__ q, const T* __restrict__ k, cons
     __syncthreads();
     factors_merge<T>(D, sA, sD, sTm, w);
     __syncthreads();
-    s2g_tri<T, NTHR, true>(gTm + cidx * CH_TRI_ELEMS, sTm, LC, threadIdx.x);
-    s2g_tri<T, NTHR, true>(gP + cidx * CH_TRI_ELEMS, sP, LC, threadIdx.x);
+    s2g_tri<T, NTHR, true>(gTm + (int64_t)it * CH_TRI_ELEMS, sTm, LC, threadIdx.x);
+    s2g_tri<T, NTHR, true>(gP + (int64_t)it * CH_TRI_ELEMS, sP, LC, threadIdx.x);
     __syncthreads();  // LDS free for the next item
   }
 }
